@@ -1,0 +1,116 @@
+/*
+ * vxm_q8.h -- C ABI of the MI355X (gfx950) Q8_0 matmul path for the VoxCPM2
+ * C runtime (stevenke1981/voxcpm-cpp).
+ *
+ * The reference executes every projection as ggml_mul_mat(W_q8_0, x_f32)
+ * inside graphs run by vcpm_backend_compute_graph (src/ggml_backend.c:557-599).
+ * This library replaces that arithmetic with hand-written HIP kernels behind
+ * plain C entry points: no torch types, no C++ exceptions, int status codes.
+ *
+ * Conventions
+ *  - Every entry point returns VXM_OK (0) or a vxm_status code; the message of
+ *    the last failure on a context is returned by vxm_last_error().
+ *  - Pointers named *_dev are device pointers (from vxm_malloc, or any HIP
+ *    allocation on the context's device).  Host buffers are caller-owned.
+ *  - Compute calls are asynchronous and ordered on the context's stream
+ *    (vxm_get_stream); nothing synchronises the host except vxm_sync and the
+ *    vxm_memcpy_* / upload / download calls, which are the host-boundary
+ *    points the reference API implies (src/ggml_backend.c:356-457).
+ *  - Activation matrices use the ggml layout of a [K, M] tensor: M rows of K
+ *    contiguous floats, row m at x + m*K.  Outputs are [N, M]: y[m*N + n].
+ *  - A quantized activation is two device arrays: xq int8 [M][K] and xd fp16
+ *    bits [M][K/32] (the scale of block b of row m at xd[m*(K/32) + b]).
+ */
+#ifndef VXM_Q8_H
+#define VXM_Q8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same values as vcpm_status (include/voxcpm.h:14-23). */
+typedef enum vxm_status {
+    VXM_OK = 0,
+    VXM_ERR_INVALID_ARG = 1,
+    VXM_ERR_IO = 2,
+    VXM_ERR_MODEL_FORMAT = 3,
+    VXM_ERR_UNSUPPORTED_ARCH = 4,
+    VXM_ERR_BACKEND = 5,
+    VXM_ERR_OOM = 6,
+    VXM_ERR_NOT_IMPLEMENTED = 7
+} vxm_status;
+
+/* Activation quantizer variants (ggml-cpu quantize_row_q8_0 on x86 vs
+ * quantize_row_q8_0_ref); the weights of a GGUF file use the _ref rule. */
+#define VXM_QUANT_REF 0
+#define VXM_QUANT_X86 1
+
+/* Kernel path for vxm_mul_mat_*: AUTO picks by M. */
+#define VXM_PATH_AUTO 0
+#define VXM_PATH_GEMV 1   /* weight-streaming GEMV, any M (loops over rows of x) */
+#define VXM_PATH_MFMA 2   /* LDS-staged int8 MFMA GEMM                           */
+
+typedef struct vxm_ctx vxm_ctx;
+typedef struct vxm_weight vxm_weight;
+
+/* ---- context -------------------------------------------------------------
+ * Replaces vcpm_backend_init / vcpm_backend_free (src/ggml_backend.c:49-140)
+ * for this path: one context = one device + one stream. */
+int         vxm_open(int device, vxm_ctx **out);
+int         vxm_close(vxm_ctx *ctx);
+int         vxm_sync(vxm_ctx *ctx);
+void       *vxm_get_stream(vxm_ctx *ctx);
+const char *vxm_last_error(const vxm_ctx *ctx);
+int         vxm_set_quant_variant(vxm_ctx *ctx, int variant);
+int         vxm_set_path(vxm_ctx *ctx, int path);
+
+/* Device memory and host-boundary copies (ggml_backend_tensor_set/get,
+ * src/ggml_backend.c:356-380,422-457).  The copies return when complete. */
+int vxm_malloc(vxm_ctx *ctx, size_t bytes, void **out_dev);
+int vxm_free(vxm_ctx *ctx, void *dev);
+int vxm_memcpy_h2d(vxm_ctx *ctx, void *dst_dev, const void *src_host, size_t bytes);
+int vxm_memcpy_d2h(vxm_ctx *ctx, void *dst_host, const void *src_dev, size_t bytes);
+
+/* ---- Q8_0 weights --------------------------------------------------------
+ * Upload of a GGUF Q8_0 tensor with ne = [k, n_rows] (34-byte blocks: fp16 d,
+ * int8 qs[32]; rows of k/32 blocks), as vcpm_model_offload does
+ * (src/model_loader.c:665-700).  The device copy is repacked (quants and
+ * scales split) but vxm_download_q8_0 re-emits the exact GGUF bytes. */
+int     vxm_upload_q8_0(vxm_ctx *ctx, const void *gguf_rows, int64_t n_rows, int64_t k,
+                        vxm_weight **out);
+int     vxm_download_q8_0(vxm_ctx *ctx, const vxm_weight *w, void *gguf_rows);
+int     vxm_weight_free(vxm_ctx *ctx, vxm_weight *w);
+int64_t vxm_weight_rows(const vxm_weight *w);
+int64_t vxm_weight_cols(const vxm_weight *w);
+
+/* ---- the matmul (ggml_mul_mat on Q8_0, src/projections.h:24-29) ---------- */
+/* x (fp32 [M][K]) -> Q8_0 activation, per block d = amax/127. */
+int vxm_quantize_q8_0(vxm_ctx *ctx, const float *x_dev, int64_t M, int64_t K, int variant,
+                      int8_t *xq_dev, uint16_t *xd_dev);
+/* y = W . x with x quantized internally (ggml_mul_mat(W, x) semantics). */
+int vxm_mul_mat_q8_0(vxm_ctx *ctx, const vxm_weight *w, const float *x_dev, int64_t M,
+                     float *y_dev);
+/* y = W . x for an already quantized activation. */
+int vxm_mul_mat_q8_0_q8_0(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq_dev,
+                          const uint16_t *xd_dev, int64_t M, float *y_dev);
+/* Debug: int32 per-block sums of vec_dot_q8_0_q8_0, out[(m*N + n)*(K/32) + b]. */
+int vxm_block_dots_q8_0(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq_dev,
+                        const uint16_t *xd_dev, int64_t M, int32_t *out_dev);
+
+/* ---- host helpers (no device work) --------------------------------------
+ * GGUF Q8_0 quantization of F32 rows with the weight rule of
+ * ggml_quantize_chunk (tools/quantize.c:292): d = amax/127 (fp16),
+ * qs = roundf(x / d).  Writes rows * (k/32) 34-byte blocks. */
+int vxm_host_quantize_q8_0(const float *x, int64_t rows, int64_t k, void *gguf_rows);
+/* Seeded synthetic N(mean, std^2) data: SplitMix64 (as in the reference's
+ * CFM noise, src/gen_step.c:409-431) with Box-Muller in double; element i is
+ * stream element offset + i.  No reference counterpart: benchmark inputs. */
+int vxm_host_randn(uint64_t seed, uint64_t offset, int64_t n, float mean, float std, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VXM_Q8_H */

@@ -1,0 +1,323 @@
+"""ctypes view of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, the smoke check and the
+benchmark's CPU-baseline leg, never by the product.  See vxm_oracle.c for
+the reference citations of each function.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+BASE_LIB = os.path.join(HERE, "libcpubase.so")
+
+QUANT_REF = 0
+QUANT_X86 = 1
+
+_P = C.c_void_p
+_I64 = C.c_int64
+_I = C.c_int
+_F = C.c_float
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class Cfg(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_int32), ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32),
+        ("head_dim", C.c_int32), ("ffn", C.c_int32), ("eps", C.c_float),
+        ("rope_theta", C.c_float), ("no_rope", C.c_int32), ("scale", C.c_float),
+        ("rope_ff", C.c_void_p), ("quant_variant", C.c_int32),
+    ]
+
+
+class Layer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("wq", "wk", "wv", "wo", "wg", "wu", "wd", "g_in", "g_post")] + [
+        ("wtype", C.c_int32)]
+
+
+class LocDiT(C.Structure):
+    _fields_ = [
+        ("layers", C.c_void_p), ("n_layers", C.c_int32),
+        ("in_proj", C.c_void_p), ("in_bias", C.c_void_p),
+        ("cond_proj", C.c_void_p), ("cond_bias", C.c_void_p),
+        ("out_proj", C.c_void_p), ("out_bias", C.c_void_p),
+        ("norm", C.c_void_p),
+        ("t_w1", C.c_void_p), ("t_w2", C.c_void_p), ("dt_w1", C.c_void_p), ("dt_w2", C.c_void_p),
+        ("t_b1", C.c_void_p), ("t_b2", C.c_void_p), ("dt_b1", C.c_void_p), ("dt_b2", C.c_void_p),
+        ("feat", C.c_int32),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        L = C.CDLL(LIB)
+        L.orc_fp32_to_fp16.restype = C.c_uint16
+        L.orc_fp32_to_fp16.argtypes = [_F]
+        L.orc_fp16_to_fp32.restype = _F
+        L.orc_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.orc_bf16_round.restype = _F
+        L.orc_bf16_round.argtypes = [_F]
+        L.orc_fp32_to_fp16_n.argtypes = [_P, _P, _I64]
+        L.orc_fp16_to_fp32_n.argtypes = [_P, _P, _I64]
+        L.orc_bf16_round_n.argtypes = [_P, _P, _I64]
+        L.orc_quantize_row_q8_0.argtypes = [_P, _P, _I64, _I]
+        L.orc_quantize_rows_q8_0.argtypes = [_P, _P, _I64, _I64, _I]
+        L.orc_dequantize_row_q8_0.argtypes = [_P, _P, _I64]
+        L.orc_block_dots_q8_0.argtypes = [_P, _P, _I64, _I64, _I64, _P]
+        L.orc_mul_mat_q8_0.argtypes = [_P, _P, _I64, _I64, _I64, _P]
+        L.orc_mul_mat_q8_0_f64.argtypes = [_P, _P, _I64, _I64, _I64, _P]
+        L.orc_rms_norm.argtypes = [_P, _P, _I64, _I64, _F, _P]
+        L.orc_rope_neox.argtypes = [_P, _I64, _I64, C.c_int32, _F, _P]
+        L.orc_silu.restype = _F
+        L.orc_silu.argtypes = [_F]
+        L.orc_minicpm4_block.argtypes = [C.POINTER(Cfg), C.POINTER(Layer), _P, _I64, _P, _P, _I64,
+                                         C.c_int32, _I]
+        L.orc_attention.argtypes = [C.POINTER(Cfg), C.POINTER(Layer), _P, _I64, _P, _P, _I64, C.c_int32, _I, _P]
+        L.orc_mlp.argtypes = [C.POINTER(Cfg), C.POINTER(Layer), _P, _I64, _P]
+        L.orc_minicpm4_forward.argtypes = [C.POINTER(Cfg), _P, C.c_int32, _P, _P, _I64, _P, _P, _I64,
+                                           C.c_int32]
+        L.orc_sinusoid_embed.argtypes = [_F, C.c_int32, _P]
+        L.orc_locdit_forward.argtypes = [C.POINTER(Cfg), C.POINTER(LocDiT), _P, _P, C.c_int32, C.c_int32,
+                                         _F, _F, _P, _P]
+        L.orc_cfm_sway_t_bf16.restype = _F
+        L.orc_cfm_sway_t_bf16.argtypes = [_I, _I]
+        L.orc_cfm_uniform_t_bf16.restype = _F
+        L.orc_cfm_uniform_t_bf16.argtypes = [_I, _I]
+        L.orc_cfm_cfg_zero_star.restype = _F
+        L.orc_cfm_cfg_zero_star.argtypes = [_P, _P, _I, _F]
+        L.orc_cfm_zero_star_steps.argtypes = [_I]
+        L.orc_cfm_solve.argtypes = [C.POINTER(Cfg), C.POINTER(LocDiT), _P, _P, C.c_int32, C.c_int32, _P,
+                                    _I, _F, _I, _I]
+        _lib = L
+    return _lib
+
+
+# ---- number formats ----
+
+def fp32_to_fp16_bits(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_fp32_to_fp16_n(_p(x), _p(out), x.size)
+    return out
+
+
+def fp16_bits_to_fp32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().orc_fp16_to_fp32_n(_p(h), _p(out), h.size)
+    return out
+
+
+def bf16_round(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.float32)
+    lib().orc_bf16_round_n(_p(x), _p(out), x.size)
+    return out
+
+
+# ---- Q8_0 ----
+
+def quantize_rows(x, variant):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    out = np.empty(rows * (k // 32) * 34, dtype=np.uint8)
+    lib().orc_quantize_rows_q8_0(_p(x), _p(out), rows, k, variant)
+    return out
+
+
+def dequantize_rows(q, rows, k):
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    out = np.empty((rows, k), dtype=np.float32)
+    rb = k // 32 * 34
+    for r in range(rows):
+        lib().orc_dequantize_row_q8_0(_p(q[r * rb:(r + 1) * rb]), _p(out[r]), k)
+    return out
+
+
+def split_q8(q, rows, k):
+    """GGUF rows -> (qs int8 [rows][k], d fp16 bits [rows][k/32])."""
+    b = np.ascontiguousarray(q, dtype=np.uint8).reshape(rows, k // 32, 34)
+    d = b[:, :, :2].copy().view(np.uint16).reshape(rows, k // 32)
+    qs = b[:, :, 2:].copy().view(np.int8).reshape(rows, k)
+    return qs, d
+
+
+def join_q8(qs, d):
+    rows, k = qs.shape
+    b = np.empty((rows, k // 32, 34), dtype=np.uint8)
+    b[:, :, :2] = np.ascontiguousarray(d, dtype=np.uint16).reshape(rows, k // 32, 1).view(np.uint8)
+    b[:, :, 2:] = np.ascontiguousarray(qs, dtype=np.int8).reshape(rows, k // 32, 32).view(np.uint8)
+    return b.reshape(-1)
+
+
+def block_dots(w, xq, N, K, M):
+    out = np.empty((M, N, K // 32), dtype=np.int32)
+    lib().orc_block_dots_q8_0(_p(w), _p(xq), N, K, M, _p(out))
+    return out
+
+
+def mul_mat(w, xq, N, K, M):
+    y = np.empty((M, N), dtype=np.float32)
+    lib().orc_mul_mat_q8_0(_p(w), _p(xq), N, K, M, _p(y))
+    return y
+
+
+def mul_mat_f64(w, xq, N, K, M):
+    y = np.empty((M, N), dtype=np.float64)
+    lib().orc_mul_mat_q8_0_f64(_p(w), _p(xq), N, K, M, _p(y))
+    return y
+
+
+def rms_norm(x, g, eps):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, n = x.shape
+    y = np.empty_like(x)
+    gg = None if g is None else np.ascontiguousarray(g, dtype=np.float32)
+    lib().orc_rms_norm(_p(x), _p(gg), rows, n, eps, _p(y))
+    return y
+
+
+def rope_neox(x, n_heads, head_dim, pos, theta, ff=None):
+    x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    f = None if ff is None else np.ascontiguousarray(ff, dtype=np.float32)
+    lib().orc_rope_neox(_p(x), n_heads, head_dim, pos, theta, _p(f))
+    return x
+
+
+# ---- MiniCPM4 ----
+
+# LongRoPE short factors of the VoxCPM2 lm_config (src/minicpm4.c:49-66):
+# model constants, one per rotary pair when head_dim == 128.
+ROPE_SHORT_FACTORS = np.array([
+    0.9977997200, 1.0146582960, 1.0349680405, 1.0594292461,
+    1.0888815017, 1.1243301355, 1.1669771036, 1.2182568067,
+    1.2798772354, 1.3538666752, 1.4426259040, 1.5489853360,
+    1.6762658237, 1.8283407612, 2.0096956086, 2.2254789275,
+    2.4815363797, 2.7844159346, 3.1413289096, 3.5600478448,
+    4.0487193801, 4.6155695421, 5.2684819497, 6.0144385919,
+    6.8588300492, 7.8046682500, 8.8517684937, 9.9960050583,
+    11.2287664413, 12.5367574692, 13.9022579193, 15.3038854599,
+    16.7178382874, 18.1194648743, 19.4849643707, 20.7929573059,
+    22.0257186890, 23.1699542999, 24.2170543671, 25.1628932953,
+    26.0072841644, 26.7532405853, 27.4061527252, 27.9730033875,
+    28.4616756439, 28.8803939819, 29.2373065948, 29.5401859283,
+    29.7962436676, 30.0120277405, 30.1933822632, 30.3454570770,
+    30.4727382660, 30.5790977478, 30.6678562164, 30.7418460846,
+    30.8034667969, 30.8547458649, 30.8973922729, 30.9328403473,
+    30.9622936249, 30.9867553711, 31.0070648193, 31.0239238739,
+], dtype=np.float32)
+
+
+def make_cfg(hidden, n_heads, n_kv_heads, head_dim, ffn, eps=1e-6, rope_theta=10000.0, no_rope=0,
+             scale=1.0, rope_ff=None, quant_variant=QUANT_X86):
+    c = Cfg(hidden, n_heads, n_kv_heads, head_dim, ffn, eps, rope_theta, no_rope, scale, None, quant_variant)
+    c._keep = None
+    if rope_ff is not None:
+        ff = np.ascontiguousarray(rope_ff, dtype=np.float32)
+        c._keep = ff
+        c.rope_ff = ff.ctypes.data
+    return c
+
+
+class LayerW:
+    """Host copy of one block's weights: GGUF Q8_0 byte arrays + F32 gains."""
+
+    names = ("wq", "wk", "wv", "wo", "wg", "wu", "wd", "g_in", "g_post")
+
+    def __init__(self, wtype=0, **kw):
+        self.wtype = wtype
+        for n in self.names:
+            v = kw.get(n)
+            setattr(self, n, None if v is None else np.ascontiguousarray(v))
+
+    def struct(self):
+        return Layer(*[(None if getattr(self, n) is None else getattr(self, n).ctypes.data) for n in self.names],
+                     self.wtype)
+
+
+def minicpm4_block(cfg, lw, x, k_cache=None, v_cache=None, capacity=0, pos=0, no_causal=0):
+    x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    M = x.shape[0]
+    s = lw.struct()
+    rc = lib().orc_minicpm4_block(C.byref(cfg), C.byref(s), _p(x), M, _p(k_cache), _p(v_cache), capacity, pos,
+                                  no_causal)
+    assert rc == 0
+    return x
+
+
+def attention(cfg, lw, xn, k_cache=None, v_cache=None, capacity=0, pos=0, no_causal=0):
+    xn = np.ascontiguousarray(xn, dtype=np.float32)
+    M = xn.shape[0]
+    out = np.empty((M, cfg.hidden), dtype=np.float32)
+    s = lw.struct()
+    rc = lib().orc_attention(C.byref(cfg), C.byref(s), _p(xn), M, _p(k_cache), _p(v_cache), capacity, pos,
+                             no_causal, _p(out))
+    assert rc == 0
+    return out
+
+
+def mlp(cfg, lw, xn):
+    xn = np.ascontiguousarray(xn, dtype=np.float32)
+    M = xn.shape[0]
+    out = np.empty((M, cfg.hidden), dtype=np.float32)
+    s = lw.struct()
+    lib().orc_mlp(C.byref(cfg), C.byref(s), _p(xn), M, _p(out))
+    return out
+
+
+def minicpm4_forward(cfg, layers, final_norm, x, k_caches, v_caches, capacity, pos):
+    x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    M = x.shape[0]
+    arr = (Layer * len(layers))(*[l.struct() for l in layers])
+    kp = (C.c_void_p * len(layers))(*[k.ctypes.data for k in k_caches])
+    vp = (C.c_void_p * len(layers))(*[v.ctypes.data for v in v_caches])
+    fn = None if final_norm is None else np.ascontiguousarray(final_norm, dtype=np.float32)
+    rc = lib().orc_minicpm4_forward(C.byref(cfg), C.cast(arr, C.c_void_p), len(layers), _p(fn), _p(x), M,
+                                    C.cast(kp, C.c_void_p), C.cast(vp, C.c_void_p), capacity, pos)
+    assert rc == 0
+    return x
+
+
+# ---- CFM ----
+
+def sway_t(step, n):
+    return lib().orc_cfm_sway_t_bf16(step, n)
+
+
+def uniform_t(step, n):
+    return lib().orc_cfm_uniform_t_bf16(step, n)
+
+
+def cfg_zero_star(negative, positive, cfg_value):
+    neg = np.ascontiguousarray(negative, dtype=np.float32).copy()
+    pos = np.ascontiguousarray(positive, dtype=np.float32)
+    st = lib().orc_cfm_cfg_zero_star(_p(neg), _p(pos), neg.size, cfg_value)
+    return st, neg
+
+
+def zero_star_steps(n):
+    return lib().orc_cfm_zero_star_steps(n)
+
+
+def sinusoid(t, dim):
+    out = np.empty(dim, dtype=np.float32)
+    lib().orc_sinusoid_embed(t, dim, _p(out))
+    return out

@@ -1,0 +1,124 @@
+"""GPU parity of the Q8_0 matmul path against the CPU oracle.
+
+Bar: quantized activations and int32 per-block sums bit-exact; fp32 outputs
+within 1e-3 relative / 1e-4 absolute of the oracle's fp64 sum of the same
+per-block terms (the GPU adds the terms in a different order than ggml).
+"""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 1e-4
+
+
+def _dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def _np(t):
+    return t.cpu().numpy()
+
+
+def _case(orc, N, K, M, seed, wstd=0.02):
+    rng = np.random.default_rng(seed)
+    w = rng.normal(0, wstd, (N, K)).astype(np.float32)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    return w, x, orc.quantize_rows(w, orc.QUANT_REF)
+
+
+def _assert_close(y, ref64):
+    err = np.abs(y.astype(np.float64) - ref64)
+    bad = err > ATOL + RTOL * np.abs(ref64)
+    assert not bad.any(), f"{bad.sum()} of {bad.size} outside 1e-3 rel / 1e-4 abs, max err {err.max()}"
+
+
+def test_upload_download_round_trip(vxm_ctx, orc):
+    for N, K in ((1, 32), (7, 96), (33, 2048), (5, 6144)):
+        _, _, wq = _case(orc, N, K, 1, N + K)
+        w = vxm_ctx.upload_q8_0(wq, N, K)
+        assert np.array_equal(w.download(), wq)
+        w.free()
+
+
+@pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("M,K", [(1, 32), (3, 64), (1, 2048), (2, 6144), (17, 1024)])
+def test_quantize_bit_exact(vxm_ctx, orc, variant, M, K):
+    rng = np.random.default_rng(M * 31 + K + variant)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    x[0, :32] = 0.0                       # zero block
+    if K >= 64:
+        x[0, 32:64] = np.arange(32) - 15.5   # exact halves after scaling
+        x[0, 63] = 127.0
+    xq, xd = vxm_ctx.quantize_q8_0(_dev(x), variant)
+    ref = orc.quantize_rows(x, variant)
+    qs, d = orc.split_q8(ref, M, K)
+    assert np.array_equal(_np(xq), qs)
+    assert np.array_equal(_np(xd).view(np.uint16), d)
+
+
+@pytest.mark.parametrize("N,K,M", [(1, 32, 1), (7, 64, 3), (5, 96, 2), (64, 1024, 1), (33, 2048, 2),
+                                   (16, 6144, 1), (9, 4096, 3), (4, 3072, 1)])
+def test_block_dots_bit_exact(vxm_ctx, orc, N, K, M):
+    _, x, wq = _case(orc, N, K, M, 7 * N + K + M)
+    w = vxm_ctx.upload_q8_0(wq, N, K)
+    xq, xd = vxm_ctx.quantize_q8_0(_dev(x), 1)
+    got = _np(vxm_ctx.block_dots(w, xq, xd))
+    ref = orc.block_dots(wq, orc.quantize_rows(x, 1), N, K, M)
+    assert np.array_equal(got, ref)
+    w.free()
+
+
+@pytest.mark.parametrize("N,K,M", [(1, 32, 1), (7, 64, 3), (5, 96, 2), (257, 512, 1), (64, 1024, 1),
+                                   (130, 2048, 1), (33, 2048, 3), (16, 6144, 2), (9, 4096, 1),
+                                   (4, 3072, 2), (1000, 1024, 4)])
+def test_mul_mat_matches_oracle(vxm_ctx, orc, N, K, M):
+    _, x, wq = _case(orc, N, K, M, 11 * N + K + M)
+    w = vxm_ctx.upload_q8_0(wq, N, K)
+    y = _np(vxm_ctx.mul_mat(w, _dev(x)))
+    xq = orc.quantize_rows(x, 1)
+    _assert_close(y, orc.mul_mat_f64(wq, xq, N, K, M))
+    # and against ggml's sequential fp32 order
+    _assert_close(y, orc.mul_mat(wq, xq, N, K, M).astype(np.float64))
+    w.free()
+
+
+def test_golden_cases(vxm_ctx, orc):
+    g = np.load(os.path.join(GOLDEN, "q8_cases.npz"))
+    i = 0
+    while f"c{i}_shape" in g:
+        N, K, M = (int(v) for v in g[f"c{i}_shape"])
+        w = vxm_ctx.upload_q8_0(g[f"c{i}_wq"], N, K)
+        xq, xd = vxm_ctx.quantize_q8_0(_dev(g[f"c{i}_x"]), 1)
+        qs, d = orc.split_q8(g[f"c{i}_xq"], M, K)
+        assert np.array_equal(_np(xq), qs) and np.array_equal(_np(xd).view(np.uint16), d)
+        assert np.array_equal(_np(vxm_ctx.block_dots(w, xq, xd)), g[f"c{i}_sums"])
+        _assert_close(_np(vxm_ctx.mul_mat_q8(w, xq, xd)), g[f"c{i}_y64"])
+        w.free()
+        i += 1
+    assert i == 6
+
+
+@pytest.mark.parametrize("N,K", [(6144, 2048), (2048, 6144)])
+def test_decode_gemv_full_size_seed0(vxm_ctx, orc, N, K):
+    """The GEMV workload: W ~ N(0, 0.02) from seed 0, x ~ N(0, 1), Q8_0 both."""
+    import vxm
+
+    w32 = vxm.host_randn(0, N * K, 0.0, 0.02).reshape(N, K)
+    x = vxm.host_randn(0, K, 0.0, 1.0, offset=N * K).reshape(1, K)
+    wq = vxm.host_quantize_q8_0(w32)
+    assert np.array_equal(wq[: 34 * (K // 32)], orc.quantize_rows(w32[:1], orc.QUANT_REF))
+    w = vxm_ctx.upload_q8_0(wq, N, K)
+    xq, xd = vxm_ctx.quantize_q8_0(_dev(x), 1)
+    xq_ref = orc.quantize_rows(x, 1)
+    # every int32 block sum bit-exact
+    assert np.array_equal(_np(vxm_ctx.block_dots(w, xq, xd)), orc.block_dots(wq, xq_ref, N, K, 1))
+    y = _np(vxm_ctx.mul_mat_q8(w, xq, xd))
+    _assert_close(y, orc.mul_mat_f64(wq, xq_ref, N, K, 1))
+    w.free()

@@ -1,0 +1,270 @@
+// runtime.hip -- context, device memory, host-boundary copies and the Q8_0
+// weight upload (GGUF rows -> split device layout) of the gfx950 library.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "vxm_internal.h"
+
+int vxm_fail(vxm_ctx *ctx, int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    if (ctx) ctx->err = buf;
+    return code;
+}
+
+static std::string g_open_err;
+
+extern "C" int vxm_open(int device, vxm_ctx **out) {
+    if (!out) return VXM_ERR_INVALID_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        g_open_err = "no HIP device";
+        return VXM_ERR_BACKEND;
+    }
+    if (device < 0 || device >= n) {
+        g_open_err = "device index out of range";
+        return VXM_ERR_INVALID_ARG;
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        g_open_err = "hipGetDeviceProperties failed";
+        return VXM_ERR_BACKEND;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        g_open_err = std::string("unsupported architecture ") + prop.gcnArchName + " (built for gfx950)";
+        return VXM_ERR_UNSUPPORTED_ARCH;
+    }
+    if (hipSetDevice(device) != hipSuccess) {
+        g_open_err = "hipSetDevice failed";
+        return VXM_ERR_BACKEND;
+    }
+    vxm_ctx *ctx = new vxm_ctx();
+    ctx->device = device;
+    ctx->n_cu = prop.multiProcessorCount;
+    // A blocking stream: ordered with work on the legacy default stream, so
+    // callers that stage inputs there (torch, hipMemcpy) need no extra sync.
+    if (hipStreamCreate(&ctx->stream) != hipSuccess) {
+        delete ctx;
+        g_open_err = "hipStreamCreate failed";
+        return VXM_ERR_BACKEND;
+    }
+    *out = ctx;
+    return VXM_OK;
+}
+
+extern "C" int vxm_close(vxm_ctx *ctx) {
+    if (!ctx) return VXM_ERR_INVALID_ARG;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    if (ctx->act_buf) hipFree(ctx->act_buf);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return VXM_OK;
+}
+
+extern "C" int vxm_sync(vxm_ctx *ctx) {
+    if (!ctx) return VXM_ERR_INVALID_ARG;
+    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return VXM_OK;
+}
+
+extern "C" void *vxm_get_stream(vxm_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+extern "C" const char *vxm_last_error(const vxm_ctx *ctx) {
+    return ctx ? ctx->err.c_str() : g_open_err.c_str();
+}
+
+extern "C" int vxm_set_quant_variant(vxm_ctx *ctx, int variant) {
+    if (!ctx) return VXM_ERR_INVALID_ARG;
+    if (variant != VXM_QUANT_REF && variant != VXM_QUANT_X86)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "unknown quantizer variant %d", variant);
+    ctx->quant_variant = variant;
+    return VXM_OK;
+}
+
+extern "C" int vxm_set_path(vxm_ctx *ctx, int path) {
+    if (!ctx) return VXM_ERR_INVALID_ARG;
+    if (path < VXM_PATH_AUTO || path > VXM_PATH_MFMA)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "unknown kernel path %d", path);
+    ctx->path = path;
+    return VXM_OK;
+}
+
+extern "C" int vxm_malloc(vxm_ctx *ctx, size_t bytes, void **out_dev) {
+    if (!ctx || !out_dev) return VXM_ERR_INVALID_ARG;
+    *out_dev = nullptr;
+    if (bytes == 0) bytes = 256;
+    if (hipMalloc(out_dev, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return vxm_fail(ctx, VXM_ERR_OOM, "hipMalloc of %zu bytes failed", bytes);
+    }
+    return VXM_OK;
+}
+
+extern "C" int vxm_free(vxm_ctx *ctx, void *dev) {
+    if (!ctx) return VXM_ERR_INVALID_ARG;
+    if (dev) VXM_HIP(ctx, hipFree(dev));
+    return VXM_OK;
+}
+
+extern "C" int vxm_memcpy_h2d(vxm_ctx *ctx, void *dst_dev, const void *src_host, size_t bytes) {
+    if (!ctx || (!dst_dev && bytes) || (!src_host && bytes)) return VXM_ERR_INVALID_ARG;
+    VXM_HIP(ctx, hipMemcpyAsync(dst_dev, src_host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return VXM_OK;
+}
+
+extern "C" int vxm_memcpy_d2h(vxm_ctx *ctx, void *dst_host, const void *src_dev, size_t bytes) {
+    if (!ctx || (!dst_host && bytes) || (!src_dev && bytes)) return VXM_ERR_INVALID_ARG;
+    VXM_HIP(ctx, hipMemcpyAsync(dst_host, src_dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return VXM_OK;
+}
+
+int vxm_ensure_act(vxm_ctx *ctx, size_t bytes) {
+    if (ctx->act_bytes >= bytes) return VXM_OK;
+    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->act_buf) VXM_HIP(ctx, hipFree(ctx->act_buf));
+    ctx->act_buf = nullptr;
+    ctx->act_bytes = 0;
+    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+    if (hipMalloc(&ctx->act_buf, want) != hipSuccess) {
+        (void)hipGetLastError();
+        return vxm_fail(ctx, VXM_ERR_OOM, "activation scratch of %zu bytes failed", want);
+    }
+    ctx->act_bytes = want;
+    return VXM_OK;
+}
+
+// ---- weight repack --------------------------------------------------------
+
+// One thread per 34-byte block: split into quants / scales / GEMV scales.
+__global__ void k_repack_q8_0(const uint16_t *__restrict__ src, int64_t nblocks, int64_t nb,
+                              int C, int8_t *__restrict__ qs, uint16_t *__restrict__ d,
+                              uint16_t *__restrict__ dg) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint16_t *blk = src + i * 17;   // 34 bytes = 17 half-words, 2-byte aligned
+    uint32_t w[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) w[j] = (uint32_t)blk[1 + 2 * j] | ((uint32_t)blk[2 + 2 * j] << 16);
+    uint4 *dst = (uint4 *)(qs + i * 32);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    d[i] = blk[0];
+    if (dg) {
+        int64_t row = i / nb, b = i % nb;
+        int64_t c = b / 32, p = b % 32;
+        dg[row * nb + p * C + c] = blk[0];
+    }
+}
+
+__global__ void k_unpack_q8_0(const int8_t *__restrict__ qs, const uint16_t *__restrict__ d,
+                              int64_t nblocks, uint16_t *__restrict__ dst) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint4 *s = (const uint4 *)(qs + i * 32);
+    uint4 a = s[0], b = s[1];
+    uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint16_t *o = dst + i * 17;
+    o[0] = d[i];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        o[1 + 2 * j] = (uint16_t)(w[j] & 0xffffu);
+        o[2 + 2 * j] = (uint16_t)(w[j] >> 16);
+    }
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+extern "C" int vxm_upload_q8_0(vxm_ctx *ctx, const void *gguf_rows, int64_t n_rows, int64_t k,
+                               vxm_weight **out) {
+    if (!ctx || !gguf_rows || !out) return VXM_ERR_INVALID_ARG;
+    *out = nullptr;
+    if (n_rows <= 0 || k <= 0 || k % VXM_QK != 0)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG,
+                        "Q8_0 tensor needs k %% 32 == 0 and positive sizes (n=%lld k=%lld)",
+                        (long long)n_rows, (long long)k);
+    const int64_t nb = k / VXM_QK, nblocks = n_rows * nb;
+    const size_t raw = (size_t)nblocks * VXM_BLOCK_BYTES;
+    const bool gemv_perm = (k % 1024) == 0;
+    const size_t qs_b = align256((size_t)n_rows * k);
+    const size_t d_b = align256((size_t)nblocks * 2);
+    const size_t total = qs_b + d_b + (gemv_perm ? d_b : 0);
+    vxm_weight *w = new vxm_weight();
+    w->n = n_rows;
+    w->k = k;
+    if (hipMalloc(&w->base, total) != hipSuccess) {
+        (void)hipGetLastError();
+        delete w;
+        return vxm_fail(ctx, VXM_ERR_OOM, "weight allocation of %zu bytes failed", total);
+    }
+    w->bytes = total;
+    w->qs = (int8_t *)w->base;
+    w->d = (uint16_t *)((char *)w->base + qs_b);
+    w->dg = gemv_perm ? (uint16_t *)((char *)w->base + qs_b + d_b) : nullptr;
+    void *tmp = nullptr;
+    if (hipMalloc(&tmp, raw) != hipSuccess) {
+        (void)hipGetLastError();
+        hipFree(w->base);
+        delete w;
+        return vxm_fail(ctx, VXM_ERR_OOM, "staging allocation of %zu bytes failed", raw);
+    }
+    int rc = VXM_OK;
+    if (hipMemcpyAsync(tmp, gguf_rows, raw, hipMemcpyHostToDevice, ctx->stream) != hipSuccess) {
+        rc = vxm_fail(ctx, VXM_ERR_BACKEND, "weight upload copy failed");
+    } else {
+        const int threads = 256;
+        const int64_t grid = (nblocks + threads - 1) / threads;
+        hipLaunchKernelGGL(k_repack_q8_0, dim3((unsigned)grid), dim3(threads), 0, ctx->stream,
+                           (const uint16_t *)tmp, nblocks, nb, (int)(k / 1024), w->qs, w->d, w->dg);
+        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess)
+            rc = vxm_fail(ctx, VXM_ERR_BACKEND, "weight repack failed");
+    }
+    hipFree(tmp);
+    if (rc != VXM_OK) {
+        hipFree(w->base);
+        delete w;
+        return rc;
+    }
+    *out = w;
+    return VXM_OK;
+}
+
+extern "C" int vxm_download_q8_0(vxm_ctx *ctx, const vxm_weight *w, void *gguf_rows) {
+    if (!ctx || !w || !gguf_rows) return VXM_ERR_INVALID_ARG;
+    const int64_t nblocks = w->n * (w->k / VXM_QK);
+    const size_t raw = (size_t)nblocks * VXM_BLOCK_BYTES;
+    void *tmp = nullptr;
+    if (hipMalloc(&tmp, raw) != hipSuccess) {
+        (void)hipGetLastError();
+        return vxm_fail(ctx, VXM_ERR_OOM, "download staging of %zu bytes failed", raw);
+    }
+    const int threads = 256;
+    const int64_t grid = (nblocks + threads - 1) / threads;
+    hipLaunchKernelGGL(k_unpack_q8_0, dim3((unsigned)grid), dim3(threads), 0, ctx->stream, w->qs,
+                       w->d, nblocks, (uint16_t *)tmp);
+    int rc = VXM_OK;
+    if (hipGetLastError() != hipSuccess ||
+        hipMemcpyAsync(gguf_rows, tmp, raw, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess)
+        rc = vxm_fail(ctx, VXM_ERR_BACKEND, "weight download failed");
+    hipFree(tmp);
+    return rc;
+}
+
+extern "C" int vxm_weight_free(vxm_ctx *ctx, vxm_weight *w) {
+    if (!ctx) return VXM_ERR_INVALID_ARG;
+    if (!w) return VXM_OK;
+    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (w->base) VXM_HIP(ctx, hipFree(w->base));
+    delete w;
+    return VXM_OK;
+}
+
+extern "C" int64_t vxm_weight_rows(const vxm_weight *w) { return w ? w->n : -1; }
+extern "C" int64_t vxm_weight_cols(const vxm_weight *w) { return w ? w->k : -1; }

@@ -1,0 +1,113 @@
+// vxm_internal.h -- shared definitions of the gfx950 Q8_0 library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/vxm_q8.h"
+
+#define VXM_QK 32
+#define VXM_BLOCK_BYTES 34
+
+struct vxm_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    int quant_variant = VXM_QUANT_X86;
+    int path = VXM_PATH_AUTO;
+    int n_cu = 256;
+    // scratch for internally quantized activations (vxm_mul_mat_q8_0)
+    void *act_buf = nullptr;
+    size_t act_bytes = 0;
+};
+
+// Device layout of a Q8_0 matrix (n_rows x k).  The GGUF row of k/32 34-byte
+// blocks is split so every kernel reads 16-byte aligned, fully coalesced
+// spans:
+//   qs : int8  [n][k]        quants, row-major
+//   d  : fp16  [n][k/32]     scales, row-major (GEMM path, download)
+//   dg : fp16  [n][k/32]     scales permuted for the GEMV path when
+//                            k % 1024 == 0: element p*C + c of a row holds
+//                            block c*32 + p (C = k/1024), so the two lanes
+//                            that share block c*32 + p read their C scales
+//                            from one contiguous span.
+struct vxm_weight {
+    int64_t n = 0, k = 0;
+    int8_t *qs = nullptr;
+    uint16_t *d = nullptr;
+    uint16_t *dg = nullptr;
+    void *base = nullptr;   // single allocation holding qs, d, dg
+    size_t bytes = 0;
+};
+
+int vxm_fail(vxm_ctx *ctx, int code, const char *fmt, ...);
+
+#define VXM_HIP(ctx, call)                                                              \
+    do {                                                                                \
+        hipError_t e_ = (call);                                                         \
+        if (e_ != hipSuccess)                                                           \
+            return vxm_fail((ctx), VXM_ERR_BACKEND, "%s failed: %s (%s:%d)", #call,      \
+                            hipGetErrorString(e_), __FILE__, __LINE__);                 \
+    } while (0)
+
+#define VXM_CHECK_LAUNCH(ctx) VXM_HIP(ctx, hipGetLastError())
+
+// ---- device helpers -------------------------------------------------------
+
+__device__ __forceinline__ float vxm_h2f(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float)v;
+}
+
+__device__ __forceinline__ uint16_t vxm_f2h(float f) {
+    _Float16 v = (_Float16)f;   // v_cvt_f16_f32, round to nearest even
+    uint16_t h;
+    __builtin_memcpy(&h, &v, 2);
+    return h;
+}
+
+// F32 -> BF16 -> F32 with round to nearest even and quiet NaN (the rule of
+// minicpm_bf16_round, src/minicpm4.c:39-42).
+__device__ __forceinline__ float vxm_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    uint32_t h = ((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 64u)
+                                                    : ((u + (0x7fffu + ((u >> 16) & 1u))) >> 16);
+    return __uint_as_float(h << 16);
+}
+
+// sum of 16 int8 x int8 products held as 4 packed dwords each
+__device__ __forceinline__ int vxm_dot16(const int4 a, const int4 b, int acc) {
+    acc = __builtin_amdgcn_sdot4(a.x, b.x, acc, false);
+    acc = __builtin_amdgcn_sdot4(a.y, b.y, acc, false);
+    acc = __builtin_amdgcn_sdot4(a.z, b.z, acc, false);
+    acc = __builtin_amdgcn_sdot4(a.w, b.w, acc, false);
+    return acc;
+}
+
+template <typename T>
+__device__ __forceinline__ T vxm_shfl_xor(T v, int mask) {
+    return __shfl_xor(v, mask, 64);
+}
+
+__device__ __forceinline__ float vxm_wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+__device__ __forceinline__ float vxm_wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
+// ---- host-side launch helpers implemented per translation unit ------------
+int vxm_launch_quantize(vxm_ctx *ctx, const float *x, int64_t M, int64_t K, int variant,
+                        int8_t *xq, uint16_t *xd);
+int vxm_launch_mul_mat(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd,
+                       int64_t M, float *y);
+int vxm_ensure_act(vxm_ctx *ctx, size_t bytes);

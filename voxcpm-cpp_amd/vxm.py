@@ -1,0 +1,249 @@
+"""Python host mirror of the gfx950 Q8_0 library (libvxm_q8.so).
+
+This module binds the C ABI declared in include/vxm_q8.h with ctypes and
+offers the reference's operator vocabulary on top of it: ``mul_mat`` is
+ggml_mul_mat(W_q8_0, x) (src/projections.h:24-29), ``rms_norm`` is
+vcpm_rms_norm (src/minicpm4.c:132-152), and so on.  Device memory is
+torch's (tensors on ``cuda:N``); torch is plumbing here, every computation
+runs in the library's HIP kernels.  Nothing in this module falls back to a
+CPU path: a missing library or a failed call raises ``VxmError``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libvxm_q8.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "vxm_q8.h")
+
+QUANT_REF = 0
+QUANT_X86 = 1
+PATH_AUTO = 0
+PATH_GEMV = 1
+PATH_MFMA = 2
+
+STATUS = {
+    0: "VXM_OK",
+    1: "VXM_ERR_INVALID_ARG",
+    2: "VXM_ERR_IO",
+    3: "VXM_ERR_MODEL_FORMAT",
+    4: "VXM_ERR_UNSUPPORTED_ARCH",
+    5: "VXM_ERR_BACKEND",
+    6: "VXM_ERR_OOM",
+    7: "VXM_ERR_NOT_IMPLEMENTED",
+}
+
+
+class VxmError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"{STATUS.get(code, code)}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+_P = C.c_void_p
+_I64 = C.c_int64
+_I = C.c_int
+_F = C.c_float
+_U64 = C.c_uint64
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "vxm_open": (_I, [_I, C.POINTER(_P)]),
+    "vxm_close": (_I, [_P]),
+    "vxm_sync": (_I, [_P]),
+    "vxm_get_stream": (_P, [_P]),
+    "vxm_last_error": (C.c_char_p, [_P]),
+    "vxm_set_quant_variant": (_I, [_P, _I]),
+    "vxm_set_path": (_I, [_P, _I]),
+    "vxm_malloc": (_I, [_P, C.c_size_t, C.POINTER(_P)]),
+    "vxm_free": (_I, [_P, _P]),
+    "vxm_memcpy_h2d": (_I, [_P, _P, _P, C.c_size_t]),
+    "vxm_memcpy_d2h": (_I, [_P, _P, _P, C.c_size_t]),
+    "vxm_upload_q8_0": (_I, [_P, _P, _I64, _I64, C.POINTER(_P)]),
+    "vxm_download_q8_0": (_I, [_P, _P, _P]),
+    "vxm_weight_free": (_I, [_P, _P]),
+    "vxm_weight_rows": (_I64, [_P]),
+    "vxm_weight_cols": (_I64, [_P]),
+    "vxm_quantize_q8_0": (_I, [_P, _P, _I64, _I64, _I, _P, _P]),
+    "vxm_mul_mat_q8_0": (_I, [_P, _P, _P, _I64, _P]),
+    "vxm_mul_mat_q8_0_q8_0": (_I, [_P, _P, _P, _P, _I64, _P]),
+    "vxm_block_dots_q8_0": (_I, [_P, _P, _P, _P, _I64, _P]),
+    "vxm_host_quantize_q8_0": (_I, [_P, _I64, _I64, _P]),
+    "vxm_host_randn": (_I, [_U64, _U64, _I64, _F, _F, _P]),
+}
+
+
+def header_functions(path=HEADER):
+    """Names of every function the public header declares."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vxm_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib():
+    """Load libvxm_q8.so (built in-tree); raise if it is missing."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise VxmError(5, f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _ptr(t):
+    """Device (or host numpy) pointer of a tensor/array, None for None."""
+    if t is None:
+        return None
+    if hasattr(t, "data_ptr"):
+        return C.c_void_p(t.data_ptr())
+    if hasattr(t, "ctypes"):
+        return t.ctypes.data_as(C.c_void_p)
+    return C.c_void_p(int(t))
+
+
+class Context:
+    """One device + one stream (vxm_open); closes on ``close()``."""
+
+    def __init__(self, device=0):
+        L = lib()
+        h = C.c_void_p()
+        rc = L.vxm_open(device, C.byref(h))
+        if rc:
+            raise VxmError(rc, L.vxm_last_error(None).decode())
+        self.h = h
+        self.device = device
+        self._stream = None
+
+    def check(self, rc):
+        if rc:
+            raise VxmError(rc, lib().vxm_last_error(self.h).decode())
+
+    def close(self):
+        if self.h:
+            self.check(lib().vxm_close(self.h))
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def sync(self):
+        self.check(lib().vxm_sync(self.h))
+
+    @property
+    def stream_handle(self):
+        return lib().vxm_get_stream(self.h)
+
+    def torch_stream(self):
+        """The context's HIP stream as a torch ExternalStream (for events)."""
+        import torch
+
+        if self._stream is None:
+            self._stream = torch.cuda.ExternalStream(self.stream_handle, device=f"cuda:{self.device}")
+        return self._stream
+
+    def set_quant_variant(self, v):
+        self.check(lib().vxm_set_quant_variant(self.h, v))
+
+    def set_path(self, p):
+        self.check(lib().vxm_set_path(self.h, p))
+
+    # ---- weights ----
+    def upload_q8_0(self, gguf_rows, n_rows, k):
+        """gguf_rows: host numpy uint8 array of n_rows*(k/32)*34 bytes."""
+        import numpy as np
+
+        buf = np.ascontiguousarray(gguf_rows, dtype=np.uint8)
+        if buf.size != n_rows * (k // 32) * 34:
+            raise VxmError(1, f"expected {n_rows * (k // 32) * 34} bytes, got {buf.size}")
+        h = C.c_void_p()
+        self.check(lib().vxm_upload_q8_0(self.h, _ptr(buf), n_rows, k, C.byref(h)))
+        return Q8Weight(self, h, n_rows, k)
+
+    # ---- ops (device tensors) ----
+    def quantize_q8_0(self, x, variant=QUANT_X86, xq=None, xd=None):
+        import torch
+
+        M, K = x.shape
+        xq = torch.empty((M, K), dtype=torch.int8, device=x.device) if xq is None else xq
+        xd = torch.empty((M, K // 32), dtype=torch.int16, device=x.device) if xd is None else xd
+        self.check(lib().vxm_quantize_q8_0(self.h, _ptr(x), M, K, variant, _ptr(xq), _ptr(xd)))
+        return xq, xd
+
+    def mul_mat(self, w, x, y=None):
+        """ggml_mul_mat(W, x): x fp32 [M][K] -> y fp32 [M][N]."""
+        import torch
+
+        M = x.shape[0]
+        y = torch.empty((M, w.n), dtype=torch.float32, device=x.device) if y is None else y
+        self.check(lib().vxm_mul_mat_q8_0(self.h, w.h, _ptr(x), M, _ptr(y)))
+        return y
+
+    def mul_mat_q8(self, w, xq, xd, y=None):
+        import torch
+
+        M = xq.shape[0]
+        y = torch.empty((M, w.n), dtype=torch.float32, device=xq.device) if y is None else y
+        self.check(lib().vxm_mul_mat_q8_0_q8_0(self.h, w.h, _ptr(xq), _ptr(xd), M, _ptr(y)))
+        return y
+
+    def block_dots(self, w, xq, xd):
+        import torch
+
+        M = xq.shape[0]
+        out = torch.empty((M, w.n, w.k // 32), dtype=torch.int32, device=xq.device)
+        self.check(lib().vxm_block_dots_q8_0(self.h, w.h, _ptr(xq), _ptr(xd), M, _ptr(out)))
+        return out
+
+
+class Q8Weight:
+    def __init__(self, ctx, h, n, k):
+        self.ctx, self.h, self.n, self.k = ctx, h, n, k
+
+    def download(self):
+        import numpy as np
+
+        out = np.empty(self.n * (self.k // 32) * 34, dtype=np.uint8)
+        self.ctx.check(lib().vxm_download_q8_0(self.ctx.h, self.h, _ptr(out)))
+        return out
+
+    def free(self):
+        if self.h:
+            self.ctx.check(lib().vxm_weight_free(self.ctx.h, self.h))
+            self.h = None
+
+
+# ---- host helpers (no device work) ----
+
+def host_randn(seed, n, mean=0.0, std=1.0, offset=0):
+    import numpy as np
+
+    out = np.empty(n, dtype=np.float32)
+    rc = lib().vxm_host_randn(seed, offset, n, mean, std, _ptr(out))
+    if rc:
+        raise VxmError(rc, "vxm_host_randn")
+    return out
+
+
+def host_quantize_q8_0(x):
+    """GGUF Q8_0 rows of a float32 [rows][k] array (weight rule)."""
+    import numpy as np
+
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    out = np.empty(rows * (k // 32) * 34, dtype=np.uint8)
+    rc = lib().vxm_host_quantize_q8_0(_ptr(x), rows, k, _ptr(out))
+    if rc:
+        raise VxmError(rc, "vxm_host_quantize_q8_0")
+    return out
