@@ -100,6 +100,71 @@ int vxm_mul_mat_q8_0_q8_0(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq_de
 int vxm_block_dots_q8_0(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq_dev,
                         const uint16_t *xd_dev, int64_t M, int32_t *out_dev);
 
+/* ---- block ops -----------------------------------------------------------
+ * vcpm_rms_norm (src/minicpm4.c:132-152) on rows x [rows][n]: y = BF16(BF16(
+ * x / sqrt(mean(x^2) + eps)) * gain).  gain may be NULL (plain ggml_rms_norm
+ * + BF16).  If xq/xd are non-NULL the output is also quantized to Q8_0 with
+ * the context's activation rule (the input of the next ggml_mul_mat). */
+int vxm_rms_norm(vxm_ctx *ctx, const float *x_dev, const float *gain_dev, int64_t rows, int64_t n,
+                 float eps, float *y_dev, int8_t *xq_dev, uint16_t *xd_dev);
+
+/* ---- MiniCPM4 stack ------------------------------------------------------
+ * Mirrors vcpm_minicpm4_config (src/minicpm4.h:14-27). */
+typedef struct vxm_minicpm4_config {
+    int32_t hidden_size;
+    int32_t n_layers;
+    int32_t n_heads;
+    int32_t n_kv_heads;
+    int32_t intermediate_size;
+    int32_t head_dim;
+    float   rms_norm_eps;
+    int32_t rope_theta;
+    int32_t no_rope;          /* 1 for the residual LM (RALM), src/ralm.c:15-29 */
+    float   scale_depth;      /* DeepNorm: residual scale = scale_depth/sqrt(n_layers) if > 0 */
+    /* head_dim/2 rope frequency factors (host memory), or NULL for the
+     * reference rule: the VoxCPM2 LongRoPE short factors when head_dim == 128
+     * (src/minicpm4.c:49-66,183-190), none otherwise. */
+    const float *rope_freq_factors;
+} vxm_minicpm4_config;
+
+/* One block's weights in host memory: GGUF Q8_0 rows for the seven
+ * projections (vcpm_layer_weights, src/transformer.h:27-48) and F32 gains. */
+typedef struct vxm_layer_weights_q8_0 {
+    const void  *q_proj, *k_proj, *v_proj, *o_proj, *gate_proj, *up_proj, *down_proj;
+    const float *input_layernorm, *post_attention_layernorm;
+} vxm_layer_weights_q8_0;
+
+typedef struct vxm_minicpm4 vxm_minicpm4;
+typedef struct vxm_kv_cache vxm_kv_cache;
+
+/* Uploads cfg->n_layers blocks (+ optional final norm, host F32 [hidden]). */
+int vxm_minicpm4_create(vxm_ctx *ctx, const vxm_minicpm4_config *cfg,
+                        const vxm_layer_weights_q8_0 *layers, const float *final_norm,
+                        vxm_minicpm4 **out);
+int vxm_minicpm4_free(vxm_minicpm4 *m);
+
+/* f16 KV cache (the reference keeps F32, src/minicpm4.c:93-122): per layer,
+ * K and V are [n_kv_heads][capacity][head_dim]. */
+int     vxm_kv_cache_create(vxm_ctx *ctx, int32_t n_layers, int32_t n_kv_heads, int32_t head_dim,
+                            int32_t capacity, vxm_kv_cache **out);
+int     vxm_kv_cache_free(vxm_kv_cache *kv);
+int     vxm_kv_cache_reset(vxm_kv_cache *kv);                 /* n_used = 0 (vcpm_gen_reset) */
+int     vxm_kv_cache_set_used(vxm_kv_cache *kv, int32_t n_used);
+int32_t vxm_kv_cache_used(const vxm_kv_cache *kv);
+int     vxm_kv_cache_layer(vxm_kv_cache *kv, int32_t layer, uint16_t **k_dev, uint16_t **v_dev);
+
+/* vcpm_minicpm4_block (src/minicpm4.c:467-532) for one layer, in place on
+ * x [n_tokens][hidden].  Causal: tokens take positions pos.. and are appended
+ * to the cache at the same rows.  no_causal: attention over the n_tokens
+ * fresh tokens only (LocDiT/LocEnc use), positions from pos, cache untouched. */
+int vxm_minicpm4_block(vxm_minicpm4 *m, vxm_kv_cache *kv, int32_t layer, float *x_dev,
+                       int64_t n_tokens, int32_t pos, int no_causal);
+/* vcpm_minicpm4_forward (src/minicpm4.c:536-572): all layers (causal) and
+ * the final norm, in place on x [n_tokens][hidden]; positions and cache rows
+ * pos..pos+n_tokens-1; sets the cache's n_used to pos + n_tokens. */
+int vxm_minicpm4_forward(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x_dev, int64_t n_tokens,
+                         int32_t pos);
+
 /* ---- host helpers (no device work) --------------------------------------
  * GGUF Q8_0 quantization of F32 rows with the weight rule of
  * ggml_quantize_chunk (tools/quantize.c:292): d = amax/127 (fp16),

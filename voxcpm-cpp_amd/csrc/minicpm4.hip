@@ -1,0 +1,351 @@
+// minicpm4.hip -- the MiniCPM4 block / stack on gfx950 (vcpm_minicpm4_block
+// and vcpm_minicpm4_forward, src/minicpm4.c:467-572) driven as a sequence of
+// stream-ordered kernels, plus the f16 KV cache.
+//
+// Device layout of one block:
+//   wqkv : Q8_0 [(n_heads + 2 n_kv) * head_dim][hidden]   q rows, then k, then v
+//   wo   : Q8_0 [hidden][n_heads * head_dim]
+//   wgu  : Q8_0 [2 * ffn][hidden]                          gate rows, then up
+//   wd   : Q8_0 [hidden][ffn]
+//   g_in, g_post : fp32 [hidden]
+// Kernel sequence per layer (M tokens):
+//   rms_norm(+residual of the previous layer) -> Q8_0 x
+//   QKV matmul -> rope + BF16 + f16 KV append -> attention -> Q8_0
+//   O matmul -> residual + post norm -> Q8_0
+//   gate/up matmul -> SwiGLU + Q8_0 -> down matmul (residual folded into the
+//   next layer's norm, or the final norm).
+#include <math.h>
+
+#include <vector>
+
+#include "vxm_model.h"
+
+// LongRoPE short factors of the VoxCPM2 lm_config (src/minicpm4.c:49-66):
+// model constants, one per rotary pair, applied when head_dim == 128.
+static const float kVoxcpm2RopeShortFactors[64] = {
+    0.9977997200f,  1.0146582960f,  1.0349680405f,  1.0594292461f,  1.0888815017f,  1.1243301355f,
+    1.1669771036f,  1.2182568067f,  1.2798772354f,  1.3538666752f,  1.4426259040f,  1.5489853360f,
+    1.6762658237f,  1.8283407612f,  2.0096956086f,  2.2254789275f,  2.4815363797f,  2.7844159346f,
+    3.1413289096f,  3.5600478448f,  4.0487193801f,  4.6155695421f,  5.2684819497f,  6.0144385919f,
+    6.8588300492f,  7.8046682500f,  8.8517684937f,  9.9960050583f,  11.2287664413f, 12.5367574692f,
+    13.9022579193f, 15.3038854599f, 16.7178382874f, 18.1194648743f, 19.4849643707f, 20.7929573059f,
+    22.0257186890f, 23.1699542999f, 24.2170543671f, 25.1628932953f, 26.0072841644f, 26.7532405853f,
+    27.4061527252f, 27.9730033875f, 28.4616756439f, 28.8803939819f, 29.2373065948f, 29.5401859283f,
+    29.7962436676f, 30.0120277405f, 30.1933822632f, 30.3454570770f, 30.4727382660f, 30.5790977478f,
+    30.6678562164f, 30.7418460846f, 30.8034667969f, 30.8547458649f, 30.8973922729f, 30.9328403473f,
+    30.9622936249f, 30.9867553711f, 31.0070648193f, 31.0239238739f,
+};
+
+// ---------------------------------------------------------------------------
+// workspace
+// ---------------------------------------------------------------------------
+int vxm_ws_ensure(vxm_ctx *ctx, vxm_workspace &ws, int64_t M, int64_t H, int64_t qd, int64_t kvd, int64_t F,
+                  int64_t local_kv) {
+    const int64_t kmax = std::max(std::max(H, qd), F);
+    struct Part { size_t bytes; void **dst; };
+    std::vector<Part> parts = {
+        {(size_t)(M * kmax), (void **)&ws.xq},
+        {(size_t)(M * (kmax / 32) * 2), (void **)&ws.xd},
+        {(size_t)(M * (qd + 2 * kvd) * 4), (void **)&ws.qkv},
+        {(size_t)(M * qd * 4), (void **)&ws.q},
+        {(size_t)(M * qd * 4), (void **)&ws.att},
+        {(size_t)(M * H * 4), (void **)&ws.o},
+        {(size_t)(M * 2 * F * 4), (void **)&ws.gu},
+        {(size_t)(M * H * 4), (void **)&ws.dn},
+        {(size_t)(local_kv * 2), (void **)&ws.lk},
+        {(size_t)(local_kv * 2), (void **)&ws.lv},
+    };
+    size_t total = 0;
+    for (auto &p : parts) total += (p.bytes + 255) & ~(size_t)255;
+    if (total <= ws.bytes) {
+        char *b = (char *)ws.base;
+        for (auto &p : parts) { *p.dst = b; b += (p.bytes + 255) & ~(size_t)255; }
+        return VXM_OK;
+    }
+    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ws.base) VXM_HIP(ctx, hipFree(ws.base));
+    ws.base = nullptr;
+    ws.bytes = 0;
+    if (hipMalloc(&ws.base, total) != hipSuccess) {
+        (void)hipGetLastError();
+        return vxm_fail(ctx, VXM_ERR_OOM, "workspace of %zu bytes failed", total);
+    }
+    ws.bytes = total;
+    char *b = (char *)ws.base;
+    for (auto &p : parts) { *p.dst = b; b += (p.bytes + 255) & ~(size_t)255; }
+    return VXM_OK;
+}
+
+void vxm_ws_free(vxm_workspace &ws) {
+    if (ws.base) (void)hipFree(ws.base);
+    ws = vxm_workspace();
+}
+
+// ---------------------------------------------------------------------------
+// block weights
+// ---------------------------------------------------------------------------
+static int upload_concat(vxm_ctx *ctx, const void *a, int64_t na, const void *b, int64_t nb_rows, const void *c,
+                         int64_t nc, int64_t k, vxm_weight **out) {
+    const size_t rb = (size_t)(k / 32) * 34;
+    std::vector<uint8_t> buf(rb * (size_t)(na + nb_rows + nc));
+    memcpy(buf.data(), a, rb * na);
+    if (b) memcpy(buf.data() + rb * na, b, rb * nb_rows);
+    if (c) memcpy(buf.data() + rb * (na + nb_rows), c, rb * nc);
+    return vxm_upload_q8_0(ctx, buf.data(), na + nb_rows + nc, k, out);
+}
+
+static int upload_f32(vxm_ctx *ctx, const float *src, int64_t n, float **out) {
+    *out = nullptr;
+    if (!src) return VXM_OK;
+    if (hipMalloc((void **)out, n * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        return vxm_fail(ctx, VXM_ERR_OOM, "gain upload failed");
+    }
+    VXM_HIP(ctx, hipMemcpy(*out, src, n * 4, hipMemcpyHostToDevice));
+    return VXM_OK;
+}
+
+int vxm_block_upload(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_layer_weights_q8_0 &w, vxm_block &b) {
+    if (!w.q_proj || !w.k_proj || !w.v_proj || !w.o_proj || !w.gate_proj || !w.up_proj || !w.down_proj)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "layer weights: a projection is NULL");
+    const int64_t qd = (int64_t)d.nh * d.hd, kvd = (int64_t)d.nkv * d.hd;
+    int rc;
+    if ((rc = upload_concat(ctx, w.q_proj, qd, w.k_proj, kvd, w.v_proj, kvd, d.H, &b.wqkv))) return rc;
+    if ((rc = vxm_upload_q8_0(ctx, w.o_proj, d.H, qd, &b.wo))) return rc;
+    if ((rc = upload_concat(ctx, w.gate_proj, d.F, w.up_proj, d.F, nullptr, 0, d.H, &b.wgu))) return rc;
+    if ((rc = vxm_upload_q8_0(ctx, w.down_proj, d.H, d.F, &b.wd))) return rc;
+    if ((rc = upload_f32(ctx, w.input_layernorm, d.H, &b.g_in))) return rc;
+    if ((rc = upload_f32(ctx, w.post_attention_layernorm, d.H, &b.g_post))) return rc;
+    return VXM_OK;
+}
+
+void vxm_block_free(vxm_ctx *ctx, vxm_block &b) {
+    vxm_weight_free(ctx, b.wqkv);
+    vxm_weight_free(ctx, b.wo);
+    vxm_weight_free(ctx, b.wgu);
+    vxm_weight_free(ctx, b.wd);
+    if (b.g_in) (void)hipFree(b.g_in);
+    if (b.g_post) (void)hipFree(b.g_post);
+    b = vxm_block();
+}
+
+int vxm_rope_setup(vxm_ctx *ctx, int hd, int32_t theta, const float *ff_host, float **ff_dev, float *theta_scale) {
+    // ggml_rope_ext: theta_scale = powf(freq_base, -2.0f / n_dims), on the host
+    *theta_scale = powf((float)theta, -2.0f / (float)hd);
+    const float *src = ff_host ? ff_host : (hd == 128 ? kVoxcpm2RopeShortFactors : nullptr);
+    *ff_dev = nullptr;
+    if (!src) return VXM_OK;
+    return upload_f32(ctx, src, hd / 2, ff_dev);
+}
+
+// ---------------------------------------------------------------------------
+// one block over M tokens (attention half and MLP half)
+// ---------------------------------------------------------------------------
+// x: [M][H] residual stream.  On entry xq/xd already hold Q8_0(rms_norm_in(x)).
+// Leaves ws.dn = raw down projection; the caller folds it into x.
+int vxm_block_run(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_block &b, vxm_workspace &ws, float *x,
+                  int64_t M, const vxm_attn_site &site) {
+    const int64_t qd = (int64_t)d.nh * d.hd, kvd = (int64_t)d.nkv * d.hd;
+    const int var = ctx->quant_variant;
+    int rc;
+    if ((rc = vxm_launch_mul_mat(ctx, b.wqkv, ws.xq, ws.xd, M, ws.qkv))) return rc;
+    if ((rc = vxm_launch_rope_kv(ctx, ws.qkv, M, d.nh, d.nkv, d.hd, site.pos0, site.S, d.theta_scale, d.ff,
+                                 d.no_rope, ws.q, site.kc, site.vc, site.cap, site.seg_stride, site.cache_pos0)))
+        return rc;
+    if ((rc = vxm_launch_attention(ctx, ws.q, site.kc, site.vc, ws.att, M, d.nh, d.nkv, d.hd, site.cap,
+                                   site.seg_stride, site.S, site.cache_pos0, site.causal)))
+        return rc;
+    if ((rc = vxm_launch_quantize(ctx, ws.att, M, qd, var, ws.xq, ws.xd))) return rc;
+    if ((rc = vxm_launch_mul_mat(ctx, b.wo, ws.xq, ws.xd, M, ws.o))) return rc;
+    // x = bf16(x + scale*bf16(o)); post-attention norm -> Q8_0
+    if ((rc = vxm_launch_rmsnorm(ctx, x, ws.o, d.res_scale, b.g_post, M, d.H, d.eps, nullptr, ws.xq, ws.xd, var)))
+        return rc;
+    if ((rc = vxm_launch_mul_mat(ctx, b.wgu, ws.xq, ws.xd, M, ws.gu))) return rc;
+    if ((rc = vxm_launch_swiglu_quant(ctx, ws.gu, M, d.F, 2 * d.F, ws.xq, ws.xd, nullptr, var))) return rc;
+    if ((rc = vxm_launch_mul_mat(ctx, b.wd, ws.xq, ws.xd, M, ws.dn))) return rc;
+    (void)kvd;
+    return VXM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" int vxm_rms_norm(vxm_ctx *ctx, const float *x_dev, const float *gain_dev, int64_t rows, int64_t n,
+                            float eps, float *y_dev, int8_t *xq_dev, uint16_t *xd_dev) {
+    if (!ctx) return VXM_ERR_INVALID_ARG;
+    if (!x_dev || (!y_dev && !xq_dev) || (xq_dev && !xd_dev) || rows < 0)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "rms_norm: bad arguments");
+    return vxm_launch_rmsnorm(ctx, (float *)x_dev, nullptr, 1.0f, gain_dev, rows, n, eps, y_dev, xq_dev, xd_dev,
+                              ctx->quant_variant);
+}
+
+extern "C" int vxm_kv_cache_create(vxm_ctx *ctx, int32_t n_layers, int32_t n_kv_heads, int32_t head_dim,
+                                   int32_t capacity, vxm_kv_cache **out) {
+    if (!ctx || !out) return VXM_ERR_INVALID_ARG;
+    *out = nullptr;
+    if (n_layers <= 0 || n_kv_heads <= 0 || head_dim <= 0 || capacity <= 0)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "kv cache: sizes must be positive");
+    vxm_kv_cache *kv = new vxm_kv_cache();
+    kv->ctx = ctx;
+    kv->n_layers = n_layers;
+    kv->nkv = n_kv_heads;
+    kv->hd = head_dim;
+    kv->cap = capacity;
+    kv->layer_elems = (int64_t)n_kv_heads * capacity * head_dim;
+    const size_t bytes = (size_t)kv->layer_elems * 2 * 2 * n_layers;
+    if (hipMalloc(&kv->base, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        delete kv;
+        return vxm_fail(ctx, VXM_ERR_OOM, "kv cache of %zu bytes failed", bytes);
+    }
+    VXM_HIP(ctx, hipMemsetAsync(kv->base, 0, bytes, ctx->stream));
+    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    *out = kv;
+    return VXM_OK;
+}
+
+extern "C" int vxm_kv_cache_free(vxm_kv_cache *kv) {
+    if (!kv) return VXM_ERR_INVALID_ARG;
+    (void)hipStreamSynchronize(kv->ctx->stream);
+    if (kv->base) (void)hipFree(kv->base);
+    delete kv;
+    return VXM_OK;
+}
+
+extern "C" int vxm_kv_cache_reset(vxm_kv_cache *kv) {
+    if (!kv) return VXM_ERR_INVALID_ARG;
+    kv->n_used = 0;
+    return VXM_OK;
+}
+
+extern "C" int vxm_kv_cache_set_used(vxm_kv_cache *kv, int32_t n_used) {
+    if (!kv) return VXM_ERR_INVALID_ARG;
+    if (n_used < 0 || n_used > kv->cap)
+        return vxm_fail(kv->ctx, VXM_ERR_INVALID_ARG, "kv cache: n_used %d outside [0, %d]", n_used, kv->cap);
+    kv->n_used = n_used;
+    return VXM_OK;
+}
+
+extern "C" int32_t vxm_kv_cache_used(const vxm_kv_cache *kv) { return kv ? kv->n_used : -1; }
+
+extern "C" int vxm_kv_cache_layer(vxm_kv_cache *kv, int32_t layer, uint16_t **k_dev, uint16_t **v_dev) {
+    if (!kv || !k_dev || !v_dev) return VXM_ERR_INVALID_ARG;
+    if (layer < 0 || layer >= kv->n_layers)
+        return vxm_fail(kv->ctx, VXM_ERR_INVALID_ARG, "kv cache: layer %d out of range", layer);
+    *k_dev = kv->k(layer);
+    *v_dev = kv->v(layer);
+    return VXM_OK;
+}
+
+extern "C" int vxm_minicpm4_create(vxm_ctx *ctx, const vxm_minicpm4_config *cfg, const vxm_layer_weights_q8_0 *layers,
+                                   const float *final_norm, vxm_minicpm4 **out) {
+    if (!ctx || !cfg || !layers || !out) return VXM_ERR_INVALID_ARG;
+    *out = nullptr;
+    const vxm_minicpm4_config &c = *cfg;
+    if (c.n_layers <= 0 || c.hidden_size <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 ||
+        c.intermediate_size <= 0 || c.n_heads % c.n_kv_heads || c.head_dim % 2 || c.hidden_size % 32 ||
+        c.intermediate_size % 32 || (c.n_heads * c.head_dim) % 32 || c.head_dim > 256)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "minicpm4 config: unsupported sizes");
+    vxm_minicpm4 *m = new vxm_minicpm4();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->cfg.rope_freq_factors = nullptr;
+    vxm_block_dims &d = m->dims;
+    d.H = c.hidden_size;
+    d.nh = c.n_heads;
+    d.nkv = c.n_kv_heads;
+    d.hd = c.head_dim;
+    d.F = c.intermediate_size;
+    d.eps = c.rms_norm_eps;
+    d.no_rope = c.no_rope;
+    d.res_scale = (c.scale_depth > 0.0f) ? c.scale_depth / sqrtf((float)c.n_layers) : 1.0f;
+    int rc = vxm_rope_setup(ctx, d.hd, c.rope_theta, c.rope_freq_factors, &d.ff, &d.theta_scale);
+    m->blocks.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers && rc == VXM_OK; l++) rc = vxm_block_upload(ctx, d, layers[l], m->blocks[l]);
+    if (rc == VXM_OK) rc = upload_f32(ctx, final_norm, d.H, &m->final_norm);
+    if (rc != VXM_OK) {
+        vxm_minicpm4_free(m);
+        return rc;
+    }
+    *out = m;
+    return VXM_OK;
+}
+
+extern "C" int vxm_minicpm4_free(vxm_minicpm4 *m) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    (void)hipStreamSynchronize(m->ctx->stream);
+    for (auto &b : m->blocks) vxm_block_free(m->ctx, b);
+    if (m->final_norm) (void)hipFree(m->final_norm);
+    if (m->dims.ff) (void)hipFree(m->dims.ff);
+    vxm_ws_free(m->ws);
+    delete m;
+    return VXM_OK;
+}
+
+static int check_run(vxm_minicpm4 *m, vxm_kv_cache *kv, const float *x, int64_t M, int32_t pos, int causal) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    if (!x || M <= 0 || pos < 0) return vxm_fail(m->ctx, VXM_ERR_INVALID_ARG, "minicpm4: bad x / n_tokens / pos");
+    if (causal) {
+        if (!kv) return vxm_fail(m->ctx, VXM_ERR_INVALID_ARG, "minicpm4: causal run needs a kv cache");
+        if (kv->n_layers < m->cfg.n_layers || kv->nkv != m->dims.nkv || kv->hd != m->dims.hd)
+            return vxm_fail(m->ctx, VXM_ERR_INVALID_ARG, "minicpm4: kv cache shape does not match the model");
+        if ((int64_t)pos + M > kv->cap)
+            return vxm_fail(m->ctx, VXM_ERR_INVALID_ARG, "minicpm4: pos %d + %lld tokens exceeds capacity %d", pos,
+                            (long long)M, kv->cap);
+    }
+    return VXM_OK;
+}
+
+extern "C" int vxm_minicpm4_block(vxm_minicpm4 *m, vxm_kv_cache *kv, int32_t layer, float *x_dev, int64_t n_tokens,
+                                  int32_t pos, int no_causal) {
+    int rc = check_run(m, kv, x_dev, n_tokens, pos, !no_causal);
+    if (rc) return rc;
+    if (layer < 0 || layer >= m->cfg.n_layers)
+        return vxm_fail(m->ctx, VXM_ERR_INVALID_ARG, "minicpm4: layer %d out of range", layer);
+    vxm_ctx *ctx = m->ctx;
+    const vxm_block_dims &d = m->dims;
+    const int64_t qd = (int64_t)d.nh * d.hd, kvd = (int64_t)d.nkv * d.hd;
+    const int64_t local = no_causal ? (int64_t)d.nkv * n_tokens * d.hd : 0;
+    if ((rc = vxm_ws_ensure(ctx, m->ws, n_tokens, d.H, qd, kvd, d.F, local))) return rc;
+    vxm_attn_site site;
+    if (no_causal) {
+        site = vxm_attn_site{m->ws.lk, m->ws.lv, (int)n_tokens, 0, (int)n_tokens, pos, 0, 0};
+    } else {
+        site = vxm_attn_site{kv->k(layer), kv->v(layer), kv->cap, 0, (int)n_tokens, pos, pos, 1};
+    }
+    const vxm_block &b = m->blocks[layer];
+    if ((rc = vxm_launch_rmsnorm(ctx, x_dev, nullptr, 1.0f, b.g_in, n_tokens, d.H, d.eps, nullptr, m->ws.xq,
+                                 m->ws.xd, ctx->quant_variant)))
+        return rc;
+    if ((rc = vxm_block_run(ctx, d, b, m->ws, x_dev, n_tokens, site))) return rc;
+    return vxm_launch_residual(ctx, x_dev, m->ws.dn, d.res_scale, n_tokens * d.H);
+}
+
+extern "C" int vxm_minicpm4_forward(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x_dev, int64_t n_tokens, int32_t pos) {
+    int rc = check_run(m, kv, x_dev, n_tokens, pos, 1);
+    if (rc) return rc;
+    vxm_ctx *ctx = m->ctx;
+    const vxm_block_dims &d = m->dims;
+    const int64_t qd = (int64_t)d.nh * d.hd, kvd = (int64_t)d.nkv * d.hd;
+    if ((rc = vxm_ws_ensure(ctx, m->ws, n_tokens, d.H, qd, kvd, d.F, 0))) return rc;
+    const int var = ctx->quant_variant;
+    for (int l = 0; l < m->cfg.n_layers; l++) {
+        const vxm_block &b = m->blocks[l];
+        // residual of the previous layer's MLP folded into this layer's input norm
+        if ((rc = vxm_launch_rmsnorm(ctx, x_dev, l ? m->ws.dn : nullptr, d.res_scale, b.g_in, n_tokens, d.H, d.eps,
+                                     nullptr, m->ws.xq, m->ws.xd, var)))
+            return rc;
+        vxm_attn_site site{kv->k(l), kv->v(l), kv->cap, 0, (int)n_tokens, pos, pos, 1};
+        if ((rc = vxm_block_run(ctx, d, b, m->ws, x_dev, n_tokens, site))) return rc;
+    }
+    // last residual + final norm (in place), or the residual alone
+    if (m->final_norm) {
+        if ((rc = vxm_launch_rmsnorm(ctx, x_dev, m->ws.dn, d.res_scale, m->final_norm, n_tokens, d.H, d.eps, x_dev,
+                                     nullptr, nullptr, var)))
+            return rc;
+    } else if ((rc = vxm_launch_residual(ctx, x_dev, m->ws.dn, d.res_scale, n_tokens * d.H))) {
+        return rc;
+    }
+    kv->n_used = pos + (int32_t)n_tokens;
+    return VXM_OK;
+}

@@ -1,0 +1,370 @@
+// ops.hip -- the non-matmul pieces of the MiniCPM4 block on gfx950:
+// RMSNorm (+ residual, + Q8_0 activation quantization), NEOX RoPE with the
+// f16 KV-cache append, softmax attention over the f16 cache, SwiGLU (+ Q8_0
+// quantization).  Every rounding step follows the reference graph
+// (src/minicpm4.c) as restated by the oracle; contraction is off, so each
+// a*b+c below rounds twice like the reference's scalar code.
+#include "vxm_ops.h"
+
+// ---------------------------------------------------------------------------
+// block-wide reductions (blockDim.x == 256)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double block_sum_f64(double v, double *sh) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += sh[i];
+    return t;
+}
+
+__device__ __forceinline__ float block_max_f32(float v, float *sh) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    float t = sh[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) t = fmaxf(t, sh[i]);
+    return t;
+}
+
+// Quantize 32 values held 8 per lane by 4 consecutive lanes (lane & 3 = part)
+// with the x86 rule (id = 127/amax, round half even) or the _ref rule.
+__device__ __forceinline__ void quant_block_4lanes(const float v[8], int variant, int8_t *q8,
+                                                   uint16_t *dout, bool write_d) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    const float d = __fdiv_rn(amax, 127.0f);
+    float id;
+    if (variant == VXM_QUANT_X86) id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    else id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        float q = variant == VXM_QUANT_X86 ? rintf(v[i] * id) : roundf(v[i] * id);
+        q = fminf(fmaxf(q, -128.0f), 127.0f);
+        const uint32_t b = (uint32_t)(uint8_t)(int8_t)(int)q;
+        if (i < 4) lo |= b << (8 * i);
+        else hi |= b << (8 * (i - 4));
+    }
+    *(uint2 *)q8 = make_uint2(lo, hi);
+    if (write_d) *dout = vxm_f2h(d);
+}
+
+// ---------------------------------------------------------------------------
+// [h = bf16(h + scale * bf16(delta))]; y = vcpm_rms_norm(h) (src/minicpm4.c:132-152):
+// ggml_rms_norm (sum of fp32 squares in double, mean = (float)(sum/n),
+// scale = 1/sqrtf(mean + eps)), BF16, * gain, BF16.  Outputs y (fp32, if
+// non-null) and its Q8_0 quantization (xq/xd, if non-null).
+// One workgroup of 256 threads per row; n % 8 == 0 and n <= 8 * 256 * VXM_NORM_CHUNKS.
+// ---------------------------------------------------------------------------
+#define VXM_NORM_CHUNKS 4
+__global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const float *__restrict__ delta,
+                                                 float res_scale, const float *__restrict__ gain, int n,
+                                                 float eps, float *__restrict__ y, int8_t *__restrict__ xq,
+                                                 uint16_t *__restrict__ xd, int variant) {
+    __shared__ double shd[4];
+    const int row = blockIdx.x;
+    float *hr = h + (int64_t)row * n;
+    const float *dr = delta ? delta + (int64_t)row * n : nullptr;
+    float v[VXM_NORM_CHUNKS][8];
+    double ss = 0.0;
+#pragma unroll
+    for (int c = 0; c < VXM_NORM_CHUNKS; c++) {
+        const int base = (c * 256 + threadIdx.x) * 8;
+        if (base < n) {
+            float4 a = *(const float4 *)(hr + base), b = *(const float4 *)(hr + base + 4);
+            v[c][0] = a.x; v[c][1] = a.y; v[c][2] = a.z; v[c][3] = a.w;
+            v[c][4] = b.x; v[c][5] = b.y; v[c][6] = b.z; v[c][7] = b.w;
+            if (dr) {
+                float4 p = *(const float4 *)(dr + base), q = *(const float4 *)(dr + base + 4);
+                float dd[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    float o = vxm_bf16(dd[i]);
+                    if (res_scale != 1.0f) o = o * res_scale;
+                    v[c][i] = vxm_bf16(v[c][i] + o);
+                }
+                *(float4 *)(hr + base) = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+                *(float4 *)(hr + base + 4) = make_float4(v[c][4], v[c][5], v[c][6], v[c][7]);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) ss += (double)(v[c][i] * v[c][i]);
+        }
+    }
+    const double tot = block_sum_f64(ss, shd);
+    if (!y && !xq) return;
+    const float mean = (float)(tot / (double)n);
+    const float sc = __fdiv_rn(1.0f, __fsqrt_rn(mean + eps));
+#pragma unroll
+    for (int c = 0; c < VXM_NORM_CHUNKS; c++) {
+        const int base = (c * 256 + threadIdx.x) * 8;
+        if (base >= n) continue;   // whole 32-blocks live in 4 consecutive lanes: n % 32 == 0
+        float o[8];
+        float4 g0 = gain ? *(const float4 *)(gain + base) : make_float4(1, 1, 1, 1);
+        float4 g1 = gain ? *(const float4 *)(gain + base + 4) : make_float4(1, 1, 1, 1);
+        const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float t = vxm_bf16(v[c][i] * sc);
+            o[i] = gain ? vxm_bf16(t * g[i]) : t;
+        }
+        if (y) {
+            float *yr = y + (int64_t)row * n + base;
+            *(float4 *)yr = make_float4(o[0], o[1], o[2], o[3]);
+            *(float4 *)(yr + 4) = make_float4(o[4], o[5], o[6], o[7]);
+        }
+        if (xq) {
+            const int64_t e = (int64_t)row * n + base;
+            quant_block_4lanes(o, variant, xq + e, xd + e / 32, (threadIdx.x & 3) == 0);
+        }
+    }
+}
+
+int vxm_launch_rmsnorm(vxm_ctx *ctx, float *h, const float *delta, float res_scale, const float *gain,
+                       int64_t rows, int64_t n, float eps, float *y, int8_t *xq, uint16_t *xd, int variant) {
+    if (rows <= 0) return VXM_OK;
+    if (n % 32 != 0 || n > 8 * 256 * VXM_NORM_CHUNKS)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "rms_norm: n=%lld must be a multiple of 32 and <= %d",
+                        (long long)n, 8 * 256 * VXM_NORM_CHUNKS);
+    hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(256), 0, ctx->stream, h, delta, res_scale, gain,
+                       (int)n, eps, y, xq, xd, variant);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Q/K/V post-processing of vcpm_attention (src/minicpm4.c:270-320): BF16 of
+// the projections, NEOX RoPE (ggml_rope_ext: theta_0 = pos, theta_{i+1} =
+// theta_i * theta_scale, pair (i, i+hd/2) rotated by theta_i / ff_i; BF16),
+// K and V appended to the f16 cache.  qkv: raw projections [M][qd + 2*kvd].
+// Tokens come in segments of S (one per CFG branch); token t has position
+// pos0 + t % S and segment t / S, whose cache starts at seg * seg_stride.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_rope_kv(const float *__restrict__ qkv, int nh, int nkv, int hd,
+                                                 int pos0, int S, float theta_scale, const float *__restrict__ ff,
+                                                 int no_rope, float *__restrict__ q_out, uint16_t *__restrict__ kc,
+                                                 uint16_t *__restrict__ vc, int cap, int64_t seg_stride,
+                                                 int cache_pos0) {
+    const int t = blockIdx.x;
+    const int seg = t / S, ti = t % S;
+    const int pos = pos0 + ti;
+    const int half = hd / 2;
+    const int qd = nh * hd, kvd = nkv * hd;
+    const float *row = qkv + (int64_t)t * (qd + 2 * kvd);
+    uint16_t *kseg = kc + seg * seg_stride, *vseg = vc + seg * seg_stride;
+    const int cpos = cache_pos0 + ti;
+    // q and k pairs
+    for (int idx = threadIdx.x; idx < (nh + nkv) * half; idx += blockDim.x) {
+        const int head = idx / half, i = idx % half;
+        const bool isq = head < nh;
+        const float *src = isq ? row + head * hd : row + qd + (head - nh) * hd;
+        float x0 = vxm_bf16(src[i]), x1 = vxm_bf16(src[i + half]);
+        float y0 = x0, y1 = x1;
+        if (!no_rope) {
+            float theta = (float)pos;
+            for (int k = 0; k < i; k++) theta = theta * theta_scale;
+            const float th = ff ? __fdiv_rn(theta, ff[i]) : theta;
+            const float c = cosf(th), s = sinf(th);
+            y0 = vxm_bf16(x0 * c - x1 * s);
+            y1 = vxm_bf16(x0 * s + x1 * c);
+        }
+        if (isq) {
+            float *qo = q_out + (int64_t)t * qd + head * hd;
+            qo[i] = y0;
+            qo[i + half] = y1;
+        } else {
+            const int kh = head - nh;
+            uint16_t *kd = kseg + ((int64_t)kh * cap + cpos) * hd;
+            kd[i] = vxm_f2h(y0);
+            kd[i + half] = vxm_f2h(y1);
+        }
+    }
+    // v
+    for (int idx = threadIdx.x; idx < kvd; idx += blockDim.x) {
+        const int kh = idx / hd, dd = idx % hd;
+        const float val = vxm_bf16(row[qd + kvd + idx]);
+        vseg[((int64_t)kh * cap + cpos) * hd + dd] = vxm_f2h(val);
+    }
+}
+
+int vxm_launch_rope_kv(vxm_ctx *ctx, const float *qkv, int64_t M, int nh, int nkv, int hd, int pos0, int S,
+                       float theta_scale, const float *ff, int no_rope, float *q_out, uint16_t *kc,
+                       uint16_t *vc, int cap, int64_t seg_stride, int cache_pos0) {
+    if (M <= 0) return VXM_OK;
+    hipLaunchKernelGGL(k_rope_kv, dim3((unsigned)M), dim3(256), 0, ctx->stream, qkv, nh, nkv, hd, pos0, S,
+                       theta_scale, ff, no_rope, q_out, kc, vc, cap, seg_stride, cache_pos0);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// gqa_group_attn (src/minicpm4.c:232-248) for one (token, query head):
+// s_j = (k_j . q) * (1/sqrt(hd)); p = softmax (sum in double, scaled by
+// (float)(1/sum)); out = sum_j p_j v_j.  Query head h reads kv head
+// h / (nh / nkv).  Causal: token t of a segment sees cache rows
+// [0, kv_base + t]; non-causal: rows [0, S).  Scores live in LDS (kv_len <= cap).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_attention(const float *__restrict__ q, const uint16_t *__restrict__ kc,
+                                                   const uint16_t *__restrict__ vc, float *__restrict__ out, int nh,
+                                                   int nkv, int hd, int cap, int64_t seg_stride, int S,
+                                                   int kv_base, int causal) {
+    extern __shared__ float lds[];
+    __shared__ float red[8];
+    __shared__ double redd[4];
+    const int h = blockIdx.x, t = blockIdx.y;
+    const int seg = t / S, ti = t % S;
+    const int kvh = h / (nh / nkv);
+    const int kv_len = causal ? kv_base + ti + 1 : S;
+    const uint16_t *kb = kc + seg * seg_stride + (int64_t)kvh * cap * hd;
+    const uint16_t *vb = vc + seg * seg_stride + (int64_t)kvh * cap * hd;
+    float *sq = lds;              // [hd]
+    float *sc = lds + hd;         // [kv_len]
+    float *part = sc + cap;       // [256]
+    const float *qr = q + (int64_t)t * nh * hd + h * hd;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) sq[d] = qr[d];
+    __syncthreads();
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)hd));
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < kv_len; j += blockDim.x) {
+        const uint16_t *kr = kb + (int64_t)j * hd;
+        float s = 0.0f;
+        for (int d = 0; d < hd; d++) s += vxm_h2f(kr[d]) * sq[d];
+        s = s * scale;
+        sc[j] = s;
+        mx = fmaxf(mx, s);
+    }
+    mx = block_max_f32(mx, red);
+    double sum = 0.0;
+    for (int j = threadIdx.x; j < kv_len; j += blockDim.x) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        sum += (double)e;
+    }
+    sum = block_sum_f64(sum, redd);
+    const float inv = (float)(1.0 / sum);
+    for (int j = threadIdx.x; j < kv_len; j += blockDim.x) sc[j] = sc[j] * inv;
+    __syncthreads();
+    // out[d] = sum_j v[j][d] * p_j: thread (sl, d) sums a contiguous j-slice,
+    // slices are added in order (hd <= 256, checked by the launcher).
+    const int slices = blockDim.x / hd;
+    const int d = threadIdx.x % hd, sl = threadIdx.x / hd;
+    float acc = 0.0f;
+    if (sl < slices) {
+        const int jper = (kv_len + slices - 1) / slices;
+        const int j0 = sl * jper, j1 = min(kv_len, j0 + jper);
+        for (int j = j0; j < j1; j++) acc += vxm_h2f(vb[(int64_t)j * hd + d]) * sc[j];
+    }
+    part[threadIdx.x] = acc;
+    __syncthreads();
+    if (sl == 0) {
+        float tot = 0.0f;
+        for (int s2 = 0; s2 < slices; s2++) tot += part[s2 * hd + d];
+        out[(int64_t)t * nh * hd + h * hd + d] = tot;
+    }
+}
+
+int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
+                         int64_t M, int nh, int nkv, int hd, int cap, int64_t seg_stride, int S, int kv_base,
+                         int causal) {
+    if (M <= 0) return VXM_OK;
+    if (hd > 256 || hd <= 0 || nkv <= 0 || nh % nkv)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "attention: head_dim %d / heads %d,%d unsupported", hd, nh, nkv);
+    const size_t lds = (size_t)(hd + cap + 256) * sizeof(float);
+    if (lds > 160 * 1024)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "attention: capacity %d exceeds the LDS score buffer", cap);
+    hipLaunchKernelGGL(k_attention, dim3(nh, (unsigned)M), dim3(256), lds, ctx->stream, q, kc, vc, out, nh, nkv,
+                       hd, cap, seg_stride, S, kv_base, causal);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// vcpm_mlp activation (src/minicpm4.c:441-456): p = bf16(bf16(silu(bf16(g))) *
+// bf16(u)), silu(x) = x / (1 + expf(-x)), then Q8_0 quantization of p.
+// Row m of gate/up: gu + m*ld (gate, F values) and gu + m*ld + F (up), the
+// output layout of the fused [gate; up] projection.  8 values per thread.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_swiglu_quant(const float *__restrict__ gu, int64_t F, int64_t ld,
+                                                      int64_t total, int8_t *__restrict__ xq,
+                                                      uint16_t *__restrict__ xd, float *__restrict__ p_out,
+                                                      int variant) {
+    const int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (e >= total) return;   // total, F % 32 == 0: 4-lane groups are all live or all dead
+    const int64_t m = e / F, j = e % F;
+    const float *g = gu + m * ld + j, *u = gu + m * ld + F + j;
+    float4 g0 = *(const float4 *)g, g1 = *(const float4 *)(g + 4);
+    float4 u0 = *(const float4 *)u, u1 = *(const float4 *)(u + 4);
+    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float gb = vxm_bf16(gv[i]);
+        const float s = vxm_bf16(__fdiv_rn(gb, 1.0f + expf(-gb)));
+        p[i] = vxm_bf16(s * vxm_bf16(uv[i]));
+    }
+    if (p_out) {
+        *(float4 *)(p_out + e) = make_float4(p[0], p[1], p[2], p[3]);
+        *(float4 *)(p_out + e + 4) = make_float4(p[4], p[5], p[6], p[7]);
+    }
+    quant_block_4lanes(p, variant, xq + e, xd + e / 32, (threadIdx.x & 3) == 0);
+}
+
+int vxm_launch_swiglu_quant(vxm_ctx *ctx, const float *gu, int64_t M, int64_t F, int64_t ld, int8_t *xq,
+                            uint16_t *xd, float *p_out, int variant) {
+    const int64_t total = M * F;
+    if (total <= 0) return VXM_OK;
+    if (F % 32) return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "swiglu: width %lld not a multiple of 32", (long long)F);
+    const int64_t threads = total / 8;
+    hipLaunchKernelGGL(k_swiglu_quant, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, gu, F,
+                       ld, total, xq, xd, p_out, variant);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// h = bf16(h + scale * bf16(delta)) (the residual adds of
+// vcpm_minicpm4_block, src/minicpm4.c:496-528), elementwise.
+// ---------------------------------------------------------------------------
+__global__ void k_residual(float *__restrict__ h, const float *__restrict__ delta, float scale, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float o = vxm_bf16(delta[i]);
+    if (scale != 1.0f) o = o * scale;
+    h[i] = vxm_bf16(h[i] + o);
+}
+
+int vxm_launch_residual(vxm_ctx *ctx, float *h, const float *delta, float scale, int64_t n) {
+    if (n <= 0) return VXM_OK;
+    hipLaunchKernelGGL(k_residual, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, h, delta, scale, n);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}
+
+// y = bf16(x + bias) per row (ggml_add of a repeated bias then BF16,
+// src/locdit.c:190-210 and :118-121); bias may be null (BF16 only).
+__global__ void k_bias_bf16(const float *__restrict__ x, const float *__restrict__ bias, float *__restrict__ y,
+                            int64_t rows, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * n) return;
+    float v = x[i];
+    if (bias) v = v + bias[i % n];
+    y[i] = vxm_bf16(v);
+}
+
+int vxm_launch_bias_bf16(vxm_ctx *ctx, const float *x, const float *bias, float *y, int64_t rows, int64_t n) {
+    if (rows * n <= 0) return VXM_OK;
+    hipLaunchKernelGGL(k_bias_bf16, dim3((unsigned)((rows * n + 255) / 256)), dim3(256), 0, ctx->stream, x, bias,
+                       y, rows, n);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}

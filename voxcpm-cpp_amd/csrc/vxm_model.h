@@ -1,0 +1,71 @@
+// vxm_model.h -- internal types of the MiniCPM4 / LocDiT drivers.
+#pragma once
+
+#include <algorithm>
+#include <vector>
+
+#include "vxm_ops.h"
+
+struct vxm_block_dims {
+    int64_t H = 0, F = 0;
+    int nh = 0, nkv = 0, hd = 0;
+    float eps = 1e-6f;
+    int no_rope = 0;
+    float res_scale = 1.0f;
+    float theta_scale = 1.0f;   // powf(rope_theta, -2/head_dim), host-computed
+    float *ff = nullptr;        // device rope frequency factors [hd/2] or null
+};
+
+struct vxm_block {
+    vxm_weight *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wd = nullptr;
+    float *g_in = nullptr, *g_post = nullptr;
+};
+
+// Scratch of one model for M tokens.
+struct vxm_workspace {
+    void *base = nullptr;
+    size_t bytes = 0;
+    int8_t *xq = nullptr;
+    uint16_t *xd = nullptr;
+    float *qkv = nullptr, *q = nullptr, *att = nullptr, *o = nullptr, *gu = nullptr, *dn = nullptr;
+    uint16_t *lk = nullptr, *lv = nullptr;   // fresh K/V of non-causal runs
+};
+
+// Where a block's attention reads and writes K/V.
+struct vxm_attn_site {
+    uint16_t *kc, *vc;
+    int cap;               // rows per kv head in the cache
+    int64_t seg_stride;    // elements between segment caches (CFG branches)
+    int S;                 // tokens per segment
+    int pos0;              // rope position of token 0 of a segment
+    int cache_pos0;        // cache row of token 0 (causal: keys 0..cache_pos0+t)
+    int causal;
+};
+
+struct vxm_kv_cache {
+    vxm_ctx *ctx = nullptr;
+    int n_layers = 0, nkv = 0, hd = 0, cap = 0;
+    int32_t n_used = 0;
+    int64_t layer_elems = 0;   // nkv * cap * hd
+    void *base = nullptr;      // [layer][k|v][nkv][cap][hd] f16
+    uint16_t *k(int l) { return (uint16_t *)base + (int64_t)l * 2 * layer_elems; }
+    uint16_t *v(int l) { return (uint16_t *)base + ((int64_t)l * 2 + 1) * layer_elems; }
+};
+
+struct vxm_minicpm4 {
+    vxm_ctx *ctx = nullptr;
+    vxm_minicpm4_config cfg{};
+    vxm_block_dims dims;
+    std::vector<vxm_block> blocks;
+    float *final_norm = nullptr;
+    vxm_workspace ws;
+};
+
+int vxm_ws_ensure(vxm_ctx *ctx, vxm_workspace &ws, int64_t M, int64_t H, int64_t qd, int64_t kvd, int64_t F,
+                  int64_t local_kv);
+void vxm_ws_free(vxm_workspace &ws);
+int vxm_block_upload(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_layer_weights_q8_0 &w, vxm_block &b);
+void vxm_block_free(vxm_ctx *ctx, vxm_block &b);
+int vxm_rope_setup(vxm_ctx *ctx, int hd, int32_t theta, const float *ff_host, float **ff_dev, float *theta_scale);
+int vxm_block_run(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_block &b, vxm_workspace &ws, float *x,
+                  int64_t M, const vxm_attn_site &site);

@@ -72,6 +72,17 @@ _SIGS = {
     "vxm_mul_mat_q8_0": (_I, [_P, _P, _P, _I64, _P]),
     "vxm_mul_mat_q8_0_q8_0": (_I, [_P, _P, _P, _P, _I64, _P]),
     "vxm_block_dots_q8_0": (_I, [_P, _P, _P, _P, _I64, _P]),
+    "vxm_rms_norm": (_I, [_P, _P, _P, _I64, _I64, _F, _P, _P, _P]),
+    "vxm_minicpm4_create": (_I, [_P, _P, _P, _P, C.POINTER(_P)]),
+    "vxm_minicpm4_free": (_I, [_P]),
+    "vxm_kv_cache_create": (_I, [_P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.POINTER(_P)]),
+    "vxm_kv_cache_free": (_I, [_P]),
+    "vxm_kv_cache_reset": (_I, [_P]),
+    "vxm_kv_cache_set_used": (_I, [_P, C.c_int32]),
+    "vxm_kv_cache_used": (C.c_int32, [_P]),
+    "vxm_kv_cache_layer": (_I, [_P, C.c_int32, C.POINTER(_P), C.POINTER(_P)]),
+    "vxm_minicpm4_block": (_I, [_P, _P, C.c_int32, _P, _I64, C.c_int32, _I]),
+    "vxm_minicpm4_forward": (_I, [_P, _P, _P, _I64, C.c_int32]),
     "vxm_host_quantize_q8_0": (_I, [_P, _I64, _I64, _P]),
     "vxm_host_randn": (_I, [_U64, _U64, _I64, _F, _F, _P]),
 }
@@ -198,6 +209,19 @@ class Context:
         self.check(lib().vxm_mul_mat_q8_0_q8_0(self.h, w.h, _ptr(xq), _ptr(xd), M, _ptr(y)))
         return y
 
+    def rms_norm(self, x, gain, eps, quantize=False):
+        """vcpm_rms_norm on device rows; returns y (and Q8_0 (xq, xd) if asked)."""
+        import torch
+
+        rows, n = x.shape
+        y = torch.empty_like(x)
+        xq = xd = None
+        if quantize:
+            xq = torch.empty((rows, n), dtype=torch.int8, device=x.device)
+            xd = torch.empty((rows, n // 32), dtype=torch.int16, device=x.device)
+        self.check(lib().vxm_rms_norm(self.h, _ptr(x), _ptr(gain), rows, n, eps, _ptr(y), _ptr(xq), _ptr(xd)))
+        return (y, xq, xd) if quantize else y
+
     def block_dots(self, w, xq, xd):
         import torch
 
@@ -205,6 +229,127 @@ class Context:
         out = torch.empty((M, w.n, w.k // 32), dtype=torch.int32, device=xq.device)
         self.check(lib().vxm_block_dots_q8_0(self.h, w.h, _ptr(xq), _ptr(xd), M, _ptr(out)))
         return out
+
+
+class MiniCPM4Config(C.Structure):
+    """Mirror of vxm_minicpm4_config (vcpm_minicpm4_config, src/minicpm4.h:14-27)."""
+
+    _fields_ = [
+        ("hidden_size", C.c_int32), ("n_layers", C.c_int32), ("n_heads", C.c_int32),
+        ("n_kv_heads", C.c_int32), ("intermediate_size", C.c_int32), ("head_dim", C.c_int32),
+        ("rms_norm_eps", C.c_float), ("rope_theta", C.c_int32), ("no_rope", C.c_int32),
+        ("scale_depth", C.c_float), ("rope_freq_factors", C.c_void_p),
+    ]
+
+
+class LayerWeightsQ8(C.Structure):
+    """Mirror of vxm_layer_weights_q8_0 (host pointers)."""
+
+    _fields_ = [(n, C.c_void_p) for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj",
+                                          "down_proj", "input_layernorm", "post_attention_layernorm")]
+
+
+class KVCache:
+    """f16 KV cache: per layer K, V [n_kv_heads][capacity][head_dim]."""
+
+    def __init__(self, ctx, n_layers, n_kv_heads, head_dim, capacity):
+        h = C.c_void_p()
+        ctx.check(lib().vxm_kv_cache_create(ctx.h, n_layers, n_kv_heads, head_dim, capacity, C.byref(h)))
+        self.ctx, self.h = ctx, h
+        self.n_layers, self.nkv, self.hd, self.cap = n_layers, n_kv_heads, head_dim, capacity
+
+    def layer(self, l):
+        k, v = C.c_void_p(), C.c_void_p()
+        self.ctx.check(lib().vxm_kv_cache_layer(self.h, l, C.byref(k), C.byref(v)))
+        return k.value, v.value
+
+    def upload(self, l, k_host, v_host):
+        """Copy host f16 bits [nkv][cap][hd] into layer l (a host-boundary copy)."""
+        import numpy as np
+
+        k, v = self.layer(l)
+        n = self.nkv * self.cap * self.hd * 2
+        for dst, src in ((k, k_host), (v, v_host)):
+            a = np.ascontiguousarray(src, dtype=np.uint16)
+            assert a.nbytes == n
+            self.ctx.check(lib().vxm_memcpy_h2d(self.ctx.h, C.c_void_p(dst), _ptr(a), n))
+
+    def download(self, l):
+        import numpy as np
+
+        k, v = self.layer(l)
+        out = []
+        for src in (k, v):
+            a = np.empty((self.nkv, self.cap, self.hd), dtype=np.uint16)
+            self.ctx.check(lib().vxm_memcpy_d2h(self.ctx.h, _ptr(a), C.c_void_p(src), a.nbytes))
+            out.append(a)
+        return out
+
+    @property
+    def used(self):
+        return lib().vxm_kv_cache_used(self.h)
+
+    def set_used(self, n):
+        self.ctx.check(lib().vxm_kv_cache_set_used(self.h, n))
+
+    def reset(self):
+        self.ctx.check(lib().vxm_kv_cache_reset(self.h))
+
+    def free(self):
+        if self.h:
+            self.ctx.check(lib().vxm_kv_cache_free(self.h))
+            self.h = None
+
+
+class MiniCPM4:
+    """vcpm_minicpm4 on the device: n_layers blocks of GGUF Q8_0 weights."""
+
+    def __init__(self, ctx, cfg: dict, layers, final_norm=None):
+        import numpy as np
+
+        self.ctx = ctx
+        self._keep = []
+        ff = cfg.get("rope_freq_factors")
+        if ff is not None:
+            ff = np.ascontiguousarray(ff, dtype=np.float32)
+            self._keep.append(ff)
+        c = MiniCPM4Config(cfg["hidden_size"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"],
+                           cfg["intermediate_size"], cfg["head_dim"], cfg.get("rms_norm_eps", 1e-6),
+                           int(cfg.get("rope_theta", 10000)), int(cfg.get("no_rope", 0)),
+                           float(cfg.get("scale_depth", 0.0)), None if ff is None else ff.ctypes.data)
+        self.cfg = cfg
+        arr = (LayerWeightsQ8 * len(layers))()
+        names = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj",
+                 "input_layernorm", "post_attention_layernorm")
+        for i, lw in enumerate(layers):
+            for n in names:
+                a = np.ascontiguousarray(lw[n])
+                self._keep.append(a)
+                setattr(arr[i], n, a.ctypes.data)
+        fn = None
+        if final_norm is not None:
+            fn = np.ascontiguousarray(final_norm, dtype=np.float32)
+            self._keep.append(fn)
+        h = C.c_void_p()
+        ctx.check(lib().vxm_minicpm4_create(ctx.h, C.byref(c), C.cast(arr, C.c_void_p),
+                                            None if fn is None else fn.ctypes.data_as(C.c_void_p), C.byref(h)))
+        self.h = h
+        self._keep = []
+
+    def block(self, kv, layer, x, pos, no_causal=0):
+        """In place on x (fp32 [n_tokens][hidden] device tensor)."""
+        self.ctx.check(lib().vxm_minicpm4_block(self.h, None if kv is None else kv.h, layer, _ptr(x), x.shape[0],
+                                                pos, no_causal))
+        return x
+
+    def forward(self, kv, x, pos):
+        self.ctx.check(lib().vxm_minicpm4_forward(self.h, kv.h, _ptr(x), x.shape[0], pos))
+        return x
+
+    def free(self):
+        if self.h:
+            self.ctx.check(lib().vxm_minicpm4_free(self.h))
+            self.h = None
 
 
 class Q8Weight:
