@@ -1,9 +1,16 @@
-"""Benchmark of the Q8_0 matmul path on one MI355X.
+"""Benchmark of the Q8_0 matmul hot path on one MI355X.
 
-Default workload: the Q8_0 decode GEMV (W ~ N(0, 0.02) from seed 0, x ~ N(0,1),
-both Q8_0) at 6144x2048 and 2048x6144, streamed over >= 64 rotated weight
-copies so the working set (> 850 MB) exceeds the 256 MB Infinity Cache.
-Prints one JSON line.  --gpus above 1 is refused: this build runs on one GPU.
+Workload (the "step"): one decode token through a 28-layer MiniCPM4-style
+stack (hidden 2048, 16 q / 2 kv heads of 128, SwiGLU 6144, Q8_0 weights
+~ N(0, 0.02) from seed 1), batch 1, f16 KV cache growing from context 256 to
+320 over 64 tokens, weights rotated through 3 device copies (4.2 GB, far
+beyond the 256 MB Infinity Cache).  `value` is the algorithmic weight + KV
+bytes of a step over its time (GB/s); the line also carries us per step, the
+isolated Q8_0 GEMV (6144x2048 and 2048x6144 over 64 rotated copies), one
+decoder layer step at context 512, the roofline of the dominant kernel and
+the host-CPU baseline (the oracle's SIMD restatement of ggml's CPU path).
+
+--gpus above 1 is refused: this build runs on one GPU.
 """
 import argparse
 import json
@@ -15,6 +22,11 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "voxcpm-cpp_amd"))
 
 HBM_PEAK_GBS = 8000.0
+H, NH, NKV, HD, F, L = 2048, 16, 2, 128, 6144, 28
+
+
+def log(msg):
+    print(f"# {msg}", file=sys.stderr, flush=True)
 
 
 def q8_bytes(n, k):
@@ -22,51 +34,180 @@ def q8_bytes(n, k):
 
 
 def gemv_bytes(n, k):
-    # weights + quantized activation (K int8 + K/32 fp16) + fp32 output
+    # weights + quantized activation (K int8 + K/32 fp16 scales) + fp32 output
     return q8_bytes(n, k) + k + k // 32 * 2 + 4 * n
 
 
-def time_gemv(ctx, torch, vxm, N, K, copies, steps, warmup):
+def layer_weight_bytes():
+    qd, kvd = NH * HD, NKV * HD
+    return (q8_bytes(qd, H) + 2 * q8_bytes(kvd, H) + q8_bytes(H, qd) + 2 * q8_bytes(F, H) + q8_bytes(H, F))
+
+
+def step_bytes(ctx_len, n_layers=L):
+    """Algorithmic HBM bytes of one decode token: Q8_0 weights, gains, KV read + append."""
+    kv_read = 2 * NKV * HD * 2 * (ctx_len + 1)
+    return n_layers * (layer_weight_bytes() + 2 * H * 4 + kv_read)
+
+
+def make_layers(vxm, seed, n_layers):
+    """Seeded synthetic Q8_0 layers (GGUF rows) and gains."""
+    qd, kvd = NH * HD, NKV * HD
+    shapes = [("q_proj", qd, H), ("k_proj", kvd, H), ("v_proj", kvd, H), ("o_proj", H, qd),
+              ("gate_proj", F, H), ("up_proj", F, H), ("down_proj", H, F)]
+    per_layer = sum(n * k for _, n, k in shapes) + 2 * H
+    layers = []
+    for l in range(n_layers):
+        off = l * per_layer
+        d = {}
+        for name, n, k in shapes:
+            w = vxm.host_randn(seed, n * k, 0.0, 0.02, offset=off).reshape(n, k)
+            d[name] = vxm.host_quantize_q8_0(w)
+            off += n * k
+        d["input_layernorm"] = vxm.host_randn(seed, H, 1.0, 0.02, offset=off)
+        d["post_attention_layernorm"] = vxm.host_randn(seed, H, 1.0, 0.02, offset=off + H)
+        layers.append(d)
+    return layers
+
+
+def kv_prefill(vxm, kv, n_layers, ctx_len, seed):
+    """Cache rows [0, ctx_len) of every layer from N(0,1), BF16-representable f16."""
+    import numpy as np
+
+    import torch
+
+    for l in range(n_layers):
+        ks = []
+        for j in range(2):
+            v = vxm.host_randn(seed + 100 + l, NKV * kv.cap * HD, 0.0, 1.0, offset=j * NKV * kv.cap * HD)
+            v = v.reshape(NKV, kv.cap, HD)
+            v[:, ctx_len:] = 0.0
+            bf = torch.from_numpy(v).to(torch.bfloat16).to(torch.float16).numpy().view(np.uint16)
+            ks.append(bf)
+        kv.upload(l, ks[0], ks[1])
+    kv.set_used(ctx_len)
+
+
+class Timer:
+    """HIP events on the library's stream."""
+
+    def __init__(self, torch, ctx):
+        self.torch, self.st = torch, ctx.torch_stream()
+        self.e0 = torch.cuda.Event(enable_timing=True)
+        self.e1 = torch.cuda.Event(enable_timing=True)
+
+    def start(self):
+        self.e0.record(self.st)
+
+    def stop_ms(self):
+        self.e1.record(self.st)
+        self.e1.synchronize()
+        return self.e0.elapsed_time(self.e1)
+
+
+def bench_gemv(ctx, torch, vxm, N, K, copies, reps):
     import numpy as np
 
     w32 = vxm.host_randn(0, N * K, 0.0, 0.02).reshape(N, K)
     x = vxm.host_randn(0, K, 0.0, 1.0, offset=N * K).reshape(1, K)
     wq = vxm.host_quantize_q8_0(w32)
     ws = [ctx.upload_q8_0(wq, N, K) for _ in range(copies)]
-    xd = torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0")
-    xq, xs = ctx.quantize_q8_0(xd, vxm.QUANT_X86)
+    xq, xs = ctx.quantize_q8_0(torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0"), vxm.QUANT_X86)
     y = torch.empty((1, N), dtype=torch.float32, device="cuda:0")
-    ctx.sync()
-    L = vxm.lib()
-    h = ctx.h
+    L_ = vxm.lib()
     args = [(w.h, vxm._ptr(xq), vxm._ptr(xs), vxm._ptr(y)) for w in ws]
-    for _ in range(warmup):
-        for a in args:
-            L.vxm_mul_mat_q8_0_q8_0(h, a[0], a[1], a[2], 1, a[3])
+    for a in args:
+        L_.vxm_mul_mat_q8_0_q8_0(ctx.h, a[0], a[1], a[2], 1, a[3])
     ctx.sync()
-    st = ctx.torch_stream()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    for _ in range(steps):
+    t = Timer(torch, ctx)
+    t.start()
+    for _ in range(reps):
         for a in args:
-            L.vxm_mul_mat_q8_0_q8_0(h, a[0], a[1], a[2], 1, a[3])
-    e1.record(st)
-    e1.synchronize()
-    ms = e0.elapsed_time(e1)
-    launches = steps * len(args)
-    us = ms * 1000.0 / launches
+            L_.vxm_mul_mat_q8_0_q8_0(ctx.h, a[0], a[1], a[2], 1, a[3])
+    us = t.stop_ms() * 1000.0 / (reps * copies)
     for w in ws:
         w.free()
     return us
 
 
+def bench_decode(ctx, torch, vxm, layers, n_layers, copies, ctx0, steps, warmup, mode):
+    """Decode `steps` tokens from context ctx0, rotating over `copies` weight copies."""
+    cfg = dict(hidden_size=H, n_layers=n_layers, n_heads=NH, n_kv_heads=NKV, head_dim=HD, intermediate_size=F,
+               rms_norm_eps=1e-6, rope_theta=10000)
+    fn = vxm.host_randn(11, H, 1.0, 0.02)
+    models = [vxm.MiniCPM4(ctx, cfg, layers, final_norm=fn) for _ in range(copies)]
+    for m in models:
+        m.set_decode_mode(mode)
+    cap = 1024
+    kv = vxm.KVCache(ctx, n_layers, NKV, HD, cap)
+    kv_prefill(vxm, kv, n_layers, ctx0, 5)
+    x = torch.from_numpy(vxm.host_randn(3, H, 0.0, 1.0).reshape(1, H)).to("cuda:0")
+    # warmup tokens, then rewind the cache to ctx0
+    for i in range(warmup):
+        models[i % copies].forward(kv, x, ctx0 + i)
+    ctx.sync()
+    kv.set_used(ctx0)
+    t = Timer(torch, ctx)
+    t.start()
+    for i in range(steps):
+        models[i % copies].forward(kv, x, ctx0 + i)
+    ms = t.stop_ms()
+    for m in models:
+        m.check()
+    ok = bool(torch.isfinite(x).all().item())
+    kv.free()
+    for m in models:
+        m.free()
+    return ms * 1000.0 / steps, ok
+
+
+def cpu_baseline(vxm, layers, n_layers, ctx0, tokens, threads):
+    """The oracle's SIMD restatement of ggml's CPU Q8_0 decode (1 copy of weights)."""
+    import ctypes as C
+
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    base = C.CDLL(oracle.BASE_LIB)
+    base.cb_set_threads.argtypes = [C.c_int]
+    base.cb_isa.restype = C.c_int
+    base.cb_minicpm4_forward.argtypes = [C.POINTER(oracle.Cfg), C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
+                                         C.c_int64, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32]
+    cfg = oracle.make_cfg(H, NH, NKV, HD, F, eps=1e-6, rope_theta=10000.0, rope_ff=oracle.ROPE_SHORT_FACTORS)
+    lws = [oracle.LayerW(wq=d["q_proj"], wk=d["k_proj"], wv=d["v_proj"], wo=d["o_proj"], wg=d["gate_proj"],
+                         wu=d["up_proj"], wd=d["down_proj"], g_in=d["input_layernorm"],
+                         g_post=d["post_attention_layernorm"]) for d in layers[:n_layers]]
+    arr = (oracle.Layer * n_layers)(*[l.struct() for l in lws])
+    cap = ctx0 + tokens + 1
+    rng = np.random.default_rng(5)
+    kcs = [oracle.fp32_to_fp16_bits(rng.normal(0, 1, NKV * cap * HD).astype(np.float32)) for _ in range(n_layers)]
+    vcs = [oracle.fp32_to_fp16_bits(rng.normal(0, 1, NKV * cap * HD).astype(np.float32)) for _ in range(n_layers)]
+    kp = (C.c_void_p * n_layers)(*[k.ctypes.data for k in kcs])
+    vp = (C.c_void_p * n_layers)(*[v.ctypes.data for v in vcs])
+    fn = np.ones(H, np.float32)
+    x = rng.normal(0, 1, H).astype(np.float32)
+    base.cb_set_threads(threads)
+    # one untimed token to warm caches / thread pool
+    base.cb_minicpm4_forward(C.byref(cfg), C.cast(arr, C.c_void_p), n_layers, fn.ctypes.data, x.ctypes.data, 1,
+                             C.cast(kp, C.c_void_p), C.cast(vp, C.c_void_p), cap, ctx0)
+    t0 = time.perf_counter()
+    for i in range(tokens):
+        base.cb_minicpm4_forward(C.byref(cfg), C.cast(arr, C.c_void_p), n_layers, fn.ctypes.data, x.ctypes.data,
+                                 1, C.cast(kp, C.c_void_p), C.cast(vp, C.c_void_p), cap, ctx0 + i)
+    dt = time.perf_counter() - t0
+    return dt * 1e6 / tokens, ("avx512-vnni" if base.cb_isa() else "avx2")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--copies", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=64, help="decode tokens timed (context 256 -> 256+steps)")
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--copies", type=int, default=3, help="rotated copies of the 28-layer weights")
+    ap.add_argument("--mode", default="auto", choices=["auto", "kernels", "persistent"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-tokens", type=int, default=2)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -75,31 +216,67 @@ def main():
     import torch
     import vxm
 
+    mode = {"auto": 0, "kernels": 1, "persistent": 2}[args.mode]
     ctx = vxm.Context(0)
     res = {}
     for (N, K) in ((6144, 2048), (2048, 6144)):
-        us = time_gemv(ctx, torch, vxm, N, K, args.copies, args.steps, args.warmup)
+        us = bench_gemv(ctx, torch, vxm, N, K, 64, 10)
         gbs = gemv_bytes(N, K) / (us * 1e-6) / 1e9
-        res[f"{N}x{K}"] = {"us": us, "GBs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS}
-        print(f"# gemv {N}x{K}: {us:.3f} us/launch, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)",
-              file=sys.stderr, flush=True)
+        res[f"{N}x{K}"] = {"us": round(us, 3), "GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"gemv {N}x{K}: {us:.3f} us/launch, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
+
+    t0 = time.time()
+    layers = make_layers(vxm, 1, L)
+    log(f"generated {L} Q8_0 layers in {time.time() - t0:.1f} s")
+
+    # one decoder layer, context 512 (8 rotated copies of the layer)
+    us1, _ = bench_decode(ctx, torch, vxm, layers[:1], 1, 8, 512, 64, 4, mode)
+    layer_b = step_bytes(512, 1)
+    log(f"one layer decode @ctx512: {us1:.2f} us, {layer_b / (us1 * 1e-6) / 1e9:.1f} GB/s")
+
+    us_step, finite = bench_decode(ctx, torch, vxm, layers, L, args.copies, 256, args.steps, args.warmup, mode)
+    mean_ctx = 256 + (args.steps - 1) / 2.0
+    sb = step_bytes(mean_ctx)
+    gbs = sb / (us_step * 1e-6) / 1e9
+    log(f"28-layer decode step: {us_step:.1f} us/token, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM), "
+        f"finite={finite}")
     ctx.close()
-    main_key = "6144x2048"
+
+    cpu = None
+    if not args.no_cpu:
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        c1, isa = cpu_baseline(vxm, layers, L, 256, args.cpu_tokens, 1)
+        cn, _ = cpu_baseline(vxm, layers, L, 256, args.cpu_tokens, threads)
+        log(f"cpu baseline: 1 thread {c1 / 1000:.1f} ms/token, {threads} threads {cn / 1000:.1f} ms/token ({isa})")
+        cpu = {"value": round(sb / (cn * 1e-6) / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"{args.cpu_tokens} decode tokens of the 28-layer stack at context 256 (SIMD {isa} "
+                         f"restatement of ggml-cpu Q8_0 mul_mat)",
+               "us_per_step": round(cn, 1), "us_per_step_1thread": round(c1, 1),
+               "speedup_vs_cpu_all_cores": round(cn / us_step, 1),
+               "speedup_vs_cpu_1thread": round(c1 / us_step, 1)}
+
     out = {
         "metric": "Q8_0 decode GEMV GB/s (% HBM peak) + us per 28-layer decode step, 1 GPU",
-        "value": res[main_key]["GBs"],
+        "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": res[main_key]["us"] / 1000.0,
+        "ms_per_step": round(us_step / 1000.0, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic",
-        "config": {"workload": "Q8_0 decode GEMV 6144x2048, 64 rotated weight copies"},
+        "config": {"workload": "28-layer MiniCPM4 decode, batch 1, hidden 2048, 16/2 heads x 128, FFN 6144, "
+                               "Q8_0 N(0,0.02) seed 1, f16 KV ctx 256->320, 3 rotated weight copies",
+                   "decode_mode": args.mode},
+        "us_per_step": round(us_step, 2),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "step_bytes": int(sb),
         "gemv": res,
+        "layer_decode_ctx512_us": round(us1, 3),
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out))
 

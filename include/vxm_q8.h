@@ -165,6 +165,19 @@ int vxm_minicpm4_block(vxm_minicpm4 *m, vxm_kv_cache *kv, int32_t layer, float *
 int vxm_minicpm4_forward(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x_dev, int64_t n_tokens,
                          int32_t pos);
 
+/* Decode (n_tokens == 1) strategy of vxm_minicpm4_forward:
+ * VXM_DECODE_AUTO picks the fastest available, VXM_DECODE_KERNELS runs one
+ * kernel per op, VXM_DECODE_PERSISTENT runs the whole stack in one
+ * cooperative launch.  No reference counterpart (ggml has one graph path). */
+#define VXM_DECODE_AUTO 0
+#define VXM_DECODE_KERNELS 1
+#define VXM_DECODE_PERSISTENT 2
+int vxm_minicpm4_set_decode_mode(vxm_minicpm4 *m, int mode);
+/* Synchronises the context's stream and reports a device-side failure of the
+ * persistent decode (a workgroup that timed out waiting for its inputs) as
+ * VXM_ERR_BACKEND, then clears it.  Decode calls themselves never block. */
+int vxm_minicpm4_check(vxm_minicpm4 *m);
+
 /* ---- host helpers (no device work) --------------------------------------
  * GGUF Q8_0 quantization of F32 rows with the weight rule of
  * ggml_quantize_chunk (tools/quantize.c:292): d = amax/127 (fp16),

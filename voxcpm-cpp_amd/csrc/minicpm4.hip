@@ -3,9 +3,10 @@
 // stream-ordered kernels, plus the f16 KV cache.
 //
 // Device layout of one block:
-//   wqkv : Q8_0 [(n_heads + 2 n_kv) * head_dim][hidden]   q rows, then k, then v
+//   wqkv : Q8_0 [(n_heads + 2 n_kv) * head_dim][hidden]   q rows, then k, then v;
+//          q and k rows pair-interleaved per head (dims i, i + hd/2 -> rows 2i, 2i+1)
 //   wo   : Q8_0 [hidden][n_heads * head_dim]
-//   wgu  : Q8_0 [2 * ffn][hidden]                          gate rows, then up
+//   wgu  : Q8_0 [2 * ffn][hidden]                          gate n at row 2n, up n at 2n+1
 //   wd   : Q8_0 [hidden][ffn]
 //   g_in, g_post : fp32 [hidden]
 // Kernel sequence per layer (M tokens):
@@ -84,14 +85,38 @@ void vxm_ws_free(vxm_workspace &ws) {
 // ---------------------------------------------------------------------------
 // block weights
 // ---------------------------------------------------------------------------
-static int upload_concat(vxm_ctx *ctx, const void *a, int64_t na, const void *b, int64_t nb_rows, const void *c,
-                         int64_t nc, int64_t k, vxm_weight **out) {
-    const size_t rb = (size_t)(k / 32) * 34;
-    std::vector<uint8_t> buf(rb * (size_t)(na + nb_rows + nc));
-    memcpy(buf.data(), a, rb * na);
-    if (b) memcpy(buf.data() + rb * na, b, rb * nb_rows);
-    if (c) memcpy(buf.data() + rb * (na + nb_rows), c, rb * nc);
-    return vxm_upload_q8_0(ctx, buf.data(), na + nb_rows + nc, k, out);
+// Fused QKV rows: for every q head and k head, dims (i, i + hd/2) become rows
+// (2i, 2i + 1), so each NEOX rotary pair is produced by one wave; v rows keep
+// their order.
+static int upload_qkv(vxm_ctx *ctx, const void *q, const void *k, const void *v, int nh, int nkv, int hd,
+                      int64_t K, vxm_weight **out) {
+    const size_t rb = (size_t)(K / 32) * 34;
+    const int64_t qd = (int64_t)nh * hd, kvd = (int64_t)nkv * hd;
+    std::vector<uint8_t> buf(rb * (size_t)(qd + 2 * kvd));
+    auto put = [&](int64_t dst, const void *src, int64_t row) {
+        memcpy(buf.data() + rb * dst, (const uint8_t *)src + rb * row, rb);
+    };
+    for (int head = 0; head < nh + nkv; head++) {
+        const void *src = head < nh ? q : k;
+        const int64_t base = head < nh ? (int64_t)head * hd : (int64_t)(head - nh) * hd;
+        for (int i = 0; i < hd / 2; i++) {
+            put((int64_t)head * hd + 2 * i, src, base + i);
+            put((int64_t)head * hd + 2 * i + 1, src, base + i + hd / 2);
+        }
+    }
+    memcpy(buf.data() + rb * (qd + kvd), v, rb * kvd);
+    return vxm_upload_q8_0(ctx, buf.data(), qd + 2 * kvd, K, out);
+}
+
+// Fused gate/up rows interleaved: row 2n = gate n, row 2n + 1 = up n.
+static int upload_gate_up(vxm_ctx *ctx, const void *gate, const void *up, int64_t F, int64_t K, vxm_weight **out) {
+    const size_t rb = (size_t)(K / 32) * 34;
+    std::vector<uint8_t> buf(rb * (size_t)(2 * F));
+    for (int64_t n = 0; n < F; n++) {
+        memcpy(buf.data() + rb * (2 * n), (const uint8_t *)gate + rb * n, rb);
+        memcpy(buf.data() + rb * (2 * n + 1), (const uint8_t *)up + rb * n, rb);
+    }
+    return vxm_upload_q8_0(ctx, buf.data(), 2 * F, K, out);
 }
 
 static int upload_f32(vxm_ctx *ctx, const float *src, int64_t n, float **out) {
@@ -110,9 +135,10 @@ int vxm_block_upload(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_layer_weig
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "layer weights: a projection is NULL");
     const int64_t qd = (int64_t)d.nh * d.hd, kvd = (int64_t)d.nkv * d.hd;
     int rc;
-    if ((rc = upload_concat(ctx, w.q_proj, qd, w.k_proj, kvd, w.v_proj, kvd, d.H, &b.wqkv))) return rc;
+    (void)kvd;
+    if ((rc = upload_qkv(ctx, w.q_proj, w.k_proj, w.v_proj, d.nh, d.nkv, d.hd, d.H, &b.wqkv))) return rc;
     if ((rc = vxm_upload_q8_0(ctx, w.o_proj, d.H, qd, &b.wo))) return rc;
-    if ((rc = upload_concat(ctx, w.gate_proj, d.F, w.up_proj, d.F, nullptr, 0, d.H, &b.wgu))) return rc;
+    if ((rc = upload_gate_up(ctx, w.gate_proj, w.up_proj, d.F, d.H, &b.wgu))) return rc;
     if ((rc = vxm_upload_q8_0(ctx, w.down_proj, d.H, d.F, &b.wd))) return rc;
     if ((rc = upload_f32(ctx, w.input_layernorm, d.H, &b.g_in))) return rc;
     if ((rc = upload_f32(ctx, w.post_attention_layernorm, d.H, &b.g_post))) return rc;
@@ -275,10 +301,24 @@ extern "C" int vxm_minicpm4_free(vxm_minicpm4 *m) {
     if (!m) return VXM_ERR_INVALID_ARG;
     (void)hipStreamSynchronize(m->ctx->stream);
     for (auto &b : m->blocks) vxm_block_free(m->ctx, b);
+    vxm_persistent_free(m);
     if (m->final_norm) (void)hipFree(m->final_norm);
     if (m->dims.ff) (void)hipFree(m->dims.ff);
     vxm_ws_free(m->ws);
     delete m;
+    return VXM_OK;
+}
+
+extern "C" int vxm_minicpm4_check(vxm_minicpm4 *m) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    return vxm_persistent_check(m);
+}
+
+extern "C" int vxm_minicpm4_set_decode_mode(vxm_minicpm4 *m, int mode) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    if (mode < VXM_DECODE_AUTO || mode > VXM_DECODE_PERSISTENT)
+        return vxm_fail(m->ctx, VXM_ERR_INVALID_ARG, "unknown decode mode %d", mode);
+    m->decode_mode = mode;
     return VXM_OK;
 }
 
@@ -327,8 +367,19 @@ extern "C" int vxm_minicpm4_forward(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x_
     vxm_ctx *ctx = m->ctx;
     const vxm_block_dims &d = m->dims;
     const int64_t qd = (int64_t)d.nh * d.hd, kvd = (int64_t)d.nkv * d.hd;
-    if ((rc = vxm_ws_ensure(ctx, m->ws, n_tokens, d.H, qd, kvd, d.F, 0))) return rc;
     const int var = ctx->quant_variant;
+    if (n_tokens == 1 && m->decode_mode != VXM_DECODE_KERNELS) {
+        const bool ok = vxm_persistent_supported(m, kv) && var == VXM_QUANT_X86;
+        if (ok) {
+            if ((rc = vxm_persistent_decode(m, kv, x_dev, pos))) return rc;
+            kv->n_used = pos + 1;
+            return VXM_OK;
+        }
+        if (m->decode_mode == VXM_DECODE_PERSISTENT)
+            return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED,
+                            "persistent decode: no kernel for this shape / device / quantizer");
+    }
+    if ((rc = vxm_ws_ensure(ctx, m->ws, n_tokens, d.H, qd, kvd, d.F, 0))) return rc;
     for (int l = 0; l < m->cfg.n_layers; l++) {
         const vxm_block &b = m->blocks[l];
         // residual of the previous layer's MLP folded into this layer's input norm

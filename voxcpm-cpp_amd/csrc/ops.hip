@@ -166,8 +166,9 @@ __global__ __launch_bounds__(256) void k_rope_kv(const float *__restrict__ qkv, 
     for (int idx = threadIdx.x; idx < (nh + nkv) * half; idx += blockDim.x) {
         const int head = idx / half, i = idx % half;
         const bool isq = head < nh;
+        // q and k rows are stored pair-interleaved: head row 2i is dim i, 2i+1 is dim i + hd/2
         const float *src = isq ? row + head * hd : row + qd + (head - nh) * hd;
-        float x0 = vxm_bf16(src[i]), x1 = vxm_bf16(src[i + half]);
+        float x0 = vxm_bf16(src[2 * i]), x1 = vxm_bf16(src[2 * i + 1]);
         float y0 = x0, y1 = x1;
         if (!no_rope) {
             float theta = (float)pos;
@@ -290,8 +291,8 @@ int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const
 // ---------------------------------------------------------------------------
 // vcpm_mlp activation (src/minicpm4.c:441-456): p = bf16(bf16(silu(bf16(g))) *
 // bf16(u)), silu(x) = x / (1 + expf(-x)), then Q8_0 quantization of p.
-// Row m of gate/up: gu + m*ld (gate, F values) and gu + m*ld + F (up), the
-// output layout of the fused [gate; up] projection.  8 values per thread.
+// Row m of the fused gate/up projection holds 2F values interleaved: gate n at
+// gu[m*ld + 2n], up n at gu[m*ld + 2n + 1].  8 outputs per thread.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_swiglu_quant(const float *__restrict__ gu, int64_t F, int64_t ld,
                                                       int64_t total, int8_t *__restrict__ xq,
@@ -300,11 +301,13 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const float *__restrict__ 
     const int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
     if (e >= total) return;   // total, F % 32 == 0: 4-lane groups are all live or all dead
     const int64_t m = e / F, j = e % F;
-    const float *g = gu + m * ld + j, *u = gu + m * ld + F + j;
-    float4 g0 = *(const float4 *)g, g1 = *(const float4 *)(g + 4);
-    float4 u0 = *(const float4 *)u, u1 = *(const float4 *)(u + 4);
-    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-    const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    const float4 *s = (const float4 *)(gu + m * ld + 2 * j);
+    float gv[8], uv[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float4 a = s[k];
+        gv[2 * k] = a.x; uv[2 * k] = a.y; gv[2 * k + 1] = a.z; uv[2 * k + 1] = a.w;
+    }
     float p[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {

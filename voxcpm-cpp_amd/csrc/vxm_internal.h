@@ -48,9 +48,11 @@ int vxm_fail(vxm_ctx *ctx, int code, const char *fmt, ...);
 #define VXM_HIP(ctx, call)                                                              \
     do {                                                                                \
         hipError_t e_ = (call);                                                         \
-        if (e_ != hipSuccess)                                                           \
+        if (e_ != hipSuccess) {                                                         \
+            (void)hipGetLastError(); /* do not leave the error for the next check */    \
             return vxm_fail((ctx), VXM_ERR_BACKEND, "%s failed: %s (%s:%d)", #call,      \
                             hipGetErrorString(e_), __FILE__, __LINE__);                 \
+        }                                                                               \
     } while (0)
 
 #define VXM_CHECK_LAUNCH(ctx) VXM_HIP(ctx, hipGetLastError())

@@ -52,6 +52,8 @@ struct vxm_kv_cache {
     uint16_t *v(int l) { return (uint16_t *)base + ((int64_t)l * 2 + 1) * layer_elems; }
 };
 
+struct vxm_persistent_state;
+
 struct vxm_minicpm4 {
     vxm_ctx *ctx = nullptr;
     vxm_minicpm4_config cfg{};
@@ -59,7 +61,16 @@ struct vxm_minicpm4 {
     std::vector<vxm_block> blocks;
     float *final_norm = nullptr;
     vxm_workspace ws;
+    int decode_mode = VXM_DECODE_AUTO;
+    vxm_persistent_state *pstate = nullptr;
 };
+
+// persistent single-launch decode (decode_persistent.hip)
+bool vxm_persistent_supported(const vxm_minicpm4 *m, const vxm_kv_cache *kv);
+int vxm_persistent_max_cap(const vxm_block_dims &d);
+int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t pos);
+int vxm_persistent_check(vxm_minicpm4 *m);
+void vxm_persistent_free(vxm_minicpm4 *m);
 
 int vxm_ws_ensure(vxm_ctx *ctx, vxm_workspace &ws, int64_t M, int64_t H, int64_t qd, int64_t kvd, int64_t F,
                   int64_t local_kv);

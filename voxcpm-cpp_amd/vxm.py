@@ -83,6 +83,8 @@ _SIGS = {
     "vxm_kv_cache_layer": (_I, [_P, C.c_int32, C.POINTER(_P), C.POINTER(_P)]),
     "vxm_minicpm4_block": (_I, [_P, _P, C.c_int32, _P, _I64, C.c_int32, _I]),
     "vxm_minicpm4_forward": (_I, [_P, _P, _P, _I64, C.c_int32]),
+    "vxm_minicpm4_set_decode_mode": (_I, [_P, _I]),
+    "vxm_minicpm4_check": (_I, [_P]),
     "vxm_host_quantize_q8_0": (_I, [_P, _I64, _I64, _P]),
     "vxm_host_randn": (_I, [_U64, _U64, _I64, _F, _F, _P]),
 }
@@ -341,6 +343,14 @@ class MiniCPM4:
         self.ctx.check(lib().vxm_minicpm4_block(self.h, None if kv is None else kv.h, layer, _ptr(x), x.shape[0],
                                                 pos, no_causal))
         return x
+
+    def set_decode_mode(self, mode):
+        """0 auto, 1 one kernel per op, 2 persistent whole-stack launch."""
+        self.ctx.check(lib().vxm_minicpm4_set_decode_mode(self.h, mode))
+
+    def check(self):
+        """Sync and raise if a persistent decode launch failed on the device."""
+        self.ctx.check(lib().vxm_minicpm4_check(self.h))
 
     def forward(self, kv, x, pos):
         self.ctx.check(lib().vxm_minicpm4_forward(self.h, kv.h, _ptr(x), x.shape[0], pos))
