@@ -1,58 +1,152 @@
 // decode_persistent.hip -- one decode token through the whole MiniCPM4 stack
 // (vcpm_minicpm4_forward with n_tokens = 1, src/minicpm4.c:536-572) in ONE
-// cooperative launch of one workgroup per CU.
+// cooperative launch of one 512-thread workgroup per CU.
 //
-// Why: on MI355X a kernel boundary costs ~1.3-2.4 us and a cross-XCD signal
-// ~1.5 us, against ~6.3 us of HBM streaming per layer; one launch per op
-// (10 per layer) spends more time in boundaries than in streaming.
+// Why one launch: on MI355X a dependent kernel boundary costs ~2.7 us (1.6 us
+// in a HIP graph) against ~6.3 us of HBM streaming per layer; one launch per
+// op would spend more time in boundaries than in streaming.
 //
-// Dataflow: each layer is five phases
+// Dataflow.  Each layer is five phases
 //   A  rms_norm(x) -> Q8_0 -> QKV rows -> BF16 -> NEOX rope -> q, k, v
 //   B  attention (+ f16 KV append), one workgroup per query head
 //   C  O rows -> h1 = BF16(x + BF16(o))
 //   D  rms_norm(h1) -> Q8_0 -> gate/up rows -> p = SwiGLU
 //   E  Q8_0(p) -> down rows -> x' = BF16(h1 + BF16(d))
-// and every phase publishes its outputs as 64-bit tagged words: a 32-bit tag
+// Every phase publishes its outputs as 64-bit tagged words: a 32-bit tag
 // (launch epoch, layer, phase) over 32 bits of payload -- two BF16 values
 // (q/k/v, h1, p and x are all BF16-rounded by the reference graph) or one
 // fp32 (the attention output).  Each word is one relaxed agent-scope atomic
-// store.  A consumer polls the words it needs until every tag is the expected
-// one, so data and synchronisation arrive together: one cross-XCD latency per
-// phase and no grid barrier.  Every workgroup needs every element of its
-// inputs, so the all-to-all dependency also protects the single-buffered
-// channels against write-after-read.
+// store, so no fence (and no L2 writeback) is ever needed: a consumer reads
+// the words it needs until every tag is the expected one.  Every workgroup
+// needs every element of its inputs, so the all-to-all dependency also
+// protects the single-buffered channels against write-after-read.
 //
-// Waves: wave 0 of each workgroup only polls inputs (and stages the RMSNorm
-// gains) into LDS; waves 1..3 own fixed weight rows of every matrix and keep
-// them in registers.  The loads of the next phase's rows are issued right
-// after the current phase's inputs arrive.  Vector-memory counters retire in
-// order, so keeping polls and prefetches in different waves is what lets a
-// poll complete while megabytes of weights are still in flight.
-// The arithmetic per row is exactly that of the GEMV kernel (q8_matmul.hip):
-// per-block int32 sums, then (float)sumi * (d_w * d_x).
+// Work split.  In every phase workgroup g owns a fixed, contiguous block of
+// weight rows (10 QKV, 8 O, 48 gate/up, 8 down rows at the TSLM shape).  Its
+// rows are cut into units of one 1 KiB chunk (1024 quants + 32 scales); the
+// seven compute waves take units round-robin, so every wave streams the same
+// number of bytes (+-1 unit).  A unit's dot product yields one fp32 partial;
+// the partials of a row are added in chunk order from LDS.
+//
+// Weight streaming.  Wave 0 only reads the phase inputs; waves 1..7 stream
+// weights through a register ring (9 slots at the TSLM shape, whose schedule
+// has 27 units per layer) with a fixed lookahead of P units: after consuming
+// the unit at stream position j the wave issues the loads of position j + P
+// (which may belong to the next phase or the next layer), so the weights of
+// the next phase are in flight while a phase waits for its inputs.  Barriers
+// fence LDS only (s_barrier with LDS-scoped fences), so they never drain the
+// weight loads in flight.
+//
+// Latency budget.  A wave64 VALU instruction issues once per 4 cycles and a
+// workgroup has two waves per SIMD, so the serial work between two phases is
+// counted in instructions: reductions run on DPP (not ds_bpermute), BF16
+// rounding on v_cvt_pk_bf16_f32, RMSNorm's sum of squares is formed by the
+// reading wave while it unpacks the input, and the norm is fused with the
+// Q8_0 quantization over all 512 threads.
+//
+// The arithmetic per row is that of the GEMV kernel (q8_matmul.hip): per-block
+// int32 sums, then (float)sumi * (d_w * d_x); only the fp32 order of the
+// block terms differs (lane tree within a chunk, chunks in order).
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <utility>
+
 #include "vxm_model.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+// Phase timestamps for profiling builds (-DVXM_PERSISTENT_TRACE): slot k of
+// layer l of this workgroup gets the 100 MHz real-time counter.  Compiled
+// out of the library.
+#ifdef VXM_PERSISTENT_TRACE
+#define VXM_TS(cond, k)                                                                              \
+    do {                                                                                             \
+        if ((cond) && p.trace)                                                                       \
+            p.trace[(size_t)blockIdx.x * p.trace_stride + 2 + l * 12 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define VXM_TS(cond, k) do { } while (0)
+#endif
+
 namespace {
 
-constexpr int kWaves = 4;              // waves per workgroup: 1 poller + 3 compute
+constexpr int kWaves = 8;              // waves per workgroup: 1 reader + 7 compute
 constexpr int kCW = kWaves - 1;
 constexpr int kThreads = kWaves * 64;
-constexpr int kSpin = 1 << 17;         // poll retries before giving up
-// Every channel is written as kRep replicas; workgroup b polls replica
-// b % kRep.  256 workgroups reading one copy concentrate the coherent loads
-// on the few memory channels behind those lines; replicas spread them out.
+constexpr int kG = 256;                // workgroups: one per CU
+constexpr int kSpin = 1 << 17;         // poll rounds before giving up
+constexpr int kLook = 8;               // weight units in flight per compute wave
+// Every channel is written as kRep replicas; workgroup b reads replica
+// b % kRep, so the coherent loads of 256 workgroups spread over many lines.
 constexpr int kRep = 16;
 constexpr int kPad = 64;               // words between replicas
+constexpr int kAttnKB = 8;             // attention: key loads in flight per lane
 
 __host__ __device__ constexpr int rep_stride(int words) { return words + kPad; }
+__host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
+__host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
 enum Phase { PH_X = 0, PH_QKV = 1, PH_ATT = 2, PH_H1 = 3, PH_P = 4 };
+
+template <int H_, int NH_, int NKV_, int HD_, int F_>
+struct Shape {
+    static constexpr int H = H_, NH = NH_, NKV = NKV_, HD = HD_, F = F_;
+    static constexpr int QD = NH * HD, KVD = NKV * HD, NQKV = QD + 2 * KVD;
+    static constexpr int QPK = NH / NKV;
+    // rows per workgroup per phase, 1 KiB chunks per row, units per workgroup
+    static constexpr int RA = NQKV / kG, RC = H / kG, RD = 2 * F / kG, RE = H / kG;
+    static constexpr int CA = H / 1024, CC = QD / 1024, CD = H / 1024, CE = F / 1024;
+    static constexpr int UA = RA * CA, UC = RC * CC, UD = RD * CD, UE = RE * CE;
+    // ring slots per compute wave: A, C, D, E units of one layer
+    static constexpr int SA = cdiv(UA, kCW), SC = cdiv(UC, kCW), SD = cdiv(UD, kCW), SE = cdiv(UE, kCW);
+    static constexpr int OA = 0, OC = SA, OD = SA + SC, OE = SA + SC + SD, NS = SA + SC + SD + SE;
+    static constexpr int P = kLook < NS ? kLook : NS;
+    // ring size: the smallest divisor of NS that holds P units, so the slot of
+    // stream position l*NS + s is s % RING for every layer l
+    static constexpr int ring_size() {
+        for (int r = P; r <= NS; r++)
+            if (NS % r == 0) return r;
+        return NS;
+    }
+    static constexpr int RING = ring_size();
+    static constexpr int UMAX = cmax(cmax(UA, UC), cmax(UD, UE));
+    static constexpr int KMAX = cmax(cmax(H, QD), F);
+    static constexpr int BIG = cmax(cmax(QD, F), H);
+    static_assert(NQKV % kG == 0 && H % kG == 0 && (2 * F) % kG == 0, "rows must split over 256 workgroups");
+    static_assert(RA % 2 == 0 && RC % 2 == 0 && RD % 4 == 0 && RE % 2 == 0, "rows per workgroup");
+    static_assert(H % 1024 == 0 && QD % 1024 == 0 && F % 1024 == 0, "K must be a multiple of 1024");
+    static_assert(H <= 4 * kThreads && (H & (H - 1)) == 0, "hidden: one norm pass, power of two");
+    static_assert(HD == 128 && NH % NKV == 0, "heads: the attention maps one key to a row of 16 lanes");
+    static_assert(NH <= kG && QPK * 8 <= kG && NH <= 64, "attention workgroups");
+    // LDS layout, in floats (the int8 quants go last, 16-byte aligned)
+    static constexpr int L_XS = 0;                  // layer input x              [H]
+    static constexpr int L_H1 = L_XS + H;           // h1                         [H]
+    static constexpr int L_GN = L_H1 + H;           // RMSNorm gain of the phase  [H]
+    static constexpr int L_BIG = L_GN + H;          // att / p / final norm       [BIG]
+    static constexpr int L_XD = L_BIG + BIG;        // activation block scales    [KMAX/32]
+    static constexpr int L_CS = L_XD + KMAX / 32;   // rope cos/sin               [HD]
+    static constexpr int L_AQ = L_CS + HD;          // attention q, k, v          [3 HD]
+    static constexpr int L_PART = L_AQ + 3 * HD;    // unit partials              [UMAX]
+    static constexpr int L_RED = L_PART + UMAX;     // reductions / wave partials [kWaves * HD]
+    static constexpr int L_SC = L_RED + kWaves * HD;// attention scores           [cap + 1]
+    __host__ __device__ static int xq_off(int cap) { return ((L_SC + cap + 1) * 4 + 15) & ~15; }
+    __host__ __device__ static int bytes(int cap) { return xq_off(cap) + KMAX; }
+};
+
+// workgroup that runs the attention of query head h: the heads of one kv
+// group land on workgroups of one XCD (dispatch is round-robin over the 8
+// XCDs), so the group's K/V rows are shared through that XCD's L2.
+template <class S>
+__device__ __forceinline__ int attn_wg(int h) { return (h % S::QPK) * 8 + h / S::QPK; }
 
 __device__ __forceinline__ uint32_t make_tag(uint32_t epoch, int layer, int phase) {
     return (epoch << 12) | ((uint32_t)layer << 3) | (uint32_t)phase;
 }
+
+// F32 -> BF16 (round to nearest even) -> F32 on v_cvt_pk_bf16_f32; the same
+// rounding as minicpm_bf16_round (src/minicpm4.c:39-42) for every non-NaN.
+__device__ __forceinline__ float bf16r(float f) { return (float)(__bf16)f; }
 
 // two BF16-valued floats (low 16 bits zero) in one 32-bit payload
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
@@ -67,6 +161,15 @@ __device__ __forceinline__ uint64_t get_word(const uint64_t *src) {
     return __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Workgroup barrier that orders LDS only.  Global traffic between waves of a
+// workgroup goes through the agent-scope tagged words, so the barrier never
+// has to wait for the weight loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ int dot16(const v4i a, const v4i b) {
     int acc = __builtin_amdgcn_sdot4(a.x, b.x, 0, false);
     acc = __builtin_amdgcn_sdot4(a.y, b.y, acc, false);
@@ -75,17 +178,101 @@ __device__ __forceinline__ int dot16(const v4i a, const v4i b) {
     return acc;
 }
 
-__device__ __forceinline__ float pair_sum(float v) {
-#pragma unroll
-    for (int m = 2; m <= 32; m <<= 1) v += __shfl_xor(v, m, 64);
+// ---- cross-lane reductions on DPP (VALU data sharing, a few cycles per step;
+// __shfl_xor goes through ds_bpermute at LDS latency) ----------------------
+// dpp control codes (GFX9): quad_perm, row_shr:n = 0x110 + n,
+// row_half_mirror = 0x141, row_bcast:15 = 0x142, row_bcast:31 = 0x143
+constexpr int kDppXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppMirror8 = 0x141;
+
+template <int CTRL, int RM = 0xF>
+__device__ __forceinline__ int dpp_i(int v) {   // lanes with no source (or outside RM) read 0
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, RM, 0xF, false);
+}
+template <int CTRL, int RM = 0xF>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL, RM>(__float_as_int(v)));
+}
+template <int CTRL, int RM = 0xF>
+__device__ __forceinline__ float dpp_keep_f(float v) {   // lanes with no source keep v
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, RM, 0xF, false));
+}
+template <int CTRL, int RM = 0xF>
+__device__ __forceinline__ double dpp_d(double v) {
+    const int lo = dpp_i<CTRL, RM>(__double2loint(v)), hi = dpp_i<CTRL, RM>(__double2hiint(v));
+    return __hiloint2double(hi, lo);
+}
+
+// inclusive prefix sums within rows of 16, then across rows: lane 63 holds
+// the wave total (lane 15 + 16r holds the total of rows 0..r)
+__device__ __forceinline__ float wave_sum_63(float v) {
+    v += dpp_f<0x111>(v);
+    v += dpp_f<0x112>(v);
+    v += dpp_f<0x114>(v);
+    v += dpp_f<0x118>(v);
+    v += dpp_f<0x142, 0xA>(v);
+    v += dpp_f<0x143, 0xC>(v);
     return v;
+}
+__device__ __forceinline__ double wave_sum_63_d(double v) {
+    v += dpp_d<0x111>(v);
+    v += dpp_d<0x112>(v);
+    v += dpp_d<0x114>(v);
+    v += dpp_d<0x118>(v);
+    v += dpp_d<0x142, 0xA>(v);
+    v += dpp_d<0x143, 0xC>(v);
+    return v;
+}
+__device__ __forceinline__ float wave_max_63(float v) {
+    v = fmaxf(v, dpp_keep_f<0x111>(v));
+    v = fmaxf(v, dpp_keep_f<0x112>(v));
+    v = fmaxf(v, dpp_keep_f<0x114>(v));
+    v = fmaxf(v, dpp_keep_f<0x118>(v));
+    v = fmaxf(v, dpp_keep_f<0x142, 0xA>(v));
+    v = fmaxf(v, dpp_keep_f<0x143, 0xC>(v));
+    return v;
+}
+// sum over each row of 16 lanes, valid in lane 15 of the row
+__device__ __forceinline__ float row16_sum_15(float v) {
+    v += dpp_f<0x111>(v);
+    v += dpp_f<0x112>(v);
+    v += dpp_f<0x114>(v);
+    v += dpp_f<0x118>(v);
+    return v;
+}
+// max over each aligned group of 8 lanes, valid in all 8
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppMirror8>(v));
+    return v;
+}
+
+__device__ __forceinline__ float swiglu(float g, float u) {
+    const float gb = bf16r(g);
+    const float s = bf16r(__fdiv_rn(gb, 1.0f + expf(-gb)));
+    return bf16r(s * bf16r(u));
+}
+
+// A zero the compiler cannot see through: address arithmetic that uses it is
+// recomputed where it is needed instead of being hoisted out of the layer
+// loop, which would keep ~100 loop-invariant offsets live in registers.
+__device__ __forceinline__ int opaque_zero() {
+    int z = 0;
+    asm volatile("" : "+s"(z));
+    return z;
+}
+__device__ __forceinline__ int opaque_v(int x) {   // per-lane value, recomputed at each use
+    asm volatile("" : "+v"(x));
+    return x;
 }
 
 }  // namespace
 
 struct vxm_player {
     const int8_t *qkv_qs, *o_qs, *gu_qs, *d_qs;
-    const uint16_t *qkv_dg, *o_dg, *gu_dg, *d_dg;
+    const uint16_t *qkv_d, *o_d, *gu_d, *d_d;   // natural scale layout [rows][k/32]
     const float *g_in, *g_post;
     uint16_t *kc, *vc;
 };
@@ -97,97 +284,111 @@ struct vxm_pparams {
     float *x;          // [H] input of layer 0 and output (after the final norm)
     // tagged channels, each kRep replicas of rep_stride(words) words
     uint64_t *xb;      // 2 x [H/2] layer inputs (BF16 pairs), by layer parity
-    uint64_t *qkvb;    // [(QD + 2 KVD)/2] q, k (rope'd, pair-interleaved per head) and v (BF16 pairs)
+    uint64_t *qkvb;    // [NQKV/2] q, k (rope'd, pair-interleaved per head) and v (BF16 pairs)
     uint64_t *attb;    // [QD] attention output (fp32)
     uint64_t *h1b;     // [H/2] BF16 pairs
     uint64_t *pb;      // [F/2] BF16 pairs
+    const int8_t *dummy_q;     // 1 KiB of zeros: loads of units a wave does not own
+    const uint16_t *dummy_d;   // 32 zero scales
     int *err;
     const float *ff;
     float theta_scale, eps, res_scale;
     int pos, cap, no_rope;
     uint32_t epoch;
+#ifdef VXM_PERSISTENT_TRACE
+    uint64_t *trace;
+    int trace_stride;
+#endif
 };
 
 namespace {
 
-// LDS layout (dynamic): floats, then int8 quants (16-byte aligned).
-template <int H, int QD, int F, int HD>
-struct Lds {
-    static constexpr int KMAX = (H > QD ? (H > F ? H : F) : (QD > F ? QD : F));
-    static constexpr int XS = 0;                  // x of the layer            [H]
-    static constexpr int H1 = XS + H;             // h1 / normed-x scratch     [H]
-    static constexpr int GN = H1 + H;             // RMSNorm gain of the phase [H]
-    static constexpr int XD = GN + H;             // activation block scales   [KMAX/32]
-    static constexpr int CS = XD + KMAX / 32;     // rope cos/sin              [HD]
-    static constexpr int AQ = CS + HD;            // attention q, k, v         [3 HD]
-    static constexpr int RED = AQ + 3 * HD;       // reductions / partials     [2 kThreads]
-    static constexpr int SC = RED + 2 * kThreads; // scores / staged vectors   [max(cap + 1, KMAX)]
-    __host__ __device__ static int sc_len(int cap) { return cap + 1 > KMAX ? cap + 1 : KMAX; }
-    __host__ __device__ static int xq_off(int cap) { return ((SC + sc_len(cap)) * 4 + 15) & ~15; }
-    __host__ __device__ static int bytes(int cap) { return xq_off(cap) + KMAX; }
-};
+// The layer table through the constant address space: the compiler then
+// reads it with scalar loads (counted by lgkmcnt).  A vector load of a
+// pointer would be counted by vmcnt, which retires in order, so waiting for
+// it would also wait for every weight load in flight.
+typedef const __attribute__((address_space(4))) vxm_player *vxm_ptab;
+__device__ __forceinline__ vxm_ptab layer_tab(const vxm_pparams &p) { return (vxm_ptab)p.layers; }
 
-// Wave 0 polls n tagged words; word i at src(i); put(i, payload) stores the
-// payload into LDS.  All loads of a round are issued before any is checked.
-// Sets *bail on timeout or when another workgroup aborted.
-template <int PER, typename Src, typename Put>
-__device__ void poll_words(Src src, int n, uint32_t tag, Put put, int *err, int *bail) {
+__device__ __forceinline__ bool give_up(const vxm_pparams &p, int &it, int *bail) {
+    if (++it > kSpin || __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+        __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *bail = 1;
+        return true;
+    }
+    return false;
+}
+
+// Wave 0: read the n tagged words src[0..n) (lane l owns words l + 64k, all
+// loads of a round in flight) into LDS: PAIRS unpacks two BF16 values per
+// word to dst[2i], dst[2i+1], otherwise one fp32 to dst[i].  Words whose tag
+// is not yet `tag` are read again next round.  Returns this lane's sum of
+// the squares of its values in double (exact for BF16-valued inputs).
+template <int NPL, bool PAIRS>
+__device__ double read_words(const vxm_pparams &p, const uint64_t *src, int n, uint32_t tag, float *dst, int *bail) {
+    static_assert(NPL <= 64, "words per lane");
     const int lane = threadIdx.x & 63;
-    uint64_t w[PER];
-    bool done[PER];
+    uint64_t pending = 0;
 #pragma unroll
-    for (int k = 0; k < PER; k++) done[k] = lane + k * 64 >= n;
+    for (int k = 0; k < NPL; k++)
+        if (lane + 64 * k < n) pending |= 1ull << k;
+    double ss = 0.0;
     int it = 0;
     while (true) {
+        uint64_t w[NPL];
 #pragma unroll
-        for (int k = 0; k < PER; k++)
-            if (!done[k]) w[k] = get_word(src(lane + k * 64));
-        bool all = true;
+        for (int k = 0; k < NPL; k++)
+            if (pending & (1ull << k)) w[k] = get_word(src + lane + 64 * k);
 #pragma unroll
-        for (int k = 0; k < PER; k++) {
-            if (!done[k]) {
-                if ((uint32_t)(w[k] >> 32) == tag) {
-                    put(lane + k * 64, (uint32_t)w[k]);
-                    done[k] = true;
+        for (int k = 0; k < NPL; k++) {
+            if ((pending & (1ull << k)) && (uint32_t)(w[k] >> 32) == tag) {
+                const uint32_t v = (uint32_t)w[k];
+                const int i = lane + 64 * k;
+                if (PAIRS) {
+                    const float a = __uint_as_float(v << 16), b = __uint_as_float(v & 0xffff0000u);
+                    *(float2 *)(dst + 2 * i) = make_float2(a, b);
+                    ss += (double)(a * a) + (double)(b * b);
                 } else {
-                    all = false;
+                    dst[i] = __uint_as_float(v);
                 }
+                pending &= ~(1ull << k);
             }
         }
-        if (all) break;
-        if (++it > kSpin || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *bail = 1;
-            break;
-        }
+        if (__all(pending == 0)) break;
+        if (give_up(p, it, bail)) break;
         __builtin_amdgcn_s_sleep(1);
+    }
+    return ss;
+}
+
+// Wave 0: wait until the first word of each of the n producers (word i * stride)
+// carries tag.  Used where the wait is long (the attention output), so that
+// 240 waiting workgroups read 16 words per round instead of 2048.
+__device__ void wait_sentinels(const vxm_pparams &p, const uint64_t *src, int n, int stride, uint32_t tag,
+                               int *bail) {
+    const int lane = threadIdx.x & 63;
+    bool done = lane >= n;
+    int it = 0;
+    while (true) {
+        if (!done) done = (uint32_t)(get_word(src + lane * stride) >> 32) == tag;
+        if (__all(done)) return;
+        if (give_up(p, it, bail)) return;
+        __builtin_amdgcn_s_sleep(2);
     }
 }
 
-// Wave 0: BF16-pair words -> dst floats (2 per word)
-template <int PER>
-__device__ void poll_pairs(const uint64_t *src, int nwords, uint32_t tag, float *dst, int *err, int *bail) {
-    poll_words<PER>([src](int i) { return src + i; }, nwords, tag,
-                    [dst](int i, uint32_t v) {
-                        dst[2 * i] = __uint_as_float(v << 16);
-                        dst[2 * i + 1] = __uint_as_float(v & 0xffff0000u);
-                    },
-                    err, bail);
-}
-
-// Wave 0: plain copy of n floats (gains) into LDS
-__device__ void stage_f32(const float *src, int n, float *dst) {
+// Wave 0: plain copy of n floats (gains) into LDS, n % 256 == 0
+__device__ __forceinline__ void stage_f32(const float *src, int n, float *dst) {
     const int lane = threadIdx.x & 63;
     for (int i = lane * 4; i < n; i += 256) *(float4 *)(dst + i) = *(const float4 *)(src + i);
 }
 
 __device__ __forceinline__ double wg_sum_d(double v, float *red) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    v = wave_sum_63_d(v);
     double *r = (double *)red;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) r[threadIdx.x >> 6] = v;
-    __syncthreads();
+    lds_barrier();
+    if ((threadIdx.x & 63) == 63) r[threadIdx.x >> 6] = v;
+    lds_barrier();
     double t = 0.0;
 #pragma unroll
     for (int i = 0; i < kWaves; i++) t += r[i];
@@ -195,146 +396,351 @@ __device__ __forceinline__ double wg_sum_d(double v, float *red) {
 }
 
 __device__ __forceinline__ float wg_max_f(float v, float *red) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
+    v = wave_max_63(v);
+    lds_barrier();
+    if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = v;
+    lds_barrier();
     float t = red[0];
 #pragma unroll
     for (int i = 1; i < kWaves; i++) t = fmaxf(t, red[i]);
     return t;
 }
 
-// Q8_0 (x86 rule) of n values in LDS (n % 32 == 0): 8 values per thread, 4 threads per block.
+// Q8_0 (x86 rule: id = 127/amax, round half even) of 4 values held by each
+// lane of an aligned group of 8 lanes (one 32-value block); writes the four
+// quants and, from the group's first lane, the fp16-rounded block scale.
+__device__ __forceinline__ void quant4(const float v[4], int8_t *xq4, float *xd1, bool first) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = max8(amax);
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float q = fminf(fmaxf(rintf(v[i] * id), -128.0f), 127.0f);
+        w |= (uint32_t)(uint8_t)(int8_t)(int)q << (8 * i);
+    }
+    *(uint32_t *)xq4 = w;
+    if (first) *xd1 = vxm_h2f(vxm_f2h(d));
+}
+
+// Q8_0 of n values in LDS (n % 32 == 0), 4 values per thread.
 __device__ void quantize_lds(const float *src, int n, int8_t *xq, float *xd) {
-    for (int base = threadIdx.x * 8; base < n; base += kThreads * 8) {
-        float v[8];
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            v[i] = src[base + i];
-            amax = fmaxf(amax, fabsf(v[i]));
-        }
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        const float d = __fdiv_rn(amax, 127.0f);
-        const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float q = fminf(fmaxf(rintf(v[i] * id), -128.0f), 127.0f);
-            const uint32_t b = (uint32_t)(uint8_t)(int8_t)(int)q;
-            if (i < 4) lo |= b << (8 * i);
-            else hi |= b << (8 * (i - 4));
-        }
-        *(uint2 *)(xq + base) = make_uint2(lo, hi);
-        if ((threadIdx.x & 3) == 0) xd[base / 32] = vxm_h2f(vxm_f2h(d));   // the fp16-rounded scale
+    for (int base = threadIdx.x * 4; base < n; base += kThreads * 4) {
+        const float4 a = *(const float4 *)(src + base);
+        const float v[4] = {a.x, a.y, a.z, a.w};
+        quant4(v, xq + base, xd + base / 32, (threadIdx.x & 7) == 0);
     }
 }
 
-// vcpm_rms_norm of src (LDS) with gain (LDS): BF16(BF16(x*scale)*g) into dst (LDS).
+// vcpm_rms_norm (src/minicpm4.c:132-152) fused with the Q8_0 of its output:
+// y = BF16(BF16(x * sc) * g), sc = 1 / sqrt(sum(x^2) / n + eps), 4 values per
+// thread, n <= 4 * kThreads.  sumsq is the exact double sum of squares.
+template <int N>
+__device__ __forceinline__ void norm_quant(const float *x, const float *g, double sumsq, float eps, int8_t *xq,
+                                           float *xd) {
+    const float mean = (float)(sumsq * (1.0 / (double)N));   // N is a power of two: exact
+    const float sc = __fdiv_rn(1.0f, __fsqrt_rn(mean + eps));
+    const int base = threadIdx.x * 4;
+    if (base < N) {
+        const float4 a = *(const float4 *)(x + base), b = *(const float4 *)(g + base);
+        const float v[4] = {bf16r(bf16r(a.x * sc) * b.x), bf16r(bf16r(a.y * sc) * b.y),
+                            bf16r(bf16r(a.z * sc) * b.z), bf16r(bf16r(a.w * sc) * b.w)};
+        quant4(v, xq + base, xd + base / 32, (threadIdx.x & 7) == 0);
+    }
+}
+
+// vcpm_rms_norm of src (LDS) with gain (LDS) into dst (LDS), all threads.
 __device__ void rmsnorm_lds(const float *src, const float *gain, int n, float eps, float *dst, float *red) {
     double ss = 0.0;
     for (int i = threadIdx.x; i < n; i += kThreads) ss += (double)(src[i] * src[i]);
     const double tot = wg_sum_d(ss, red);
     const float mean = (float)(tot / (double)n);
     const float sc = __fdiv_rn(1.0f, __fsqrt_rn(mean + eps));
-    for (int i = threadIdx.x; i < n; i += kThreads) dst[i] = vxm_bf16(vxm_bf16(src[i] * sc) * gain[i]);
-    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += kThreads) dst[i] = bf16r(bf16r(src[i] * sc) * gain[i]);
 }
 
-template <int NR, int C>
-__device__ __forceinline__ void load_rows(const int8_t *qs, const uint16_t *dg, const int (&rows)[NR],
-                                          v4i (&w)[NR][C], uint32_t (&d)[NR][C]) {
-    const int lane = threadIdx.x & 63;
-    const int pair = lane >> 1;
-#pragma unroll
-    for (int r = 0; r < NR; r++) {
-        const int8_t *p = qs + (int64_t)rows[r] * (C * 1024) + lane * 16;
-#pragma unroll
-        for (int c = 0; c < C; c++) w[r][c] = __builtin_nontemporal_load((const v4i *)(p + c * 1024));
-        const uint16_t *q = dg + (int64_t)rows[r] * (C * 32) + pair * C;
-#pragma unroll
-        for (int c = 0; c < C; c++) d[r][c] = __builtin_nontemporal_load(q + c);
+// ---- the weight ring ---------------------------------------------------------
+// Slot s of a compute wave's per-layer schedule belongs to phase ph(s) and is
+// its k-th unit: workgroup-local unit u = ci + 7k (ci = compute wave index).
+template <class S, int s>
+struct Slot {
+    static constexpr int ph = s < S::OC ? 0 : s < S::OD ? 1 : s < S::OE ? 2 : 3;
+    static constexpr int k = s - (ph == 0 ? S::OA : ph == 1 ? S::OC : ph == 2 ? S::OD : S::OE);
+    static constexpr int U = ph == 0 ? S::UA : ph == 1 ? S::UC : ph == 2 ? S::UD : S::UE;
+    static constexpr int C = ph == 0 ? S::CA : ph == 1 ? S::CC : ph == 2 ? S::CD : S::CE;
+    static constexpr int R = ph == 0 ? S::RA : ph == 1 ? S::RC : ph == 2 ? S::RD : S::RE;
+};
+
+template <class S>
+struct Ring {
+    v4i q[S::RING];
+    uint32_t d[S::RING];
+};
+
+// The ring's loads are issued as inline asm so that the compiler does not
+// track them: its wait insertion cannot count pending loads across the phase
+// branches and the layer loop and would drain the whole ring (vmcnt(0)) at
+// every phase.  Before a unit is used, ring_wait waits until at most N vector
+// memory instructions of the wave are pending; in steady state the 2(P-1)
+// loads of the next P-1 units were issued after the unit's own two, and
+// vmcnt retires in order, so the unit's data is in.  Other vector memory
+// instructions of the wave only make the wait stricter.  The "+v" operands
+// tie the registers to the wait, so no use is scheduled before it.
+__device__ __forceinline__ void ring_ld16(v4i &dst, const void *ptr) {
+    asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(dst) : "v"(ptr));
+}
+__device__ __forceinline__ void ring_ld2(uint32_t &dst, const void *ptr) {
+    asm volatile("global_load_ushort %0, %1, off nt" : "=v"(dst) : "v"(ptr));
+}
+template <int N>
+__device__ __forceinline__ void ring_wait(v4i &q, uint32_t &d) {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(q), "+v"(d) : "n"(N));
+}
+
+// Issue the loads of slot s for layer l (dummy loads past the last layer or
+// for a unit the wave does not own, so every wave issues the same count).
+template <class S, int s>
+__device__ __forceinline__ void ring_issue(Ring<S> &rg, const vxm_pparams &p, int l, int wg, int ci, int lane) {
+    using T = Slot<S, s>;
+    const int u = ci + opaque_zero() + kCW * T::k;
+    const int lq = opaque_v(lane * 16), ld = opaque_v(lane >> 1);
+    const int8_t *q = p.dummy_q + lq;
+    const uint16_t *d = p.dummy_d + ld;
+    if (u < T::U && l < p.n_layers) {
+        vxm_ptab Ly = layer_tab(p) + l;
+        const int row = (wg + opaque_zero()) * T::R + u / T::C, c = u % T::C;
+        constexpr int K = T::C * 1024;
+        const int8_t *bq = T::ph == 0 ? Ly->qkv_qs : T::ph == 1 ? Ly->o_qs : T::ph == 2 ? Ly->gu_qs : Ly->d_qs;
+        const uint16_t *bd = T::ph == 0 ? Ly->qkv_d : T::ph == 1 ? Ly->o_d : T::ph == 2 ? Ly->gu_d : Ly->d_d;
+        q = bq + ((int64_t)row * K + c * 1024) + lq;
+        d = bd + ((int64_t)row * (K / 32) + c * 32) + ld;
+    }
+    rg.q[s % S::RING] = __builtin_nontemporal_load((const v4i *)q);
+    rg.d[s % S::RING] = __builtin_nontemporal_load(d);
+}
+
+template <class S, int... ss>
+__device__ __forceinline__ void ring_prime(Ring<S> &rg, const vxm_pparams &p, int wg, int ci, int lane,
+                                           std::integer_sequence<int, ss...>) {
+    (ring_issue<S, ss>(rg, p, 0, wg, ci, lane), ...);
+}
+
+// Consume the K slots of one phase starting at slot OFF: dot product of each
+// unit with the quantized activation in LDS, partial to part[u]; after each
+// unit, the loads P positions ahead are issued.
+template <class S, int OFF, int K, int k = 0>
+__device__ __forceinline__ void ring_phase(Ring<S> &rg, const vxm_pparams &p, int l, int wg, int ci, int lane,
+                                           const int8_t *xq, const float *xd, float *part) {
+    if constexpr (k < K) {
+        constexpr int s = OFF + k;
+        using T = Slot<S, s>;
+        const int u = ci + kCW * k;
+        const int c = u % T::C;
+        const v4i xv = *(const v4i *)(xq + c * 1024 + lane * 16);
+        const float xs = xd[c * 32 + (lane >> 1)];
+        int si = dot16(rg.q[s % S::RING], xv);
+        si += dpp_i<kDppXor1>(si);                  // exact int32 sum of the lane pair's block
+        float a = (float)si * (vxm_h2f((uint16_t)rg.d[s % S::RING]) * xs);
+        a = wave_sum_63((lane & 1) ? 0.0f : a);     // one term per block
+        if (lane == 63 && u < T::U) part[u] = a;
+        constexpr int sn = (s + S::P) % S::NS;
+        ring_issue<S, sn>(rg, p, l + (s + S::P >= S::NS ? 1 : 0), wg, ci, lane);
+        ring_phase<S, OFF, K, k + 1>(rg, p, l, wg, ci, lane, xq, xd, part);
     }
 }
 
-template <int NR, int C>
-__device__ __forceinline__ void dot_rows(const v4i (&w)[NR][C], const uint32_t (&d)[NR][C], const int8_t *xq,
-                                         const float *xd, float (&out)[NR]) {
-    const int lane = threadIdx.x & 63;
-    const int pair = lane >> 1;
-    v4i xv[C];
-    float xs[C];
-#pragma unroll
-    for (int c = 0; c < C; c++) {
-        xv[c] = *(const v4i *)(xq + c * 1024 + lane * 16);
-        xs[c] = xd[c * 32 + pair];
-    }
-#pragma unroll
-    for (int r = 0; r < NR; r++) {
-        float a = 0.0f;
-#pragma unroll
-        for (int c = 0; c < C; c++) {
-            int s = dot16(w[r][c], xv[c]);
-            s += __shfl_xor(s, 1, 64);
-            a += (float)s * (vxm_h2f((uint16_t)d[r][c]) * xs[c]);
-        }
-        out[r] = pair_sum(a);
-    }
-}
-
-// Unit u of a phase owns rows [R*u, R*u + R); rows of invalid units are
-// clamped to the last unit (loaded, never stored).
-template <int U, int R>
-__device__ __forceinline__ void unit_rows(int cw, int W, int n_units, int (&rows)[U * R], bool (&valid)[U],
-                                          int (&unit)[U]) {
-#pragma unroll
-    for (int k = 0; k < U; k++) {
-        const int u = cw + k * W;
-        valid[k] = u < n_units;
-        unit[k] = valid[k] ? u : n_units - 1;
-#pragma unroll
-        for (int r = 0; r < R; r++) rows[k * R + r] = unit[k] * R + r;
-    }
-}
-
-__device__ __forceinline__ float swiglu(float g, float u) {
-    const float gb = vxm_bf16(g);
-    const float s = vxm_bf16(__fdiv_rn(gb, 1.0f + expf(-gb)));
-    return vxm_bf16(s * vxm_bf16(u));
-}
-
-
-// The whole decode for one wave type.  POLLER = wave 0 of the workgroup
-// (polls inputs, stages gains); otherwise a compute wave (owns weight rows).
-// Both instantiations walk the same phase schedule and execute the same
-// __syncthreads() sequence; keeping them separate functions keeps the polling
-// registers and the weight registers out of each other's live ranges.
-template <bool POLLER, int H, int NH, int NKV, int HD, int F, int G>
-__device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int *bail) {
-    constexpr int QD = NH * HD, KVD = NKV * HD, NQKV = QD + 2 * KVD;
-    constexpr int W = G * kCW;                                   // compute waves in the grid
-    constexpr int CH = H / 1024, CQ = QD / 1024, CF = F / 1024;
-    constexpr int NA = NQKV / 2, NC = H / 2, ND = F / 2, NE = H / 2;   // output words per phase
-    constexpr int UA = (NA + W - 1) / W, UC = (NC + W - 1) / W, UD = (ND + W - 1) / W, UE = (NE + W - 1) / W;
-    constexpr int LPK = HD / 8, KPW = 64 / LPK;                  // attention: lanes per key, keys per wave
-    constexpr int KB = 8;                                        // attention: key loads in flight per lane
-    constexpr int SX = rep_stride(H / 2), SQ = rep_stride(NA), SAT = rep_stride(QD), SP = rep_stride(ND);
-    const int rp = blockIdx.x % kRep;                            // replica this workgroup polls
-    using L = Lds<H, QD, F, HD>;
-    static_assert(H % 1024 == 0 && QD % 1024 == 0 && F % 1024 == 0, "K must be a multiple of 1024");
-    static_assert(HD % 8 == 0 && HD <= 256 && 64 % LPK == 0, "head_dim");
-
-    float *xs = lds + L::XS, *h1s = lds + L::H1, *gn = lds + L::GN, *xd = lds + L::XD, *cs = lds + L::CS;
-    float *aq = lds + L::AQ, *red = lds + L::RED, *sc = lds + L::SC;
-    int8_t *xq = (int8_t *)lds + L::xq_off(p.cap);
-
+// Attention of query head h for layer l (vcpm_attention's gqa_group_attn,
+// src/minicpm4.c:232-248): wave 0 reads q_h, k_g, v_g; all waves then read
+// the f16 cache rows [0, pos) of group g, use the fresh k, v for row pos,
+// and publish the 128 fp32 outputs.  The group's first head appends k, v.
+template <class S>
+__device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int h, float *lds, int *bail) {
+    constexpr int QD = S::QD, KVD = S::KVD, HD = S::HD;
+    constexpr int SQ = rep_stride(S::NQKV / 2), SAT = rep_stride(QD);
+    constexpr int LPK = HD / 8, KPW = 64 / LPK;                  // lanes per key, keys per wave
+    constexpr int PERB = kWaves * KPW * kAttnKB;                 // keys per batch
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int cw = blockIdx.x * kCW + (POLLER ? 0 : wave - 1);
+    const int rp = blockIdx.x % kRep, g = h / S::QPK, pos = p.pos;
+    const uint32_t ep = p.epoch;
+    vxm_ptab Ly = layer_tab(p) + l;
+    float *aq = lds + S::L_AQ, *red = lds + S::L_RED, *sc = lds + S::L_SC;
+    if (wave == 0) {
+        // q_h and k_g (pair-interleaved: word w = dims w, w + HD/2) and v_g
+        // (natural pairs) -> aq[0..3HD) in natural order; lane l owns word w = l
+        // of each of the three parts
+        const uint64_t *qkvb = p.qkvb + rp * SQ;
+        const uint64_t *src[3] = {qkvb + h * (HD / 2), qkvb + (QD + g * HD) / 2, qkvb + (QD + KVD + g * HD) / 2};
+        const uint32_t tag = make_tag(ep, l, PH_QKV);
+        uint32_t pending = 7;
+        int it = 0;
+        while (true) {
+            uint64_t w[3];
+#pragma unroll
+            for (int k = 0; k < 3; k++)
+                if (pending & (1u << k)) w[k] = get_word(src[k] + lane);
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                if ((pending & (1u << k)) && (uint32_t)(w[k] >> 32) == tag) {
+                    const uint32_t v = (uint32_t)w[k];
+                    const float a = __uint_as_float(v << 16), b = __uint_as_float(v & 0xffff0000u);
+                    float *dst = aq + k * HD;
+                    if (k < 2) {
+                        dst[lane] = a;
+                        dst[lane + HD / 2] = b;
+                    } else {
+                        *(float2 *)(dst + 2 * lane) = make_float2(a, b);
+                    }
+                    pending &= ~(1u << k);
+                }
+            }
+            if (__all(pending == 0)) break;
+            if (give_up(p, it, bail)) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    lds_barrier();
+    if (*bail) return;
+    VXM_TS(threadIdx.x == 0, 3);
+    const float *qh = aq, *kcur = aq + HD, *vcur = aq + 2 * HD;
+    uint16_t *const kc = Ly->kc, *const vc = Ly->vc;
+    const uint16_t *kb = kc + (int64_t)g * p.cap * HD;
+    const uint16_t *vb = vc + (int64_t)g * p.cap * HD;
+    // KV append: the first query head of each group writes the f16 rows at pos
+    if (h % S::QPK == 0) {
+        uint16_t *kw = kc + ((int64_t)g * p.cap + pos) * HD;
+        uint16_t *vw = vc + ((int64_t)g * p.cap + pos) * HD;
+        for (int d = threadIdx.x; d < HD; d += kThreads) {
+            kw[d] = vxm_f2h(kcur[d]);
+            vw[d] = vxm_f2h(vcur[d]);
+        }
+    }
+    const int kv_len = pos + 1;
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
+    const int sub = lane % LPK, kin = lane / LPK;
+    float qv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) qv[i] = qh[sub * 8 + i];
+    // batch jb covers keys jb + (k * kWaves + wave) * KPW + kin, k < kAttnKB
+    float mx = -INFINITY;
+    for (int jb = 0; jb < kv_len; jb += PERB) {
+        uint4 raw[kAttnKB];
+#pragma unroll
+        for (int k = 0; k < kAttnKB; k++) {
+            const int j = jb + (k * kWaves + wave) * KPW + kin;
+            raw[k] = j < pos ? *(const uint4 *)(kb + (int64_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < kAttnKB; k++) {
+            const int j = jb + (k * kWaves + wave) * KPW + kin;
+            float kv8[8];
+            if (j == pos) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) kv8[i] = vxm_h2f(vxm_f2h(kcur[sub * 8 + i]));
+            } else {
+                const uint32_t wv[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    kv8[2 * i] = vxm_h2f((uint16_t)(wv[i] & 0xffffu));
+                    kv8[2 * i + 1] = vxm_h2f((uint16_t)(wv[i] >> 16));
+                }
+            }
+            float pt = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) pt += kv8[i] * qv[i];
+            pt = row16_sum_15(pt);
+            if (j < kv_len && sub == LPK - 1) {
+                const float s = pt * scale;
+                sc[j] = s;
+                mx = fmaxf(mx, s);
+            }
+        }
+    }
+    mx = wg_max_f(mx, red);
+    double sum = 0.0;
+    for (int j = threadIdx.x; j < kv_len; j += kThreads) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        sum += (double)e;
+    }
+    sum = wg_sum_d(sum, red);
+    const float inv = (float)(1.0 / sum);
+    for (int j = threadIdx.x; j < kv_len; j += kThreads) sc[j] = sc[j] * inv;
+    lds_barrier();
+    // out[d] = sum_j p_j v_j[d]: lane (kin, sub) accumulates dims sub*8..+8 over its keys
+    float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int jb = 0; jb < kv_len; jb += PERB) {
+        uint4 raw[kAttnKB];
+#pragma unroll
+        for (int k = 0; k < kAttnKB; k++) {
+            const int j = jb + (k * kWaves + wave) * KPW + kin;
+            raw[k] = j < pos ? *(const uint4 *)(vb + (int64_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < kAttnKB; k++) {
+            const int j = jb + (k * kWaves + wave) * KPW + kin;
+            if (j >= kv_len) continue;
+            const float pj = sc[j];
+            if (j == pos) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[i] += vxm_h2f(vxm_f2h(vcur[sub * 8 + i])) * pj;
+            } else {
+                const uint32_t wv[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    o[2 * i] += vxm_h2f((uint16_t)(wv[i] & 0xffffu)) * pj;
+                    o[2 * i + 1] += vxm_h2f((uint16_t)(wv[i] >> 16)) * pj;
+                }
+            }
+        }
+    }
+    // reduce over the KPW key lanes of the wave, then over waves (fixed order)
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int m = LPK; m < 64; m <<= 1) o[i] += __shfl_xor(o[i], m, 64);
+    lds_barrier();   // red is reused below
+    if (kin == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) red[wave * HD + sub * 8 + i] = o[i];
+    }
+    lds_barrier();
+    const uint32_t tg = make_tag(ep, l, PH_ATT);
+    for (int t = threadIdx.x; t < HD * kRep; t += kThreads) {
+        const int d = t % HD, r = t / HD;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) v += red[w * HD + d];
+        put_word(p.attb + r * SAT + h * HD + d, __float_as_uint(v), tg);
+    }
+    VXM_TS(threadIdx.x == 0, 4);
+}
+
+// The whole decode.  Wave 0 reads the inputs of each phase (and forms
+// RMSNorm's sum of squares on the way); waves 1..7 stream weights and
+// publish the outputs.  All waves walk the same phase schedule and barrier
+// sequence.
+template <class S>
+__device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int *bail) {
+    constexpr int H = S::H, QD = S::QD, KVD = S::KVD, HD = S::HD, F = S::F, NH = S::NH;
+    constexpr int SX = rep_stride(H / 2), SQ = rep_stride(S::NQKV / 2), SAT = rep_stride(QD), SP = rep_stride(F / 2);
+    const int wg = blockIdx.x;
+    const int rp = wg % kRep;
+    float *xs = lds + S::L_XS, *h1s = lds + S::L_H1, *gn = lds + S::L_GN, *big = lds + S::L_BIG;
+    float *xd = lds + S::L_XD, *cs = lds + S::L_CS, *part = lds + S::L_PART, *red = lds + S::L_RED;
+    double *ssq = (double *)red;   // sum of squares from the reading wave
+    int8_t *xq = (int8_t *)lds + S::xq_off(p.cap);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const bool reader = wave == 0;
+    const int ci = __builtin_amdgcn_readfirstlane(wave - 1);   // compute wave index (uniform)
+    const int t = threadIdx.x - 64;                             // compute thread index
     const int pos = p.pos;
     const uint32_t ep = p.epoch;
+    // the query head this workgroup attends for, or -1
+    int head = -1;
+    for (int h = 0; h < NH; h++)
+        if (attn_wg<S>(h) == wg) head = h;
 
     // rope cos/sin of this token's position (ggml_rope_ext NEOX, iterative theta)
     for (int i = threadIdx.x; i < HD / 2; i += kThreads) {
@@ -345,297 +751,173 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         cs[2 * i + 1] = sinf(th);
     }
 
-    // compute waves: fixed unit ownership and the weight registers
-    int rA[2 * UA], rC[2 * UC], rD[4 * UD], rE[2 * UE];
-    bool vA[UA], vC[UC], vD[UD], vE[UE];
-    int uA[UA], uC[UC], uD[UD], uE[UE];
-    v4i wA[POLLER ? 1 : 2 * UA][CH], wC[POLLER ? 1 : 2 * UC][CQ], wD[POLLER ? 1 : 4 * UD][CH],
-        wE[POLLER ? 1 : 2 * UE][CF];
-    uint32_t dA[POLLER ? 1 : 2 * UA][CH], dC[POLLER ? 1 : 2 * UC][CQ], dD[POLLER ? 1 : 4 * UD][CH],
-        dE[POLLER ? 1 : 2 * UE][CF];
-    if constexpr (!POLLER) {
-        unit_rows<UA, 2>(cw, W, NA, rA, vA, uA);
-        unit_rows<UC, 2>(cw, W, NC, rC, vC, uC);
-        unit_rows<UD, 4>(cw, W, ND, rD, vD, uD);
-        unit_rows<UE, 2>(cw, W, NE, rE, vE, uE);
-        load_rows<2 * UA, CH>(p.layers[0].qkv_qs, p.layers[0].qkv_dg, rA, wA, dA);
-    }
+    Ring<S> rg;
+    if (!reader) ring_prime<S>(rg, p, wg, ci, lane, std::make_integer_sequence<int, S::P>{});
 
     for (int l = 0; l < p.n_layers; l++) {
-        const vxm_player &Ly = p.layers[l];
+        vxm_ptab Ly = layer_tab(p) + l;
         // ---------------- A: norm + QKV + rope ----------------
-        if constexpr (POLLER) {
-            stage_f32(Ly.g_in, H, gn);
+        if (reader) {
+            stage_f32(Ly->g_in, H, gn);
+            double ss = 0.0;
             if (l == 0) {
-                for (int i = lane * 4; i < H; i += 256) *(float4 *)(xs + i) = *(const float4 *)(p.x + i);
+                for (int i = lane * 4; i < H; i += 256) {
+                    const float4 v = *(const float4 *)(p.x + i);
+                    *(float4 *)(xs + i) = v;
+                    ss += (double)(v.x * v.x) + (double)(v.y * v.y) + (double)(v.z * v.z) + (double)(v.w * v.w);
+                }
             } else {
-                poll_pairs<(H / 2 + 63) / 64>(p.xb + ((l & 1) * kRep + rp) * SX, H / 2, make_tag(ep, l, PH_X), xs,
-                                              p.err, bail);
+                ss = read_words<cdiv(H / 2, 64), true>(p, p.xb + ((l & 1) * kRep + rp) * SX, H / 2,
+                                                       make_tag(ep, l, PH_X), xs, bail);
             }
+            ss = wave_sum_63_d(ss);
+            if (lane == 63) ssq[0] = ss;
         }
-        __syncthreads();
+        lds_barrier();
         if (*bail) return;
-        if constexpr (!POLLER) load_rows<2 * UC, CQ>(Ly.o_qs, Ly.o_dg, rC, wC, dC);
-        rmsnorm_lds(xs, gn, H, p.eps, h1s, red);
-        quantize_lds(h1s, H, xq, xd);
-        __syncthreads();
-        if constexpr (!POLLER) {
-            float out[2 * UA];
-            dot_rows<2 * UA, CH>(wA, dA, xq, xd, out);
-            if (lane < kRep) {
-                const uint32_t tg = make_tag(ep, l, PH_QKV);
+        VXM_TS(threadIdx.x == 0, 0);
+        norm_quant<H>(xs, gn, ssq[0], p.eps, xq, xd);
+        lds_barrier();
+        if (!reader) ring_phase<S, S::OA, S::SA>(rg, p, l, wg, ci, lane, xq, xd, part);
+        lds_barrier();
+        VXM_TS(threadIdx.x == 0, 1);
+        if (!reader && t < S::RA / 2 * kRep) {
+            // RA/2 output words x kRep replicas, one store per thread
+            const int wi = t / kRep, r = t % kRep;
+            const int gw = wg * (S::RA / 2) + wi;        // global word = row pair
+            float y[2];
 #pragma unroll
-                for (int k = 0; k < UA; k++) {
-                    if (!vA[k]) continue;
-                    const int row = 2 * uA[k];
-                    const float x0 = vxm_bf16(out[2 * k]), x1 = vxm_bf16(out[2 * k + 1]);
-                    float y0 = x0, y1 = x1;
-                    if (row < QD + KVD && !p.no_rope) {
-                        const int i = (row % HD) / 2;
-                        const float c = cs[2 * i], s = cs[2 * i + 1];
-                        y0 = vxm_bf16(x0 * c - x1 * s);
-                        y1 = vxm_bf16(x0 * s + x1 * c);
-                    }
-                    put_word(p.qkvb + lane * SQ + uA[k], pack_bf16x2(y0, y1), tg);
-                }
+            for (int j = 0; j < 2; j++) {
+                float a = 0.0f;
+#pragma unroll
+                for (int c = 0; c < S::CA; c++) a += part[(2 * wi + j) * S::CA + c];
+                y[j] = bf16r(a);
             }
+            float y0 = y[0], y1 = y[1];
+            if (2 * gw < QD + KVD && !p.no_rope) {
+                const int i = gw % (HD / 2);
+                const float c = cs[2 * i], s = cs[2 * i + 1];
+                y0 = bf16r(y[0] * c - y[1] * s);
+                y1 = bf16r(y[0] * s + y[1] * c);
+            }
+            put_word(p.qkvb + r * SQ + gw, pack_bf16x2(y0, y1), make_tag(ep, l, PH_QKV));
         }
-        // ---------------- B: attention, workgroup h = query head h ----------------
-        if (blockIdx.x < NH) {
-            const int h = blockIdx.x, g = h / (NH / NKV);
-            if constexpr (POLLER) {
-                // q_h and k_g (pair-interleaved: word w = dims w, w + HD/2) and
-                // v_g (natural pairs) -> aq[0..3HD) in natural order
-                const uint64_t *qkvb = p.qkvb + rp * SQ;
-                poll_words<(3 * HD / 2 + 63) / 64>(
-                    [qkvb, h, g](int i) {
-                        const int part = i / (HD / 2), w = i % (HD / 2);
-                        return part == 0 ? qkvb + h * (HD / 2) + w
-                                         : part == 1 ? qkvb + (QD + g * HD) / 2 + w : qkvb + (QD + KVD + g * HD) / 2 + w;
-                    },
-                    3 * HD / 2, make_tag(ep, l, PH_QKV),
-                    [aq](int i, uint32_t v) {
-                        const int part = i / (HD / 2), w = i % (HD / 2);
-                        const float a = __uint_as_float(v << 16), b = __uint_as_float(v & 0xffff0000u);
-                        float *dst = aq + part * HD;
-                        if (part < 2) {
-                            dst[w] = a;
-                            dst[w + HD / 2] = b;
-                        } else {
-                            dst[2 * w] = a;
-                            dst[2 * w + 1] = b;
-                        }
-                    },
-                    p.err, bail);
-            }
-            __syncthreads();
+        // ---------------- B: attention, one workgroup per query head ----------------
+        if (head >= 0) {
+            attention_phase<S>(p, l, head, lds, bail);
             if (*bail) return;
-            const float *qh = aq, *kcur = aq + HD, *vcur = aq + 2 * HD;
-            const uint16_t *kb = Ly.kc + (int64_t)g * p.cap * HD;
-            const uint16_t *vb = Ly.vc + (int64_t)g * p.cap * HD;
-            // KV append: the first query head of each group writes the whole f16
-            // rows of K and V at pos (one workgroup per row).
-            if (h % (NH / NKV) == 0) {
-                uint16_t *kw = Ly.kc + ((int64_t)g * p.cap + pos) * HD;
-                uint16_t *vw = Ly.vc + ((int64_t)g * p.cap + pos) * HD;
-                for (int d = threadIdx.x; d < HD; d += kThreads) {
-                    kw[d] = vxm_f2h(kcur[d]);
-                    vw[d] = vxm_f2h(vcur[d]);
-                }
-            }
-            const int kv_len = pos + 1;
-            const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
-            const int sub = lane % LPK, kin = lane / LPK;
-            float qv[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) qv[i] = qh[sub * 8 + i];
-            // batch jb covers keys jb + (k * kWaves + wave) * KPW + kin, k < KB
-            constexpr int PERB = kWaves * KPW * KB;
-            float mx = -INFINITY;
-            for (int jb = 0; jb < kv_len; jb += PERB) {
-                uint4 raw[KB];
-#pragma unroll
-                for (int k = 0; k < KB; k++) {
-                    const int j = jb + (k * kWaves + wave) * KPW + kin;
-                    raw[k] = j < pos ? *(const uint4 *)(kb + (int64_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
-                }
-#pragma unroll
-                for (int k = 0; k < KB; k++) {
-                    const int j = jb + (k * kWaves + wave) * KPW + kin;
-                    float kv8[8];
-                    if (j == pos) {
-#pragma unroll
-                        for (int i = 0; i < 8; i++) kv8[i] = vxm_h2f(vxm_f2h(kcur[sub * 8 + i]));
-                    } else {
-                        const uint32_t wv[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            kv8[2 * i] = vxm_h2f((uint16_t)(wv[i] & 0xffffu));
-                            kv8[2 * i + 1] = vxm_h2f((uint16_t)(wv[i] >> 16));
-                        }
-                    }
-                    float part = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < 8; i++) part += kv8[i] * qv[i];
-#pragma unroll
-                    for (int m = 1; m < LPK; m <<= 1) part += __shfl_xor(part, m, 64);
-                    if (j < kv_len && sub == 0) {
-                        const float s = part * scale;
-                        sc[j] = s;
-                        mx = fmaxf(mx, s);
-                    }
-                }
-            }
-            mx = wg_max_f(mx, red);
-            double sum = 0.0;
-            for (int j = threadIdx.x; j < kv_len; j += kThreads) {
-                const float e = expf(sc[j] - mx);
-                sc[j] = e;
-                sum += (double)e;
-            }
-            sum = wg_sum_d(sum, red);
-            const float inv = (float)(1.0 / sum);
-            for (int j = threadIdx.x; j < kv_len; j += kThreads) sc[j] = sc[j] * inv;
-            __syncthreads();
-            // out[d] = sum_j p_j v_j[d]: lane (kin, sub) accumulates dims sub*8..+8 over its keys
-            float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            for (int jb = 0; jb < kv_len; jb += PERB) {
-                uint4 raw[KB];
-#pragma unroll
-                for (int k = 0; k < KB; k++) {
-                    const int j = jb + (k * kWaves + wave) * KPW + kin;
-                    raw[k] = j < pos ? *(const uint4 *)(vb + (int64_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
-                }
-#pragma unroll
-                for (int k = 0; k < KB; k++) {
-                    const int j = jb + (k * kWaves + wave) * KPW + kin;
-                    if (j >= kv_len) continue;
-                    const float pj = sc[j];
-                    if (j == pos) {
-#pragma unroll
-                        for (int i = 0; i < 8; i++) o[i] += vxm_h2f(vxm_f2h(vcur[sub * 8 + i])) * pj;
-                    } else {
-                        const uint32_t wv[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            o[2 * i] += vxm_h2f((uint16_t)(wv[i] & 0xffffu)) * pj;
-                            o[2 * i + 1] += vxm_h2f((uint16_t)(wv[i] >> 16)) * pj;
-                        }
-                    }
-                }
-            }
-            // reduce over the KPW key lanes of the wave, then over waves (fixed order)
-#pragma unroll
-            for (int i = 0; i < 8; i++)
-#pragma unroll
-                for (int m = LPK; m < 64; m <<= 1) o[i] += __shfl_xor(o[i], m, 64);
-            if (kin == 0) {
-#pragma unroll
-                for (int i = 0; i < 8; i++) red[wave * HD + sub * 8 + i] = o[i];
-            }
-            __syncthreads();
-            const uint32_t tg = make_tag(ep, l, PH_ATT);
-            for (int d = threadIdx.x; d < HD; d += kThreads) {
-                float t = 0.0f;
-#pragma unroll
-                for (int w = 0; w < kWaves; w++) t += red[w * HD + d];
-#pragma unroll
-                for (int r = 0; r < kRep; r++) put_word(p.attb + r * SAT + h * HD + d, __float_as_uint(t), tg);
-            }
-            __syncthreads();
         }
         // ---------------- C: O rows + residual ----------------
-        if constexpr (POLLER) {
-            const uint64_t *attb = p.attb + rp * SAT;
-            poll_words<(QD + 63) / 64>([attb](int i) { return attb + i; }, QD, make_tag(ep, l, PH_ATT),
-                                       [sc](int i, uint32_t v) { sc[i] = __uint_as_float(v); }, p.err, bail);
+        if (reader) {
+            const uint64_t *src = p.attb + rp * SAT;
+            const uint32_t tag = make_tag(ep, l, PH_ATT);
+            wait_sentinels(p, src, NH, HD, tag, bail);
+            static_assert(QD % 128 == 0 && QD / 128 <= 24, "attention channel halves");
+            if (!*bail) read_words<QD / 128, false>(p, src, QD / 2, tag, big, bail);
+            if (!*bail) read_words<QD / 128, false>(p, src + QD / 2, QD / 2, tag, big + QD / 2, bail);
         }
-        __syncthreads();
+        lds_barrier();
         if (*bail) return;
-        if constexpr (!POLLER) load_rows<4 * UD, CH>(Ly.gu_qs, Ly.gu_dg, rD, wD, dD);
-        quantize_lds(sc, QD, xq, xd);
-        __syncthreads();
-        if constexpr (!POLLER) {
-            float out[2 * UC];
-            dot_rows<2 * UC, CQ>(wC, dC, xq, xd, out);
-            if (lane < kRep) {
-                const uint32_t tg = make_tag(ep, l, PH_H1);
+        VXM_TS(threadIdx.x == 0, 5);
+        quantize_lds(big, QD, xq, xd);
+        lds_barrier();
+        if (!reader) ring_phase<S, S::OC, S::SC>(rg, p, l, wg, ci, lane, xq, xd, part);
+        lds_barrier();
+        VXM_TS(threadIdx.x == 0, 6);
+        if (!reader && t < S::RC / 2 * kRep) {
+            const int wi = t / kRep, r = t % kRep;
+            const int row = wg * S::RC + 2 * wi;
+            float hh[2];
 #pragma unroll
-                for (int k = 0; k < UC; k++) {
-                    if (!vC[k]) continue;
-                    const int r = 2 * uC[k];
-                    float o0 = vxm_bf16(out[2 * k]), o1 = vxm_bf16(out[2 * k + 1]);
-                    if (p.res_scale != 1.0f) { o0 = o0 * p.res_scale; o1 = o1 * p.res_scale; }
-                    put_word(p.h1b + lane * SX + uC[k], pack_bf16x2(vxm_bf16(xs[r] + o0), vxm_bf16(xs[r + 1] + o1)),
-                             tg);
-                }
+            for (int j = 0; j < 2; j++) {
+                float a = 0.0f;
+#pragma unroll
+                for (int c = 0; c < S::CC; c++) a += part[(2 * wi + j) * S::CC + c];
+                float o = bf16r(a);
+                if (p.res_scale != 1.0f) o = o * p.res_scale;
+                hh[j] = bf16r(xs[row + j] + o);
             }
+            put_word(p.h1b + r * SX + row / 2, pack_bf16x2(hh[0], hh[1]), make_tag(ep, l, PH_H1));
         }
         // ---------------- D: post norm + gate/up + SwiGLU ----------------
-        if constexpr (POLLER) {
-            stage_f32(Ly.g_post, H, gn);
-            poll_pairs<(H / 2 + 63) / 64>(p.h1b + rp * SX, H / 2, make_tag(ep, l, PH_H1), h1s, p.err, bail);
+        if (reader) {
+            stage_f32(Ly->g_post, H, gn);
+            double ss = read_words<cdiv(H / 2, 64), true>(p, p.h1b + rp * SX, H / 2, make_tag(ep, l, PH_H1), h1s, bail);
+            ss = wave_sum_63_d(ss);
+            if (lane == 63) ssq[0] = ss;
         }
-        __syncthreads();
+        lds_barrier();
         if (*bail) return;
-        if constexpr (!POLLER) load_rows<2 * UE, CF>(Ly.d_qs, Ly.d_dg, rE, wE, dE);
-        rmsnorm_lds(h1s, gn, H, p.eps, sc, red);
-        quantize_lds(sc, H, xq, xd);
-        __syncthreads();
-        if constexpr (!POLLER) {
-            float out[4 * UD];
-            dot_rows<4 * UD, CH>(wD, dD, xq, xd, out);
-            if (lane < kRep) {
-                const uint32_t tg = make_tag(ep, l, PH_P);
+        VXM_TS(threadIdx.x == 0, 7);
+        norm_quant<H>(h1s, gn, ssq[0], p.eps, xq, xd);
+        lds_barrier();
+        if (!reader) ring_phase<S, S::OD, S::SD>(rg, p, l, wg, ci, lane, xq, xd, part);
+        lds_barrier();
+        VXM_TS(threadIdx.x == 0, 8);
+        if (!reader && t < S::RD / 4 * kRep) {
+            const int wi = t / kRep, r = t % kRep;
+            float v[4];
 #pragma unroll
-                for (int k = 0; k < UD; k++) {
-                    if (!vD[k]) continue;
-                    const float p0 = swiglu(out[4 * k], out[4 * k + 1]);
-                    const float p1 = swiglu(out[4 * k + 2], out[4 * k + 3]);
-                    put_word(p.pb + lane * SP + uD[k], pack_bf16x2(p0, p1), tg);
-                }
+            for (int j = 0; j < 4; j++) {
+                float a = 0.0f;
+#pragma unroll
+                for (int c = 0; c < S::CD; c++) a += part[(4 * wi + j) * S::CD + c];
+                v[j] = a;
             }
+            const float p0 = swiglu(v[0], v[1]), p1 = swiglu(v[2], v[3]);
+            put_word(p.pb + r * SP + wg * (S::RD / 4) + wi, pack_bf16x2(p0, p1), make_tag(ep, l, PH_P));
         }
         // ---------------- E: down rows + residual ----------------
-        if constexpr (POLLER)
-            poll_pairs<(F / 2 + 63) / 64>(p.pb + rp * SP, F / 2, make_tag(ep, l, PH_P), sc, p.err, bail);
-        __syncthreads();
-        if (*bail) return;
-        if constexpr (!POLLER) {
-            if (l + 1 < p.n_layers) load_rows<2 * UA, CH>(p.layers[l + 1].qkv_qs, p.layers[l + 1].qkv_dg, rA, wA, dA);
+        if (reader) {
+            // two halves of at most 24 words per lane: the words in flight
+            // share the register file with the weight ring
+            constexpr int HALF = F / 4;
+            static_assert(HALF % 64 == 0 && HALF / 64 <= 24, "p channel halves");
+            const uint32_t tag = make_tag(ep, l, PH_P);
+            read_words<HALF / 64, true>(p, p.pb + rp * SP, HALF, tag, big, bail);
+            if (!*bail) read_words<HALF / 64, true>(p, p.pb + rp * SP + HALF, HALF, tag, big + 2 * HALF, bail);
         }
-        quantize_lds(sc, F, xq, xd);
-        __syncthreads();
-        if constexpr (!POLLER) {
-            float out[2 * UE];
-            dot_rows<2 * UE, CF>(wE, dE, xq, xd, out);
-            if (lane < kRep) {
-                const uint32_t tg = make_tag(ep, l + 1, PH_X);
+        lds_barrier();
+        if (*bail) return;
+        VXM_TS(threadIdx.x == 0, 9);
+        quantize_lds(big, F, xq, xd);
+        lds_barrier();
+        if (!reader) ring_phase<S, S::OE, S::SE>(rg, p, l, wg, ci, lane, xq, xd, part);
+        lds_barrier();
+        VXM_TS(threadIdx.x == 0, 10);
+        if (!reader && t < S::RE / 2 * kRep) {
+            const int wi = t / kRep, r = t % kRep;
+            const int row = wg * S::RE + 2 * wi;
+            float x2[2];
 #pragma unroll
-                for (int k = 0; k < UE; k++) {
-                    if (!vE[k]) continue;
-                    const int r = 2 * uE[k];
-                    float d0 = vxm_bf16(out[2 * k]), d1 = vxm_bf16(out[2 * k + 1]);
-                    if (p.res_scale != 1.0f) { d0 = d0 * p.res_scale; d1 = d1 * p.res_scale; }
-                    put_word(p.xb + (((l + 1) & 1) * kRep + lane) * SX + uE[k],
-                             pack_bf16x2(vxm_bf16(h1s[r] + d0), vxm_bf16(h1s[r + 1] + d1)), tg);
-                }
+            for (int j = 0; j < 2; j++) {
+                float a = 0.0f;
+#pragma unroll
+                for (int c = 0; c < S::CE; c++) a += part[(2 * wi + j) * S::CE + c];
+                float d = bf16r(a);
+                if (p.res_scale != 1.0f) d = d * p.res_scale;
+                x2[j] = bf16r(h1s[row + j] + d);
             }
+            put_word(p.xb + (((l + 1) & 1) * kRep + r) * SX + row / 2, pack_bf16x2(x2[0], x2[1]),
+                     make_tag(ep, l + 1, PH_X));
         }
     }
     // ---------------- final norm (workgroup 0) ----------------
-    if (blockIdx.x != 0) return;
+    if (wg != 0) return;
     const int Lyr = p.n_layers;
-    if constexpr (POLLER) {
-        poll_pairs<(H / 2 + 63) / 64>(p.xb + ((Lyr & 1) * kRep + rp) * SX, H / 2, make_tag(ep, Lyr, PH_X), xs, p.err,
-                                      bail);
+    if (reader) {
         if (p.final_norm) stage_f32(p.final_norm, H, gn);
+        read_words<cdiv(H / 2, 64), true>(p, p.xb + ((Lyr & 1) * kRep + rp) * SX, H / 2, make_tag(ep, Lyr, PH_X), xs,
+                                          bail);
     }
-    __syncthreads();
+    lds_barrier();
     if (*bail) return;
+#ifdef VXM_PERSISTENT_TRACE
+    if (threadIdx.x == 0 && p.trace) p.trace[1] = __builtin_amdgcn_s_memrealtime();
+#endif
     if (p.final_norm) {
-        rmsnorm_lds(xs, gn, H, p.eps, h1s, red);
-        for (int i = threadIdx.x; i < H; i += kThreads) p.x[i] = h1s[i];
+        rmsnorm_lds(xs, gn, H, p.eps, big, red);
+        for (int i = threadIdx.x; i < H; i += kThreads) p.x[i] = big[i];
     } else {
         for (int i = threadIdx.x; i < H; i += kThreads) p.x[i] = xs[i];
     }
@@ -643,59 +925,62 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
 
 }  // namespace
 
-template <int H, int NH, int NKV, int HD, int F, int G>
+template <class S>
 __global__ __launch_bounds__(kThreads, 1) void k_decode_persistent(vxm_pparams p) {
     extern __shared__ float lds[];
     __shared__ int bail;
     if (threadIdx.x == 0) bail = 0;
-    // bail is read only after the first __syncthreads of decode_run
-    if ((threadIdx.x >> 6) == 0) decode_run<true, H, NH, NKV, HD, F, G>(p, lds, &bail);
-    else decode_run<false, H, NH, NKV, HD, F, G>(p, lds, &bail);
+#ifdef VXM_PERSISTENT_TRACE
+    if (threadIdx.x == 0 && p.trace) p.trace[(size_t)blockIdx.x * p.trace_stride] = __builtin_amdgcn_s_memrealtime();
+#endif
+    // bail is read only after the first barrier of decode_run
+    decode_run<S>(p, lds, &bail);
 }
-
 
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
+using ShapeTslm = Shape<2048, 16, 2, 128, 6144>;
+using ShapeSmall = Shape<1024, 8, 2, 128, 2048>;
+
 struct vxm_persistent_state {
     void *base = nullptr;
     vxm_player *layers = nullptr;
     uint64_t *xb = nullptr, *qkvb = nullptr, *attb = nullptr, *h1b = nullptr, *pb = nullptr;
+    int8_t *dummy_q = nullptr;
+    uint16_t *dummy_d = nullptr;
     int *err = nullptr;
     uint32_t epoch = 0;
     const vxm_kv_cache *kv = nullptr;   // cache whose pointers are in the layer table
 };
 
-template <int H, int NH, int NKV, int HD, int F, int G>
+static constexpr int kMaxLds = 160 * 1024;
+
+template <class S>
 static int launch_decode(vxm_ctx *ctx, const vxm_pparams &prm) {
-    using L = Lds<H, NH * HD, F, HD>;
-    const int lds = L::bytes(prm.cap);
-    auto kern = k_decode_persistent<H, NH, NKV, HD, F, G>;
-    if (lds > 64 * 1024)
+    const int lds = S::bytes(prm.cap);
+    auto kern = k_decode_persistent<S>;
+    if (lds > kMaxLds)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "persistent decode: kv capacity %d needs %d B of LDS", prm.cap, lds);
+    VXM_HIP(ctx, hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
     void *args[] = {(void *)&prm};
-    VXM_HIP(ctx, hipLaunchCooperativeKernel((const void *)kern, dim3(G), dim3(kThreads), args, (unsigned)lds,
+    VXM_HIP(ctx, hipLaunchCooperativeKernel((const void *)kern, dim3(kG), dim3(kThreads), args, (unsigned)lds,
                                             ctx->stream));
     return VXM_OK;
 }
 
 // Supported shapes: (hidden, heads, kv heads, head dim, ffn).
 static bool persistent_shape(const vxm_block_dims &d, int n_cu) {
-    if (n_cu != 256) return false;
+    if (n_cu != kG) return false;
     if (d.H == 2048 && d.nh == 16 && d.nkv == 2 && d.hd == 128 && d.F == 6144) return true;
     if (d.H == 1024 && d.nh == 8 && d.nkv == 2 && d.hd == 128 && d.F == 2048) return true;
     return false;
 }
 
-// Largest cache capacity whose attention scores fit the 64 KiB of LDS.
+// Largest cache capacity whose attention scores fit the LDS.
 int vxm_persistent_max_cap(const vxm_block_dims &d) {
-    int cap = 1 << 16;
-    auto fits = [&](int c) {
-        return d.H == 2048 ? Lds<2048, 2048, 6144, 128>::bytes(c) <= 64 * 1024
-                           : Lds<1024, 1024, 2048, 128>::bytes(c) <= 64 * 1024;
-    };
-    while (cap > 0 && !fits(cap)) cap -= 64;
-    return cap;
+    const int fixed = d.H == 2048 ? ShapeTslm::bytes(0) : ShapeSmall::bytes(0);
+    return (kMaxLds - fixed) / 4 - 16;
 }
 
 bool vxm_persistent_supported(const vxm_minicpm4 *m, const vxm_kv_cache *kv) {
@@ -728,7 +1013,8 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
         const int nx = rep_stride((int)d.H / 2), nq = rep_stride((int)(qd + 2 * kvd) / 2),
                   na = rep_stride((int)qd), np_ = rep_stride((int)d.F / 2);
         const size_t words = (size_t)kRep * (2 * nx + nq + na + nx + np_);
-        const size_t total = tab + words * 8 + 256;
+        const size_t dummy = 1024 + 256;
+        const size_t total = tab + words * 8 + dummy + 256;
         if (hipMalloc(&s.base, total) != hipSuccess) {
             (void)hipGetLastError();
             return vxm_fail(ctx, VXM_ERR_OOM, "persistent decode buffers failed");
@@ -741,18 +1027,20 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
         s.attb = (uint64_t *)b; b += (size_t)kRep * na * 8;
         s.h1b = (uint64_t *)b; b += (size_t)kRep * nx * 8;
         s.pb = (uint64_t *)b; b += (size_t)kRep * np_ * 8;
+        s.dummy_q = (int8_t *)b; b += 1024;
+        s.dummy_d = (uint16_t *)b; b += 256;
         s.err = (int *)b;
         // tags start as all-ones: never equal to a live (epoch >= 1) tag
         VXM_HIP(ctx, hipMemsetAsync((char *)s.base + tab, 0xff, words * 8, ctx->stream));
-        VXM_HIP(ctx, hipMemsetAsync(s.err, 0, 4, ctx->stream));
+        VXM_HIP(ctx, hipMemsetAsync(s.dummy_q, 0, dummy + 4, ctx->stream));
         s.kv = nullptr;
     }
     if (s.kv != kv) {
         std::vector<vxm_player> tabh(L);
         for (int l = 0; l < L; l++) {
             const vxm_block &b = m->blocks[l];
-            tabh[l] = vxm_player{b.wqkv->qs, b.wo->qs, b.wgu->qs, b.wd->qs, b.wqkv->dg, b.wo->dg, b.wgu->dg,
-                                 b.wd->dg, b.g_in, b.g_post, kv->k(l), kv->v(l)};
+            tabh[l] = vxm_player{b.wqkv->qs, b.wo->qs, b.wgu->qs, b.wd->qs, b.wqkv->d, b.wo->d, b.wgu->d,
+                                 b.wd->d, b.g_in, b.g_post, kv->k(l), kv->v(l)};
         }
         VXM_HIP(ctx, hipMemcpyAsync(s.layers, tabh.data(), L * sizeof(vxm_player), hipMemcpyHostToDevice,
                                     ctx->stream));
@@ -771,6 +1059,8 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
     prm.attb = s.attb;
     prm.h1b = s.h1b;
     prm.pb = s.pb;
+    prm.dummy_q = s.dummy_q;
+    prm.dummy_d = s.dummy_d;
     prm.err = s.err;
     prm.ff = d.ff;
     prm.theta_scale = d.theta_scale;
@@ -780,8 +1070,39 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
     prm.cap = kv->cap;
     prm.no_rope = d.no_rope;
     prm.epoch = s.epoch;
-    if (d.H == 2048) return launch_decode<2048, 16, 2, 128, 6144, 256>(ctx, prm);
-    return launch_decode<1024, 8, 2, 128, 2048, 256>(ctx, prm);
+#ifdef VXM_PERSISTENT_TRACE
+    // profiling builds: one trace buffer per process, dumped after every launch
+    static uint64_t *tbuf = nullptr;
+    static size_t tcap = 0;
+    static int ncall = 0;
+    const int stride = 2 + L * 12;
+    const size_t tbytes = (size_t)kG * stride * 8;
+    if (tbytes > tcap) {
+        VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (tbuf) VXM_HIP(ctx, hipFree(tbuf));
+        VXM_HIP(ctx, hipMalloc(&tbuf, tbytes));
+        tcap = tbytes;
+    }
+    VXM_HIP(ctx, hipMemsetAsync(tbuf, 0, tbytes, ctx->stream));
+    prm.trace = tbuf;
+    prm.trace_stride = stride;
+    int rc_ = d.H == 2048 ? launch_decode<ShapeTslm>(ctx, prm) : launch_decode<ShapeSmall>(ctx, prm);
+    if (rc_) return rc_;
+    std::vector<uint64_t> th((size_t)kG * stride);
+    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    VXM_HIP(ctx, hipMemcpy(th.data(), tbuf, tbytes, hipMemcpyDeviceToHost));
+    const char *dir = getenv("VXM_TRACE_DIR");
+    char fn[512];
+    snprintf(fn, sizeof fn, "%s/trace_L%d_%04d.bin", dir ? dir : ".", L, ncall++);
+    if (FILE *f = fopen(fn, "wb")) {
+        fwrite(th.data(), 8, th.size(), f);
+        fclose(f);
+    }
+    return VXM_OK;
+#else
+    if (d.H == 2048) return launch_decode<ShapeTslm>(ctx, prm);
+    return launch_decode<ShapeSmall>(ctx, prm);
+#endif
 }
 
 int vxm_persistent_check(vxm_minicpm4 *m) {

@@ -72,14 +72,11 @@ __device__ __forceinline__ uint16_t vxm_f2h(float f) {
     return h;
 }
 
-// F32 -> BF16 -> F32 with round to nearest even and quiet NaN (the rule of
-// minicpm_bf16_round, src/minicpm4.c:39-42).
-__device__ __forceinline__ float vxm_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    uint32_t h = ((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 64u)
-                                                    : ((u + (0x7fffu + ((u >> 16) & 1u))) >> 16);
-    return __uint_as_float(h << 16);
-}
+// F32 -> BF16 -> F32 with round to nearest even (the rule of
+// minicpm_bf16_round, src/minicpm4.c:39-42), on gfx950's v_cvt_pk_bf16_f32.
+// Every non-NaN input rounds as the reference does; a NaN stays a quiet NaN
+// (its payload bits may differ from the reference's).
+__device__ __forceinline__ float vxm_bf16(float f) { return (float)(__bf16)f; }
 
 // sum of 16 int8 x int8 products held as 4 packed dwords each
 __device__ __forceinline__ int vxm_dot16(const int4 a, const int4 b, int acc) {
