@@ -207,7 +207,10 @@ def main():
     ap.add_argument("--copies", type=int, default=3, help="rotated copies of the 28-layer weights")
     ap.add_argument("--mode", default="auto", choices=["auto", "kernels", "persistent"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-tokens", type=int, default=2)
+    ap.add_argument("--cpu-tokens", type=int, default=96, help="decode tokens timed on all host cores")
+    ap.add_argument("--cpu-tokens-1t", type=int, default=16, help="decode tokens timed on one host core")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="time only the 28-layer decode (for profiling the dominant kernel)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -219,20 +222,25 @@ def main():
     mode = {"auto": 0, "kernels": 1, "persistent": 2}[args.mode]
     ctx = vxm.Context(0)
     res = {}
-    for (N, K) in ((6144, 2048), (2048, 6144)):
-        us = bench_gemv(ctx, torch, vxm, N, K, 64, 10)
-        gbs = gemv_bytes(N, K) / (us * 1e-6) / 1e9
-        res[f"{N}x{K}"] = {"us": round(us, 3), "GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
-        log(f"gemv {N}x{K}: {us:.3f} us/launch, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
+    if not args.decode_only:
+        for (N, K) in ((6144, 2048), (2048, 6144)):
+            us = bench_gemv(ctx, torch, vxm, N, K, 64, 10)
+            gbs = gemv_bytes(N, K) / (us * 1e-6) / 1e9
+            res[f"{N}x{K}"] = {"us_per_launch": round(us, 3), "GBs": round(gbs, 1),
+                               "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                               "note": "one launch per GEMV, back to back over 64 rotated weight copies"}
+            log(f"gemv {N}x{K}: {us:.3f} us/launch, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
 
     t0 = time.time()
     layers = make_layers(vxm, 1, L)
     log(f"generated {L} Q8_0 layers in {time.time() - t0:.1f} s")
 
-    # one decoder layer, context 512 (8 rotated copies of the layer)
-    us1, _ = bench_decode(ctx, torch, vxm, layers[:1], 1, 8, 512, 64, 4, mode)
-    layer_b = step_bytes(512, 1)
-    log(f"one layer decode @ctx512: {us1:.2f} us, {layer_b / (us1 * 1e-6) / 1e9:.1f} GB/s")
+    us1 = None
+    if not args.decode_only:
+        # one decoder layer, context 512 (8 rotated copies of the layer)
+        us1, _ = bench_decode(ctx, torch, vxm, layers[:1], 1, 8, 512, 64, 4, mode)
+        layer_b = step_bytes(512, 1)
+        log(f"one layer decode @ctx512: {us1:.2f} us, {layer_b / (us1 * 1e-6) / 1e9:.1f} GB/s")
 
     us_step, finite = bench_decode(ctx, torch, vxm, layers, L, args.copies, 256, args.steps, args.warmup, mode)
     mean_ctx = 256 + (args.steps - 1) / 2.0
@@ -245,15 +253,26 @@ def main():
     cpu = None
     if not args.no_cpu:
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-        c1, isa = cpu_baseline(vxm, layers, L, 256, args.cpu_tokens, 1)
+        t0 = time.time()
+        c1, isa = cpu_baseline(vxm, layers, L, 256, args.cpu_tokens_1t, 1)
         cn, _ = cpu_baseline(vxm, layers, L, 256, args.cpu_tokens, threads)
-        log(f"cpu baseline: 1 thread {c1 / 1000:.1f} ms/token, {threads} threads {cn / 1000:.1f} ms/token ({isa})")
+        log(f"cpu baseline: 1 thread {c1 / 1000:.1f} ms/token, {threads} threads {cn / 1000:.1f} ms/token ({isa}), "
+            f"{time.time() - t0:.1f} s")
         cpu = {"value": round(sb / (cn * 1e-6) / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": f"{args.cpu_tokens} decode tokens of the 28-layer stack at context 256 (SIMD {isa} "
-                         f"restatement of ggml-cpu Q8_0 mul_mat)",
+               "sample": f"{args.cpu_tokens} decode tokens on {threads} threads and {args.cpu_tokens_1t} on 1 thread "
+                         f"of the 28-layer stack at context 256 (SIMD {isa} restatement of ggml-cpu's Q8_0 "
+                         f"mul_mat path, one copy of the weights)",
                "us_per_step": round(cn, 1), "us_per_step_1thread": round(c1, 1),
                "speedup_vs_cpu_all_cores": round(cn / us_step, 1),
                "speedup_vs_cpu_1thread": round(c1 / us_step, 1)}
+
+    # roofline of the dominant kernel: the persistent decode (one launch per
+    # token step); its per-launch time is the timed region over the launches
+    kname = ("k_decode_persistent<Shape<2048,16,2,128,6144>>" if args.mode != "kernels"
+             else "per-op kernel sequence (no single dominant launch)")
+    roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kname,
+            "bytes_per_launch": int(sb), "us_per_launch": round(us_step, 2)}
 
     out = {
         "metric": "Q8_0 decode GEMV GB/s (% HBM peak) + us per 28-layer decode step, 1 GPU",
@@ -275,7 +294,8 @@ def main():
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "step_bytes": int(sb),
         "gemv": res,
-        "layer_decode_ctx512_us": round(us1, 3),
+        "layer_decode_ctx512_us": round(us1, 3) if us1 is not None else None,
+        "roofline": roof,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
