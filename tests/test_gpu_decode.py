@@ -1,7 +1,8 @@
 """GPU parity of the single-launch (persistent) decode against the oracle and
-against the one-kernel-per-op path, at the MiniCPM4 TSLM shape and a smaller
-shape, with RoPE (LongRoPE factors) and without (RALM), over consecutive
-tokens so the per-launch tags and the KV append are exercised.
+against the one-kernel-per-op path, at the MiniCPM4 TSLM / RALM shape (the
+only shape the single-launch kernel is built for), with RoPE (LongRoPE
+factors) and without (RALM), over consecutive tokens so the per-launch tags
+and the KV append are exercised.  Other shapes take the per-op path.
 
 Two last-ulp differences from the oracle are parity unpinned: the device's
 cosf/sinf against glibc's (rope), and the persistent attention's score sum
@@ -82,14 +83,15 @@ def test_persistent_first_token_single_layer_exact(vxm_ctx, orc):
 
 
 @pytest.mark.parametrize("shape,L,ctx0,steps,no_rope", [
-    ("small", 3, 0, 3, 0),
-    ("small", 2, 200, 2, 1),
+    ("tslm", 3, 0, 3, 0),       # empty cache: the first tokens attend to themselves only
+    ("tslm", 2, 200, 2, 1),     # the residual LM (RALM): no rope
     ("tslm", 2, 256, 3, 0),
+    ("tslm", 1, 700, 2, 0),     # more keys than one attention batch
 ])
 def test_persistent_decode_matches_oracle(vxm_ctx, orc, shape, L, ctx0, steps, no_rope):
     import vxm
 
-    cap = 512
+    cap = 1024
     s, rng, c, lws, fn, models, kvs, kcs, vcs = _setup(orc, vxm, vxm_ctx, shape, L, cap, ctx0, 31 + L + ctx0,
                                                        no_rope)
     oc = orc_cfg(orc, c)
@@ -132,7 +134,7 @@ def test_persistent_decode_repeatable(vxm_ctx, orc):
     dataflow tags, not timing, decide what each workgroup reads)."""
     import vxm
 
-    s, rng, c, lws, fn, models, kvs, kcs, vcs = _setup(orc, vxm, vxm_ctx, "small", 2, 256, 40, 5)
+    s, rng, c, lws, fn, models, kvs, kcs, vcs = _setup(orc, vxm, vxm_ctx, "tslm", 2, 256, 40, 5)
     x = rng.normal(0, 1, (1, s["H"])).astype(np.float32)
     outs = []
     for _ in range(3):
@@ -142,6 +144,29 @@ def test_persistent_decode_repeatable(vxm_ctx, orc):
         outs.append(xd.cpu().numpy())
     models[2].check()
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
+    for m in models.values():
+        m.free()
+    for kv in kvs.values():
+        kv.free()
+
+
+def test_persistent_unsupported_shape_falls_back(vxm_ctx, orc):
+    """A shape without a single-launch kernel: AUTO decodes on the per-op path
+    (still matching the oracle), PERSISTENT is refused with NOT_IMPLEMENTED."""
+    import vxm
+
+    s, rng, c, lws, fn, models, kvs, kcs, vcs = _setup(orc, vxm, vxm_ctx, "small", 1, 256, 16, 9)
+    x = rng.normal(0, 1, (1, s["H"])).astype(np.float32)
+    m_auto = vxm.MiniCPM4(vxm_ctx, c, lws, final_norm=fn)   # decode mode AUTO
+    xd = _dev(x)
+    m_auto.forward(kvs[1], xd, 16)
+    vxm_ctx.sync()
+    ref = orc.minicpm4_forward(orc_cfg(orc, c), [to_orc(orc, l) for l in lws], fn, x, kcs, vcs, 256, 16)
+    assert_stack_close(xd.cpu().numpy(), ref, what="auto small")
+    with pytest.raises(vxm.VxmError) as e:
+        models[2].forward(kvs[2], _dev(x), 16)
+    assert e.value.code == 7   # VXM_ERR_NOT_IMPLEMENTED
+    m_auto.free()
     for m in models.values():
         m.free()
     for kv in kvs.values():

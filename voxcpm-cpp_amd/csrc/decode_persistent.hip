@@ -23,19 +23,23 @@
 //
 // Work split.  In every phase workgroup g owns a fixed, contiguous block of
 // weight rows (10 QKV, 8 O, 48 gate/up, 8 down rows at the TSLM shape).  Its
-// rows are cut into units of one 1 KiB chunk (1024 quants + 32 scales); the
+// rows are cut into units of 2 KiB (64 blocks: 2048 quants + 64 scales); the
 // seven compute waves take units round-robin, so every wave streams the same
-// number of bytes (+-1 unit).  A unit's dot product yields one fp32 partial;
-// the partials of a row are added in chunk order from LDS.
+// number of bytes (+-1 unit).  Lane l of a wave owns block l of its unit, so
+// a unit's dot product is 8 sdot4 per lane and one wave sum.  The partials of
+// a row are added in unit order from LDS.
 //
 // Weight streaming.  Wave 0 only reads the phase inputs; waves 1..7 stream
-// weights through a register ring (9 slots at the TSLM shape, whose schedule
-// has 27 units per layer) with a fixed lookahead of P units: after consuming
-// the unit at stream position j the wave issues the loads of position j + P
-// (which may belong to the next phase or the next layer), so the weights of
-// the next phase are in flight while a phase waits for its inputs.  Barriers
-// fence LDS only (s_barrier with LDS-scoped fences), so they never drain the
-// weight loads in flight.
+// weights with direct-to-LDS loads (global_load_lds_dwordx4) into a ring of
+// RING unit slots per wave, with a fixed lookahead of P units: after
+// consuming the unit at stream position j the wave issues the loads of
+// position j + P (which may belong to the next phase or the next layer), so
+// the weights of the next phase are in flight while a phase waits for its
+// inputs.  The loads are inline asm with explicit vmcnt waits: the compiler
+// neither tracks them (its wait insertion would drain the ring at every phase
+// branch) nor holds their data in registers (nothing it can spill or move
+// before the data lands).  Barriers fence LDS only (s_barrier with
+// LDS-scoped fences), so they never drain the weight loads in flight.
 //
 // Latency budget.  A wave64 VALU instruction issues once per 4 cycles and a
 // workgroup has two waves per SIMD, so the serial work between two phases is
@@ -76,12 +80,13 @@ constexpr int kCW = kWaves - 1;
 constexpr int kThreads = kWaves * 64;
 constexpr int kG = 256;                // workgroups: one per CU
 constexpr int kSpin = 1 << 17;         // poll rounds before giving up
-constexpr int kLook = 8;               // weight units in flight per compute wave
+constexpr int kLook = 5;               // 2 KiB weight units in the LDS ring per compute wave
+constexpr int kUnit = 2048;            // quant bytes per unit (64 blocks)
+constexpr int kSlot = kUnit + 128;     // LDS bytes per ring slot: quants, then 64 fp16 scales
 // Every channel is written as kRep replicas; workgroup b reads replica
 // b % kRep, so the coherent loads of 256 workgroups spread over many lines.
 constexpr int kRep = 16;
 constexpr int kPad = 64;               // words between replicas
-constexpr int kAttnKB = 8;             // attention: key loads in flight per lane
 
 __host__ __device__ constexpr int rep_stride(int words) { return words + kPad; }
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
@@ -94,14 +99,17 @@ struct Shape {
     static constexpr int H = H_, NH = NH_, NKV = NKV_, HD = HD_, F = F_;
     static constexpr int QD = NH * HD, KVD = NKV * HD, NQKV = QD + 2 * KVD;
     static constexpr int QPK = NH / NKV;
-    // rows per workgroup per phase, 1 KiB chunks per row, units per workgroup
+    // rows per workgroup per phase, 2 KiB units per row, units per workgroup
     static constexpr int RA = NQKV / kG, RC = H / kG, RD = 2 * F / kG, RE = H / kG;
-    static constexpr int CA = H / 1024, CC = QD / 1024, CD = H / 1024, CE = F / 1024;
+    static constexpr int CA = H / kUnit, CC = QD / kUnit, CD = H / kUnit, CE = F / kUnit;
     static constexpr int UA = RA * CA, UC = RC * CC, UD = RD * CD, UE = RE * CE;
     // ring slots per compute wave: A, C, D, E units of one layer
     static constexpr int SA = cdiv(UA, kCW), SC = cdiv(UC, kCW), SD = cdiv(UD, kCW), SE = cdiv(UE, kCW);
     static constexpr int OA = 0, OC = SA, OD = SA + SC, OE = SA + SC + SD, NS = SA + SC + SD + SE;
     static constexpr int P = kLook < NS ? kLook : NS;
+    // vector memory instructions issued after a unit's three DMAs before it
+    // is consumed: the 3 DMAs of each of the next P-1 units
+    static constexpr int WAIT = 3 * (P - 1);
     // ring size: the smallest divisor of NS that holds P units, so the slot of
     // stream position l*NS + s is s % RING for every layer l
     static constexpr int ring_size() {
@@ -110,12 +118,13 @@ struct Shape {
         return NS;
     }
     static constexpr int RING = ring_size();
+    static constexpr int RING_BYTES = kCW * RING * kSlot;
     static constexpr int UMAX = cmax(cmax(UA, UC), cmax(UD, UE));
     static constexpr int KMAX = cmax(cmax(H, QD), F);
     static constexpr int BIG = cmax(cmax(QD, F), H);
     static_assert(NQKV % kG == 0 && H % kG == 0 && (2 * F) % kG == 0, "rows must split over 256 workgroups");
     static_assert(RA % 2 == 0 && RC % 2 == 0 && RD % 4 == 0 && RE % 2 == 0, "rows per workgroup");
-    static_assert(H % 1024 == 0 && QD % 1024 == 0 && F % 1024 == 0, "K must be a multiple of 1024");
+    static_assert(H % kUnit == 0 && QD % kUnit == 0 && F % kUnit == 0, "K must be a multiple of 2048");
     static_assert(H <= 4 * kThreads && (H & (H - 1)) == 0, "hidden: one norm pass, power of two");
     static_assert(HD == 128 && NH % NKV == 0, "heads: the attention maps one key to a row of 16 lanes");
     static_assert(NH <= kG && QPK * 8 <= kG && NH <= 64, "attention workgroups");
@@ -131,7 +140,8 @@ struct Shape {
     static constexpr int L_RED = L_PART + UMAX;     // reductions / wave partials [kWaves * HD]
     static constexpr int L_SC = L_RED + kWaves * HD;// attention scores           [cap + 1]
     __host__ __device__ static int xq_off(int cap) { return ((L_SC + cap + 1) * 4 + 15) & ~15; }
-    __host__ __device__ static int bytes(int cap) { return xq_off(cap) + KMAX; }
+    __host__ __device__ static int ring_off(int cap) { return xq_off(cap) + KMAX; }   // 16-byte aligned
+    __host__ __device__ static int bytes(int cap) { return ring_off(cap) + RING_BYTES; }
 };
 
 // workgroup that runs the attention of query head h: the heads of one kv
@@ -267,6 +277,10 @@ __device__ __forceinline__ int opaque_v(int x) {   // per-lane value, recomputed
     asm volatile("" : "+v"(x));
     return x;
 }
+// threadIdx.x through an opaque copy: the index arithmetic of a helper that
+// runs inside the layer loop stays there instead of being hoisted (with long
+// live ranges) into the kernel prologue.
+__device__ __forceinline__ int tid_now() { return opaque_v((int)threadIdx.x); }
 
 }  // namespace
 
@@ -288,8 +302,8 @@ struct vxm_pparams {
     uint64_t *attb;    // [QD] attention output (fp32)
     uint64_t *h1b;     // [H/2] BF16 pairs
     uint64_t *pb;      // [F/2] BF16 pairs
-    const int8_t *dummy_q;     // 1 KiB of zeros: loads of units a wave does not own
-    const uint16_t *dummy_d;   // 32 zero scales
+    const int8_t *dummy_q;     // 2 KiB of zeros: loads of units a wave does not own
+    const uint16_t *dummy_d;   // 64 zero scales
     int *err;
     const float *ff;
     float theta_scale, eps, res_scale;
@@ -327,7 +341,7 @@ __device__ __forceinline__ bool give_up(const vxm_pparams &p, int &it, int *bail
 template <int NPL, bool PAIRS>
 __device__ double read_words(const vxm_pparams &p, const uint64_t *src, int n, uint32_t tag, float *dst, int *bail) {
     static_assert(NPL <= 64, "words per lane");
-    const int lane = threadIdx.x & 63;
+    const int lane = tid_now() & 63;
     uint64_t pending = 0;
 #pragma unroll
     for (int k = 0; k < NPL; k++)
@@ -366,7 +380,7 @@ __device__ double read_words(const vxm_pparams &p, const uint64_t *src, int n, u
 // 240 waiting workgroups read 16 words per round instead of 2048.
 __device__ void wait_sentinels(const vxm_pparams &p, const uint64_t *src, int n, int stride, uint32_t tag,
                                int *bail) {
-    const int lane = threadIdx.x & 63;
+    const int lane = tid_now() & 63;
     bool done = lane >= n;
     int it = 0;
     while (true) {
@@ -379,7 +393,7 @@ __device__ void wait_sentinels(const vxm_pparams &p, const uint64_t *src, int n,
 
 // Wave 0: plain copy of n floats (gains) into LDS, n % 256 == 0
 __device__ __forceinline__ void stage_f32(const float *src, int n, float *dst) {
-    const int lane = threadIdx.x & 63;
+    const int lane = tid_now() & 63;
     for (int i = lane * 4; i < n; i += 256) *(float4 *)(dst + i) = *(const float4 *)(src + i);
 }
 
@@ -387,7 +401,7 @@ __device__ __forceinline__ double wg_sum_d(double v, float *red) {
     v = wave_sum_63_d(v);
     double *r = (double *)red;
     lds_barrier();
-    if ((threadIdx.x & 63) == 63) r[threadIdx.x >> 6] = v;
+    if ((tid_now() & 63) == 63) r[tid_now() >> 6] = v;
     lds_barrier();
     double t = 0.0;
 #pragma unroll
@@ -398,7 +412,7 @@ __device__ __forceinline__ double wg_sum_d(double v, float *red) {
 __device__ __forceinline__ float wg_max_f(float v, float *red) {
     v = wave_max_63(v);
     lds_barrier();
-    if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = v;
+    if ((tid_now() & 63) == 63) red[tid_now() >> 6] = v;
     lds_barrier();
     float t = red[0];
 #pragma unroll
@@ -426,10 +440,10 @@ __device__ __forceinline__ void quant4(const float v[4], int8_t *xq4, float *xd1
 
 // Q8_0 of n values in LDS (n % 32 == 0), 4 values per thread.
 __device__ void quantize_lds(const float *src, int n, int8_t *xq, float *xd) {
-    for (int base = threadIdx.x * 4; base < n; base += kThreads * 4) {
+    for (int base = tid_now() * 4; base < n; base += kThreads * 4) {
         const float4 a = *(const float4 *)(src + base);
         const float v[4] = {a.x, a.y, a.z, a.w};
-        quant4(v, xq + base, xd + base / 32, (threadIdx.x & 7) == 0);
+        quant4(v, xq + base, xd + base / 32, (tid_now() & 7) == 0);
     }
 }
 
@@ -441,23 +455,23 @@ __device__ __forceinline__ void norm_quant(const float *x, const float *g, doubl
                                            float *xd) {
     const float mean = (float)(sumsq * (1.0 / (double)N));   // N is a power of two: exact
     const float sc = __fdiv_rn(1.0f, __fsqrt_rn(mean + eps));
-    const int base = threadIdx.x * 4;
+    const int base = tid_now() * 4;
     if (base < N) {
         const float4 a = *(const float4 *)(x + base), b = *(const float4 *)(g + base);
         const float v[4] = {bf16r(bf16r(a.x * sc) * b.x), bf16r(bf16r(a.y * sc) * b.y),
                             bf16r(bf16r(a.z * sc) * b.z), bf16r(bf16r(a.w * sc) * b.w)};
-        quant4(v, xq + base, xd + base / 32, (threadIdx.x & 7) == 0);
+        quant4(v, xq + base, xd + base / 32, (tid_now() & 7) == 0);
     }
 }
 
 // vcpm_rms_norm of src (LDS) with gain (LDS) into dst (LDS), all threads.
 __device__ void rmsnorm_lds(const float *src, const float *gain, int n, float eps, float *dst, float *red) {
     double ss = 0.0;
-    for (int i = threadIdx.x; i < n; i += kThreads) ss += (double)(src[i] * src[i]);
+    for (int i = tid_now(); i < n; i += kThreads) ss += (double)(src[i] * src[i]);
     const double tot = wg_sum_d(ss, red);
     const float mean = (float)(tot / (double)n);
     const float sc = __fdiv_rn(1.0f, __fsqrt_rn(mean + eps));
-    for (int i = threadIdx.x; i < n; i += kThreads) dst[i] = bf16r(bf16r(src[i] * sc) * gain[i]);
+    for (int i = tid_now(); i < n; i += kThreads) dst[i] = bf16r(bf16r(src[i] * sc) * gain[i]);
 }
 
 // ---- the weight ring ---------------------------------------------------------
@@ -472,82 +486,113 @@ struct Slot {
     static constexpr int R = ph == 0 ? S::RA : ph == 1 ? S::RC : ph == 2 ? S::RD : S::RE;
 };
 
-template <class S>
-struct Ring {
-    v4i q[S::RING];
-    uint32_t d[S::RING];
-};
+// The ring's loads: direct-to-LDS DMA issued as inline asm.  Lane l of
+// global_load_lds_dwordx4 writes its 16 bytes at M0 + 16 l.  A unit is three
+// instructions: quants [0, 1024) and [1024, 2048) by all lanes, and the 128
+// bytes of scales by lanes 0..7 (exec narrowed inside the asm and restored).
+// Before the DMA overwrites a slot, lgkmcnt(0) guarantees that the wave's
+// LDS reads of the slot's previous unit have completed.
+__device__ __forceinline__ void dma_unit(uint32_t lds_slot, const int8_t *q, const uint16_t *d, int lane) {
+    const int8_t *q0 = q + lane * 16;
+    const int8_t *q1 = q0 + 1024;
+    const char *dd = (const char *)d + (lane & 7) * 16;
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_slot);
+    uint64_t saved;
+    uint32_t saved_m0;
+    // m0 and exec are saved and restored inside the statement, so the
+    // compiler's view of both is unchanged
+    asm volatile(
+        "s_waitcnt lgkmcnt(0)\n\t"
+        "s_mov_b32 %1, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %3, off\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %4, off\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, 0xff\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %5, off\n\t"
+        "s_mov_b64 exec, %0\n\t"
+        "s_mov_b32 m0, %1"
+        : "=&s"(saved), "=&s"(saved_m0)
+        : "s"(m0v), "v"(q0), "v"(q1), "v"(dd)
+        : "memory", "scc");
+}
 
-// The ring's loads are issued as inline asm so that the compiler does not
-// track them: its wait insertion cannot count pending loads across the phase
-// branches and the layer loop and would drain the whole ring (vmcnt(0)) at
-// every phase.  Before a unit is used, ring_wait waits until at most N vector
-// memory instructions of the wave are pending; in steady state the 2(P-1)
-// loads of the next P-1 units were issued after the unit's own two, and
-// vmcnt retires in order, so the unit's data is in.  Other vector memory
-// instructions of the wave only make the wait stricter.  The "+v" operands
-// tie the registers to the wait, so no use is scheduled before it.
-__device__ __forceinline__ void ring_ld16(v4i &dst, const void *ptr) {
-    asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(dst) : "v"(ptr));
-}
-__device__ __forceinline__ void ring_ld2(uint32_t &dst, const void *ptr) {
-    asm volatile("global_load_ushort %0, %1, off nt" : "=v"(dst) : "v"(ptr));
-}
+// Wait until at most N vector memory instructions of the wave are pending.
+// In steady state the 3(P-1) DMAs of the next P-1 units were issued after a
+// unit's own three, and vmcnt retires in order, so the unit is in LDS.
+// Other vector memory instructions of the wave only make the wait stricter.
 template <int N>
-__device__ __forceinline__ void ring_wait(v4i &q, uint32_t &d) {
+__device__ __forceinline__ void ring_wait() {
     static_assert(N >= 0 && N <= 63, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(q), "+v"(d) : "n"(N));
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Issue the loads of slot s for layer l (dummy loads past the last layer or
-// for a unit the wave does not own, so every wave issues the same count).
+// Weight addresses of slot s of layer l for compute wave ci (the zero
+// buffers past the last layer or for a unit the wave does not own, so every
+// wave issues the same count of loads).
 template <class S, int s>
-__device__ __forceinline__ void ring_issue(Ring<S> &rg, const vxm_pparams &p, int l, int wg, int ci, int lane) {
+__device__ __forceinline__ void unit_addr(const vxm_pparams &p, int l, int wg, int ci, const int8_t *&q,
+                                          const uint16_t *&d) {
     using T = Slot<S, s>;
-    const int u = ci + opaque_zero() + kCW * T::k;
-    const int lq = opaque_v(lane * 16), ld = opaque_v(lane >> 1);
-    const int8_t *q = p.dummy_q + lq;
-    const uint16_t *d = p.dummy_d + ld;
+    const int u = ci + kCW * T::k;
+    q = p.dummy_q;
+    d = p.dummy_d;
     if (u < T::U && l < p.n_layers) {
         vxm_ptab Ly = layer_tab(p) + l;
-        const int row = (wg + opaque_zero()) * T::R + u / T::C, c = u % T::C;
-        constexpr int K = T::C * 1024;
+        const int row = wg * T::R + u / T::C, c = u % T::C;
+        constexpr int K = T::C * kUnit;
         const int8_t *bq = T::ph == 0 ? Ly->qkv_qs : T::ph == 1 ? Ly->o_qs : T::ph == 2 ? Ly->gu_qs : Ly->d_qs;
         const uint16_t *bd = T::ph == 0 ? Ly->qkv_d : T::ph == 1 ? Ly->o_d : T::ph == 2 ? Ly->gu_d : Ly->d_d;
-        q = bq + ((int64_t)row * K + c * 1024) + lq;
-        d = bd + ((int64_t)row * (K / 32) + c * 32) + ld;
+        q = bq + (int64_t)row * K + c * kUnit;
+        d = bd + (int64_t)row * (K / 32) + c * (kUnit / 32);
     }
-    rg.q[s % S::RING] = __builtin_nontemporal_load((const v4i *)q);
-    rg.d[s % S::RING] = __builtin_nontemporal_load(d);
+}
+
+// Issue the DMAs of slot s of layer l into ring slot s % RING.
+template <class S, int s>
+__device__ __forceinline__ void ring_issue(const vxm_pparams &p, uint32_t ring_lds, int l, int wg, int ci, int lane) {
+    const int8_t *q;
+    const uint16_t *d;
+    unit_addr<S, s>(p, l, wg, ci, q, d);
+    dma_unit(ring_lds + (s % S::RING) * kSlot, q, d, lane);
 }
 
 template <class S, int... ss>
-__device__ __forceinline__ void ring_prime(Ring<S> &rg, const vxm_pparams &p, int wg, int ci, int lane,
+__device__ __forceinline__ void ring_prime(const vxm_pparams &p, uint32_t ring_lds, int wg, int ci, int lane,
                                            std::integer_sequence<int, ss...>) {
-    (ring_issue<S, ss>(rg, p, 0, wg, ci, lane), ...);
+    (ring_issue<S, ss>(p, ring_lds, 0, wg, ci, lane), ...);
 }
 
 // Consume the K slots of one phase starting at slot OFF: dot product of each
-// unit with the quantized activation in LDS, partial to part[u]; after each
-// unit, the loads P positions ahead are issued.
+// unit (lane l: block l) with the quantized activation in LDS, partial to
+// part[u]; after each unit, the loads P positions ahead are issued.
 template <class S, int OFF, int K, int k = 0>
-__device__ __forceinline__ void ring_phase(Ring<S> &rg, const vxm_pparams &p, int l, int wg, int ci, int lane,
-                                           const int8_t *xq, const float *xd, float *part) {
+__device__ __forceinline__ void ring_phase(const vxm_pparams &p, const int8_t *ring, uint32_t ring_lds, int l, int wg,
+                                           int ci, int lane, const int8_t *xq, const float *xd, float *part) {
     if constexpr (k < K) {
         constexpr int s = OFF + k;
         using T = Slot<S, s>;
         const int u = ci + kCW * k;
         const int c = u % T::C;
-        const v4i xv = *(const v4i *)(xq + c * 1024 + lane * 16);
-        const float xs = xd[c * 32 + (lane >> 1)];
-        int si = dot16(rg.q[s % S::RING], xv);
-        si += dpp_i<kDppXor1>(si);                  // exact int32 sum of the lane pair's block
-        float a = (float)si * (vxm_h2f((uint16_t)rg.d[s % S::RING]) * xs);
-        a = wave_sum_63((lane & 1) ? 0.0f : a);     // one term per block
+        const v4i x0 = *(const v4i *)(xq + c * kUnit + lane * 32);
+        const v4i x1 = *(const v4i *)(xq + c * kUnit + lane * 32 + 16);
+        const float xs = xd[c * (kUnit / 32) + lane];
+        ring_wait<S::WAIT>();
+        const int8_t *slot = ring + (s % S::RING) * kSlot;
+        const v4i w0 = *(const v4i *)(slot + lane * 32);
+        const v4i w1 = *(const v4i *)(slot + lane * 32 + 16);
+        const uint16_t dw = *(const uint16_t *)(slot + kUnit + lane * 2);
+        const int si = dot16(w1, x1) + dot16(w0, x0);   // exact int32 block sum
+        const float a = wave_sum_63((float)si * (vxm_h2f(dw) * xs));
         if (lane == 63 && u < T::U) part[u] = a;
         constexpr int sn = (s + S::P) % S::NS;
-        ring_issue<S, sn>(rg, p, l + (s + S::P >= S::NS ? 1 : 0), wg, ci, lane);
-        ring_phase<S, OFF, K, k + 1>(rg, p, l, wg, ci, lane, xq, xd, part);
+        ring_issue<S, sn>(p, ring_lds, l + (s + S::P >= S::NS ? 1 : 0), wg, ci, lane);
+        ring_phase<S, OFF, K, k + 1>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
     }
 }
 
@@ -555,17 +600,44 @@ __device__ __forceinline__ void ring_phase(Ring<S> &rg, const vxm_pparams &p, in
 // src/minicpm4.c:232-248): wave 0 reads q_h, k_g, v_g; all waves then read
 // the f16 cache rows [0, pos) of group g, use the fresh k, v for row pos,
 // and publish the 128 fp32 outputs.  The group's first head appends k, v.
+// K or V rows of one attention batch: lane (kin, sub) of wave w loads dims
+// sub*8..+8 of key jb + (k * kWaves + w) * KPW + kin for k < KB; keys at or
+// past pos (the current token comes from LDS) load nothing.
+template <int KB, int HD>
+__device__ __forceinline__ void attn_load(const uint16_t *base, int jb, int pos, uint4 (&r)[KB]) {
+    constexpr int LPK = HD / 8, KPW = 64 / LPK;
+    const int tid = tid_now(), wave = tid >> 6, lane = tid & 63, sub = lane % LPK, kin = lane / LPK;
+#pragma unroll
+    for (int k = 0; k < KB; k++) {
+        const int j = jb + (k * kWaves + wave) * KPW + kin;
+        r[k] = j < pos ? *(const uint4 *)(base + (int64_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
+    }
+}
+
+// Attention of query head h for layer l (vcpm_attention's gqa_group_attn,
+// src/minicpm4.c:232-248).  The cached K and V rows [0, pos) do not depend
+// on this layer's projections, so every wave issues its loads of the first
+// batch (up to 320 keys) before wave 0 reads q_h, k_g, v_g: the cache fetch
+// overlaps the QKV exchange.  The current token's k, v come from LDS; the
+// group's first head appends them to the cache.  Output: 128 fp32.
 template <class S>
 __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int h, float *lds, int *bail) {
     constexpr int QD = S::QD, KVD = S::KVD, HD = S::HD;
     constexpr int SQ = rep_stride(S::NQKV / 2), SAT = rep_stride(QD);
     constexpr int LPK = HD / 8, KPW = 64 / LPK;                  // lanes per key, keys per wave
-    constexpr int PERB = kWaves * KPW * kAttnKB;                 // keys per batch
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    constexpr int KB = 10;                                       // keys per lane per batch
+    constexpr int PERB = kWaves * KPW * KB;                      // keys per batch (320)
+    const int tid = tid_now(), wave = tid >> 6, lane = tid & 63;
     const int rp = blockIdx.x % kRep, g = h / S::QPK, pos = p.pos;
     const uint32_t ep = p.epoch;
     vxm_ptab Ly = layer_tab(p) + l;
     float *aq = lds + S::L_AQ, *red = lds + S::L_RED, *sc = lds + S::L_SC;
+    uint16_t *const kc = Ly->kc, *const vc = Ly->vc;
+    const uint16_t *kb = kc + (int64_t)g * p.cap * HD;
+    const uint16_t *vb = vc + (int64_t)g * p.cap * HD;
+    uint4 kr[KB], vr[KB];
+    attn_load<KB, HD>(kb, 0, pos, kr);
+    attn_load<KB, HD>(vb, 0, pos, vr);
     if (wave == 0) {
         // q_h and k_g (pair-interleaved: word w = dims w, w + HD/2) and v_g
         // (natural pairs) -> aq[0..3HD) in natural order; lane l owns word w = l
@@ -602,16 +674,13 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     }
     lds_barrier();
     if (*bail) return;
-    VXM_TS(threadIdx.x == 0, 3);
+    VXM_TS(tid_now() == 0, 3);
     const float *qh = aq, *kcur = aq + HD, *vcur = aq + 2 * HD;
-    uint16_t *const kc = Ly->kc, *const vc = Ly->vc;
-    const uint16_t *kb = kc + (int64_t)g * p.cap * HD;
-    const uint16_t *vb = vc + (int64_t)g * p.cap * HD;
     // KV append: the first query head of each group writes the f16 rows at pos
     if (h % S::QPK == 0) {
         uint16_t *kw = kc + ((int64_t)g * p.cap + pos) * HD;
         uint16_t *vw = vc + ((int64_t)g * p.cap + pos) * HD;
-        for (int d = threadIdx.x; d < HD; d += kThreads) {
+        for (int d = tid; d < HD; d += kThreads) {
             kw[d] = vxm_f2h(kcur[d]);
             vw[d] = vxm_f2h(vcur[d]);
         }
@@ -622,24 +691,19 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     float qv[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) qv[i] = qh[sub * 8 + i];
-    // batch jb covers keys jb + (k * kWaves + wave) * KPW + kin, k < kAttnKB
+    // scores: batch jb covers keys jb + (k * kWaves + wave) * KPW + kin
     float mx = -INFINITY;
     for (int jb = 0; jb < kv_len; jb += PERB) {
-        uint4 raw[kAttnKB];
+        if (jb > 0) attn_load<KB, HD>(kb, jb, pos, kr);
 #pragma unroll
-        for (int k = 0; k < kAttnKB; k++) {
-            const int j = jb + (k * kWaves + wave) * KPW + kin;
-            raw[k] = j < pos ? *(const uint4 *)(kb + (int64_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int k = 0; k < kAttnKB; k++) {
+        for (int k = 0; k < KB; k++) {
             const int j = jb + (k * kWaves + wave) * KPW + kin;
             float kv8[8];
             if (j == pos) {
 #pragma unroll
                 for (int i = 0; i < 8; i++) kv8[i] = vxm_h2f(vxm_f2h(kcur[sub * 8 + i]));
             } else {
-                const uint32_t wv[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+                const uint32_t wv[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     kv8[2 * i] = vxm_h2f((uint16_t)(wv[i] & 0xffffu));
@@ -651,34 +715,29 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
             for (int i = 0; i < 8; i++) pt += kv8[i] * qv[i];
             pt = row16_sum_15(pt);
             if (j < kv_len && sub == LPK - 1) {
-                const float s = pt * scale;
-                sc[j] = s;
-                mx = fmaxf(mx, s);
+                const float s2 = pt * scale;
+                sc[j] = s2;
+                mx = fmaxf(mx, s2);
             }
         }
     }
     mx = wg_max_f(mx, red);
     double sum = 0.0;
-    for (int j = threadIdx.x; j < kv_len; j += kThreads) {
+    for (int j = tid; j < kv_len; j += kThreads) {
         const float e = expf(sc[j] - mx);
         sc[j] = e;
         sum += (double)e;
     }
     sum = wg_sum_d(sum, red);
     const float inv = (float)(1.0 / sum);
-    for (int j = threadIdx.x; j < kv_len; j += kThreads) sc[j] = sc[j] * inv;
+    for (int j = tid; j < kv_len; j += kThreads) sc[j] = sc[j] * inv;
     lds_barrier();
     // out[d] = sum_j p_j v_j[d]: lane (kin, sub) accumulates dims sub*8..+8 over its keys
     float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int jb = 0; jb < kv_len; jb += PERB) {
-        uint4 raw[kAttnKB];
+        if (jb > 0) attn_load<KB, HD>(vb, jb, pos, vr);
 #pragma unroll
-        for (int k = 0; k < kAttnKB; k++) {
-            const int j = jb + (k * kWaves + wave) * KPW + kin;
-            raw[k] = j < pos ? *(const uint4 *)(vb + (int64_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int k = 0; k < kAttnKB; k++) {
+        for (int k = 0; k < KB; k++) {
             const int j = jb + (k * kWaves + wave) * KPW + kin;
             if (j >= kv_len) continue;
             const float pj = sc[j];
@@ -686,7 +745,7 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
 #pragma unroll
                 for (int i = 0; i < 8; i++) o[i] += vxm_h2f(vxm_f2h(vcur[sub * 8 + i])) * pj;
             } else {
-                const uint32_t wv[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+                const uint32_t wv[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     o[2 * i] += vxm_h2f((uint16_t)(wv[i] & 0xffffu)) * pj;
@@ -695,11 +754,15 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
             }
         }
     }
-    // reduce over the KPW key lanes of the wave, then over waves (fixed order)
+    // reduce over the KPW = 4 key rows of the wave (lanes l, l^16, l^32,
+    // l^48) with permlane swaps, then over waves in a fixed order
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-#pragma unroll
-        for (int m = LPK; m < 64; m <<= 1) o[i] += __shfl_xor(o[i], m, 64);
+    for (int i = 0; i < 8; i++) {
+        const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(o[i]), __float_as_uint(o[i]), false, false);
+        o[i] = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+        const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(o[i]), __float_as_uint(o[i]), false, false);
+        o[i] = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+    }
     lds_barrier();   // red is reused below
     if (kin == 0) {
 #pragma unroll
@@ -707,14 +770,14 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     }
     lds_barrier();
     const uint32_t tg = make_tag(ep, l, PH_ATT);
-    for (int t = threadIdx.x; t < HD * kRep; t += kThreads) {
+    for (int t = tid; t < HD * kRep; t += kThreads) {
         const int d = t % HD, r = t / HD;
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; w++) v += red[w * HD + d];
         put_word(p.attb + r * SAT + h * HD + d, __float_as_uint(v), tg);
     }
-    VXM_TS(threadIdx.x == 0, 4);
+    VXM_TS(tid_now() == 0, 4);
 }
 
 // The whole decode.  Wave 0 reads the inputs of each phase (and forms
@@ -731,10 +794,10 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
     float *xd = lds + S::L_XD, *cs = lds + S::L_CS, *part = lds + S::L_PART, *red = lds + S::L_RED;
     double *ssq = (double *)red;   // sum of squares from the reading wave
     int8_t *xq = (int8_t *)lds + S::xq_off(p.cap);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = tid_now() >> 6, lane = tid_now() & 63;
     const bool reader = wave == 0;
     const int ci = __builtin_amdgcn_readfirstlane(wave - 1);   // compute wave index (uniform)
-    const int t = threadIdx.x - 64;                             // compute thread index
+    const int t = tid_now() - 64;                             // compute thread index
     const int pos = p.pos;
     const uint32_t ep = p.epoch;
     // the query head this workgroup attends for, or -1
@@ -743,7 +806,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         if (attn_wg<S>(h) == wg) head = h;
 
     // rope cos/sin of this token's position (ggml_rope_ext NEOX, iterative theta)
-    for (int i = threadIdx.x; i < HD / 2; i += kThreads) {
+    for (int i = tid_now(); i < HD / 2; i += kThreads) {
         float theta = (float)pos;
         for (int k = 0; k < i; k++) theta = theta * p.theta_scale;
         const float th = p.ff ? __fdiv_rn(theta, p.ff[i]) : theta;
@@ -751,8 +814,10 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         cs[2 * i + 1] = sinf(th);
     }
 
-    Ring<S> rg;
-    if (!reader) ring_prime<S>(rg, p, wg, ci, lane, std::make_integer_sequence<int, S::P>{});
+    // this wave's ring slots in LDS (compute waves only)
+    const int8_t *ring = (const int8_t *)lds + S::ring_off(p.cap) + (reader ? 0 : ci) * S::RING * kSlot;
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
+    if (!reader) ring_prime<S>(p, ring_lds, wg, ci, lane, std::make_integer_sequence<int, S::P>{});
 
     for (int l = 0; l < p.n_layers; l++) {
         vxm_ptab Ly = layer_tab(p) + l;
@@ -775,12 +840,12 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         }
         lds_barrier();
         if (*bail) return;
-        VXM_TS(threadIdx.x == 0, 0);
+        VXM_TS(tid_now() == 0, 0);
         norm_quant<H>(xs, gn, ssq[0], p.eps, xq, xd);
         lds_barrier();
-        if (!reader) ring_phase<S, S::OA, S::SA>(rg, p, l, wg, ci, lane, xq, xd, part);
+        if (!reader) ring_phase<S, S::OA, S::SA>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
         lds_barrier();
-        VXM_TS(threadIdx.x == 0, 1);
+        VXM_TS(tid_now() == 0, 1);
         if (!reader && t < S::RA / 2 * kRep) {
             // RA/2 output words x kRep replicas, one store per thread
             const int wi = t / kRep, r = t % kRep;
@@ -818,12 +883,12 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         }
         lds_barrier();
         if (*bail) return;
-        VXM_TS(threadIdx.x == 0, 5);
+        VXM_TS(tid_now() == 0, 5);
         quantize_lds(big, QD, xq, xd);
         lds_barrier();
-        if (!reader) ring_phase<S, S::OC, S::SC>(rg, p, l, wg, ci, lane, xq, xd, part);
+        if (!reader) ring_phase<S, S::OC, S::SC>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
         lds_barrier();
-        VXM_TS(threadIdx.x == 0, 6);
+        VXM_TS(tid_now() == 0, 6);
         if (!reader && t < S::RC / 2 * kRep) {
             const int wi = t / kRep, r = t % kRep;
             const int row = wg * S::RC + 2 * wi;
@@ -848,12 +913,12 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         }
         lds_barrier();
         if (*bail) return;
-        VXM_TS(threadIdx.x == 0, 7);
+        VXM_TS(tid_now() == 0, 7);
         norm_quant<H>(h1s, gn, ssq[0], p.eps, xq, xd);
         lds_barrier();
-        if (!reader) ring_phase<S, S::OD, S::SD>(rg, p, l, wg, ci, lane, xq, xd, part);
+        if (!reader) ring_phase<S, S::OD, S::SD>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
         lds_barrier();
-        VXM_TS(threadIdx.x == 0, 8);
+        VXM_TS(tid_now() == 0, 8);
         if (!reader && t < S::RD / 4 * kRep) {
             const int wi = t / kRep, r = t % kRep;
             float v[4];
@@ -879,12 +944,12 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         }
         lds_barrier();
         if (*bail) return;
-        VXM_TS(threadIdx.x == 0, 9);
+        VXM_TS(tid_now() == 0, 9);
         quantize_lds(big, F, xq, xd);
         lds_barrier();
-        if (!reader) ring_phase<S, S::OE, S::SE>(rg, p, l, wg, ci, lane, xq, xd, part);
+        if (!reader) ring_phase<S, S::OE, S::SE>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
         lds_barrier();
-        VXM_TS(threadIdx.x == 0, 10);
+        VXM_TS(tid_now() == 0, 10);
         if (!reader && t < S::RE / 2 * kRep) {
             const int wi = t / kRep, r = t % kRep;
             const int row = wg * S::RE + 2 * wi;
@@ -913,13 +978,13 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
     lds_barrier();
     if (*bail) return;
 #ifdef VXM_PERSISTENT_TRACE
-    if (threadIdx.x == 0 && p.trace) p.trace[1] = __builtin_amdgcn_s_memrealtime();
+    if (tid_now() == 0 && p.trace) p.trace[1] = __builtin_amdgcn_s_memrealtime();
 #endif
     if (p.final_norm) {
         rmsnorm_lds(xs, gn, H, p.eps, big, red);
-        for (int i = threadIdx.x; i < H; i += kThreads) p.x[i] = big[i];
+        for (int i = tid_now(); i < H; i += kThreads) p.x[i] = big[i];
     } else {
-        for (int i = threadIdx.x; i < H; i += kThreads) p.x[i] = xs[i];
+        for (int i = tid_now(); i < H; i += kThreads) p.x[i] = xs[i];
     }
 }
 
@@ -941,7 +1006,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_persistent(vxm_pparams p
 // host side
 // ---------------------------------------------------------------------------
 using ShapeTslm = Shape<2048, 16, 2, 128, 6144>;
-using ShapeSmall = Shape<1024, 8, 2, 128, 2048>;
 
 struct vxm_persistent_state {
     void *base = nullptr;
@@ -973,13 +1037,12 @@ static int launch_decode(vxm_ctx *ctx, const vxm_pparams &prm) {
 static bool persistent_shape(const vxm_block_dims &d, int n_cu) {
     if (n_cu != kG) return false;
     if (d.H == 2048 && d.nh == 16 && d.nkv == 2 && d.hd == 128 && d.F == 6144) return true;
-    if (d.H == 1024 && d.nh == 8 && d.nkv == 2 && d.hd == 128 && d.F == 2048) return true;
     return false;
 }
 
 // Largest cache capacity whose attention scores fit the LDS.
 int vxm_persistent_max_cap(const vxm_block_dims &d) {
-    const int fixed = d.H == 2048 ? ShapeTslm::bytes(0) : ShapeSmall::bytes(0);
+    const int fixed = ShapeTslm::bytes(0);
     return (kMaxLds - fixed) / 4 - 16;
 }
 
@@ -1013,7 +1076,7 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
         const int nx = rep_stride((int)d.H / 2), nq = rep_stride((int)(qd + 2 * kvd) / 2),
                   na = rep_stride((int)qd), np_ = rep_stride((int)d.F / 2);
         const size_t words = (size_t)kRep * (2 * nx + nq + na + nx + np_);
-        const size_t dummy = 1024 + 256;
+        const size_t dummy = kUnit + 256;
         const size_t total = tab + words * 8 + dummy + 256;
         if (hipMalloc(&s.base, total) != hipSuccess) {
             (void)hipGetLastError();
@@ -1027,7 +1090,7 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
         s.attb = (uint64_t *)b; b += (size_t)kRep * na * 8;
         s.h1b = (uint64_t *)b; b += (size_t)kRep * nx * 8;
         s.pb = (uint64_t *)b; b += (size_t)kRep * np_ * 8;
-        s.dummy_q = (int8_t *)b; b += 1024;
+        s.dummy_q = (int8_t *)b; b += kUnit;
         s.dummy_d = (uint16_t *)b; b += 256;
         s.err = (int *)b;
         // tags start as all-ones: never equal to a live (epoch >= 1) tag
@@ -1086,7 +1149,7 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
     VXM_HIP(ctx, hipMemsetAsync(tbuf, 0, tbytes, ctx->stream));
     prm.trace = tbuf;
     prm.trace_stride = stride;
-    int rc_ = d.H == 2048 ? launch_decode<ShapeTslm>(ctx, prm) : launch_decode<ShapeSmall>(ctx, prm);
+    int rc_ = launch_decode<ShapeTslm>(ctx, prm);
     if (rc_) return rc_;
     std::vector<uint64_t> th((size_t)kG * stride);
     VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -1100,8 +1163,7 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
     }
     return VXM_OK;
 #else
-    if (d.H == 2048) return launch_decode<ShapeTslm>(ctx, prm);
-    return launch_decode<ShapeSmall>(ctx, prm);
+    return launch_decode<ShapeTslm>(ctx, prm);
 #endif
 }
 
