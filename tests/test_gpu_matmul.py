@@ -122,3 +122,69 @@ def test_decode_gemv_full_size_seed0(vxm_ctx, orc, N, K):
     y = _np(vxm_ctx.mul_mat_q8(w, xq, xd))
     _assert_close(y, orc.mul_mat_f64(wq, xq_ref, N, K, 1))
     w.free()
+
+
+@pytest.fixture
+def mfma_path(vxm_ctx):
+    import vxm
+
+    vxm_ctx.set_path(vxm.PATH_MFMA)
+    yield vxm_ctx
+    vxm_ctx.set_path(vxm.PATH_AUTO)
+
+
+# Shapes whose MFMA GEMM runs without a K split on a 256-CU device: either fewer than
+# 8 blocks per row (no split is ever taken) or at least 256 64x64 output tiles.
+@pytest.mark.parametrize("N,K,M", [(100, 224, 70), (300, 128, 200), (64, 32, 1), (1024, 192, 512),
+                                   (2048, 6144, 512), (6144, 2048, 256), (4096, 256, 300)])
+def test_mfma_gemm_bit_exact_vs_sequential(mfma_path, orc, N, K, M):
+    """Without a K split the GEMM adds the per-block terms in ggml's sequential order."""
+    ctx = mfma_path
+    _, x, wq = _case(orc, N, K, M, 13 * N + K + M)
+    w = ctx.upload_q8_0(wq, N, K)
+    y = _np(ctx.mul_mat(w, _dev(x)))
+    xq = orc.quantize_rows(x, 1)
+    ref = orc.mul_mat(wq, xq, N, K, M)
+    assert np.array_equal(y, ref), f"max diff {np.abs(y - ref).max()}"
+    w.free()
+
+
+# Small-M shapes (CFM / short prefill) where the K dimension is split to fill the device.
+@pytest.mark.parametrize("N,K,M", [(1024, 1024, 48), (2560, 2048, 16), (6144, 2048, 8), (2048, 6144, 48),
+                                   (1000, 4096, 100), (33, 2048, 3), (130, 1024, 9)])
+def test_mfma_gemm_split_k(mfma_path, orc, N, K, M):
+    ctx = mfma_path
+    _, x, wq = _case(orc, N, K, M, 17 * N + K + M)
+    w = ctx.upload_q8_0(wq, N, K)
+    xq_d, xd_d = ctx.quantize_q8_0(_dev(x), 1)
+    y = _np(ctx.mul_mat_q8(w, xq_d, xd_d))
+    xq = orc.quantize_rows(x, 1)
+    _assert_close(y, orc.mul_mat_f64(wq, xq, N, K, M))
+    _assert_close(y, orc.mul_mat(wq, xq, N, K, M).astype(np.float64))
+    # the exact block sums do not depend on the path
+    assert np.array_equal(_np(ctx.block_dots(w, xq_d, xd_d)), orc.block_dots(wq, xq, N, K, M))
+    w.free()
+
+
+def test_auto_path_switches_at_eight_rows(vxm_ctx, orc):
+    """AUTO takes the GEMV below 8 rows and the MFMA GEMM from 8; both meet the oracle bar
+    and the repeated call is deterministic."""
+    import vxm
+
+    N, K = 2048, 2048
+    for M in (7, 8, 64):
+        _, x, wq = _case(orc, N, K, M, M)
+        w = vxm_ctx.upload_q8_0(wq, N, K)
+        xd = _dev(x)
+        y_auto = _np(vxm_ctx.mul_mat(w, xd))
+        assert np.array_equal(y_auto, _np(vxm_ctx.mul_mat(w, xd)))
+        vxm_ctx.set_path(vxm.PATH_GEMV)
+        y_gemv = _np(vxm_ctx.mul_mat(w, xd))
+        vxm_ctx.set_path(vxm.PATH_MFMA)
+        y_mfma = _np(vxm_ctx.mul_mat(w, xd))
+        vxm_ctx.set_path(vxm.PATH_AUTO)
+        assert np.array_equal(y_auto, y_gemv if M < 8 else y_mfma)
+        ref = orc.mul_mat_f64(wq, orc.quantize_rows(x, 1), N, K, M)
+        _assert_close(y_gemv, ref)
+        _assert_close(y_mfma, ref)
+        w.free()

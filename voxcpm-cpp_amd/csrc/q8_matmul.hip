@@ -204,6 +204,162 @@ __global__ void k_block_dots(const int8_t *__restrict__ qs, const int8_t *__rest
     out[i] = s;
 }
 
+
+// ---------------------------------------------------------------------------
+// Q8_0 x Q8_0 GEMM on int8 MFMA, for M rows of activations (prefill, CFM).
+// gfx950's v_mfma_i32_32x32x32_i8 contracts K = 32 -- exactly one Q8_0
+// block -- so one instruction yields the exact int32 block sums of a 32 x 32
+// sub-tile.  Lane l supplies A row l % 32 and B row (weight row) l % 32, k
+// half l / 32; result register v of lane l is row 8(v/4) + 4(l/32) + v%4,
+// column l % 32.  Each lane then adds term = (float)sumi * (d_w * d_x) to its
+// fp32 accumulators block after block: ggml's generic vec_dot_q8_0_q8_0
+// order, so without a K split the output is bit-exact with a sequential
+// per-block fp32 sum.  (Per block and element that is four VALU operations
+// against 1/1024 of an MFMA, which bounds the MFMA duty cycle.)
+//
+// Workgroup: 256 threads (4 waves) on a 64 (M) x 64 (N) tile, wave w on the
+// 32 x 32 sub-tile (w / 2, w % 2).  K moves through LDS GKS blocks at a time,
+// double-buffered through registers.  Tiles are ordered so that the M tiles
+// sharing one weight tile run on one XCD (workgroups are dispatched round
+// robin over the 8 XCDs): the weight tile is fetched into that XCD's L2 once.
+// blockIdx.y = K split: split z adds blocks [z*bps, (z+1)*bps) and writes its
+// partial tile to part[z] (the caller reduces), or y directly when splits = 1.
+// ---------------------------------------------------------------------------
+typedef int v16i __attribute__((ext_vector_type(16)));
+constexpr int GM = 64, GN = 64, GKS = 4;     // tile M, N; blocks per LDS stage
+constexpr int GROW = GKS * 32 + 16;          // padded LDS row (bytes) against bank conflicts
+
+__global__ __launch_bounds__(256) void k_gemm_q8_0_mfma(const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd,
+                                                        const int8_t *__restrict__ wq, const uint16_t *__restrict__ wd,
+                                                        float *__restrict__ y, int M, int N, int K, int tiles_m,
+                                                        int tiles_n, int bps) {
+    __shared__ __align__(16) int8_t As[2][GM * GROW];
+    __shared__ __align__(16) int8_t Bs[2][GN * GROW];
+    __shared__ __align__(16) float Ad[2][GKS][GM];
+    __shared__ __align__(16) float Bd[2][GKS][GN];
+    const int id = blockIdx.x, xcd = id % 8, k8 = id / 8;
+    const int tn = (k8 / tiles_m) * 8 + xcd, tm = k8 % tiles_m;
+    if (tn >= tiles_n) return;
+    const int m0 = tm * GM, n0 = tn * GN;
+    const int nb = K / 32;
+    const int b0 = blockIdx.y * bps, b1 = min(nb, b0 + bps);
+    if (b0 >= b1) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // stage loader: thread t moves 16-byte chunks c = t, t + 256 of each 64 x 128-byte tile
+    // (row c / 8, chunk c % 8) and one scale (block t / 64, row t % 64) of each side
+    auto load = [&](int kb0, v4i (&ra)[2], v4i (&rb)[2], float &sa, float &sb) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int c = tid + 256 * h, r = c >> 3, ch = c & 7, kb = kb0 + (ch >> 1);
+            const bool okk = kb < b1;
+            const int m = m0 + r, n = n0 + r;
+            ra[h] = (okk && m < M) ? *(const v4i *)(xq + (int64_t)m * K + kb * 32 + (ch & 1) * 16) : v4i{0, 0, 0, 0};
+            rb[h] = (okk && n < N) ? *(const v4i *)(wq + (int64_t)n * K + kb * 32 + (ch & 1) * 16) : v4i{0, 0, 0, 0};
+        }
+        const int kb = kb0 + (tid >> 6), r = tid & 63;
+        sa = (kb < b1 && m0 + r < M) ? vxm_h2f(xd[(int64_t)(m0 + r) * nb + kb]) : 0.0f;
+        sb = (kb < b1 && n0 + r < N) ? vxm_h2f(wd[(int64_t)(n0 + r) * nb + kb]) : 0.0f;
+    };
+    auto store = [&](int buf, const v4i (&ra)[2], const v4i (&rb)[2], float sa, float sb) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int c = tid + 256 * h, r = c >> 3, ch = c & 7;
+            *(v4i *)(As[buf] + r * GROW + ch * 16) = ra[h];
+            *(v4i *)(Bs[buf] + r * GROW + ch * 16) = rb[h];
+        }
+        Ad[buf][tid >> 6][tid & 63] = sa;
+        Bd[buf][tid >> 6][tid & 63] = sb;
+    };
+
+    float acc[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[v] = 0.0f;
+    v4i ra[2], rb[2];
+    float sa, sb;
+    load(b0, ra, rb, sa, sb);
+    store(0, ra, rb, sa, sb);
+    __syncthreads();
+    int buf = 0;
+    for (int kb0 = b0; kb0 < b1; kb0 += GKS) {
+        const bool more = kb0 + GKS < b1;
+        if (more) load(kb0 + GKS, ra, rb, sa, sb);
+        const int8_t *arow = As[buf] + (wm * 32 + (lane & 31)) * GROW + (lane >> 5) * 16;
+        const int8_t *brow = Bs[buf] + (wn * 32 + (lane & 31)) * GROW + (lane >> 5) * 16;
+#pragma unroll
+        for (int kb = 0; kb < GKS; kb++) {
+            if (kb0 + kb >= b1) break;
+            const v4i a = *(const v4i *)(arow + kb * 32);
+            const v4i b = *(const v4i *)(brow + kb * 32);
+            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
+            const float dw = Bd[buf][kb][wn * 32 + (lane & 31)];
+            const float *dxr = Ad[buf][kb] + wm * 32 + 4 * (lane >> 5);
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 dx = *(const float4 *)(dxr + 8 * g);
+                const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int v = 4 * g + e;
+                    acc[v] = acc[v] + (float)c[v] * (dw * dxv[e]);
+                }
+            }
+        }
+        if (more) {
+            store(buf ^ 1, ra, rb, sa, sb);
+            buf ^= 1;
+        }
+        __syncthreads();
+    }
+    float *out = y + (int64_t)blockIdx.y * M * N;
+    const int n = n0 + wn * 32 + (lane & 31);
+    if (n < N) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int m = m0 + wm * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            if (m < M) out[(int64_t)m * N + n] = acc[v];
+        }
+    }
+}
+
+// y = sum over the K splits of part[z], added in split order.
+__global__ void k_split_reduce(const float *__restrict__ part, int splits, int64_t mn, float *__restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= mn) return;
+    float s = part[i];
+    for (int z = 1; z < splits; z++) s = s + part[(int64_t)z * mn + i];
+    y[i] = s;
+}
+
+static int launch_gemm(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                       float *y) {
+    const int N = (int)w->n, K = (int)w->k, nb = K / 32;
+    const int tiles_m = (int)((M + GM - 1) / GM), tiles_n = (N + GN - 1) / GN;
+    const int grid_x = 8 * tiles_m * ((tiles_n + 7) / 8);
+    // split K until the grid covers the CUs (each split at least one LDS stage)
+    int splits = 1;
+    while ((int64_t)tiles_m * tiles_n * splits < ctx->n_cu && nb / (splits * 2) >= GKS) splits *= 2;
+    const int bps = (nb + splits - 1) / splits;
+    splits = (nb + bps - 1) / bps;   // every split then owns at least one block
+    float *dst = y;
+    if (splits > 1) {
+        int rc = vxm_ensure_split(ctx, (size_t)splits * M * N * sizeof(float));
+        if (rc) return rc;
+        dst = (float *)ctx->split_buf;
+    }
+    hipLaunchKernelGGL(k_gemm_q8_0_mfma, dim3(grid_x, splits), dim3(256), 0, ctx->stream, xq, xd, w->qs, w->d, dst,
+                       (int)M, N, K, tiles_m, tiles_n, bps);
+    VXM_CHECK_LAUNCH(ctx);
+    if (splits > 1) {
+        const int64_t mn = M * N;
+        hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, ctx->stream, dst, splits,
+                           mn, y);
+        VXM_CHECK_LAUNCH(ctx);
+    }
+    return VXM_OK;
+}
+
 template <int C, int R>
 static void launch_gemv_c(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd,
                           int64_t M, float *y) {
@@ -213,10 +369,16 @@ static void launch_gemv_c(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, c
                        y, (int)w->n, (int)M);
 }
 
+// Rows of activations from which the MFMA GEMM replaces the weight-streaming
+// GEMV (which re-reads each activation row per weight row group).
+constexpr int kMfmaMinRows = 8;
+
 int vxm_launch_mul_mat(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd,
                        int64_t M, float *y) {
     if (M <= 0) return VXM_OK;
     const int64_t K = w->k;
+    const bool mfma = ctx->path == VXM_PATH_MFMA || (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
+    if (mfma) return launch_gemm(ctx, w, xq, xd, M, y);
     bool done = false;
     if (w->dg) {
         switch (K / 1024) {

@@ -61,6 +61,7 @@ extern "C" int vxm_close(vxm_ctx *ctx) {
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
     if (ctx->act_buf) hipFree(ctx->act_buf);
+    if (ctx->split_buf) hipFree(ctx->split_buf);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return VXM_OK;
@@ -137,6 +138,20 @@ int vxm_ensure_act(vxm_ctx *ctx, size_t bytes) {
         return vxm_fail(ctx, VXM_ERR_OOM, "activation scratch of %zu bytes failed", want);
     }
     ctx->act_bytes = want;
+    return VXM_OK;
+}
+
+int vxm_ensure_split(vxm_ctx *ctx, size_t bytes) {
+    if (ctx->split_bytes >= bytes) return VXM_OK;
+    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->split_buf) VXM_HIP(ctx, hipFree(ctx->split_buf));
+    ctx->split_buf = nullptr;
+    ctx->split_bytes = 0;
+    if (hipMalloc(&ctx->split_buf, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return vxm_fail(ctx, VXM_ERR_OOM, "GEMM split scratch of %zu bytes failed", bytes);
+    }
+    ctx->split_bytes = bytes;
     return VXM_OK;
 }
 
