@@ -22,6 +22,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "voxcpm-cpp_amd"))
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA
 H, NH, NKV, HD, F, L = 2048, 16, 2, 128, 6144, 28
 
 
@@ -160,6 +161,64 @@ def bench_decode(ctx, torch, vxm, layers, n_layers, copies, ctx0, steps, warmup,
     return ms * 1000.0 / steps, ok
 
 
+def bench_gemm(ctx, torch, vxm, N, K, M, reps):
+    """One Q8_0 x Q8_0 matmul of M activation rows (the MFMA GEMM), back to back."""
+    import numpy as np
+
+    w32 = vxm.host_randn(7, N * K, 0.0, 0.02).reshape(N, K)
+    x = vxm.host_randn(8, M * K, 0.0, 1.0).reshape(M, K)
+    w = ctx.upload_q8_0(vxm.host_quantize_q8_0(w32), N, K)
+    xq, xs = ctx.quantize_q8_0(torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0"), vxm.QUANT_X86)
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda:0")
+    L_ = vxm.lib()
+    a = (w.h, vxm._ptr(xq), vxm._ptr(xs), vxm._ptr(y))
+    for _ in range(3):
+        L_.vxm_mul_mat_q8_0_q8_0(ctx.h, a[0], a[1], a[2], M, a[3])
+    ctx.sync()
+    t = Timer(torch, ctx)
+    t.start()
+    for _ in range(reps):
+        L_.vxm_mul_mat_q8_0_q8_0(ctx.h, a[0], a[1], a[2], M, a[3])
+    us = t.stop_ms() * 1000.0 / reps
+    w.free()
+    return us
+
+
+def prefill_ops(M, n_layers=L):
+    """int8 multiply-adds x 2 of the Q8_0 GEMMs and f32 attention flops of an M-token causal prefill."""
+    qd, kvd = NH * HD, NKV * HD
+    weights = qd * H + 2 * kvd * H + H * qd + 2 * F * H + H * F
+    gemm = 2 * M * weights * n_layers
+    pairs = M * (M + 1) // 2
+    attn = 2 * 2 * pairs * NH * HD * n_layers
+    return gemm, attn
+
+
+def bench_prefill(ctx, torch, vxm, layers, n_layers, M, reps):
+    """M-token causal prefill of the stack from position 0 (vxm_minicpm4_forward)."""
+    cfg = dict(hidden_size=H, n_layers=n_layers, n_heads=NH, n_kv_heads=NKV, head_dim=HD, intermediate_size=F,
+               rms_norm_eps=1e-6, rope_theta=10000)
+    fn = vxm.host_randn(11, H, 1.0, 0.02)
+    m = vxm.MiniCPM4(ctx, cfg, layers, final_norm=fn)
+    kv = vxm.KVCache(ctx, n_layers, NKV, HD, M)
+    x0 = torch.from_numpy(vxm.host_randn(4, M * H, 0.0, 1.0).reshape(M, H)).to("cuda:0")
+    x = x0.clone()
+    m.forward(kv, x, 0)
+    ctx.sync()
+    t = Timer(torch, ctx)
+    ms = 0.0
+    for _ in range(reps):
+        x.copy_(x0)
+        torch.cuda.synchronize()
+        t.start()
+        m.forward(kv, x, 0)
+        ms += t.stop_ms()
+    ok = bool(torch.isfinite(x).all().item())
+    kv.free()
+    m.free()
+    return ms * 1000.0 / reps, ok
+
+
 def cpu_baseline(vxm, layers, n_layers, ctx0, tokens, threads):
     """The oracle's SIMD restatement of ggml's CPU Q8_0 decode (1 copy of weights)."""
     import ctypes as C
@@ -211,6 +270,9 @@ def main():
     ap.add_argument("--cpu-tokens-1t", type=int, default=16, help="decode tokens timed on one host core")
     ap.add_argument("--decode-only", action="store_true",
                     help="time only the 28-layer decode (for profiling the dominant kernel)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="time only the prefill legs (MFMA GEMMs and the 512-token 28-layer prefill)")
+    ap.add_argument("--prefill-tokens", type=int, default=512)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -222,6 +284,33 @@ def main():
     mode = {"auto": 0, "kernels": 1, "persistent": 2}[args.mode]
     ctx = vxm.Context(0)
     res = {}
+    pre = None
+    if not args.decode_only:
+        M = args.prefill_tokens
+        gemms = {}
+        for name, (N, K) in (("qkv", (NH * HD + 2 * NKV * HD, H)), ("o", (H, NH * HD)), ("gate_up", (2 * F, H)),
+                             ("down", (H, F))):
+            us = bench_gemm(ctx, torch, vxm, N, K, M, 20)
+            tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+            gemms[name] = {"N": N, "K": K, "M": M, "us": round(us, 2), "TOPs": round(tops, 1),
+                           "mfma_frac": round(tops / INT8_PEAK_TOPS, 4)}
+            log(f"gemm {name} {N}x{K} M={M}: {us:.2f} us, {tops:.1f} TOP/s ({100 * tops / INT8_PEAK_TOPS:.1f}% int8)")
+        t0 = time.time()
+        pl = make_layers(vxm, 1, L)
+        log(f"generated {L} Q8_0 layers in {time.time() - t0:.1f} s")
+        us_pre, fin = bench_prefill(ctx, torch, vxm, pl, L, M, 3)
+        g_ops, a_flops = prefill_ops(M)
+        pre = {"tokens": M, "layers": L, "us": round(us_pre, 1), "tokens_per_s": round(M / (us_pre * 1e-6), 1),
+               "gemm_TOPs": round(g_ops / (us_pre * 1e-6) / 1e12, 1),
+               "gemm_mfma_frac_of_step": round(g_ops / (us_pre * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
+               "attention_GFLOP": round(a_flops / 1e9, 2), "finite": fin, "gemm": gemms}
+        log(f"prefill {M} tokens x {L} layers: {us_pre:.1f} us ({M / (us_pre * 1e-6):.0f} tok/s), "
+            f"GEMM work {g_ops / (us_pre * 1e-6) / 1e12:.1f} TOP/s over the step, finite={fin}")
+        del pl
+        if args.prefill_only:
+            print(json.dumps({"prefill": pre}))
+            ctx.close()
+            return
     if not args.decode_only:
         for (N, K) in ((6144, 2048), (2048, 6144)):
             us = bench_gemv(ctx, torch, vxm, N, K, 64, 10)
@@ -295,6 +384,7 @@ def main():
         "step_bytes": int(sb),
         "gemv": res,
         "layer_decode_ctx512_us": round(us1, 3) if us1 is not None else None,
+        "prefill": pre,
         "roofline": roof,
         "cpu_baseline": cpu,
     }

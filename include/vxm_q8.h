@@ -178,6 +178,65 @@ int vxm_minicpm4_set_decode_mode(vxm_minicpm4 *m, int mode);
  * VXM_ERR_BACKEND, then clears it.  Decode calls themselves never block. */
 int vxm_minicpm4_check(vxm_minicpm4 *m);
 
+/* ---- LocDiT and the CFM solver -------------------------------------------
+ * Mirrors vcpm_locdit_config (src/locdit.h:26-34) plus the projection widths. */
+typedef struct vxm_locdit_config {
+    int32_t hidden_size;
+    int32_t n_layers;
+    int32_t n_heads;
+    int32_t n_kv_heads;
+    int32_t intermediate_size;
+    int32_t head_dim;
+    int32_t feat_dim;         /* latent width of x and of the velocity (in_proj / out_proj) */
+    int32_t cond_dim;         /* width of the cond tokens (cond_proj) */
+    float   rms_norm_eps;
+    int32_t rope_theta;       /* the reference uses 10000 (src/locdit.c:351) */
+    /* head_dim/2 rope factors (host), or NULL for the MiniCPM4 rule (LongRoPE
+     * short factors when head_dim == 128, none otherwise) */
+    const float *rope_freq_factors;
+} vxm_locdit_config;
+
+/* vcpm_locdit_weights (src/locdit.h:41-68): GGUF Q8_0 rows and F32 vectors in host
+ * memory.  Biases may be NULL. */
+typedef struct vxm_locdit_weights_q8_0 {
+    const vxm_layer_weights_q8_0 *layers;                   /* n_layers blocks */
+    const void  *in_proj;   const float *in_bias;          /* [hidden][feat_dim]  */
+    const void  *cond_proj; const float *cond_bias;        /* [hidden][cond_dim]  */
+    const void  *out_proj;  const float *out_bias;         /* [feat_dim][hidden]  */
+    const float *norm;                                     /* [hidden]            */
+    const void  *t_w1, *t_w2, *dt_w1, *dt_w2;              /* [hidden][hidden]    */
+    const float *t_b1, *t_b2, *dt_b1, *dt_b2;
+} vxm_locdit_weights_q8_0;
+
+typedef struct vxm_locdit vxm_locdit;
+
+int vxm_locdit_create(vxm_ctx *ctx, const vxm_locdit_config *cfg, const vxm_locdit_weights_q8_0 *w,
+                      vxm_locdit **out);
+int vxm_locdit_free(vxm_locdit *m);
+
+/* vcpm_locdit_forward (src/locdit.c:216-400): velocity of x for one branch.
+ * x [P][feat_dim], cond [Pc][cond_dim], mu [2][hidden] or NULL (the
+ * unconditional branch: zero rows), out [P][feat_dim]; t and dt are the
+ * timestep scalars.  Sequence [mu(2), t(1), cond(Pc), x(P)], 12 non-causal
+ * rope blocks from position 0, RMSNorm of the x rows, out_proj.  The
+ * reference uses Pc == P. */
+int vxm_locdit_forward(vxm_locdit *m, const float *x_dev, const float *cond_dev, int32_t P, int32_t Pc,
+                       float t, float dt, const float *mu_dev, float *out_dev);
+
+/* The CFM Euler loop of vcpm_gen_step (src/gen_step.c:583-649), on the
+ * device with no host synchronisation: for each step past the zero-init
+ * steps (when use_zero_star), t from the schedule, the conditional (mu) and
+ * unconditional (no mu) velocities in ONE batch of 2 x (3 + Pc + P) rows,
+ * CFG-Zero* (vcpm_cfm_cfg_zero_star, src/cfm_solver.c:65-93) and
+ * x = bf16(x + bf16(dt * v)).  Without CFG (cfg_value == 1 or mu == NULL,
+ * src/gen_step.c:475) only the conditional branch runs.  x [P][feat_dim] is
+ * updated in place. */
+#define VXM_CFM_SWAY 0      /* vcpm_cfm_sway_t_bf16 (src/cfm_solver.c:27-37) */
+#define VXM_CFM_UNIFORM 1   /* t = bf16(1 - step / n_steps) */
+int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev, int32_t P, int32_t Pc,
+                  const float *mu_dev, int32_t n_steps, float cfg_value, int32_t schedule,
+                  int32_t use_zero_star);
+
 /* ---- host helpers (no device work) --------------------------------------
  * GGUF Q8_0 quantization of F32 rows with the weight rule of
  * ggml_quantize_chunk (tools/quantize.c:292): d = amax/127 (fp16),
@@ -187,6 +246,19 @@ int vxm_host_quantize_q8_0(const float *x, int64_t rows, int64_t k, void *gguf_r
  * CFM noise, src/gen_step.c:409-431) with Box-Muller in double; element i is
  * stream element offset + i.  No reference counterpart: benchmark inputs. */
 int vxm_host_randn(uint64_t seed, uint64_t offset, int64_t n, float mean, float std, float *out);
+/* dit_sinusoidal_t_embed (src/locdit.c:163-188) of a scalar t: dim floats. */
+int vxm_host_sinusoid_embed(float t, int32_t dim, float *out);
+/* CFM time of a step: VXM_CFM_SWAY = vcpm_cfm_sway_t_bf16
+ * (src/cfm_solver.c:27-37), VXM_CFM_UNIFORM = bf16(1 - step / n_steps). */
+float vxm_host_cfm_t(int32_t step, int32_t n_steps, int32_t schedule);
+/* vcpm_cfm_zero_star_steps (src/gen_step.c:50-54). */
+int32_t vxm_host_cfm_zero_star_steps(int32_t n_steps);
+/* The NEOX rope angles of ggml_rope_ext as vcpm_rope uses them
+ * (src/minicpm4.c:165-223): for positions pos0 .. pos0+n_pos-1, head_dim/2
+ * (cos, sin) pairs each, out[p * head_dim + 2i (+1)]; ff = head_dim/2
+ * frequency factors or NULL.  The device kernels read this table. */
+int vxm_host_rope_cache(float base, int32_t head_dim, const float *ff, int32_t pos0, int32_t n_pos,
+                        float *out);
 
 #ifdef __cplusplus
 }

@@ -97,6 +97,8 @@ def lib():
         L.orc_sinusoid_embed.argtypes = [_F, C.c_int32, _P]
         L.orc_locdit_forward.argtypes = [C.POINTER(Cfg), C.POINTER(LocDiT), _P, _P, C.c_int32, C.c_int32,
                                          _F, _F, _P, _P]
+        L.orc_locdit_forward_states.argtypes = [C.POINTER(Cfg), C.POINTER(LocDiT), _P, _P, C.c_int32, C.c_int32,
+                                                _F, _F, _P, _P, _P]
         L.orc_cfm_sway_t_bf16.restype = _F
         L.orc_cfm_sway_t_bf16.argtypes = [_I, _I]
         L.orc_cfm_uniform_t_bf16.restype = _F
@@ -321,3 +323,67 @@ def sinusoid(t, dim):
     out = np.empty(dim, dtype=np.float32)
     lib().orc_sinusoid_embed(t, dim, _p(out))
     return out
+
+
+# ---- LocDiT / CFM ----
+
+class LocDiTW:
+    """Host copy of LocDiT weights: GGUF Q8_0 rows + F32 vectors (biases may be None)."""
+
+    names = ("in_proj", "in_bias", "cond_proj", "cond_bias", "out_proj", "out_bias", "norm",
+             "t_w1", "t_w2", "dt_w1", "dt_w2", "t_b1", "t_b2", "dt_b1", "dt_b2")
+
+    def __init__(self, layers, feat, **kw):
+        self.layers = layers
+        self.feat = feat
+        for n in self.names:
+            v = kw.get(n)
+            setattr(self, n, None if v is None else np.ascontiguousarray(v))
+
+    def struct(self):
+        self._arr = (Layer * max(1, len(self.layers)))(*[l.struct() for l in self.layers])
+        g = {n: (None if getattr(self, n) is None else getattr(self, n).ctypes.data) for n in self.names}
+        return LocDiT(C.cast(self._arr, C.c_void_p).value, len(self.layers), g["in_proj"], g["in_bias"],
+                      g["cond_proj"], g["cond_bias"], g["out_proj"], g["out_bias"], g["norm"], g["t_w1"],
+                      g["t_w2"], g["dt_w1"], g["dt_w2"], g["t_b1"], g["t_b2"], g["dt_b1"], g["dt_b2"], self.feat)
+
+
+def locdit_forward(cfg, w, x, cond, t, dt=0.0, mu=None):
+    """orc_locdit_forward: velocity [P][feat] of x [P][feat] with cond [Pc][feat], mu [2][hidden] or None."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    cond = np.ascontiguousarray(cond, dtype=np.float32)
+    mu = None if mu is None else np.ascontiguousarray(mu, dtype=np.float32)
+    P, Pc = x.shape[0], cond.shape[0]
+    out = np.empty((P, w.feat), dtype=np.float32)
+    s = w.struct()
+    rc = lib().orc_locdit_forward(C.byref(cfg), C.byref(s), _p(x), _p(cond), P, Pc, t, dt, _p(mu), _p(out))
+    assert rc == 0
+    return out
+
+
+def locdit_states(cfg, w, x, cond, t, dt=0.0, mu=None):
+    """orc_locdit_forward_states: (velocity, sequence entering each block + after the last)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    cond = np.ascontiguousarray(cond, dtype=np.float32)
+    mu = None if mu is None else np.ascontiguousarray(mu, dtype=np.float32)
+    P, Pc = x.shape[0], cond.shape[0]
+    S, H = 3 + Pc + P, cfg.hidden
+    out = np.empty((P, w.feat), dtype=np.float32)
+    states = np.empty((len(w.layers) + 1, S, H), dtype=np.float32)
+    s = w.struct()
+    rc = lib().orc_locdit_forward_states(C.byref(cfg), C.byref(s), _p(x), _p(cond), P, Pc, t, dt, _p(mu), _p(out),
+                                         _p(states))
+    assert rc == 0
+    return out, states
+
+
+def cfm_solve(cfg, w, x, cond, mu, n_steps, cfg_value, schedule=0, use_zero_star=1):
+    """orc_cfm_solve: the CFM Euler loop (schedule 0 sway, 1 uniform); returns the final x."""
+    x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    cond = np.ascontiguousarray(cond, dtype=np.float32)
+    mu = None if mu is None else np.ascontiguousarray(mu, dtype=np.float32)
+    s = w.struct()
+    rc = lib().orc_cfm_solve(C.byref(cfg), C.byref(s), _p(x), _p(cond), x.shape[0], cond.shape[0], _p(mu),
+                             n_steps, cfg_value, schedule, use_zero_star)
+    assert rc == 0
+    return x

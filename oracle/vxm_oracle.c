@@ -506,6 +506,15 @@ static void time_mlp(const orc_locdit *w, int dt, const float *emb, int64_t H, f
 int orc_locdit_forward(const orc_cfg *cfg, const orc_locdit *w, const float *x,
                        const float *cond, int32_t P, int32_t Pc, float t, float dt,
                        const float *mu, float *out) {
+    return orc_locdit_forward_states(cfg, w, x, cond, P, Pc, t, dt, mu, out, NULL);
+}
+
+/* orc_locdit_forward that also copies the sequence [S][hidden] entering each
+ * block and leaving the last one into states[(n_layers + 1)][S][hidden]
+ * (when non-NULL), for layer-by-layer comparisons. */
+int orc_locdit_forward_states(const orc_cfg *cfg, const orc_locdit *w, const float *x,
+                              const float *cond, int32_t P, int32_t Pc, float t, float dt,
+                              const float *mu, float *out, float *states) {
     const int64_t H = cfg->hidden, F = w->feat;
     const int64_t S = 3 + Pc + P;
     const int var = cfg->quant_variant;
@@ -521,8 +530,11 @@ int orc_locdit_forward(const orc_cfg *cfg, const orc_locdit *w, const float *x,
     for (int64_t i = 0; i < H; i++) seq[2 * H + i] = orc_bf16_round(tf[i] + dtf[i]);
     linear_bias_bf16(w->cond_proj, w->cond_bias, cond, H, F, Pc, seq + 3 * H, var);
     linear_bias_bf16(w->in_proj, w->in_bias, x, H, F, P, seq + (3 + Pc) * H, var);
-    for (int32_t l = 0; l < w->n_layers; l++)
+    for (int32_t l = 0; l < w->n_layers; l++) {
+        if (states) memcpy(states + (size_t)l * S * H, seq, sizeof(float) * (size_t)(S * H));
         orc_minicpm4_block(cfg, &w->layers[l], seq, S, NULL, NULL, 0, 0, 1);
+    }
+    if (states) memcpy(states + (size_t)w->n_layers * S * H, seq, sizeof(float) * (size_t)(S * H));
     float *hn = (float *)malloc(sizeof(float) * (size_t)(P * H));
     orc_rms_norm(seq + (3 + Pc) * H, w->norm, P, H, cfg->eps, hn);
     linear_bias_bf16(w->out_proj, w->out_bias, hn, F, H, P, out, var);
@@ -581,8 +593,10 @@ int orc_cfm_zero_star_steps(int n_steps) {
     return z > 1 ? z : 1;
 }
 
-/* The CFM Euler loop of vcpm_gen_step (src/gen_step.c:583-649) with CFG:
- * velocities of the cond (mu) and uncond (mu = 0) branches, CFG-Zero* blend,
+/* The CFM Euler loop of vcpm_gen_step (src/gen_step.c:583-649): with CFG
+ * (cfg_value != 1 and mu given, src/gen_step.c:475) the velocities of the
+ * cond (mu) and uncond (mu = 0) branches and their CFG-Zero* blend, else the
+ * cond velocity alone; then
  * x = bf16(x + bf16(step * v)).  schedule 0 = sway, 1 = uniform.  x is the
  * [P][feat] latent, updated in place. */
 int orc_cfm_solve(const orc_cfg *cfg, const orc_locdit *w, float *x, const float *cond,
@@ -592,6 +606,7 @@ int orc_cfm_solve(const orc_cfg *cfg, const orc_locdit *w, float *x, const float
     float *vc = (float *)malloc(sizeof(float) * (size_t)n);
     float *vu = (float *)malloc(sizeof(float) * (size_t)n);
     const int zs = use_zero_star ? orc_cfm_zero_star_steps(n_steps) : 0;
+    const int use_cfg = cfg_value != 1.0f && mu != NULL;   /* src/gen_step.c:475 */
     for (int step = 0; step < n_steps; step++) {
         if (step < zs) continue;
         const float t = schedule ? orc_cfm_uniform_t_bf16(step, n_steps) : orc_cfm_sway_t_bf16(step, n_steps);
@@ -599,8 +614,12 @@ int orc_cfm_solve(const orc_cfg *cfg, const orc_locdit *w, float *x, const float
                                   : orc_cfm_sway_t_bf16(step + 1, n_steps);
         const float dtv = orc_bf16_round(-(t - nt));
         orc_locdit_forward(cfg, w, x, cond, P, Pc, t, 0.0f, mu, vc);
-        orc_locdit_forward(cfg, w, x, cond, P, Pc, t, 0.0f, NULL, vu);
-        orc_cfm_cfg_zero_star(vu, vc, n, cfg_value);
+        if (use_cfg) {
+            orc_locdit_forward(cfg, w, x, cond, P, Pc, t, 0.0f, NULL, vu);
+            orc_cfm_cfg_zero_star(vu, vc, n, cfg_value);
+        } else {
+            memcpy(vu, vc, sizeof(float) * (size_t)n);
+        }
         for (int j = 0; j < n; j++) x[j] = orc_bf16_round(x[j] + orc_bf16_round(dtv * vu[j]));
     }
     free(vc); free(vu);

@@ -106,6 +106,9 @@ void  orc_sinusoid_embed(float t, int32_t dim, float *out);
 int   orc_locdit_forward(const orc_cfg *cfg, const orc_locdit *w, const float *x,
                          const float *cond, int32_t P, int32_t Pc, float t, float dt,
                          const float *mu, float *out);
+int   orc_locdit_forward_states(const orc_cfg *cfg, const orc_locdit *w, const float *x,
+                                const float *cond, int32_t P, int32_t Pc, float t, float dt,
+                                const float *mu, float *out, float *states);
 float orc_cfm_sway_t_bf16(int step, int n_steps);
 float orc_cfm_uniform_t_bf16(int step, int n_steps);
 float orc_cfm_cfg_zero_star(float *negative, const float *positive, int n, float cfg_value);

@@ -1,0 +1,227 @@
+"""GPU parity of the LocDiT velocity network and the device CFM loop against the oracle.
+
+Velocities pass through BF16 after every op (src/locdit.c:118-121), so their
+bar is the block bar: >= 99.5% of elements within 1e-3 rel / 1e-4 abs of the
+oracle, every element within 4 BF16 ulps (+1e-4), relative L2 < 1e-3.
+
+Full-width blocks are compared one by one (each device block fed the
+oracle's input to that block) against the block's intrinsic sensitivity:
+Q8_0 re-quantization of every activation plus non-causal attention make one
+last-bit difference anywhere (the GPU sums in a different order) spread over
+the whole sequence.  The oracle's own block output moves by a relative L2 up
+to ~4e-3 and up to 2^-7 of a row's scale when ONE input element moves by one
+BF16 ulp (test_locdit_host.py::test_oracle_block_sensitivity_to_one_ulp).
+Sensitivity bar: relative L2 < 5e-3 and every element within 2^-6 of its
+row's largest magnitude.  Over 12 blocks this compounds, so the end-to-end
+velocity of the deep stack carries a gross-error bar (relative L2 < 5e-2).
+
+The loop mechanics (batching both CFG branches, CFG-Zero*, the Euler update)
+are checked exactly: with every projection on the MFMA GEMM the batched solve
+equals single-branch device forwards followed by the reference's host loop.
+Whole trajectories against the oracle carry a wider bar: every Euler step
+feeds x back through in_proj and Q8_0 re-quantization, and CFG-Zero*'s scale
+st* is one BF16 scalar, so a last-bit difference anywhere moves the whole
+trajectory.  The oracle's own 3-step trajectory moves by a relative L2 up to
+~1.4e-2 (max 0.08) when ONE element of x0 moves by one BF16 ulp
+(test_locdit_host.py::test_oracle_cfm_trajectory_sensitivity).  Trajectory
+bar: relative L2 < 3e-2 and every element within 1/8 absolute.
+"""
+import numpy as np
+import pytest
+
+from locdit_case import make_inputs, make_locdit
+from test_gpu_minicpm4 import assert_layer_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    import torch
+
+    return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+SMALL = dict(H=256, L=2, nh=4, nkv=2, hd=64, F=512, feat=64)
+
+
+def _model(vxm_ctx, orc, seed, H, L, nh, nkv, hd, F, feat, bias=True, keep=None):
+    import vxm
+
+    cfg, w, ow, ocfg = make_locdit(orc, seed, H, L, nh, nkv, hd, F, feat, bias)
+    if keep is not None:
+        keep.update(cfg=cfg, w=w)
+    return vxm.LocDiT(vxm_ctx, cfg, w), ow, ocfg
+
+
+@pytest.mark.parametrize("with_mu", [True, False])
+@pytest.mark.parametrize("P,Pc,t,dt", [(4, 5, 0.7, 0.0), (2, 2, 1.0, 0.25), (1, 0, 0.05, 0.0)])
+def test_locdit_forward_small(vxm_ctx, orc, with_mu, P, Pc, t, dt):
+    m, ow, ocfg = _model(vxm_ctx, orc, 11, **SMALL)
+    x, cond, mu = make_inputs(12 + P, P, Pc, SMALL["feat"], SMALL["H"])
+    mu = mu if with_mu else None
+    v = m.forward(_dev(x), _dev(cond) if Pc else None, t, dt, _dev(mu)).cpu().numpy()
+    ref = orc.locdit_forward(ocfg, ow, x, cond, t, dt, mu)
+    assert_layer_close(v, ref, what=f"locdit P={P} Pc={Pc} mu={with_mu}")
+    m.free()
+
+
+def test_locdit_forward_head_dim_128_no_bias(vxm_ctx, orc):
+    """head_dim 128 takes the LongRoPE factors (src/minicpm4.c:183-190); biases absent."""
+    m, ow, ocfg = _model(vxm_ctx, orc, 21, H=256, L=2, nh=2, nkv=1, hd=128, F=512, feat=32, bias=False)
+    x, cond, mu = make_inputs(22, 3, 4, 32, 256)
+    v = m.forward(_dev(x), _dev(cond), 0.4, 0.0, _dev(mu)).cpu().numpy()
+    assert_layer_close(v, orc.locdit_forward(ocfg, ow, x, cond, 0.4, 0.0, mu), what="locdit hd128")
+    m.free()
+
+
+@pytest.mark.parametrize("schedule", [0, 1])
+@pytest.mark.parametrize("cfg_value,with_mu", [(2.0, True), (1.0, True), (2.0, False)])
+def test_cfm_solve_small(vxm_ctx, orc, schedule, cfg_value, with_mu):
+    """The whole Euler loop on the device (both CFG branches in one batch) against
+    orc_cfm_solve (two separate forwards per step)."""
+    m, ow, ocfg = _model(vxm_ctx, orc, 31, **SMALL)
+    x0, cond, mu = make_inputs(32, 4, 5, SMALL["feat"], SMALL["H"])
+    mu = mu if with_mu else None
+    x = _dev(x0)
+    m.cfm_solve(x, _dev(cond), _dev(mu), 6, cfg_value, schedule, True)
+    ref = orc.cfm_solve(ocfg, ow, x0, cond, mu, 6, cfg_value, schedule, 1)
+    assert_trajectory_close(x.cpu().numpy(), ref, what=f"cfm sched={schedule} cfg={cfg_value} mu={with_mu}")
+    m.free()
+
+
+def assert_sensitivity_close(y, ref, what=""):
+    y, ref = np.asarray(y, np.float64), np.asarray(ref, np.float64)
+    rel = np.linalg.norm(y - ref) / max(np.linalg.norm(ref), 1e-30)
+    scale = np.abs(ref).max(axis=-1, keepdims=True)
+    worst = (np.abs(y - ref) / np.maximum(scale, 1e-30)).max()
+    print(f"{what}: rel_l2 {rel:.2e} worst/row-scale {worst:.2e}")
+    assert rel < 5e-3 and worst <= 2.0 ** -6, (what, rel, worst)
+
+
+def assert_trajectory_close(y, ref, what=""):
+    y, ref = np.asarray(y, np.float64), np.asarray(ref, np.float64)
+    rel = np.linalg.norm(y - ref) / max(np.linalg.norm(ref), 1e-30)
+    mx = np.abs(y - ref).max()
+    print(f"{what}: rel_l2 {rel:.2e} max_abs {mx:.3e}")
+    assert rel < 3e-2 and mx <= 1.0 / 8, (what, rel, mx)
+
+
+def test_cfm_solve_matches_stepwise_forwards(vxm_ctx, orc):
+    """Batched CFG steps == two single-branch forwards per step + the reference's host
+    CFG-Zero* and Euler update, bit for bit (no zero-init step).  Every projection
+    takes the MFMA GEMM, whose per-row result does not depend on the row count."""
+    import torch
+    import vxm
+
+    m, ow, ocfg = _model(vxm_ctx, orc, 41, **SMALL)
+    vxm_ctx.set_path(vxm.PATH_MFMA)
+    x0, cond, mu = make_inputs(42, 4, 5, SMALL["feat"], SMALL["H"])
+    xd, cd, md = _dev(x0), _dev(cond), _dev(mu)
+    n = 3
+    x = xd.clone()
+    m.cfm_solve(x, cd, md, n, 2.0, 1, False)
+    xs = x0.copy()
+    for step in range(n):
+        t, nt = orc.uniform_t(step, n), orc.uniform_t(step + 1, n)
+        dt = orc.bf16_round(np.float32([-(np.float32(t) - np.float32(nt))]))[0]
+        vc = m.forward(_dev(xs), cd, t, 0.0, md).cpu().numpy()
+        vu = m.forward(_dev(xs), cd, t, 0.0, None).cpu().numpy()
+        _, v = orc.cfg_zero_star(vu, vc, 2.0)
+        xs = orc.bf16_round(xs + orc.bf16_round(np.float32(dt) * v))
+    torch.cuda.synchronize()
+    vxm_ctx.set_path(vxm.PATH_AUTO)
+    got = x.cpu().numpy()
+    assert np.array_equal(got, xs), f"max diff {np.abs(got - xs).max()}"
+    m.free()
+
+
+FULL = dict(H=1024, L=12, nh=16, nkv=16, hd=64, F=4096, feat=64)
+
+
+def test_locdit_full_width_one_block(vxm_ctx, orc):
+    """Full width (hidden 1024, 16 x 64 heads, FFN 4096, 24 rows) with one block: the
+    whole driver (time MLPs, projections, assembly, slice, norm, out_proj)."""
+    m, ow, ocfg = _model(vxm_ctx, orc, 51, **dict(FULL, L=1))
+    x, cond, mu = make_inputs(52, 4, 17, 64, 1024)
+    v = m.forward(_dev(x), _dev(cond), 0.6, 0.0, _dev(mu)).cpu().numpy()
+    assert_layer_close(v, orc.locdit_forward(ocfg, ow, x, cond, 0.6, 0.0, mu), what="locdit full width L=1")
+    m.free()
+
+
+def test_locdit_full_size_forward(vxm_ctx, orc):
+    """The CFM velocity workload: hidden 1024, 12 layers, 16 x 64 heads, FFN 4096;
+    4 latent tokens + 17 cond tokens + mu(2) + t(1) = 24 rows per branch.  Every
+    block meets the block bar against the oracle's input to it; the end-to-end
+    velocity meets the gross bar."""
+    import vxm
+
+    keep = {}
+    m, ow, ocfg = _model(vxm_ctx, orc, 51, **FULL, keep=keep)
+    x, cond, mu = make_inputs(52, 4, 17, 64, 1024)
+    v = m.forward(_dev(x), _dev(cond), 0.6, 0.0, _dev(mu)).cpu().numpy()
+    ref, states = orc.locdit_states(ocfg, ow, x, cond, 0.6, 0.0, mu)
+    c = keep["cfg"]
+    blocks = vxm.MiniCPM4(vxm_ctx, dict(hidden_size=c["hidden_size"], n_layers=c["n_layers"],
+                                        n_heads=c["n_heads"], n_kv_heads=c["n_kv_heads"], head_dim=c["head_dim"],
+                                        intermediate_size=c["intermediate_size"], rms_norm_eps=1e-6,
+                                        rope_theta=10000), keep["w"]["layers"])
+    for l in range(c["n_layers"]):
+        h = _dev(states[l])
+        blocks.block(None, l, h, 0, 1)
+        assert_sensitivity_close(h.cpu().numpy(), states[l + 1], what=f"locdit block {l}")
+    blocks.free()
+    rel = np.linalg.norm(v.astype(np.float64) - ref) / np.linalg.norm(ref)
+    print(f"end-to-end velocity rel_l2 {rel:.3e}")
+    assert np.isfinite(v).all() and rel < 5e-2
+    m.free()
+
+
+def test_cfm_full_width_one_block(vxm_ctx, orc):
+    """Full-width CFG solve (one block) over 3 uniform steps against the oracle."""
+    m, ow, ocfg = _model(vxm_ctx, orc, 61, **dict(FULL, L=1))
+    x0, cond, mu = make_inputs(62, 4, 17, 64, 1024)
+    x = _dev(x0)
+    m.cfm_solve(x, _dev(cond), _dev(mu), 3, 2.0, 1, False)
+    assert_trajectory_close(x.cpu().numpy(), orc.cfm_solve(ocfg, ow, x0, cond, mu, 3, 2.0, 1, 0),
+                            what="cfm full width L=1")
+    m.free()
+
+
+def test_cfm_full_size_one_step_and_repeatable(vxm_ctx, orc):
+    """The 12-block solve: one full Euler step (t 1 -> 0, so x moves by the whole
+    blended velocity, CFG 2 doubling velocity differences) within the gross bar
+    of the deep stack, and ten steps finite and bit-identical across runs."""
+    import torch
+
+    m, ow, ocfg = _model(vxm_ctx, orc, 61, **FULL)
+    x0, cond, mu = make_inputs(62, 4, 17, 64, 1024)
+    cd, md = _dev(cond), _dev(mu)
+    x = _dev(x0)
+    m.cfm_solve(x, cd, md, 1, 2.0, 1, True)
+    ref = orc.cfm_solve(ocfg, ow, x0, cond, mu, 1, 2.0, 1, 1)
+    rel = np.linalg.norm(x.cpu().numpy().astype(np.float64) - ref) / np.linalg.norm(ref)
+    print(f"cfm 12 blocks, 1 step: rel_l2 {rel:.3e}")
+    assert rel < 1e-1
+    # ten uniform steps twice: finite and bit-identical
+    outs = []
+    for _ in range(2):
+        x = _dev(x0)
+        m.cfm_solve(x, cd, md, 10, 2.0, 1, True)
+        torch.cuda.synchronize()
+        outs.append(x.cpu().numpy())
+    assert np.isfinite(outs[0]).all() and np.array_equal(outs[0], outs[1])
+    assert not np.array_equal(outs[0], x0)
+    m.free()
+
+
+def test_locdit_rejects_bad_sizes(vxm_ctx, orc):
+    import vxm
+
+    m, _, _ = _model(vxm_ctx, orc, 71, **SMALL)
+    x = _dev(np.zeros((65, 64), np.float32))
+    with pytest.raises(vxm.VxmError) as e:
+        m.forward(x, None, 0.5)          # P * feat = 4160 > 2048
+    assert e.value.code == 1
+    with pytest.raises(vxm.VxmError):
+        m.cfm_solve(_dev(np.zeros((2, 64), np.float32)), None, None, 4, 2.0, 7, True)
+    m.free()

@@ -305,8 +305,8 @@ struct vxm_pparams {
     const int8_t *dummy_q;     // 2 KiB of zeros: loads of units a wave does not own
     const uint16_t *dummy_d;   // 64 zero scales
     int *err;
-    const float *ff;
-    float theta_scale, eps, res_scale;
+    const float2 *rope_cs;   // (cos, sin) table [position][HD/2]
+    float eps, res_scale;
     int pos, cap, no_rope;
     uint32_t epoch;
 #ifdef VXM_PERSISTENT_TRACE
@@ -805,13 +805,13 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
     for (int h = 0; h < NH; h++)
         if (attn_wg<S>(h) == wg) head = h;
 
-    // rope cos/sin of this token's position (ggml_rope_ext NEOX, iterative theta)
-    for (int i = tid_now(); i < HD / 2; i += kThreads) {
-        float theta = (float)pos;
-        for (int k = 0; k < i; k++) theta = theta * p.theta_scale;
-        const float th = p.ff ? __fdiv_rn(theta, p.ff[i]) : theta;
-        cs[2 * i] = cosf(th);
-        cs[2 * i + 1] = sinf(th);
+    // rope cos/sin of this token's position (ggml_rope_ext NEOX angles, host table)
+    if (!p.no_rope) {
+        for (int i = tid_now(); i < HD / 2; i += kThreads) {
+            const float2 r = p.rope_cs[(int64_t)pos * (HD / 2) + i];
+            cs[2 * i] = r.x;
+            cs[2 * i + 1] = r.y;
+        }
     }
 
     // this wave's ring slots in LDS (compute waves only)
@@ -1125,8 +1125,7 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
     prm.dummy_q = s.dummy_q;
     prm.dummy_d = s.dummy_d;
     prm.err = s.err;
-    prm.ff = d.ff;
-    prm.theta_scale = d.theta_scale;
+    prm.rope_cs = d.rope_cs;
     prm.eps = d.eps;
     prm.res_scale = d.res_scale;
     prm.pos = pos;

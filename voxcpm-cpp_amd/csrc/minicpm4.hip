@@ -155,13 +155,42 @@ void vxm_block_free(vxm_ctx *ctx, vxm_block &b) {
     b = vxm_block();
 }
 
-int vxm_rope_setup(vxm_ctx *ctx, int hd, int32_t theta, const float *ff_host, float **ff_dev, float *theta_scale) {
-    // ggml_rope_ext: theta_scale = powf(freq_base, -2.0f / n_dims), on the host
-    *theta_scale = powf((float)theta, -2.0f / (float)hd);
-    const float *src = ff_host ? ff_host : (hd == 128 ? kVoxcpm2RopeShortFactors : nullptr);
-    *ff_dev = nullptr;
-    if (!src) return VXM_OK;
-    return upload_f32(ctx, src, hd / 2, ff_dev);
+void vxm_rope_setup(vxm_block_dims &d, int32_t theta, const float *ff_host) {
+    d.rope_base = (float)theta;
+    const float *src = ff_host ? ff_host : (d.hd == 128 ? kVoxcpm2RopeShortFactors : nullptr);
+    d.ff_host.clear();
+    if (src) d.ff_host.assign(src, src + d.hd / 2);
+}
+
+// Rope table rows [0, n_pos): grown to at least twice its size (or 1024 rows)
+// when a call needs a position beyond it.  Growing synchronises the stream
+// once; steady-state calls only read the table.
+int vxm_rope_ensure(vxm_ctx *ctx, vxm_block_dims &d, int64_t n_pos) {
+    if (n_pos <= d.rope_rows) return VXM_OK;
+    if (n_pos > (1 << 24)) return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "rope: position %lld", (long long)n_pos);
+    const int64_t rows = std::max<int64_t>(std::max<int64_t>(n_pos, 2 * (int64_t)d.rope_rows), 1024);
+    const int64_t half = d.hd / 2;
+    std::vector<float> host((size_t)(rows * half * 2));
+    int rc = vxm_host_rope_cache(d.rope_base, d.hd, d.ff_host.empty() ? nullptr : d.ff_host.data(), 0,
+                                 (int32_t)rows, host.data());
+    if (rc) return vxm_fail(ctx, rc, "rope: table of %lld rows", (long long)rows);
+    float2 *t = nullptr;
+    if (hipMalloc((void **)&t, host.size() * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        return vxm_fail(ctx, VXM_ERR_OOM, "rope: table of %lld rows", (long long)rows);
+    }
+    VXM_HIP(ctx, hipMemcpyAsync(t, host.data(), host.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (d.rope_cs) VXM_HIP(ctx, hipFree(d.rope_cs));
+    d.rope_cs = t;
+    d.rope_rows = (int)rows;
+    return VXM_OK;
+}
+
+void vxm_rope_free(vxm_block_dims &d) {
+    if (d.rope_cs) (void)hipFree(d.rope_cs);
+    d.rope_cs = nullptr;
+    d.rope_rows = 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -175,7 +204,7 @@ int vxm_block_run(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_block &b, vxm
     const int var = ctx->quant_variant;
     int rc;
     if ((rc = vxm_launch_mul_mat(ctx, b.wqkv, ws.xq, ws.xd, M, ws.qkv))) return rc;
-    if ((rc = vxm_launch_rope_kv(ctx, ws.qkv, M, d.nh, d.nkv, d.hd, site.pos0, site.S, d.theta_scale, d.ff,
+    if ((rc = vxm_launch_rope_kv(ctx, ws.qkv, M, d.nh, d.nkv, d.hd, site.pos0, site.S, d.rope_cs, d.rope_rows,
                                  d.no_rope, ws.q, site.kc, site.vc, site.cap, site.seg_stride, site.cache_pos0)))
         return rc;
     if ((rc = vxm_launch_attention(ctx, ws.q, site.kc, site.vc, ws.att, M, d.nh, d.nkv, d.hd, site.cap,
@@ -285,7 +314,8 @@ extern "C" int vxm_minicpm4_create(vxm_ctx *ctx, const vxm_minicpm4_config *cfg,
     d.eps = c.rms_norm_eps;
     d.no_rope = c.no_rope;
     d.res_scale = (c.scale_depth > 0.0f) ? c.scale_depth / sqrtf((float)c.n_layers) : 1.0f;
-    int rc = vxm_rope_setup(ctx, d.hd, c.rope_theta, c.rope_freq_factors, &d.ff, &d.theta_scale);
+    vxm_rope_setup(d, c.rope_theta, c.rope_freq_factors);
+    int rc = VXM_OK;
     m->blocks.resize(c.n_layers);
     for (int l = 0; l < c.n_layers && rc == VXM_OK; l++) rc = vxm_block_upload(ctx, d, layers[l], m->blocks[l]);
     if (rc == VXM_OK) rc = upload_f32(ctx, final_norm, d.H, &m->final_norm);
@@ -303,7 +333,7 @@ extern "C" int vxm_minicpm4_free(vxm_minicpm4 *m) {
     for (auto &b : m->blocks) vxm_block_free(m->ctx, b);
     vxm_persistent_free(m);
     if (m->final_norm) (void)hipFree(m->final_norm);
-    if (m->dims.ff) (void)hipFree(m->dims.ff);
+    vxm_rope_free(m->dims);
     vxm_ws_free(m->ws);
     delete m;
     return VXM_OK;
@@ -333,7 +363,7 @@ static int check_run(vxm_minicpm4 *m, vxm_kv_cache *kv, const float *x, int64_t 
             return vxm_fail(m->ctx, VXM_ERR_INVALID_ARG, "minicpm4: pos %d + %lld tokens exceeds capacity %d", pos,
                             (long long)M, kv->cap);
     }
-    return VXM_OK;
+    return m->dims.no_rope ? VXM_OK : vxm_rope_ensure(m->ctx, m->dims, (int64_t)pos + M);
 }
 
 extern "C" int vxm_minicpm4_block(vxm_minicpm4 *m, vxm_kv_cache *kv, int32_t layer, float *x_dev, int64_t n_tokens,

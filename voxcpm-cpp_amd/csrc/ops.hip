@@ -143,14 +143,15 @@ int vxm_launch_rmsnorm(vxm_ctx *ctx, float *h, const float *delta, float res_sca
 
 // ---------------------------------------------------------------------------
 // Q/K/V post-processing of vcpm_attention (src/minicpm4.c:270-320): BF16 of
-// the projections, NEOX RoPE (ggml_rope_ext: theta_0 = pos, theta_{i+1} =
-// theta_i * theta_scale, pair (i, i+hd/2) rotated by theta_i / ff_i; BF16),
-// K and V appended to the f16 cache.  qkv: raw projections [M][qd + 2*kvd].
+// the projections, NEOX RoPE (pair (i, i+hd/2) rotated by the angle of
+// ggml_rope_ext, theta_i / ff_i with theta_0 = pos, theta_{i+1} = theta_i *
+// theta_scale; BF16), K and V appended to the f16 cache.  cs holds the
+// host-computed (cos, sin) of every (position, pair): [position][hd/2].  qkv: raw projections [M][qd + 2*kvd].
 // Tokens come in segments of S (one per CFG branch); token t has position
 // pos0 + t % S and segment t / S, whose cache starts at seg * seg_stride.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_rope_kv(const float *__restrict__ qkv, int nh, int nkv, int hd,
-                                                 int pos0, int S, float theta_scale, const float *__restrict__ ff,
+                                                 int pos0, int S, const float2 *__restrict__ cs,
                                                  int no_rope, float *__restrict__ q_out, uint16_t *__restrict__ kc,
                                                  uint16_t *__restrict__ vc, int cap, int64_t seg_stride,
                                                  int cache_pos0) {
@@ -171,10 +172,8 @@ __global__ __launch_bounds__(256) void k_rope_kv(const float *__restrict__ qkv, 
         float x0 = vxm_bf16(src[2 * i]), x1 = vxm_bf16(src[2 * i + 1]);
         float y0 = x0, y1 = x1;
         if (!no_rope) {
-            float theta = (float)pos;
-            for (int k = 0; k < i; k++) theta = theta * theta_scale;
-            const float th = ff ? __fdiv_rn(theta, ff[i]) : theta;
-            const float c = cosf(th), s = sinf(th);
+            const float2 r = cs[(int64_t)pos * half + i];
+            const float c = r.x, s = r.y;
             y0 = vxm_bf16(x0 * c - x1 * s);
             y1 = vxm_bf16(x0 * s + x1 * c);
         }
@@ -198,11 +197,14 @@ __global__ __launch_bounds__(256) void k_rope_kv(const float *__restrict__ qkv, 
 }
 
 int vxm_launch_rope_kv(vxm_ctx *ctx, const float *qkv, int64_t M, int nh, int nkv, int hd, int pos0, int S,
-                       float theta_scale, const float *ff, int no_rope, float *q_out, uint16_t *kc,
+                       const float2 *cs, int cs_rows, int no_rope, float *q_out, uint16_t *kc,
                        uint16_t *vc, int cap, int64_t seg_stride, int cache_pos0) {
     if (M <= 0) return VXM_OK;
+    if (!no_rope && (!cs || pos0 + std::min<int64_t>(M, S) > cs_rows))
+        return vxm_fail(ctx, VXM_ERR_BACKEND, "rope: table holds %d positions, %lld needed", cs_rows,
+                        (long long)(pos0 + std::min<int64_t>(M, S)));
     hipLaunchKernelGGL(k_rope_kv, dim3((unsigned)M), dim3(256), 0, ctx->stream, qkv, nh, nkv, hd, pos0, S,
-                       theta_scale, ff, no_rope, q_out, kc, vc, cap, seg_stride, cache_pos0);
+                       cs, no_rope, q_out, kc, vc, cap, seg_stride, cache_pos0);
     VXM_CHECK_LAUNCH(ctx);
     return VXM_OK;
 }

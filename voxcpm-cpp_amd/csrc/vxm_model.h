@@ -12,8 +12,13 @@ struct vxm_block_dims {
     float eps = 1e-6f;
     int no_rope = 0;
     float res_scale = 1.0f;
-    float theta_scale = 1.0f;   // powf(rope_theta, -2/head_dim), host-computed
-    float *ff = nullptr;        // device rope frequency factors [hd/2] or null
+    // NEOX rope: the (cos, sin) of every (position, pair) is computed on the
+    // host with the C library (as ggml-cpu's rope cache is) and read from a
+    // device table [rope_rows][hd/2], grown on demand.
+    float rope_base = 10000.0f;
+    std::vector<float> ff_host;   // frequency factors [hd/2], empty = none
+    float2 *rope_cs = nullptr;
+    int rope_rows = 0;
 };
 
 struct vxm_block {
@@ -77,6 +82,8 @@ int vxm_ws_ensure(vxm_ctx *ctx, vxm_workspace &ws, int64_t M, int64_t H, int64_t
 void vxm_ws_free(vxm_workspace &ws);
 int vxm_block_upload(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_layer_weights_q8_0 &w, vxm_block &b);
 void vxm_block_free(vxm_ctx *ctx, vxm_block &b);
-int vxm_rope_setup(vxm_ctx *ctx, int hd, int32_t theta, const float *ff_host, float **ff_dev, float *theta_scale);
+void vxm_rope_setup(vxm_block_dims &d, int32_t theta, const float *ff_host);
+int vxm_rope_ensure(vxm_ctx *ctx, vxm_block_dims &d, int64_t n_pos);
+void vxm_rope_free(vxm_block_dims &d);
 int vxm_block_run(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_block &b, vxm_workspace &ws, float *x,
                   int64_t M, const vxm_attn_site &site);

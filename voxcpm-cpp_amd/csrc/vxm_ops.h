@@ -5,7 +5,7 @@
 int vxm_launch_rmsnorm(vxm_ctx *ctx, float *h, const float *delta, float res_scale, const float *gain,
                        int64_t rows, int64_t n, float eps, float *y, int8_t *xq, uint16_t *xd, int variant);
 int vxm_launch_rope_kv(vxm_ctx *ctx, const float *qkv, int64_t M, int nh, int nkv, int hd, int pos0, int S,
-                       float theta_scale, const float *ff, int no_rope, float *q_out, uint16_t *kc,
+                       const float2 *cs, int cs_rows, int no_rope, float *q_out, uint16_t *kc,
                        uint16_t *vc, int cap, int64_t seg_stride, int cache_pos0);
 int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
                          int64_t M, int nh, int nkv, int hd, int cap, int64_t seg_stride, int S, int kv_base,

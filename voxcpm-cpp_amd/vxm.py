@@ -87,7 +87,18 @@ _SIGS = {
     "vxm_minicpm4_check": (_I, [_P]),
     "vxm_host_quantize_q8_0": (_I, [_P, _I64, _I64, _P]),
     "vxm_host_randn": (_I, [_U64, _U64, _I64, _F, _F, _P]),
+    "vxm_locdit_create": (_I, [_P, _P, _P, C.POINTER(_P)]),
+    "vxm_locdit_free": (_I, [_P]),
+    "vxm_locdit_forward": (_I, [_P, _P, _P, C.c_int32, C.c_int32, _F, _F, _P, _P]),
+    "vxm_cfm_solve": (_I, [_P, _P, _P, C.c_int32, C.c_int32, _P, C.c_int32, _F, C.c_int32, C.c_int32]),
+    "vxm_host_sinusoid_embed": (_I, [_F, C.c_int32, _P]),
+    "vxm_host_cfm_t": (_F, [C.c_int32, C.c_int32, C.c_int32]),
+    "vxm_host_cfm_zero_star_steps": (C.c_int32, [C.c_int32]),
+    "vxm_host_rope_cache": (_I, [_F, C.c_int32, _P, C.c_int32, C.c_int32, _P]),
 }
+
+CFM_SWAY = 0
+CFM_UNIFORM = 1
 
 
 def header_functions(path=HEADER):
@@ -362,6 +373,94 @@ class MiniCPM4:
             self.h = None
 
 
+class LocDiTConfig(C.Structure):
+    """Mirror of vxm_locdit_config (vcpm_locdit_config, src/locdit.h:26-34)."""
+
+    _fields_ = [
+        ("hidden_size", C.c_int32), ("n_layers", C.c_int32), ("n_heads", C.c_int32),
+        ("n_kv_heads", C.c_int32), ("intermediate_size", C.c_int32), ("head_dim", C.c_int32),
+        ("feat_dim", C.c_int32), ("cond_dim", C.c_int32), ("rms_norm_eps", C.c_float),
+        ("rope_theta", C.c_int32), ("rope_freq_factors", C.c_void_p),
+    ]
+
+
+LOCDIT_TENSORS = ("in_proj", "in_bias", "cond_proj", "cond_bias", "out_proj", "out_bias", "norm",
+                  "t_w1", "t_w2", "dt_w1", "dt_w2", "t_b1", "t_b2", "dt_b1", "dt_b2")
+
+
+class LocDiTWeightsQ8(C.Structure):
+    """Mirror of vxm_locdit_weights_q8_0 (vcpm_locdit_weights, src/locdit.h:41-68)."""
+
+    _fields_ = [("layers", C.c_void_p)] + [(n, C.c_void_p) for n in LOCDIT_TENSORS]
+
+
+class LocDiT:
+    """vcpm_locdit on the device, plus the CFM solver that drives it.
+
+    ``weights``: dict with GGUF Q8_0 rows for in_proj [hidden][feat], cond_proj
+    [hidden][cond], out_proj [feat][hidden], t_w1/t_w2/dt_w1/dt_w2 [hidden][hidden],
+    F32 biases / norm (biases may be None) and ``layers`` (MiniCPM4 block dicts)."""
+
+    def __init__(self, ctx, cfg: dict, weights: dict):
+        import numpy as np
+
+        self.ctx = ctx
+        keep = []
+        ff = cfg.get("rope_freq_factors")
+        if ff is not None:
+            ff = np.ascontiguousarray(ff, dtype=np.float32)
+            keep.append(ff)
+        c = LocDiTConfig(cfg["hidden_size"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"],
+                         cfg["intermediate_size"], cfg["head_dim"], cfg["feat_dim"], cfg.get("cond_dim", cfg["feat_dim"]),
+                         cfg.get("rms_norm_eps", 1e-6), int(cfg.get("rope_theta", 10000)),
+                         None if ff is None else ff.ctypes.data)
+        self.cfg = cfg
+        layers = weights.get("layers", [])
+        arr = (LayerWeightsQ8 * max(1, len(layers)))()
+        names = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj",
+                 "input_layernorm", "post_attention_layernorm")
+        for i, lw in enumerate(layers):
+            for n in names:
+                a = np.ascontiguousarray(lw[n])
+                keep.append(a)
+                setattr(arr[i], n, a.ctypes.data)
+        w = LocDiTWeightsQ8()
+        w.layers = C.cast(arr, C.c_void_p).value
+        for n in LOCDIT_TENSORS:
+            v = weights.get(n)
+            if v is not None:
+                a = np.ascontiguousarray(v)
+                keep.append(a)
+                setattr(w, n, a.ctypes.data)
+        h = C.c_void_p()
+        ctx.check(lib().vxm_locdit_create(ctx.h, C.byref(c), C.byref(w), C.byref(h)))
+        self.h = h
+
+    def forward(self, x, cond, t, dt=0.0, mu=None, out=None):
+        """Velocity [P][feat] of x [P][feat] (device tensors); mu [2][hidden] or None."""
+        import torch
+
+        P = x.shape[0]
+        Pc = 0 if cond is None else cond.shape[0]
+        if out is None:
+            out = torch.empty((P, self.cfg["feat_dim"]), dtype=torch.float32, device=x.device)
+        self.ctx.check(lib().vxm_locdit_forward(self.h, _ptr(x), _ptr(cond), P, Pc, t, dt, _ptr(mu), _ptr(out)))
+        return out
+
+    def cfm_solve(self, x, cond, mu, n_steps, cfg_value=2.0, schedule=CFM_SWAY, use_zero_star=True):
+        """The Euler loop, in place on x [P][feat] (device tensor)."""
+        P = x.shape[0]
+        Pc = 0 if cond is None else cond.shape[0]
+        self.ctx.check(lib().vxm_cfm_solve(self.h, _ptr(x), _ptr(cond), P, Pc, _ptr(mu), n_steps, cfg_value,
+                                           schedule, int(use_zero_star)))
+        return x
+
+    def free(self):
+        if self.h:
+            self.ctx.check(lib().vxm_locdit_free(self.h))
+            self.h = None
+
+
 class Q8Weight:
     def __init__(self, ctx, h, n, k):
         self.ctx, self.h, self.n, self.k = ctx, h, n, k
@@ -401,4 +500,34 @@ def host_quantize_q8_0(x):
     rc = lib().vxm_host_quantize_q8_0(_ptr(x), rows, k, _ptr(out))
     if rc:
         raise VxmError(rc, "vxm_host_quantize_q8_0")
+    return out
+
+
+def host_sinusoid_embed(t, dim):
+    import numpy as np
+
+    out = np.empty(dim, dtype=np.float32)
+    rc = lib().vxm_host_sinusoid_embed(t, dim, _ptr(out))
+    if rc:
+        raise VxmError(rc, "vxm_host_sinusoid_embed")
+    return out
+
+
+def host_cfm_t(step, n_steps, schedule=CFM_SWAY):
+    return lib().vxm_host_cfm_t(step, n_steps, schedule)
+
+
+def host_cfm_zero_star_steps(n_steps):
+    return lib().vxm_host_cfm_zero_star_steps(n_steps)
+
+
+def host_rope_cache(base, head_dim, ff, pos0, n_pos):
+    """(cos, sin) rope table [n_pos][head_dim/2][2] of ggml_rope_ext's NEOX angles."""
+    import numpy as np
+
+    out = np.empty((n_pos, head_dim // 2, 2), dtype=np.float32)
+    ffa = None if ff is None else np.ascontiguousarray(ff, dtype=np.float32)
+    rc = lib().vxm_host_rope_cache(base, head_dim, _ptr(ffa), pos0, n_pos, _ptr(out))
+    if rc:
+        raise VxmError(rc, "vxm_host_rope_cache")
     return out
