@@ -26,6 +26,21 @@ INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA
 H, NH, NKV, HD, F, L = 2048, 16, 2, 128, 6144, 28
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_persistent_28L_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 PMC summary (FETCH_SIZE and
+    WRITE_SIZE scaled against a copy kernel), or None when the summary is absent."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic bytes per launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(msg):
     print(f"# {msg}", file=sys.stderr, flush=True)
 
@@ -219,6 +234,68 @@ def bench_prefill(ctx, torch, vxm, layers, n_layers, M, reps):
     return ms * 1000.0 / reps, ok
 
 
+DIT = dict(H=1024, L=12, NH=16, HD=64, F=4096, FEAT=64, P=4, PC=17)
+
+
+def make_locdit(vxm, seed):
+    """Seeded synthetic LocDiT (hidden 1024, 12 blocks, 16 x 64 MHA, FFN 4096), Q8_0 N(0, 0.02)."""
+    H, F, FEAT, NHD = DIT["H"], DIT["F"], DIT["FEAT"], DIT["NH"] * DIT["HD"]
+    off = [0]
+
+    def q8(n, k):
+        w = vxm.host_randn(seed, n * k, 0.0, 0.02, offset=off[0]).reshape(n, k)
+        off[0] += n * k
+        return vxm.host_quantize_q8_0(w)
+
+    def vec(n, mean=0.0, std=0.02):
+        v = vxm.host_randn(seed, n, mean, std, offset=off[0])
+        off[0] += n
+        return v
+
+    layers = [dict(q_proj=q8(NHD, H), k_proj=q8(NHD, H), v_proj=q8(NHD, H), o_proj=q8(H, NHD),
+                   gate_proj=q8(F, H), up_proj=q8(F, H), down_proj=q8(H, F), input_layernorm=vec(H, 1.0),
+                   post_attention_layernorm=vec(H, 1.0)) for _ in range(DIT["L"])]
+    w = dict(layers=layers, in_proj=q8(H, FEAT), in_bias=vec(H), cond_proj=q8(H, FEAT), cond_bias=vec(H),
+             out_proj=q8(FEAT, H), out_bias=vec(FEAT), norm=vec(H, 1.0), t_w1=q8(H, H), t_w2=q8(H, H),
+             dt_w1=q8(H, H), dt_w2=q8(H, H), t_b1=vec(H), t_b2=vec(H), dt_b1=vec(H), dt_b2=vec(H))
+    cfg = dict(hidden_size=H, n_layers=DIT["L"], n_heads=DIT["NH"], n_kv_heads=DIT["NH"], head_dim=DIT["HD"],
+               intermediate_size=F, feat_dim=FEAT, cond_dim=FEAT, rms_norm_eps=1e-6, rope_theta=10000)
+    return cfg, w
+
+
+def locdit_eval_bytes():
+    """Q8_0 bytes of one LocDiT evaluation: 12 blocks + in/out/cond projections."""
+    H, F, FEAT, NHD = DIT["H"], DIT["F"], DIT["FEAT"], DIT["NH"] * DIT["HD"]
+    blk = q8_bytes(3 * NHD, H) + q8_bytes(H, NHD) + 2 * q8_bytes(F, H) + q8_bytes(H, F)
+    return DIT["L"] * blk + 2 * q8_bytes(H, FEAT) + q8_bytes(FEAT, H)
+
+
+def bench_cfm(ctx, torch, vxm, reps, n_steps=10):
+    """CFM solves: n_steps uniform Euler steps, CFG 2.0 with CFG-Zero* (both branches in one
+    batch of 2 x 24 rows per LocDiT evaluation), latent 4 x 64, 17 cond tokens."""
+    cfg, w = make_locdit(vxm, 21)
+    m = vxm.LocDiT(ctx, cfg, w)
+    P, PC, H, FEAT = DIT["P"], DIT["PC"], DIT["H"], DIT["FEAT"]
+    x0 = torch.from_numpy(vxm.host_randn(22, P * FEAT).reshape(P, FEAT)).to("cuda:0")
+    cond = torch.from_numpy(vxm.host_randn(23, PC * FEAT).reshape(PC, FEAT)).to("cuda:0")
+    mu = torch.from_numpy(vxm.host_randn(24, 2 * H).reshape(2, H)).to("cuda:0")
+    x = x0.clone()
+    m.cfm_solve(x, cond, mu, n_steps, 2.0, vxm.CFM_UNIFORM, True)
+    ctx.sync()
+    t = Timer(torch, ctx)
+    ms = 0.0
+    for _ in range(reps):
+        x.copy_(x0)
+        torch.cuda.synchronize()
+        t.start()
+        m.cfm_solve(x, cond, mu, n_steps, 2.0, vxm.CFM_UNIFORM, True)
+        ms += t.stop_ms()
+    ok = bool(torch.isfinite(x).all().item())
+    m.free()
+    evals = n_steps - vxm.host_cfm_zero_star_steps(n_steps)
+    return ms * 1000.0 / reps, evals, ok
+
+
 def cpu_baseline(vxm, layers, n_layers, ctx0, tokens, threads):
     """The oracle's SIMD restatement of ggml's CPU Q8_0 decode (1 copy of weights)."""
     import ctypes as C
@@ -273,6 +350,9 @@ def main():
     ap.add_argument("--prefill-only", action="store_true",
                     help="time only the prefill legs (MFMA GEMMs and the 512-token 28-layer prefill)")
     ap.add_argument("--prefill-tokens", type=int, default=512)
+    ap.add_argument("--cfm-only", action="store_true", help="time only the CFM solve leg")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run 3 device copies of 256 MiB (a known-traffic kernel for HBM counter scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -282,9 +362,33 @@ def main():
     import vxm
 
     mode = {"auto": 0, "kernels": 1, "persistent": 2}[args.mode]
+    if args.copy_calibration:
+        a = torch.empty(64 << 20, dtype=torch.float32, device="cuda:0").fill_(1.0)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x 256 MiB device copies (read 256 MiB + write 256 MiB each)")
+        del a, b
     ctx = vxm.Context(0)
     res = {}
     pre = None
+    cfm = None
+    if not args.decode_only and not args.prefill_only:
+        us_cfm, evals, fin = bench_cfm(ctx, torch, vxm, 5)
+        eb = locdit_eval_bytes()
+        ops = 2 * 2 * (3 + DIT["PC"] + DIT["P"]) * (eb * 32 // 34)
+        cfm = {"us_per_solve": round(us_cfm, 1), "evals": evals, "us_per_eval": round(us_cfm / evals, 1),
+               "weight_GBs": round(evals * eb / (us_cfm * 1e-6) / 1e9, 1),
+               "int8_TOPs": round(evals * ops / (us_cfm * 1e-6) / 1e12, 2), "finite": fin,
+               "note": "10 uniform steps, CFG 2.0 + CFG-Zero* (first step skipped), both branches batched "
+                       "(M = 2 x 24); weights 214 MB per evaluation, Infinity-Cache resident"}
+        log(f"cfm solve: {us_cfm:.1f} us for {evals} evaluations ({us_cfm / evals:.1f} us each), "
+            f"{cfm['weight_GBs']} GB/s of weights, finite={fin}")
+        if args.cfm_only:
+            print(json.dumps({"cfm": cfm}))
+            ctx.close()
+            return
     if not args.decode_only:
         M = args.prefill_tokens
         gemms = {}
@@ -360,7 +464,8 @@ def main():
     kname = ("k_decode_persistent<Shape<2048,16,2,128,6144>>" if args.mode != "kernels"
              else "per-op kernel sequence (no single dominant launch)")
     roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kname,
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic() if args.mode != "kernels" else None, "kernel": kname,
             "bytes_per_launch": int(sb), "us_per_launch": round(us_step, 2)}
 
     out = {
@@ -385,6 +490,7 @@ def main():
         "gemv": res,
         "layer_decode_ctx512_us": round(us1, 3) if us1 is not None else None,
         "prefill": pre,
+        "cfm": cfm,
         "roofline": roof,
         "cpu_baseline": cpu,
     }
