@@ -212,89 +212,162 @@ __global__ void k_block_dots(const int8_t *__restrict__ qs, const int8_t *__rest
 // sub-tile.  Lane l supplies A row l % 32 and B row (weight row) l % 32, k
 // half l / 32; result register v of lane l is row 8(v/4) + 4(l/32) + v%4,
 // column l % 32.  Each lane then adds term = (float)sumi * (d_w * d_x) to its
-// fp32 accumulators block after block: ggml's generic vec_dot_q8_0_q8_0
-// order, so without a K split the output is bit-exact with a sequential
-// per-block fp32 sum.  (Per block and element that is four VALU operations
-// against 1/1024 of an MFMA, which bounds the MFMA duty cycle.)
+// fp32 accumulators (one fused multiply-add per element and block).  That
+// scale-and-add is the bound: per (element, block) it takes 3 VALU
+// operations (convert, d_w * d_x, fma) against 1/1024 of a 32-cycle MFMA, so
+// the VALU caps the int8 MFMA near 1/6 of its peak under exact per-block
+// Q8_0 semantics.  The kernel is built so that the VALU is the only limit:
+// * a wave owns a 32 (M) x 64 (N) strip -- two MFMAs per block share the A
+//   operand and the 16 activation scales a lane needs, which halves the LDS
+//   bytes per element (the scales would otherwise load the LDS as much as
+//   the epilogue loads the VALU);
+// * the MFMAs of block j+1 are issued before the epilogue of block j, so the
+//   matrix core runs under the VALU work of the same wave;
+// * blocks past the end of K are zero-filled in LDS and add exact zeros, so
+//   the inner loop has no per-block branch.
 //
-// Workgroup: 256 threads (4 waves) on a 64 (M) x 64 (N) tile, wave w on the
-// 32 x 32 sub-tile (w / 2, w % 2).  K moves through LDS GKS blocks at a time,
+// Workgroup: 512 threads (8 waves) on a 64 (M) x 64 (N) tile: wave w owns
+// rows 32 (w % 2) .. +31 and K quarter w / 2 (blocks [q KS/4, (q+1) KS/4) of
+// every KS-block LDS stage); the four quarters are added through LDS in
+// quarter order at the end.  K moves through LDS KS blocks per stage,
 // double-buffered through registers.  Tiles are ordered so that the M tiles
 // sharing one weight tile run on one XCD (workgroups are dispatched round
 // robin over the 8 XCDs): the weight tile is fetched into that XCD's L2 once.
-// blockIdx.y = K split: split z adds blocks [z*bps, (z+1)*bps) and writes its
-// partial tile to part[z] (the caller reduces), or y directly when splits = 1.
+//
+// blockIdx.y = K split z (blocks [z*bps, (z+1)*bps)).  With splits > 1 each
+// workgroup publishes its partial tile in part[z] as 64-bit words (launch
+// epoch << 32 | fp32 bits, relaxed agent-scope stores: no fence, no L2
+// writeback), then counts itself in cnt[tile].  The last workgroup of a tile
+// to arrive resets the counter, reads every partial word until its tag shows
+// this launch's epoch (a bounded wait: the words are already on their way),
+// adds them in split order and writes y -- the result does not depend on the
+// arrival order.  DOTS = true writes the int32 block sums to
+// dots[(m*N + n)*nb + b] instead (debug; no scaling, no split).
 // ---------------------------------------------------------------------------
 typedef int v16i __attribute__((ext_vector_type(16)));
-constexpr int GM = 64, GN = 64, GKS = 4;     // tile M, N; blocks per LDS stage
-constexpr int GROW = GKS * 32 + 16;          // padded LDS row (bytes) against bank conflicts
+constexpr int GM = 64, GN = 64;              // output tile
+constexpr int kGemmThreads = 512;
+constexpr int kGemmSpin = 1 << 20;           // bound of the wait for one partial word
+constexpr int kGemmMaxSplits = 4;
 
-__global__ __launch_bounds__(256) void k_gemm_q8_0_mfma(const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd,
-                                                        const int8_t *__restrict__ wq, const uint16_t *__restrict__ wd,
-                                                        float *__restrict__ y, int M, int N, int K, int tiles_m,
-                                                        int tiles_n, int bps) {
-    __shared__ __align__(16) int8_t As[2][GM * GROW];
-    __shared__ __align__(16) int8_t Bs[2][GN * GROW];
-    __shared__ __align__(16) float Ad[2][GKS][GM];
-    __shared__ __align__(16) float Bd[2][GKS][GN];
+// KS = Q8_0 blocks per LDS stage (8 or 16).  LDS: 2 stages x (A + B) x 64 rows
+// x (32 KS + 16) bytes + the scales; the K-quarter reduction reuses it.
+template <int KS>
+struct GemmLds {
+    static constexpr int ROW = KS * 32 + 16;   // padded row (bytes) against bank conflicts
+    int8_t a[2][GM * ROW];
+    int8_t b[2][GN * ROW];
+    float ad[2][KS][GM];
+    float bd[2][KS][GN];
+};
+
+template <int KS, bool DOTS>
+#ifndef VXM_GEMM_PIPE
+#define VXM_GEMM_PIPE 1
+#endif
+#ifndef VXM_GEMM_WAVES_PER_SIMD
+#define VXM_GEMM_WAVES_PER_SIMD 2
+#endif
+__global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_q8_0_mfma(
+    const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd, const int8_t *__restrict__ wq,
+    const uint16_t *__restrict__ wd, float *__restrict__ y, uint64_t *__restrict__ part, int *__restrict__ cnt,
+    int32_t *__restrict__ dots, int M, int N, int K, int tiles_m, int tiles_n, int bps, int splits,
+    uint32_t epoch) {
+    static_assert(KS % 8 == 0, "a stage is a multiple of 8 blocks (64 KS scales per side = whole 512-thread rounds)");
+    constexpr int ROW = GemmLds<KS>::ROW;
+    constexpr int CH = KS / 4;                 // 16-byte chunks per thread per side and stage
+    constexpr int NQ = KS / 4;                 // blocks per wave per stage
+    __shared__ __align__(16) GemmLds<KS> L;
+    __shared__ int last_sh;
+    static_assert(sizeof(GemmLds<KS>) >= 3 * 2 * 64 * 32 * sizeof(float), "K-quarter reduction buffer");
     const int id = blockIdx.x, xcd = id % 8, k8 = id / 8;
     const int tn = (k8 / tiles_m) * 8 + xcd, tm = k8 % tiles_m;
     if (tn >= tiles_n) return;
     const int m0 = tm * GM, n0 = tn * GN;
     const int nb = K / 32;
-    const int b0 = blockIdx.y * bps, b1 = min(nb, b0 + bps);
-    if (b0 >= b1) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int z = blockIdx.y;
+    const int b0 = z * bps, b1 = min(nb, b0 + bps);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, kq = wave >> 1;
 
-    // stage loader: thread t moves 16-byte chunks c = t, t + 256 of each 64 x 128-byte tile
-    // (row c / 8, chunk c % 8) and one scale (block t / 64, row t % 64) of each side
-    auto load = [&](int kb0, v4i (&ra)[2], v4i (&rb)[2], float &sa, float &sb) {
+    // stage loader: chunk c = tid + 512 h of a side is row c / (2 KS), 16-byte piece
+    // c % (2 KS) (block piece / 2, half piece % 2); scale c of the 2 x KS x 64 is side
+    // c / (64 KS), block (c % (64 KS)) / 64, row c % 64.  All loads are unconditional
+    // buffer loads: rows past M (N) fall outside the buffer's range and read as zeros;
+    // blocks past b1 read real neighbours but get a zero scale at the store, so they
+    // add exact zeros.  Scales stay fp16 bits until the store: converting them here
+    // would make the compiler wait for the whole stage before the current MFMAs.
+    const __amdgpu_buffer_rsrc_t ra_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)xq, (short)0, M * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)wq, (short)0, N * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t sa_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)xd, (short)0, M * nb * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t sb_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)wd, (short)0, N * nb * 2, 0x00020000);
+    auto load = [&](int kb0, v4i (&ra)[CH], v4i (&rb)[CH], uint16_t (&sc)[CH]) {
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int c = tid + 256 * h, r = c >> 3, ch = c & 7, kb = kb0 + (ch >> 1);
-            const bool okk = kb < b1;
-            const int m = m0 + r, n = n0 + r;
-            ra[h] = (okk && m < M) ? *(const v4i *)(xq + (int64_t)m * K + kb * 32 + (ch & 1) * 16) : v4i{0, 0, 0, 0};
-            rb[h] = (okk && n < N) ? *(const v4i *)(wq + (int64_t)n * K + kb * 32 + (ch & 1) * 16) : v4i{0, 0, 0, 0};
+        for (int h = 0; h < CH; h++) {
+            const int c = tid + kGemmThreads * h, r = c / (2 * KS), pc = c % (2 * KS);
+            const int koff = (kb0 + (pc >> 1)) * 32 + (pc & 1) * 16;
+            ra[h] = __builtin_amdgcn_raw_buffer_load_b128(ra_rsrc, (m0 + r) * K + koff, 0, 0);
+            rb[h] = __builtin_amdgcn_raw_buffer_load_b128(rb_rsrc, (n0 + r) * K + koff, 0, 0);
+            // side is uniform: tid < 512 and 64 KS is a multiple of 512
+            constexpr int kSidePer = 64 * KS / kGemmThreads;
+            const bool side_b = h / kSidePer != 0;
+            const int t = c % (64 * KS), sb = kb0 + t / 64, rr = t % 64;
+            if (DOTS) sc[h] = 0;   // block sums only: scales are not read
+            else if (!side_b) sc[h] = __builtin_amdgcn_raw_buffer_load_b16(sa_rsrc, ((m0 + rr) * nb + sb) * 2, 0, 0);
+            else sc[h] = __builtin_amdgcn_raw_buffer_load_b16(sb_rsrc, ((n0 + rr) * nb + sb) * 2, 0, 0);
         }
-        const int kb = kb0 + (tid >> 6), r = tid & 63;
-        sa = (kb < b1 && m0 + r < M) ? vxm_h2f(xd[(int64_t)(m0 + r) * nb + kb]) : 0.0f;
-        sb = (kb < b1 && n0 + r < N) ? vxm_h2f(wd[(int64_t)(n0 + r) * nb + kb]) : 0.0f;
     };
-    auto store = [&](int buf, const v4i (&ra)[2], const v4i (&rb)[2], float sa, float sb) {
+    auto store = [&](int buf, int kb0, const v4i (&ra)[CH], const v4i (&rb)[CH], const uint16_t (&sc)[CH]) {
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int c = tid + 256 * h, r = c >> 3, ch = c & 7;
-            *(v4i *)(As[buf] + r * GROW + ch * 16) = ra[h];
-            *(v4i *)(Bs[buf] + r * GROW + ch * 16) = rb[h];
+        for (int h = 0; h < CH; h++) {
+            const int c = tid + kGemmThreads * h, r = c / (2 * KS), pc = c % (2 * KS);
+            *(v4i *)(L.a[buf] + r * ROW + pc * 16) = ra[h];
+            *(v4i *)(L.b[buf] + r * ROW + pc * 16) = rb[h];
+            constexpr int kSidePer = 64 * KS / kGemmThreads;
+            const int t = c % (64 * KS);
+            const float v = kb0 + t / 64 < b1 ? vxm_h2f(sc[h]) : 0.0f;
+            if (h / kSidePer == 0) L.ad[buf][t / 64][t % 64] = v;
+            else L.bd[buf][t / 64][t % 64] = v;
         }
-        Ad[buf][tid >> 6][tid & 63] = sa;
-        Bd[buf][tid >> 6][tid & 63] = sb;
     };
 
-    float acc[16];
+    float acc[2][16];
 #pragma unroll
-    for (int v = 0; v < 16; v++) acc[v] = 0.0f;
-    v4i ra[2], rb[2];
-    float sa, sb;
-    load(b0, ra, rb, sa, sb);
-    store(0, ra, rb, sa, sb);
+    for (int v = 0; v < 16; v++) acc[0][v] = acc[1][v] = 0.0f;
+    v4i ra[CH], rb[CH];
+    uint16_t sc[CH];
+    load(b0, ra, rb, sc);
+    store(0, b0, ra, rb, sc);
     __syncthreads();
     int buf = 0;
-    for (int kb0 = b0; kb0 < b1; kb0 += GKS) {
-        const bool more = kb0 + GKS < b1;
-        if (more) load(kb0 + GKS, ra, rb, sa, sb);
-        const int8_t *arow = As[buf] + (wm * 32 + (lane & 31)) * GROW + (lane >> 5) * 16;
-        const int8_t *brow = Bs[buf] + (wn * 32 + (lane & 31)) * GROW + (lane >> 5) * 16;
+    const int lr = lane & 31, lh = lane >> 5;
+    for (int kb0 = b0; kb0 < b1; kb0 += KS) {
+        const bool more = kb0 + KS < b1;
+        if (more) load(kb0 + KS, ra, rb, sc);
+        const int8_t *arow = L.a[buf] + (wm * 32 + lr) * ROW + lh * 16 + kq * NQ * 32;
+        const int8_t *brow0 = L.b[buf] + lr * ROW + lh * 16 + kq * NQ * 32;
+        const int8_t *brow1 = brow0 + 32 * ROW;
+        const float *adq = &L.ad[buf][kq * NQ][wm * 32 + 4 * lh];
+        const float *bdq = &L.bd[buf][kq * NQ][lr];
+        // epilogue of block j of this quarter: scale and add (or, DOTS, write the sums)
+        auto epi = [&](const v16i &c0, const v16i &c1, int j) {
+            if (DOTS) {
+                const int kb = kb0 + kq * NQ + j;
 #pragma unroll
-        for (int kb = 0; kb < GKS; kb++) {
-            if (kb0 + kb >= b1) break;
-            const v4i a = *(const v4i *)(arow + kb * 32);
-            const v4i b = *(const v4i *)(brow + kb * 32);
-            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{}, 0, 0, 0);
-            const float dw = Bd[buf][kb][wn * 32 + (lane & 31)];
-            const float *dxr = Ad[buf][kb] + wm * 32 + 4 * (lane >> 5);
+                for (int half = 0; half < 2; half++) {
+                    const int n = n0 + half * 32 + lr;
+                    const v16i &c = half ? c1 : c0;
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        const int m = m0 + wm * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                        if (kb < b1 && m < M && n < N) dots[((int64_t)m * N + n) * nb + kb] = c[v];
+                    }
+                }
+                return;
+            }
+            const float dw0 = bdq[j * GN], dw1 = bdq[j * GN + 32];
+            const float *dxr = adq + j * GM;
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const float4 dx = *(const float4 *)(dxr + 8 * g);
@@ -302,61 +375,204 @@ __global__ __launch_bounds__(256) void k_gemm_q8_0_mfma(const int8_t *__restrict
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int v = 4 * g + e;
-                    acc[v] = acc[v] + (float)c[v] * (dw * dxv[e]);
+                    acc[0][v] = __builtin_fmaf((float)c0[v], dw0 * dxv[e], acc[0][v]);
+                    acc[1][v] = __builtin_fmaf((float)c1[v], dw1 * dxv[e], acc[1][v]);
                 }
+            }
+        };
+        auto mma = [&](int j, v16i &c0, v16i &c1) {
+            const v4i a = *(const v4i *)(arow + j * 32);
+            c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, *(const v4i *)(brow0 + j * 32), v16i{}, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, *(const v4i *)(brow1 + j * 32), v16i{}, 0, 0, 0);
+        };
+        // next block's products first: the matrix core runs under this block's epilogue
+        if (VXM_GEMM_PIPE) {
+            v16i c0, c1;
+            mma(0, c0, c1);
+#pragma unroll(KS == 8 ? NQ : 1)
+            for (int j = 0; j < NQ - 1; j++) {
+                v16i n0v, n1v;
+                mma(j + 1, n0v, n1v);
+                epi(c0, c1, j);
+                c0 = n0v;
+                c1 = n1v;
+            }
+            epi(c0, c1, NQ - 1);
+        } else {
+#pragma unroll(KS == 8 ? NQ : 1)
+            for (int j = 0; j < NQ; j++) {
+                v16i c0, c1;
+                mma(j, c0, c1);
+                epi(c0, c1, j);
             }
         }
         if (more) {
-            store(buf ^ 1, ra, rb, sa, sb);
+            store(buf ^ 1, kb0 + KS, ra, rb, sc);
             buf ^= 1;
         }
         __syncthreads();
     }
-    float *out = y + (int64_t)blockIdx.y * M * N;
-    const int n = n0 + wn * 32 + (lane & 31);
-    if (n < N) {
+    if (DOTS) return;
+    // add the K quarters in order: quarters 1..3 hand their strips to quarter 0
+    float *red = (float *)&L;   // [3 quarters][2 strips][32 values][64 lanes], free after the last barrier
+    if (kq > 0) {
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            const int m = m0 + wm * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-            if (m < M) out[(int64_t)m * N + n] = acc[v];
+            red[(((kq - 1) * 2 + wm) * 32 + v) * 64 + lane] = acc[0][v];
+            red[(((kq - 1) * 2 + wm) * 32 + 16 + v) * 64 + lane] = acc[1][v];
+        }
+    }
+    __syncthreads();
+    if (kq == 0) {
+#pragma unroll
+        for (int q = 0; q < 3; q++) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                acc[0][v] = acc[0][v] + red[((q * 2 + wm) * 32 + v) * 64 + lane];
+                acc[1][v] = acc[1][v] + red[((q * 2 + wm) * 32 + 16 + v) * 64 + lane];
+            }
+        }
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            const int n = n0 + half * 32 + lr;
+            if (n >= N) continue;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int m = m0 + wm * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                if (m >= M) continue;
+                const int64_t i = (int64_t)m * N + n;
+                if (splits == 1) {
+                    y[i] = acc[half][v];
+                } else {
+                    const uint64_t word = ((uint64_t)epoch << 32) | __float_as_uint(acc[half][v]);
+                    __hip_atomic_store(part + (int64_t)z * M * N + i, word, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+    }
+    if (splits == 1) return;
+    // split fix-up: count arrivals; the last one reduces the tagged partials in split order
+    __syncthreads();
+    const int tile = tm * tiles_n + tn;
+    if (tid == 0) {
+        const int prev = __hip_atomic_fetch_add(cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_sh = prev == splits - 1;
+        if (last_sh) __hip_atomic_store(cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last_sh) return;
+    // thread t reduces elements t + 512 j, j < 8, four at a time: all 4 x splits words
+    // are requested before any tag is checked
+    constexpr int EPT = GM * GN / kGemmThreads, EPP = 4;
+    const int64_t MN = (int64_t)M * N;
+#pragma unroll
+    for (int j0 = 0; j0 < EPT; j0 += EPP) {
+        uint64_t w[EPP][kGemmMaxSplits];
+#pragma unroll
+        for (int j = 0; j < EPP; j++) {
+            const int e = tid + kGemmThreads * (j0 + j), m = m0 + e / GN, nn = n0 + e % GN;
+            const bool live = m < M && nn < N;
+            const int64_t i = live ? (int64_t)m * N + nn : 0;
+#pragma unroll
+            for (int zz = 0; zz < kGemmMaxSplits; zz++)
+                w[j][zz] = (live && zz < splits)
+                               ? __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                               : ((uint64_t)epoch << 32);
+        }
+#pragma unroll
+        for (int j = 0; j < EPP; j++) {
+            const int e = tid + kGemmThreads * (j0 + j), m = m0 + e / GN, nn = n0 + e % GN;
+            if (m >= M || nn >= N) continue;
+            const int64_t i = (int64_t)m * N + nn;
+            float s = 0.0f;
+#pragma unroll
+            for (int zz = 0; zz < kGemmMaxSplits; zz++) {
+                if (zz >= splits) break;
+                uint64_t v = w[j][zz];
+                for (int spin = 0; (uint32_t)(v >> 32) != epoch && spin < kGemmSpin; spin++) {
+                    __builtin_amdgcn_s_sleep(1);
+                    v = __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                const float p = __uint_as_float((uint32_t)v);
+                s = zz ? s + p : p;
+            }
+            y[i] = s;
         }
     }
 }
 
-// y = sum over the K splits of part[z], added in split order.
-__global__ void k_split_reduce(const float *__restrict__ part, int splits, int64_t mn, float *__restrict__ y) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= mn) return;
-    float s = part[i];
-    for (int z = 1; z < splits; z++) s = s + part[(int64_t)z * mn + i];
-    y[i] = s;
+// Tile grid, stage depth and K split.  Single-row-tile GEMMs (M <= 64) take
+// 16-block stages, the others 8-block stages (two workgroups per CU); the K split (at most 4 ways, each part at least 2 stages)
+// brings the grid towards one workgroup per CU.
+struct GemmPlan {
+    int tiles_m, tiles_n, splits, bps, ks;
+};
+
+static GemmPlan gemm_plan(vxm_ctx *ctx, int64_t M, int N, int nb) {
+    GemmPlan p;
+    p.tiles_m = (int)((M + GM - 1) / GM);
+    p.tiles_n = (N + GN - 1) / GN;
+    p.ks = p.tiles_m == 1 ? 16 : 8;
+    int s = 1;
+    while (s < kGemmMaxSplits && (int64_t)p.tiles_m * p.tiles_n * s < ctx->n_cu && nb / (s * 2) >= 2 * p.ks) s *= 2;
+    p.bps = (nb + s - 1) / s;
+    p.splits = (nb + p.bps - 1) / p.bps;   // every split then owns at least one block
+    return p;
+}
+
+template <int KS>
+static void launch_gemm_ks(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                           float *y, const GemmPlan &p, uint64_t *part, int *cnt, uint32_t epoch) {
+    const int grid_x = 8 * p.tiles_m * ((p.tiles_n + 7) / 8);
+    hipLaunchKernelGGL((k_gemm_q8_0_mfma<KS, false>), dim3(grid_x, p.splits), dim3(kGemmThreads), 0, ctx->stream,
+                       xq, xd, w->qs, w->d, y, part, cnt, nullptr, (int)M, (int)w->n, (int)w->k, p.tiles_m,
+                       p.tiles_n, p.bps, p.splits, epoch);
+}
+
+// Buffer-load offsets are 32-bit: every row tile of A and W must lie below 2 GiB.
+static bool gemm_fits(int64_t M, int64_t N, int64_t K) {
+    const int64_t lim = (int64_t)1 << 31;
+    return (M + GM) * K < lim && (N + GN) * K < lim;
 }
 
 static int launch_gemm(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                        float *y) {
     const int N = (int)w->n, K = (int)w->k, nb = K / 32;
+    if (!gemm_fits(M, N, K))
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "mul_mat: %lld x %d x %d exceeds the GEMM's 2 GiB operand range",
+                        (long long)M, N, K);
+    const GemmPlan p = gemm_plan(ctx, M, N, nb);
+    uint64_t *part = nullptr;
+    int *cnt = nullptr;
+    uint32_t epoch = 0;
+    if (p.splits > 1) {
+        int rc = vxm_ensure_split(ctx, (size_t)p.splits * M * N * sizeof(uint64_t), (size_t)p.tiles_m * p.tiles_n);
+        if (rc) return rc;
+        part = (uint64_t *)ctx->split_buf;
+        cnt = ctx->split_cnt;
+        // tag of this launch's partial words; the buffer starts zeroed, so 0 is never used
+        if (++ctx->split_epoch == 0) ctx->split_epoch = 1;
+        epoch = ctx->split_epoch;
+    }
+    if (p.ks == 16) launch_gemm_ks<16>(ctx, w, xq, xd, M, y, p, part, cnt, epoch);
+    else launch_gemm_ks<8>(ctx, w, xq, xd, M, y, p, part, cnt, epoch);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}
+
+// int32 block sums through the MFMA (the GEMM's own products, unscaled).
+static int launch_gemm_dots(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                            int32_t *out) {
+    const int N = (int)w->n, K = (int)w->k, nb = K / 32;
+    if (!gemm_fits(M, N, K))
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "block_dots: %lld x %d x %d exceeds the GEMM's 2 GiB operand range",
+                        (long long)M, N, K);
     const int tiles_m = (int)((M + GM - 1) / GM), tiles_n = (N + GN - 1) / GN;
     const int grid_x = 8 * tiles_m * ((tiles_n + 7) / 8);
-    // split K until the grid covers the CUs (each split at least one LDS stage)
-    int splits = 1;
-    while ((int64_t)tiles_m * tiles_n * splits < ctx->n_cu && nb / (splits * 2) >= GKS) splits *= 2;
-    const int bps = (nb + splits - 1) / splits;
-    splits = (nb + bps - 1) / bps;   // every split then owns at least one block
-    float *dst = y;
-    if (splits > 1) {
-        int rc = vxm_ensure_split(ctx, (size_t)splits * M * N * sizeof(float));
-        if (rc) return rc;
-        dst = (float *)ctx->split_buf;
-    }
-    hipLaunchKernelGGL(k_gemm_q8_0_mfma, dim3(grid_x, splits), dim3(256), 0, ctx->stream, xq, xd, w->qs, w->d, dst,
-                       (int)M, N, K, tiles_m, tiles_n, bps);
+    hipLaunchKernelGGL((k_gemm_q8_0_mfma<8, true>), dim3(grid_x, 1), dim3(kGemmThreads), 0, ctx->stream, xq, xd,
+                       w->qs, w->d, nullptr, nullptr, nullptr, out, (int)M, N, K, tiles_m, tiles_n, nb, 1, 0u);
     VXM_CHECK_LAUNCH(ctx);
-    if (splits > 1) {
-        const int64_t mn = M * N;
-        hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, ctx->stream, dst, splits,
-                           mn, y);
-        VXM_CHECK_LAUNCH(ctx);
-    }
     return VXM_OK;
 }
 
@@ -449,6 +665,9 @@ extern "C" int vxm_block_dots_q8_0(vxm_ctx *ctx, const vxm_weight *w, const int8
     if (rc) return rc;
     const int64_t total = M * w->n * (w->k / VXM_QK);
     if (total == 0) return VXM_OK;
+    // the MFMA GEMM's own block sums where the GEMM serves this M
+    const bool mfma = ctx->path == VXM_PATH_MFMA || (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
+    if (mfma) return launch_gemm_dots(ctx, w, xq_dev, xd_dev, M, out_dev);
     const int64_t grid = (total + 255) / 256;
     hipLaunchKernelGGL(k_block_dots, dim3((unsigned)grid), dim3(256), 0, ctx->stream, w->qs, xq_dev, w->n,
                        w->k, M, out_dev);

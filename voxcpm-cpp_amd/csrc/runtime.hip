@@ -62,6 +62,7 @@ extern "C" int vxm_close(vxm_ctx *ctx) {
     hipStreamSynchronize(ctx->stream);
     if (ctx->act_buf) hipFree(ctx->act_buf);
     if (ctx->split_buf) hipFree(ctx->split_buf);
+    if (ctx->split_cnt) hipFree(ctx->split_cnt);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return VXM_OK;
@@ -141,17 +142,33 @@ int vxm_ensure_act(vxm_ctx *ctx, size_t bytes) {
     return VXM_OK;
 }
 
-int vxm_ensure_split(vxm_ctx *ctx, size_t bytes) {
-    if (ctx->split_bytes >= bytes) return VXM_OK;
-    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    if (ctx->split_buf) VXM_HIP(ctx, hipFree(ctx->split_buf));
-    ctx->split_buf = nullptr;
-    ctx->split_bytes = 0;
-    if (hipMalloc(&ctx->split_buf, bytes) != hipSuccess) {
-        (void)hipGetLastError();
-        return vxm_fail(ctx, VXM_ERR_OOM, "GEMM split scratch of %zu bytes failed", bytes);
+int vxm_ensure_split(vxm_ctx *ctx, size_t bytes, size_t n_counters) {
+    if (ctx->split_bytes < bytes) {
+        VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->split_buf) VXM_HIP(ctx, hipFree(ctx->split_buf));
+        ctx->split_buf = nullptr;
+        ctx->split_bytes = 0;
+        if (hipMalloc(&ctx->split_buf, bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            return vxm_fail(ctx, VXM_ERR_OOM, "GEMM split scratch of %zu bytes failed", bytes);
+        }
+        // tagged partial words: tag 0 never matches a launch
+        VXM_HIP(ctx, hipMemsetAsync(ctx->split_buf, 0, bytes, ctx->stream));
+        ctx->split_bytes = bytes;
     }
-    ctx->split_bytes = bytes;
+    if (ctx->split_ncnt < n_counters) {
+        VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->split_cnt) VXM_HIP(ctx, hipFree(ctx->split_cnt));
+        ctx->split_cnt = nullptr;
+        ctx->split_ncnt = 0;
+        const size_t n = n_counters < 4096 ? 4096 : n_counters;
+        if (hipMalloc((void **)&ctx->split_cnt, n * sizeof(int)) != hipSuccess) {
+            (void)hipGetLastError();
+            return vxm_fail(ctx, VXM_ERR_OOM, "GEMM split counters failed");
+        }
+        VXM_HIP(ctx, hipMemsetAsync(ctx->split_cnt, 0, n * sizeof(int), ctx->stream));
+        ctx->split_ncnt = n;
+    }
     return VXM_OK;
 }
 

@@ -22,9 +22,13 @@ struct vxm_ctx {
     // scratch for internally quantized activations (vxm_mul_mat_q8_0)
     void *act_buf = nullptr;
     size_t act_bytes = 0;
-    // K-split partial tiles of the MFMA GEMM
+    // K-split partial tiles of the MFMA GEMM and its per-tile arrival counters
+    // (zero between launches: the last workgroup of a tile resets its counter)
     void *split_buf = nullptr;
     size_t split_bytes = 0;
+    int *split_cnt = nullptr;
+    size_t split_ncnt = 0;
+    uint32_t split_epoch = 0;   // tag of the last split launch's partial words
 };
 
 // Device layout of a Q8_0 matrix (n_rows x k).  The GGUF row of k/32 34-byte
@@ -113,4 +117,4 @@ int vxm_launch_quantize(vxm_ctx *ctx, const float *x, int64_t M, int64_t K, int 
 int vxm_launch_mul_mat(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd,
                        int64_t M, float *y);
 int vxm_ensure_act(vxm_ctx *ctx, size_t bytes);
-int vxm_ensure_split(vxm_ctx *ctx, size_t bytes);
+int vxm_ensure_split(vxm_ctx *ctx, size_t bytes, size_t n_counters);
