@@ -80,7 +80,7 @@ constexpr int kCW = kWaves - 1;
 constexpr int kThreads = kWaves * 64;
 constexpr int kG = 256;                // workgroups: one per CU
 constexpr int kSpin = 1 << 17;         // poll rounds before giving up
-constexpr int kLook = 5;               // 2 KiB weight units in the LDS ring per compute wave
+constexpr int kLook = 7;               // 2 KiB weight units in the LDS ring per compute wave
 constexpr int kUnit = 2048;            // quant bytes per unit (64 blocks)
 constexpr int kSlot = kUnit + 128;     // LDS bytes per ring slot: quants, then 64 fp16 scales
 // Every channel is written as kRep replicas; workgroup b reads replica
@@ -106,22 +106,23 @@ struct Shape {
     // ring slots per compute wave: A, C, D, E units of one layer
     static constexpr int SA = cdiv(UA, kCW), SC = cdiv(UC, kCW), SD = cdiv(UD, kCW), SE = cdiv(UE, kCW);
     static constexpr int OA = 0, OC = SA, OD = SA + SC, OE = SA + SC + SD, NS = SA + SC + SD + SE;
+    // lookahead: as many units as the widest phase gives one wave (SD for the
+    // MLP), so a phase's whole share of weights is in flight while it waits
+    // for its inputs
     static constexpr int P = kLook < NS ? kLook : NS;
+    static_assert(P >= SD && P >= SE, "the lookahead covers a phase");
     // vector memory instructions issued after a unit's three DMAs before it
     // is consumed: the 3 DMAs of each of the next P-1 units
     static constexpr int WAIT = 3 * (P - 1);
-    // ring size: the smallest divisor of NS that holds P units, so the slot of
-    // stream position l*NS + s is s % RING for every layer l
-    static constexpr int ring_size() {
-        for (int r = P; r <= NS; r++)
-            if (NS % r == 0) return r;
-        return NS;
-    }
-    static constexpr int RING = ring_size();
+    // the ring has P slots: stream position q = l*NS + s lives in slot q % P,
+    // and the unit issued when q is consumed (q + P) takes q's slot
+    static constexpr int RING = P;
     static constexpr int RING_BYTES = kCW * RING * kSlot;
     static constexpr int UMAX = cmax(cmax(UA, UC), cmax(UD, UE));
     static constexpr int KMAX = cmax(cmax(H, QD), F);
-    static constexpr int BIG = cmax(cmax(QD, F), H);
+    // att (QD fp32) / p (F BF16 values as F/2 pairs) / final norm (H fp32) /
+    // attention scores (cap + 1 fp32, phase B only)
+    static constexpr int BIG = cmax(cmax(QD, F / 2), H);
     static_assert(NQKV % kG == 0 && H % kG == 0 && (2 * F) % kG == 0, "rows must split over 256 workgroups");
     static_assert(RA % 2 == 0 && RC % 2 == 0 && RD % 4 == 0 && RE % 2 == 0, "rows per workgroup");
     static_assert(H % kUnit == 0 && QD % kUnit == 0 && F % kUnit == 0, "K must be a multiple of 2048");
@@ -132,16 +133,17 @@ struct Shape {
     static constexpr int L_XS = 0;                  // layer input x              [H]
     static constexpr int L_H1 = L_XS + H;           // h1                         [H]
     static constexpr int L_GN = L_H1 + H;           // RMSNorm gain of the phase  [H]
-    static constexpr int L_BIG = L_GN + H;          // att / p / final norm       [BIG]
+    static constexpr int L_BIG = L_GN + H;          // att / p / final norm / scores [BIG]
     static constexpr int L_XD = L_BIG + BIG;        // activation block scales    [KMAX/32]
     static constexpr int L_CS = L_XD + KMAX / 32;   // rope cos/sin               [HD]
     static constexpr int L_AQ = L_CS + HD;          // attention q, k, v          [3 HD]
     static constexpr int L_PART = L_AQ + 3 * HD;    // unit partials              [UMAX]
     static constexpr int L_RED = L_PART + UMAX;     // reductions / wave partials [kWaves * HD]
-    static constexpr int L_SC = L_RED + kWaves * HD;// attention scores           [cap + 1]
-    __host__ __device__ static int xq_off(int cap) { return ((L_SC + cap + 1) * 4 + 15) & ~15; }
-    __host__ __device__ static int ring_off(int cap) { return xq_off(cap) + KMAX; }   // 16-byte aligned
-    __host__ __device__ static int bytes(int cap) { return ring_off(cap) + RING_BYTES; }
+    static constexpr int L_END = L_RED + kWaves * HD;
+    static constexpr int XQ_OFF = (L_END * 4 + 15) & ~15;          // int8 quants [KMAX]
+    static constexpr int RING_OFF = XQ_OFF + KMAX;                   // 16-byte aligned
+    static constexpr int BYTES = RING_OFF + RING_BYTES;
+    static constexpr int MAX_CAP = BIG - 1;                          // scores fit BIG
 };
 
 // workgroup that runs the attention of query head h: the heads of one kv
@@ -323,6 +325,17 @@ namespace {
 // it would also wait for every weight load in flight.
 typedef const __attribute__((address_space(4))) vxm_player *vxm_ptab;
 __device__ __forceinline__ vxm_ptab layer_tab(const vxm_pparams &p) { return (vxm_ptab)p.layers; }
+// Entry l of the layer table through a uniform address.  Under register
+// pressure the compiler may keep l or the table base in VGPRs; the entry's
+// fields would then be fetched with vector loads, whose in-order completion
+// (vmcnt) would make every fetch wait for the whole weight ring.  Read-first-
+// lane makes the address scalar, so the fields are scalar (lgkmcnt) loads.
+__device__ __forceinline__ vxm_ptab layer_at(const vxm_pparams &p, int l) {
+    const uint64_t a = (uint64_t)(uintptr_t)(layer_tab(p) + l);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return (vxm_ptab)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
 
 __device__ __forceinline__ bool give_up(const vxm_pparams &p, int &it, int *bail) {
     if (++it > kSpin || __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
@@ -338,7 +351,7 @@ __device__ __forceinline__ bool give_up(const vxm_pparams &p, int &it, int *bail
 // word to dst[2i], dst[2i+1], otherwise one fp32 to dst[i].  Words whose tag
 // is not yet `tag` are read again next round.  Returns this lane's sum of
 // the squares of its values in double (exact for BF16-valued inputs).
-template <int NPL, bool PAIRS>
+template <int NPL, bool PAIRS, bool RAW = false>
 __device__ double read_words(const vxm_pparams &p, const uint64_t *src, int n, uint32_t tag, float *dst, int *bail) {
     static_assert(NPL <= 64, "words per lane");
     const int lane = tid_now() & 63;
@@ -358,7 +371,9 @@ __device__ double read_words(const vxm_pparams &p, const uint64_t *src, int n, u
             if ((pending & (1ull << k)) && (uint32_t)(w[k] >> 32) == tag) {
                 const uint32_t v = (uint32_t)w[k];
                 const int i = lane + 64 * k;
-                if (PAIRS) {
+                if (RAW) {
+                    ((uint32_t *)dst)[i] = v;   // the BF16 pair as is
+                } else if (PAIRS) {
                     const float a = __uint_as_float(v << 16), b = __uint_as_float(v & 0xffff0000u);
                     *(float2 *)(dst + 2 * i) = make_float2(a, b);
                     ss += (double)(a * a) + (double)(b * b);
@@ -443,6 +458,16 @@ __device__ void quantize_lds(const float *src, int n, int8_t *xq, float *xd) {
     for (int base = tid_now() * 4; base < n; base += kThreads * 4) {
         const float4 a = *(const float4 *)(src + base);
         const float v[4] = {a.x, a.y, a.z, a.w};
+        quant4(v, xq + base, xd + base / 32, (tid_now() & 7) == 0);
+    }
+}
+
+// Q8_0 of n BF16 values stored as pairs (low half first) in LDS, 4 values per thread.
+__device__ void quantize_lds_bf16x2(const uint32_t *src, int n, int8_t *xq, float *xd) {
+    for (int base = tid_now() * 4; base < n; base += kThreads * 4) {
+        const uint2 w = *(const uint2 *)(src + base / 2);
+        const float v[4] = {__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                            __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u)};
         quant4(v, xq + base, xd + base / 32, (tid_now() & 7) == 0);
     }
 }
@@ -543,7 +568,7 @@ __device__ __forceinline__ void unit_addr(const vxm_pparams &p, int l, int wg, i
     q = p.dummy_q;
     d = p.dummy_d;
     if (u < T::U && l < p.n_layers) {
-        vxm_ptab Ly = layer_tab(p) + l;
+        vxm_ptab Ly = layer_at(p, l);
         const int row = wg * T::R + u / T::C, c = u % T::C;
         constexpr int K = T::C * kUnit;
         const int8_t *bq = T::ph == 0 ? Ly->qkv_qs : T::ph == 1 ? Ly->o_qs : T::ph == 2 ? Ly->gu_qs : Ly->d_qs;
@@ -553,13 +578,19 @@ __device__ __forceinline__ void unit_addr(const vxm_pparams &p, int l, int wg, i
     }
 }
 
-// Issue the DMAs of slot s of layer l into ring slot s % RING.
+// Ring slot of stream position l*NS + s (l is uniform: a scalar computation).
+template <class S, int s>
+__device__ __forceinline__ int ring_slot(int l) {
+    return __builtin_amdgcn_readfirstlane((l * S::NS + s) % S::RING);
+}
+
+// Issue the DMAs of slot s of layer l into its ring slot.
 template <class S, int s>
 __device__ __forceinline__ void ring_issue(const vxm_pparams &p, uint32_t ring_lds, int l, int wg, int ci, int lane) {
     const int8_t *q;
     const uint16_t *d;
     unit_addr<S, s>(p, l, wg, ci, q, d);
-    dma_unit(ring_lds + (s % S::RING) * kSlot, q, d, lane);
+    dma_unit(ring_lds + ring_slot<S, s>(l) * kSlot, q, d, lane);
 }
 
 template <class S, int... ss>
@@ -583,7 +614,7 @@ __device__ __forceinline__ void ring_phase(const vxm_pparams &p, const int8_t *r
         const v4i x1 = *(const v4i *)(xq + c * kUnit + lane * 32 + 16);
         const float xs = xd[c * (kUnit / 32) + lane];
         ring_wait<S::WAIT>();
-        const int8_t *slot = ring + (s % S::RING) * kSlot;
+        const int8_t *slot = ring + ring_slot<S, s>(l) * kSlot;
         const v4i w0 = *(const v4i *)(slot + lane * 32);
         const v4i w1 = *(const v4i *)(slot + lane * 32 + 16);
         const uint16_t dw = *(const uint16_t *)(slot + kUnit + lane * 2);
@@ -630,8 +661,8 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     const int tid = tid_now(), wave = tid >> 6, lane = tid & 63;
     const int rp = blockIdx.x % kRep, g = h / S::QPK, pos = p.pos;
     const uint32_t ep = p.epoch;
-    vxm_ptab Ly = layer_tab(p) + l;
-    float *aq = lds + S::L_AQ, *red = lds + S::L_RED, *sc = lds + S::L_SC;
+    vxm_ptab Ly = layer_at(p, l);
+    float *aq = lds + S::L_AQ, *red = lds + S::L_RED, *sc = lds + S::L_BIG;   // scores: BIG is free in phase B
     uint16_t *const kc = Ly->kc, *const vc = Ly->vc;
     const uint16_t *kb = kc + (int64_t)g * p.cap * HD;
     const uint16_t *vb = vc + (int64_t)g * p.cap * HD;
@@ -793,7 +824,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
     float *xs = lds + S::L_XS, *h1s = lds + S::L_H1, *gn = lds + S::L_GN, *big = lds + S::L_BIG;
     float *xd = lds + S::L_XD, *cs = lds + S::L_CS, *part = lds + S::L_PART, *red = lds + S::L_RED;
     double *ssq = (double *)red;   // sum of squares from the reading wave
-    int8_t *xq = (int8_t *)lds + S::xq_off(p.cap);
+    int8_t *xq = (int8_t *)lds + S::XQ_OFF;
     const int wave = tid_now() >> 6, lane = tid_now() & 63;
     const bool reader = wave == 0;
     const int ci = __builtin_amdgcn_readfirstlane(wave - 1);   // compute wave index (uniform)
@@ -815,12 +846,12 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
     }
 
     // this wave's ring slots in LDS (compute waves only)
-    const int8_t *ring = (const int8_t *)lds + S::ring_off(p.cap) + (reader ? 0 : ci) * S::RING * kSlot;
+    const int8_t *ring = (const int8_t *)lds + S::RING_OFF + (reader ? 0 : ci) * S::RING * kSlot;
     const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
     if (!reader) ring_prime<S>(p, ring_lds, wg, ci, lane, std::make_integer_sequence<int, S::P>{});
 
     for (int l = 0; l < p.n_layers; l++) {
-        vxm_ptab Ly = layer_tab(p) + l;
+        vxm_ptab Ly = layer_at(p, l);
         // ---------------- A: norm + QKV + rope ----------------
         if (reader) {
             stage_f32(Ly->g_in, H, gn);
@@ -939,13 +970,13 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             constexpr int HALF = F / 4;
             static_assert(HALF % 64 == 0 && HALF / 64 <= 24, "p channel halves");
             const uint32_t tag = make_tag(ep, l, PH_P);
-            read_words<HALF / 64, true>(p, p.pb + rp * SP, HALF, tag, big, bail);
-            if (!*bail) read_words<HALF / 64, true>(p, p.pb + rp * SP + HALF, HALF, tag, big + 2 * HALF, bail);
+            read_words<HALF / 64, true, true>(p, p.pb + rp * SP, HALF, tag, big, bail);
+            if (!*bail) read_words<HALF / 64, true, true>(p, p.pb + rp * SP + HALF, HALF, tag, big + HALF, bail);
         }
         lds_barrier();
         if (*bail) return;
         VXM_TS(tid_now() == 0, 9);
-        quantize_lds(big, F, xq, xd);
+        quantize_lds_bf16x2((const uint32_t *)big, F, xq, xd);
         lds_barrier();
         if (!reader) ring_phase<S, S::OE, S::SE>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
         lds_barrier();
@@ -1022,7 +1053,7 @@ static constexpr int kMaxLds = 160 * 1024;
 
 template <class S>
 static int launch_decode(vxm_ctx *ctx, const vxm_pparams &prm) {
-    const int lds = S::bytes(prm.cap);
+    const int lds = S::BYTES;
     auto kern = k_decode_persistent<S>;
     if (lds > kMaxLds)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "persistent decode: kv capacity %d needs %d B of LDS", prm.cap, lds);
@@ -1042,8 +1073,8 @@ static bool persistent_shape(const vxm_block_dims &d, int n_cu) {
 
 // Largest cache capacity whose attention scores fit the LDS.
 int vxm_persistent_max_cap(const vxm_block_dims &d) {
-    const int fixed = ShapeTslm::bytes(0);
-    return (kMaxLds - fixed) / 4 - 16;
+    (void)d;
+    return ShapeTslm::MAX_CAP;
 }
 
 bool vxm_persistent_supported(const vxm_minicpm4 *m, const vxm_kv_cache *kv) {
