@@ -227,6 +227,16 @@ __device__ __forceinline__ float wave_sum_63(float v) {
     v += dpp_f<0x143, 0xC>(v);
     return v;
 }
+// Two independent wave_sum_63 chains interleaved, so each DPP step of one
+// hides the latency of the other's.
+__device__ __forceinline__ void wave_sum_63_x2(float &a, float &b) {
+    a += dpp_f<0x111>(a); b += dpp_f<0x111>(b);
+    a += dpp_f<0x112>(a); b += dpp_f<0x112>(b);
+    a += dpp_f<0x114>(a); b += dpp_f<0x114>(b);
+    a += dpp_f<0x118>(a); b += dpp_f<0x118>(b);
+    a += dpp_f<0x142, 0xA>(a); b += dpp_f<0x142, 0xA>(b);
+    a += dpp_f<0x143, 0xC>(a); b += dpp_f<0x143, 0xC>(b);
+}
 __device__ __forceinline__ double wave_sum_63_d(double v) {
     v += dpp_d<0x111>(v);
     v += dpp_d<0x112>(v);
@@ -601,25 +611,52 @@ __device__ __forceinline__ void ring_prime(const vxm_pparams &p, uint32_t ring_l
 
 // Consume the K slots of one phase starting at slot OFF: dot product of each
 // unit (lane l: block l) with the quantized activation in LDS, partial to
-// part[u]; after each unit, the loads P positions ahead are issued.
+// part[u]; after each unit, the loads P positions ahead are issued.  Units go
+// two at a time: both are waited for, read and reduced together (two
+// independent dependency chains), then both refills are issued.
+template <class S, int s>
+__device__ __forceinline__ float unit_dot(const int8_t *ring, int l, int ci, int lane, const int8_t *xq,
+                                          const float *xd) {
+    using T = Slot<S, s>;
+    const int u = ci + kCW * T::k;
+    const int c = u % T::C;
+    const v4i x0 = *(const v4i *)(xq + c * kUnit + lane * 32);
+    const v4i x1 = *(const v4i *)(xq + c * kUnit + lane * 32 + 16);
+    const float xs = xd[c * (kUnit / 32) + lane];
+    const int8_t *slot = ring + ring_slot<S, s>(l) * kSlot;
+    const v4i w0 = *(const v4i *)(slot + lane * 32);
+    const v4i w1 = *(const v4i *)(slot + lane * 32 + 16);
+    const uint16_t dw = *(const uint16_t *)(slot + kUnit + lane * 2);
+    const int si = dot16(w1, x1) + dot16(w0, x0);   // exact int32 block sum
+    return (float)si * (vxm_h2f(dw) * xs);
+}
+
 template <class S, int OFF, int K, int k = 0>
 __device__ __forceinline__ void ring_phase(const vxm_pparams &p, const int8_t *ring, uint32_t ring_lds, int l, int wg,
                                            int ci, int lane, const int8_t *xq, const float *xd, float *part) {
-    if constexpr (k < K) {
+    if constexpr (k + 1 < K) {
+        constexpr int s = OFF + k;
+        using T0 = Slot<S, s>;
+        using T1 = Slot<S, s + 1>;
+        const int u0 = ci + kCW * T0::k, u1 = ci + kCW * T1::k;
+        ring_wait<S::WAIT - 3>();   // units s and s + 1 are in LDS
+        float a = unit_dot<S, s>(ring, l, ci, lane, xq, xd);
+        float b = unit_dot<S, s + 1>(ring, l, ci, lane, xq, xd);
+        wave_sum_63_x2(a, b);
+        if (lane == 63) {
+            if (u0 < T0::U) part[u0] = a;
+            if (u1 < T1::U) part[u1] = b;
+        }
+        constexpr int sn0 = (s + S::P) % S::NS, sn1 = (s + 1 + S::P) % S::NS;
+        ring_issue<S, sn0>(p, ring_lds, l + (s + S::P >= S::NS ? 1 : 0), wg, ci, lane);
+        ring_issue<S, sn1>(p, ring_lds, l + (s + 1 + S::P >= S::NS ? 1 : 0), wg, ci, lane);
+        ring_phase<S, OFF, K, k + 2>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+    } else if constexpr (k < K) {
         constexpr int s = OFF + k;
         using T = Slot<S, s>;
-        const int u = ci + kCW * k;
-        const int c = u % T::C;
-        const v4i x0 = *(const v4i *)(xq + c * kUnit + lane * 32);
-        const v4i x1 = *(const v4i *)(xq + c * kUnit + lane * 32 + 16);
-        const float xs = xd[c * (kUnit / 32) + lane];
+        const int u = ci + kCW * T::k;
         ring_wait<S::WAIT>();
-        const int8_t *slot = ring + ring_slot<S, s>(l) * kSlot;
-        const v4i w0 = *(const v4i *)(slot + lane * 32);
-        const v4i w1 = *(const v4i *)(slot + lane * 32 + 16);
-        const uint16_t dw = *(const uint16_t *)(slot + kUnit + lane * 2);
-        const int si = dot16(w1, x1) + dot16(w0, x0);   // exact int32 block sum
-        const float a = wave_sum_63((float)si * (vxm_h2f(dw) * xs));
+        const float a = wave_sum_63(unit_dot<S, s>(ring, l, ci, lane, xq, xd));
         if (lane == 63 && u < T::U) part[u] = a;
         constexpr int sn = (s + S::P) % S::NS;
         ring_issue<S, sn>(p, ring_lds, l + (s + S::P >= S::NS ? 1 : 0), wg, ci, lane);
@@ -863,16 +900,22 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
                     ss += (double)(v.x * v.x) + (double)(v.y * v.y) + (double)(v.z * v.z) + (double)(v.w * v.w);
                 }
             } else {
-                ss = read_words<cdiv(H / 2, 64), true>(p, p.xb + ((l & 1) * kRep + rp) * SX, H / 2,
+                ss = read_words<cdiv(H / 4, 64), true>(p, p.xb + ((l & 1) * kRep + rp) * SX, H / 4,
                                                        make_tag(ep, l, PH_X), xs, bail);
             }
             ss = wave_sum_63_d(ss);
             if (lane == 63) ssq[0] = ss;
+        } else if (wave == 1 && l > 0) {
+            // the second half of x, read in parallel with wave 0's
+            double ss = read_words<cdiv(H / 4, 64), true>(p, p.xb + ((l & 1) * kRep + rp) * SX + H / 4, H / 4,
+                                                          make_tag(ep, l, PH_X), xs + H / 2, bail);
+            ss = wave_sum_63_d(ss);
+            if (lane == 63) ssq[1] = ss;
         }
         lds_barrier();
         if (*bail) return;
         VXM_TS(tid_now() == 0, 0);
-        norm_quant<H>(xs, gn, ssq[0], p.eps, xq, xd);
+        norm_quant<H>(xs, gn, l > 0 ? ssq[0] + ssq[1] : ssq[0], p.eps, xq, xd);
         lds_barrier();
         if (!reader) ring_phase<S, S::OA, S::SA>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
         lds_barrier();
@@ -904,13 +947,15 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             if (*bail) return;
         }
         // ---------------- C: O rows + residual ----------------
-        if (reader) {
+        if (wave < 2) {
+            // waves 0 and 1 (idle until this input arrives) each read one half:
+            // the two rounds of loads are in flight together
             const uint64_t *src = p.attb + rp * SAT;
             const uint32_t tag = make_tag(ep, l, PH_ATT);
             wait_sentinels(p, src, NH, HD, tag, bail);
             static_assert(QD % 128 == 0 && QD / 128 <= 24, "attention channel halves");
-            if (!*bail) read_words<QD / 128, false>(p, src, QD / 2, tag, big, bail);
-            if (!*bail) read_words<QD / 128, false>(p, src + QD / 2, QD / 2, tag, big + QD / 2, bail);
+            const int hf = wave * (QD / 2);
+            if (!*bail) read_words<QD / 128, false>(p, src + hf, QD / 2, tag, big + hf, bail);
         }
         lds_barrier();
         if (*bail) return;
@@ -936,16 +981,18 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             put_word(p.h1b + r * SX + row / 2, pack_bf16x2(hh[0], hh[1]), make_tag(ep, l, PH_H1));
         }
         // ---------------- D: post norm + gate/up + SwiGLU ----------------
-        if (reader) {
-            stage_f32(Ly->g_post, H, gn);
-            double ss = read_words<cdiv(H / 2, 64), true>(p, p.h1b + rp * SX, H / 2, make_tag(ep, l, PH_H1), h1s, bail);
+        if (wave < 2) {
+            // waves 0 and 1 each read one half of h1 (and wave 0 stages the gain)
+            if (reader) stage_f32(Ly->g_post, H, gn);
+            double ss = read_words<cdiv(H / 4, 64), true>(p, p.h1b + rp * SX + wave * (H / 4), H / 4,
+                                                          make_tag(ep, l, PH_H1), h1s + wave * (H / 2), bail);
             ss = wave_sum_63_d(ss);
-            if (lane == 63) ssq[0] = ss;
+            if (lane == 63) ssq[wave] = ss;
         }
         lds_barrier();
         if (*bail) return;
         VXM_TS(tid_now() == 0, 7);
-        norm_quant<H>(h1s, gn, ssq[0], p.eps, xq, xd);
+        norm_quant<H>(h1s, gn, ssq[0] + ssq[1], p.eps, xq, xd);
         lds_barrier();
         if (!reader) ring_phase<S, S::OD, S::SD>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
         lds_barrier();
@@ -964,14 +1011,12 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             put_word(p.pb + r * SP + wg * (S::RD / 4) + wi, pack_bf16x2(p0, p1), make_tag(ep, l, PH_P));
         }
         // ---------------- E: down rows + residual ----------------
-        if (reader) {
-            // two halves of at most 24 words per lane: the words in flight
-            // share the register file with the weight ring
-            constexpr int HALF = F / 4;
-            static_assert(HALF % 64 == 0 && HALF / 64 <= 24, "p channel halves");
+        if (wave < 4) {
+            // waves 0..3 (idle until this input arrives) each read one quarter
+            constexpr int QW = F / 8;
+            static_assert(QW % 64 == 0 && QW / 64 <= 24, "p channel quarters");
             const uint32_t tag = make_tag(ep, l, PH_P);
-            read_words<HALF / 64, true, true>(p, p.pb + rp * SP, HALF, tag, big, bail);
-            if (!*bail) read_words<HALF / 64, true, true>(p, p.pb + rp * SP + HALF, HALF, tag, big + HALF, bail);
+            read_words<QW / 64, true, true>(p, p.pb + rp * SP + wave * QW, QW, tag, big + wave * QW, bail);
         }
         lds_barrier();
         if (*bail) return;
