@@ -981,18 +981,18 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             put_word(p.h1b + r * SX + row / 2, pack_bf16x2(hh[0], hh[1]), make_tag(ep, l, PH_H1));
         }
         // ---------------- D: post norm + gate/up + SwiGLU ----------------
-        if (wave < 2) {
-            // waves 0 and 1 each read one half of h1 (and wave 0 stages the gain)
-            if (reader) stage_f32(Ly->g_post, H, gn);
-            double ss = read_words<cdiv(H / 4, 64), true>(p, p.h1b + rp * SX + wave * (H / 4), H / 4,
-                                                          make_tag(ep, l, PH_H1), h1s + wave * (H / 2), bail);
+        if (reader) {
+            // the reader alone: a compute wave's loads would wait (in-order
+            // vmcnt) for the D units it has just put in flight
+            stage_f32(Ly->g_post, H, gn);
+            double ss = read_words<cdiv(H / 2, 64), true>(p, p.h1b + rp * SX, H / 2, make_tag(ep, l, PH_H1), h1s, bail);
             ss = wave_sum_63_d(ss);
-            if (lane == 63) ssq[wave] = ss;
+            if (lane == 63) ssq[0] = ss;
         }
         lds_barrier();
         if (*bail) return;
         VXM_TS(tid_now() == 0, 7);
-        norm_quant<H>(h1s, gn, ssq[0] + ssq[1], p.eps, xq, xd);
+        norm_quant<H>(h1s, gn, ssq[0], p.eps, xq, xd);
         lds_barrier();
         if (!reader) ring_phase<S, S::OD, S::SD>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
         lds_barrier();
