@@ -275,12 +275,163 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ q, 
     }
 }
 
+// ---------------------------------------------------------------------------
+// The same attention for many queries of one segment (prefill), on f16 MFMA
+// (v_mfma_f32_32x32x16_f16: lane l supplies A[l%32][8(l/32)..+8] and
+// B[8(l/32)..+8][l%32]; result register v of lane l is row 8(v/4) + 4(l/32)
+// + v%4, column l%32).  One workgroup (4 waves) per (query head, tile of
+// AQ = 32 consecutive tokens):
+//   scores  S = Q K^T * scale over the tile's key span [0, kv_end): the
+//           queries are BF16 values and the cache holds f16, both exact in
+//           f16, so every product is exact and only the fp32 summation order
+//           differs from the reference's; wave w takes key block w of each
+//           128-key stage;
+//   softmax per query row over its own kv_len (8 threads per row: max, expf,
+//           sum in double), p = e * (float)(1 / sum), 0 past kv_len;
+//   output  O = P V: wave w owns output dims [32w, 32w + 32); P enters the
+//           MFMA as f16 hi + lo halves (two products, ~22 bits of p), V as
+//           a transposed f16 tile.
+// The score buffer holds AKV keys: longer spans take k_attention.
+// ---------------------------------------------------------------------------
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+constexpr int AQ = 32, AKV = 512, ATH = 256;
+
+template <int HD>
+__global__ __launch_bounds__(ATH) void k_attention_mfma(const float *__restrict__ q, const uint16_t *__restrict__ kc,
+                                                        const uint16_t *__restrict__ vc, float *__restrict__ out,
+                                                        int M, int nh, int nkv, int cap, int kv_base, int causal) {
+    constexpr int QP = HD + 8;      // f16 row pitch of Q and K tiles (16-byte pad)
+    constexpr int KS = 128;         // keys per K stage (one 32-key block per wave)
+    constexpr int VS = 64;          // keys per V stage
+    constexpr int VP = VS + 8;      // f16 row pitch of the transposed V tile
+    constexpr int SP = AKV + 4;     // fp32 score row pitch
+    __shared__ __align__(16) _Float16 Qh[AQ * QP];
+    __shared__ __align__(16) _Float16 Kh[KS * QP];
+    __shared__ __align__(16) _Float16 Vt[HD * VP];
+    __shared__ __align__(16) float Sc[AQ * SP];
+    const int h = blockIdx.x, t0 = blockIdx.y * AQ, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kvh = h / (nh / nkv);
+    const uint16_t *kb = kc + (int64_t)kvh * cap * HD;
+    const uint16_t *vb = vc + (int64_t)kvh * cap * HD;
+    const int nq = min(AQ, M - t0);
+    const int kv_end = causal ? kv_base + t0 + nq : M;
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
+    const int lr = lane & 31, lh = lane >> 5;
+    for (int i = tid; i < AQ * HD; i += ATH) {
+        const int r = i / HD, d = i % HD;
+        Qh[r * QP + d] = (_Float16)(r < nq ? q[(int64_t)(t0 + r) * nh * HD + h * HD + d] : 0.0f);
+    }
+    // pass 1: scores, 128 keys per stage
+    for (int k0 = 0; k0 < kv_end; k0 += KS) {
+        __syncthreads();
+        for (int i = tid * 8; i < KS * HD; i += ATH * 8) {
+            const int r = i / HD, d = i % HD;
+            uint4 w = make_uint4(0, 0, 0, 0);
+            if (k0 + r < kv_end) w = *(const uint4 *)(kb + (int64_t)(k0 + r) * HD + d);
+            *(uint4 *)(Kh + r * QP + d) = w;
+        }
+        __syncthreads();
+        const int kblk = k0 + 32 * wave;
+        if (kblk < kv_end) {
+            v16f c = v16f{};
+#pragma unroll
+            for (int kk = 0; kk < HD / 16; kk++) {
+                const v8h a = *(const v8h *)(Qh + lr * QP + 16 * kk + 8 * lh);
+                const v8h b = *(const v8h *)(Kh + (32 * wave + lr) * QP + 16 * kk + 8 * lh);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+            }
+#pragma unroll
+            for (int v = 0; v < 16; v++) Sc[(8 * (v >> 2) + 4 * lh + (v & 3)) * SP + kblk + lr] = c[v] * scale;
+        }
+    }
+    __syncthreads();
+    // pass 2: softmax of each row over its kv_len (8 threads per row)
+    {
+        const int qi = tid >> 3, sub = tid & 7;
+        const int kvl = qi < nq ? (causal ? kv_base + t0 + qi + 1 : M) : 0;
+        float *row = Sc + qi * SP;
+        float mx = -INFINITY;
+        for (int j = sub; j < kvl; j += 8) mx = fmaxf(mx, row[j]);
+#pragma unroll
+        for (int m = 4; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 8));
+        double sum = 0.0;
+        for (int j = sub; j < kvl; j += 8) {
+            const float e = expf(row[j] - mx);
+            row[j] = e;
+            sum += (double)e;
+        }
+#pragma unroll
+        for (int m = 4; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 8);
+        const float inv = kvl > 0 ? (float)(1.0 / sum) : 0.0f;
+        const int span = (kv_end + VS - 1) / VS * VS;
+        for (int j = sub; j < span; j += 8) row[j] = j < kvl ? row[j] * inv : 0.0f;
+    }
+    // pass 3: O = P V, 64 keys per stage; wave w < HD/32 owns dims [32w, 32w + 32)
+    v16f o = v16f{};
+    for (int v0 = 0; v0 < kv_end; v0 += VS) {
+        __syncthreads();
+        // transpose: thread moves 8 dims of one key row into column (key) of Vt
+        for (int i = tid * 8; i < VS * HD; i += ATH * 8) {
+            const int r = i / HD, d = i % HD;
+            uint4 w = make_uint4(0, 0, 0, 0);
+            if (v0 + r < kv_end) w = *(const uint4 *)(vb + (int64_t)(v0 + r) * HD + d);
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                ((uint16_t *)Vt)[(d + 2 * e) * VP + r] = (uint16_t)(ww[e] & 0xffffu);
+                ((uint16_t *)Vt)[(d + 2 * e + 1) * VP + r] = (uint16_t)(ww[e] >> 16);
+            }
+        }
+        __syncthreads();
+        if (wave < HD / 32) {
+#pragma unroll
+            for (int ks = 0; ks < VS; ks += 16) {
+                const float *pr = Sc + lr * SP + v0 + ks + 8 * lh;
+                const float4 p0 = *(const float4 *)pr, p1 = *(const float4 *)(pr + 4);
+                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                v8h ahi, alo;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const _Float16 hi = (_Float16)pv[e];
+                    ahi[e] = hi;
+                    alo[e] = (_Float16)(pv[e] - (float)hi);
+                }
+                const v8h b = *(const v8h *)(Vt + (32 * wave + lr) * VP + ks + 8 * lh);
+                o = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, b, o, 0, 0, 0);
+                o = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, b, o, 0, 0, 0);
+            }
+        }
+    }
+    if (wave < HD / 32) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int qi = 8 * (v >> 2) + 4 * lh + (v & 3);
+            if (qi < nq) out[(int64_t)(t0 + qi) * nh * HD + h * HD + 32 * wave + lr] = o[v];
+        }
+    }
+}
+
 int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
                          int64_t M, int nh, int nkv, int hd, int cap, int64_t seg_stride, int S, int kv_base,
                          int causal) {
     if (M <= 0) return VXM_OK;
     if (hd > 256 || hd <= 0 || nkv <= 0 || nh % nkv)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "attention: head_dim %d / heads %d,%d unsupported", hd, nh, nkv);
+    // many queries of a single segment whose key span fits the score buffer: the MFMA kernel
+    const int64_t span = causal ? kv_base + M : M;
+    if (S == M && M >= AQ && span <= AKV && span <= cap && (hd == 128 || hd == 64)) {
+        const dim3 grid(nh, (unsigned)((M + AQ - 1) / AQ));
+        if (hd == 128)
+            hipLaunchKernelGGL(k_attention_mfma<128>, grid, dim3(ATH), 0, ctx->stream, q, kc, vc, out, (int)M, nh,
+                               nkv, cap, kv_base, causal);
+        else
+            hipLaunchKernelGGL(k_attention_mfma<64>, grid, dim3(ATH), 0, ctx->stream, q, kc, vc, out, (int)M, nh,
+                               nkv, cap, kv_base, causal);
+        VXM_CHECK_LAUNCH(ctx);
+        return VXM_OK;
+    }
     const size_t lds = (size_t)(hd + cap + 256) * sizeof(float);
     if (lds > 160 * 1024)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "attention: capacity %d exceeds the LDS score buffer", cap);
