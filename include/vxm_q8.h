@@ -237,6 +237,93 @@ int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev, int32_t P,
                   const float *mu_dev, int32_t n_steps, float cfg_value, int32_t schedule,
                   int32_t use_zero_star);
 
+/* ---- LocEnc and the per-token LM update ----------------------------------
+ * Mirrors vcpm_locenc_config (src/locenc.h:49-60); max_seq_len and
+ * patch_size are unused there and left out. */
+typedef struct vxm_locenc_config {
+    int32_t hidden_size;
+    int32_t n_layers;
+    int32_t n_heads;
+    int32_t n_kv_heads;
+    int32_t intermediate_size;
+    int32_t head_dim;
+    int32_t feat_dim;         /* latent width of one patch position (in_proj input) */
+    float   rms_norm_eps;
+    int32_t rope_theta;       /* the reference passes 10000 (src/locenc.c:100-110) */
+    /* head_dim/2 rope frequency factors (host), or NULL for the reference
+     * rule (the LongRoPE short factors when head_dim == 128). */
+    const float *rope_freq_factors;
+} vxm_locenc_config;
+
+/* vcpm_locenc_weights (src/locenc.h:67-73): GGUF Q8_0 rows of in_proj
+ * [hidden][feat_dim] and of the blocks; F32 host copies of the vectors. */
+typedef struct vxm_locenc_weights_q8_0 {
+    const vxm_layer_weights_q8_0 *layers;
+    const void  *in_proj;   const float *in_bias;     /* in_bias may be NULL   */
+    const float *special_token;                       /* [hidden] or NULL      */
+    const float *norm;                                /* [hidden] final RMSNorm */
+} vxm_locenc_weights_q8_0;
+
+typedef struct vxm_locenc vxm_locenc;
+
+int vxm_locenc_create(vxm_ctx *ctx, const vxm_locenc_config *cfg, const vxm_locenc_weights_q8_0 *w,
+                      vxm_locenc **out);
+int vxm_locenc_free(vxm_locenc *m);
+
+/* vcpm_locenc_forward (src/locenc.c:44-131) on x [P][feat_dim]: h = in_proj x
+ * + bias (F32, no BF16), the special token prepended as row 0, n_layers
+ * bidirectional rope blocks (positions 0..), final RMSNorm.  out is the
+ * special token's row [hidden]; without a special token it is every row
+ * [P][hidden]. */
+int vxm_locenc_forward(vxm_locenc *m, const float *x_dev, int32_t P, float *out_dev);
+
+/* The scalar quantizer core of the FSQ layer, vcpm_fsq_quantize
+ * (src/fsq.c:16-29): y = round(tanh(x) * s) * (1/s) elementwise, round half
+ * away from zero (ggml_round); quant_scale <= 0 copies x. */
+int vxm_fsq_quantize(vxm_ctx *ctx, const float *x_dev, int64_t n, float quant_scale, float *y_dev);
+
+/* Widths and FSQ scale of gen_lm_update (src/gen_step.c:712-927). */
+typedef struct vxm_lm_update_config {
+    int32_t lm_hidden;        /* TSLM hidden (audio embedding, FSQ output)    */
+    int32_t enc_hidden;       /* LocEnc hidden                                */
+    int32_t fsq_dim;          /* rows of fsq.in_proj                          */
+    int32_t res_hidden;       /* RALM hidden                                  */
+    float   fsq_quant_scale;  /* voxcpm.fsq_quant_scale, 9 by default (src/model_loader.c:60,152) */
+} vxm_lm_update_config;
+
+/* The projections around the two LMs (src/gen_init.c:325-348), GGUF Q8_0
+ * rows and F32 biases (each bias may be NULL).  fsq_in == NULL means the
+ * model has no FSQ layer: its output is the TSLM hidden unchanged
+ * (src/gen_step.c:272). */
+typedef struct vxm_lm_update_weights_q8_0 {
+    const void *enc_to_lm;     const float *enc_to_lm_bias;   /* [lm_hidden][enc_hidden] */
+    const void *fsq_in;        const float *fsq_in_bias;      /* [fsq_dim][lm_hidden]    */
+    const void *fsq_out;       const float *fsq_out_bias;     /* [lm_hidden][fsq_dim]    */
+    const void *fusion_concat;                                /* [res_hidden][2 lm_hidden] */
+} vxm_lm_update_weights_q8_0;
+
+typedef struct vxm_lm_update vxm_lm_update;
+
+/* The update borrows enc, tslm and ralm (RALM = no_rope MiniCPM4); they must
+ * outlive it. */
+int vxm_lm_update_create(vxm_ctx *ctx, const vxm_lm_update_config *cfg, const vxm_lm_update_weights_q8_0 *w,
+                         vxm_locenc *enc, vxm_minicpm4 *tslm, vxm_minicpm4 *ralm, vxm_lm_update **out);
+int vxm_lm_update_free(vxm_lm_update *u);
+
+/* gen_lm_update (src/gen_step.c:712-927) for the patch just generated,
+ * prev_patch [P][feat_dim] (device), at sequence position pos:
+ *   audio_embed = enc_to_lm(LocEnc(prev_patch)) + bias           [lm_hidden]
+ *   base_hidden = TSLM(audio_embed), cache row pos               [lm_hidden]
+ *   fsq         = fsq_out(FSQ(fsq_in(base_hidden) + b)) + b      [lm_hidden]
+ *   ralm_hidden = RALM(fusion_concat([fsq ; audio_embed])), row pos [res_hidden]
+ * The reference reads audio_embed / base_hidden / fsq back to the host
+ * between the two LM graphs; here the whole chain is stream-ordered on the
+ * device with no host synchronisation.  audio_embed_dev and fsq_dev may be
+ * NULL; base_hidden_dev and ralm_hidden_dev receive the LM states. */
+int vxm_lm_update_step(vxm_lm_update *u, vxm_kv_cache *tslm_kv, vxm_kv_cache *ralm_kv,
+                       const float *prev_patch_dev, int32_t P, int32_t pos, float *audio_embed_dev,
+                       float *base_hidden_dev, float *fsq_dev, float *ralm_hidden_dev);
+
 /* ---- host helpers (no device work) --------------------------------------
  * GGUF Q8_0 quantization of F32 rows with the weight rule of
  * ggml_quantize_chunk (tools/quantize.c:292): d = amax/127 (fp16),

@@ -60,6 +60,15 @@ class LocDiT(C.Structure):
     ]
 
 
+class LocEnc(C.Structure):
+    _fields_ = [
+        ("layers", C.c_void_p), ("n_layers", C.c_int32),
+        ("in_proj", C.c_void_p), ("in_bias", C.c_void_p),
+        ("special", C.c_void_p), ("norm", C.c_void_p),
+        ("feat", C.c_int32),
+    ]
+
+
 _lib = None
 
 
@@ -108,6 +117,8 @@ def lib():
         L.orc_cfm_zero_star_steps.argtypes = [_I]
         L.orc_cfm_solve.argtypes = [C.POINTER(Cfg), C.POINTER(LocDiT), _P, _P, C.c_int32, C.c_int32, _P,
                                     _I, _F, _I, _I]
+        L.orc_locenc_forward.argtypes = [C.POINTER(Cfg), C.POINTER(LocEnc), _P, C.c_int32, _P, _P]
+        L.orc_fsq_quantize.argtypes = [_P, _I64, _F, _P]
         _lib = L
     return _lib
 
@@ -387,3 +398,81 @@ def cfm_solve(cfg, w, x, cond, mu, n_steps, cfg_value, schedule=0, use_zero_star
                              n_steps, cfg_value, schedule, use_zero_star)
     assert rc == 0
     return x
+
+
+# ---- LocEnc / FSQ / LM update ----
+
+class LocEncW:
+    """Host copy of LocEnc weights: GGUF Q8_0 rows of in_proj + F32 vectors (in_bias / special may be None)."""
+
+    names = ("in_proj", "in_bias", "special", "norm")
+
+    def __init__(self, layers, feat, **kw):
+        self.layers = layers
+        self.feat = feat
+        for n in self.names:
+            v = kw.get(n)
+            setattr(self, n, None if v is None else np.ascontiguousarray(v))
+
+    def struct(self):
+        self._arr = (Layer * max(1, len(self.layers)))(*[l.struct() for l in self.layers])
+        g = {n: (None if getattr(self, n) is None else getattr(self, n).ctypes.data) for n in self.names}
+        return LocEnc(C.cast(self._arr, C.c_void_p).value, len(self.layers), g["in_proj"], g["in_bias"],
+                      g["special"], g["norm"], self.feat)
+
+
+def locenc_forward(cfg, w, x, states=False):
+    """orc_locenc_forward: [hidden] (special-token row) or [P][hidden]; with states=True also the
+    sequence entering each block and leaving the last."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    P, H = x.shape[0], cfg.hidden
+    S = P + (w.special is not None)
+    out = np.empty((1 if w.special is not None else P, H), dtype=np.float32)
+    st = np.empty((len(w.layers) + 1, S, H), dtype=np.float32) if states else None
+    s = w.struct()
+    rc = lib().orc_locenc_forward(C.byref(cfg), C.byref(s), _p(x), P, _p(out), _p(st))
+    assert rc == 0
+    out = out[0] if w.special is not None else out
+    return (out, st) if states else out
+
+
+def fsq_quantize(x, quant_scale):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().orc_fsq_quantize(_p(x), x.size, quant_scale, _p(y))
+    return y
+
+
+def linear(w, x, N, K, bias=None, variant=QUANT_X86):
+    """ggml_mul_mat of Q8_0 rows w [N][K] with F32 x [M][K] (x quantized to Q8_0), plus an F32 bias."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    y = mul_mat(w, quantize_rows(x, variant), N, K, x.shape[0])
+    if bias is not None:
+        y = (y + np.asarray(bias, np.float32)).astype(np.float32)
+    return y
+
+
+def lm_update(enc_cfg, enc_w, tslm, ralm, pw, prev_patch, pos, fsq_scale=9.0, variant=QUANT_X86):
+    """gen_lm_update (src/gen_step.c:712-927) composed from the oracle pieces.
+
+    tslm / ralm: dicts with cfg, layers, norm, k, v (per-layer f16 caches, updated in place), cap.
+    pw: dict of the projections (enc_to_lm, enc_to_lm_bias, fsq_in, fsq_in_bias, fsq_out, fsq_out_bias,
+    fusion) as GGUF Q8_0 rows / F32 vectors, with widths L (lm hidden), E, Fq, R.
+    Returns (audio_embed, base_hidden, fsq, ralm_hidden)."""
+    L, E, R = pw["L"], pw["E"], pw["R"]
+    fe = locenc_forward(enc_cfg, enc_w, prev_patch)
+    audio = linear(pw["enc_to_lm"], fe, L, E, pw.get("enc_to_lm_bias"), variant)[0]
+    base = minicpm4_forward(tslm["cfg"], tslm["layers"], tslm["norm"], audio[None], tslm["k"], tslm["v"],
+                            tslm["cap"], pos)[0]
+    if pw.get("fsq_in") is not None:
+        Fq = pw["Fq"]
+        h = linear(pw["fsq_in"], base, Fq, L, pw.get("fsq_in_bias"), variant)[0]
+        q = fsq_quantize(h, fsq_scale)
+        fsq = linear(pw["fsq_out"], q, L, Fq, pw.get("fsq_out_bias"), variant)[0]
+    else:
+        fsq = base.copy()
+    cat = np.concatenate([fsq, audio]).astype(np.float32)
+    ralm_in = linear(pw["fusion"], cat, R, 2 * L, None, variant)[0]
+    ralm_h = minicpm4_forward(ralm["cfg"], ralm["layers"], ralm["norm"], ralm_in[None], ralm["k"], ralm["v"],
+                              ralm["cap"], pos)[0]
+    return audio, base, fsq, ralm_h

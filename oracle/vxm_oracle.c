@@ -625,3 +625,45 @@ int orc_cfm_solve(const orc_cfg *cfg, const orc_locdit *w, float *x, const float
     free(vc); free(vu);
     return 0;
 }
+
+/* vcpm_locenc_forward (src/locenc.c:44-131): h = in_proj x + bias, F32 (the
+ * reference adds no BF16 round here); the special token prepended as row 0
+ * (src/locenc.c:65-85); n_layers bidirectional MiniCPM4 blocks with rope from
+ * position 0, theta 10000, residual scale 1 (src/locenc.c:87-112); the final
+ * RMSNorm (src/locenc.c:114-116); the special token's row is the output
+ * (src/locenc.c:118-128), every row when there is no special token. */
+int orc_locenc_forward(const orc_cfg *cfg, const orc_locenc *w, const float *x, int32_t P,
+                       float *out, float *states) {
+    const int64_t H = cfg->hidden, F = w->feat;
+    const int64_t off = w->special ? 1 : 0, S = off + P;
+    float *seq = (float *)calloc((size_t)(S * H), sizeof(float));
+    if (w->special) memcpy(seq, w->special, sizeof(float) * (size_t)H);
+    mul_mat_f32_in(w->in_proj, x, H, F, P, seq + off * H, cfg->quant_variant);
+    if (w->in_bias)
+        for (int64_t r = 0; r < P; r++)
+            for (int64_t i = 0; i < H; i++) seq[(off + r) * H + i] = seq[(off + r) * H + i] + w->in_bias[i];
+    for (int32_t l = 0; l < w->n_layers; l++) {
+        if (states) memcpy(states + (size_t)l * S * H, seq, sizeof(float) * (size_t)(S * H));
+        orc_minicpm4_block(cfg, &w->layers[l], seq, S, NULL, NULL, 0, 0, 1);
+    }
+    if (states) memcpy(states + (size_t)w->n_layers * S * H, seq, sizeof(float) * (size_t)(S * H));
+    orc_rms_norm(seq, w->norm, off ? 1 : S, H, cfg->eps, out);
+    free(seq);
+    return 0;
+}
+
+/* vcpm_fsq_quantize (src/fsq.c:16-29): ggml_tanh, ggml_scale by s, ggml_round
+ * (roundf: half away from zero), ggml_scale by 1.0f / s.  s <= 0 is the
+ * identity (the reference returns x unchanged). */
+void orc_fsq_quantize(const float *x, int64_t n, float quant_scale, float *y) {
+    const float inv = quant_scale > 0.0f ? 1.0f / quant_scale : 0.0f;
+    for (int64_t i = 0; i < n; i++) {
+        float v = x[i];
+        if (quant_scale > 0.0f) {
+            const float t = tanhf(v);
+            const float sc = t * quant_scale;
+            v = roundf(sc) * inv;
+        }
+        y[i] = v;
+    }
+}

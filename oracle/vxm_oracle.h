@@ -117,6 +117,23 @@ int   orc_cfm_solve(const orc_cfg *cfg, const orc_locdit *w, float *x, const flo
                     int32_t P, int32_t Pc, const float *mu, int n_steps, float cfg_value,
                     int schedule, int use_zero_star);
 
+/* ---- LocEnc, FSQ ---- */
+typedef struct orc_locenc {
+    const orc_layer *layers;
+    int32_t n_layers;
+    const uint8_t *in_proj;  const float *in_bias;     /* hidden x feat (Q8_0 rows) */
+    const float   *special;                            /* hidden, or NULL */
+    const float   *norm;                               /* hidden */
+    int32_t feat;
+} orc_locenc;
+
+/* out: the special token's row [hidden], or every row [P][hidden] without
+ * one; states (optional): the sequence entering each block and leaving the
+ * last, [(n_layers + 1)][P + has_special][hidden]. */
+int  orc_locenc_forward(const orc_cfg *cfg, const orc_locenc *w, const float *x, int32_t P,
+                        float *out, float *states);
+void orc_fsq_quantize(const float *x, int64_t n, float quant_scale, float *y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,362 @@
+// lm_update.hip -- the per-token LM update of the VoxCPM2 generation loop
+// (gen_lm_update, src/gen_step.c:712-927) on gfx950: the LocEnc feature
+// encoder (vcpm_locenc_forward, src/locenc.c:44-131), the audio embedding
+// projection, the TSLM decode step, the FSQ layer (gen_fsq_hidden,
+// src/gen_step.c:268-290 with vcpm_fsq_quantize, src/fsq.c:16-29), the
+// fusion projection and the RALM decode step.
+//
+// The reference computes this as two graphs with the host reading the audio
+// embedding, the TSLM hidden and the FSQ output in between.  Here every piece
+// is a stream-ordered launch on device buffers: M = 1 projections take the
+// Q8_0 GEMV, the two LM steps take vxm_minicpm4_forward (the persistent
+// decode kernel where it applies), the encoder's P + 1 rows take the block
+// kernels.  No host synchronisation.
+#include <math.h>
+#include <string.h>
+
+#include <vector>
+
+#include "vxm_model.h"
+
+struct vxm_locenc {
+    vxm_ctx *ctx = nullptr;
+    vxm_locenc_config cfg{};
+    vxm_block_dims dims;
+    std::vector<vxm_block> blocks;
+    vxm_weight *in_proj = nullptr;
+    float *in_bias = nullptr, *special = nullptr, *norm = nullptr;
+    vxm_workspace ws;
+    void *buf = nullptr;   // seq [S][H], xh [P][H], aq/ad of x
+    size_t buf_bytes = 0;
+    float *seq = nullptr, *xh = nullptr;
+    int8_t *aq = nullptr;
+    uint16_t *ad = nullptr;
+};
+
+struct vxm_lm_update {
+    vxm_ctx *ctx = nullptr;
+    vxm_lm_update_config cfg{};
+    vxm_locenc *enc = nullptr;
+    vxm_minicpm4 *tslm = nullptr, *ralm = nullptr;
+    vxm_weight *enc_to_lm = nullptr, *fsq_in = nullptr, *fsq_out = nullptr, *fusion = nullptr;
+    float *enc_to_lm_bias = nullptr, *fsq_in_bias = nullptr, *fsq_out_bias = nullptr;
+    float inv_scale = 0.0f;
+    void *buf = nullptr;
+    float *fe = nullptr;     // LocEnc output [enc_hidden]
+    float *cat = nullptr;    // [fsq (lm_hidden) ; audio_embed (lm_hidden)]
+    float *fh = nullptr;     // raw fsq.in_proj output [fsq_dim]
+    int8_t *aq = nullptr;    // Q8_0 of the widest input (2 lm_hidden)
+    uint16_t *ad = nullptr;
+};
+
+// ---------------------------------------------------------------------------
+// kernels
+// ---------------------------------------------------------------------------
+// LocEnc sequence (src/locenc.c:55-85): row 0 the special token when there is
+// one, then in_proj(x) + bias, all F32 (no BF16 here in the reference).
+__global__ void k_locenc_assemble(float *__restrict__ seq, const float *__restrict__ special,
+                                  const float *__restrict__ xh, const float *__restrict__ xb, int H) {
+    const int row = blockIdx.x, off = special ? 1 : 0;
+    float *dst = seq + (int64_t)row * H;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        float v;
+        if (row < off) {
+            v = special[i];
+        } else {
+            v = xh[(int64_t)(row - off) * H + i];
+            if (xb) v = v + xb[i];
+        }
+        dst[i] = v;
+    }
+}
+
+// y = x + b (ggml_add of a bias, F32); also into y2 when non-null.
+__global__ void k_bias_add(const float *__restrict__ x, const float *__restrict__ b, float *__restrict__ y,
+                           float *__restrict__ y2, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float v = x[i];
+    if (b) v = v + b[i];
+    y[i] = v;
+    if (y2) y2[i] = v;
+}
+
+// FSQ core (src/fsq.c:16-29) after the in_proj bias (src/gen_step.c:273-276):
+// v = x + b; y = roundf(tanhf(v) * s) * inv_s with inv_s = 1/s computed on the
+// host in float (ggml_scale by 1.0f / quant_scale); s <= 0: y = v.
+__global__ void k_fsq(const float *__restrict__ x, const float *__restrict__ b, float *__restrict__ y, int64_t n,
+                      float s, float inv_s) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float v = x[i];
+    if (b) v = v + b[i];
+    if (s > 0.0f) v = roundf(tanhf(v) * s) * inv_s;
+    y[i] = v;
+}
+
+static unsigned grid_of(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+int vxm_upload_vec(vxm_ctx *ctx, const float *src, int64_t n, float **out) {
+    *out = nullptr;
+    if (!src) return VXM_OK;
+    if (hipMalloc((void **)out, n * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        *out = nullptr;
+        return vxm_fail(ctx, VXM_ERR_OOM, "vector upload of %lld floats failed", (long long)n);
+    }
+    VXM_HIP(ctx, hipMemcpy(*out, src, n * 4, hipMemcpyHostToDevice));
+    return VXM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// LocEnc
+// ---------------------------------------------------------------------------
+constexpr int kLocEncMaxRows = 4096;
+
+static int locenc_bufs(vxm_locenc *m, int64_t S, int64_t P) {
+    vxm_ctx *ctx = m->ctx;
+    const int64_t H = m->dims.H, feat = m->cfg.feat_dim;
+    const size_t parts[4] = {(size_t)(S * H * 4), (size_t)(P * H * 4), (size_t)(P * feat),
+                             (size_t)(P * (feat / 32) * 2)};
+    size_t total = 0;
+    for (size_t p : parts) total += (p + 255) & ~(size_t)255;
+    if (total > m->buf_bytes) {
+        VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (m->buf) VXM_HIP(ctx, hipFree(m->buf));
+        m->buf = nullptr;
+        m->buf_bytes = 0;
+        if (hipMalloc(&m->buf, total) != hipSuccess) {
+            (void)hipGetLastError();
+            return vxm_fail(ctx, VXM_ERR_OOM, "locenc: buffers of %zu bytes failed", total);
+        }
+        m->buf_bytes = total;
+    }
+    char *b = (char *)m->buf;
+    void **dst[4] = {(void **)&m->seq, (void **)&m->xh, (void **)&m->aq, (void **)&m->ad};
+    for (int i = 0; i < 4; i++) {
+        *dst[i] = b;
+        b += (parts[i] + 255) & ~(size_t)255;
+    }
+    return VXM_OK;
+}
+
+extern "C" int vxm_locenc_free(vxm_locenc *m) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    vxm_ctx *ctx = m->ctx;
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto &b : m->blocks) vxm_block_free(ctx, b);
+    if (m->in_proj) vxm_weight_free(ctx, m->in_proj);
+    for (float *p : {m->in_bias, m->special, m->norm})
+        if (p) (void)hipFree(p);
+    vxm_rope_free(m->dims);
+    vxm_ws_free(m->ws);
+    if (m->buf) (void)hipFree(m->buf);
+    delete m;
+    return VXM_OK;
+}
+
+extern "C" int vxm_locenc_create(vxm_ctx *ctx, const vxm_locenc_config *cfg, const vxm_locenc_weights_q8_0 *w,
+                                 vxm_locenc **out) {
+    if (!ctx || !cfg || !w || !out) return VXM_ERR_INVALID_ARG;
+    *out = nullptr;
+    const vxm_locenc_config &c = *cfg;
+    if (c.n_layers < 0 || c.hidden_size <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 ||
+        c.intermediate_size <= 0 || c.n_heads % c.n_kv_heads || c.head_dim % 2 || c.hidden_size % 32 ||
+        c.intermediate_size % 32 || (c.n_heads * c.head_dim) % 32 || c.head_dim > 256 || c.feat_dim <= 0 ||
+        c.feat_dim % 32 || c.hidden_size > 8192)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "locenc config: unsupported sizes");
+    if (!w->in_proj || !w->norm || (c.n_layers > 0 && !w->layers))
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "locenc weights: in_proj, norm or layers is NULL");
+    vxm_locenc *m = new vxm_locenc();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->cfg.rope_freq_factors = nullptr;
+    vxm_block_dims &d = m->dims;
+    d.H = c.hidden_size;
+    d.nh = c.n_heads;
+    d.nkv = c.n_kv_heads;
+    d.hd = c.head_dim;
+    d.F = c.intermediate_size;
+    d.eps = c.rms_norm_eps;
+    d.no_rope = 0;          // rope on, positions from 0 (src/locenc.c:100-110)
+    d.res_scale = 1.0f;     // no DeepNorm scale for the encoder (src/locenc.c:111)
+    vxm_rope_setup(d, c.rope_theta, c.rope_freq_factors);
+    int rc = VXM_OK;
+    m->blocks.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers && rc == VXM_OK; l++) rc = vxm_block_upload(ctx, d, w->layers[l], m->blocks[l]);
+    if (rc == VXM_OK) rc = vxm_upload_q8_0(ctx, w->in_proj, d.H, c.feat_dim, &m->in_proj);
+    if (rc == VXM_OK) rc = vxm_upload_vec(ctx, w->in_bias, d.H, &m->in_bias);
+    if (rc == VXM_OK) rc = vxm_upload_vec(ctx, w->special_token, d.H, &m->special);
+    if (rc == VXM_OK) rc = vxm_upload_vec(ctx, w->norm, d.H, &m->norm);
+    if (rc != VXM_OK) {
+        vxm_locenc_free(m);
+        return rc;
+    }
+    *out = m;
+    return VXM_OK;
+}
+
+extern "C" int vxm_locenc_forward(vxm_locenc *m, const float *x_dev, int32_t P, float *out_dev) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    vxm_ctx *ctx = m->ctx;
+    const int off = m->special ? 1 : 0;
+    if (!x_dev || !out_dev || P <= 0 || (int64_t)P + off > kLocEncMaxRows)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "locenc: bad x / out / P = %d", P);
+    const vxm_block_dims &d = m->dims;
+    const int64_t H = d.H, S = (int64_t)P + off, qd = (int64_t)d.nh * d.hd, kvd = (int64_t)d.nkv * d.hd;
+    const int var = ctx->quant_variant;
+    int rc;
+    if ((rc = vxm_ws_ensure(ctx, m->ws, S, H, qd, kvd, d.F, (int64_t)d.nkv * S * d.hd))) return rc;
+    if ((rc = vxm_rope_ensure(ctx, m->dims, S))) return rc;
+    if ((rc = locenc_bufs(m, S, P))) return rc;
+    if ((rc = vxm_launch_quantize(ctx, x_dev, P, m->cfg.feat_dim, var, m->aq, m->ad))) return rc;
+    if ((rc = vxm_launch_mul_mat(ctx, m->in_proj, m->aq, m->ad, P, m->xh))) return rc;
+    hipLaunchKernelGGL(k_locenc_assemble, dim3((unsigned)S), dim3(256), 0, ctx->stream, m->seq, m->special, m->xh,
+                       m->in_bias, (int)H);
+    VXM_CHECK_LAUNCH(ctx);
+    // bidirectional blocks over the S fresh rows, positions 0..S-1, no cache
+    const vxm_attn_site site{m->ws.lk, m->ws.lv, (int)S, (int64_t)d.nkv * S * d.hd, (int)S, 0, 0, 0};
+    for (int l = 0; l < m->cfg.n_layers; l++) {
+        const vxm_block &b = m->blocks[l];
+        if ((rc = vxm_launch_rmsnorm(ctx, m->seq, l ? m->ws.dn : nullptr, 1.0f, b.g_in, S, H, d.eps, nullptr,
+                                     m->ws.xq, m->ws.xd, var)))
+            return rc;
+        if ((rc = vxm_block_run(ctx, d, b, m->ws, m->seq, S, site))) return rc;
+    }
+    // last residual + final RMSNorm of the rows that are returned: the
+    // special token's row (src/locenc.c:118-128), or every row
+    const int64_t rows = off ? 1 : S;
+    return vxm_launch_rmsnorm(ctx, m->seq, m->cfg.n_layers ? m->ws.dn : nullptr, 1.0f, m->norm, rows, H, d.eps,
+                              out_dev, nullptr, nullptr, var);
+}
+
+// ---------------------------------------------------------------------------
+// FSQ and the LM update
+// ---------------------------------------------------------------------------
+extern "C" int vxm_fsq_quantize(vxm_ctx *ctx, const float *x_dev, int64_t n, float quant_scale, float *y_dev) {
+    if (!ctx) return VXM_ERR_INVALID_ARG;
+    if (!x_dev || !y_dev || n < 0) return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "fsq_quantize: bad arguments");
+    if (n == 0) return VXM_OK;
+    const float inv = quant_scale > 0.0f ? 1.0f / quant_scale : 0.0f;
+    hipLaunchKernelGGL(k_fsq, dim3(grid_of(n)), dim3(256), 0, ctx->stream, x_dev, (const float *)nullptr, y_dev, n,
+                       quant_scale, inv);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}
+
+extern "C" int vxm_lm_update_free(vxm_lm_update *u) {
+    if (!u) return VXM_ERR_INVALID_ARG;
+    vxm_ctx *ctx = u->ctx;
+    (void)hipStreamSynchronize(ctx->stream);
+    for (vxm_weight *w : {u->enc_to_lm, u->fsq_in, u->fsq_out, u->fusion})
+        if (w) vxm_weight_free(ctx, w);
+    for (float *p : {u->enc_to_lm_bias, u->fsq_in_bias, u->fsq_out_bias})
+        if (p) (void)hipFree(p);
+    if (u->buf) (void)hipFree(u->buf);
+    delete u;
+    return VXM_OK;
+}
+
+extern "C" int vxm_lm_update_create(vxm_ctx *ctx, const vxm_lm_update_config *cfg,
+                                    const vxm_lm_update_weights_q8_0 *w, vxm_locenc *enc, vxm_minicpm4 *tslm,
+                                    vxm_minicpm4 *ralm, vxm_lm_update **out) {
+    if (!ctx || !cfg || !w || !out) return VXM_ERR_INVALID_ARG;
+    *out = nullptr;
+    const vxm_lm_update_config &c = *cfg;
+    if (!enc || !tslm || !ralm || enc->ctx != ctx || tslm->ctx != ctx || ralm->ctx != ctx)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "lm_update: encoder / TSLM / RALM missing or on another context");
+    const bool fsq = w->fsq_in != nullptr;
+    if (c.lm_hidden <= 0 || c.lm_hidden % 32 || c.enc_hidden <= 0 || c.enc_hidden % 32 || c.res_hidden <= 0 ||
+        (fsq && (c.fsq_dim <= 0 || c.fsq_dim % 32)) || c.enc_hidden != enc->dims.H || c.lm_hidden != tslm->dims.H ||
+        c.res_hidden != ralm->dims.H || enc->special == nullptr)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG,
+                        "lm_update config: widths must be multiples of 32 and match the encoder (with a "
+                        "special token), TSLM and RALM");
+    if (!w->enc_to_lm || !w->fusion_concat || (fsq && !w->fsq_out))
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "lm_update weights: a projection is NULL");
+    vxm_lm_update *u = new vxm_lm_update();
+    u->ctx = ctx;
+    u->cfg = c;
+    u->enc = enc;
+    u->tslm = tslm;
+    u->ralm = ralm;
+    u->inv_scale = c.fsq_quant_scale > 0.0f ? 1.0f / c.fsq_quant_scale : 0.0f;
+    const int64_t L = c.lm_hidden, E = c.enc_hidden, Fq = fsq ? c.fsq_dim : 0;
+    int rc = vxm_upload_q8_0(ctx, w->enc_to_lm, L, E, &u->enc_to_lm);
+    if (rc == VXM_OK) rc = vxm_upload_vec(ctx, w->enc_to_lm_bias, L, &u->enc_to_lm_bias);
+    if (rc == VXM_OK && fsq) rc = vxm_upload_q8_0(ctx, w->fsq_in, Fq, L, &u->fsq_in);
+    if (rc == VXM_OK && fsq) rc = vxm_upload_vec(ctx, w->fsq_in_bias, Fq, &u->fsq_in_bias);
+    if (rc == VXM_OK && fsq) rc = vxm_upload_q8_0(ctx, w->fsq_out, L, Fq, &u->fsq_out);
+    if (rc == VXM_OK && fsq) rc = vxm_upload_vec(ctx, w->fsq_out_bias, L, &u->fsq_out_bias);
+    if (rc == VXM_OK) rc = vxm_upload_q8_0(ctx, w->fusion_concat, c.res_hidden, 2 * L, &u->fusion);
+    if (rc == VXM_OK) {
+        const int64_t kq = std::max<int64_t>(std::max<int64_t>(2 * L, E), Fq);
+        const size_t parts[5] = {(size_t)E * 4, (size_t)(2 * L) * 4, (size_t)std::max<int64_t>(Fq, 1) * 4,
+                                 (size_t)kq, (size_t)(kq / 32) * 2};
+        size_t total = 0;
+        for (size_t p : parts) total += (p + 255) & ~(size_t)255;
+        if (hipMalloc(&u->buf, total) != hipSuccess) {
+            (void)hipGetLastError();
+            u->buf = nullptr;
+            rc = vxm_fail(ctx, VXM_ERR_OOM, "lm_update: buffers of %zu bytes failed", total);
+        } else {
+            char *b = (char *)u->buf;
+            void **dst[5] = {(void **)&u->fe, (void **)&u->cat, (void **)&u->fh, (void **)&u->aq, (void **)&u->ad};
+            for (int i = 0; i < 5; i++) {
+                *dst[i] = b;
+                b += (parts[i] + 255) & ~(size_t)255;
+            }
+        }
+    }
+    if (rc != VXM_OK) {
+        vxm_lm_update_free(u);
+        return rc;
+    }
+    *out = u;
+    return VXM_OK;
+}
+
+extern "C" int vxm_lm_update_step(vxm_lm_update *u, vxm_kv_cache *tslm_kv, vxm_kv_cache *ralm_kv,
+                                  const float *prev_patch_dev, int32_t P, int32_t pos, float *audio_embed_dev,
+                                  float *base_hidden_dev, float *fsq_dev, float *ralm_hidden_dev) {
+    if (!u) return VXM_ERR_INVALID_ARG;
+    vxm_ctx *ctx = u->ctx;
+    if (!prev_patch_dev || !base_hidden_dev || !ralm_hidden_dev || !tslm_kv || !ralm_kv || pos < 0)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "lm_update: bad patch / outputs / caches / pos");
+    const int64_t L = u->cfg.lm_hidden, Fq = u->fsq_in ? u->cfg.fsq_dim : 0;
+    const int var = ctx->quant_variant;
+    float *fsq_part = u->cat, *audio_part = u->cat + L;
+    int rc;
+    // audio embedding (src/gen_step.c:208-266)
+    if ((rc = vxm_locenc_forward(u->enc, prev_patch_dev, P, u->fe))) return rc;
+    if ((rc = vxm_launch_quantize(ctx, u->fe, 1, u->cfg.enc_hidden, var, u->aq, u->ad))) return rc;
+    if ((rc = vxm_launch_mul_mat(ctx, u->enc_to_lm, u->aq, u->ad, 1, audio_part))) return rc;
+    hipLaunchKernelGGL(k_bias_add, dim3(grid_of(L)), dim3(256), 0, ctx->stream, audio_part, u->enc_to_lm_bias,
+                       audio_part, base_hidden_dev, L);
+    VXM_CHECK_LAUNCH(ctx);
+    if (audio_embed_dev)
+        VXM_HIP(ctx, hipMemcpyAsync(audio_embed_dev, audio_part, L * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    // TSLM step at pos, in place on base_hidden (src/gen_step.c:741-771)
+    if ((rc = vxm_minicpm4_forward(u->tslm, tslm_kv, base_hidden_dev, 1, pos))) return rc;
+    // FSQ (src/gen_step.c:268-290), or the hidden unchanged without one
+    if (Fq > 0) {
+        if ((rc = vxm_launch_quantize(ctx, base_hidden_dev, 1, L, var, u->aq, u->ad))) return rc;
+        if ((rc = vxm_launch_mul_mat(ctx, u->fsq_in, u->aq, u->ad, 1, u->fh))) return rc;
+        hipLaunchKernelGGL(k_fsq, dim3(grid_of(Fq)), dim3(256), 0, ctx->stream, u->fh, u->fsq_in_bias, u->fh, Fq,
+                           u->cfg.fsq_quant_scale, u->inv_scale);
+        VXM_CHECK_LAUNCH(ctx);
+        if ((rc = vxm_launch_quantize(ctx, u->fh, 1, Fq, var, u->aq, u->ad))) return rc;
+        if ((rc = vxm_launch_mul_mat(ctx, u->fsq_out, u->aq, u->ad, 1, fsq_part))) return rc;
+        hipLaunchKernelGGL(k_bias_add, dim3(grid_of(L)), dim3(256), 0, ctx->stream, fsq_part, u->fsq_out_bias,
+                           fsq_part, fsq_dev, L);
+        VXM_CHECK_LAUNCH(ctx);
+    } else {
+        VXM_HIP(ctx, hipMemcpyAsync(fsq_part, base_hidden_dev, L * 4, hipMemcpyDeviceToDevice, ctx->stream));
+        if (fsq_dev)
+            VXM_HIP(ctx, hipMemcpyAsync(fsq_dev, base_hidden_dev, L * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    }
+    // RALM input = fusion_concat_proj([fsq ; audio_embed]) (src/gen_step.c:870-899), then the RALM step
+    if ((rc = vxm_launch_quantize(ctx, u->cat, 1, 2 * L, var, u->aq, u->ad))) return rc;
+    if ((rc = vxm_launch_mul_mat(ctx, u->fusion, u->aq, u->ad, 1, ralm_hidden_dev))) return rc;
+    return vxm_minicpm4_forward(u->ralm, ralm_kv, ralm_hidden_dev, 1, pos);
+}

@@ -85,5 +85,7 @@ void vxm_block_free(vxm_ctx *ctx, vxm_block &b);
 void vxm_rope_setup(vxm_block_dims &d, int32_t theta, const float *ff_host);
 int vxm_rope_ensure(vxm_ctx *ctx, vxm_block_dims &d, int64_t n_pos);
 void vxm_rope_free(vxm_block_dims &d);
+// F32 host vector -> new device buffer (nullptr in, nullptr out)
+int vxm_upload_vec(vxm_ctx *ctx, const float *src, int64_t n, float **out);
 int vxm_block_run(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_block &b, vxm_workspace &ws, float *x,
                   int64_t M, const vxm_attn_site &site);

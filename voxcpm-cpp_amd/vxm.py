@@ -95,6 +95,13 @@ _SIGS = {
     "vxm_host_cfm_t": (_F, [C.c_int32, C.c_int32, C.c_int32]),
     "vxm_host_cfm_zero_star_steps": (C.c_int32, [C.c_int32]),
     "vxm_host_rope_cache": (_I, [_F, C.c_int32, _P, C.c_int32, C.c_int32, _P]),
+    "vxm_locenc_create": (_I, [_P, _P, _P, C.POINTER(_P)]),
+    "vxm_locenc_free": (_I, [_P]),
+    "vxm_locenc_forward": (_I, [_P, _P, C.c_int32, _P]),
+    "vxm_fsq_quantize": (_I, [_P, _P, _I64, _F, _P]),
+    "vxm_lm_update_create": (_I, [_P, _P, _P, _P, _P, _P, C.POINTER(_P)]),
+    "vxm_lm_update_free": (_I, [_P]),
+    "vxm_lm_update_step": (_I, [_P, _P, _P, _P, C.c_int32, C.c_int32, _P, _P, _P, _P]),
 }
 
 CFM_SWAY = 0
@@ -234,6 +241,15 @@ class Context:
             xd = torch.empty((rows, n // 32), dtype=torch.int16, device=x.device)
         self.check(lib().vxm_rms_norm(self.h, _ptr(x), _ptr(gain), rows, n, eps, _ptr(y), _ptr(xq), _ptr(xd)))
         return (y, xq, xd) if quantize else y
+
+    def fsq_quantize(self, x, quant_scale, y=None):
+        """vcpm_fsq_quantize on a device tensor: round(tanh(x) * s) / s."""
+        import torch
+
+        if y is None:
+            y = torch.empty_like(x)
+        self.check(lib().vxm_fsq_quantize(self.h, _ptr(x), x.numel(), quant_scale, _ptr(y)))
+        return y
 
     def block_dots(self, w, xq, xd):
         import torch
@@ -531,3 +547,151 @@ def host_rope_cache(base, head_dim, ff, pos0, n_pos):
     if rc:
         raise VxmError(rc, "vxm_host_rope_cache")
     return out
+
+
+class LocEncConfig(C.Structure):
+    """Mirror of vxm_locenc_config (vcpm_locenc_config, src/locenc.h:49-60)."""
+
+    _fields_ = [
+        ("hidden_size", C.c_int32), ("n_layers", C.c_int32), ("n_heads", C.c_int32),
+        ("n_kv_heads", C.c_int32), ("intermediate_size", C.c_int32), ("head_dim", C.c_int32),
+        ("feat_dim", C.c_int32), ("rms_norm_eps", C.c_float), ("rope_theta", C.c_int32),
+        ("rope_freq_factors", C.c_void_p),
+    ]
+
+
+LOCENC_TENSORS = ("in_proj", "in_bias", "special_token", "norm")
+
+
+class LocEncWeightsQ8(C.Structure):
+    """Mirror of vxm_locenc_weights_q8_0 (vcpm_locenc_weights, src/locenc.h:67-73)."""
+
+    _fields_ = [("layers", C.c_void_p)] + [(n, C.c_void_p) for n in LOCENC_TENSORS]
+
+
+def _layer_array(layers, keep):
+    import numpy as np
+
+    arr = (LayerWeightsQ8 * max(1, len(layers)))()
+    names = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj",
+             "input_layernorm", "post_attention_layernorm")
+    for i, lw in enumerate(layers):
+        for n in names:
+            a = np.ascontiguousarray(lw[n])
+            keep.append(a)
+            setattr(arr[i], n, a.ctypes.data)
+    keep.append(arr)
+    return C.cast(arr, C.c_void_p).value
+
+
+class LocEnc:
+    """vcpm_locenc (the feature encoder) on the device.
+
+    ``weights``: in_proj GGUF Q8_0 rows [hidden][feat], F32 in_bias / special_token /
+    norm (in_bias and special_token may be None) and ``layers`` (MiniCPM4 block dicts)."""
+
+    def __init__(self, ctx, cfg: dict, weights: dict):
+        import numpy as np
+
+        self.ctx = ctx
+        keep = []
+        ff = cfg.get("rope_freq_factors")
+        if ff is not None:
+            ff = np.ascontiguousarray(ff, dtype=np.float32)
+            keep.append(ff)
+        c = LocEncConfig(cfg["hidden_size"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"],
+                         cfg["intermediate_size"], cfg["head_dim"], cfg["feat_dim"], cfg.get("rms_norm_eps", 1e-6),
+                         int(cfg.get("rope_theta", 10000)), None if ff is None else ff.ctypes.data)
+        self.cfg = cfg
+        self.has_special = weights.get("special_token") is not None
+        w = LocEncWeightsQ8()
+        w.layers = _layer_array(weights.get("layers", []), keep)
+        for n in LOCENC_TENSORS:
+            v = weights.get(n)
+            if v is not None:
+                a = np.ascontiguousarray(v)
+                keep.append(a)
+                setattr(w, n, a.ctypes.data)
+        h = C.c_void_p()
+        ctx.check(lib().vxm_locenc_create(ctx.h, C.byref(c), C.byref(w), C.byref(h)))
+        self.h = h
+
+    def forward(self, x, out=None):
+        """x [P][feat] device tensor -> [hidden] (special-token row) or [P][hidden]."""
+        import torch
+
+        P, H = x.shape[0], self.cfg["hidden_size"]
+        if out is None:
+            shape = (H,) if self.has_special else (P, H)
+            out = torch.empty(shape, dtype=torch.float32, device=x.device)
+        self.ctx.check(lib().vxm_locenc_forward(self.h, _ptr(x), P, _ptr(out)))
+        return out
+
+    def free(self):
+        if self.h:
+            self.ctx.check(lib().vxm_locenc_free(self.h))
+            self.h = None
+
+
+class LMUpdateConfig(C.Structure):
+    """Mirror of vxm_lm_update_config."""
+
+    _fields_ = [("lm_hidden", C.c_int32), ("enc_hidden", C.c_int32), ("fsq_dim", C.c_int32),
+                ("res_hidden", C.c_int32), ("fsq_quant_scale", C.c_float)]
+
+
+LM_UPDATE_TENSORS = ("enc_to_lm", "enc_to_lm_bias", "fsq_in", "fsq_in_bias", "fsq_out", "fsq_out_bias",
+                     "fusion_concat")
+
+
+class LMUpdateWeightsQ8(C.Structure):
+    """Mirror of vxm_lm_update_weights_q8_0."""
+
+    _fields_ = [(n, C.c_void_p) for n in LM_UPDATE_TENSORS]
+
+
+class LMUpdate:
+    """gen_lm_update on the device: LocEnc -> enc_to_lm -> TSLM step -> FSQ -> fusion -> RALM step.
+    Borrows enc / tslm / ralm (keeps Python references to them)."""
+
+    def __init__(self, ctx, cfg: dict, weights: dict, enc, tslm, ralm):
+        import numpy as np
+
+        self.ctx, self.cfg = ctx, cfg
+        self._owners = (enc, tslm, ralm)
+        keep = []
+        w = LMUpdateWeightsQ8()
+        for n in LM_UPDATE_TENSORS:
+            v = weights.get(n)
+            if v is not None:
+                a = np.ascontiguousarray(v)
+                keep.append(a)
+                setattr(w, n, a.ctypes.data)
+        c = LMUpdateConfig(cfg["lm_hidden"], cfg["enc_hidden"], cfg.get("fsq_dim", 0), cfg["res_hidden"],
+                           cfg.get("fsq_quant_scale", 9.0))
+        h = C.c_void_p()
+        ctx.check(lib().vxm_lm_update_create(ctx.h, C.byref(c), C.byref(w), enc.h, tslm.h, ralm.h, C.byref(h)))
+        self.h = h
+
+    def step(self, tslm_kv, ralm_kv, prev_patch, pos, audio_embed=None, base_hidden=None, fsq=None,
+             ralm_hidden=None):
+        """Returns (audio_embed, base_hidden, fsq, ralm_hidden) device tensors."""
+        import torch
+
+        dev = prev_patch.device
+        L, R = self.cfg["lm_hidden"], self.cfg["res_hidden"]
+
+        def new(t, n):
+            return torch.empty(n, dtype=torch.float32, device=dev) if t is None else t
+
+        audio_embed, base_hidden, fsq, ralm_hidden = (new(audio_embed, L), new(base_hidden, L), new(fsq, L),
+                                                      new(ralm_hidden, R))
+        self.ctx.check(lib().vxm_lm_update_step(self.h, tslm_kv.h, ralm_kv.h, _ptr(prev_patch), prev_patch.shape[0],
+                                                pos, _ptr(audio_embed), _ptr(base_hidden), _ptr(fsq),
+                                                _ptr(ralm_hidden)))
+        return audio_embed, base_hidden, fsq, ralm_hidden
+
+    def free(self):
+        if self.h:
+            self.ctx.check(lib().vxm_lm_update_free(self.h))
+            self.h = None
