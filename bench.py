@@ -7,8 +7,10 @@ stack (hidden 2048, 16 q / 2 kv heads of 128, SwiGLU 6144, Q8_0 weights
 beyond the 256 MB Infinity Cache).  `value` is the algorithmic weight + KV
 bytes of a step over its time (GB/s); the line also carries us per step, the
 isolated Q8_0 GEMV (6144x2048 and 2048x6144 over 64 rotated copies), one
-decoder layer step at context 512, the roofline of the dominant kernel and
-the host-CPU baseline (the oracle's SIMD restatement of ggml's CPU path).
+decoder layer step at context 512, the 512-token prefill, the CFM solve, the
+per-token LM update (LocEnc + TSLM + FSQ + RALM), the roofline of the
+dominant kernel and the host-CPU baseline (the oracle's SIMD restatement of
+ggml's CPU path).
 
 --gpus above 1 is refused: this build runs on one GPU.
 """
@@ -65,9 +67,9 @@ def step_bytes(ctx_len, n_layers=L):
     return n_layers * (layer_weight_bytes() + 2 * H * 4 + kv_read)
 
 
-def make_layers(vxm, seed, n_layers):
+def make_layers(vxm, seed, n_layers, hidden=H, nh=NH, nkv=NKV, hd=HD, ffn=F):
     """Seeded synthetic Q8_0 layers (GGUF rows) and gains."""
-    qd, kvd = NH * HD, NKV * HD
+    H, qd, kvd, F = hidden, nh * hd, nkv * hd, ffn
     shapes = [("q_proj", qd, H), ("k_proj", kvd, H), ("v_proj", kvd, H), ("o_proj", H, qd),
               ("gate_proj", F, H), ("up_proj", F, H), ("down_proj", H, F)]
     per_layer = sum(n * k for _, n, k in shapes) + 2 * H
@@ -296,6 +298,80 @@ def bench_cfm(ctx, torch, vxm, reps, n_steps=10):
     return ms * 1000.0 / reps, evals, ok
 
 
+# the per-token LM update: LocEnc (hidden 1024, 12 bidirectional blocks, 16 / 2 heads x 128, FFN 4096,
+# one 4-position latent patch + the special token), the TSLM above, an 8-layer RALM of the same block
+# shape without rope, FSQ 2048 -> 512 -> 2048 and the fusion projection 4096 -> 2048
+ENC = dict(H=1024, L=12, NH=16, NKV=2, HD=128, F=4096, FEAT=64, P=4)
+RALM_L, FSQ_DIM = 8, 512
+
+
+def lm_update_bytes(ctx_len):
+    """Algorithmic HBM bytes of one LM update: every weight once, gains, both LMs' KV read + append."""
+    e = ENC
+    qd, kvd = e["NH"] * e["HD"], e["NKV"] * e["HD"]
+    enc_blk = (q8_bytes(qd, e["H"]) + 2 * q8_bytes(kvd, e["H"]) + q8_bytes(e["H"], qd) + 2 * q8_bytes(e["F"], e["H"])
+               + q8_bytes(e["H"], e["F"]) + 2 * e["H"] * 4)
+    proj = (q8_bytes(e["H"], e["FEAT"]) + q8_bytes(H, e["H"]) + q8_bytes(FSQ_DIM, H) + q8_bytes(H, FSQ_DIM)
+            + q8_bytes(H, 2 * H))
+    return step_bytes(ctx_len) + step_bytes(ctx_len, RALM_L) + e["L"] * enc_blk + proj
+
+
+def bench_lm_update(ctx, torch, vxm, tslm_layers, ctx0, steps, warmup):
+    """gen_lm_update per generated patch: LocEnc + enc_to_lm, the 28-layer TSLM step, FSQ, the fusion
+    projection and the 8-layer RALM step, one stream-ordered call per token."""
+    e = ENC
+    enc_layers = make_layers(vxm, 31, e["L"], e["H"], e["NH"], e["NKV"], e["HD"], e["F"])
+    ralm_layers = make_layers(vxm, 32, RALM_L)
+    off = [0]
+
+    def q8(n, k):
+        w = vxm.host_randn(33, n * k, 0.0, 0.02, offset=off[0]).reshape(n, k)
+        off[0] += n * k
+        return vxm.host_quantize_q8_0(w)
+
+    def vec(n, mean=0.0, std=0.02):
+        v = vxm.host_randn(33, n, mean, std, offset=off[0])
+        off[0] += n
+        return v
+
+    enc = vxm.LocEnc(ctx, dict(hidden_size=e["H"], n_layers=e["L"], n_heads=e["NH"], n_kv_heads=e["NKV"],
+                               head_dim=e["HD"], intermediate_size=e["F"], feat_dim=e["FEAT"], rms_norm_eps=1e-6,
+                               rope_theta=10000),
+                     dict(layers=enc_layers, in_proj=q8(e["H"], e["FEAT"]), in_bias=vec(e["H"]),
+                          special_token=vec(e["H"], 0.0, 1.0), norm=vec(e["H"], 1.0)))
+    cfg = dict(hidden_size=H, n_layers=L, n_heads=NH, n_kv_heads=NKV, head_dim=HD, intermediate_size=F,
+               rms_norm_eps=1e-6, rope_theta=10000)
+    tslm = vxm.MiniCPM4(ctx, cfg, tslm_layers, final_norm=vec(H, 1.0))
+    ralm = vxm.MiniCPM4(ctx, dict(cfg, n_layers=RALM_L, no_rope=1), ralm_layers, final_norm=vec(H, 1.0))
+    pw = dict(enc_to_lm=q8(H, e["H"]), enc_to_lm_bias=vec(H), fsq_in=q8(FSQ_DIM, H), fsq_in_bias=vec(FSQ_DIM),
+              fsq_out=q8(H, FSQ_DIM), fsq_out_bias=vec(H), fusion_concat=q8(H, 2 * H))
+    u = vxm.LMUpdate(ctx, dict(lm_hidden=H, enc_hidden=e["H"], fsq_dim=FSQ_DIM, res_hidden=H, fsq_quant_scale=9.0),
+                     pw, enc, tslm, ralm)
+    tkv = vxm.KVCache(ctx, L, NKV, HD, 1024)
+    rkv = vxm.KVCache(ctx, RALM_L, NKV, HD, 1024)
+    kv_prefill(vxm, tkv, L, ctx0, 5)
+    kv_prefill(vxm, rkv, RALM_L, ctx0, 6)
+    patch = torch.from_numpy(vxm.host_randn(34, e["P"] * e["FEAT"]).reshape(e["P"], e["FEAT"])).to("cuda:0")
+    outs = [torch.empty(H, dtype=torch.float32, device="cuda:0") for _ in range(4)]
+    for i in range(warmup):
+        u.step(tkv, rkv, patch, ctx0 + i, *outs)
+    ctx.sync()
+    tkv.set_used(ctx0)
+    rkv.set_used(ctx0)
+    t = Timer(torch, ctx)
+    t.start()
+    for i in range(steps):
+        u.step(tkv, rkv, patch, ctx0 + i, *outs)
+    ms = t.stop_ms()
+    tslm.check()
+    ralm.check()
+    ok = all(bool(torch.isfinite(o).all().item()) for o in outs)
+    u.free()
+    for o in (enc, tslm, ralm, tkv, rkv):
+        o.free()
+    return ms * 1000.0 / steps, ok
+
+
 def cpu_baseline(vxm, layers, n_layers, ctx0, tokens, threads):
     """The oracle's SIMD restatement of ggml's CPU Q8_0 decode (1 copy of weights)."""
     import ctypes as C
@@ -441,6 +517,15 @@ def main():
     gbs = sb / (us_step * 1e-6) / 1e9
     log(f"28-layer decode step: {us_step:.1f} us/token, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM), "
         f"finite={finite}")
+    lmu = None
+    if not args.decode_only:
+        us_u, fin_u = bench_lm_update(ctx, torch, vxm, layers, 256, args.steps, args.warmup)
+        ub = lm_update_bytes(mean_ctx)
+        lmu = {"us_per_update": round(us_u, 1), "bytes": int(ub), "GBs": round(ub / (us_u * 1e-6) / 1e9, 1),
+               "hbm_frac": round(ub / (us_u * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "finite": fin_u,
+               "note": f"LocEnc 12 x hidden 1024 on a 4-position patch + 28-layer TSLM step + FSQ 512 + fusion + "
+                       f"{RALM_L}-layer RALM step, ctx 256->{256 + args.steps}, one call per token, no host sync"}
+        log(f"lm update (LocEnc + TSLM + FSQ + RALM): {us_u:.1f} us/token, {lmu['GBs']} GB/s, finite={fin_u}")
     ctx.close()
 
     cpu = None
@@ -491,6 +576,7 @@ def main():
         "layer_decode_ctx512_us": round(us1, 3) if us1 is not None else None,
         "prefill": pre,
         "cfm": cfm,
+        "lm_update": lmu,
         "roofline": roof,
         "cpu_baseline": cpu,
     }
