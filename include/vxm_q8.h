@@ -324,6 +324,66 @@ int vxm_lm_update_step(vxm_lm_update *u, vxm_kv_cache *tslm_kv, vxm_kv_cache *ra
                        const float *prev_patch_dev, int32_t P, int32_t pos, float *audio_embed_dev,
                        float *base_hidden_dev, float *fsq_dev, float *ralm_hidden_dev);
 
+/* ---- GGUF reader (host only) ----------------------------------------------
+ * A read-only, memory-mapped GGUF v2/v3 file: tensor directory, key/value
+ * metadata and tensor bytes in place.  Stands in for ggml's
+ * gguf_init_from_file as vcpm_model_load uses it (src/model_loader.c:101-120)
+ * for the tensors of this path; the tensor bytes of a Q8_0 tensor are exactly
+ * the GGUF rows vxm_upload_q8_0 and the *_weights_q8_0 structs take. */
+typedef struct vxm_gguf vxm_gguf;
+
+/* ggml type ids of the tensors this path reads */
+#define VXM_GGML_F32 0
+#define VXM_GGML_F16 1
+#define VXM_GGML_Q8_0 8
+#define VXM_GGML_BF16 30
+
+typedef struct vxm_gguf_tensor_info {
+    const char *name;        /* valid while the file is open */
+    int32_t     type;        /* ggml type id */
+    int32_t     n_dims;
+    int64_t     ne[4];       /* ne[0] = row length; unused dims are 1 */
+    int64_t     n_elements;
+    uint64_t    offset;      /* from the start of the data section */
+    const void *data;        /* bytes in the mapping */
+    uint64_t    nbytes;      /* 0 for a type whose size the reader does not know */
+} vxm_gguf_tensor_info;
+
+/* Opens and validates path (magic, version 2 or 3, every tensor inside the
+ * file and aligned to general.alignment).  Errors: VXM_ERR_IO (unreadable),
+ * VXM_ERR_MODEL_FORMAT (not a valid GGUF); err (may be NULL) gets the reason. */
+int vxm_gguf_open(const char *path, vxm_gguf **out, char *err, size_t err_size);
+int vxm_gguf_close(vxm_gguf *g);
+const char *vxm_gguf_last_error(const vxm_gguf *g);
+int32_t vxm_gguf_version(const vxm_gguf *g);
+int64_t vxm_gguf_n_tensors(const vxm_gguf *g);
+/* index of a tensor by name (vcpm_model_get_tensor), -1 if absent */
+int64_t vxm_gguf_find_tensor(const vxm_gguf *g, const char *name);
+int vxm_gguf_tensor(const vxm_gguf *g, int64_t idx, vxm_gguf_tensor_info *out);
+/* Metadata with defaults, as get_key_i32 / get_key_f32 / get_key_str
+ * (src/model_loader.c:20-41).  Integer keys of any width and bool keys read
+ * as int; float keys also accept F64 and integers. */
+int32_t vxm_gguf_get_i32(const vxm_gguf *g, const char *key, int32_t def);
+float vxm_gguf_get_f32(const vxm_gguf *g, const char *key, float def);
+const char *vxm_gguf_get_str(const vxm_gguf *g, const char *key, const char *def);
+/* F32 copy of an F32 / F16 / BF16 / Q8_0 tensor of n elements, as
+ * vcpm_model_ensure_f32 makes for norms, biases and special tokens
+ * (src/model_loader.c:254-352): Q8_0 values are (float)qs * fp32(d). */
+int vxm_gguf_tensor_f32(const vxm_gguf *g, int64_t idx, float *out, int64_t n);
+/* The nine tensors of block `layer` named as fill_minicpm4_weights does
+ * (src/gen_init.c:34-67): "<prefix>.<layer>.self_attn.q_proj.weight", ...
+ * with prefix "base_lm.blk", "residual_lm.blk", "feat_encoder.blk" or
+ * "feat_decoder.estimator.blk".  The seven projections (2-D Q8_0) point into
+ * the mapping; the two norms are written as F32 to norms[2 * hidden]. */
+int vxm_gguf_layer_q8_0(vxm_gguf *g, const char *prefix, int32_t layer, int64_t hidden, float *norms,
+                        vxm_layer_weights_q8_0 *out);
+/* The TSLM (residual = 0) or RALM (residual = 1) config from the voxcpm.*
+ * keys with vcpm_model_config_default's defaults and vcpm_model_load's
+ * sanitisation (src/model_loader.c:52-97,139-219): eps below 1e-7 becomes
+ * 1e-5, scale_depth is 0 unless voxcpm.use_mup.  VXM_ERR_UNSUPPORTED_ARCH
+ * unless general.architecture is "voxcpm2". */
+int vxm_gguf_minicpm4_config(vxm_gguf *g, int32_t residual, vxm_minicpm4_config *cfg);
+
 /* ---- host helpers (no device work) --------------------------------------
  * GGUF Q8_0 quantization of F32 rows with the weight rule of
  * ggml_quantize_chunk (tools/quantize.c:292): d = amax/127 (fp16),

@@ -102,6 +102,19 @@ _SIGS = {
     "vxm_lm_update_create": (_I, [_P, _P, _P, _P, _P, _P, C.POINTER(_P)]),
     "vxm_lm_update_free": (_I, [_P]),
     "vxm_lm_update_step": (_I, [_P, _P, _P, _P, C.c_int32, C.c_int32, _P, _P, _P, _P]),
+    "vxm_gguf_open": (_I, [C.c_char_p, C.POINTER(_P), C.c_char_p, C.c_size_t]),
+    "vxm_gguf_close": (_I, [_P]),
+    "vxm_gguf_last_error": (C.c_char_p, [_P]),
+    "vxm_gguf_version": (C.c_int32, [_P]),
+    "vxm_gguf_n_tensors": (_I64, [_P]),
+    "vxm_gguf_find_tensor": (_I64, [_P, C.c_char_p]),
+    "vxm_gguf_tensor": (_I, [_P, _I64, _P]),
+    "vxm_gguf_get_i32": (C.c_int32, [_P, C.c_char_p, C.c_int32]),
+    "vxm_gguf_get_f32": (_F, [_P, C.c_char_p, _F]),
+    "vxm_gguf_get_str": (C.c_char_p, [_P, C.c_char_p, C.c_char_p]),
+    "vxm_gguf_tensor_f32": (_I, [_P, _I64, _P, _I64]),
+    "vxm_gguf_layer_q8_0": (_I, [_P, C.c_char_p, C.c_int32, _I64, _P, _P]),
+    "vxm_gguf_minicpm4_config": (_I, [_P, C.c_int32, _P]),
 }
 
 CFM_SWAY = 0
@@ -351,6 +364,9 @@ class MiniCPM4:
         names = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj",
                  "input_layernorm", "post_attention_layernorm")
         for i, lw in enumerate(layers):
+            if isinstance(lw, LayerWeightsQ8):   # pointers already set (e.g. into a GGUF mapping)
+                arr[i] = lw
+                continue
             for n in names:
                 a = np.ascontiguousarray(lw[n])
                 self._keep.append(a)
@@ -695,3 +711,104 @@ class LMUpdate:
         if self.h:
             self.ctx.check(lib().vxm_lm_update_free(self.h))
             self.h = None
+
+
+GGML_F32, GGML_F16, GGML_Q8_0, GGML_BF16 = 0, 1, 8, 30
+
+
+class GGUFTensorInfo(C.Structure):
+    """Mirror of vxm_gguf_tensor_info."""
+
+    _fields_ = [("name", C.c_char_p), ("type", C.c_int32), ("n_dims", C.c_int32), ("ne", C.c_int64 * 4),
+                ("n_elements", C.c_int64), ("offset", C.c_uint64), ("data", C.c_void_p), ("nbytes", C.c_uint64)]
+
+
+class GGUF:
+    """A memory-mapped GGUF file (host only): tensors by name as numpy views, metadata getters, F32
+    copies and per-block Q8_0 weights as the reference names them."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        err = C.create_string_buffer(512)
+        rc = lib().vxm_gguf_open(str(path).encode(), C.byref(h), err, len(err))
+        if rc:
+            raise VxmError(rc, err.value.decode())
+        self.h = h
+        self._norms = []
+
+    def close(self):
+        if self.h:
+            lib().vxm_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _check(self, rc):
+        if rc:
+            raise VxmError(rc, (lib().vxm_gguf_last_error(self.h) or b"").decode())
+
+    @property
+    def version(self):
+        return lib().vxm_gguf_version(self.h)
+
+    def __len__(self):
+        return lib().vxm_gguf_n_tensors(self.h)
+
+    def find(self, name):
+        return lib().vxm_gguf_find_tensor(self.h, name.encode())
+
+    def info(self, idx_or_name):
+        idx = self.find(idx_or_name) if isinstance(idx_or_name, str) else idx_or_name
+        if idx < 0:
+            raise KeyError(idx_or_name)
+        ti = GGUFTensorInfo()
+        self._check(lib().vxm_gguf_tensor(self.h, idx, C.byref(ti)))
+        return ti
+
+    def raw(self, name):
+        """The tensor's bytes (a copy) as uint8."""
+        import numpy as np
+
+        ti = self.info(name)
+        return np.ctypeslib.as_array((C.c_uint8 * ti.nbytes).from_address(ti.data)).copy()
+
+    def f32(self, name):
+        import numpy as np
+
+        idx = self.find(name)
+        if idx < 0:
+            raise KeyError(name)
+        ti = self.info(idx)
+        out = np.empty(ti.n_elements, dtype=np.float32)
+        self._check(lib().vxm_gguf_tensor_f32(self.h, idx, out.ctypes.data_as(C.c_void_p), out.size))
+        return out
+
+    def get_i32(self, key, default=0):
+        return lib().vxm_gguf_get_i32(self.h, key.encode(), default)
+
+    def get_f32(self, key, default=0.0):
+        return lib().vxm_gguf_get_f32(self.h, key.encode(), default)
+
+    def get_str(self, key, default=None):
+        v = lib().vxm_gguf_get_str(self.h, key.encode(), None if default is None else default.encode())
+        return None if v is None else v.decode()
+
+    def layer_q8_0(self, prefix, layer, hidden):
+        """LayerWeightsQ8 pointing into the mapping; the F32 norms live as long as this object."""
+        import numpy as np
+
+        norms = np.empty(2 * hidden, dtype=np.float32)
+        self._norms.append(norms)
+        w = LayerWeightsQ8()
+        self._check(lib().vxm_gguf_layer_q8_0(self.h, prefix.encode(), layer, hidden,
+                                              norms.ctypes.data_as(C.c_void_p), C.byref(w)))
+        return w
+
+    def minicpm4_config(self, residual=False):
+        c = MiniCPM4Config()
+        self._check(lib().vxm_gguf_minicpm4_config(self.h, int(residual), C.byref(c)))
+        return {f: getattr(c, f) for f, _ in MiniCPM4Config._fields_}
