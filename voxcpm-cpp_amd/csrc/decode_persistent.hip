@@ -567,24 +567,43 @@ __device__ __forceinline__ void ring_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Weight addresses of slot s of layer l for compute wave ci (the zero
+// The four weight streams of one layer (quants and scales of QKV, O,
+// gate/up, down), read from the table once per layer and then held in
+// registers: the DMA statement clobbers memory, so an address derived from a
+// table load inside the ring would be re-fetched (and waited for) before
+// every unit's DMAs.  valid = 0 past the last layer.
+struct UnitBases {
+    const int8_t *q[4];
+    const uint16_t *d[4];
+    int valid;
+};
+
+__device__ __forceinline__ UnitBases unit_bases(const vxm_pparams &p, int l) {
+    UnitBases b{};
+    b.valid = l < p.n_layers;
+    if (b.valid) {
+        vxm_ptab Ly = layer_at(p, l);
+        b.q[0] = Ly->qkv_qs; b.q[1] = Ly->o_qs; b.q[2] = Ly->gu_qs; b.q[3] = Ly->d_qs;
+        b.d[0] = Ly->qkv_d;  b.d[1] = Ly->o_d;  b.d[2] = Ly->gu_d;  b.d[3] = Ly->d_d;
+    }
+    return b;
+}
+
+// Weight addresses of slot s for compute wave ci in the layer of B (the zero
 // buffers past the last layer or for a unit the wave does not own, so every
 // wave issues the same count of loads).
 template <class S, int s>
-__device__ __forceinline__ void unit_addr(const vxm_pparams &p, int l, int wg, int ci, const int8_t *&q,
-                                          const uint16_t *&d) {
+__device__ __forceinline__ void unit_addr(const vxm_pparams &p, const UnitBases &B, int wg, int ci,
+                                          const int8_t *&q, const uint16_t *&d) {
     using T = Slot<S, s>;
     const int u = ci + kCW * T::k;
     q = p.dummy_q;
     d = p.dummy_d;
-    if (u < T::U && l < p.n_layers) {
-        vxm_ptab Ly = layer_at(p, l);
+    if (u < T::U && B.valid) {
         const int row = wg * T::R + u / T::C, c = u % T::C;
         constexpr int K = T::C * kUnit;
-        const int8_t *bq = T::ph == 0 ? Ly->qkv_qs : T::ph == 1 ? Ly->o_qs : T::ph == 2 ? Ly->gu_qs : Ly->d_qs;
-        const uint16_t *bd = T::ph == 0 ? Ly->qkv_d : T::ph == 1 ? Ly->o_d : T::ph == 2 ? Ly->gu_d : Ly->d_d;
-        q = bq + (int64_t)row * K + c * kUnit;
-        d = bd + (int64_t)row * (K / 32) + c * (kUnit / 32);
+        q = B.q[T::ph] + (int64_t)row * K + c * kUnit;
+        d = B.d[T::ph] + (int64_t)row * (K / 32) + c * (kUnit / 32);
     }
 }
 
@@ -594,19 +613,20 @@ __device__ __forceinline__ int ring_slot(int l) {
     return __builtin_amdgcn_readfirstlane((l * S::NS + s) % S::RING);
 }
 
-// Issue the DMAs of slot s of layer l into its ring slot.
+// Issue the DMAs of slot s of layer l (weights of B) into its ring slot.
 template <class S, int s>
-__device__ __forceinline__ void ring_issue(const vxm_pparams &p, uint32_t ring_lds, int l, int wg, int ci, int lane) {
+__device__ __forceinline__ void ring_issue(const vxm_pparams &p, const UnitBases &B, uint32_t ring_lds, int l, int wg,
+                                           int ci, int lane) {
     const int8_t *q;
     const uint16_t *d;
-    unit_addr<S, s>(p, l, wg, ci, q, d);
+    unit_addr<S, s>(p, B, wg, ci, q, d);
     dma_unit(ring_lds + ring_slot<S, s>(l) * kSlot, q, d, lane);
 }
 
 template <class S, int... ss>
-__device__ __forceinline__ void ring_prime(const vxm_pparams &p, uint32_t ring_lds, int wg, int ci, int lane,
-                                           std::integer_sequence<int, ss...>) {
-    (ring_issue<S, ss>(p, ring_lds, 0, wg, ci, lane), ...);
+__device__ __forceinline__ void ring_prime(const vxm_pparams &p, const UnitBases &B0, uint32_t ring_lds, int wg,
+                                           int ci, int lane, std::integer_sequence<int, ss...>) {
+    (ring_issue<S, ss>(p, B0, ring_lds, 0, wg, ci, lane), ...);
 }
 
 // Consume the K slots of one phase starting at slot OFF: dot product of each
@@ -632,8 +652,9 @@ __device__ __forceinline__ float unit_dot(const int8_t *ring, int l, int ci, int
 }
 
 template <class S, int OFF, int K, int k = 0>
-__device__ __forceinline__ void ring_phase(const vxm_pparams &p, const int8_t *ring, uint32_t ring_lds, int l, int wg,
-                                           int ci, int lane, const int8_t *xq, const float *xd, float *part) {
+__device__ __forceinline__ void ring_phase(const vxm_pparams &p, const UnitBases &cur, const UnitBases &nxt,
+                                           const int8_t *ring, uint32_t ring_lds, int l, int wg, int ci, int lane,
+                                           const int8_t *xq, const float *xd, float *part) {
     if constexpr (k + 1 < K) {
         constexpr int s = OFF + k;
         using T0 = Slot<S, s>;
@@ -648,9 +669,11 @@ __device__ __forceinline__ void ring_phase(const vxm_pparams &p, const int8_t *r
             if (u1 < T1::U) part[u1] = b;
         }
         constexpr int sn0 = (s + S::P) % S::NS, sn1 = (s + 1 + S::P) % S::NS;
-        ring_issue<S, sn0>(p, ring_lds, l + (s + S::P >= S::NS ? 1 : 0), wg, ci, lane);
-        ring_issue<S, sn1>(p, ring_lds, l + (s + 1 + S::P >= S::NS ? 1 : 0), wg, ci, lane);
-        ring_phase<S, OFF, K, k + 2>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+        ring_issue<S, sn0>(p, s + S::P >= S::NS ? nxt : cur, ring_lds, l + (s + S::P >= S::NS ? 1 : 0), wg, ci,
+                           lane);
+        ring_issue<S, sn1>(p, s + 1 + S::P >= S::NS ? nxt : cur, ring_lds, l + (s + 1 + S::P >= S::NS ? 1 : 0), wg,
+                           ci, lane);
+        ring_phase<S, OFF, K, k + 2>(p, cur, nxt, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
     } else if constexpr (k < K) {
         constexpr int s = OFF + k;
         using T = Slot<S, s>;
@@ -659,8 +682,8 @@ __device__ __forceinline__ void ring_phase(const vxm_pparams &p, const int8_t *r
         const float a = wave_sum_63(unit_dot<S, s>(ring, l, ci, lane, xq, xd));
         if (lane == 63 && u < T::U) part[u] = a;
         constexpr int sn = (s + S::P) % S::NS;
-        ring_issue<S, sn>(p, ring_lds, l + (s + S::P >= S::NS ? 1 : 0), wg, ci, lane);
-        ring_phase<S, OFF, K, k + 1>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+        ring_issue<S, sn>(p, s + S::P >= S::NS ? nxt : cur, ring_lds, l + (s + S::P >= S::NS ? 1 : 0), wg, ci, lane);
+        ring_phase<S, OFF, K, k + 1>(p, cur, nxt, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
     }
 }
 
@@ -885,10 +908,12 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
     // this wave's ring slots in LDS (compute waves only)
     const int8_t *ring = (const int8_t *)lds + S::RING_OFF + (reader ? 0 : ci) * S::RING * kSlot;
     const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
-    if (!reader) ring_prime<S>(p, ring_lds, wg, ci, lane, std::make_integer_sequence<int, S::P>{});
+    UnitBases cur = unit_bases(p, 0);
+    if (!reader) ring_prime<S>(p, cur, ring_lds, wg, ci, lane, std::make_integer_sequence<int, S::P>{});
 
     for (int l = 0; l < p.n_layers; l++) {
         vxm_ptab Ly = layer_at(p, l);
+        const UnitBases nxt = unit_bases(p, l + 1);
         // ---------------- A: norm + QKV + rope ----------------
         if (reader) {
             stage_f32(Ly->g_in, H, gn);
@@ -917,7 +942,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         VXM_TS(tid_now() == 0, 0);
         norm_quant<H>(xs, gn, l > 0 ? ssq[0] + ssq[1] : ssq[0], p.eps, xq, xd);
         lds_barrier();
-        if (!reader) ring_phase<S, S::OA, S::SA>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+        if (!reader) ring_phase<S, S::OA, S::SA>(p, cur, nxt, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
         lds_barrier();
         VXM_TS(tid_now() == 0, 1);
         if (!reader && t < S::RA / 2 * kRep) {
@@ -962,7 +987,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         VXM_TS(tid_now() == 0, 5);
         quantize_lds(big, QD, xq, xd);
         lds_barrier();
-        if (!reader) ring_phase<S, S::OC, S::SC>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+        if (!reader) ring_phase<S, S::OC, S::SC>(p, cur, nxt, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
         lds_barrier();
         VXM_TS(tid_now() == 0, 6);
         if (!reader && t < S::RC / 2 * kRep) {
@@ -994,7 +1019,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         VXM_TS(tid_now() == 0, 7);
         norm_quant<H>(h1s, gn, ssq[0], p.eps, xq, xd);
         lds_barrier();
-        if (!reader) ring_phase<S, S::OD, S::SD>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+        if (!reader) ring_phase<S, S::OD, S::SD>(p, cur, nxt, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
         lds_barrier();
         VXM_TS(tid_now() == 0, 8);
         if (!reader && t < S::RD / 4 * kRep) {
@@ -1023,7 +1048,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         VXM_TS(tid_now() == 0, 9);
         quantize_lds_bf16x2((const uint32_t *)big, F, xq, xd);
         lds_barrier();
-        if (!reader) ring_phase<S, S::OE, S::SE>(p, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+        if (!reader) ring_phase<S, S::OE, S::SE>(p, cur, nxt, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
         lds_barrier();
         VXM_TS(tid_now() == 0, 10);
         if (!reader && t < S::RE / 2 * kRep) {
@@ -1042,6 +1067,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             put_word(p.xb + (((l + 1) & 1) * kRep + r) * SX + row / 2, pack_bf16x2(x2[0], x2[1]),
                      make_tag(ep, l + 1, PH_X));
         }
+        cur = nxt;
     }
     // ---------------- final norm (workgroup 0) ----------------
     if (wg != 0) return;
