@@ -1094,14 +1094,20 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
 
 template <class S>
 __global__ __launch_bounds__(kThreads, 1) void k_decode_persistent(vxm_pparams p) {
-    extern __shared__ float lds[];
-    __shared__ int bail;
-    if (threadIdx.x == 0) bail = 0;
+    // All of the workgroup's LDS is this one dynamic array, so it starts at
+    // address 0 and every 16-byte layout offset is 16-byte aligned.  (A static
+    // __shared__ variable beside it would place the dynamic array right after
+    // the static bytes, at only 4-byte alignment: every ds_read_b128 of the
+    // ring and the activations would then be split by the LDS.)  The bail
+    // flag lives past the layout, at byte S::BYTES.
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    int *bail = (int *)((char *)lds + S::BYTES);
+    if (threadIdx.x == 0) *bail = 0;
 #ifdef VXM_PERSISTENT_TRACE
     if (threadIdx.x == 0 && p.trace) p.trace[(size_t)blockIdx.x * p.trace_stride] = __builtin_amdgcn_s_memrealtime();
 #endif
     // bail is read only after the first barrier of decode_run
-    decode_run<S>(p, lds, &bail);
+    decode_run<S>(p, lds, bail);
 }
 
 // ---------------------------------------------------------------------------
@@ -1124,7 +1130,7 @@ static constexpr int kMaxLds = 160 * 1024;
 
 template <class S>
 static int launch_decode(vxm_ctx *ctx, const vxm_pparams &prm) {
-    const int lds = S::BYTES;
+    const int lds = S::BYTES + 16;   // the layout + the bail flag
     auto kern = k_decode_persistent<S>;
     if (lds > kMaxLds)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "persistent decode: kv capacity %d needs %d B of LDS", prm.cap, lds);
