@@ -59,6 +59,7 @@
 #include "vxm_model.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 // Phase timestamps for profiling builds (-DVXM_PERSISTENT_TRACE): slot k of
 // layer l of this workgroup gets the 100 MHz real-time counter.  Compiled
@@ -779,9 +780,13 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     const int kv_len = pos + 1;
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
     const int sub = lane % LPK, kin = lane / LPK;
-    float qv[8];
+    // q_h as f16 pairs: q is BF16-valued (8 mantissa bits), so f16 holds it
+    // exactly at the magnitudes of a projection; the f16 x f16 products of
+    // v_dot2_f32_f16 are exact in f32 and only the summation order differs
+    // from a sequential fp32 dot product
+    half2_t q2[4];
 #pragma unroll
-    for (int i = 0; i < 8; i++) qv[i] = qh[sub * 8 + i];
+    for (int i = 0; i < 4; i++) q2[i] = half2_t{(_Float16)qh[sub * 8 + 2 * i], (_Float16)qh[sub * 8 + 2 * i + 1]};
     // scores: batch jb covers keys jb + (k * kWaves + wave) * KPW + kin
     float mx = -INFINITY;
     for (int jb = 0; jb < kv_len; jb += PERB) {
@@ -789,21 +794,15 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
 #pragma unroll
         for (int k = 0; k < KB; k++) {
             const int j = jb + (k * kWaves + wave) * KPW + kin;
-            float kv8[8];
+            uint32_t wv[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
             if (j == pos) {
 #pragma unroll
-                for (int i = 0; i < 8; i++) kv8[i] = vxm_h2f(vxm_f2h(kcur[sub * 8 + i]));
-            } else {
-                const uint32_t wv[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    kv8[2 * i] = vxm_h2f((uint16_t)(wv[i] & 0xffffu));
-                    kv8[2 * i + 1] = vxm_h2f((uint16_t)(wv[i] >> 16));
-                }
+                for (int i = 0; i < 4; i++)
+                    wv[i] = (uint32_t)vxm_f2h(kcur[sub * 8 + 2 * i]) | ((uint32_t)vxm_f2h(kcur[sub * 8 + 2 * i + 1]) << 16);
             }
             float pt = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) pt += kv8[i] * qv[i];
+            for (int i = 0; i < 4; i++) pt = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, wv[i]), q2[i], pt, false);
             pt = row16_sum_15(pt);
             if (j < kv_len && sub == LPK - 1) {
                 const float s2 = pt * scale;
@@ -832,16 +831,18 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
             const int j = jb + (k * kWaves + wave) * KPW + kin;
             if (j >= kv_len) continue;
             const float pj = sc[j];
+            uint32_t wv[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
             if (j == pos) {
 #pragma unroll
-                for (int i = 0; i < 8; i++) o[i] += vxm_h2f(vxm_f2h(vcur[sub * 8 + i])) * pj;
-            } else {
-                const uint32_t wv[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
+                for (int i = 0; i < 4; i++)
+                    wv[i] = (uint32_t)vxm_f2h(vcur[sub * 8 + 2 * i]) | ((uint32_t)vxm_f2h(vcur[sub * 8 + 2 * i + 1]) << 16);
+            }
+            // one mixed-precision fma per value: the f16 operand is widened exactly
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    o[2 * i] += vxm_h2f((uint16_t)(wv[i] & 0xffffu)) * pj;
-                    o[2 * i + 1] += vxm_h2f((uint16_t)(wv[i] >> 16)) * pj;
-                }
+            for (int i = 0; i < 4; i++) {
+                const half2_t v2 = __builtin_bit_cast(half2_t, wv[i]);
+                o[2 * i] = __builtin_fmaf(pj, (float)v2.x, o[2 * i]);
+                o[2 * i + 1] = __builtin_fmaf(pj, (float)v2.y, o[2 * i + 1]);
             }
         }
     }
@@ -861,12 +862,15 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     }
     lds_barrier();
     const uint32_t tg = make_tag(ep, l, PH_ATT);
-    for (int t = tid; t < HD * kRep; t += kThreads) {
-        const int d = t % HD, r = t / HD;
+    static_assert(kThreads % HD == 0 && kRep % (kThreads / HD) == 0, "attention output replicas");
+    {
+        // thread t owns dim t % HD; the wave partials are summed once, in a
+        // fixed order, and stored to kRep / (kThreads / HD) replicas
+        const int d = tid % HD;
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; w++) v += red[w * HD + d];
-        put_word(p.attb + r * SAT + h * HD + d, __float_as_uint(v), tg);
+        for (int r = tid / HD; r < kRep; r += kThreads / HD) put_word(p.attb + r * SAT + h * HD + d, __float_as_uint(v), tg);
     }
     VXM_TS(tid_now() == 0, 4);
 }
