@@ -112,9 +112,6 @@ struct Shape {
     // for its inputs
     static constexpr int P = kLook < NS ? kLook : NS;
     static_assert(P >= SD && P >= SE, "the lookahead covers a phase");
-    // vector memory instructions issued after a unit's three DMAs before it
-    // is consumed: the 3 DMAs of each of the next P-1 units
-    static constexpr int WAIT = 3 * (P - 1);
     // the ring has P slots: stream position q = l*NS + s lives in slot q % P,
     // and the unit issued when q is consumed (q + P) takes q's slot
     static constexpr int RING = P;
@@ -558,10 +555,8 @@ __device__ __forceinline__ void dma_unit(uint32_t lds_slot, const int8_t *q, con
         : "memory", "scc");
 }
 
-// Wait until at most N vector memory instructions of the wave are pending.
-// In steady state the 3(P-1) DMAs of the next P-1 units were issued after a
-// unit's own three, and vmcnt retires in order, so the unit is in LDS.
-// Other vector memory instructions of the wave only make the wait stricter.
+// Wait until at most N vector memory instructions of the wave are pending
+// (they retire in order).
 template <int N>
 __device__ __forceinline__ void ring_wait() {
     static_assert(N >= 0 && N <= 63, "vmcnt range");
@@ -652,16 +647,30 @@ __device__ __forceinline__ float unit_dot(const int8_t *ring, int l, int ci, int
     return (float)si * (vxm_h2f(dw) * xs);
 }
 
+// Consume the K slots of one phase starting at slot OFF: dot product of each
+// unit (lane l: block l) with the quantized activation in LDS, partial to
+// part[u].  Units go two at a time: both are waited for, read and reduced
+// together (two independent dependency chains).  No loads are issued here:
+// the refills of the phase's slots go out after its outputs are published
+// (ring_refill), while the workgroup waits for the next phase's inputs.  All
+// 7 compute waves issuing DMAs at once saturate the CU's address unit, and a
+// wave's load issue blocks until it is accepted, so refills issued between
+// units stalled the compute by about as long as the compute itself.
+// At phase start every slot of the phase is in flight or landed, and the
+// only ring loads issued after slot k's are those of the phase's later
+// slots: 3 (P - 1 - k) of them, so vmcnt(3 (P - 1 - k)) means slot k is in
+// LDS.  (Other vector memory instructions of the wave are issued later and
+// only make the wait stricter.)
 template <class S, int OFF, int K, int k = 0>
-__device__ __forceinline__ void ring_phase(const vxm_pparams &p, const UnitBases &cur, const UnitBases &nxt,
-                                           const int8_t *ring, uint32_t ring_lds, int l, int wg, int ci, int lane,
-                                           const int8_t *xq, const float *xd, float *part) {
+__device__ __forceinline__ void ring_phase(const int8_t *ring, int l, int ci, int lane, const int8_t *xq,
+                                           const float *xd, float *part) {
+    static_assert(K <= S::P, "a phase's slots are all in the ring at its start");
     if constexpr (k + 1 < K) {
         constexpr int s = OFF + k;
         using T0 = Slot<S, s>;
         using T1 = Slot<S, s + 1>;
         const int u0 = ci + kCW * T0::k, u1 = ci + kCW * T1::k;
-        ring_wait<S::WAIT - 3>();   // units s and s + 1 are in LDS
+        ring_wait<3 * (S::P - 2 - k)>();   // slots k and k + 1 are in LDS
         float a = unit_dot<S, s>(ring, l, ci, lane, xq, xd);
         float b = unit_dot<S, s + 1>(ring, l, ci, lane, xq, xd);
         wave_sum_63_x2(a, b);
@@ -669,22 +678,28 @@ __device__ __forceinline__ void ring_phase(const vxm_pparams &p, const UnitBases
             if (u0 < T0::U) part[u0] = a;
             if (u1 < T1::U) part[u1] = b;
         }
-        constexpr int sn0 = (s + S::P) % S::NS, sn1 = (s + 1 + S::P) % S::NS;
-        ring_issue<S, sn0>(p, s + S::P >= S::NS ? nxt : cur, ring_lds, l + (s + S::P >= S::NS ? 1 : 0), wg, ci,
-                           lane);
-        ring_issue<S, sn1>(p, s + 1 + S::P >= S::NS ? nxt : cur, ring_lds, l + (s + 1 + S::P >= S::NS ? 1 : 0), wg,
-                           ci, lane);
-        ring_phase<S, OFF, K, k + 2>(p, cur, nxt, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+        ring_phase<S, OFF, K, k + 2>(ring, l, ci, lane, xq, xd, part);
     } else if constexpr (k < K) {
         constexpr int s = OFF + k;
         using T = Slot<S, s>;
         const int u = ci + kCW * T::k;
-        ring_wait<S::WAIT>();
+        ring_wait<3 * (S::P - 1 - k)>();
         const float a = wave_sum_63(unit_dot<S, s>(ring, l, ci, lane, xq, xd));
         if (lane == 63 && u < T::U) part[u] = a;
-        constexpr int sn = (s + S::P) % S::NS;
-        ring_issue<S, sn>(p, s + S::P >= S::NS ? nxt : cur, ring_lds, l + (s + S::P >= S::NS ? 1 : 0), wg, ci, lane);
-        ring_phase<S, OFF, K, k + 1>(p, cur, nxt, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+        ring_phase<S, OFF, K, k + 1>(ring, l, ci, lane, xq, xd, part);
+    }
+}
+
+// Refill the K slots of the phase at OFF with the units P positions ahead
+// (in the next layer's weights past the end of the schedule).
+template <class S, int OFF, int K, int k = 0>
+__device__ __forceinline__ void ring_refill(const vxm_pparams &p, const UnitBases &cur, const UnitBases &nxt,
+                                            uint32_t ring_lds, int l, int wg, int ci, int lane) {
+    if constexpr (k < K) {
+        constexpr int s = OFF + k, sn = (s + S::P) % S::NS;
+        constexpr bool wrap = s + S::P >= S::NS;
+        ring_issue<S, sn>(p, wrap ? nxt : cur, ring_lds, l + (wrap ? 1 : 0), wg, ci, lane);
+        ring_refill<S, OFF, K, k + 1>(p, cur, nxt, ring_lds, l, wg, ci, lane);
     }
 }
 
@@ -946,7 +961,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         VXM_TS(tid_now() == 0, 0);
         norm_quant<H>(xs, gn, l > 0 ? ssq[0] + ssq[1] : ssq[0], p.eps, xq, xd);
         lds_barrier();
-        if (!reader) ring_phase<S, S::OA, S::SA>(p, cur, nxt, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+        if (!reader) ring_phase<S, S::OA, S::SA>(ring, l, ci, lane, xq, xd, part);
         lds_barrier();
         VXM_TS(tid_now() == 0, 1);
         if (!reader && t < S::RA / 2 * kRep) {
@@ -970,6 +985,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             }
             put_word(p.qkvb + r * SQ + gw, pack_bf16x2(y0, y1), make_tag(ep, l, PH_QKV));
         }
+        if (!reader) ring_refill<S, S::OA, S::SA>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         // ---------------- B: attention, one workgroup per query head ----------------
         if (head >= 0) {
             attention_phase<S>(p, l, head, lds, bail);
@@ -991,7 +1007,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         VXM_TS(tid_now() == 0, 5);
         quantize_lds(big, QD, xq, xd);
         lds_barrier();
-        if (!reader) ring_phase<S, S::OC, S::SC>(p, cur, nxt, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+        if (!reader) ring_phase<S, S::OC, S::SC>(ring, l, ci, lane, xq, xd, part);
         lds_barrier();
         VXM_TS(tid_now() == 0, 6);
         if (!reader && t < S::RC / 2 * kRep) {
@@ -1009,6 +1025,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             }
             put_word(p.h1b + r * SX + row / 2, pack_bf16x2(hh[0], hh[1]), make_tag(ep, l, PH_H1));
         }
+        if (!reader) ring_refill<S, S::OC, S::SC>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         // ---------------- D: post norm + gate/up + SwiGLU ----------------
         if (reader) {
             // the reader alone: a compute wave's loads would wait (in-order
@@ -1023,7 +1040,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         VXM_TS(tid_now() == 0, 7);
         norm_quant<H>(h1s, gn, ssq[0], p.eps, xq, xd);
         lds_barrier();
-        if (!reader) ring_phase<S, S::OD, S::SD>(p, cur, nxt, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+        if (!reader) ring_phase<S, S::OD, S::SD>(ring, l, ci, lane, xq, xd, part);
         lds_barrier();
         VXM_TS(tid_now() == 0, 8);
         if (!reader && t < S::RD / 4 * kRep) {
@@ -1039,6 +1056,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             const float p0 = swiglu(v[0], v[1]), p1 = swiglu(v[2], v[3]);
             put_word(p.pb + r * SP + wg * (S::RD / 4) + wi, pack_bf16x2(p0, p1), make_tag(ep, l, PH_P));
         }
+        if (!reader) ring_refill<S, S::OD, S::SD>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         // ---------------- E: down rows + residual ----------------
         if (wave < 4) {
             // waves 0..3 (idle until this input arrives) each read one quarter
@@ -1052,7 +1070,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         VXM_TS(tid_now() == 0, 9);
         quantize_lds_bf16x2((const uint32_t *)big, F, xq, xd);
         lds_barrier();
-        if (!reader) ring_phase<S, S::OE, S::SE>(p, cur, nxt, ring, ring_lds, l, wg, ci, lane, xq, xd, part);
+        if (!reader) ring_phase<S, S::OE, S::SE>(ring, l, ci, lane, xq, xd, part);
         lds_barrier();
         VXM_TS(tid_now() == 0, 10);
         if (!reader && t < S::RE / 2 * kRep) {
@@ -1071,8 +1089,11 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             put_word(p.xb + (((l + 1) & 1) * kRep + r) * SX + row / 2, pack_bf16x2(x2[0], x2[1]),
                      make_tag(ep, l + 1, PH_X));
         }
+        if (!reader) ring_refill<S, S::OE, S::SE>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         cur = nxt;
     }
+    // the refills past the last layer (zero units) land before the workgroup ends
+    ring_wait<0>();
     // ---------------- final norm (workgroup 0) ----------------
     if (wg != 0) return;
     const int Lyr = p.n_layers;
