@@ -427,6 +427,7 @@ def main():
                     help="time only the prefill legs (MFMA GEMMs and the 512-token 28-layer prefill)")
     ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--cfm-only", action="store_true", help="time only the CFM solve leg")
+    ap.add_argument("--gemv-only", action="store_true", help="time only the isolated Q8_0 GEMV leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 device copies of 256 MiB (a known-traffic kernel for HBM counter scaling)")
     args = ap.parse_args()
@@ -450,7 +451,7 @@ def main():
     res = {}
     pre = None
     cfm = None
-    if not args.decode_only and not args.prefill_only:
+    if not args.decode_only and not args.prefill_only and not args.gemv_only:
         us_cfm, evals, fin = bench_cfm(ctx, torch, vxm, 5)
         eb = locdit_eval_bytes()
         ops = 2 * 2 * (3 + DIT["PC"] + DIT["P"]) * (eb * 32 // 34)
@@ -465,7 +466,7 @@ def main():
             print(json.dumps({"cfm": cfm}))
             ctx.close()
             return
-    if not args.decode_only:
+    if not args.decode_only and not args.gemv_only:
         M = args.prefill_tokens
         gemms = {}
         for name, (N, K) in (("qkv", (NH * HD + 2 * NKV * HD, H)), ("o", (H, NH * HD)), ("gate_up", (2 * F, H)),
@@ -499,6 +500,10 @@ def main():
                                "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                                "note": "one launch per GEMV, back to back over 64 rotated weight copies"}
             log(f"gemv {N}x{K}: {us:.3f} us/launch, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
+        if args.gemv_only:
+            print(json.dumps({"gemv": res}))
+            ctx.close()
+            return
 
     t0 = time.time()
     layers = make_layers(vxm, 1, L)

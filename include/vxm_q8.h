@@ -51,7 +51,9 @@ typedef enum vxm_status {
 /* Kernel path for vxm_mul_mat_*: AUTO picks by M. */
 #define VXM_PATH_AUTO 0
 #define VXM_PATH_GEMV 1   /* weight-streaming GEMV, any M (loops over rows of x) */
-#define VXM_PATH_MFMA 2   /* LDS-staged int8 MFMA GEMM                           */
+#define VXM_PATH_MFMA 2   /* int8 MFMA: register-fed small-M kernel up to 64 rows
+                           * (N % 16 == 0, K % 256 == 0), else the LDS-tiled GEMM */
+#define VXM_PATH_MFMA_TILED 3 /* the LDS-tiled MFMA GEMM for every M            */
 
 typedef struct vxm_ctx vxm_ctx;
 typedef struct vxm_weight vxm_weight;

@@ -170,6 +170,47 @@ def test_mfma_gemm_split_k(mfma_path, orc, N, K, M):
     w.free()
 
 
+# Shapes of the register-fed small-M MFMA kernel (M <= 64, N % 64 == 0, K % 512 == 0):
+# the LocDiT projections at M = 2 x 24, a single 64-row group, partial m-tiles, one
+# 16-block stage, several stages per split (long K) and 2 to 8 K splits.  The tiled GEMM (forced) must meet the same bar on the same inputs.
+@pytest.mark.parametrize("N,K,M", [(8192, 1024, 48), (3072, 1024, 48), (1024, 1024, 48), (1024, 4096, 48),
+                                   (2048, 6144, 48), (64, 512, 5), (64, 32768, 64), (2560, 2048, 16),
+                                   (6144, 2048, 8), (128, 1536, 33), (1024, 512, 1), (4096, 1024, 64)])
+def test_mfma_small_m(vxm_ctx, orc, N, K, M):
+    import vxm
+
+    _, x, wq = _case(orc, N, K, M, 19 * N + K + M)
+    w = vxm_ctx.upload_q8_0(wq, N, K)
+    xq_d, xd_d = vxm_ctx.quantize_q8_0(_dev(x), 1)
+    ref = orc.mul_mat_f64(wq, orc.quantize_rows(x, 1), N, K, M)
+    try:
+        vxm_ctx.set_path(vxm.PATH_MFMA)
+        y = _np(vxm_ctx.mul_mat_q8(w, xq_d, xd_d))
+        _assert_close(y, ref)
+        # the split reduction adds in a fixed order: a repeat is bit-identical
+        assert np.array_equal(y, _np(vxm_ctx.mul_mat_q8(w, xq_d, xd_d)))
+        vxm_ctx.set_path(vxm.PATH_MFMA_TILED)
+        _assert_close(_np(vxm_ctx.mul_mat_q8(w, xq_d, xd_d)), ref)
+    finally:
+        vxm_ctx.set_path(vxm.PATH_AUTO)
+    w.free()
+
+
+def test_mfma_small_m_back_to_back_shapes(vxm_ctx, orc):
+    """Consecutive split launches of different shapes share the tagged partial buffer:
+    each must read only its own launch's words."""
+    cases = []
+    for (N, K, M) in ((1024, 4096, 48), (1024, 1024, 40), (1024, 4096, 48), (3072, 1024, 24)):
+        _, x, wq = _case(orc, N, K, M, 7 * N + 3 * K + M)
+        w = vxm_ctx.upload_q8_0(wq, N, K)
+        xq_d, xd_d = vxm_ctx.quantize_q8_0(_dev(x), 1)
+        cases.append((w, xq_d, xd_d, orc.mul_mat_f64(wq, orc.quantize_rows(x, 1), N, K, M)))
+    ys = [vxm_ctx.mul_mat_q8(w, a, b) for (w, a, b, _) in cases]
+    for y, (w, _, _, ref) in zip(ys, cases):
+        _assert_close(_np(y), ref)
+        w.free()
+
+
 def test_auto_path_switches_at_eight_rows(vxm_ctx, orc):
     """AUTO takes the GEMV below 8 rows and the MFMA GEMM from 8; both meet the oracle bar
     and the repeated call is deterministic."""

@@ -218,7 +218,7 @@ extern "C" int vxm_locenc_forward(vxm_locenc *m, const float *x_dev, int32_t P, 
     const vxm_attn_site site{m->ws.lk, m->ws.lv, (int)S, (int64_t)d.nkv * S * d.hd, (int)S, 0, 0, 0};
     for (int l = 0; l < m->cfg.n_layers; l++) {
         const vxm_block &b = m->blocks[l];
-        if ((rc = vxm_launch_rmsnorm(ctx, m->seq, l ? m->ws.dn : nullptr, 1.0f, b.g_in, S, H, d.eps, nullptr,
+        if ((rc = vxm_launch_rmsnorm(ctx, m->seq, l ? m->ws.dn_out : vxm_parts{}, 1.0f, b.g_in, S, H, d.eps, nullptr,
                                      m->ws.xq, m->ws.xd, var)))
             return rc;
         if ((rc = vxm_block_run(ctx, d, b, m->ws, m->seq, S, site))) return rc;
@@ -226,7 +226,7 @@ extern "C" int vxm_locenc_forward(vxm_locenc *m, const float *x_dev, int32_t P, 
     // last residual + final RMSNorm of the rows that are returned: the
     // special token's row (src/locenc.c:118-128), or every row
     const int64_t rows = off ? 1 : S;
-    return vxm_launch_rmsnorm(ctx, m->seq, m->cfg.n_layers ? m->ws.dn : nullptr, 1.0f, m->norm, rows, H, d.eps,
+    return vxm_launch_rmsnorm(ctx, m->seq, m->cfg.n_layers ? m->ws.dn_out : vxm_parts{}, 1.0f, m->norm, rows, H, d.eps,
                               out_dev, nullptr, nullptr, var);
 }
 

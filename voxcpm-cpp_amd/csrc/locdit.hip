@@ -283,7 +283,7 @@ static int dit_eval(vxm_locdit *m, const float *x, int P, int Pc, int n_seg, con
     const vxm_attn_site site{m->ws.lk, m->ws.lv, (int)S, (int64_t)d.nkv * S * d.hd, (int)S, 0, 0, 0};
     for (int l = 0; l < m->cfg.n_layers; l++) {
         const vxm_block &b = m->blocks[l];
-        if ((rc = vxm_launch_rmsnorm(ctx, m->seq, l ? m->ws.dn : nullptr, 1.0f, b.g_in, M, H, d.eps, nullptr,
+        if ((rc = vxm_launch_rmsnorm(ctx, m->seq, l ? m->ws.dn_out : vxm_parts{}, 1.0f, b.g_in, M, H, d.eps, nullptr,
                                      m->ws.xq, m->ws.xd, var)))
             return rc;
         if ((rc = vxm_block_run(ctx, d, b, m->ws, m->seq, M, site))) return rc;
@@ -291,7 +291,8 @@ static int dit_eval(vxm_locdit *m, const float *x, int P, int Pc, int n_seg, con
     // last residual + final RMSNorm of the x rows of each segment (src/locdit.c:373-390)
     for (int g = 0; g < n_seg; g++) {
         const int64_t r0 = g * S + 3 + Pc;
-        const float *delta = m->cfg.n_layers ? m->ws.dn + r0 * H : nullptr;
+        const vxm_parts &dn = m->ws.dn_out;
+        const vxm_parts delta = m->cfg.n_layers ? vxm_parts{dn.p + r0 * H, dn.n, dn.stride} : vxm_parts{};
         if ((rc = vxm_launch_rmsnorm(ctx, m->seq + r0 * H, delta, 1.0f, m->norm, P, H, d.eps, nullptr,
                                      m->aq + (int64_t)g * P * H, m->ad + (int64_t)g * P * (H / 32), var)))
             return rc;

@@ -43,16 +43,19 @@ static const float kVoxcpm2RopeShortFactors[64] = {
 int vxm_ws_ensure(vxm_ctx *ctx, vxm_workspace &ws, int64_t M, int64_t H, int64_t qd, int64_t kvd, int64_t F,
                   int64_t local_kv) {
     const int64_t kmax = std::max(std::max(H, qd), F);
+    // small batches: the projections may arrive as K-split slices of the small-M GEMM
+    const int pf = M <= VXM_SMALL_MAX_ROWS ? VXM_MAX_PARTS : 1;
+    ws.max_parts = pf;
     struct Part { size_t bytes; void **dst; };
     std::vector<Part> parts = {
         {(size_t)(M * kmax), (void **)&ws.xq},
         {(size_t)(M * (kmax / 32) * 2), (void **)&ws.xd},
-        {(size_t)(M * (qd + 2 * kvd) * 4), (void **)&ws.qkv},
+        {(size_t)(pf * M * (qd + 2 * kvd) * 4), (void **)&ws.qkv},
         {(size_t)(M * qd * 4), (void **)&ws.q},
         {(size_t)(M * qd * 4), (void **)&ws.att},
-        {(size_t)(M * H * 4), (void **)&ws.o},
-        {(size_t)(M * 2 * F * 4), (void **)&ws.gu},
-        {(size_t)(M * H * 4), (void **)&ws.dn},
+        {(size_t)(pf * M * H * 4), (void **)&ws.o},
+        {(size_t)(pf * M * 2 * F * 4), (void **)&ws.gu},
+        {(size_t)(pf * M * H * 4), (void **)&ws.dn},
         {(size_t)(local_kv * 2), (void **)&ws.lk},
         {(size_t)(local_kv * 2), (void **)&ws.lv},
     };
@@ -202,23 +205,27 @@ int vxm_block_run(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_block &b, vxm
                   int64_t M, const vxm_attn_site &site) {
     const int64_t qd = (int64_t)d.nh * d.hd, kvd = (int64_t)d.nkv * d.hd;
     const int var = ctx->quant_variant;
-    int rc;
-    if ((rc = vxm_launch_mul_mat(ctx, b.wqkv, ws.xq, ws.xd, M, ws.qkv))) return rc;
-    if ((rc = vxm_launch_rope_kv(ctx, ws.qkv, M, d.nh, d.nkv, d.hd, site.pos0, site.S, d.rope_cs, d.rope_rows,
-                                 d.no_rope, ws.q, site.kc, site.vc, site.cap, site.seg_stride, site.cache_pos0)))
+    int rc, np;
+    if ((rc = vxm_launch_mul_mat_parts(ctx, b.wqkv, ws.xq, ws.xd, M, ws.qkv, ws.max_parts, &np))) return rc;
+    if ((rc = vxm_launch_rope_kv(ctx, vxm_parts{ws.qkv, np, M * (qd + 2 * kvd)}, M, d.nh, d.nkv, d.hd, site.pos0,
+                                 site.S, d.rope_cs, d.rope_rows, d.no_rope, ws.q, site.kc, site.vc, site.cap,
+                                 site.seg_stride, site.cache_pos0)))
         return rc;
     if ((rc = vxm_launch_attention(ctx, ws.q, site.kc, site.vc, ws.att, M, d.nh, d.nkv, d.hd, site.cap,
                                    site.seg_stride, site.S, site.cache_pos0, site.causal)))
         return rc;
     if ((rc = vxm_launch_quantize(ctx, ws.att, M, qd, var, ws.xq, ws.xd))) return rc;
-    if ((rc = vxm_launch_mul_mat(ctx, b.wo, ws.xq, ws.xd, M, ws.o))) return rc;
+    if ((rc = vxm_launch_mul_mat_parts(ctx, b.wo, ws.xq, ws.xd, M, ws.o, ws.max_parts, &np))) return rc;
     // x = bf16(x + scale*bf16(o)); post-attention norm -> Q8_0
-    if ((rc = vxm_launch_rmsnorm(ctx, x, ws.o, d.res_scale, b.g_post, M, d.H, d.eps, nullptr, ws.xq, ws.xd, var)))
+    if ((rc = vxm_launch_rmsnorm(ctx, x, vxm_parts{ws.o, np, M * d.H}, d.res_scale, b.g_post, M, d.H, d.eps, nullptr,
+                                 ws.xq, ws.xd, var)))
         return rc;
-    if ((rc = vxm_launch_mul_mat(ctx, b.wgu, ws.xq, ws.xd, M, ws.gu))) return rc;
-    if ((rc = vxm_launch_swiglu_quant(ctx, ws.gu, M, d.F, 2 * d.F, ws.xq, ws.xd, nullptr, var))) return rc;
-    if ((rc = vxm_launch_mul_mat(ctx, b.wd, ws.xq, ws.xd, M, ws.dn))) return rc;
-    (void)kvd;
+    if ((rc = vxm_launch_mul_mat_parts(ctx, b.wgu, ws.xq, ws.xd, M, ws.gu, ws.max_parts, &np))) return rc;
+    if ((rc = vxm_launch_swiglu_quant(ctx, vxm_parts{ws.gu, np, M * 2 * d.F}, M, d.F, 2 * d.F, ws.xq, ws.xd, nullptr,
+                                      var)))
+        return rc;
+    if ((rc = vxm_launch_mul_mat_parts(ctx, b.wd, ws.xq, ws.xd, M, ws.dn, ws.max_parts, &np))) return rc;
+    ws.dn_out = vxm_parts{ws.dn, np, M * d.H};
     return VXM_OK;
 }
 
@@ -230,7 +237,7 @@ extern "C" int vxm_rms_norm(vxm_ctx *ctx, const float *x_dev, const float *gain_
     if (!ctx) return VXM_ERR_INVALID_ARG;
     if (!x_dev || (!y_dev && !xq_dev) || (xq_dev && !xd_dev) || rows < 0)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "rms_norm: bad arguments");
-    return vxm_launch_rmsnorm(ctx, (float *)x_dev, nullptr, 1.0f, gain_dev, rows, n, eps, y_dev, xq_dev, xd_dev,
+    return vxm_launch_rmsnorm(ctx, (float *)x_dev, vxm_parts{}, 1.0f, gain_dev, rows, n, eps, y_dev, xq_dev, xd_dev,
                               ctx->quant_variant);
 }
 
@@ -384,11 +391,11 @@ extern "C" int vxm_minicpm4_block(vxm_minicpm4 *m, vxm_kv_cache *kv, int32_t lay
         site = vxm_attn_site{kv->k(layer), kv->v(layer), kv->cap, 0, (int)n_tokens, pos, pos, 1};
     }
     const vxm_block &b = m->blocks[layer];
-    if ((rc = vxm_launch_rmsnorm(ctx, x_dev, nullptr, 1.0f, b.g_in, n_tokens, d.H, d.eps, nullptr, m->ws.xq,
+    if ((rc = vxm_launch_rmsnorm(ctx, x_dev, vxm_parts{}, 1.0f, b.g_in, n_tokens, d.H, d.eps, nullptr, m->ws.xq,
                                  m->ws.xd, ctx->quant_variant)))
         return rc;
     if ((rc = vxm_block_run(ctx, d, b, m->ws, x_dev, n_tokens, site))) return rc;
-    return vxm_launch_residual(ctx, x_dev, m->ws.dn, d.res_scale, n_tokens * d.H);
+    return vxm_launch_residual(ctx, x_dev, m->ws.dn_out, d.res_scale, n_tokens * d.H);
 }
 
 extern "C" int vxm_minicpm4_forward(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x_dev, int64_t n_tokens, int32_t pos) {
@@ -413,7 +420,7 @@ extern "C" int vxm_minicpm4_forward(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x_
     for (int l = 0; l < m->cfg.n_layers; l++) {
         const vxm_block &b = m->blocks[l];
         // residual of the previous layer's MLP folded into this layer's input norm
-        if ((rc = vxm_launch_rmsnorm(ctx, x_dev, l ? m->ws.dn : nullptr, d.res_scale, b.g_in, n_tokens, d.H, d.eps,
+        if ((rc = vxm_launch_rmsnorm(ctx, x_dev, l ? m->ws.dn_out : vxm_parts{}, d.res_scale, b.g_in, n_tokens, d.H, d.eps,
                                      nullptr, m->ws.xq, m->ws.xd, var)))
             return rc;
         vxm_attn_site site{kv->k(l), kv->v(l), kv->cap, 0, (int)n_tokens, pos, pos, 1};
@@ -421,10 +428,10 @@ extern "C" int vxm_minicpm4_forward(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x_
     }
     // last residual + final norm (in place), or the residual alone
     if (m->final_norm) {
-        if ((rc = vxm_launch_rmsnorm(ctx, x_dev, m->ws.dn, d.res_scale, m->final_norm, n_tokens, d.H, d.eps, x_dev,
+        if ((rc = vxm_launch_rmsnorm(ctx, x_dev, m->ws.dn_out, d.res_scale, m->final_norm, n_tokens, d.H, d.eps, x_dev,
                                      nullptr, nullptr, var)))
             return rc;
-    } else if ((rc = vxm_launch_residual(ctx, x_dev, m->ws.dn, d.res_scale, n_tokens * d.H))) {
+    } else if ((rc = vxm_launch_residual(ctx, x_dev, m->ws.dn_out, d.res_scale, n_tokens * d.H))) {
         return rc;
     }
     kv->n_used = pos + (int32_t)n_tokens;

@@ -67,14 +67,14 @@ __device__ __forceinline__ void quant_block_4lanes(const float v[8], int variant
 // One workgroup of 256 threads per row; n % 8 == 0 and n <= 8 * 256 * VXM_NORM_CHUNKS.
 // ---------------------------------------------------------------------------
 #define VXM_NORM_CHUNKS 4
-__global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const float *__restrict__ delta,
-                                                 float res_scale, const float *__restrict__ gain, int n,
-                                                 float eps, float *__restrict__ y, int8_t *__restrict__ xq,
+__global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const vxm_parts delta, float res_scale,
+                                                 const float *__restrict__ gain, int n, float eps,
+                                                 float *__restrict__ y, int8_t *__restrict__ xq,
                                                  uint16_t *__restrict__ xd, int variant) {
     __shared__ double shd[4];
     const int row = blockIdx.x;
     float *hr = h + (int64_t)row * n;
-    const float *dr = delta ? delta + (int64_t)row * n : nullptr;
+    const float *dr = delta.p ? delta.p + (int64_t)row * n : nullptr;
     float v[VXM_NORM_CHUNKS][8];
     double ss = 0.0;
 #pragma unroll
@@ -86,6 +86,12 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const fl
             v[c][4] = b.x; v[c][5] = b.y; v[c][6] = b.z; v[c][7] = b.w;
             if (dr) {
                 float4 p = *(const float4 *)(dr + base), q = *(const float4 *)(dr + base + 4);
+                for (int z = 1; z < delta.n; z++) {   // K-split slices, added in order
+                    const float4 p2 = *(const float4 *)(dr + z * delta.stride + base);
+                    const float4 q2 = *(const float4 *)(dr + z * delta.stride + base + 4);
+                    p.x = p.x + p2.x; p.y = p.y + p2.y; p.z = p.z + p2.z; p.w = p.w + p2.w;
+                    q.x = q.x + q2.x; q.y = q.y + q2.y; q.z = q.z + q2.z; q.w = q.w + q2.w;
+                }
                 float dd[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
@@ -129,7 +135,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const fl
     }
 }
 
-int vxm_launch_rmsnorm(vxm_ctx *ctx, float *h, const float *delta, float res_scale, const float *gain,
+int vxm_launch_rmsnorm(vxm_ctx *ctx, float *h, vxm_parts delta, float res_scale, const float *gain,
                        int64_t rows, int64_t n, float eps, float *y, int8_t *xq, uint16_t *xd, int variant) {
     if (rows <= 0) return VXM_OK;
     if (n % 32 != 0 || n > 8 * 256 * VXM_NORM_CHUNKS)
@@ -150,7 +156,7 @@ int vxm_launch_rmsnorm(vxm_ctx *ctx, float *h, const float *delta, float res_sca
 // Tokens come in segments of S (one per CFG branch); token t has position
 // pos0 + t % S and segment t / S, whose cache starts at seg * seg_stride.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_rope_kv(const float *__restrict__ qkv, int nh, int nkv, int hd,
+__global__ __launch_bounds__(256) void k_rope_kv(const vxm_parts qkv, int nh, int nkv, int hd,
                                                  int pos0, int S, const float2 *__restrict__ cs,
                                                  int no_rope, float *__restrict__ q_out, uint16_t *__restrict__ kc,
                                                  uint16_t *__restrict__ vc, int cap, int64_t seg_stride,
@@ -160,7 +166,13 @@ __global__ __launch_bounds__(256) void k_rope_kv(const float *__restrict__ qkv, 
     const int pos = pos0 + ti;
     const int half = hd / 2;
     const int qd = nh * hd, kvd = nkv * hd;
-    const float *row = qkv + (int64_t)t * (qd + 2 * kvd);
+    const float *row = qkv.p + (int64_t)t * (qd + 2 * kvd);
+    // the projection: its K-split slices added in order
+    auto at = [&](int i) {
+        float v = row[i];
+        for (int z = 1; z < qkv.n; z++) v = v + row[z * qkv.stride + i];
+        return v;
+    };
     uint16_t *kseg = kc + seg * seg_stride, *vseg = vc + seg * seg_stride;
     const int cpos = cache_pos0 + ti;
     // q and k pairs
@@ -168,8 +180,8 @@ __global__ __launch_bounds__(256) void k_rope_kv(const float *__restrict__ qkv, 
         const int head = idx / half, i = idx % half;
         const bool isq = head < nh;
         // q and k rows are stored pair-interleaved: head row 2i is dim i, 2i+1 is dim i + hd/2
-        const float *src = isq ? row + head * hd : row + qd + (head - nh) * hd;
-        float x0 = vxm_bf16(src[2 * i]), x1 = vxm_bf16(src[2 * i + 1]);
+        const int src = isq ? head * hd : qd + (head - nh) * hd;
+        float x0 = vxm_bf16(at(src + 2 * i)), x1 = vxm_bf16(at(src + 2 * i + 1));
         float y0 = x0, y1 = x1;
         if (!no_rope) {
             const float2 r = cs[(int64_t)pos * half + i];
@@ -191,12 +203,12 @@ __global__ __launch_bounds__(256) void k_rope_kv(const float *__restrict__ qkv, 
     // v
     for (int idx = threadIdx.x; idx < kvd; idx += blockDim.x) {
         const int kh = idx / hd, dd = idx % hd;
-        const float val = vxm_bf16(row[qd + kvd + idx]);
+        const float val = vxm_bf16(at(qd + kvd + idx));
         vseg[((int64_t)kh * cap + cpos) * hd + dd] = vxm_f2h(val);
     }
 }
 
-int vxm_launch_rope_kv(vxm_ctx *ctx, const float *qkv, int64_t M, int nh, int nkv, int hd, int pos0, int S,
+int vxm_launch_rope_kv(vxm_ctx *ctx, vxm_parts qkv, int64_t M, int nh, int nkv, int hd, int pos0, int S,
                        const float2 *cs, int cs_rows, int no_rope, float *q_out, uint16_t *kc,
                        uint16_t *vc, int cap, int64_t seg_stride, int cache_pos0) {
     if (M <= 0) return VXM_OK;
@@ -447,18 +459,22 @@ int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const
 // Row m of the fused gate/up projection holds 2F values interleaved: gate n at
 // gu[m*ld + 2n], up n at gu[m*ld + 2n + 1].  8 outputs per thread.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_swiglu_quant(const float *__restrict__ gu, int64_t F, int64_t ld,
+__global__ __launch_bounds__(256) void k_swiglu_quant(const vxm_parts gu, int64_t F, int64_t ld,
                                                       int64_t total, int8_t *__restrict__ xq,
                                                       uint16_t *__restrict__ xd, float *__restrict__ p_out,
                                                       int variant) {
     const int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
     if (e >= total) return;   // total, F % 32 == 0: 4-lane groups are all live or all dead
     const int64_t m = e / F, j = e % F;
-    const float4 *s = (const float4 *)(gu + m * ld + 2 * j);
+    const float *s = gu.p + m * ld + 2 * j;
     float gv[8], uv[8];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        const float4 a = s[k];
+        float4 a = *(const float4 *)(s + 4 * k);
+        for (int z = 1; z < gu.n; z++) {   // K-split slices, added in order
+            const float4 b = *(const float4 *)(s + z * gu.stride + 4 * k);
+            a.x = a.x + b.x; a.y = a.y + b.y; a.z = a.z + b.z; a.w = a.w + b.w;
+        }
         gv[2 * k] = a.x; uv[2 * k] = a.y; gv[2 * k + 1] = a.z; uv[2 * k + 1] = a.w;
     }
     float p[8];
@@ -475,7 +491,7 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const float *__restrict__ 
     quant_block_4lanes(p, variant, xq + e, xd + e / 32, (threadIdx.x & 3) == 0);
 }
 
-int vxm_launch_swiglu_quant(vxm_ctx *ctx, const float *gu, int64_t M, int64_t F, int64_t ld, int8_t *xq,
+int vxm_launch_swiglu_quant(vxm_ctx *ctx, vxm_parts gu, int64_t M, int64_t F, int64_t ld, int8_t *xq,
                             uint16_t *xd, float *p_out, int variant) {
     const int64_t total = M * F;
     if (total <= 0) return VXM_OK;
@@ -491,15 +507,17 @@ int vxm_launch_swiglu_quant(vxm_ctx *ctx, const float *gu, int64_t M, int64_t F,
 // h = bf16(h + scale * bf16(delta)) (the residual adds of
 // vcpm_minicpm4_block, src/minicpm4.c:496-528), elementwise.
 // ---------------------------------------------------------------------------
-__global__ void k_residual(float *__restrict__ h, const float *__restrict__ delta, float scale, int64_t n) {
+__global__ void k_residual(float *__restrict__ h, const vxm_parts delta, float scale, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    float o = vxm_bf16(delta[i]);
+    float d = delta.p[i];
+    for (int z = 1; z < delta.n; z++) d = d + delta.p[z * delta.stride + i];
+    float o = vxm_bf16(d);
     if (scale != 1.0f) o = o * scale;
     h[i] = vxm_bf16(h[i] + o);
 }
 
-int vxm_launch_residual(vxm_ctx *ctx, float *h, const float *delta, float scale, int64_t n) {
+int vxm_launch_residual(vxm_ctx *ctx, float *h, vxm_parts delta, float scale, int64_t n) {
     if (n <= 0) return VXM_OK;
     hipLaunchKernelGGL(k_residual, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, h, delta, scale, n);
     VXM_CHECK_LAUNCH(ctx);

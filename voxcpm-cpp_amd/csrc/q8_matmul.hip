@@ -502,6 +502,159 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
     }
 }
 
+// ---------------------------------------------------------------------------
+// Small-M MFMA GEMM (M <= 64: the CFM batch of both CFG branches, LocEnc
+// patches, short prompts).  Each weight byte feeds at most 64 products here,
+// so the weight stream sets the time: every weight byte is loaded once, with
+// 16-byte loads, straight into MFMA operand registers; the activations (a few
+// KiB per K stage) are staged once per workgroup in LDS and shared by its
+// waves.
+//
+// v_mfma_i32_16x16x32_i8 takes one Q8_0 block: A = 16 weight rows x 32 bytes,
+// B = 32 x 16 activation rows; lane group q = l / 16 supplies 8 bytes of the
+// block for row r = l % 16 and receives the sums D[4q + v][r], v < 4.  The
+// products only need A and B to give a lane group the same 8 bytes of the
+// block.  Weights: lane (q, r) loads 16 bytes at byte 16q of a block pair of
+// row r (q < 2: first block, halves q; q >= 2: second block, halves q - 2);
+// one permlane32 swap per dword exchanges the high 8 bytes of lanes 0-31 with
+// the low 8 bytes of lanes 32-63, after which the low 8 bytes of lane group
+// q hold bytes off(q) = 16 (q & 1) + 8 (q >> 1) of the first block and the
+// high 8 bytes the same bytes of the second block.  Activations are written
+// to LDS with the 8-byte pieces of each block in off(q) order, so lane group
+// q reads its piece at 8q; the LDS row pitch is 16 mod 256 bytes, which maps
+// each half-wave's 8-byte reads onto distinct banks.
+//
+// Workgroup = 4 waves, wave w owning weight rows n0 + 16w .. +15, over the K
+// blocks [z*bps, (z+1)*bps) in stages of kSmallStage blocks; split z writes
+// its partial product to y + z*M*N (the consumer adds the slices in order).
+// Rows past M read as zeros (outside the buffer range) and are not written.
+// ---------------------------------------------------------------------------
+constexpr int kSmallStage = 8;                        // K blocks per LDS stage
+constexpr int kSmallPitch = kSmallStage * 32 + 16;    // LDS bytes per activation row
+constexpr int kSmallRG = 4;                           // 16-row groups (waves) per workgroup
+
+__device__ __forceinline__ float half_at(const v4i &v, int j) {
+    const uint32_t w = (uint32_t)v[j >> 1];
+    return vxm_h2f((uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu)));
+}
+
+__device__ __forceinline__ long pack64(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
+
+template <int MT>
+__global__ __launch_bounds__(64 * kSmallRG) void k_gemm_q8_0_small(const int8_t *__restrict__ xq,
+                                                                   const uint16_t *__restrict__ xd,
+                                                                   const int8_t *__restrict__ wq,
+                                                                   const uint16_t *__restrict__ wd,
+                                                                   float *__restrict__ y, int M, int N, int K,
+                                                                   int bps) {
+    constexpr int SB = kSmallStage, ROWS = 16 * MT, NT = 64 * kSmallRG;
+    __shared__ __align__(16) int8_t xs[ROWS * kSmallPitch];
+    __shared__ float xds[ROWS][SB + 1];
+    const int nb = K / 32;
+    const int g = blockIdx.x, z = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, r = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nw = g * 16 * kSmallRG + 16 * wave;
+    const int zb0 = z * bps, zb1 = min(nb, zb0 + bps);
+    const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)wq, (short)0, N * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)xq, (short)0, M * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t wd_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void *)wd, (short)0, N * nb * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xd_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void *)xd, (short)0, M * nb * 2, 0x00020000);
+
+    float acc[MT][4];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[t][v] = 0.0f;
+    for (int kb0 = zb0; kb0 < zb1; kb0 += SB) {
+        // weight pairs and scales of this stage (HBM): issued first, consumed after the staging
+        v4i wv[SB / 2], dwv[4];
+#pragma unroll
+        for (int p = 0; p < SB / 2; p++)
+            wv[p] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, (nw + r) * K + (kb0 + 2 * p) * 32 + 16 * q, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            dwv[v] = __builtin_amdgcn_raw_buffer_load_b128(wd_rsrc, ((nw + 4 * q + v) * nb + kb0) * 2, 0, 0);
+        // activations of the stage -> LDS: 16-byte piece c = (row, block, half)
+        __syncthreads();   // the previous stage's LDS reads are done
+        constexpr int PIECES = ROWS * SB * 2;
+#pragma unroll
+        for (int c0 = 0; c0 < PIECES; c0 += NT) {
+            const int c = c0 + tid;
+            if (PIECES % NT == 0 || c < PIECES) {
+                const int row = c / (2 * SB), b = (c / 2) % SB, h = c & 1;
+                const v4i v = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, row * K + (kb0 + b) * 32 + 16 * h, 0, 0);
+                int8_t *dst = xs + row * kSmallPitch + b * 32;
+                *(long *)(dst + 8 * h) = pack64((uint32_t)v.x, (uint32_t)v.y);
+                *(long *)(dst + 8 * h + 16) = pack64((uint32_t)v.z, (uint32_t)v.w);
+            }
+        }
+        for (int c = tid; c < ROWS * SB; c += NT) {
+            const int row = c / SB, b = c % SB;
+            const uint16_t hv = __builtin_amdgcn_raw_buffer_load_b16(xd_rsrc, (row * nb + kb0 + b) * 2, 0, 0);
+            xds[row][b] = kb0 + b < zb1 ? vxm_h2f(hv) : 0.0f;
+        }
+        __syncthreads();
+        // per block pair: the pair's operands, then all 2 MT products, then their scaling
+#pragma unroll
+        for (int p = 0; p < SB / 2; p++) {
+            // lanes 0-31 trade their high halves for the low halves of lanes 32-63
+            const auto s0 = __builtin_amdgcn_permlane32_swap((uint32_t)wv[p].x, (uint32_t)wv[p].z, false, false);
+            const auto s1 = __builtin_amdgcn_permlane32_swap((uint32_t)wv[p].y, (uint32_t)wv[p].w, false, false);
+            const long a[2] = {pack64(s0[0], s1[0]), pack64(s0[1], s1[1])};
+            long bx[2][MT];
+            float dx[2][MT];
+#pragma unroll
+            for (int e = 0; e < 2; e++)
+#pragma unroll
+                for (int t = 0; t < MT; t++) {
+                    bx[e][t] = *(const long *)(xs + (16 * t + r) * kSmallPitch + (2 * p + e) * 32 + 8 * q);
+                    dx[e][t] = xds[16 * t + r][2 * p + e];
+                }
+            v4i c[2][MT];
+#pragma unroll
+            for (int e = 0; e < 2; e++)
+#pragma unroll
+                for (int t = 0; t < MT; t++) c[e][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[e], bx[e][t], v4i{}, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int b = 2 * p + e;
+                float dw[4];
+#pragma unroll
+                for (int v = 0; v < 4; v++) dw[v] = half_at(dwv[v], b);
+#pragma unroll
+                for (int t = 0; t < MT; t++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        acc[t][v] = __builtin_fmaf((float)c[e][t][v], dw[v] * dx[e][t], acc[t][v]);
+            }
+        }
+    }
+    float *yz = y + (int64_t)z * M * N;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        const int m = 16 * t + r;
+        if (m >= M) continue;
+#pragma unroll
+        for (int v = 0; v < 4; v++) yz[(int64_t)m * N + nw + 4 * q + v] = acc[t][v];
+    }
+}
+
+// y[i] = sum of the n slices in slice order (the public entry's K-split fix-up).
+__global__ void k_sum_parts(const float *__restrict__ p, int n, int64_t stride, float *__restrict__ y,
+                            int64_t count) {
+    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i >= count) return;   // count % 4 == 0
+    float4 s = *(const float4 *)(p + i);
+    for (int z = 1; z < n; z++) {
+        const float4 v = *(const float4 *)(p + z * stride + i);
+        s.x = s.x + v.x; s.y = s.y + v.y; s.z = s.z + v.z; s.w = s.w + v.w;
+    }
+    *(float4 *)(y + i) = s;
+}
+
 // Tile grid, stage depth and K split.  Single-row-tile GEMMs (M <= 64) take
 // 16-block stages, the others 8-block stages (two workgroups per CU); the K split (at most 4 ways, each part at least 2 stages)
 // brings the grid towards one workgroup per CU.
@@ -561,6 +714,80 @@ static int launch_gemm(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, cons
     return VXM_OK;
 }
 
+// Rows of activations from which the MFMA GEMM replaces the weight-streaming
+// GEMV (which re-reads each activation row per weight row group).
+constexpr int kMfmaMinRows = 8;
+
+// Small-M plan: K splits in whole stages, doubling while the grid leaves CUs
+// idle (at most max_parts).  Shapes outside the kernel's layout (N % 64,
+// K % 256, M > 64, operands of 2 GiB) take the tiled GEMM.
+struct SmallPlan {
+    int mt, bps, splits, groups;
+};
+
+static bool small_plan(vxm_ctx *ctx, int64_t M, int64_t N, int64_t K, int max_parts, SmallPlan &p) {
+    if (M < 1 || M > VXM_SMALL_MAX_ROWS || N % (16 * kSmallRG) || K % (32 * kSmallStage)) return false;
+    // 32-bit buffer offsets: the weights, and the activation rows of every m-tile
+    if (N * K >= ((int64_t)1 << 31) || VXM_SMALL_MAX_ROWS * K >= ((int64_t)1 << 31)) return false;
+    const int nb = (int)(K / 32), stages = nb / kSmallStage;
+    p.mt = (int)((M + 15) / 16);
+    p.groups = (int)(N / (16 * kSmallRG));
+    int s = 1;
+    while (s * 2 <= max_parts && s * 2 <= stages && (int64_t)p.groups * s < ctx->n_cu) s *= 2;
+    const int per = (stages + s - 1) / s;   // stages per split
+    p.bps = per * kSmallStage;
+    p.splits = (nb + p.bps - 1) / p.bps;
+    return true;
+}
+
+static void launch_small(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                         float *y, const SmallPlan &p) {
+    const dim3 grid(p.groups, p.splits), block(64 * kSmallRG);
+    const int N = (int)w->n, K = (int)w->k;
+    switch (p.mt) {
+        case 1: hipLaunchKernelGGL(k_gemm_q8_0_small<1>, grid, block, 0, ctx->stream, xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps); break;
+        case 2: hipLaunchKernelGGL(k_gemm_q8_0_small<2>, grid, block, 0, ctx->stream, xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps); break;
+        case 3: hipLaunchKernelGGL(k_gemm_q8_0_small<3>, grid, block, 0, ctx->stream, xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps); break;
+        default: hipLaunchKernelGGL(k_gemm_q8_0_small<4>, grid, block, 0, ctx->stream, xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps); break;
+    }
+}
+
+// Public entry: a split product goes through the context's scratch and one
+// fix-up launch that adds the slices in order.
+static int launch_gemm_small(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                             float *y, const SmallPlan &p) {
+    if (p.splits == 1) {
+        launch_small(ctx, w, xq, xd, M, y, p);
+        VXM_CHECK_LAUNCH(ctx);
+        return VXM_OK;
+    }
+    const int64_t count = M * w->n;
+    int rc = vxm_ensure_parts(ctx, (size_t)p.splits * count * sizeof(float));
+    if (rc) return rc;
+    float *scratch = (float *)ctx->parts_buf;
+    launch_small(ctx, w, xq, xd, M, scratch, p);
+    VXM_CHECK_LAUNCH(ctx);
+    const int64_t threads = count / 4;   // N % 64 == 0
+    hipLaunchKernelGGL(k_sum_parts, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, scratch,
+                       p.splits, count, y, count);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}
+
+int vxm_launch_mul_mat_parts(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                             float *y, int max_parts, int *parts) {
+    *parts = 1;
+    if (M <= 0) return VXM_OK;
+    SmallPlan sp;
+    const bool small = (ctx->path == VXM_PATH_MFMA || (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows)) &&
+                       small_plan(ctx, M, w->n, w->k, max_parts < VXM_MAX_PARTS ? max_parts : VXM_MAX_PARTS, sp);
+    if (!small) return vxm_launch_mul_mat(ctx, w, xq, xd, M, y);
+    launch_small(ctx, w, xq, xd, M, y, sp);
+    VXM_CHECK_LAUNCH(ctx);
+    *parts = sp.splits;
+    return VXM_OK;
+}
+
 // int32 block sums through the MFMA (the GEMM's own products, unscaled).
 static int launch_gemm_dots(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                             int32_t *out) {
@@ -585,16 +812,19 @@ static void launch_gemv_c(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, c
                        y, (int)w->n, (int)M);
 }
 
-// Rows of activations from which the MFMA GEMM replaces the weight-streaming
-// GEMV (which re-reads each activation row per weight row group).
-constexpr int kMfmaMinRows = 8;
 
 int vxm_launch_mul_mat(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd,
                        int64_t M, float *y) {
     if (M <= 0) return VXM_OK;
     const int64_t K = w->k;
-    const bool mfma = ctx->path == VXM_PATH_MFMA || (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
-    if (mfma) return launch_gemm(ctx, w, xq, xd, M, y);
+    const bool mfma = ctx->path == VXM_PATH_MFMA || ctx->path == VXM_PATH_MFMA_TILED ||
+                      (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
+    if (mfma) {
+        SmallPlan sp;
+        if (ctx->path != VXM_PATH_MFMA_TILED && small_plan(ctx, M, w->n, K, VXM_MAX_PARTS, sp))
+            return launch_gemm_small(ctx, w, xq, xd, M, y, sp);
+        return launch_gemm(ctx, w, xq, xd, M, y);
+    }
     bool done = false;
     if (w->dg) {
         switch (K / 1024) {
@@ -666,7 +896,8 @@ extern "C" int vxm_block_dots_q8_0(vxm_ctx *ctx, const vxm_weight *w, const int8
     const int64_t total = M * w->n * (w->k / VXM_QK);
     if (total == 0) return VXM_OK;
     // the MFMA GEMM's own block sums where the GEMM serves this M
-    const bool mfma = ctx->path == VXM_PATH_MFMA || (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
+    const bool mfma = ctx->path == VXM_PATH_MFMA || ctx->path == VXM_PATH_MFMA_TILED ||
+                      (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
     if (mfma) return launch_gemm_dots(ctx, w, xq_dev, xd_dev, M, out_dev);
     const int64_t grid = (total + 255) / 256;
     hipLaunchKernelGGL(k_block_dots, dim3((unsigned)grid), dim3(256), 0, ctx->stream, w->qs, xq_dev, w->n,

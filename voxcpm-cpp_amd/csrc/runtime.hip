@@ -63,6 +63,7 @@ extern "C" int vxm_close(vxm_ctx *ctx) {
     if (ctx->act_buf) hipFree(ctx->act_buf);
     if (ctx->split_buf) hipFree(ctx->split_buf);
     if (ctx->split_cnt) hipFree(ctx->split_cnt);
+    if (ctx->parts_buf) hipFree(ctx->parts_buf);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return VXM_OK;
@@ -90,7 +91,7 @@ extern "C" int vxm_set_quant_variant(vxm_ctx *ctx, int variant) {
 
 extern "C" int vxm_set_path(vxm_ctx *ctx, int path) {
     if (!ctx) return VXM_ERR_INVALID_ARG;
-    if (path < VXM_PATH_AUTO || path > VXM_PATH_MFMA)
+    if (path < VXM_PATH_AUTO || path > VXM_PATH_MFMA_TILED)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "unknown kernel path %d", path);
     ctx->path = path;
     return VXM_OK;
@@ -139,6 +140,20 @@ int vxm_ensure_act(vxm_ctx *ctx, size_t bytes) {
         return vxm_fail(ctx, VXM_ERR_OOM, "activation scratch of %zu bytes failed", want);
     }
     ctx->act_bytes = want;
+    return VXM_OK;
+}
+
+int vxm_ensure_parts(vxm_ctx *ctx, size_t bytes) {
+    if (ctx->parts_bytes >= bytes) return VXM_OK;
+    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->parts_buf) VXM_HIP(ctx, hipFree(ctx->parts_buf));
+    ctx->parts_buf = nullptr;
+    ctx->parts_bytes = 0;
+    if (hipMalloc(&ctx->parts_buf, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return vxm_fail(ctx, VXM_ERR_OOM, "GEMM slice scratch of %zu bytes failed", bytes);
+    }
+    ctx->parts_bytes = bytes;
     return VXM_OK;
 }
 

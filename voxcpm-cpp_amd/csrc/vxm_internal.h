@@ -29,6 +29,9 @@ struct vxm_ctx {
     int *split_cnt = nullptr;
     size_t split_ncnt = 0;
     uint32_t split_epoch = 0;   // tag of the last split launch's partial words
+    // K-split slices of the small-M GEMM behind the public matmul entries
+    void *parts_buf = nullptr;
+    size_t parts_bytes = 0;
 };
 
 // Device layout of a Q8_0 matrix (n_rows x k).  The GGUF row of k/32 34-byte
@@ -116,5 +119,22 @@ int vxm_launch_quantize(vxm_ctx *ctx, const float *x, int64_t M, int64_t K, int 
                         int8_t *xq, uint16_t *xd);
 int vxm_launch_mul_mat(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd,
                        int64_t M, float *y);
+// A matmul output held as n fp32 slices `stride` elements apart whose sum, added in
+// slice order, is the product (the small-M GEMM's K splits, left for the consumer).
+struct vxm_parts {
+    const float *p;
+    int n;
+    int64_t stride;
+};
+__host__ __device__ inline vxm_parts vxm_one_part(const float *p) { return vxm_parts{p, 1, 0}; }
+
+constexpr int VXM_SMALL_MAX_ROWS = 64;   // rows of x the small-M GEMM takes
+constexpr int VXM_MAX_PARTS = 8;         // its K splits
+
+// The product as up to max_parts slices of M x N at y, y + M*N, ...; *parts = the
+// number written (1 unless the small-M GEMM splits K).
+int vxm_launch_mul_mat_parts(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd,
+                             int64_t M, float *y, int max_parts, int *parts);
 int vxm_ensure_act(vxm_ctx *ctx, size_t bytes);
+int vxm_ensure_parts(vxm_ctx *ctx, size_t bytes);
 int vxm_ensure_split(vxm_ctx *ctx, size_t bytes, size_t n_counters);

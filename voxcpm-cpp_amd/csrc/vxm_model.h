@@ -34,6 +34,8 @@ struct vxm_workspace {
     uint16_t *xd = nullptr;
     float *qkv = nullptr, *q = nullptr, *att = nullptr, *o = nullptr, *gu = nullptr, *dn = nullptr;
     uint16_t *lk = nullptr, *lv = nullptr;   // fresh K/V of non-causal runs
+    int max_parts = 1;                       // K-split slices the projection buffers hold
+    vxm_parts dn_out{};                      // the last block's down projection (slices of dn)
 };
 
 // Where a block's attention reads and writes K/V.

@@ -2,15 +2,15 @@
 #pragma once
 #include "vxm_internal.h"
 
-int vxm_launch_rmsnorm(vxm_ctx *ctx, float *h, const float *delta, float res_scale, const float *gain,
+int vxm_launch_rmsnorm(vxm_ctx *ctx, float *h, vxm_parts delta, float res_scale, const float *gain,
                        int64_t rows, int64_t n, float eps, float *y, int8_t *xq, uint16_t *xd, int variant);
-int vxm_launch_rope_kv(vxm_ctx *ctx, const float *qkv, int64_t M, int nh, int nkv, int hd, int pos0, int S,
+int vxm_launch_rope_kv(vxm_ctx *ctx, vxm_parts qkv, int64_t M, int nh, int nkv, int hd, int pos0, int S,
                        const float2 *cs, int cs_rows, int no_rope, float *q_out, uint16_t *kc,
                        uint16_t *vc, int cap, int64_t seg_stride, int cache_pos0);
 int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
                          int64_t M, int nh, int nkv, int hd, int cap, int64_t seg_stride, int S, int kv_base,
                          int causal);
-int vxm_launch_swiglu_quant(vxm_ctx *ctx, const float *gu, int64_t M, int64_t F, int64_t ld, int8_t *xq,
+int vxm_launch_swiglu_quant(vxm_ctx *ctx, vxm_parts gu, int64_t M, int64_t F, int64_t ld, int8_t *xq,
                             uint16_t *xd, float *p_out, int variant);
-int vxm_launch_residual(vxm_ctx *ctx, float *h, const float *delta, float scale, int64_t n);
+int vxm_launch_residual(vxm_ctx *ctx, float *h, vxm_parts delta, float scale, int64_t n);
 int vxm_launch_bias_bf16(vxm_ctx *ctx, const float *x, const float *bias, float *y, int64_t rows, int64_t n);

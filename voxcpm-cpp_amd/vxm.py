@@ -23,6 +23,7 @@ QUANT_X86 = 1
 PATH_AUTO = 0
 PATH_GEMV = 1
 PATH_MFMA = 2
+PATH_MFMA_TILED = 3
 
 STATUS = {
     0: "VXM_OK",
