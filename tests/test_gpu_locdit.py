@@ -214,6 +214,39 @@ def test_cfm_full_size_one_step_and_repeatable(vxm_ctx, orc):
     m.free()
 
 
+def test_cfm_graph_replays_match_eager(vxm_ctx, orc):
+    """vxm_cfm_solve records its Euler loop as a HIP graph on the second call with the
+    same arguments and buffers and replays it afterwards: every replay, with eager work
+    and synchronizations in between, is bit-identical to the eager first call; a call
+    with other arguments runs eagerly and the recorded loop still replays correctly."""
+    import torch
+
+    m, _, _ = _model(vxm_ctx, orc, 81, **FULL)
+    x0, cond, mu = make_inputs(82, 4, 17, 64, 1024)
+    cd, md = _dev(cond), _dev(mu)
+    x0d = _dev(x0)
+    x = torch.empty_like(x0d)
+    other = _dev(x0[:1])
+
+    def solve(n_steps=10):
+        x.copy_(x0d)
+        m.cfm_solve(x, cd, md, n_steps, 2.0, 1, True)
+        torch.cuda.synchronize()
+        return x.cpu().numpy()
+
+    eager = solve()                      # first call with this key: eager
+    assert np.isfinite(eager).all() and not np.array_equal(eager, x0)
+    for rep in range(4):                 # recorded, then replayed
+        assert np.array_equal(solve(), eager), f"run {rep + 2}"
+        m.forward(other, None, 0.25)     # eager work on the same model between replays
+        torch.cuda.synchronize()
+    five = solve(5)                      # another key: eager
+    assert not np.array_equal(five, eager)
+    for rep in range(3):                 # back to the first key: eager, recorded, replayed
+        assert np.array_equal(solve(), eager), f"return run {rep}"
+    m.free()
+
+
 def test_locdit_rejects_bad_sizes(vxm_ctx, orc):
     import vxm
 

@@ -48,6 +48,10 @@ struct vxm_locdit {
     float *pin = nullptr;
     size_t pin_floats = 0;
     hipEvent_t pin_done = nullptr;
+    // the Euler loop of vxm_cfm_solve as a HIP graph, valid for one set of
+    // arguments and device buffers (cfm_key); built on the second call with a key
+    hipGraphExec_t cfm_exec = nullptr;
+    std::vector<uint64_t> cfm_key, cfm_last_eager;
 };
 
 // ---------------------------------------------------------------------------
@@ -327,6 +331,27 @@ static int prepare(vxm_locdit *m, const float *cond, int32_t P, int32_t Pc, int 
     return VXM_OK;
 }
 
+// Everything a recorded Euler loop depends on: arguments, the device buffers
+// its launches address, and the context settings that pick its kernels.
+static std::vector<uint64_t> cfm_graph_key(vxm_locdit *m, const float *x, const float *cond, const float *mu,
+                                           int P, int Pc, int n_steps, float cfg_value, int schedule, int zero_star) {
+    vxm_ctx *ctx = m->ctx;
+    uint32_t cfg_bits;
+    memcpy(&cfg_bits, &cfg_value, 4);
+    return {(uint64_t)(uintptr_t)x, (uint64_t)(uintptr_t)cond, (uint64_t)(uintptr_t)mu, (uint64_t)P, (uint64_t)Pc,
+            (uint64_t)n_steps, cfg_bits, (uint64_t)schedule, (uint64_t)zero_star, (uint64_t)ctx->path,
+            (uint64_t)ctx->quant_variant, (uint64_t)ctx->n_cu, (uint64_t)(uintptr_t)m->ws.base, m->ws.bytes,
+            (uint64_t)(uintptr_t)m->buf, m->buf_bytes, (uint64_t)(uintptr_t)m->dims.rope_cs,
+            (uint64_t)m->dims.rope_rows, (uint64_t)(uintptr_t)ctx->parts_buf, ctx->parts_bytes,
+            (uint64_t)(uintptr_t)ctx->split_buf, ctx->split_bytes};
+}
+
+static void cfm_graph_drop(vxm_locdit *m) {
+    if (m->cfm_exec) (void)hipGraphExecDestroy(m->cfm_exec);
+    m->cfm_exec = nullptr;
+    m->cfm_key.clear();
+}
+
 static int cfm_update(vxm_locdit *m, int P, int use_cfg, float cfg_value, float dt, float *x, float *v_out) {
     vxm_ctx *ctx = m->ctx;
     const int feat = m->cfg.feat_dim, n = P * feat;
@@ -349,6 +374,7 @@ extern "C" int vxm_locdit_free(vxm_locdit *m) {
         if (w) vxm_weight_free(ctx, w);
     for (float *p : {m->in_bias, m->cond_bias, m->out_bias, m->norm, m->t_b1, m->t_b2, m->dt_b1, m->dt_b2})
         if (p) (void)hipFree(p);
+    cfm_graph_drop(m);
     vxm_rope_free(m->dims);
     vxm_ws_free(m->ws);
     if (m->buf) (void)hipFree(m->buf);
@@ -459,9 +485,46 @@ extern "C" int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev,
     if ((rc = prepare(m, cond_dev, P, Pc, live, n_seg))) return rc;
     if ((rc = time_features(m, ts.data(), live, 0.0f))) return rc;   // dt input is 0 (src/gen_step.c:601)
     const int64_t H = m->dims.H;
-    for (int k = 0; k < live; k++) {
-        if ((rc = dit_eval(m, x_dev, P, Pc, n_seg, mu_dev, 1, m->tc + (int64_t)k * H))) return rc;
-        if ((rc = cfm_update(m, P, use_cfg, cfg_value, dts[k], x_dev, nullptr))) return rc;
+    auto euler_loop = [&]() -> int {
+        for (int k = 0; k < live; k++) {
+            int r = dit_eval(m, x_dev, P, Pc, n_seg, mu_dev, 1, m->tc + (int64_t)k * H);
+            if (r == VXM_OK) r = cfm_update(m, P, use_cfg, cfg_value, dts[k], x_dev, nullptr);
+            if (r) return r;
+        }
+        return VXM_OK;
+    };
+    // The loop is ~100 dependent launches per step: replay it as one HIP graph
+    // when this call's key matches the recorded one; record it on the second
+    // call with a key (the first, eager, call grows every buffer it needs, so
+    // nothing allocates under capture).
+    vxm_ctx *ctx = m->ctx;
+    const std::vector<uint64_t> key = cfm_graph_key(m, x_dev, cond_dev, mu_dev, P, Pc, n_steps, cfg_value,
+                                                    schedule, use_zero_star);
+    if (m->cfm_exec && key == m->cfm_key) {
+        VXM_HIP(ctx, hipGraphLaunch(m->cfm_exec, ctx->stream));
+        return VXM_OK;
     }
+    if (key != m->cfm_last_eager) {
+        m->cfm_last_eager = key;
+        return euler_loop();
+    }
+    cfm_graph_drop(m);
+    VXM_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    rc = euler_loop();
+    ctx->capturing = false;
+    hipGraph_t graph = nullptr;
+    const hipError_t ec = hipStreamEndCapture(ctx->stream, &graph);
+    if (rc == VXM_OK && ec != hipSuccess)
+        rc = vxm_fail(ctx, VXM_ERR_BACKEND, "cfm: graph capture failed: %s", hipGetErrorString(ec));
+    if (rc == VXM_OK && hipGraphInstantiate(&m->cfm_exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+        m->cfm_exec = nullptr;
+        rc = vxm_fail(ctx, VXM_ERR_BACKEND, "cfm: graph instantiation failed");
+    }
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipGetLastError();
+    if (rc) return rc;
+    m->cfm_key = key;
+    VXM_HIP(ctx, hipGraphLaunch(m->cfm_exec, ctx->stream));
     return VXM_OK;
 }

@@ -207,14 +207,24 @@ int vxm_block_run(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_block &b, vxm
     const int var = ctx->quant_variant;
     int rc, np;
     if ((rc = vxm_launch_mul_mat_parts(ctx, b.wqkv, ws.xq, ws.xd, M, ws.qkv, ws.max_parts, &np))) return rc;
-    if ((rc = vxm_launch_rope_kv(ctx, vxm_parts{ws.qkv, np, M * (qd + 2 * kvd)}, M, d.nh, d.nkv, d.hd, site.pos0,
-                                 site.S, d.rope_cs, d.rope_rows, d.no_rope, ws.q, site.kc, site.vc, site.cap,
-                                 site.seg_stride, site.cache_pos0)))
-        return rc;
-    if ((rc = vxm_launch_attention(ctx, ws.q, site.kc, site.vc, ws.att, M, d.nh, d.nkv, d.hd, site.cap,
-                                   site.seg_stride, site.S, site.cache_pos0, site.causal)))
-        return rc;
-    if ((rc = vxm_launch_quantize(ctx, ws.att, M, qd, var, ws.xq, ws.xd))) return rc;
+    const bool local = !site.causal && site.cache_pos0 == 0 && site.S > 0 && M % site.S == 0 &&
+                       vxm_attention_local_fits(site.S, d.hd);
+    if (local) {
+        // fresh K/V within each segment: RoPE, attention and the output's Q8_0 in one launch
+        if ((rc = vxm_launch_attention_local(ctx, vxm_parts{ws.qkv, np, M * (qd + 2 * kvd)}, M, d.nh, d.nkv, d.hd,
+                                             site.S, site.pos0, d.rope_cs, d.rope_rows, d.no_rope, ws.xq, ws.xd,
+                                             var)))
+            return rc;
+    } else {
+        if ((rc = vxm_launch_rope_kv(ctx, vxm_parts{ws.qkv, np, M * (qd + 2 * kvd)}, M, d.nh, d.nkv, d.hd,
+                                     site.pos0, site.S, d.rope_cs, d.rope_rows, d.no_rope, ws.q, site.kc, site.vc,
+                                     site.cap, site.seg_stride, site.cache_pos0)))
+            return rc;
+        if ((rc = vxm_launch_attention(ctx, ws.q, site.kc, site.vc, ws.att, M, d.nh, d.nkv, d.hd, site.cap,
+                                       site.seg_stride, site.S, site.cache_pos0, site.causal)))
+            return rc;
+        if ((rc = vxm_launch_quantize(ctx, ws.att, M, qd, var, ws.xq, ws.xd))) return rc;
+    }
     if ((rc = vxm_launch_mul_mat_parts(ctx, b.wo, ws.xq, ws.xd, M, ws.o, ws.max_parts, &np))) return rc;
     // x = bf16(x + scale*bf16(o)); post-attention norm -> Q8_0
     if ((rc = vxm_launch_rmsnorm(ctx, x, vxm_parts{ws.o, np, M * d.H}, d.res_scale, b.g_post, M, d.H, d.eps, nullptr,

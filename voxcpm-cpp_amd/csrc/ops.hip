@@ -454,6 +454,215 @@ int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const
 }
 
 // ---------------------------------------------------------------------------
+// Non-causal attention within segments of S tokens at positions pos0 ..
+// pos0+S-1 with fresh K/V (the LocDiT and LocEnc blocks): k_rope_kv, the
+// f16 K/V rounding, k_attention and the Q8_0 quantization of the output in
+// one launch, with the same rounding steps and summation orders as those
+// kernels.  One workgroup (256 threads) per (query head, segment) keeps the
+// segment's q of its head and k, v of its kv head in LDS; qkv may arrive as
+// K-split slices.  Output: the Q8_0 rows of the attention output (xq, xd).
+// ---------------------------------------------------------------------------
+constexpr int kLocalMaxS = 64, kLocalMaxElems = 2048;   // S, and S * hd per operand
+
+bool vxm_attention_local_fits(int S, int hd) {
+    return S >= 1 && S <= kLocalMaxS && (hd == 64 || hd == 128) && (int64_t)S * hd <= kLocalMaxElems;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, int nh, int nkv, int S, int pos0,
+                                                         const float2 *__restrict__ cs, int no_rope,
+                                                         int8_t *__restrict__ xq, uint16_t *__restrict__ xd,
+                                                         int variant) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    constexpr int HALF = HD / 2, HP = HD + 4;
+    const int h = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    const int kvh = h / (nh / nkv);
+    const int qd = nh * HD, kvd = nkv * HD, ld = qd + 2 * kvd;
+    const int SP = S + 1;
+    // raw q (later the output), raw k, v: [S][HD]; rotated q, rotated k: [S][HD + 4]
+    // (the pad spreads the score loop's 16-byte row reads over the banks); P: [S][S + 1];
+    // row max and 1/sum: [S] each
+    float *Qr = lds, *Kr = Qr + S * HD, *V = Kr + S * HD, *Q = V + S * HD, *Kf = Q + S * HP, *P = Kf + S * HP;
+    float *mx = P + S * SP, *inv = mx + S;
+    // 1. the segment's raw q (head h), k and v (kv head kvh) rows, K-split slices added
+    //    in order; the loads of up to four slices are in flight together
+    {
+        constexpr int kMaxPer = (3 * kLocalMaxElems / 4 + 255) / 256;   // float4s per thread
+        constexpr int PR = 3 * HD / 4;                                 // float4s per row
+        const int total = S * PR;
+        int64_t src[kMaxPer];
+        float4 acc4[kMaxPer];
+#pragma unroll
+        for (int k = 0; k < kMaxPer; k++) {
+            const int f = min(tid + 256 * k, total - 1);
+            const int ti = f / PR, c4 = f % PR, part = c4 / (HD / 4), off = 4 * (c4 % (HD / 4));
+            const int col = part == 0 ? h * HD : part == 1 ? qd + kvh * HD : qd + kvd + kvh * HD;
+            src[k] = (int64_t)(g * S + ti) * ld + col + off;
+            acc4[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        for (int z0 = 0; z0 < qkv.n; z0 += 4) {
+            float4 b[4][kMaxPer];
+            // threads past the end load (and drop) the last element: no divergent loads
+#pragma unroll
+            for (int zz = 0; zz < 4; zz++)
+#pragma unroll
+                for (int k = 0; k < kMaxPer; k++)
+                    if (z0 + zz < qkv.n) b[zz][k] = *(const float4 *)(qkv.p + (z0 + zz) * qkv.stride + src[k]);
+#pragma unroll
+            for (int zz = 0; zz < 4; zz++)
+#pragma unroll
+                for (int k = 0; k < kMaxPer; k++)
+                    if (z0 + zz < qkv.n) {
+                        if (z0 + zz == 0) {
+                            acc4[k] = b[zz][k];
+                        } else {
+                            acc4[k].x = acc4[k].x + b[zz][k].x; acc4[k].y = acc4[k].y + b[zz][k].y;
+                            acc4[k].z = acc4[k].z + b[zz][k].z; acc4[k].w = acc4[k].w + b[zz][k].w;
+                        }
+                    }
+        }
+#pragma unroll
+        for (int k = 0; k < kMaxPer; k++) {
+            const int f = tid + 256 * k;
+            if (f < total) {
+                const int ti = f / PR, c4 = f % PR, part = c4 / (HD / 4), off = 4 * (c4 % (HD / 4));
+                *(float4 *)((part == 0 ? Qr : part == 1 ? Kr : V) + ti * HD + off) = acc4[k];
+            }
+        }
+    }
+    __syncthreads();
+    // 2. BF16 + RoPE of q and k (pair-interleaved rows: row 2i = dim i, 2i+1 = dim
+    //    i + hd/2), the f16 cache rounding of k and v
+    for (int idx = tid; idx < S * HALF; idx += 256) {
+        const int ti = idx / HALF, i = idx % HALF;
+        float c = 1.0f, sn = 0.0f;
+        if (!no_rope) {
+            const float2 r = cs[(int64_t)(pos0 + ti) * HALF + i];
+            c = r.x;
+            sn = r.y;
+        }
+#pragma unroll
+        for (int which = 0; which < 2; which++) {
+            const float *sp = (which ? Kr : Qr) + ti * HD;
+            const float x0 = vxm_bf16(sp[2 * i]), x1 = vxm_bf16(sp[2 * i + 1]);
+            float y0 = x0, y1 = x1;
+            if (!no_rope) {
+                y0 = vxm_bf16(x0 * c - x1 * sn);
+                y1 = vxm_bf16(x0 * sn + x1 * c);
+            }
+            if (which) {
+                y0 = vxm_h2f(vxm_f2h(y0));
+                y1 = vxm_h2f(vxm_f2h(y1));
+            }
+            float *dst = (which ? Kf : Q) + ti * HP;
+            dst[i] = y0;
+            dst[i + HALF] = y1;
+        }
+    }
+    for (int idx = tid; idx < S * HD; idx += 256) V[idx] = vxm_h2f(vxm_f2h(vxm_bf16(V[idx])));
+    __syncthreads();
+    // 3. scores s_ij = (k_j . q_i) * scale, d in order
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
+    for (int idx = tid; idx < S * S; idx += 256) {
+        const int i = idx / S, j = idx % S;
+        const float4 *kr = (const float4 *)(Kf + j * HP), *qr = (const float4 *)(Q + i * HP);
+        float sc = 0.0f;
+#pragma unroll 8
+        for (int d4 = 0; d4 < HD / 4; d4++) {
+            const float4 a = kr[d4], b = qr[d4];
+            sc += a.x * b.x;
+            sc += a.y * b.y;
+            sc += a.z * b.z;
+            sc += a.w * b.w;
+        }
+        P[i * SP + j] = sc * scale;
+    }
+    __syncthreads();
+    // 4. softmax: row max, exponentials, the row sum in double and (float)(1/sum)
+    if (tid < S) {
+        float m = -INFINITY;
+        for (int j = 0; j < S; j++) m = fmaxf(m, P[tid * SP + j]);
+        mx[tid] = m;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < S * S; idx += 256) {
+        const int i = idx / S, j = idx % S;
+        P[i * SP + j] = expf(P[i * SP + j] - mx[i]);
+    }
+    __syncthreads();
+    if (tid < S) {
+        double sum = 0.0;
+        for (int j = 0; j < S; j++) sum += (double)P[tid * SP + j];
+        inv[tid] = (float)(1.0 / sum);
+    }
+    __syncthreads();
+    // 5. out[i][d] = sum_j v[j][d] p_ij, p_ij = e_ij * inv_i, over the j-slices of
+    //    k_attention (256 / hd of them, each summed in order, then added in order);
+    //    thread (row group rg, dim d) owns rows rg, rg + R, ...
+    {
+        constexpr int R = 256 / HD, MAXR = kLocalMaxElems / 256;
+        const int d = tid % HD, rg = tid / HD;
+        const int slices = 256 / HD, jper = (S + slices - 1) / slices;
+        // rows past S read row S - 1 with a zero weight: the loop has no divergent reads
+        float tot[MAXR], acc[MAXR], iv[MAXR];
+        int prow[MAXR];
+#pragma unroll
+        for (int k = 0; k < MAXR; k++) {
+            tot[k] = 0.0f;
+            iv[k] = rg + R * k < S ? inv[rg + R * k] : 0.0f;
+            prow[k] = min(rg + R * k, S - 1) * SP;
+        }
+        for (int sl = 0; sl < slices; sl++) {
+            const int j0 = sl * jper, j1 = min(S, j0 + jper);
+#pragma unroll
+            for (int k = 0; k < MAXR; k++) acc[k] = 0.0f;
+            for (int j = j0; j < j1; j++) {
+                const float v = V[j * HD + d];
+#pragma unroll
+                for (int k = 0; k < MAXR; k++) acc[k] += v * (P[prow[k] + j] * iv[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < MAXR; k++) tot[k] += acc[k];
+        }
+#pragma unroll
+        for (int k = 0; k < MAXR; k++)
+            if (rg + R * k < S) Qr[(rg + R * k) * HD + d] = tot[k];
+    }
+    __syncthreads();
+    // 6. Q8_0 of the output rows: thread (i, c) holds dims 8c .. 8c+7, four consecutive
+    //    threads one 32-block (S * HD / 8 % 4 == 0: whole 4-lane groups stop together)
+    constexpr int CPR = HD / 8;
+    for (int idx = tid; idx < S * CPR; idx += 256) {
+        const int i = idx / CPR, c = idx % CPR;
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = Qr[i * HD + 8 * c + e];
+        const int64_t el = (int64_t)(g * S + i) * qd + h * HD + 8 * c;
+        quant_block_4lanes(o, variant, xq + el, xd + el / 32, (tid & 3) == 0);
+    }
+}
+
+int vxm_launch_attention_local(vxm_ctx *ctx, vxm_parts qkv, int64_t M, int nh, int nkv, int hd, int S, int pos0,
+                               const float2 *cs, int cs_rows, int no_rope, int8_t *xq, uint16_t *xd, int variant) {
+    if (M <= 0) return VXM_OK;
+    if (!vxm_attention_local_fits(S, hd) || M % S || nkv <= 0 || nh % nkv)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "local attention: S=%d hd=%d M=%lld unsupported", S, hd,
+                        (long long)M);
+    if (!no_rope && (!cs || pos0 + S > cs_rows))
+        return vxm_fail(ctx, VXM_ERR_BACKEND, "rope: table holds %d positions, %d needed", cs_rows, pos0 + S);
+    const size_t lds = (size_t)(3 * S * hd + 2 * S * (hd + 4) + S * (S + 1) + 2 * S) * sizeof(float);
+    const dim3 grid(nh, (unsigned)(M / S));
+    if (hd == 64)
+        hipLaunchKernelGGL(k_attention_local<64>, grid, dim3(256), lds, ctx->stream, qkv, nh, nkv, S, pos0, cs, no_rope,
+                           xq, xd, variant);
+    else
+        hipLaunchKernelGGL(k_attention_local<128>, grid, dim3(256), lds, ctx->stream, qkv, nh, nkv, S, pos0, cs,
+                           no_rope, xq, xd, variant);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}
+
+// ---------------------------------------------------------------------------
 // vcpm_mlp activation (src/minicpm4.c:441-456): p = bf16(bf16(silu(bf16(g))) *
 // bf16(u)), silu(x) = x / (1 + expf(-x)), then Q8_0 quantization of p.
 // Row m of the fused gate/up projection holds 2F values interleaved: gate n at

@@ -14,3 +14,6 @@ int vxm_launch_swiglu_quant(vxm_ctx *ctx, vxm_parts gu, int64_t M, int64_t F, in
                             uint16_t *xd, float *p_out, int variant);
 int vxm_launch_residual(vxm_ctx *ctx, float *h, vxm_parts delta, float scale, int64_t n);
 int vxm_launch_bias_bf16(vxm_ctx *ctx, const float *x, const float *bias, float *y, int64_t rows, int64_t n);
+bool vxm_attention_local_fits(int S, int hd);
+int vxm_launch_attention_local(vxm_ctx *ctx, vxm_parts qkv, int64_t M, int nh, int nkv, int hd, int S, int pos0,
+                               const float2 *cs, int cs_rows, int no_rope, int8_t *xq, uint16_t *xd, int variant);
