@@ -85,13 +85,21 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const vx
             v[c][0] = a.x; v[c][1] = a.y; v[c][2] = a.z; v[c][3] = a.w;
             v[c][4] = b.x; v[c][5] = b.y; v[c][6] = b.z; v[c][7] = b.w;
             if (dr) {
-                float4 p = *(const float4 *)(dr + base), q = *(const float4 *)(dr + base + 4);
-                for (int z = 1; z < delta.n; z++) {   // K-split slices, added in order
-                    const float4 p2 = *(const float4 *)(dr + z * delta.stride + base);
-                    const float4 q2 = *(const float4 *)(dr + z * delta.stride + base + 4);
-                    p.x = p.x + p2.x; p.y = p.y + p2.y; p.z = p.z + p2.z; p.w = p.w + p2.w;
-                    q.x = q.x + q2.x; q.y = q.y + q2.y; q.z = q.z + q2.z; q.w = q.w + q2.w;
-                }
+                // K-split slices: all loads in flight, then added in order
+                float4 ps[VXM_MAX_PARTS], qs[VXM_MAX_PARTS];
+#pragma unroll
+                for (int z = 0; z < VXM_MAX_PARTS; z++)
+                    if (z < delta.n) {
+                        ps[z] = *(const float4 *)(dr + z * delta.stride + base);
+                        qs[z] = *(const float4 *)(dr + z * delta.stride + base + 4);
+                    }
+                float4 p = ps[0], q = qs[0];
+#pragma unroll
+                for (int z = 1; z < VXM_MAX_PARTS; z++)
+                    if (z < delta.n) {
+                        p.x = p.x + ps[z].x; p.y = p.y + ps[z].y; p.z = p.z + ps[z].z; p.w = p.w + ps[z].w;
+                        q.x = q.x + qs[z].x; q.y = q.y + qs[z].y; q.z = q.z + qs[z].z; q.w = q.w + qs[z].w;
+                    }
                 float dd[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
@@ -679,10 +687,18 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const vxm_parts gu, int64_
     float gv[8], uv[8];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
+        // K-split slices: up to four loads in flight, added in order
         float4 a = *(const float4 *)(s + 4 * k);
-        for (int z = 1; z < gu.n; z++) {   // K-split slices, added in order
-            const float4 b = *(const float4 *)(s + z * gu.stride + 4 * k);
-            a.x = a.x + b.x; a.y = a.y + b.y; a.z = a.z + b.z; a.w = a.w + b.w;
+        for (int z0 = 1; z0 < gu.n; z0 += 4) {
+            float4 b[4];
+#pragma unroll
+            for (int zz = 0; zz < 4; zz++)
+                if (z0 + zz < gu.n) b[zz] = *(const float4 *)(s + (z0 + zz) * gu.stride + 4 * k);
+#pragma unroll
+            for (int zz = 0; zz < 4; zz++)
+                if (z0 + zz < gu.n) {
+                    a.x = a.x + b[zz].x; a.y = a.y + b[zz].y; a.z = a.z + b[zz].z; a.w = a.w + b[zz].w;
+                }
         }
         gv[2 * k] = a.x; uv[2 * k] = a.y; gv[2 * k + 1] = a.z; uv[2 * k + 1] = a.w;
     }

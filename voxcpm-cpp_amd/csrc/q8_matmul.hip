@@ -568,41 +568,58 @@ __global__ __launch_bounds__(64 * kSmallRG) void k_gemm_q8_0_small(const int8_t 
     for (int t = 0; t < MT; t++)
 #pragma unroll
         for (int v = 0; v < 4; v++) acc[t][v] = 0.0f;
-    for (int kb0 = zb0; kb0 < zb1; kb0 += SB) {
-        // weight pairs and scales of this stage (HBM): issued first, consumed after the staging
-        v4i wv[SB / 2], dwv[4];
+    // One stage's operands in registers: weight pairs and scales (HBM), activation
+    // pieces and scales (L2).  The next stage's loads are issued before this stage's
+    // products, two register sets alternating.
+    constexpr int PIECES = ROWS * SB * 2, PPT = (PIECES + NT - 1) / NT, SPT = (ROWS * SB + NT - 1) / NT;
+    struct Stage {
+        v4i wv[SB / 2], dwv[4], xv[PPT];
+        uint16_t xh[SPT];
+    };
+    auto issue = [&](Stage &st, int kb0) {
 #pragma unroll
         for (int p = 0; p < SB / 2; p++)
-            wv[p] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, (nw + r) * K + (kb0 + 2 * p) * 32 + 16 * q, 0, 0);
+            st.wv[p] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, (nw + r) * K + (kb0 + 2 * p) * 32 + 16 * q, 0, 0);
 #pragma unroll
         for (int v = 0; v < 4; v++)
-            dwv[v] = __builtin_amdgcn_raw_buffer_load_b128(wd_rsrc, ((nw + 4 * q + v) * nb + kb0) * 2, 0, 0);
-        // activations of the stage -> LDS: 16-byte piece c = (row, block, half)
-        __syncthreads();   // the previous stage's LDS reads are done
-        constexpr int PIECES = ROWS * SB * 2;
+            st.dwv[v] = __builtin_amdgcn_raw_buffer_load_b128(wd_rsrc, ((nw + 4 * q + v) * nb + kb0) * 2, 0, 0);
+        // activation piece c = (row, block, half); threads past the end reload the last piece
 #pragma unroll
-        for (int c0 = 0; c0 < PIECES; c0 += NT) {
-            const int c = c0 + tid;
+        for (int k = 0; k < PPT; k++) {
+            const int c = min(k * NT + tid, PIECES - 1);
+            const int row = c / (2 * SB), b = (c / 2) % SB, h = c & 1;
+            st.xv[k] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, row * K + (kb0 + b) * 32 + 16 * h, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < SPT; k++) {
+            const int c = min(k * NT + tid, ROWS * SB - 1);
+            st.xh[k] = __builtin_amdgcn_raw_buffer_load_b16(xd_rsrc, ((c / SB) * nb + kb0 + c % SB) * 2, 0, 0);
+        }
+    };
+    auto run = [&](const Stage &st, int kb0) {
+        __syncthreads();   // the previous stage's LDS reads are done
+#pragma unroll
+        for (int k = 0; k < PPT; k++) {
+            const int c = k * NT + tid;
             if (PIECES % NT == 0 || c < PIECES) {
                 const int row = c / (2 * SB), b = (c / 2) % SB, h = c & 1;
-                const v4i v = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, row * K + (kb0 + b) * 32 + 16 * h, 0, 0);
                 int8_t *dst = xs + row * kSmallPitch + b * 32;
-                *(long *)(dst + 8 * h) = pack64((uint32_t)v.x, (uint32_t)v.y);
-                *(long *)(dst + 8 * h + 16) = pack64((uint32_t)v.z, (uint32_t)v.w);
+                *(long *)(dst + 8 * h) = pack64((uint32_t)st.xv[k].x, (uint32_t)st.xv[k].y);
+                *(long *)(dst + 8 * h + 16) = pack64((uint32_t)st.xv[k].z, (uint32_t)st.xv[k].w);
             }
         }
-        for (int c = tid; c < ROWS * SB; c += NT) {
-            const int row = c / SB, b = c % SB;
-            const uint16_t hv = __builtin_amdgcn_raw_buffer_load_b16(xd_rsrc, (row * nb + kb0 + b) * 2, 0, 0);
-            xds[row][b] = kb0 + b < zb1 ? vxm_h2f(hv) : 0.0f;
+#pragma unroll
+        for (int k = 0; k < SPT; k++) {
+            const int c = k * NT + tid;
+            if ((ROWS * SB) % NT == 0 || c < ROWS * SB) xds[c / SB][c % SB] = kb0 + c % SB < zb1 ? vxm_h2f(st.xh[k]) : 0.0f;
         }
         __syncthreads();
         // per block pair: the pair's operands, then all 2 MT products, then their scaling
 #pragma unroll
         for (int p = 0; p < SB / 2; p++) {
             // lanes 0-31 trade their high halves for the low halves of lanes 32-63
-            const auto s0 = __builtin_amdgcn_permlane32_swap((uint32_t)wv[p].x, (uint32_t)wv[p].z, false, false);
-            const auto s1 = __builtin_amdgcn_permlane32_swap((uint32_t)wv[p].y, (uint32_t)wv[p].w, false, false);
+            const auto s0 = __builtin_amdgcn_permlane32_swap((uint32_t)st.wv[p].x, (uint32_t)st.wv[p].z, false, false);
+            const auto s1 = __builtin_amdgcn_permlane32_swap((uint32_t)st.wv[p].y, (uint32_t)st.wv[p].w, false, false);
             const long a[2] = {pack64(s0[0], s1[0]), pack64(s0[1], s1[1])};
             long bx[2][MT];
             float dx[2][MT];
@@ -623,7 +640,7 @@ __global__ __launch_bounds__(64 * kSmallRG) void k_gemm_q8_0_small(const int8_t 
                 const int b = 2 * p + e;
                 float dw[4];
 #pragma unroll
-                for (int v = 0; v < 4; v++) dw[v] = half_at(dwv[v], b);
+                for (int v = 0; v < 4; v++) dw[v] = half_at(st.dwv[v], b);
 #pragma unroll
                 for (int t = 0; t < MT; t++)
 #pragma unroll
@@ -631,6 +648,16 @@ __global__ __launch_bounds__(64 * kSmallRG) void k_gemm_q8_0_small(const int8_t 
                         acc[t][v] = __builtin_fmaf((float)c[e][t][v], dw[v] * dx[e][t], acc[t][v]);
             }
         }
+    };
+    Stage sa, sb;
+    if (zb0 < zb1) issue(sa, zb0);
+    for (int kb0 = zb0; kb0 < zb1; kb0 += 2 * SB) {
+        const bool b_live = kb0 + SB < zb1;
+        if (b_live) issue(sb, kb0 + SB);
+        run(sa, kb0);
+        if (!b_live) break;
+        if (kb0 + 2 * SB < zb1) issue(sa, kb0 + 2 * SB);
+        run(sb, kb0 + SB);
     }
     float *yz = y + (int64_t)z * M * N;
 #pragma unroll
