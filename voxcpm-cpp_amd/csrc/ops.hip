@@ -477,40 +477,52 @@ bool vxm_attention_local_fits(int S, int hd) {
 }
 
 template <int HD>
-__global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, int nh, int nkv, int S, int pos0,
+__global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, int nh, int nkv, int S, int RB, int pos0,
                                                          const float2 *__restrict__ cs, int no_rope,
                                                          int8_t *__restrict__ xq, uint16_t *__restrict__ xd,
                                                          int variant) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     constexpr int HALF = HD / 2, HP = HD + 4;
     const int h = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    const int q0 = blockIdx.z * RB, nq = min(RB, S - q0);   // this workgroup's query rows
     const int kvh = h / (nh / nkv);
     const int qd = nh * HD, kvd = nkv * HD, ld = qd + 2 * kvd;
     const int SP = S + 1;
-    // raw q (later the output), raw k, v: [S][HD]; rotated q, rotated k: [S][HD + 4]
-    // (the pad spreads the score loop's 16-byte row reads over the banks); P: [S][S + 1];
-    // row max and 1/sum: [S] each
-    float *Qr = lds, *Kr = Qr + S * HD, *V = Kr + S * HD, *Q = V + S * HD, *Kf = Q + S * HP, *P = Kf + S * HP;
-    float *mx = P + S * SP, *inv = mx + S;
-    // 1. the segment's raw q (head h), k and v (kv head kvh) rows, K-split slices added
-    //    in order; the loads of up to four slices are in flight together
+    // raw k, v: [S][HD]; raw q (later the output): [RB][HD]; rotated k: [S][HD + 4],
+    // rotated q: [RB][HD + 4] (the pad spreads the score loop's 16-byte row reads over
+    // the banks); P: [RB][S + 1]; row max and 1/sum: [RB] each
+    float *Kr = lds, *V = Kr + S * HD, *Qr = V + S * HD, *Kf = Qr + RB * HD, *Q = Kf + S * HP, *P = Q + RB * HP;
+    float *mx = P + RB * SP, *inv = mx + RB;
+    // 1. raw q (rows q0 .. q0+nq-1 of head h), k and v (all S rows of kv head kvh),
+    //    K-split slices added in order; the loads of up to four slices are in flight together
     {
         constexpr int kMaxPer = (3 * kLocalMaxElems / 4 + 255) / 256;   // float4s per thread
-        constexpr int PR = 3 * HD / 4;                                 // float4s per row
-        const int total = S * PR;
+        constexpr int R4 = HD / 4;                                      // float4s per row
+        const int nqf = nq * R4, total = nqf + 2 * S * R4;
         int64_t src[kMaxPer];
+        float *dst[kMaxPer];
         float4 acc4[kMaxPer];
 #pragma unroll
         for (int k = 0; k < kMaxPer; k++) {
-            const int f = min(tid + 256 * k, total - 1);
-            const int ti = f / PR, c4 = f % PR, part = c4 / (HD / 4), off = 4 * (c4 % (HD / 4));
-            const int col = part == 0 ? h * HD : part == 1 ? qd + kvh * HD : qd + kvd + kvh * HD;
-            src[k] = (int64_t)(g * S + ti) * ld + col + off;
+            const int f = min(tid + 256 * k, total - 1);   // threads past the end reload the last element
+            int row, col;
+            if (f < nqf) {
+                row = q0 + f / R4;
+                col = h * HD;
+                dst[k] = Qr + (f / R4) * HD;
+            } else {
+                const int e = f - nqf, part = e / (S * R4), rr = (e % (S * R4)) / R4;
+                row = rr;
+                col = part == 0 ? qd + kvh * HD : qd + kvd + kvh * HD;
+                dst[k] = (part == 0 ? Kr : V) + rr * HD;
+            }
+            const int off = 4 * (f % R4);
+            src[k] = (int64_t)(g * S + row) * ld + col + off;
+            dst[k] += off;
             acc4[k] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
         for (int z0 = 0; z0 < qkv.n; z0 += 4) {
             float4 b[4][kMaxPer];
-            // threads past the end load (and drop) the last element: no divergent loads
 #pragma unroll
             for (int zz = 0; zz < 4; zz++)
 #pragma unroll
@@ -530,48 +542,42 @@ __global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, in
                     }
         }
 #pragma unroll
-        for (int k = 0; k < kMaxPer; k++) {
-            const int f = tid + 256 * k;
-            if (f < total) {
-                const int ti = f / PR, c4 = f % PR, part = c4 / (HD / 4), off = 4 * (c4 % (HD / 4));
-                *(float4 *)((part == 0 ? Qr : part == 1 ? Kr : V) + ti * HD + off) = acc4[k];
-            }
-        }
+        for (int k = 0; k < kMaxPer; k++)
+            if (tid + 256 * k < total) *(float4 *)dst[k] = acc4[k];
     }
     __syncthreads();
     // 2. BF16 + RoPE of q and k (pair-interleaved rows: row 2i = dim i, 2i+1 = dim
     //    i + hd/2), the f16 cache rounding of k and v
-    for (int idx = tid; idx < S * HALF; idx += 256) {
-        const int ti = idx / HALF, i = idx % HALF;
+    for (int idx = tid; idx < (S + nq) * HALF; idx += 256) {
+        const int rr = idx / HALF, i = idx % HALF;
+        const bool isk = rr < S;
+        const int lr = isk ? rr : rr - S, pos = pos0 + (isk ? rr : q0 + lr);
         float c = 1.0f, sn = 0.0f;
         if (!no_rope) {
-            const float2 r = cs[(int64_t)(pos0 + ti) * HALF + i];
+            const float2 r = cs[(int64_t)pos * HALF + i];
             c = r.x;
             sn = r.y;
         }
-#pragma unroll
-        for (int which = 0; which < 2; which++) {
-            const float *sp = (which ? Kr : Qr) + ti * HD;
-            const float x0 = vxm_bf16(sp[2 * i]), x1 = vxm_bf16(sp[2 * i + 1]);
-            float y0 = x0, y1 = x1;
-            if (!no_rope) {
-                y0 = vxm_bf16(x0 * c - x1 * sn);
-                y1 = vxm_bf16(x0 * sn + x1 * c);
-            }
-            if (which) {
-                y0 = vxm_h2f(vxm_f2h(y0));
-                y1 = vxm_h2f(vxm_f2h(y1));
-            }
-            float *dst = (which ? Kf : Q) + ti * HP;
-            dst[i] = y0;
-            dst[i + HALF] = y1;
+        const float *sp = (isk ? Kr : Qr) + lr * HD;
+        const float x0 = vxm_bf16(sp[2 * i]), x1 = vxm_bf16(sp[2 * i + 1]);
+        float y0 = x0, y1 = x1;
+        if (!no_rope) {
+            y0 = vxm_bf16(x0 * c - x1 * sn);
+            y1 = vxm_bf16(x0 * sn + x1 * c);
         }
+        if (isk) {
+            y0 = vxm_h2f(vxm_f2h(y0));
+            y1 = vxm_h2f(vxm_f2h(y1));
+        }
+        float *dp = (isk ? Kf : Q) + lr * HP;
+        dp[i] = y0;
+        dp[i + HALF] = y1;
     }
     for (int idx = tid; idx < S * HD; idx += 256) V[idx] = vxm_h2f(vxm_f2h(vxm_bf16(V[idx])));
     __syncthreads();
     // 3. scores s_ij = (k_j . q_i) * scale, d in order
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
-    for (int idx = tid; idx < S * S; idx += 256) {
+    for (int idx = tid; idx < nq * S; idx += 256) {
         const int i = idx / S, j = idx % S;
         const float4 *kr = (const float4 *)(Kf + j * HP), *qr = (const float4 *)(Q + i * HP);
         float sc = 0.0f;
@@ -587,18 +593,18 @@ __global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, in
     }
     __syncthreads();
     // 4. softmax: row max, exponentials, the row sum in double and (float)(1/sum)
-    if (tid < S) {
+    if (tid < nq) {
         float m = -INFINITY;
         for (int j = 0; j < S; j++) m = fmaxf(m, P[tid * SP + j]);
         mx[tid] = m;
     }
     __syncthreads();
-    for (int idx = tid; idx < S * S; idx += 256) {
+    for (int idx = tid; idx < nq * S; idx += 256) {
         const int i = idx / S, j = idx % S;
         P[i * SP + j] = expf(P[i * SP + j] - mx[i]);
     }
     __syncthreads();
-    if (tid < S) {
+    if (tid < nq) {
         double sum = 0.0;
         for (int j = 0; j < S; j++) sum += (double)P[tid * SP + j];
         inv[tid] = (float)(1.0 / sum);
@@ -606,19 +612,19 @@ __global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, in
     __syncthreads();
     // 5. out[i][d] = sum_j v[j][d] p_ij, p_ij = e_ij * inv_i, over the j-slices of
     //    k_attention (256 / hd of them, each summed in order, then added in order);
-    //    thread (row group rg, dim d) owns rows rg, rg + R, ...
+    //    thread (row group rg, dim d) owns rows rg, rg + R, ...; rows past nq read row
+    //    nq - 1 with a zero weight, so the loop has no divergent reads
     {
         constexpr int R = 256 / HD, MAXR = kLocalMaxElems / 256;
         const int d = tid % HD, rg = tid / HD;
         const int slices = 256 / HD, jper = (S + slices - 1) / slices;
-        // rows past S read row S - 1 with a zero weight: the loop has no divergent reads
         float tot[MAXR], acc[MAXR], iv[MAXR];
         int prow[MAXR];
 #pragma unroll
         for (int k = 0; k < MAXR; k++) {
             tot[k] = 0.0f;
-            iv[k] = rg + R * k < S ? inv[rg + R * k] : 0.0f;
-            prow[k] = min(rg + R * k, S - 1) * SP;
+            iv[k] = rg + R * k < nq ? inv[rg + R * k] : 0.0f;
+            prow[k] = min(rg + R * k, nq - 1) * SP;
         }
         for (int sl = 0; sl < slices; sl++) {
             const int j0 = sl * jper, j1 = min(S, j0 + jper);
@@ -634,18 +640,18 @@ __global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, in
         }
 #pragma unroll
         for (int k = 0; k < MAXR; k++)
-            if (rg + R * k < S) Qr[(rg + R * k) * HD + d] = tot[k];
+            if (rg + R * k < nq) Qr[(rg + R * k) * HD + d] = tot[k];
     }
     __syncthreads();
     // 6. Q8_0 of the output rows: thread (i, c) holds dims 8c .. 8c+7, four consecutive
-    //    threads one 32-block (S * HD / 8 % 4 == 0: whole 4-lane groups stop together)
+    //    threads one 32-block (hd / 8 % 4 == 0: whole 4-lane groups stop together)
     constexpr int CPR = HD / 8;
-    for (int idx = tid; idx < S * CPR; idx += 256) {
+    for (int idx = tid; idx < nq * CPR; idx += 256) {
         const int i = idx / CPR, c = idx % CPR;
         float o[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) o[e] = Qr[i * HD + 8 * c + e];
-        const int64_t el = (int64_t)(g * S + i) * qd + h * HD + 8 * c;
+        const int64_t el = (int64_t)(g * S + q0 + i) * qd + h * HD + 8 * c;
         quant_block_4lanes(o, variant, xq + el, xd + el / 32, (tid & 3) == 0);
     }
 }
@@ -658,13 +664,16 @@ int vxm_launch_attention_local(vxm_ctx *ctx, vxm_parts qkv, int64_t M, int nh, i
                         (long long)M);
     if (!no_rope && (!cs || pos0 + S > cs_rows))
         return vxm_fail(ctx, VXM_ERR_BACKEND, "rope: table holds %d positions, %d needed", cs_rows, pos0 + S);
-    const size_t lds = (size_t)(3 * S * hd + 2 * S * (hd + 4) + S * (S + 1) + 2 * S) * sizeof(float);
-    const dim3 grid(nh, (unsigned)(M / S));
+    // query rows per workgroup: blocks of 8 spread a segment's rows over several CUs
+    // (each block re-derives the segment's k and v)
+    const int RB = S < 8 ? S : 8, QB = (S + RB - 1) / RB;
+    const size_t lds = (size_t)(2 * S * hd + RB * hd + (S + RB) * (hd + 4) + RB * (S + 1) + 2 * RB) * sizeof(float);
+    const dim3 grid(nh, (unsigned)(M / S), QB);
     if (hd == 64)
-        hipLaunchKernelGGL(k_attention_local<64>, grid, dim3(256), lds, ctx->stream, qkv, nh, nkv, S, pos0, cs, no_rope,
-                           xq, xd, variant);
+        hipLaunchKernelGGL(k_attention_local<64>, grid, dim3(256), lds, ctx->stream, qkv, nh, nkv, S, RB, pos0, cs,
+                           no_rope, xq, xd, variant);
     else
-        hipLaunchKernelGGL(k_attention_local<128>, grid, dim3(256), lds, ctx->stream, qkv, nh, nkv, S, pos0, cs,
+        hipLaunchKernelGGL(k_attention_local<128>, grid, dim3(256), lds, ctx->stream, qkv, nh, nkv, S, RB, pos0, cs,
                            no_rope, xq, xd, variant);
     VXM_CHECK_LAUNCH(ctx);
     return VXM_OK;
