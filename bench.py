@@ -147,6 +147,26 @@ def bench_gemv(ctx, torch, vxm, N, K, copies, reps):
     return us
 
 
+def bench_copy_floor(torch, nbytes, copies, reps):
+    """Per-launch time of a device copy moving nbytes (nbytes/2 read + nbytes/2 written), back to back
+    over `copies` rotated buffer pairs: what one launch of that much traffic costs on this device."""
+    n = nbytes // 8
+    src = [torch.ones(n, dtype=torch.float32, device="cuda:0") for _ in range(copies)]
+    dst = [torch.empty_like(a) for a in src]
+    for a, b in zip(src, dst):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        for a, b in zip(src, dst):
+            b.copy_(a)
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / (reps * copies)
+
+
 def bench_decode(ctx, torch, vxm, layers, n_layers, copies, ctx0, steps, warmup, mode):
     """Decode `steps` tokens from context ctx0, rotating over `copies` weight copies."""
     cfg = dict(hidden_size=H, n_layers=n_layers, n_heads=NH, n_kv_heads=NKV, head_dim=HD, intermediate_size=F,
@@ -499,10 +519,16 @@ def main():
         for (N, K) in ((6144, 2048), (2048, 6144)):
             us = bench_gemv(ctx, torch, vxm, N, K, 64, 10)
             gbs = gemv_bytes(N, K) / (us * 1e-6) / 1e9
+            cus = bench_copy_floor(torch, gemv_bytes(N, K), 64, 10)
+            cgbs = gemv_bytes(N, K) / (cus * 1e-6) / 1e9
             res[f"{N}x{K}"] = {"us_per_launch": round(us, 3), "GBs": round(gbs, 1),
                                "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                               "note": "one launch per GEMV, back to back over 64 rotated weight copies"}
-            log(f"gemv {N}x{K}: {us:.3f} us/launch, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
+                               "copy_floor_us_per_launch": round(cus, 3), "copy_floor_GBs": round(cgbs, 1),
+                               "note": "one launch per GEMV, back to back over 64 rotated weight copies; "
+                                       "copy_floor: a device copy moving the same bytes, back to back over 64 "
+                                       "rotated buffers"}
+            log(f"gemv {N}x{K}: {us:.3f} us/launch, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM); "
+                f"copy of the same bytes {cus:.3f} us/launch, {cgbs:.1f} GB/s")
         if args.gemv_only:
             print(json.dumps({"gemv": res}))
             ctx.close()
