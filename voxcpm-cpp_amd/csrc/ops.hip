@@ -471,18 +471,19 @@ int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const
 // K-split slices.  Output: the Q8_0 rows of the attention output (xq, xd).
 // ---------------------------------------------------------------------------
 constexpr int kLocalMaxS = 64, kLocalMaxElems = 2048;   // S, and S * hd per operand
+constexpr int kLocalRB = 8;                              // query rows per workgroup
 
 bool vxm_attention_local_fits(int S, int hd) {
     return S >= 1 && S <= kLocalMaxS && (hd == 64 || hd == 128) && (int64_t)S * hd <= kLocalMaxElems;
 }
 
 template <int HD>
-__global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, int nh, int nkv, int S, int RB, int pos0,
+__global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, int nh, int nkv, int S, int pos0,
                                                          const float2 *__restrict__ cs, int no_rope,
                                                          int8_t *__restrict__ xq, uint16_t *__restrict__ xd,
                                                          int variant) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    constexpr int HALF = HD / 2, HP = HD + 4;
+    constexpr int HALF = HD / 2, HP = HD + 4, RB = kLocalRB;
     const int h = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
     const int q0 = blockIdx.z * RB, nq = min(RB, S - q0);   // this workgroup's query rows
     const int kvh = h / (nh / nkv);
@@ -495,6 +496,8 @@ __global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, in
     float *mx = P + RB * SP, *inv = mx + RB;
     // 1. raw q (rows q0 .. q0+nq-1 of head h), k and v (all S rows of kv head kvh),
     //    K-split slices added in order; the loads of up to four slices are in flight together
+    constexpr int kRopePer = ((kLocalMaxElems / HD + RB) * HALF + 255) / 256;
+    float2 csr[kRopePer];
     {
         constexpr int kMaxPer = (3 * kLocalMaxElems / 4 + 255) / 256;   // float4s per thread
         constexpr int R4 = HD / 4;                                      // float4s per row
@@ -520,6 +523,16 @@ __global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, in
             src[k] = (int64_t)(g * S + row) * ld + col + off;
             dst[k] += off;
             acc4[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        // the rope table entries of this thread's phase-2 items, fetched with the projections
+        if (!no_rope) {
+#pragma unroll
+            for (int k = 0; k < kRopePer; k++) {
+                const int idx = min(tid + 256 * k, (S + nq) * HALF - 1);
+                const int rr = idx / HALF, i = idx % HALF;
+                const int pos = pos0 + (rr < S ? rr : q0 + rr - S);
+                csr[k] = cs[(int64_t)pos * HALF + i];
+            }
         }
         for (int z0 = 0; z0 < qkv.n; z0 += 4) {
             float4 b[4][kMaxPer];
@@ -548,15 +561,17 @@ __global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, in
     __syncthreads();
     // 2. BF16 + RoPE of q and k (pair-interleaved rows: row 2i = dim i, 2i+1 = dim
     //    i + hd/2), the f16 cache rounding of k and v
-    for (int idx = tid; idx < (S + nq) * HALF; idx += 256) {
+#pragma unroll
+    for (int k = 0; k < kRopePer; k++) {
+        const int idx = tid + 256 * k;
+        if (idx >= (S + nq) * HALF) break;
         const int rr = idx / HALF, i = idx % HALF;
         const bool isk = rr < S;
-        const int lr = isk ? rr : rr - S, pos = pos0 + (isk ? rr : q0 + lr);
+        const int lr = isk ? rr : rr - S;
         float c = 1.0f, sn = 0.0f;
         if (!no_rope) {
-            const float2 r = cs[(int64_t)pos * HALF + i];
-            c = r.x;
-            sn = r.y;
+            c = csr[k].x;
+            sn = csr[k].y;
         }
         const float *sp = (isk ? Kr : Qr) + lr * HD;
         const float x0 = vxm_bf16(sp[2 * i]), x1 = vxm_bf16(sp[2 * i + 1]);
@@ -615,7 +630,7 @@ __global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, in
     //    thread (row group rg, dim d) owns rows rg, rg + R, ...; rows past nq read row
     //    nq - 1 with a zero weight, so the loop has no divergent reads
     {
-        constexpr int R = 256 / HD, MAXR = kLocalMaxElems / 256;
+        constexpr int R = 256 / HD, MAXR = (RB + R - 1) / R;
         const int d = tid % HD, rg = tid / HD;
         const int slices = 256 / HD, jper = (S + slices - 1) / slices;
         float tot[MAXR], acc[MAXR], iv[MAXR];
@@ -630,6 +645,7 @@ __global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, in
             const int j0 = sl * jper, j1 = min(S, j0 + jper);
 #pragma unroll
             for (int k = 0; k < MAXR; k++) acc[k] = 0.0f;
+#pragma unroll 4
             for (int j = j0; j < j1; j++) {
                 const float v = V[j * HD + d];
 #pragma unroll
@@ -666,14 +682,14 @@ int vxm_launch_attention_local(vxm_ctx *ctx, vxm_parts qkv, int64_t M, int nh, i
         return vxm_fail(ctx, VXM_ERR_BACKEND, "rope: table holds %d positions, %d needed", cs_rows, pos0 + S);
     // query rows per workgroup: blocks of 8 spread a segment's rows over several CUs
     // (each block re-derives the segment's k and v)
-    const int RB = S < 8 ? S : 8, QB = (S + RB - 1) / RB;
+    const int RB = kLocalRB, QB = (S + RB - 1) / RB;
     const size_t lds = (size_t)(2 * S * hd + RB * hd + (S + RB) * (hd + 4) + RB * (S + 1) + 2 * RB) * sizeof(float);
     const dim3 grid(nh, (unsigned)(M / S), QB);
     if (hd == 64)
-        hipLaunchKernelGGL(k_attention_local<64>, grid, dim3(256), lds, ctx->stream, qkv, nh, nkv, S, RB, pos0, cs,
+        hipLaunchKernelGGL(k_attention_local<64>, grid, dim3(256), lds, ctx->stream, qkv, nh, nkv, S, pos0, cs,
                            no_rope, xq, xd, variant);
     else
-        hipLaunchKernelGGL(k_attention_local<128>, grid, dim3(256), lds, ctx->stream, qkv, nh, nkv, S, RB, pos0, cs,
+        hipLaunchKernelGGL(k_attention_local<128>, grid, dim3(256), lds, ctx->stream, qkv, nh, nkv, S, pos0, cs,
                            no_rope, xq, xd, variant);
     VXM_CHECK_LAUNCH(ctx);
     return VXM_OK;
