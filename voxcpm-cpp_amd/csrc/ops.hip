@@ -76,6 +76,18 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const vx
     float *hr = h + (int64_t)row * n;
     const float *dr = delta.p ? delta.p + (int64_t)row * n : nullptr;
     float v[VXM_NORM_CHUNKS][8];
+    // the gain, fetched with the row (it is needed right after the reduction)
+    float4 gl[VXM_NORM_CHUNKS][2];
+#pragma unroll
+    for (int c = 0; c < VXM_NORM_CHUNKS; c++) {
+        const int base = (c * 256 + threadIdx.x) * 8;
+        if (gain && base < n) {
+            gl[c][0] = *(const float4 *)(gain + base);
+            gl[c][1] = *(const float4 *)(gain + base + 4);
+        } else {
+            gl[c][0] = gl[c][1] = make_float4(1, 1, 1, 1);
+        }
+    }
     double ss = 0.0;
 #pragma unroll
     for (int c = 0; c < VXM_NORM_CHUNKS; c++) {
@@ -123,8 +135,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const vx
         const int base = (c * 256 + threadIdx.x) * 8;
         if (base >= n) continue;   // whole 32-blocks live in 4 consecutive lanes: n % 32 == 0
         float o[8];
-        float4 g0 = gain ? *(const float4 *)(gain + base) : make_float4(1, 1, 1, 1);
-        float4 g1 = gain ? *(const float4 *)(gain + base + 4) : make_float4(1, 1, 1, 1);
+        const float4 g0 = gl[c][0], g1 = gl[c][1];
         const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
 #pragma unroll
         for (int i = 0; i < 8; i++) {
