@@ -232,7 +232,12 @@ int vxm_locdit_forward(vxm_locdit *m, const float *x_dev, const float *cond_dev,
  * CFG-Zero* (vcpm_cfm_cfg_zero_star, src/cfm_solver.c:65-93) and
  * x = bf16(x + bf16(dt * v)).  Without CFG (cfg_value == 1 or mu == NULL,
  * src/gen_step.c:475) only the conditional branch runs.  x [P][feat_dim] is
- * updated in place. */
+ * updated in place.
+ * The first call with a given set of arguments (x, cond and mu pointers, P, Pc,
+ * n_steps, cfg_value, schedule, use_zero_star) runs the loop eagerly; the
+ * second records it as a HIP graph and every later call with the same
+ * arguments (and the same internal buffers) replays that graph, reading the
+ * current contents of x, cond and mu.  Results are identical either way. */
 #define VXM_CFM_SWAY 0      /* vcpm_cfm_sway_t_bf16 (src/cfm_solver.c:27-37) */
 #define VXM_CFM_UNIFORM 1   /* t = bf16(1 - step / n_steps) */
 int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev, int32_t P, int32_t Pc,
