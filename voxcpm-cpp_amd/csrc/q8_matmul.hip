@@ -245,6 +245,7 @@ __global__ void k_block_dots(const int8_t *__restrict__ qs, const int8_t *__rest
 // dots[(m*N + n)*nb + b] instead (debug; no scaling, no split).
 // ---------------------------------------------------------------------------
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 constexpr int GM = 64, GN = 64;              // output tile
 constexpr int kGemmThreads = 512;
 constexpr int kGemmSpin = 1 << 20;           // bound of the wait for one partial word
@@ -348,8 +349,10 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
         const int8_t *arow = L.a[buf] + (wm * 32 + lr) * ROW + lh * 16 + kq * NQ * 32;
         const int8_t *brow0 = L.b[buf] + lr * ROW + lh * 16 + kq * NQ * 32;
         const int8_t *brow1 = brow0 + 32 * ROW;
-        const float *adq = &L.ad[buf][kq * NQ][wm * 32 + 4 * lh];
-        const float *bdq = &L.bd[buf][kq * NQ][lr];
+        // per-lane scale operands of the outer product below: row scale of row lr of this
+        // strip, column scale of column lr of tile half lh
+        const float *adq = &L.ad[buf][kq * NQ][wm * 32 + lr];
+        const float *bdq = &L.bd[buf][kq * NQ][32 * lh + lr];
         // epilogue of block j of this quarter: scale and add (or, DOTS, write the sums)
         auto epi = [&](const v16i &c0, const v16i &c1, int j) {
             if (DOTS) {
@@ -366,18 +369,15 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
                 }
                 return;
             }
-            const float dw0 = bdq[j * GN], dw1 = bdq[j * GN + 32];
-            const float *dxr = adq + j * GM;
+            // the 2 x 32 x 32 scale products d_x[m] * d_w[n] of this block come from one
+            // two-block f32 outer product on the matrix core (block h = lanes 32h..32h+31
+            // supply d_x of row lr and d_w of column 32h + lr) in the layout of c0 / c1;
+            // each product of two fp16 values is exact in fp32, as the VALU product was
+            const v32f sc = __builtin_amdgcn_mfma_f32_32x32x1f32(adq[j * GM], bdq[j * GN], v32f{}, 0, 0, 0);
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const float4 dx = *(const float4 *)(dxr + 8 * g);
-                const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int v = 4 * g + e;
-                    acc[0][v] = __builtin_fmaf((float)c0[v], dw0 * dxv[e], acc[0][v]);
-                    acc[1][v] = __builtin_fmaf((float)c1[v], dw1 * dxv[e], acc[1][v]);
-                }
+            for (int v = 0; v < 16; v++) {
+                acc[0][v] = __builtin_fmaf((float)c0[v], sc[v], acc[0][v]);
+                acc[1][v] = __builtin_fmaf((float)c1[v], sc[16 + v], acc[1][v]);
             }
         };
         auto mma = [&](int j, v16i &c0, v16i &c1) {
@@ -552,16 +552,20 @@ __global__ __launch_bounds__(64 * kSmallRG) void k_gemm_q8_0_small(const int8_t 
     __shared__ float xds[ROWS][SB + 1];
     const int nb = K / 32;
     const int g = blockIdx.x, z = blockIdx.y;
+    // row tile of x: rows m0 .. m0 + Mt - 1 (one tile unless M > 16 MT)
+    const int m0 = blockIdx.z * ROWS, Mt = min(ROWS, M - m0);
+    xq += (int64_t)m0 * K;
+    xd += (int64_t)m0 * nb;
     const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, r = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nw = g * 16 * kSmallRG + 16 * wave;
     const int zb0 = z * bps, zb1 = min(nb, zb0 + bps);
     const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)wq, (short)0, N * K, 0x00020000);
-    const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)xq, (short)0, M * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)xq, (short)0, Mt * K, 0x00020000);
     const __amdgpu_buffer_rsrc_t wd_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)wd, (short)0, N * nb * 2, 0x00020000);
     const __amdgpu_buffer_rsrc_t xd_rsrc =
-        __builtin_amdgcn_make_buffer_rsrc((void *)xd, (short)0, M * nb * 2, 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void *)xd, (short)0, Mt * nb * 2, 0x00020000);
 
     float acc[MT][4];
 #pragma unroll
@@ -659,11 +663,11 @@ __global__ __launch_bounds__(64 * kSmallRG) void k_gemm_q8_0_small(const int8_t 
         if (kb0 + 2 * SB < zb1) issue(sa, kb0 + 2 * SB);
         run(sb, kb0 + SB);
     }
-    float *yz = y + (int64_t)z * M * N;
+    float *yz = y + (int64_t)z * M * N + (int64_t)m0 * N;
 #pragma unroll
     for (int t = 0; t < MT; t++) {
         const int m = 16 * t + r;
-        if (m >= M) continue;
+        if (m >= Mt) continue;
 #pragma unroll
         for (int v = 0; v < 4; v++) yz[(int64_t)m * N + nw + 4 * q + v] = acc[t][v];
     }
@@ -752,18 +756,20 @@ constexpr int kMfmaMinRows = 8;
 // idle (at most max_parts).  Shapes outside the kernel's layout (N % 64,
 // K % 256, M > 64, operands of 2 GiB) take the tiled GEMM.
 struct SmallPlan {
-    int mt, bps, splits, groups;
+    int mt, bps, splits, groups, mtiles;
 };
 
-static bool small_plan(vxm_ctx *ctx, int64_t M, int64_t N, int64_t K, int max_parts, SmallPlan &p) {
-    if (M < 1 || M > VXM_SMALL_MAX_ROWS || N % (16 * kSmallRG) || K % (32 * kSmallStage)) return false;
-    // 32-bit buffer offsets: the weights, and the activation rows of every m-tile
-    if (N * K >= ((int64_t)1 << 31) || VXM_SMALL_MAX_ROWS * K >= ((int64_t)1 << 31)) return false;
+static bool small_plan(vxm_ctx *ctx, int64_t M, int64_t N, int64_t K, int max_parts, SmallPlan &p,
+                       int64_t max_rows = VXM_SMALL_MAX_ROWS) {
+    if (M < 1 || M > max_rows || N % (16 * kSmallRG) || K % (32 * kSmallStage)) return false;
+    // 32-bit buffer offsets: the weights, and the activation rows of every row tile
+    if (N * K >= ((int64_t)1 << 31) || VXM_SMALL_MAX_ROWS * K >= ((int64_t)1 << 31) || M >= (1 << 20)) return false;
     const int nb = (int)(K / 32), stages = nb / kSmallStage;
-    p.mt = (int)((M + 15) / 16);
+    p.mt = M > VXM_SMALL_MAX_ROWS ? 4 : (int)((M + 15) / 16);
+    p.mtiles = (int)((M + 16 * p.mt - 1) / (16 * p.mt));
     p.groups = (int)(N / (16 * kSmallRG));
     int s = 1;
-    while (s * 2 <= max_parts && s * 2 <= stages && (int64_t)p.groups * s < ctx->n_cu) s *= 2;
+    while (s * 2 <= max_parts && s * 2 <= stages && (int64_t)p.groups * p.mtiles * s < ctx->n_cu) s *= 2;
     const int per = (stages + s - 1) / s;   // stages per split
     p.bps = per * kSmallStage;
     p.splits = (nb + p.bps - 1) / p.bps;
@@ -772,7 +778,7 @@ static bool small_plan(vxm_ctx *ctx, int64_t M, int64_t N, int64_t K, int max_pa
 
 static void launch_small(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                          float *y, const SmallPlan &p) {
-    const dim3 grid(p.groups, p.splits), block(64 * kSmallRG);
+    const dim3 grid(p.groups, p.splits, p.mtiles), block(64 * kSmallRG);
     const int N = (int)w->n, K = (int)w->k;
     switch (p.mt) {
         case 1: hipLaunchKernelGGL(k_gemm_q8_0_small<1>, grid, block, 0, ctx->stream, xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps); break;
