@@ -354,16 +354,28 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma(const float *__restrict_
         const int r = i / HD, d = i % HD;
         Qh[r * QP + d] = (_Float16)(r < nq ? q[(int64_t)(t0 + r) * nh * HD + h * HD + d] : 0.0f);
     }
-    // pass 1: scores, 128 keys per stage
+    // pass 1: scores, 128 keys per stage; the next stage's keys are loaded during this
+    // stage's products
+    constexpr int NKL = KS * HD / (ATH * 8), NVL = VS * HD / (ATH * 8);   // 16-byte loads per thread
+    static_assert(KS * HD % (ATH * 8) == 0 && VS * HD % (ATH * 8) == 0, "whole rounds of 16-byte loads");
+    uint4 kreg[NKL];
+    auto load_k = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < NKL; u++) {
+            const int i = (u * ATH + tid) * 8, r = i / HD, d = i % HD;
+            kreg[u] = k0 + r < kv_end ? *(const uint4 *)(kb + (int64_t)(k0 + r) * HD + d) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    load_k(0);
     for (int k0 = 0; k0 < kv_end; k0 += KS) {
         __syncthreads();
-        for (int i = tid * 8; i < KS * HD; i += ATH * 8) {
-            const int r = i / HD, d = i % HD;
-            uint4 w = make_uint4(0, 0, 0, 0);
-            if (k0 + r < kv_end) w = *(const uint4 *)(kb + (int64_t)(k0 + r) * HD + d);
-            *(uint4 *)(Kh + r * QP + d) = w;
+#pragma unroll
+        for (int u = 0; u < NKL; u++) {
+            const int i = (u * ATH + tid) * 8, r = i / HD, d = i % HD;
+            *(uint4 *)(Kh + r * QP + d) = kreg[u];
         }
         __syncthreads();
+        if (k0 + KS < kv_end) load_k(k0 + KS);
         const int kblk = k0 + 32 * wave;
         if (kblk < kv_end) {
             v16f c = v16f{};
@@ -401,13 +413,22 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma(const float *__restrict_
     }
     // pass 3: O = P V, 64 keys per stage; wave w < HD/32 owns dims [32w, 32w + 32)
     v16f o = v16f{};
+    uint4 vreg[NVL];
+    auto load_v = [&](int v0) {
+#pragma unroll
+        for (int u = 0; u < NVL; u++) {
+            const int i = (u * ATH + tid) * 8, r = i / HD, d = i % HD;
+            vreg[u] = v0 + r < kv_end ? *(const uint4 *)(vb + (int64_t)(v0 + r) * HD + d) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    load_v(0);
     for (int v0 = 0; v0 < kv_end; v0 += VS) {
         __syncthreads();
         // transpose: thread moves 8 dims of one key row into column (key) of Vt
-        for (int i = tid * 8; i < VS * HD; i += ATH * 8) {
-            const int r = i / HD, d = i % HD;
-            uint4 w = make_uint4(0, 0, 0, 0);
-            if (v0 + r < kv_end) w = *(const uint4 *)(vb + (int64_t)(v0 + r) * HD + d);
+#pragma unroll
+        for (int u = 0; u < NVL; u++) {
+            const int i = (u * ATH + tid) * 8, r = i / HD, d = i % HD;
+            const uint4 w = vreg[u];
             const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -416,6 +437,7 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma(const float *__restrict_
             }
         }
         __syncthreads();
+        if (v0 + VS < kv_end) load_v(v0 + VS);
         if (wave < HD / 32) {
 #pragma unroll
             for (int ks = 0; ks < VS; ks += 16) {
