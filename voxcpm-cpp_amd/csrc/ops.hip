@@ -356,8 +356,10 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma(const float *__restrict_
     }
     // pass 1: scores, 128 keys per stage; the next stage's keys are loaded during this
     // stage's products
-    constexpr int NKL = KS * HD / (ATH * 8), NVL = VS * HD / (ATH * 8);   // 16-byte loads per thread
-    static_assert(KS * HD % (ATH * 8) == 0 && VS * HD % (ATH * 8) == 0, "whole rounds of 16-byte loads");
+    constexpr int NKL = KS * HD / (ATH * 8);                // 16-byte key loads per thread
+    constexpr int NVL = (VS / 2) * (HD / 8) / ATH;          // (key pair, 8-dim chunk) items per thread
+    static_assert(KS * HD % (ATH * 8) == 0 && (VS / 2) * (HD / 8) % ATH == 0 && VS == 64,
+                  "whole rounds of loads; 32 key pairs per V stage");
     uint4 kreg[NKL];
     auto load_k = [&](int k0) {
 #pragma unroll
@@ -413,27 +415,33 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma(const float *__restrict_
     }
     // pass 3: O = P V, 64 keys per stage; wave w < HD/32 owns dims [32w, 32w + 32)
     v16f o = v16f{};
-    uint4 vreg[NVL];
+    // V item (key pair p, dims 8c .. 8c+7), p = item % 32 fastest: the transposing 32-bit
+    // LDS writes of a wave land on distinct banks
+    uint4 vreg[NVL][2];
     auto load_v = [&](int v0) {
 #pragma unroll
         for (int u = 0; u < NVL; u++) {
-            const int i = (u * ATH + tid) * 8, r = i / HD, d = i % HD;
-            vreg[u] = v0 + r < kv_end ? *(const uint4 *)(vb + (int64_t)(v0 + r) * HD + d) : make_uint4(0, 0, 0, 0);
+            const int item = u * ATH + tid, r = 2 * (item % 32), d = 8 * (item / 32);
+#pragma unroll
+            for (int e = 0; e < 2; e++)
+                vreg[u][e] = v0 + r + e < kv_end ? *(const uint4 *)(vb + (int64_t)(v0 + r + e) * HD + d)
+                                                 : make_uint4(0, 0, 0, 0);
         }
     };
     load_v(0);
     for (int v0 = 0; v0 < kv_end; v0 += VS) {
         __syncthreads();
-        // transpose: thread moves 8 dims of one key row into column (key) of Vt
+        // transpose: dims d .. d+7 of keys r, r+1 become 8 words (key r low, key r+1 high)
+        // in rows d .. d+7 of Vt
 #pragma unroll
         for (int u = 0; u < NVL; u++) {
-            const int i = (u * ATH + tid) * 8, r = i / HD, d = i % HD;
-            const uint4 w = vreg[u];
-            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+            const int item = u * ATH + tid, r = 2 * (item % 32), d = 8 * (item / 32);
+            const uint32_t a[4] = {vreg[u][0].x, vreg[u][0].y, vreg[u][0].z, vreg[u][0].w};
+            const uint32_t b[4] = {vreg[u][1].x, vreg[u][1].y, vreg[u][1].z, vreg[u][1].w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                ((uint16_t *)Vt)[(d + 2 * e) * VP + r] = (uint16_t)(ww[e] & 0xffffu);
-                ((uint16_t *)Vt)[(d + 2 * e + 1) * VP + r] = (uint16_t)(ww[e] >> 16);
+                *(uint32_t *)(Vt + (d + 2 * e) * VP + r) = (a[e] & 0xffffu) | (b[e] << 16);
+                *(uint32_t *)(Vt + (d + 2 * e + 1) * VP + r) = (a[e] >> 16) | (b[e] & 0xffff0000u);
             }
         }
         __syncthreads();
