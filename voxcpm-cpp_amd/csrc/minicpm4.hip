@@ -230,11 +230,24 @@ int vxm_block_run(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_block &b, vxm
     if ((rc = vxm_launch_rmsnorm(ctx, x, vxm_parts{ws.o, np, M * d.H}, d.res_scale, b.g_post, M, d.H, d.eps, nullptr,
                                  ws.xq, ws.xd, var)))
         return rc;
-    if ((rc = vxm_launch_mul_mat_parts(ctx, b.wgu, ws.xq, ws.xd, M, ws.gu, ws.max_parts, &np))) return rc;
-    if ((rc = vxm_launch_swiglu_quant(ctx, vxm_parts{ws.gu, np, M * 2 * d.F}, M, d.F, 2 * d.F, ws.xq, ws.xd, nullptr,
-                                      var)))
-        return rc;
-    if ((rc = vxm_launch_mul_mat_parts(ctx, b.wd, ws.xq, ws.xd, M, ws.dn, ws.max_parts, &np))) return rc;
+    // gate/up: the tiled GEMM applies SwiGLU and the Q8_0 in its epilogue when it takes the
+    // product, writing the down projection's input into the (then unused) gate/up buffer,
+    // apart from its own input
+    int8_t *pq = ws.xq;
+    uint16_t *pd = ws.xd;
+    int8_t *fq = (int8_t *)ws.gu;
+    uint16_t *fd = (uint16_t *)(fq + ((M * d.F + 255) & ~(int64_t)255));
+    if (vxm_launch_gate_up_swiglu(ctx, b.wgu, ws.xq, ws.xd, M, fq, fd, var, &rc)) {
+        if (rc) return rc;
+        pq = fq;
+        pd = fd;
+    } else {
+        if ((rc = vxm_launch_mul_mat_parts(ctx, b.wgu, ws.xq, ws.xd, M, ws.gu, ws.max_parts, &np))) return rc;
+        if ((rc = vxm_launch_swiglu_quant(ctx, vxm_parts{ws.gu, np, M * 2 * d.F}, M, d.F, 2 * d.F, ws.xq, ws.xd,
+                                          nullptr, var)))
+            return rc;
+    }
+    if ((rc = vxm_launch_mul_mat_parts(ctx, b.wd, pq, pd, M, ws.dn, ws.max_parts, &np))) return rc;
     ws.dn_out = vxm_parts{ws.dn, np, M * d.H};
     return VXM_OK;
 }

@@ -138,6 +138,8 @@ constexpr int VXM_MAX_PARTS = 8;         // its K splits
 // number written (1 unless the small-M GEMM splits K).
 int vxm_launch_mul_mat_parts(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd,
                              int64_t M, float *y, int max_parts, int *parts);
+bool vxm_launch_gate_up_swiglu(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                               int8_t *sq, uint16_t *sd, int variant, int *rc);
 int vxm_ensure_act(vxm_ctx *ctx, size_t bytes);
 int vxm_ensure_parts(vxm_ctx *ctx, size_t bytes);
 int vxm_ensure_split(vxm_ctx *ctx, size_t bytes, size_t n_counters);
