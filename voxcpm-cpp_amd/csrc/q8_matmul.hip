@@ -586,7 +586,8 @@ __global__ __launch_bounds__(64 * kSmallRG) void k_gemm_q8_0_small(const int8_t 
                                                                    const int8_t *__restrict__ wq,
                                                                    const uint16_t *__restrict__ wd,
                                                                    float *__restrict__ y, int M, int N, int K,
-                                                                   int bps) {
+                                                                   int bps, int8_t *__restrict__ sq,
+                                                                   uint16_t *__restrict__ sd, int variant) {
     constexpr int SB = kSmallStage, ROWS = 16 * MT, NT = 64 * kSmallRG;
     __shared__ __align__(16) int8_t xs[ROWS * kSmallPitch];
     __shared__ float xds[ROWS][SB + 1];
@@ -703,6 +704,53 @@ __global__ __launch_bounds__(64 * kSmallRG) void k_gemm_q8_0_small(const int8_t 
         if (kb0 + 2 * SB < zb1) issue(sa, kb0 + 2 * SB);
         run(sb, kb0 + SB);
     }
+    if (sq) {
+        // SwiGLU + Q8_0 epilogue (one split): the workgroup's 64 weight rows are 32 (gate,
+        // up) pairs, rows 4q + v with v even (gate) and v + 1 (up) in the same lane, so each
+        // activation row gets one Q8_0 block of p = bf16(bf16(silu(bf16(g))) * bf16(u)) (as in
+        // k_swiglu_quant), gathered through LDS and quantized by four threads per row with
+        // the activation rule of quant_block_4lanes.
+        __shared__ float ps[ROWS][33];
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int vp = 0; vp < 2; vp++) {
+                const float gb = vxm_bf16(acc[t][2 * vp]);
+                const float sl = vxm_bf16(__fdiv_rn(gb, 1.0f + expf(-gb)));
+                ps[16 * t + r][8 * wave + 2 * q + vp] = vxm_bf16(sl * vxm_bf16(acc[t][2 * vp + 1]));
+            }
+        __syncthreads();
+        const int F = N / 2, row = tid >> 2, part = tid & 3;
+        if (row < ROWS) {   // NT = 4 ROWS for MT = 4; fewer rows leave whole 4-lane groups idle
+            float pv[8], amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                pv[e] = ps[row][8 * part + e];
+                amax = fmaxf(amax, fabsf(pv[e]));
+            }
+            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+            const float d = __fdiv_rn(amax, 127.0f);
+            float id;
+            if (variant == VXM_QUANT_X86) id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+            else id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+            if (row < Mt) {
+                uint32_t lo = 0, hi = 0;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float qv = variant == VXM_QUANT_X86 ? rintf(pv[e] * id) : roundf(pv[e] * id);
+                    qv = fminf(fmaxf(qv, -128.0f), 127.0f);
+                    const uint32_t b = (uint32_t)(uint8_t)(int8_t)(int)qv;
+                    if (e < 4) lo |= b << (8 * e);
+                    else hi |= b << (8 * (e - 4));
+                }
+                const int64_t base = (int64_t)(m0 + row) * F + g * 32 + 8 * part;
+                *(uint2 *)(sq + base) = make_uint2(lo, hi);
+                if (part == 0) sd[base / 32] = vxm_f2h(d);
+            }
+        }
+        return;
+    }
     float *yz = y + (int64_t)z * M * N + (int64_t)m0 * N;
 #pragma unroll
     for (int t = 0; t < MT; t++) {
@@ -817,15 +865,18 @@ static bool small_plan(vxm_ctx *ctx, int64_t M, int64_t N, int64_t K, int max_pa
 }
 
 static void launch_small(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
-                         float *y, const SmallPlan &p) {
+                         float *y, const SmallPlan &p, int8_t *sq = nullptr, uint16_t *sd = nullptr,
+                         int variant = 0) {
     const dim3 grid(p.groups, p.splits, p.mtiles), block(64 * kSmallRG);
     const int N = (int)w->n, K = (int)w->k;
+#define VXM_SMALL_ARGS xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps, sq, sd, variant
     switch (p.mt) {
-        case 1: hipLaunchKernelGGL(k_gemm_q8_0_small<1>, grid, block, 0, ctx->stream, xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps); break;
-        case 2: hipLaunchKernelGGL(k_gemm_q8_0_small<2>, grid, block, 0, ctx->stream, xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps); break;
-        case 3: hipLaunchKernelGGL(k_gemm_q8_0_small<3>, grid, block, 0, ctx->stream, xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps); break;
-        default: hipLaunchKernelGGL(k_gemm_q8_0_small<4>, grid, block, 0, ctx->stream, xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps); break;
+        case 1: hipLaunchKernelGGL(k_gemm_q8_0_small<1>, grid, block, 0, ctx->stream, VXM_SMALL_ARGS); break;
+        case 2: hipLaunchKernelGGL(k_gemm_q8_0_small<2>, grid, block, 0, ctx->stream, VXM_SMALL_ARGS); break;
+        case 3: hipLaunchKernelGGL(k_gemm_q8_0_small<3>, grid, block, 0, ctx->stream, VXM_SMALL_ARGS); break;
+        default: hipLaunchKernelGGL(k_gemm_q8_0_small<4>, grid, block, 0, ctx->stream, VXM_SMALL_ARGS); break;
     }
+#undef VXM_SMALL_ARGS
 }
 
 // Public entry: a split product goes through the context's scratch and one
@@ -875,9 +926,15 @@ bool vxm_launch_gate_up_swiglu(vxm_ctx *ctx, const vxm_weight *w, const int8_t *
     const bool mfma = ctx->path == VXM_PATH_MFMA || ctx->path == VXM_PATH_MFMA_TILED ||
                       (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
     SmallPlan sp;
-    if (!mfma || M <= 0 || N % 64 || !gemm_fits(M, N, K) ||
-        (ctx->path != VXM_PATH_MFMA_TILED && small_plan(ctx, M, N, K, VXM_MAX_PARTS, sp)))
-        return false;
+    if (!mfma || M <= 0 || N % 64) return false;
+    if (ctx->path != VXM_PATH_MFMA_TILED && small_plan(ctx, M, N, K, VXM_MAX_PARTS, sp)) {
+        // the small-M kernel, unsplit (each workgroup holds whole 32-pair blocks over all of K)
+        small_plan(ctx, M, N, K, 1, sp);
+        launch_small(ctx, w, xq, xd, M, nullptr, sp, sq, sd, variant);
+        if (hipGetLastError() != hipSuccess) *rc = vxm_fail(ctx, VXM_ERR_BACKEND, "gate/up + SwiGLU launch failed");
+        return true;
+    }
+    if (!gemm_fits(M, N, K)) return false;
     const GemmPlan p = gemm_plan(ctx, M, N, nb);
     if (p.splits != 1) return false;
     const int grid_x = 8 * p.tiles_m * ((p.tiles_n + 7) / 8);
