@@ -273,7 +273,7 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
     const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd, const int8_t *__restrict__ wq,
     const uint16_t *__restrict__ wd, float *__restrict__ y, uint64_t *__restrict__ part, int *__restrict__ cnt,
     int32_t *__restrict__ dots, int M, int N, int K, int tiles_m, int tiles_n, int bps, int splits,
-    uint32_t epoch, int8_t *__restrict__ sq, uint16_t *__restrict__ sd, int variant) {
+    uint32_t epoch) {
     static_assert(KS % 8 == 0, "a stage is a multiple of 8 blocks (64 KS scales per side = whole 512-thread rounds)");
     constexpr int ROW = GemmLds<KS>::ROW;
     constexpr int CH = KS / 4;                 // 16-byte chunks per thread per side and stage
@@ -434,46 +434,6 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
             for (int q = 1; q < 4; q++) t = t + red[((q * 2 + wm) * 32 + 16 * half + v) * 64 + lane];
             fin[half][vv] = t;
         }
-    if (sq) {
-        // SwiGLU + Q8_0 epilogue (no K split, N % 64 == 0): the tile's columns are 32
-        // (gate, up) pairs, so each row's 32 products form one Q8_0 block.  Even lanes
-        // hold a gate, odd lanes its up; p = bf16(bf16(silu(bf16(g))) * bf16(u)) as in
-        // k_swiglu_quant, quantized with the activation rule of quant_block_4lanes.
-        const int F = N / 2, nbf = F / 32;
-#pragma unroll
-        for (int vv = 0; vv < 4; vv++) {
-            const int m = m0 + wm * 32 + 8 * kq + 4 * lh + vv;
-            float p[2];
-#pragma unroll
-            for (int half = 0; half < 2; half++) {
-                const float own = fin[half][vv], other = __shfl_xor(own, 1, 64);
-                if (lr & 1) {
-                    p[half] = 0.0f;
-                } else {
-                    const float gb = vxm_bf16(own);
-                    const float sl = vxm_bf16(__fdiv_rn(gb, 1.0f + expf(-gb)));
-                    p[half] = vxm_bf16(sl * vxm_bf16(other));
-                }
-            }
-            float amax = fmaxf(fabsf(p[0]), fabsf(p[1]));
-#pragma unroll
-            for (int x = 1; x < 32; x <<= 1) amax = fmaxf(amax, __shfl_xor(amax, x, 64));
-            const float d = __fdiv_rn(amax, 127.0f);
-            float id;
-            if (variant == VXM_QUANT_X86) id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-            else id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-            if (m < M && !(lr & 1)) {
-#pragma unroll
-                for (int half = 0; half < 2; half++) {
-                    float qv = variant == VXM_QUANT_X86 ? rintf(p[half] * id) : roundf(p[half] * id);
-                    qv = fminf(fmaxf(qv, -128.0f), 127.0f);
-                    sq[(int64_t)m * F + n0 / 2 + half * 16 + lr / 2] = (int8_t)(int)qv;
-                }
-                if (lr == 0) sd[(int64_t)m * nbf + n0 / 64] = vxm_f2h(d);
-            }
-        }
-        return;
-    }
 #pragma unroll
     for (int half = 0; half < 2; half++) {
         const int n = n0 + half * 32 + lr;
@@ -802,7 +762,7 @@ static void launch_gemm_ks(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, 
     const int grid_x = 8 * p.tiles_m * ((p.tiles_n + 7) / 8);
     hipLaunchKernelGGL((k_gemm_q8_0_mfma<KS, false>), dim3(grid_x, p.splits), dim3(kGemmThreads), 0, ctx->stream,
                        xq, xd, w->qs, w->d, y, part, cnt, nullptr, (int)M, (int)w->n, (int)w->k, p.tiles_m,
-                       p.tiles_n, p.bps, p.splits, epoch, nullptr, nullptr, 0);
+                       p.tiles_n, p.bps, p.splits, epoch);
 }
 
 // Buffer-load offsets are 32-bit: every row tile of A and W must lie below 2 GiB.
@@ -916,36 +876,19 @@ int vxm_launch_mul_mat_parts(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq
 }
 
 // The gate/up projection with SwiGLU and the Q8_0 of its output fused into the
-// tiled GEMM's epilogue (rows of w interleave gate n = row 2n and up n = row
+// small-M GEMM's epilogue (rows of w interleave gate n = row 2n and up n = row
 // 2n+1): sq [M][N/2] and sd [M][N/64] are the down projection's input.  Returns
-// false without launching when the product would take another kernel or a K split.
+// false without launching when the small-M kernel does not take the product (the
+// tiled GEMM plus k_swiglu_quant are faster than a fused tiled epilogue at M = 512).
 bool vxm_launch_gate_up_swiglu(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                                int8_t *sq, uint16_t *sd, int variant, int *rc) {
     *rc = VXM_OK;
-    const int N = (int)w->n, K = (int)w->k, nb = K / 32;
-    const bool mfma = ctx->path == VXM_PATH_MFMA || ctx->path == VXM_PATH_MFMA_TILED ||
-                      (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
+    const int64_t N = w->n, K = w->k;
+    const bool mfma = ctx->path == VXM_PATH_MFMA || (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
     SmallPlan sp;
-    if (!mfma || M <= 0 || N % 64) return false;
-    if (ctx->path != VXM_PATH_MFMA_TILED && small_plan(ctx, M, N, K, VXM_MAX_PARTS, sp)) {
-        // the small-M kernel, unsplit (each workgroup holds whole 32-pair blocks over all of K)
-        small_plan(ctx, M, N, K, 1, sp);
-        launch_small(ctx, w, xq, xd, M, nullptr, sp, sq, sd, variant);
-        if (hipGetLastError() != hipSuccess) *rc = vxm_fail(ctx, VXM_ERR_BACKEND, "gate/up + SwiGLU launch failed");
-        return true;
-    }
-    if (!gemm_fits(M, N, K)) return false;
-    const GemmPlan p = gemm_plan(ctx, M, N, nb);
-    if (p.splits != 1) return false;
-    const int grid_x = 8 * p.tiles_m * ((p.tiles_n + 7) / 8);
-    if (p.ks == 16)
-        hipLaunchKernelGGL((k_gemm_q8_0_mfma<16, false>), dim3(grid_x, 1), dim3(kGemmThreads), 0, ctx->stream, xq,
-                           xd, w->qs, w->d, nullptr, nullptr, nullptr, nullptr, (int)M, N, K, p.tiles_m, p.tiles_n,
-                           p.bps, 1, 0u, sq, sd, variant);
-    else
-        hipLaunchKernelGGL((k_gemm_q8_0_mfma<8, false>), dim3(grid_x, 1), dim3(kGemmThreads), 0, ctx->stream, xq,
-                           xd, w->qs, w->d, nullptr, nullptr, nullptr, nullptr, (int)M, N, K, p.tiles_m, p.tiles_n,
-                           p.bps, 1, 0u, sq, sd, variant);
+    if (!mfma || M <= 0 || N % 64 || !small_plan(ctx, M, N, K, 1, sp)) return false;
+    // unsplit: each workgroup holds whole 32-pair blocks over all of K
+    launch_small(ctx, w, xq, xd, M, nullptr, sp, sq, sd, variant);
     if (hipGetLastError() != hipSuccess) *rc = vxm_fail(ctx, VXM_ERR_BACKEND, "gate/up + SwiGLU launch failed");
     return true;
 }
@@ -960,8 +903,7 @@ static int launch_gemm_dots(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq,
     const int tiles_m = (int)((M + GM - 1) / GM), tiles_n = (N + GN - 1) / GN;
     const int grid_x = 8 * tiles_m * ((tiles_n + 7) / 8);
     hipLaunchKernelGGL((k_gemm_q8_0_mfma<8, true>), dim3(grid_x, 1), dim3(kGemmThreads), 0, ctx->stream, xq, xd,
-                       w->qs, w->d, nullptr, nullptr, nullptr, out, (int)M, N, K, tiles_m, tiles_n, nb, 1, 0u,
-                       nullptr, nullptr, 0);
+                       w->qs, w->d, nullptr, nullptr, nullptr, out, (int)M, N, K, tiles_m, tiles_n, nb, 1, 0u);
     VXM_CHECK_LAUNCH(ctx);
     return VXM_OK;
 }
