@@ -540,27 +540,34 @@ __device__ __forceinline__ float half_at(const v4i &v, int j) {
 
 __device__ __forceinline__ long pack64(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
 
-template <int MT>
-__global__ __launch_bounds__(64 * kSmallRG) void k_gemm_q8_0_small(const int8_t *__restrict__ xq,
+template <int MT, int KG>
+__global__ __launch_bounds__(64 * kSmallRG * KG) void k_gemm_q8_0_small(const int8_t *__restrict__ xq,
                                                                    const uint16_t *__restrict__ xd,
                                                                    const int8_t *__restrict__ wq,
                                                                    const uint16_t *__restrict__ wd,
                                                                    float *__restrict__ y, int M, int N, int K,
                                                                    int bps, int8_t *__restrict__ sq,
                                                                    uint16_t *__restrict__ sd, int variant) {
+    // KG groups of kSmallRG waves split the workgroup's K range in halves (KG = 2) and add
+    // their partial products through LDS at the end; NT = threads per group
     constexpr int SB = kSmallStage, ROWS = 16 * MT, NT = 64 * kSmallRG;
-    __shared__ __align__(16) int8_t xs[ROWS * kSmallPitch];
-    __shared__ float xds[ROWS][SB + 1];
+    __shared__ __align__(16) int8_t xs_all[KG][ROWS * kSmallPitch];
+    __shared__ float xds_all[KG][ROWS][SB + 1];
     const int nb = K / 32;
     const int g = blockIdx.x, z = blockIdx.y;
     // row tile of x: rows m0 .. m0 + Mt - 1 (one tile unless M > 16 MT)
     const int m0 = blockIdx.z * ROWS, Mt = min(ROWS, M - m0);
     xq += (int64_t)m0 * K;
     xd += (int64_t)m0 * nb;
-    const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, r = lane & 15;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tid_all = threadIdx.x, lane = tid_all & 63, q = lane >> 4, r = lane & 15;
+    const int wave_all = __builtin_amdgcn_readfirstlane(tid_all >> 6);
+    const int kg = wave_all / kSmallRG, wave = wave_all % kSmallRG, tid = tid_all % NT;
+    int8_t *const xs = xs_all[kg];
+    float(*const xds)[SB + 1] = xds_all[kg];
     const int nw = g * 16 * kSmallRG + 16 * wave;
-    const int zb0 = z * bps, zb1 = min(nb, zb0 + bps);
+    // this group's share of the split's K blocks (the plan makes both shares equal)
+    const int zs0 = z * bps, zs1 = min(nb, zs0 + bps), share = (zs1 - zs0) / KG;
+    const int zb0 = zs0 + kg * share, zb1 = zb0 + share;
     const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)wq, (short)0, N * K, 0x00020000);
     const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)xq, (short)0, Mt * K, 0x00020000);
     const __amdgpu_buffer_rsrc_t wd_rsrc =
@@ -664,6 +671,23 @@ __global__ __launch_bounds__(64 * kSmallRG) void k_gemm_q8_0_small(const int8_t 
         if (kb0 + 2 * SB < zb1) issue(sa, kb0 + 2 * SB);
         run(sb, kb0 + SB);
     }
+    if (KG > 1) {
+        // group 1 hands its partial products to group 0 (added as group 0 + group 1)
+        __shared__ float kred[kSmallRG][MT * 4][64];
+        if (kg == 1) {
+#pragma unroll
+            for (int t = 0; t < MT; t++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) kred[wave][t * 4 + v][lane] = acc[t][v];
+        }
+        __syncthreads();
+        if (kg == 0) {
+#pragma unroll
+            for (int t = 0; t < MT; t++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[t][v] = acc[t][v] + kred[wave][t * 4 + v][lane];
+        }
+    }
     if (sq) {
         // SwiGLU + Q8_0 epilogue (one split): the workgroup's 64 weight rows are 32 (gate,
         // up) pairs, rows 4q + v with v even (gate) and v + 1 (up) in the same lane, so each
@@ -671,17 +695,19 @@ __global__ __launch_bounds__(64 * kSmallRG) void k_gemm_q8_0_small(const int8_t 
         // k_swiglu_quant), gathered through LDS and quantized by four threads per row with
         // the activation rule of quant_block_4lanes.
         __shared__ float ps[ROWS][33];
+        if (kg == 0) {
 #pragma unroll
-        for (int t = 0; t < MT; t++)
+            for (int t = 0; t < MT; t++)
 #pragma unroll
-            for (int vp = 0; vp < 2; vp++) {
-                const float gb = vxm_bf16(acc[t][2 * vp]);
-                const float sl = vxm_bf16(__fdiv_rn(gb, 1.0f + expf(-gb)));
-                ps[16 * t + r][8 * wave + 2 * q + vp] = vxm_bf16(sl * vxm_bf16(acc[t][2 * vp + 1]));
-            }
+                for (int vp = 0; vp < 2; vp++) {
+                    const float gb = vxm_bf16(acc[t][2 * vp]);
+                    const float sl = vxm_bf16(__fdiv_rn(gb, 1.0f + expf(-gb)));
+                    ps[16 * t + r][8 * wave + 2 * q + vp] = vxm_bf16(sl * vxm_bf16(acc[t][2 * vp + 1]));
+                }
+        }
         __syncthreads();
-        const int F = N / 2, row = tid >> 2, part = tid & 3;
-        if (row < ROWS) {   // NT = 4 ROWS for MT = 4; fewer rows leave whole 4-lane groups idle
+        const int F = N / 2, row = tid_all >> 2, part = tid_all & 3;
+        if (row < ROWS) {   // group 0's threads, four per row; idle threads leave whole 4-lane groups
             float pv[8], amax = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
@@ -711,6 +737,7 @@ __global__ __launch_bounds__(64 * kSmallRG) void k_gemm_q8_0_small(const int8_t 
         }
         return;
     }
+    if (kg != 0) return;
     float *yz = y + (int64_t)z * M * N + (int64_t)m0 * N;
 #pragma unroll
     for (int t = 0; t < MT; t++) {
@@ -804,7 +831,7 @@ constexpr int kMfmaMinRows = 8;
 // idle (at most max_parts).  Shapes outside the kernel's layout (N % 64,
 // K % 256, M > 64, operands of 2 GiB) take the tiled GEMM.
 struct SmallPlan {
-    int mt, bps, splits, groups, mtiles;
+    int mt, bps, splits, groups, mtiles, kg;
 };
 
 static bool small_plan(vxm_ctx *ctx, int64_t M, int64_t N, int64_t K, int max_parts, SmallPlan &p,
@@ -821,21 +848,32 @@ static bool small_plan(vxm_ctx *ctx, int64_t M, int64_t N, int64_t K, int max_pa
     const int per = (stages + s - 1) / s;   // stages per split
     p.bps = per * kSmallStage;
     p.splits = (nb + p.bps - 1) / p.bps;
+    // two wave groups per workgroup halve each split's serial stage chain when every
+    // split (the last one included) holds an even number of stages
+    p.kg = (per % 2 == 0 && stages % 2 == 0) ? 2 : 1;
     return true;
 }
 
 static void launch_small(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                          float *y, const SmallPlan &p, int8_t *sq = nullptr, uint16_t *sd = nullptr,
                          int variant = 0) {
-    const dim3 grid(p.groups, p.splits, p.mtiles), block(64 * kSmallRG);
+    const dim3 grid(p.groups, p.splits, p.mtiles), block(64 * kSmallRG * p.kg);
     const int N = (int)w->n, K = (int)w->k;
 #define VXM_SMALL_ARGS xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps, sq, sd, variant
+#define VXM_SMALL_MT(MT)                                                                                \
+    do {                                                                                                \
+        if (p.kg == 2)                                                                                  \
+            hipLaunchKernelGGL((k_gemm_q8_0_small<MT, 2>), grid, block, 0, ctx->stream, VXM_SMALL_ARGS); \
+        else                                                                                            \
+            hipLaunchKernelGGL((k_gemm_q8_0_small<MT, 1>), grid, block, 0, ctx->stream, VXM_SMALL_ARGS); \
+    } while (0)
     switch (p.mt) {
-        case 1: hipLaunchKernelGGL(k_gemm_q8_0_small<1>, grid, block, 0, ctx->stream, VXM_SMALL_ARGS); break;
-        case 2: hipLaunchKernelGGL(k_gemm_q8_0_small<2>, grid, block, 0, ctx->stream, VXM_SMALL_ARGS); break;
-        case 3: hipLaunchKernelGGL(k_gemm_q8_0_small<3>, grid, block, 0, ctx->stream, VXM_SMALL_ARGS); break;
-        default: hipLaunchKernelGGL(k_gemm_q8_0_small<4>, grid, block, 0, ctx->stream, VXM_SMALL_ARGS); break;
+        case 1: VXM_SMALL_MT(1); break;
+        case 2: VXM_SMALL_MT(2); break;
+        case 3: VXM_SMALL_MT(3); break;
+        default: VXM_SMALL_MT(4); break;
     }
+#undef VXM_SMALL_MT
 #undef VXM_SMALL_ARGS
 }
 
