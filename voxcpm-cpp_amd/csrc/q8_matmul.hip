@@ -834,14 +834,13 @@ struct SmallPlan {
     int mt, bps, splits, groups, mtiles, kg;
 };
 
-static bool small_plan(vxm_ctx *ctx, int64_t M, int64_t N, int64_t K, int max_parts, SmallPlan &p,
-                       int64_t max_rows = VXM_SMALL_MAX_ROWS) {
-    if (M < 1 || M > max_rows || N % (16 * kSmallRG) || K % (32 * kSmallStage)) return false;
-    // 32-bit buffer offsets: the weights, and the activation rows of every row tile
-    if (N * K >= ((int64_t)1 << 31) || VXM_SMALL_MAX_ROWS * K >= ((int64_t)1 << 31) || M >= (1 << 20)) return false;
+static bool small_plan(vxm_ctx *ctx, int64_t M, int64_t N, int64_t K, int max_parts, SmallPlan &p) {
+    if (M < 1 || M > VXM_SMALL_MAX_ROWS || N % (16 * kSmallRG) || K % (32 * kSmallStage)) return false;
+    // 32-bit buffer offsets: the weights, and the activation rows
+    if (N * K >= ((int64_t)1 << 31) || VXM_SMALL_MAX_ROWS * K >= ((int64_t)1 << 31)) return false;
     const int nb = (int)(K / 32), stages = nb / kSmallStage;
-    p.mt = M > VXM_SMALL_MAX_ROWS ? 4 : (int)((M + 15) / 16);
-    p.mtiles = (int)((M + 16 * p.mt - 1) / (16 * p.mt));
+    p.mt = (int)((M + 15) / 16);
+    p.mtiles = 1;   // the kernel takes row tiles of 16 MT (blockIdx.z); M <= 64 is one tile
     p.groups = (int)(N / (16 * kSmallRG));
     int s = 1;
     while (s * 2 <= max_parts && s * 2 <= stages && (int64_t)p.groups * p.mtiles * s < ctx->n_cu) s *= 2;
