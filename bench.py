@@ -451,6 +451,7 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--cfm-only", action="store_true", help="time only the CFM solve leg")
     ap.add_argument("--gemv-only", action="store_true", help="time only the isolated Q8_0 GEMV leg")
+    ap.add_argument("--lm-update-only", action="store_true", help="time only the per-token LM update leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 device copies of 256 MiB (a known-traffic kernel for HBM counter scaling)")
     args = ap.parse_args()
@@ -474,7 +475,7 @@ def main():
     res = {}
     pre = None
     cfm = None
-    if not args.decode_only and not args.prefill_only and not args.gemv_only:
+    if not args.decode_only and not args.prefill_only and not args.gemv_only and not args.lm_update_only:
         us_cfm, evals, fin = bench_cfm(ctx, torch, vxm, 5)
         eb = locdit_eval_bytes()
         ops = 2 * 2 * (3 + DIT["PC"] + DIT["P"]) * (eb * 32 // 34)
@@ -489,7 +490,7 @@ def main():
             print(json.dumps({"cfm": cfm}))
             ctx.close()
             return
-    if not args.decode_only and not args.gemv_only:
+    if not args.decode_only and not args.gemv_only and not args.lm_update_only:
         M = args.prefill_tokens
         gemms = {}
         for name, (N, K) in (("qkv", (NH * HD + 2 * NKV * HD, H)), ("o", (H, NH * HD)), ("gate_up", (2 * F, H)),
@@ -515,7 +516,7 @@ def main():
             print(json.dumps({"prefill": pre}))
             ctx.close()
             return
-    if not args.decode_only:
+    if not args.decode_only and not args.lm_update_only:
         for (N, K) in ((6144, 2048), (2048, 6144)):
             us = bench_gemv(ctx, torch, vxm, N, K, 64, 10)
             gbs = gemv_bytes(N, K) / (us * 1e-6) / 1e9
@@ -539,14 +540,20 @@ def main():
     log(f"generated {L} Q8_0 layers in {time.time() - t0:.1f} s")
 
     us1 = None
-    if not args.decode_only:
+    if not args.decode_only and not args.lm_update_only:
         # one decoder layer, context 512 (8 rotated copies of the layer)
         us1, _ = bench_decode(ctx, torch, vxm, layers[:1], 1, 8, 512, 64, 4, mode)
         layer_b = step_bytes(512, 1)
         log(f"one layer decode @ctx512: {us1:.2f} us, {layer_b / (us1 * 1e-6) / 1e9:.1f} GB/s")
 
-    us_step, finite = bench_decode(ctx, torch, vxm, layers, L, args.copies, 256, args.steps, args.warmup, mode)
     mean_ctx = 256 + (args.steps - 1) / 2.0
+    if args.lm_update_only:
+        us_u, fin_u = bench_lm_update(ctx, torch, vxm, layers, 256, args.steps, args.warmup)
+        log(f"lm update (LocEnc + TSLM + FSQ + RALM): {us_u:.1f} us/token, finite={fin_u}")
+        print(json.dumps({"lm_update": {"us_per_update": round(us_u, 1), "finite": fin_u}}))
+        ctx.close()
+        return
+    us_step, finite = bench_decode(ctx, torch, vxm, layers, L, args.copies, 256, args.steps, args.warmup, mode)
     sb = step_bytes(mean_ctx)
     gbs = sb / (us_step * 1e-6) / 1e9
     log(f"28-layer decode step: {us_step:.1f} us/token, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM), "

@@ -826,6 +826,9 @@ static int launch_gemm(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, cons
 // Rows of activations from which the MFMA GEMM replaces the weight-streaming
 // GEMV (which re-reads each activation row per weight row group).
 constexpr int kMfmaMinRows = 8;
+// Inside the block pipeline (no fix-up launch for K splits, SwiGLU fused into
+// gate/up) the small-M kernel already beats the GEMV from 2 rows.
+constexpr int kSmallPartsMinRows = 2;
 
 // Small-M plan: K splits in whole stages, doubling while the grid leaves CUs
 // idle (at most max_parts).  Shapes outside the kernel's layout (N % 64,
@@ -903,7 +906,7 @@ int vxm_launch_mul_mat_parts(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq
     *parts = 1;
     if (M <= 0) return VXM_OK;
     SmallPlan sp;
-    const bool small = (ctx->path == VXM_PATH_MFMA || (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows)) &&
+    const bool small = (ctx->path == VXM_PATH_MFMA || (ctx->path == VXM_PATH_AUTO && M >= kSmallPartsMinRows)) &&
                        small_plan(ctx, M, w->n, w->k, max_parts < VXM_MAX_PARTS ? max_parts : VXM_MAX_PARTS, sp);
     if (!small) return vxm_launch_mul_mat(ctx, w, xq, xd, M, y);
     launch_small(ctx, w, xq, xd, M, y, sp);
@@ -921,7 +924,7 @@ bool vxm_launch_gate_up_swiglu(vxm_ctx *ctx, const vxm_weight *w, const int8_t *
                                int8_t *sq, uint16_t *sd, int variant, int *rc) {
     *rc = VXM_OK;
     const int64_t N = w->n, K = w->k;
-    const bool mfma = ctx->path == VXM_PATH_MFMA || (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
+    const bool mfma = ctx->path == VXM_PATH_MFMA || (ctx->path == VXM_PATH_AUTO && M >= kSmallPartsMinRows);
     SmallPlan sp;
     if (!mfma || M <= 0 || N % 64 || !small_plan(ctx, M, N, K, 1, sp)) return false;
     // unsplit: each workgroup holds whole 32-pair blocks over all of K
