@@ -148,6 +148,26 @@ def test_locdit_full_width_one_block(vxm_ctx, orc):
     m.free()
 
 
+@pytest.mark.parametrize("path", ["auto", "tiled", "gemv"])
+def test_locdit_full_width_one_block_every_matmul_path(vxm_ctx, orc, path):
+    """The same block through each matmul path: the small-M kernel with SwiGLU fused into
+    gate/up and K-split slices (AUTO at 24 rows), the tiled GEMM with the per-op SwiGLU,
+    and the weight-streaming GEMV; each meets the oracle bar on its own."""
+    import vxm
+
+    m, ow, ocfg = _model(vxm_ctx, orc, 53, **dict(FULL, L=1))
+    x, cond, mu = make_inputs(54, 4, 17, 64, 1024)
+    ref = orc.locdit_forward(ocfg, ow, x, cond, 0.3, 0.0, mu)
+    code = {"auto": vxm.PATH_AUTO, "tiled": vxm.PATH_MFMA_TILED, "gemv": vxm.PATH_GEMV}[path]
+    try:
+        vxm_ctx.set_path(code)
+        v = m.forward(_dev(x), _dev(cond), 0.3, 0.0, _dev(mu)).cpu().numpy()
+    finally:
+        vxm_ctx.set_path(vxm.PATH_AUTO)
+    assert_layer_close(v, ref, what=f"locdit full width L=1, {path} path")
+    m.free()
+
+
 def test_locdit_full_size_forward(vxm_ctx, orc):
     """The CFM velocity workload: hidden 1024, 12 layers, 16 x 64 heads, FFN 4096;
     4 latent tokens + 17 cond tokens + mu(2) + t(1) = 24 rows per branch.  Every
