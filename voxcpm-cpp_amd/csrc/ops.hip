@@ -64,7 +64,8 @@ __device__ __forceinline__ void quant_block_4lanes(const float v[8], int variant
 // ggml_rms_norm (sum of fp32 squares in double, mean = (float)(sum/n),
 // scale = 1/sqrtf(mean + eps)), BF16, * gain, BF16.  Outputs y (fp32, if
 // non-null) and its Q8_0 quantization (xq/xd, if non-null).
-// One workgroup of 256 threads per row; n % 8 == 0 and n <= 8 * 256 * VXM_NORM_CHUNKS.
+// One workgroup per row: 128 threads for n <= 1024, else 256; n % 8 == 0 and
+// n <= 8 * 256 * VXM_NORM_CHUNKS.
 // ---------------------------------------------------------------------------
 #define VXM_NORM_CHUNKS 4
 __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const vxm_parts delta, float res_scale,
@@ -80,7 +81,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const vx
     float4 gl[VXM_NORM_CHUNKS][2];
 #pragma unroll
     for (int c = 0; c < VXM_NORM_CHUNKS; c++) {
-        const int base = (c * 256 + threadIdx.x) * 8;
+        const int base = (c * (int)blockDim.x + threadIdx.x) * 8;
         if (gain && base < n) {
             gl[c][0] = *(const float4 *)(gain + base);
             gl[c][1] = *(const float4 *)(gain + base + 4);
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const vx
     double ss = 0.0;
 #pragma unroll
     for (int c = 0; c < VXM_NORM_CHUNKS; c++) {
-        const int base = (c * 256 + threadIdx.x) * 8;
+        const int base = (c * (int)blockDim.x + threadIdx.x) * 8;
         if (base < n) {
             float4 a = *(const float4 *)(hr + base), b = *(const float4 *)(hr + base + 4);
             v[c][0] = a.x; v[c][1] = a.y; v[c][2] = a.z; v[c][3] = a.w;
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const vx
     const float sc = __fdiv_rn(1.0f, __fsqrt_rn(mean + eps));
 #pragma unroll
     for (int c = 0; c < VXM_NORM_CHUNKS; c++) {
-        const int base = (c * 256 + threadIdx.x) * 8;
+        const int base = (c * (int)blockDim.x + threadIdx.x) * 8;
         if (base >= n) continue;   // whole 32-blocks live in 4 consecutive lanes: n % 32 == 0
         float o[8];
         const float4 g0 = gl[c][0], g1 = gl[c][1];
@@ -160,7 +161,9 @@ int vxm_launch_rmsnorm(vxm_ctx *ctx, float *h, vxm_parts delta, float res_scale,
     if (n % 32 != 0 || n > 8 * 256 * VXM_NORM_CHUNKS)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "rms_norm: n=%lld must be a multiple of 32 and <= %d",
                         (long long)n, 8 * 256 * VXM_NORM_CHUNKS);
-    hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(256), 0, ctx->stream, h, delta, res_scale, gain,
+    // rows of up to 1024 values fit 128 threads (8 values each): two waves reduce faster than four
+    const unsigned threads = n <= 8 * 128 ? 128 : 256;
+    hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(threads), 0, ctx->stream, h, delta, res_scale, gain,
                        (int)n, eps, y, xq, xd, variant);
     VXM_CHECK_LAUNCH(ctx);
     return VXM_OK;
