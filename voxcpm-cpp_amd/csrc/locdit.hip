@@ -506,13 +506,16 @@ extern "C" int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev,
     }
     if (key != m->cfm_last_eager) {
         m->cfm_last_eager = key;
-        return euler_loop();
+        ctx->no_split_tags = true;
+        rc = euler_loop();
+        ctx->no_split_tags = false;
+        return rc;
     }
     cfm_graph_drop(m);
     VXM_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-    ctx->capturing = true;
+    ctx->no_split_tags = true;
     rc = euler_loop();
-    ctx->capturing = false;
+    ctx->no_split_tags = false;
     hipGraph_t graph = nullptr;
     const hipError_t ec = hipStreamEndCapture(ctx->stream, &graph);
     if (rc == VXM_OK && ec != hipSuccess)

@@ -775,7 +775,7 @@ static GemmPlan gemm_plan(vxm_ctx *ctx, int64_t M, int N, int nb) {
     p.ks = p.tiles_m == 1 ? 16 : 8;
     int s = 1;
     // no split under graph capture: the split tags are per launch
-    while (!ctx->capturing && s < kGemmMaxSplits && (int64_t)p.tiles_m * p.tiles_n * s < ctx->n_cu &&
+    while (!ctx->no_split_tags && s < kGemmMaxSplits && (int64_t)p.tiles_m * p.tiles_n * s < ctx->n_cu &&
            nb / (s * 2) >= 2 * p.ks)
         s *= 2;
     p.bps = (nb + s - 1) / s;

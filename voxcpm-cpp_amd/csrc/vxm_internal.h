@@ -32,9 +32,11 @@ struct vxm_ctx {
     // K-split slices of the small-M GEMM behind the public matmul entries
     void *parts_buf = nullptr;
     size_t parts_bytes = 0;
-    // set while the stream is captured into a HIP graph: launches must not bake
-    // per-launch state (the tiled GEMM's split tags) into the graph
-    bool capturing = false;
+    // set around the CFM Euler loop, eager or captured into a HIP graph: the
+    // tiled GEMM takes no K split there, because its split tags are per launch
+    // (a graph would replay stale tags) and an eager run must add in the same
+    // order as the replays
+    bool no_split_tags = false;
 };
 
 // Device layout of a Q8_0 matrix (n_rows x k).  The GGUF row of k/32 34-byte
