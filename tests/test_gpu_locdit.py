@@ -234,15 +234,23 @@ def test_cfm_full_size_one_step_and_repeatable(vxm_ctx, orc):
     m.free()
 
 
-def test_cfm_graph_replays_match_eager(vxm_ctx, orc):
+# Widths off the small-M kernel's layout (N % 64, K % 256) and a head size off the fused
+# local attention: the tiled GEMM (down: a K split outside the Euler loop) and the
+# per-op attention run inside the recorded loop.
+ODD = dict(H=160, L=2, nh=5, nkv=5, hd=32, F=2080, feat=64)
+
+
+@pytest.mark.parametrize("cfg", ["full", "odd"])
+def test_cfm_graph_replays_match_eager(vxm_ctx, orc, cfg):
     """vxm_cfm_solve records its Euler loop as a HIP graph on the second call with the
     same arguments and buffers and replays it afterwards: every replay, with eager work
     and synchronizations in between, is bit-identical to the eager first call; a call
     with other arguments runs eagerly and the recorded loop still replays correctly."""
     import torch
 
-    m, _, _ = _model(vxm_ctx, orc, 81, **FULL)
-    x0, cond, mu = make_inputs(82, 4, 17, 64, 1024)
+    dims = FULL if cfg == "full" else ODD
+    m, _, _ = _model(vxm_ctx, orc, 81, **dims)
+    x0, cond, mu = make_inputs(82, 4, 17, 64, dims["H"])
     cd, md = _dev(cond), _dev(mu)
     x0d = _dev(x0)
     x = torch.empty_like(x0d)
