@@ -293,12 +293,13 @@ static int dit_eval(vxm_locdit *m, const float *x, int P, int Pc, int n_seg, con
         if ((rc = vxm_block_run(ctx, d, b, m->ws, m->seq, M, site))) return rc;
     }
     // last residual + final RMSNorm of the x rows of each segment (src/locdit.c:373-390)
-    for (int g = 0; g < n_seg; g++) {
-        const int64_t r0 = g * S + 3 + Pc;
+    // one launch over the P x rows of every segment (rows 3 + Pc .. S - 1 of each)
+    {
+        const int64_t r0 = 3 + Pc;
         const vxm_parts &dn = m->ws.dn_out;
         const vxm_parts delta = m->cfg.n_layers ? vxm_parts{dn.p + r0 * H, dn.n, dn.stride} : vxm_parts{};
-        if ((rc = vxm_launch_rmsnorm(ctx, m->seq + r0 * H, delta, 1.0f, m->norm, P, H, d.eps, nullptr,
-                                     m->aq + (int64_t)g * P * H, m->ad + (int64_t)g * P * (H / 32), var)))
+        if ((rc = vxm_launch_rmsnorm(ctx, m->seq + r0 * H, delta, 1.0f, m->norm, (int64_t)n_seg * P, H, d.eps,
+                                     nullptr, m->aq, m->ad, var, P, (int)S)))
             return rc;
     }
     return vxm_launch_mul_mat(ctx, m->out_proj, m->aq, m->ad, (int64_t)n_seg * P, m->vo);

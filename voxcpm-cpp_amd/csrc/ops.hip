@@ -71,11 +71,15 @@ __device__ __forceinline__ void quant_block_4lanes(const float v[8], int variant
 __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const vxm_parts delta, float res_scale,
                                                  const float *__restrict__ gain, int n, float eps,
                                                  float *__restrict__ y, int8_t *__restrict__ xq,
-                                                 uint16_t *__restrict__ xd, int variant) {
+                                                 uint16_t *__restrict__ xd, int variant, int seg_rows,
+                                                 int seg_stride) {
     __shared__ double shd[4];
+    // output row `row`; its h / delta row: seg_rows rows of every seg_stride (the identity
+    // when seg_rows == seg_stride)
     const int row = blockIdx.x;
-    float *hr = h + (int64_t)row * n;
-    const float *dr = delta.p ? delta.p + (int64_t)row * n : nullptr;
+    const int64_t hrow = (int64_t)(row / seg_rows) * seg_stride + row % seg_rows;
+    float *hr = h + hrow * n;
+    const float *dr = delta.p ? delta.p + hrow * n : nullptr;
     float v[VXM_NORM_CHUNKS][8];
     // the gain, fetched with the row (it is needed right after the reduction)
     float4 gl[VXM_NORM_CHUNKS][2];
@@ -156,15 +160,18 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const vx
 }
 
 int vxm_launch_rmsnorm(vxm_ctx *ctx, float *h, vxm_parts delta, float res_scale, const float *gain,
-                       int64_t rows, int64_t n, float eps, float *y, int8_t *xq, uint16_t *xd, int variant) {
+                       int64_t rows, int64_t n, float eps, float *y, int8_t *xq, uint16_t *xd, int variant,
+                       int seg_rows, int seg_stride) {
     if (rows <= 0) return VXM_OK;
+    if (seg_rows <= 0) seg_rows = seg_stride = (int)rows;
+    if (seg_stride < seg_rows) return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "rms_norm: segment stride below its rows");
     if (n % 32 != 0 || n > 8 * 256 * VXM_NORM_CHUNKS)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "rms_norm: n=%lld must be a multiple of 32 and <= %d",
                         (long long)n, 8 * 256 * VXM_NORM_CHUNKS);
     // rows of up to 1024 values fit 128 threads (8 values each): two waves reduce faster than four
     const unsigned threads = n <= 8 * 128 ? 128 : 256;
     hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(threads), 0, ctx->stream, h, delta, res_scale, gain,
-                       (int)n, eps, y, xq, xd, variant);
+                       (int)n, eps, y, xq, xd, variant, seg_rows, seg_stride);
     VXM_CHECK_LAUNCH(ctx);
     return VXM_OK;
 }

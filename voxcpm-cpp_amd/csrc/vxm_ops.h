@@ -2,8 +2,10 @@
 #pragma once
 #include "vxm_internal.h"
 
+// rows output rows; with seg_rows > 0 the h / delta rows are seg_rows of every seg_stride
 int vxm_launch_rmsnorm(vxm_ctx *ctx, float *h, vxm_parts delta, float res_scale, const float *gain,
-                       int64_t rows, int64_t n, float eps, float *y, int8_t *xq, uint16_t *xd, int variant);
+                       int64_t rows, int64_t n, float eps, float *y, int8_t *xq, uint16_t *xd, int variant,
+                       int seg_rows = 0, int seg_stride = 0);
 int vxm_launch_rope_kv(vxm_ctx *ctx, vxm_parts qkv, int64_t M, int nh, int nkv, int hd, int pos0, int S,
                        const float2 *cs, int cs_rows, int no_rope, float *q_out, uint16_t *kc,
                        uint16_t *vc, int cap, int64_t seg_stride, int cache_pos0);
