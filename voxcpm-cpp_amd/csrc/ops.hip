@@ -522,7 +522,7 @@ int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const
 // K-split slices.  Output: the Q8_0 rows of the attention output (xq, xd).
 // ---------------------------------------------------------------------------
 constexpr int kLocalMaxS = 64, kLocalMaxElems = 2048;   // S, and S * hd per operand
-constexpr int kLocalRB = 8;                              // query rows per workgroup
+constexpr int kLocalRB = 4;                              // query rows per workgroup
 
 bool vxm_attention_local_fits(int S, int hd) {
     return S >= 1 && S <= kLocalMaxS && (hd == 64 || hd == 128) && (int64_t)S * hd <= kLocalMaxElems;
@@ -731,7 +731,7 @@ int vxm_launch_attention_local(vxm_ctx *ctx, vxm_parts qkv, int64_t M, int nh, i
                         (long long)M);
     if (!no_rope && (!cs || pos0 + S > cs_rows))
         return vxm_fail(ctx, VXM_ERR_BACKEND, "rope: table holds %d positions, %d needed", cs_rows, pos0 + S);
-    // query rows per workgroup: blocks of 8 spread a segment's rows over several CUs
+    // query rows per workgroup: blocks of kLocalRB spread a segment's rows over several CUs
     // (each block re-derives the segment's k and v)
     const int RB = kLocalRB, QB = (S + RB - 1) / RB;
     const size_t lds = (size_t)(2 * S * hd + RB * hd + (S + RB) * (hd + 4) + RB * (S + 1) + 2 * RB) * sizeof(float);
