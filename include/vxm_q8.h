@@ -381,9 +381,14 @@ int vxm_gguf_tensor_f32(const vxm_gguf *g, int64_t idx, float *out, int64_t n);
  * (src/gen_init.c:34-67): "<prefix>.<layer>.self_attn.q_proj.weight", ...
  * with prefix "base_lm.blk", "residual_lm.blk", "feat_encoder.blk" or
  * "feat_decoder.estimator.blk".  The seven projections (2-D Q8_0) point into
- * the mapping; the two norms are written as F32 to norms[2 * hidden]. */
-int vxm_gguf_layer_q8_0(vxm_gguf *g, const char *prefix, int32_t layer, int64_t hidden, float *norms,
-                        vxm_layer_weights_q8_0 *out);
+ * the mapping; the two norms are written as F32 to norms[2 * hidden].
+ * q_dim = n_heads * head_dim, kv_dim = n_kv_heads * head_dim, ffn =
+ * intermediate_size: every projection must have exactly the ne = [K, N] these
+ * give (q [hidden, q_dim], k / v [hidden, kv_dim], o [q_dim, hidden], gate /
+ * up [hidden, ffn], down [ffn, hidden]), else VXM_ERR_MODEL_FORMAT, so a file
+ * whose shapes disagree with its config is never read past a tensor. */
+int vxm_gguf_layer_q8_0(vxm_gguf *g, const char *prefix, int32_t layer, int64_t hidden, int64_t q_dim,
+                        int64_t kv_dim, int64_t ffn, float *norms, vxm_layer_weights_q8_0 *out);
 /* The TSLM (residual = 0) or RALM (residual = 1) config from the voxcpm.*
  * keys with vcpm_model_config_default's defaults and vcpm_model_load's
  * sanitisation (src/model_loader.c:52-97,139-219): eps below 1e-7 becomes

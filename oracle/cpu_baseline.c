@@ -21,7 +21,11 @@
 
 static int g_threads = 1;
 
-void cb_set_threads(int n) { g_threads = n > 0 ? n : 1; }
+/* the thread count of every parallel loop: the SIMD mul_mat and the glue */
+void cb_set_threads(int n) {
+    g_threads = n > 0 ? n : 1;
+    omp_set_num_threads(g_threads);
+}
 int cb_get_threads(void) { return g_threads; }
 
 /* ---- AVX2: sum of 32 int8 x int8 products into 8 int32 lanes, as float ---- */

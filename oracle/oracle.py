@@ -115,6 +115,9 @@ def lib():
         L.orc_cfm_cfg_zero_star.restype = _F
         L.orc_cfm_cfg_zero_star.argtypes = [_P, _P, _I, _F]
         L.orc_cfm_zero_star_steps.argtypes = [_I]
+        L.orc_cfm_step_dt.restype = _F
+        L.orc_cfm_step_dt.argtypes = [_I, _I, _I]
+        L.orc_cfm_euler_update.argtypes = [_P, _P, _I, _F]
         L.orc_cfm_solve.argtypes = [C.POINTER(Cfg), C.POINTER(LocDiT), _P, _P, C.c_int32, C.c_int32, _P,
                                     _I, _F, _I, _I]
         L.orc_locenc_forward.argtypes = [C.POINTER(Cfg), C.POINTER(LocEnc), _P, C.c_int32, _P, _P]
@@ -328,6 +331,19 @@ def cfg_zero_star(negative, positive, cfg_value):
 
 def zero_star_steps(n):
     return lib().orc_cfm_zero_star_steps(n)
+
+
+def cfm_step_dt(step, n, schedule=0):
+    return lib().orc_cfm_step_dt(step, n, schedule)
+
+
+def cfm_euler_update(x, v, dt):
+    """orc_cfm_euler_update: bf16(x + bf16(dt * v)), returned as a new array."""
+    x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    assert x.size == v.size
+    lib().orc_cfm_euler_update(_p(x), _p(v), x.size, dt)
+    return x
 
 
 def sinusoid(t, dim):

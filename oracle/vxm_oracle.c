@@ -23,6 +23,11 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* Threading.  Large products run with OpenMP over independent outputs: every
+ * output element is still formed by one thread, in the sequential order
+ * written below, so results do not depend on the thread count. */
+#define ORC_PAR_MIN 4096   /* outputs x blocks below which the loops stay serial */
+
 /* ------------------------------------------------------------------------ */
 /* number formats                                                            */
 /* ------------------------------------------------------------------------ */
@@ -138,6 +143,7 @@ void orc_quantize_row_q8_0(const float *x, uint8_t *y, int64_t k, int variant) {
 
 void orc_quantize_rows_q8_0(const float *x, uint8_t *y, int64_t rows, int64_t k, int variant) {
     const int64_t rb = k / ORC_QK8_0 * ORC_Q8_0_BLOCK_BYTES;
+#pragma omp parallel for schedule(static) if (rows * k > 64 * ORC_PAR_MIN)
     for (int64_t r = 0; r < rows; r++) orc_quantize_row_q8_0(x + r * k, y + r * rb, k, variant);
 }
 
@@ -160,6 +166,7 @@ static inline int32_t block_dot(const uint8_t *a, const uint8_t *b) {
     return s;
 }
 
+
 static inline float block_scale(const uint8_t *a, const uint8_t *b) {
     uint16_t da, db; memcpy(&da, a, 2); memcpy(&db, b, 2);
     return orc_fp16_to_fp32(da) * orc_fp16_to_fp32(db);
@@ -171,6 +178,7 @@ static inline float block_scale(const uint8_t *a, const uint8_t *b) {
 void orc_block_dots_q8_0(const uint8_t *w, const uint8_t *xq, int64_t N, int64_t K,
                          int64_t M, int32_t *out) {
     const int64_t nb = K / ORC_QK8_0, rb = nb * ORC_Q8_0_BLOCK_BYTES;
+#pragma omp parallel for collapse(2) schedule(static) if (M * N * nb > ORC_PAR_MIN)
     for (int64_t m = 0; m < M; m++)
         for (int64_t n = 0; n < N; n++)
             for (int64_t b = 0; b < nb; b++)
@@ -185,6 +193,7 @@ void orc_block_dots_q8_0(const uint8_t *w, const uint8_t *xq, int64_t N, int64_t
 void orc_mul_mat_q8_0(const uint8_t *w, const uint8_t *xq, int64_t N, int64_t K,
                       int64_t M, float *y) {
     const int64_t nb = K / ORC_QK8_0, rb = nb * ORC_Q8_0_BLOCK_BYTES;
+#pragma omp parallel for collapse(2) schedule(static) if (M * N * nb > ORC_PAR_MIN)
     for (int64_t m = 0; m < M; m++)
         for (int64_t n = 0; n < N; n++) {
             float sumf = 0.0f;
@@ -201,6 +210,7 @@ void orc_mul_mat_q8_0(const uint8_t *w, const uint8_t *xq, int64_t N, int64_t K,
 void orc_mul_mat_q8_0_f64(const uint8_t *w, const uint8_t *xq, int64_t N, int64_t K,
                           int64_t M, double *y) {
     const int64_t nb = K / ORC_QK8_0, rb = nb * ORC_Q8_0_BLOCK_BYTES;
+#pragma omp parallel for collapse(2) schedule(static) if (M * N * nb > ORC_PAR_MIN)
     for (int64_t m = 0; m < M; m++)
         for (int64_t n = 0; n < N; n++) {
             double s = 0.0;
@@ -380,14 +390,21 @@ int orc_attention(const orc_cfg *cfg, const orc_layer *w, const float *xn, int64
                 kc[(hh * kvcap + base + t) * hd + d] = orc_fp32_to_fp16(k[t * kvd + hh * hd + d]);
                 vc[(hh * kvcap + base + t) * hd + d] = orc_fp32_to_fp16(v[t * kvd + hh * hd + d]);
             }
-    for (int64_t t = 0; t < M; t++) {
-        const int64_t kv_len = no_causal ? M : pos + t + 1;
-        for (int64_t h = 0; h < nh; h++) {
-            const int64_t gi = h / qpk;
-            attend_one(q + t * qd + h * hd, kc + gi * kvcap * hd, vc + gi * kvcap * hd, kv_len, hd,
-                       hd, att + t * qd + h * hd, scratch);
-        }
+    /* every (token, head) output is formed by one thread with its own scores */
+#pragma omp parallel if (M * nh > 16)
+    {
+        float *sc = (float *)malloc(sizeof(float) * (size_t)(kvcap + 1));
+#pragma omp for collapse(2) schedule(dynamic, 4)
+        for (int64_t t = 0; t < M; t++)
+            for (int64_t h = 0; h < nh; h++) {
+                const int64_t kv_len = no_causal ? M : pos + t + 1;
+                const int64_t gi = h / qpk;
+                attend_one(q + t * qd + h * hd, kc + gi * kvcap * hd, vc + gi * kvcap * hd, kv_len, hd,
+                           hd, att + t * qd + h * hd, sc);
+            }
+        free(sc);
     }
+    (void)scratch;
     layer_mul_mat(w, w->wo, att, H, qd, M, out, var);
     for (int64_t i = 0; i < M * H; i++) out[i] = orc_bf16_round(out[i]);
     free(q); free(k); free(v); free(att); free(lk); free(lv); free(scratch);
@@ -593,6 +610,19 @@ int orc_cfm_zero_star_steps(int n_steps) {
     return z > 1 ? z : 1;
 }
 
+/* The time step of Euler step `step` (src/gen_step.c:597-600): dt = bf16(-(t_k - t_{k+1}))
+ * on the schedule (0 = sway, 1 = uniform). */
+float orc_cfm_step_dt(int step, int n_steps, int schedule) {
+    const float t = schedule ? orc_cfm_uniform_t_bf16(step, n_steps) : orc_cfm_sway_t_bf16(step, n_steps);
+    const float nt = schedule ? orc_cfm_uniform_t_bf16(step + 1, n_steps) : orc_cfm_sway_t_bf16(step + 1, n_steps);
+    return orc_bf16_round(-(t - nt));
+}
+
+/* The Euler update of the CFM loop (src/gen_step.c:626-629): x = bf16(x + bf16(dt * v)). */
+void orc_cfm_euler_update(float *x, const float *v, int n, float dt) {
+    for (int j = 0; j < n; j++) x[j] = orc_bf16_round(x[j] + orc_bf16_round(dt * v[j]));
+}
+
 /* The CFM Euler loop of vcpm_gen_step (src/gen_step.c:583-649): with CFG
  * (cfg_value != 1 and mu given, src/gen_step.c:475) the velocities of the
  * cond (mu) and uncond (mu = 0) branches and their CFG-Zero* blend, else the
@@ -610,9 +640,7 @@ int orc_cfm_solve(const orc_cfg *cfg, const orc_locdit *w, float *x, const float
     for (int step = 0; step < n_steps; step++) {
         if (step < zs) continue;
         const float t = schedule ? orc_cfm_uniform_t_bf16(step, n_steps) : orc_cfm_sway_t_bf16(step, n_steps);
-        const float nt = schedule ? orc_cfm_uniform_t_bf16(step + 1, n_steps)
-                                  : orc_cfm_sway_t_bf16(step + 1, n_steps);
-        const float dtv = orc_bf16_round(-(t - nt));
+        const float dtv = orc_cfm_step_dt(step, n_steps, schedule);
         orc_locdit_forward(cfg, w, x, cond, P, Pc, t, 0.0f, mu, vc);
         if (use_cfg) {
             orc_locdit_forward(cfg, w, x, cond, P, Pc, t, 0.0f, NULL, vu);
@@ -620,7 +648,7 @@ int orc_cfm_solve(const orc_cfg *cfg, const orc_locdit *w, float *x, const float
         } else {
             memcpy(vu, vc, sizeof(float) * (size_t)n);
         }
-        for (int j = 0; j < n; j++) x[j] = orc_bf16_round(x[j] + orc_bf16_round(dtv * vu[j]));
+        orc_cfm_euler_update(x, vu, n, dtv);
     }
     free(vc); free(vu);
     return 0;

@@ -113,6 +113,8 @@ float orc_cfm_sway_t_bf16(int step, int n_steps);
 float orc_cfm_uniform_t_bf16(int step, int n_steps);
 float orc_cfm_cfg_zero_star(float *negative, const float *positive, int n, float cfg_value);
 int   orc_cfm_zero_star_steps(int n_steps);
+float orc_cfm_step_dt(int step, int n_steps, int schedule);
+void  orc_cfm_euler_update(float *x, const float *v, int n, float dt);
 int   orc_cfm_solve(const orc_cfg *cfg, const orc_locdit *w, float *x, const float *cond,
                     int32_t P, int32_t Pc, const float *mu, int n_steps, float cfg_value,
                     int schedule, int use_zero_star);

@@ -101,8 +101,9 @@ def test_layer_weights_point_into_the_file(vxm, orc, tmp_path):
     d = rand_layer(orc, rng, H, nh, nkv, hd, F)
     ts = W.voxcpm_block_tensors("base_lm.blk", 3, d, H, nh, nkv, hd, F, norm_type=W.GGML_Q8_0, orc=orc)
     p = W.write_gguf(tmp_path / "l.gguf", [("general.architecture", W.STR, "voxcpm2")], ts)
+    cfg = dict(hidden_size=H, n_heads=nh, n_kv_heads=nkv, head_dim=hd, intermediate_size=F)
     with vxm.GGUF(p) as g:
-        lw = g.layer_q8_0("base_lm.blk", 3, H)
+        lw = g.layer_q8_0("base_lm.blk", 3, cfg)
         for key, name in (("q_proj", "self_attn.q_proj.weight"), ("down_proj", "mlp.down_proj.weight")):
             ti = g.info(f"base_lm.blk.3.{name}")
             assert getattr(lw, key) == ti.data
@@ -112,10 +113,10 @@ def test_layer_weights_point_into_the_file(vxm, orc, tmp_path):
         gq = orc.dequantize_rows(orc.quantize_rows(d["input_layernorm"][None], orc.QUANT_REF), 1, H)[0]
         assert np.array_equal(gin, gq)
         with pytest.raises(vxm.VxmError) as e:
-            g.layer_q8_0("base_lm.blk", 4, H)
+            g.layer_q8_0("base_lm.blk", 4, cfg)
         assert "base_lm.blk.4.self_attn.q_proj.weight" in str(e.value) and e.value.code == 3
         with pytest.raises(vxm.VxmError):
-            g.layer_q8_0("base_lm.blk", 3, H + 32)   # norm length mismatch
+            g.layer_q8_0("base_lm.blk", 3, dict(cfg, hidden_size=H + 32))   # norm length mismatch
 
 
 def test_non_q8_projection_is_refused(vxm, orc, tmp_path):
@@ -128,8 +129,57 @@ def test_non_q8_projection_is_refused(vxm, orc, tmp_path):
     p = W.write_gguf(tmp_path / "n.gguf", [], ts)
     with vxm.GGUF(p) as g:
         with pytest.raises(vxm.VxmError) as e:
-            g.layer_q8_0("residual_lm.blk", 0, 64)
+            g.layer_q8_0("residual_lm.blk", 0, dict(hidden_size=64, n_heads=2, n_kv_heads=1, head_dim=32,
+                                                    intermediate_size=128))
         assert e.value.code == 7
+
+
+@pytest.mark.parametrize("which,ne", [
+    (0, [64, 32]),      # q_proj with half its rows
+    (3, [32, 64]),      # o_proj with a K that is not n_heads * head_dim
+    (6, [64, 64]),      # down_proj whose K is not the FFN width
+    (4, [64, 256]),     # gate_proj with more rows than the FFN
+])
+def test_wrong_shaped_projection_is_refused(vxm, orc, tmp_path, which, ne):
+    """A projection whose ne differs from the config's shape is refused with
+    VXM_ERR_MODEL_FORMAT before any byte of it is read as weights."""
+    from test_gpu_minicpm4 import rand_layer
+
+    rng = np.random.default_rng(7 + which)
+    H, nh, nkv, hd, F = 64, 2, 1, 32, 128
+    d = rand_layer(orc, rng, H, nh, nkv, hd, F)
+    ts = W.voxcpm_block_tensors("base_lm.blk", 0, d, H, nh, nkv, hd, F)
+    name = ts[which][0]
+    q = orc.quantize_rows(rng.normal(0, 0.02, (ne[1], ne[0])).astype(np.float32), orc.QUANT_REF)
+    ts[which] = W.q8_tensor(name, q, ne[1], ne[0])
+    p = W.write_gguf(tmp_path / "s.gguf", [("general.architecture", W.STR, "voxcpm2")], ts)
+    cfg = dict(hidden_size=H, n_heads=nh, n_kv_heads=nkv, head_dim=hd, intermediate_size=F)
+    with vxm.GGUF(p) as g:
+        with pytest.raises(vxm.VxmError) as e:
+            g.layer_q8_0("base_lm.blk", 0, cfg)
+        assert e.value.code == 3 and name in str(e.value), str(e.value)
+
+
+def test_missing_intermediate_size_key_is_caught_by_the_shape_check(vxm, orc, tmp_path):
+    """Without voxcpm.intermediate_size the config takes the reference's
+    default (8192); a file whose real FFN is narrower is then refused at the
+    layer load instead of being read past its gate / up / down tensors."""
+    from test_gpu_minicpm4 import rand_layer
+
+    rng = np.random.default_rng(8)
+    H, nh, nkv, hd, F = 64, 2, 1, 32, 128
+    d = rand_layer(orc, rng, H, nh, nkv, hd, F)
+    ts = W.voxcpm_block_tensors("base_lm.blk", 0, d, H, nh, nkv, hd, F)
+    kv = [("general.architecture", W.STR, "voxcpm2"), ("voxcpm.hidden_size", W.I32, H),
+          ("voxcpm.num_attention_heads", W.I32, nh), ("voxcpm.num_kv_heads", W.I32, nkv),
+          ("voxcpm.head_dim", W.I32, hd)]
+    p = W.write_gguf(tmp_path / "k.gguf", kv, ts)
+    with vxm.GGUF(p) as g:
+        cfg = g.minicpm4_config()
+        assert cfg["intermediate_size"] == 8192
+        with pytest.raises(vxm.VxmError) as e:
+            g.layer_q8_0("base_lm.blk", 0, cfg)
+        assert e.value.code == 3 and "mlp.gate_proj" in str(e.value), str(e.value)
 
 
 def test_minicpm4_config_defaults_and_sanitisation(vxm, tmp_path):

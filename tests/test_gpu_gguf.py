@@ -37,7 +37,7 @@ def test_stack_from_gguf_matches_arrays(vxm_ctx, orc, tmp_path, H, nh, nkv, hd, 
     with vxm.GGUF(path) as g:
         cfg = g.minicpm4_config()
         assert (cfg["hidden_size"], cfg["n_layers"], cfg["n_heads"], cfg["intermediate_size"]) == (H, L, nh, F)
-        a = vxm.MiniCPM4(vxm_ctx, cfg, [g.layer_q8_0("base_lm.blk", l, H) for l in range(L)],
+        a = vxm.MiniCPM4(vxm_ctx, cfg, [g.layer_q8_0("base_lm.blk", l, cfg) for l in range(L)],
                          final_norm=g.f32("base_lm.norm.weight"))
     arr = [dict(d, input_layernorm=_dq(orc, d["input_layernorm"]),
                 post_attention_layernorm=_dq(orc, d["post_attention_layernorm"])) for d in layers]

@@ -124,6 +124,52 @@ def test_decode_gemv_full_size_seed0(vxm_ctx, orc, N, K):
     w.free()
 
 
+# (path, N, K, M): the kernel vxm_mul_mat_q8_0_q8_0 runs for each is the one whose
+# int32 block sums vxm_block_dots_q8_0 returns -- chunked GEMV <C, R> (M < 8, K a
+# multiple of 1024 in {1, 2, 4, 6} KiB), generic GEMV, small-M MFMA (one or two wave
+# groups, K splits), tiled MFMA (16- or 8-block stages, K splits)
+_PRODUCTION_DOTS = [
+    (0, 6144, 2048, 1),     # decode gate/up GEMV <2, 2>
+    (0, 2048, 6144, 1),     # decode down GEMV <6, 1>
+    (0, 2560, 2048, 3),     # GEMV <2, 2>, three activation rows
+    (0, 1024, 4096, 5),     # LocEnc down at 5 rows: GEMV <4, 1>
+    (0, 256, 1024, 2),      # GEMV <1, 4>
+    (0, 7, 96, 2),          # generic GEMV
+    (0, 8192, 1024, 48),    # CFM gate/up at 2 x 24 rows: small-M
+    (0, 3072, 1024, 48),    # CFM QKV: small-M
+    (0, 1024, 4096, 48),    # CFM down: small-M, K split
+    (2, 1024, 4096, 5),     # small-M at 5 rows (the block pipeline's choice)
+    (0, 2048, 2048, 512),   # prefill O: tiled, 8-block stages
+    (3, 2048, 2048, 33),    # tiled, 16-block stages, K split
+    (0, 2560, 2048, 100),   # tiled, ragged M tile
+]
+
+
+@pytest.mark.parametrize("path,N,K,M", _PRODUCTION_DOTS)
+def test_block_dots_of_the_kernel_that_runs(vxm_ctx, orc, path, N, K, M):
+    """The int32 block sums of the kernel the matmul dispatch picks are bit-exact,
+    and that kernel's fp32 output is the oracle combine of exactly these sums."""
+    _, x, wq = _case(orc, N, K, M, 5 * N + K + 3 * M)
+    vxm_ctx.set_path(path)
+    try:
+        w = vxm_ctx.upload_q8_0(wq, N, K)
+        xq, xd = vxm_ctx.quantize_q8_0(_dev(x), 1)
+        sums = _np(vxm_ctx.block_dots(w, xq, xd))
+        y = _np(vxm_ctx.mul_mat_q8(w, xq, xd))
+        vxm_ctx.sync()
+    finally:
+        vxm_ctx.set_path(0)
+    xq_ref = orc.quantize_rows(x, 1)
+    assert np.array_equal(sums, orc.block_dots(wq, xq_ref, N, K, M))
+    # y = sum_b sumi * (d_w * d_x) over the device's own sums, in fp64
+    _, dw = orc.split_q8(wq, N, K)
+    _, dx = orc.split_q8(xq_ref, M, K)
+    scale = (dx.view(np.float16).astype(np.float32)[:, None, :] * dw.view(np.float16).astype(np.float32)[None, :, :])
+    terms = (sums.astype(np.float32) * scale).astype(np.float64)
+    _assert_close(y, terms.sum(axis=2))
+    w.free()
+
+
 @pytest.fixture
 def mfma_path(vxm_ctx):
     import vxm

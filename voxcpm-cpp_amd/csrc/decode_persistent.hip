@@ -1148,7 +1148,11 @@ struct vxm_persistent_state {
     uint16_t *dummy_d = nullptr;
     int *err = nullptr;
     uint32_t epoch = 0;
-    const vxm_kv_cache *kv = nullptr;   // cache whose pointers are in the layer table
+    // the cache whose K/V pointers are in the layer table: its unique id, base
+    // and capacity (a freed cache's struct address can come back for a new one)
+    uint64_t kv_id = 0;
+    const void *kv_base = nullptr;
+    int kv_cap = 0;
 };
 
 static constexpr int kMaxLds = 160 * 1024;
@@ -1229,9 +1233,9 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
         // tags start as all-ones: never equal to a live (epoch >= 1) tag
         VXM_HIP(ctx, hipMemsetAsync((char *)s.base + tab, 0xff, words * 8, ctx->stream));
         VXM_HIP(ctx, hipMemsetAsync(s.dummy_q, 0, dummy + 4, ctx->stream));
-        s.kv = nullptr;
+        s.kv_id = 0;
     }
-    if (s.kv != kv) {
+    if (s.kv_id != kv->id || s.kv_base != kv->base || s.kv_cap != kv->cap) {
         std::vector<vxm_player> tabh(L);
         for (int l = 0; l < L; l++) {
             const vxm_block &b = m->blocks[l];
@@ -1241,7 +1245,9 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
         VXM_HIP(ctx, hipMemcpyAsync(s.layers, tabh.data(), L * sizeof(vxm_player), hipMemcpyHostToDevice,
                                     ctx->stream));
         VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
-        s.kv = kv;
+        s.kv_id = kv->id;
+        s.kv_base = kv->base;
+        s.kv_cap = kv->cap;
     }
     s.epoch = (s.epoch + 1) & 0xfffffu;
     if (s.epoch == 0) s.epoch = 1;

@@ -378,9 +378,14 @@ extern "C" int vxm_gguf_tensor_f32(const vxm_gguf *g, int64_t idx, float *out, i
     }
 }
 
-extern "C" int vxm_gguf_layer_q8_0(vxm_gguf *g, const char *prefix, int32_t layer, int64_t hidden, float *norms,
-                                   vxm_layer_weights_q8_0 *out) {
-    if (!g || !prefix || !out || !norms || layer < 0 || hidden <= 0) return VXM_ERR_INVALID_ARG;
+extern "C" int vxm_gguf_layer_q8_0(vxm_gguf *g, const char *prefix, int32_t layer, int64_t hidden, int64_t q_dim,
+                                   int64_t kv_dim, int64_t ffn, float *norms, vxm_layer_weights_q8_0 *out) {
+    if (!g || !prefix || !out || !norms || layer < 0 || hidden <= 0 || q_dim <= 0 || kv_dim <= 0 || ffn <= 0)
+        return VXM_ERR_INVALID_ARG;
+    // ne = [K, N] of q, k, v, o, gate, up, down: the sizes the upload reads
+    // (ggml_mul_mat refuses a weight whose K differs from the activation's)
+    const int64_t want[7][2] = {{hidden, q_dim}, {hidden, kv_dim}, {hidden, kv_dim}, {q_dim, hidden},
+                                {hidden, ffn},   {hidden, ffn},    {ffn, hidden}};
     static const char *const kSuffix[9] = {
         "self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
         "self_attn.o_proj.weight", "mlp.gate_proj.weight",    "mlp.up_proj.weight",
@@ -395,6 +400,10 @@ extern "C" int vxm_gguf_layer_q8_0(vxm_gguf *g, const char *prefix, int32_t laye
         if (s < 7) {
             if (t.type != VXM_GGML_Q8_0 || t.n_dims != 2)
                 return fail(g, nullptr, 0, VXM_ERR_NOT_IMPLEMENTED, "gguf: %s is not a 2-D Q8_0 tensor", name);
+            if (t.ne[0] != want[s][0] || t.ne[1] != want[s][1])
+                return fail(g, nullptr, 0, VXM_ERR_MODEL_FORMAT, "gguf: %s has ne = [%lld, %lld], expected [%lld, %lld]",
+                            name, (long long)t.ne[0], (long long)t.ne[1], (long long)want[s][0],
+                            (long long)want[s][1]);
             proj[s] = t.data;
         } else {
             if (t.n_elements != hidden)

@@ -17,6 +17,7 @@
 //   next layer's norm, or the final norm).
 #include <math.h>
 
+#include <atomic>
 #include <vector>
 
 #include "vxm_model.h"
@@ -270,8 +271,10 @@ extern "C" int vxm_kv_cache_create(vxm_ctx *ctx, int32_t n_layers, int32_t n_kv_
     *out = nullptr;
     if (n_layers <= 0 || n_kv_heads <= 0 || head_dim <= 0 || capacity <= 0)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "kv cache: sizes must be positive");
+    static std::atomic<uint64_t> next_id{1};
     vxm_kv_cache *kv = new vxm_kv_cache();
     kv->ctx = ctx;
+    kv->id = next_id.fetch_add(1);
     kv->n_layers = n_layers;
     kv->nkv = n_kv_heads;
     kv->hd = head_dim;

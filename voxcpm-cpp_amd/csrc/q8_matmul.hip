@@ -90,13 +90,15 @@ int vxm_launch_quantize(vxm_ctx *ctx, const float *x, int64_t M, int64_t K, int 
 // the exact int32 block sum in both lanes of the pair.  The activation chunk a
 // lane needs is the same for every row, so it stays in registers.
 // All weight loads of the wave are issued before any arithmetic.
+// DOTS = true writes the exact int32 block sums this kernel forms (after the
+// lane-pair exchange) to dots[(m*N + n)*(K/32) + b] instead of y.
 // ---------------------------------------------------------------------------
-template <int C, int R>
+template <int C, int R, bool DOTS>
 __global__ __launch_bounds__(256) void k_gemv_q8_0(const int8_t *__restrict__ qs,
                                                    const uint16_t *__restrict__ dg,
                                                    const int8_t *__restrict__ xq,
                                                    const uint16_t *__restrict__ xd, float *__restrict__ y,
-                                                   int N, int M) {
+                                                   int N, int M, int32_t *__restrict__ dots) {
     constexpr int K = C * 1024;
     constexpr int NB = K / 32;
     const int lane = threadIdx.x & 63;
@@ -131,6 +133,17 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0(const int8_t *__restrict__ qs
             xv[c] = *(const v4i *)(xrow + c * 1024);
             xs[c] = vxm_h2f(xdrow[c * 32 + pair]);
         }
+        if (DOTS) {
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int c = 0; c < C; c++) {
+                    int s = dot16v(wv[r][c], xv[c], 0);
+                    s += __shfl_xor(s, 1, 64);
+                    if ((lane & 1) == 0 && row0 + r < N) dots[((int64_t)m * N + row0 + r) * NB + c * 32 + pair] = s;
+                }
+            continue;
+        }
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -156,12 +169,15 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0(const int8_t *__restrict__ qs
 // ---------------------------------------------------------------------------
 // Generic GEMV, any K % 32 == 0: one wave per row, lanes stride over the
 // row's 16-byte half blocks (the two halves of a block sit in lanes 2p, 2p+1).
+// DOTS = true writes the int32 block sums instead (as k_gemv_q8_0).
 // ---------------------------------------------------------------------------
+template <bool DOTS>
 __global__ __launch_bounds__(256) void k_gemv_q8_0_generic(const int8_t *__restrict__ qs,
                                                            const uint16_t *__restrict__ d,
                                                            const int8_t *__restrict__ xq,
                                                            const uint16_t *__restrict__ xd,
-                                                           float *__restrict__ y, int N, int K, int M) {
+                                                           float *__restrict__ y, int N, int K, int M,
+                                                           int32_t *__restrict__ dots) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= N) return;
@@ -183,25 +199,16 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_generic(const int8_t *__restr
                 sc = vxm_h2f(drow[h >> 1]) * vxm_h2f(xdrow[h >> 1]);
             }
             s += __shfl_xor(s, 1, 64);
+            if (DOTS) {
+                if (h < nh && (h & 1) == 0) dots[((int64_t)m * N + row) * nb + (h >> 1)] = s;
+                continue;
+            }
             acc += (float)s * sc;
         }
+        if (DOTS) continue;
         acc = pair_sum(acc);
         if (lane == 0) y[(int64_t)m * N + row] = acc;
     }
-}
-
-// Debug: exact int32 per-block sums, one thread per (m, n, b).
-__global__ void k_block_dots(const int8_t *__restrict__ qs, const int8_t *__restrict__ xq, int64_t N,
-                             int64_t K, int64_t M, int32_t *__restrict__ out) {
-    const int64_t nb = K / 32;
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= M * N * nb) return;
-    const int64_t b = i % nb, n = (i / nb) % N, m = i / (nb * N);
-    const v4i *a = (const v4i *)(qs + n * K + b * 32);
-    const v4i *x = (const v4i *)(xq + m * K + b * 32);
-    int s = dot16v(a[0], x[0], 0);
-    s = dot16v(a[1], x[1], s);
-    out[i] = s;
 }
 
 
@@ -273,7 +280,7 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
     const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd, const int8_t *__restrict__ wq,
     const uint16_t *__restrict__ wd, float *__restrict__ y, uint64_t *__restrict__ part, int *__restrict__ cnt,
     int32_t *__restrict__ dots, int M, int N, int K, int tiles_m, int tiles_n, int bps, int splits,
-    uint32_t epoch) {
+    uint32_t epoch, int *__restrict__ err) {
     static_assert(KS % 8 == 0, "a stage is a multiple of 8 blocks (64 KS scales per side = whole 512-thread rounds)");
     constexpr int ROW = GemmLds<KS>::ROW;
     constexpr int CH = KS / 4;                 // 16-byte chunks per thread per side and stage
@@ -486,6 +493,7 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
             if (m >= M || nn >= N) continue;
             const int64_t i = (int64_t)m * N + nn;
             float s = 0.0f;
+            bool stale = false;
 #pragma unroll
             for (int zz = 0; zz < kGemmMaxSplits; zz++) {
                 if (zz >= splits) break;
@@ -494,8 +502,15 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
                     __builtin_amdgcn_s_sleep(1);
                     v = __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
+                stale |= (uint32_t)(v >> 32) != epoch;
                 const float p = __uint_as_float((uint32_t)v);
                 s = zz ? s + p : p;
+            }
+            // a partial that never arrived: a visible NaN and the context's error word
+            // (reported by vxm_sync), never a plausible-looking stale sum
+            if (stale) {
+                s = __builtin_nanf("");
+                __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             y[i] = s;
         }
@@ -528,6 +543,8 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
 // blocks [z*bps, (z+1)*bps) in stages of kSmallStage blocks; split z writes
 // its partial product to y + z*M*N (the consumer adds the slices in order).
 // Rows past M read as zeros (outside the buffer range) and are not written.
+// DOTS = true writes the int32 block sums of the MFMAs to dots[(m*N + n)*nb + b]
+// instead (every split its own blocks; no scaling, no epilogue).
 // ---------------------------------------------------------------------------
 constexpr int kSmallStage = 8;                        // K blocks per LDS stage
 constexpr int kSmallPitch = kSmallStage * 32 + 16;    // LDS bytes per activation row
@@ -540,14 +557,15 @@ __device__ __forceinline__ float half_at(const v4i &v, int j) {
 
 __device__ __forceinline__ long pack64(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
 
-template <int MT, int KG>
+template <int MT, int KG, bool DOTS>
 __global__ __launch_bounds__(64 * kSmallRG * KG) void k_gemm_q8_0_small(const int8_t *__restrict__ xq,
                                                                    const uint16_t *__restrict__ xd,
                                                                    const int8_t *__restrict__ wq,
                                                                    const uint16_t *__restrict__ wd,
                                                                    float *__restrict__ y, int M, int N, int K,
                                                                    int bps, int8_t *__restrict__ sq,
-                                                                   uint16_t *__restrict__ sd, int variant) {
+                                                                   uint16_t *__restrict__ sd, int variant,
+                                                                   int32_t *__restrict__ dots) {
     // KG groups of kSmallRG waves split the workgroup's K range in halves (KG = 2) and add
     // their partial products through LDS at the end; NT = threads per group
     constexpr int SB = kSmallStage, ROWS = 16 * MT, NT = 64 * kSmallRG;
@@ -647,6 +665,22 @@ __global__ __launch_bounds__(64 * kSmallRG * KG) void k_gemm_q8_0_small(const in
             for (int e = 0; e < 2; e++)
 #pragma unroll
                 for (int t = 0; t < MT; t++) c[e][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[e], bx[e][t], v4i{}, 0, 0, 0);
+            if (DOTS) {
+                // lane (q, r) holds the sums of weight rows nw + 4q + v with activation row 16t + r
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const int b = kb0 + 2 * p + e;
+#pragma unroll
+                    for (int t = 0; t < MT; t++) {
+                        const int m = 16 * t + r;
+                        if (b >= zb1 || m >= Mt) continue;
+#pragma unroll
+                        for (int v = 0; v < 4; v++)
+                            dots[((int64_t)(m0 + m) * N + nw + 4 * q + v) * nb + b] = c[e][t][v];
+                    }
+                }
+                continue;
+            }
 #pragma unroll
             for (int e = 0; e < 2; e++) {
                 const int b = 2 * p + e;
@@ -671,6 +705,7 @@ __global__ __launch_bounds__(64 * kSmallRG * KG) void k_gemm_q8_0_small(const in
         if (kb0 + 2 * SB < zb1) issue(sa, kb0 + 2 * SB);
         run(sb, kb0 + SB);
     }
+    if (DOTS) return;
     if (KG > 1) {
         // group 1 hands its partial products to group 0 (added as group 0 + group 1)
         __shared__ float kred[kSmallRG][MT * 4][64];
@@ -789,7 +824,16 @@ static void launch_gemm_ks(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, 
     const int grid_x = 8 * p.tiles_m * ((p.tiles_n + 7) / 8);
     hipLaunchKernelGGL((k_gemm_q8_0_mfma<KS, false>), dim3(grid_x, p.splits), dim3(kGemmThreads), 0, ctx->stream,
                        xq, xd, w->qs, w->d, y, part, cnt, nullptr, (int)M, (int)w->n, (int)w->k, p.tiles_m,
-                       p.tiles_n, p.bps, p.splits, epoch);
+                       p.tiles_n, p.bps, p.splits, epoch, ctx->dev_err);
+}
+
+template <int KS>
+static void launch_gemm_dots_ks(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                                int32_t *dots, const GemmPlan &p) {
+    const int grid_x = 8 * p.tiles_m * ((p.tiles_n + 7) / 8);
+    hipLaunchKernelGGL((k_gemm_q8_0_mfma<KS, true>), dim3(grid_x, p.splits), dim3(kGemmThreads), 0, ctx->stream,
+                       xq, xd, w->qs, w->d, nullptr, nullptr, nullptr, dots, (int)M, (int)w->n, (int)w->k,
+                       p.tiles_m, p.tiles_n, p.bps, p.splits, 0u, ctx->dev_err);
 }
 
 // Buffer-load offsets are 32-bit: every row tile of A and W must lie below 2 GiB.
@@ -816,6 +860,7 @@ static int launch_gemm(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, cons
         // tag of this launch's partial words; the buffer starts zeroed, so 0 is never used
         if (++ctx->split_epoch == 0) ctx->split_epoch = 1;
         epoch = ctx->split_epoch;
+        ctx->split_launched = true;
     }
     if (p.ks == 16) launch_gemm_ks<16>(ctx, w, xq, xd, M, y, p, part, cnt, epoch);
     else launch_gemm_ks<8>(ctx, w, xq, xd, M, y, p, part, cnt, epoch);
@@ -858,16 +903,21 @@ static bool small_plan(vxm_ctx *ctx, int64_t M, int64_t N, int64_t K, int max_pa
 
 static void launch_small(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                          float *y, const SmallPlan &p, int8_t *sq = nullptr, uint16_t *sd = nullptr,
-                         int variant = 0) {
+                         int variant = 0, int32_t *dots = nullptr) {
     const dim3 grid(p.groups, p.splits, p.mtiles), block(64 * kSmallRG * p.kg);
     const int N = (int)w->n, K = (int)w->k;
-#define VXM_SMALL_ARGS xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps, sq, sd, variant
-#define VXM_SMALL_MT(MT)                                                                                \
-    do {                                                                                                \
-        if (p.kg == 2)                                                                                  \
-            hipLaunchKernelGGL((k_gemm_q8_0_small<MT, 2>), grid, block, 0, ctx->stream, VXM_SMALL_ARGS); \
-        else                                                                                            \
-            hipLaunchKernelGGL((k_gemm_q8_0_small<MT, 1>), grid, block, 0, ctx->stream, VXM_SMALL_ARGS); \
+#define VXM_SMALL_ARGS xq, xd, w->qs, w->d, y, (int)M, N, K, p.bps, sq, sd, variant, dots
+#define VXM_SMALL_KG(MT, D)                                                                                \
+    do {                                                                                                   \
+        if (p.kg == 2)                                                                                     \
+            hipLaunchKernelGGL((k_gemm_q8_0_small<MT, 2, D>), grid, block, 0, ctx->stream, VXM_SMALL_ARGS); \
+        else                                                                                               \
+            hipLaunchKernelGGL((k_gemm_q8_0_small<MT, 1, D>), grid, block, 0, ctx->stream, VXM_SMALL_ARGS); \
+    } while (0)
+#define VXM_SMALL_MT(MT)                    \
+    do {                                    \
+        if (dots) VXM_SMALL_KG(MT, true);   \
+        else VXM_SMALL_KG(MT, false);       \
     } while (0)
     switch (p.mt) {
         case 1: VXM_SMALL_MT(1); break;
@@ -876,6 +926,7 @@ static void launch_small(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, co
         default: VXM_SMALL_MT(4); break;
     }
 #undef VXM_SMALL_MT
+#undef VXM_SMALL_KG
 #undef VXM_SMALL_ARGS
 }
 
@@ -933,57 +984,80 @@ bool vxm_launch_gate_up_swiglu(vxm_ctx *ctx, const vxm_weight *w, const int8_t *
     return true;
 }
 
-// int32 block sums through the MFMA (the GEMM's own products, unscaled).
-static int launch_gemm_dots(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
-                            int32_t *out) {
-    const int N = (int)w->n, K = (int)w->k, nb = K / 32;
-    if (!gemm_fits(M, N, K))
-        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "block_dots: %lld x %d x %d exceeds the GEMM's 2 GiB operand range",
-                        (long long)M, N, K);
-    const int tiles_m = (int)((M + GM - 1) / GM), tiles_n = (N + GN - 1) / GN;
-    const int grid_x = 8 * tiles_m * ((tiles_n + 7) / 8);
-    hipLaunchKernelGGL((k_gemm_q8_0_mfma<8, true>), dim3(grid_x, 1), dim3(kGemmThreads), 0, ctx->stream, xq, xd,
-                       w->qs, w->d, nullptr, nullptr, nullptr, out, (int)M, N, K, tiles_m, tiles_n, nb, 1, 0u);
-    VXM_CHECK_LAUNCH(ctx);
-    return VXM_OK;
-}
-
 template <int C, int R>
 static void launch_gemv_c(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd,
-                          int64_t M, float *y) {
+                          int64_t M, float *y, int32_t *dots) {
     const int waves = (int)((w->n + R - 1) / R);
     const int grid = (waves + 3) / 4;
-    hipLaunchKernelGGL((k_gemv_q8_0<C, R>), dim3(grid), dim3(256), 0, ctx->stream, w->qs, w->dg, xq, xd,
-                       y, (int)w->n, (int)M);
+    if (dots)
+        hipLaunchKernelGGL((k_gemv_q8_0<C, R, true>), dim3(grid), dim3(256), 0, ctx->stream, w->qs, w->dg, xq, xd,
+                           nullptr, (int)w->n, (int)M, dots);
+    else
+        hipLaunchKernelGGL((k_gemv_q8_0<C, R, false>), dim3(grid), dim3(256), 0, ctx->stream, w->qs, w->dg, xq, xd,
+                           y, (int)w->n, (int)M, nullptr);
 }
 
+// The GEMV family: the chunked kernel where K / 1024 has a build, else the
+// generic one.  dots != nullptr: the same kernel's int32 block sums instead of y.
+static void launch_gemv(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                        float *y, int32_t *dots) {
+    const int64_t K = w->k;
+    if (w->dg) {
+        switch (K / 1024) {
+            case 1: launch_gemv_c<1, 4>(ctx, w, xq, xd, M, y, dots); return;
+            case 2: launch_gemv_c<2, 2>(ctx, w, xq, xd, M, y, dots); return;
+            case 4: launch_gemv_c<4, 1>(ctx, w, xq, xd, M, y, dots); return;
+            case 6: launch_gemv_c<6, 1>(ctx, w, xq, xd, M, y, dots); return;
+            default: break;
+        }
+    }
+    const int grid = (int)((w->n + 3) / 4);
+    if (dots)
+        hipLaunchKernelGGL(k_gemv_q8_0_generic<true>, dim3(grid), dim3(256), 0, ctx->stream, w->qs, w->d, xq, xd,
+                           nullptr, (int)w->n, (int)K, (int)M, dots);
+    else
+        hipLaunchKernelGGL(k_gemv_q8_0_generic<false>, dim3(grid), dim3(256), 0, ctx->stream, w->qs, w->d, xq, xd,
+                           y, (int)w->n, (int)K, (int)M, nullptr);
+}
+
+static bool use_mfma(const vxm_ctx *ctx, int64_t M) {
+    return ctx->path == VXM_PATH_MFMA || ctx->path == VXM_PATH_MFMA_TILED ||
+           (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
+}
 
 int vxm_launch_mul_mat(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd,
                        int64_t M, float *y) {
     if (M <= 0) return VXM_OK;
-    const int64_t K = w->k;
-    const bool mfma = ctx->path == VXM_PATH_MFMA || ctx->path == VXM_PATH_MFMA_TILED ||
-                      (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
-    if (mfma) {
+    if (use_mfma(ctx, M)) {
         SmallPlan sp;
-        if (ctx->path != VXM_PATH_MFMA_TILED && small_plan(ctx, M, w->n, K, VXM_MAX_PARTS, sp))
+        if (ctx->path != VXM_PATH_MFMA_TILED && small_plan(ctx, M, w->n, w->k, VXM_MAX_PARTS, sp))
             return launch_gemm_small(ctx, w, xq, xd, M, y, sp);
         return launch_gemm(ctx, w, xq, xd, M, y);
     }
-    bool done = false;
-    if (w->dg) {
-        switch (K / 1024) {
-            case 1: launch_gemv_c<1, 4>(ctx, w, xq, xd, M, y); done = true; break;
-            case 2: launch_gemv_c<2, 2>(ctx, w, xq, xd, M, y); done = true; break;
-            case 4: launch_gemv_c<4, 1>(ctx, w, xq, xd, M, y); done = true; break;
-            case 6: launch_gemv_c<6, 1>(ctx, w, xq, xd, M, y); done = true; break;
-            default: break;
+    launch_gemv(ctx, w, xq, xd, M, y, nullptr);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}
+
+// int32 block sums from the kernel vxm_launch_mul_mat picks for this M and path,
+// with the same plan (stage depth, K splits): that kernel's own integer sums.
+static int launch_block_dots(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                             int32_t *out) {
+    if (use_mfma(ctx, M)) {
+        SmallPlan sp;
+        if (ctx->path != VXM_PATH_MFMA_TILED && small_plan(ctx, M, w->n, w->k, VXM_MAX_PARTS, sp)) {
+            launch_small(ctx, w, xq, xd, M, nullptr, sp, nullptr, nullptr, 0, out);
+        } else {
+            const int N = (int)w->n, K = (int)w->k;
+            if (!gemm_fits(M, N, K))
+                return vxm_fail(ctx, VXM_ERR_INVALID_ARG,
+                                "block_dots: %lld x %d x %d exceeds the GEMM's 2 GiB operand range", (long long)M, N, K);
+            const GemmPlan p = gemm_plan(ctx, M, N, K / 32);
+            if (p.ks == 16) launch_gemm_dots_ks<16>(ctx, w, xq, xd, M, out, p);
+            else launch_gemm_dots_ks<8>(ctx, w, xq, xd, M, out, p);
         }
-    }
-    if (!done) {
-        const int grid = (int)((w->n + 3) / 4);
-        hipLaunchKernelGGL(k_gemv_q8_0_generic, dim3(grid), dim3(256), 0, ctx->stream, w->qs, w->d, xq, xd,
-                           y, (int)w->n, (int)K, (int)M);
+    } else {
+        launch_gemv(ctx, w, xq, xd, M, nullptr, out);
     }
     VXM_CHECK_LAUNCH(ctx);
     return VXM_OK;
@@ -1040,13 +1114,5 @@ extern "C" int vxm_block_dots_q8_0(vxm_ctx *ctx, const vxm_weight *w, const int8
     if (rc) return rc;
     const int64_t total = M * w->n * (w->k / VXM_QK);
     if (total == 0) return VXM_OK;
-    // the MFMA GEMM's own block sums where the GEMM serves this M
-    const bool mfma = ctx->path == VXM_PATH_MFMA || ctx->path == VXM_PATH_MFMA_TILED ||
-                      (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
-    if (mfma) return launch_gemm_dots(ctx, w, xq_dev, xd_dev, M, out_dev);
-    const int64_t grid = (total + 255) / 256;
-    hipLaunchKernelGGL(k_block_dots, dim3((unsigned)grid), dim3(256), 0, ctx->stream, w->qs, xq_dev, w->n,
-                       w->k, M, out_dev);
-    VXM_CHECK_LAUNCH(ctx);
-    return VXM_OK;
+    return launch_block_dots(ctx, w, xq_dev, xd_dev, M, out_dev);
 }

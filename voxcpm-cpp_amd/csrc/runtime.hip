@@ -52,6 +52,16 @@ extern "C" int vxm_open(int device, vxm_ctx **out) {
         g_open_err = "hipStreamCreate failed";
         return VXM_ERR_BACKEND;
     }
+    if (hipMalloc((void **)&ctx->dev_err, 256) != hipSuccess ||
+        hipMemsetAsync(ctx->dev_err, 0, 256, ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        (void)hipGetLastError();
+        if (ctx->dev_err) (void)hipFree(ctx->dev_err);
+        hipStreamDestroy(ctx->stream);
+        delete ctx;
+        g_open_err = "device error word allocation failed";
+        return VXM_ERR_BACKEND;
+    }
     *out = ctx;
     return VXM_OK;
 }
@@ -64,6 +74,7 @@ extern "C" int vxm_close(vxm_ctx *ctx) {
     if (ctx->split_buf) hipFree(ctx->split_buf);
     if (ctx->split_cnt) hipFree(ctx->split_cnt);
     if (ctx->parts_buf) hipFree(ctx->parts_buf);
+    if (ctx->dev_err) hipFree(ctx->dev_err);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return VXM_OK;
@@ -72,6 +83,17 @@ extern "C" int vxm_close(vxm_ctx *ctx) {
 extern "C" int vxm_sync(vxm_ctx *ctx) {
     if (!ctx) return VXM_ERR_INVALID_ARG;
     VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->split_launched) {
+        // a K-split GEMM since the last check: did every fix-up find its partials?
+        ctx->split_launched = false;
+        int e = 0;
+        VXM_HIP(ctx, hipMemcpy(&e, ctx->dev_err, sizeof e, hipMemcpyDeviceToHost));
+        if (e) {
+            VXM_HIP(ctx, hipMemset(ctx->dev_err, 0, sizeof e));
+            return vxm_fail(ctx, VXM_ERR_BACKEND,
+                            "mul_mat: a K-split partial tile never arrived (its outputs were written as NaN)");
+        }
+    }
     return VXM_OK;
 }
 

@@ -29,6 +29,10 @@ struct vxm_ctx {
     int *split_cnt = nullptr;
     size_t split_ncnt = 0;
     uint32_t split_epoch = 0;   // tag of the last split launch's partial words
+    // device error word: set by a split fix-up whose partial words never
+    // arrived (its output is NaN); vxm_sync reports and clears it
+    int *dev_err = nullptr;
+    bool split_launched = false;   // a split launch since the last vxm_sync check
     // K-split slices of the small-M GEMM behind the public matmul entries
     void *parts_buf = nullptr;
     size_t parts_bytes = 0;

@@ -51,6 +51,9 @@ struct vxm_attn_site {
 
 struct vxm_kv_cache {
     vxm_ctx *ctx = nullptr;
+    // unique per created cache (never reused, unlike the struct's address):
+    // what a decode that caches device pointers of a cache keys them on
+    uint64_t id = 0;
     int n_layers = 0, nkv = 0, hd = 0, cap = 0;
     int32_t n_used = 0;
     int64_t layer_elems = 0;   // nkv * cap * hd

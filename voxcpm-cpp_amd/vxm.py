@@ -114,7 +114,7 @@ _SIGS = {
     "vxm_gguf_get_f32": (_F, [_P, C.c_char_p, _F]),
     "vxm_gguf_get_str": (C.c_char_p, [_P, C.c_char_p, C.c_char_p]),
     "vxm_gguf_tensor_f32": (_I, [_P, _I64, _P, _I64]),
-    "vxm_gguf_layer_q8_0": (_I, [_P, C.c_char_p, C.c_int32, _I64, _P, _P]),
+    "vxm_gguf_layer_q8_0": (_I, [_P, C.c_char_p, C.c_int32, _I64, _I64, _I64, _I64, _P, _P]),
     "vxm_gguf_minicpm4_config": (_I, [_P, C.c_int32, _P]),
 }
 
@@ -798,15 +798,20 @@ class GGUF:
         v = lib().vxm_gguf_get_str(self.h, key.encode(), None if default is None else default.encode())
         return None if v is None else v.decode()
 
-    def layer_q8_0(self, prefix, layer, hidden):
-        """LayerWeightsQ8 pointing into the mapping; the F32 norms live as long as this object."""
+    def layer_q8_0(self, prefix, layer, cfg):
+        """LayerWeightsQ8 pointing into the mapping; the F32 norms live as long as this object.
+        cfg: a MiniCPM4 config dict (hidden_size, n_heads, n_kv_heads, head_dim,
+        intermediate_size); every projection's shape is checked against it."""
         import numpy as np
 
+        hidden = cfg["hidden_size"]
         norms = np.empty(2 * hidden, dtype=np.float32)
         self._norms.append(norms)
         w = LayerWeightsQ8()
         self._check(lib().vxm_gguf_layer_q8_0(self.h, prefix.encode(), layer, hidden,
-                                              norms.ctypes.data_as(C.c_void_p), C.byref(w)))
+                                              cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"],
+                                              cfg["intermediate_size"], norms.ctypes.data_as(C.c_void_p),
+                                              C.byref(w)))
         return w
 
     def minicpm4_config(self, residual=False):
