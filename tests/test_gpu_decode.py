@@ -171,3 +171,45 @@ def test_persistent_unsupported_shape_falls_back(vxm_ctx, orc):
         m.free()
     for kv in kvs.values():
         kv.free()
+
+
+def test_persistent_decode_after_cache_free_and_recreate(vxm_ctx, orc):
+    """One model decodes on cache A (capacity 256), A is freed, and a new cache B
+    of capacity 1024 is created (the allocator may hand B the struct address A
+    had): the decode on B must read and append B's rows, not A's."""
+    import vxm
+
+    s = SHAPES["tslm"]
+    L, ctx0 = 2, 100
+    rng = np.random.default_rng(2024)
+    lws = [rand_layer(orc, rng, s["H"], s["nh"], s["nkv"], s["hd"], s["F"]) for _ in range(L)]
+    fn = (1 + rng.normal(0, 0.02, s["H"])).astype(np.float32)
+    c = cfg_dict(s["H"], L, s["nh"], s["nkv"], s["hd"], s["F"])
+    m = vxm.MiniCPM4(vxm_ctx, c, lws, final_norm=fn)
+    m.set_decode_mode(2)
+    oc, ol = orc_cfg(orc, c), [to_orc(orc, l) for l in lws]
+    try:
+        for cap in (256, 1024, 256):
+            kv = vxm.KVCache(vxm_ctx, L, s["nkv"], s["hd"], cap)
+            kcs, vcs = [], []
+            for l in range(L):
+                k = np.zeros((s["nkv"], cap, s["hd"]), np.uint16)
+                v = np.zeros_like(k)
+                k[:, :ctx0] = orc.fp32_to_fp16_bits(orc.bf16_round(rng.normal(0, 1, (s["nkv"], ctx0, s["hd"])).astype(np.float32)))
+                v[:, :ctx0] = orc.fp32_to_fp16_bits(orc.bf16_round(rng.normal(0, 1, (s["nkv"], ctx0, s["hd"])).astype(np.float32)))
+                kv.upload(l, k, v)
+                kcs.append(k.reshape(-1).copy())
+                vcs.append(v.reshape(-1).copy())
+            x = rng.normal(0, 1, (1, s["H"])).astype(np.float32)
+            xd = _dev(x)
+            m.forward(kv, xd, ctx0)
+            vxm_ctx.sync()
+            m.check()
+            ref = orc.minicpm4_forward(oc, ol, fn, x, kcs, vcs, cap, ctx0)
+            assert_stack_close(xd.cpu().numpy(), ref, what=f"cache of capacity {cap}")
+            k0, v0 = kv.download(0)
+            # layer 0 sees identical inputs: its appended row is exact, and nothing else moved
+            assert np.array_equal(k0, kcs[0].reshape(k0.shape)) and np.array_equal(v0, vcs[0].reshape(v0.shape))
+            kv.free()
+    finally:
+        m.free()

@@ -5,30 +5,57 @@ Q8_0 weights ~ N(0, 0.02)) at full depth (28 layers):
   * the 28-layer decode of consecutive tokens from context 256 on the
     single-launch (persistent) kernel and on the one-kernel-per-op path
     (vcpm_minicpm4_forward with n_tokens = 1, src/minicpm4.c:536-572), with
-    the appended KV rows of the first, a middle and the last layer;
+    the appended KV rows of the first, a middle and the last layer; and every
+    one of the 28 layers on its own, fed the device's own input (teacher
+    forcing: each layer's arithmetic alone, no compounding);
   * the 512-token prompt prefill (the M = n_tokens GEMMs of
-    gen_prompt_eval_range, src/gen_prompt.c:186-272): per layer, each device
-    block fed the oracle its own input; the whole 28-layer stack against the
-    oracle's; and 512 tokens in one call against two chunks of 256.
+    gen_prompt_eval_range, src/gen_prompt.c:186-272): all 28 layers teacher
+    forced with the 512 K / V rows each writes, the whole 28-layer stack in one
+    call, and 512 tokens in one call against two chunks of 256.
 
-Bars.  A single block fed identical inputs is held to the prefill block bar
-(>= 99% of elements within 1e-3 rel / 1e-4 abs, every element within 4 BF16
-ulps, relative L2 <= 1e-3; the MFMA attention sums up to 512 scores and P.V
-products in its own order).  A multi-layer stack compounds BF16 rounding
-flips (one flipped activation changes every later Q8_0 block it enters), so
-stacks are held to the decode-stack bar: cosine >= 0.9995 and relative L2
-<= 2e-2, beside the oracle's own sensitivity to a one-ulp input change,
-which is printed for scale.
+Bars (the numbers are pinned on the CPU by test_oracle_sensitivity.py).  The
+device and the oracle differ only in fp32 summation order; where that moves a
+value across a BF16 rounding boundary, the flip re-quantizes a Q8_0 block and
+spreads.  The oracle itself shows the size of one flip: one BF16 ulp on one
+input element moves a full-width block's output by a relative L2 of 4e-3
+(512-token prefill; causal attention carries it to every later token) or
+5.6e-3 (decode), and the 28-layer decode output by 5.7e-2 (cosine 0.998).
+Hence:
+  * one layer, teacher forced: relative L2 <= 1e-2 and every element within
+    2^-5 of its row's largest magnitude;
+  * 28 layers: cosine >= 0.995 and relative L2 <= 0.1, with the oracle's own
+    one-ulp sensitivity printed beside the device's deviation;
+  * K / V rows written from identical inputs: >= 99% identical, relative L2
+    <= 1e-3.
 """
 import numpy as np
 import pytest
 
-from test_gpu_decode import assert_stack_close
-from test_gpu_minicpm4 import _dev, assert_layer_close, cfg_dict, orc_cfg, to_orc
+from test_gpu_minicpm4 import _dev, cfg_dict, layer_stats, orc_cfg, to_orc
 
 pytestmark = pytest.mark.gpu
 
 H, NH, NKV, HD, F, L = 2048, 16, 2, 128, 6144, 28
+LAYER_REL, LAYER_ROW = 1e-2, 2.0 ** -5      # one layer fed identical inputs
+STACK_COS, STACK_REL = 0.995, 0.1           # 28 layers
+KV_EQ, KV_REL = 0.99, 1e-3                  # K / V rows from identical inputs
+
+
+def assert_one_layer(y, ref, what):
+    y64, r64 = np.asarray(y, np.float64), np.asarray(ref, np.float64)
+    rel = float(np.linalg.norm(y64 - r64) / np.linalg.norm(r64))
+    row = float((np.abs(y64 - r64) / np.abs(r64).max(axis=-1, keepdims=True)).max())
+    print(f"{what}: rel-L2 {rel:.3g}, worst element / row max {row:.3g}, {layer_stats(y, ref)}")
+    assert rel <= LAYER_REL and row <= LAYER_ROW, (what, rel, row)
+    return rel
+
+
+def assert_stack(y, ref, what):
+    a, b = np.ravel(y).astype(np.float64), np.ravel(ref).astype(np.float64)
+    cos = float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+    rel = float(np.linalg.norm(a - b) / np.linalg.norm(b))
+    print(f"{what}: cos {cos:.6f}, rel-L2 {rel:.3g}")
+    assert cos >= STACK_COS and rel <= STACK_REL, (what, cos, rel)
 
 
 def make_layers(vxm, seed, n_layers):
@@ -69,24 +96,21 @@ def _prior_cache(orc, rng, cap, ctx0):
     return k, v
 
 
-def _kv_rows_close(orc, got_bits, want_bits, rows, what, bar=2e-2):
+def _kv_rel(orc, got_bits, want_bits, rows, what):
     g = orc.fp16_bits_to_fp32(got_bits)[:, rows].astype(np.float64)
     w = orc.fp16_bits_to_fp32(want_bits)[:, rows].astype(np.float64)
-    rel = np.linalg.norm(g - w) / np.linalg.norm(w)
+    rel = float(np.linalg.norm(g - w) / np.linalg.norm(w))
     eq = float((got_bits[:, rows] == want_bits[:, rows]).mean())
     print(f"{what}: rel-L2 {rel:.3g}, identical {eq:.4f}")
-    assert rel <= bar, (what, rel)
-    return eq
+    return rel, eq
 
 
 def _oracle_sensitivity(orc, oc, ol, fn, x, kcs, vcs, cap, pos, ref):
     """How far the oracle's own output moves when one input element moves by one
-    BF16 ulp (printed for scale beside the device's deviation)."""
+    BF16 ulp (printed beside the device's deviation)."""
     xp = x.copy()
     xp.flat[7] = np.float32(xp.flat[7] * (1 + 2.0 ** -7))
-    kc = [k.copy() for k in kcs]
-    vc = [v.copy() for v in vcs]
-    alt = orc.minicpm4_forward(oc, ol, fn, xp, kc, vc, cap, pos)
+    alt = orc.minicpm4_forward(oc, ol, fn, xp, [k.copy() for k in kcs], [v.copy() for v in vcs], cap, pos)
     return float(np.linalg.norm(alt - ref) / np.linalg.norm(ref))
 
 
@@ -124,15 +148,13 @@ def test_decode_28_layers_4_tokens_from_ctx256(vxm_ctx, orc, stack28):
                 vxm_ctx.sync()
                 outs[mode] = xd.cpu().numpy()
             models[2].check()
-            if t == 0:
-                kc0 = [k.copy() for k in kcs]
-                vc0 = [v.copy() for v in vcs]
+            kc0, vc0 = [k.copy() for k in kcs], [v.copy() for v in vcs]
             ref = orc.minicpm4_forward(oc, ol, fn, x, kcs, vcs, cap, ctx0 + t)
             if t == 0:
                 sens = _oracle_sensitivity(orc, oc, ol, fn, x, kc0, vc0, cap, ctx0, ref)
-                print(f"oracle: one BF16 ulp on one input element moves the 28-layer output by rel-L2 {sens:.3g}")
-            assert_stack_close(outs[2], ref, what=f"persistent 28 layers t={t}")
-            assert_stack_close(outs[1], ref, what=f"per-op 28 layers t={t}")
+                print(f"oracle: one BF16 ulp on one input element moves its 28-layer output by rel-L2 {sens:.3g}")
+            assert_stack(outs[2], ref, f"persistent 28 layers t={t}")
+            assert_stack(outs[1], ref, f"per-op 28 layers t={t}")
             assert kvs[2].used == ctx0 + t + 1
         rows = slice(ctx0, ctx0 + steps)
         for l in (0, 13, 27):
@@ -143,8 +165,9 @@ def test_decode_28_layers_4_tokens_from_ctx256(vxm_ctx, orc, stack28):
                 if l == 0:
                     # layer 0 of the first token sees identical inputs
                     assert np.array_equal(k2[:, ctx0], kr[:, ctx0]) and np.array_equal(v2[:, ctx0], vr[:, ctx0])
-                _kv_rows_close(orc, k2, kr, rows, f"mode {mode} layer {l} K rows")
-                _kv_rows_close(orc, v2, vr, rows, f"mode {mode} layer {l} V rows")
+                for got, want, nm in ((k2, kr, "K"), (v2, vr, "V")):
+                    rel, _ = _kv_rel(orc, got, want, rows, f"mode {mode} layer {l} {nm} rows")
+                    assert rel <= STACK_REL, (mode, l, nm, rel)
                 # rows outside the appended span are untouched
                 assert np.array_equal(k2[:, :ctx0], kr[:, :ctx0]) and not k2[:, ctx0 + steps:].any()
     finally:
@@ -154,38 +177,86 @@ def test_decode_28_layers_4_tokens_from_ctx256(vxm_ctx, orc, stack28):
             kv.free()
 
 
-def test_prefill_512_full_width_per_layer(vxm_ctx, orc, stack28):
-    """512-token causal prefill at full width, layer by layer for the first three
-    layers: each device block against the oracle's block fed the same input, and
-    the 512 K / V rows it writes."""
+def test_decode_every_layer_teacher_forced(vxm_ctx, orc, stack28):
+    """Each of the 28 layers alone at the decode shape (context 256), on the
+    single-launch kernel and on the per-op path: layer l is fed the persistent
+    path's output of layer l - 1, and the oracle's block the same input and the
+    same prior cache; the appended K / V row is compared as well."""
     import vxm
 
-    layers, fn = stack28
-    M, cap, n = 512, 512, 3
-    rng = np.random.default_rng(512)
-    c = cfg_dict(H, n, NH, NKV, HD, F)
+    layers, _ = stack28
+    cap, ctx0 = 512, 256
+    rng = np.random.default_rng(404)
+    c = cfg_dict(H, 1, NH, NKV, HD, F)
     oc = orc_cfg(orc, c)
-    m = vxm.MiniCPM4(vxm_ctx, c, layers[:n])
-    kv = vxm.KVCache(vxm_ctx, n, NKV, HD, cap)
+    x = rng.normal(0, 1, (1, H)).astype(np.float32)
+    worst, exact = 0.0, 0
+    for l in range(L):
+        k, v = _prior_cache(orc, rng, cap, ctx0)
+        outs, kvrows = {}, {}
+        for mode in (2, 1):
+            m = vxm.MiniCPM4(vxm_ctx, c, [layers[l]])
+            m.set_decode_mode(mode)
+            kv = vxm.KVCache(vxm_ctx, 1, NKV, HD, cap)
+            try:
+                kv.upload(0, k, v)
+                xd = _dev(x)
+                m.forward(kv, xd, ctx0)
+                vxm_ctx.sync()
+                m.check()
+                outs[mode] = xd.cpu().numpy()
+                kvrows[mode] = kv.download(0)
+            finally:
+                m.free()
+                kv.free()
+        kc, vc = k.reshape(-1).copy(), v.reshape(-1).copy()
+        ref = orc.minicpm4_block(oc, to_orc(orc, layers[l]), x, kc, vc, cap, ctx0, 0)
+        for mode in (2, 1):
+            rel = assert_one_layer(outs[mode], ref, f"layer {l} mode {mode}")
+            worst = max(worst, rel)
+            exact += rel == 0.0
+            # the appended row comes from identical inputs: only the projection's fp32 order differs
+            for got, want, nm in ((kvrows[mode][0], kc, "K"), (kvrows[mode][1], vc, "V")):
+                rel_kv, eq = _kv_rel(orc, got, want.reshape(NKV, cap, HD), slice(ctx0, ctx0 + 1),
+                                     f"layer {l} mode {mode} {nm} row")
+                assert rel_kv <= KV_REL and eq >= KV_EQ - 0.02, (l, mode, nm, rel_kv, eq)
+                assert np.array_equal(got[:, :ctx0], want.reshape(NKV, cap, HD)[:, :ctx0])
+        x = outs[2]
+    print(f"28 layers x 2 paths: worst rel-L2 {worst:.3g}, {exact} of 56 bit-identical")
+
+
+def test_prefill_512_every_layer_teacher_forced(vxm_ctx, orc, stack28):
+    """The 512-token causal prefill at full width, each of the 28 layers fed the
+    device's output of the previous layer: every device block against the
+    oracle's block on the same input, and the 512 K / V rows it writes."""
+    import vxm
+
+    layers, _ = stack28
+    M, cap = 512, 512
+    rng = np.random.default_rng(512)
+    c = cfg_dict(H, L, NH, NKV, HD, F)
+    oc = orc_cfg(orc, c)
+    m = vxm.MiniCPM4(vxm_ctx, c, layers)
+    kv = vxm.KVCache(vxm_ctx, L, NKV, HD, cap)
+    worst = 0.0
     try:
-        x = rng.normal(0, 1, (M, H)).astype(np.float32)
-        xd = _dev(x)
-        for l in range(n):
+        xd = _dev(rng.normal(0, 1, (M, H)).astype(np.float32))
+        for l in range(L):
             x_in = xd.cpu().numpy()
             m.block(kv, l, xd, 0)
             vxm_ctx.sync()
             kc = np.zeros(NKV * cap * HD, np.uint16)
             vc = np.zeros_like(kc)
             ref = orc.minicpm4_block(oc, to_orc(orc, layers[l]), x_in, kc, vc, cap, 0, 0)
-            assert_layer_close(xd.cpu().numpy(), ref, frac=0.99, what=f"prefill 512 layer {l}")
+            worst = max(worst, assert_one_layer(xd.cpu().numpy(), ref, f"prefill 512 layer {l}"))
             k2, v2 = kv.download(l)
             for got, want, nm in ((k2, kc, "K"), (v2, vc, "V")):
-                eq = _kv_rows_close(orc, got, want.reshape(NKV, cap, HD), slice(0, M), f"layer {l} {nm} rows",
-                                    bar=1e-3)
-                assert eq >= 0.99, (l, nm, eq)
+                rel, eq = _kv_rel(orc, got, want.reshape(NKV, cap, HD), slice(0, M), f"layer {l} {nm} rows")
+                assert rel <= KV_REL and eq >= KV_EQ, (l, nm, rel, eq)
     finally:
         m.free()
         kv.free()
+    print(f"28 prefill layers: worst rel-L2 {worst:.3g}")
 
 
 def test_prefill_512_28_layers_matches_oracle(vxm_ctx, orc, stack28):
@@ -209,11 +280,14 @@ def test_prefill_512_28_layers_matches_oracle(vxm_ctx, orc, stack28):
         kcs = [np.zeros(NKV * cap * HD, np.uint16) for _ in range(L)]
         vcs = [np.zeros(NKV * cap * HD, np.uint16) for _ in range(L)]
         ref = orc.minicpm4_forward(oc, [to_orc(orc, d) for d in layers], fn, x, kcs, vcs, cap, 0)
-        assert_stack_close(xd.cpu().numpy(), ref, what="prefill 512 x 28 layers")
+        assert_stack(xd.cpu().numpy(), ref, "prefill 512 x 28 layers")
         for l in (0, 13, 27):
             k2, v2 = kv.download(l)
-            _kv_rows_close(orc, k2, kcs[l].reshape(NKV, cap, HD), slice(0, M), f"prefill layer {l} K rows")
-            _kv_rows_close(orc, v2, vcs[l].reshape(NKV, cap, HD), slice(0, M), f"prefill layer {l} V rows")
+            for got, want, nm in ((k2, kcs[l], "K"), (v2, vcs[l], "V")):
+                rel, eq = _kv_rel(orc, got, want.reshape(NKV, cap, HD), slice(0, M), f"prefill layer {l} {nm} rows")
+                assert rel <= (KV_REL if l == 0 else STACK_REL), (l, nm, rel)
+                if l == 0:
+                    assert eq >= KV_EQ, (nm, eq)
     finally:
         m.free()
         kv.free()
@@ -222,7 +296,8 @@ def test_prefill_512_28_layers_matches_oracle(vxm_ctx, orc, stack28):
 def test_prefill_512_equals_two_chunks_of_256(vxm_ctx, orc, stack28):
     """Prompt prefill in one 512-token call against 256 tokens then 256 more at
     position 256 (gen_prompt_eval_range over segments), 28 layers: outputs and
-    the KV rows of layers 0, 13 and 27 agree to the stack bar."""
+    the KV rows of layers 0, 13 and 27 agree to the 28-layer bar; the first
+    chunk's layer-0 K / V rows to the identical-input bar."""
     import vxm
 
     layers, fn = stack28
@@ -241,14 +316,17 @@ def test_prefill_512_equals_two_chunks_of_256(vxm_ctx, orc, stack28):
         m.forward(kvb, xb1, 256)
         vxm_ctx.sync()
         assert kva.used == M and kvb.used == M
-        ya = xa.cpu().numpy()
         yb = np.concatenate([xb0.cpu().numpy(), xb1.cpu().numpy()])
-        assert_stack_close(yb, ya, what="prefill 256 + 256 vs 512")
+        assert_stack(yb, xa.cpu().numpy(), "prefill 256 + 256 vs 512")
         for l in (0, 13, 27):
             ka, va = kva.download(l)
             kb, vb = kvb.download(l)
-            _kv_rows_close(orc, kb, ka, slice(0, M), f"chunked layer {l} K rows")
-            _kv_rows_close(orc, vb, va, slice(0, M), f"chunked layer {l} V rows")
+            for got, want, nm in ((kb, ka, "K"), (vb, va, "V")):
+                rel, eq = _kv_rel(orc, got, want, slice(0, M), f"chunked layer {l} {nm} rows")
+                assert rel <= STACK_REL, (l, nm, rel)
+                if l == 0:
+                    rel0, eq0 = _kv_rel(orc, got, want, slice(0, 256), f"chunked layer 0 {nm} rows of chunk 1")
+                    assert rel0 <= KV_REL and eq0 >= KV_EQ, (nm, rel0, eq0)
     finally:
         m.free()
         kva.free()
