@@ -395,6 +395,31 @@ def bench_lm_update(ctx, torch, vxm, tslm_layers, ctx0, steps, warmup):
     return ms * 1000.0 / steps, ok
 
 
+def host_cores():
+    """CPUs this process may run on: the affinity mask, the cgroup v2 CPU quota (cpu.max) and
+    OMP_NUM_THREADS, each as found; `usable` is the smallest of them."""
+    info = {"os_cpu_count": os.cpu_count()}
+    try:
+        info["affinity"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        info["affinity"] = os.cpu_count()
+    quota = None
+    try:
+        q, per = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        info["cgroup_cpu_max"] = f"{q} {per}"
+        if q != "max":
+            quota = int(q) / int(per)
+    except (OSError, ValueError):
+        info["cgroup_cpu_max"] = None
+    info["cgroup_cpus"] = round(quota, 2) if quota else None
+    omp = os.environ.get("OMP_NUM_THREADS")
+    info["omp_num_threads"] = int(omp) if omp and omp.isdigit() else None
+    cands = [c for c in (info["affinity"], int(quota) if quota and quota >= 1 else None, info["omp_num_threads"])
+             if c]
+    info["usable"] = max(1, min(cands)) if cands else 1
+    return info
+
+
 def cpu_baseline(vxm, layers, n_layers, ctx0, tokens, threads):
     """The oracle's SIMD restatement of ggml's CPU Q8_0 decode (1 copy of weights)."""
     import ctypes as C
@@ -571,7 +596,8 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        cores = host_cores()
+        threads = cores["usable"]
         t0 = time.time()
         c1, isa = cpu_baseline(vxm, layers, L, 256, args.cpu_tokens_1t, 1)
         cn, _ = cpu_baseline(vxm, layers, L, 256, args.cpu_tokens, threads)
@@ -581,7 +607,9 @@ def main():
                "sample": f"{args.cpu_tokens} decode tokens on {threads} threads and {args.cpu_tokens_1t} on 1 thread "
                          f"of the 28-layer stack at context 256 (SIMD {isa} restatement of ggml-cpu's Q8_0 "
                          f"mul_mat path, one copy of the weights)",
+               "host": cores,
                "us_per_step": round(cn, 1), "us_per_step_1thread": round(c1, 1),
+               "thread_scaling": round(c1 / cn, 2),
                "speedup_vs_cpu_all_cores": round(cn / us_step, 1),
                "speedup_vs_cpu_1thread": round(c1 / us_step, 1)}
 
@@ -607,9 +635,10 @@ def main():
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic",
-        "config": {"workload": "28-layer MiniCPM4 decode, batch 1, hidden 2048, 16/2 heads x 128, FFN 6144, "
-                               "Q8_0 N(0,0.02) seed 1, f16 KV ctx 256->320, 3 rotated weight copies",
-                   "decode_mode": args.mode},
+        "config": {"workload": f"28-layer MiniCPM4 decode, batch 1, hidden 2048, 16/2 heads x 128, FFN 6144, "
+                               f"Q8_0 N(0,0.02) seed 1, f16 KV ctx 256->{256 + args.steps} ({args.steps} tokens "
+                               f"timed), {args.copies} rotated weight copies",
+                   "decode_mode": args.mode, "context_start": 256, "context_end": 256 + args.steps},
         "us_per_step": round(us_step, 2),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "step_bytes": int(sb),
