@@ -98,6 +98,19 @@ int vxm_mul_mat_q8_0(vxm_ctx *ctx, const vxm_weight *w, const float *x_dev, int6
 /* y = W . x for an already quantized activation. */
 int vxm_mul_mat_q8_0_q8_0(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq_dev,
                           const uint16_t *xd_dev, int64_t M, float *y_dev);
+/* vxm_mul_mat_q8_0 without any allocation: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * kernels, plans and results as vxm_mul_mat_q8_0; the quantized activation
+ * and the K-split partials live in a fixed device array of
+ * vxm_noalloc_scratch_bytes() per device (48 MiB 64 KiB), held until the
+ * process ends.  A product whose quantized activation exceeds 32 MiB, or whose
+ * K splits exceed their part of the array, is rejected with
+ * VXM_ERR_INVALID_ARG.  All calls on one device share the array: calls that
+ * overlap on a device (other streams or threads) race. */
+int vxm_mul_mat_q8_0_noalloc(vxm_ctx *ctx, const vxm_weight *w, const float *x_dev, int64_t M,
+                             float *y_dev);
+size_t vxm_noalloc_scratch_bytes(void);
 /* Debug: int32 per-block sums of vec_dot_q8_0_q8_0, out[(m*N + n)*(K/32) + b]. */
 int vxm_block_dots_q8_0(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq_dev,
                         const uint16_t *xd_dev, int64_t M, int32_t *out_dev);

@@ -7,6 +7,9 @@
 //   sumi = sum over the 32 int8 pairs of block b (exact int32).
 // Every kernel here forms exactly these per-block fp32 terms; only the order
 // of the fp32 additions over b differs from ggml's (a tree over lanes).
+#include <atomic>
+#include <mutex>
+
 #include "vxm_internal.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -842,8 +845,25 @@ static bool gemm_fits(int64_t M, int64_t N, int64_t K) {
     return (M + GM) * K < lim && (N + GN) * K < lim;
 }
 
+// Buffers of the public matmul entries' K splits when the caller brings them
+// (the allocation-free entry); null: the context's own scratch.
+struct MmWork {
+    uint64_t *words;     // tagged partial words of the tiled GEMM's splits
+    size_t words_bytes;
+    int *cnt;            // its per-tile arrival counters, zero on entry
+    size_t ncnt;
+    float *parts;        // the small-M GEMM's K-split slices
+    size_t parts_bytes;
+    std::atomic<uint32_t> *epoch;   // source of tags no earlier launch on these words used
+};
+
+__global__ void k_fill_zero(uint4 *__restrict__ p, int64_t n16) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = make_uint4(0, 0, 0, 0);
+}
+
 static int launch_gemm(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
-                       float *y) {
+                       float *y, const MmWork *wk = nullptr) {
     const int N = (int)w->n, K = (int)w->k, nb = K / 32;
     if (!gemm_fits(M, N, K))
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "mul_mat: %lld x %d x %d exceeds the GEMM's 2 GiB operand range",
@@ -853,13 +873,30 @@ static int launch_gemm(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, cons
     int *cnt = nullptr;
     uint32_t epoch = 0;
     if (p.splits > 1) {
-        int rc = vxm_ensure_split(ctx, (size_t)p.splits * M * N * sizeof(uint64_t), (size_t)p.tiles_m * p.tiles_n);
-        if (rc) return rc;
-        part = (uint64_t *)ctx->split_buf;
-        cnt = ctx->split_cnt;
-        // tag of this launch's partial words; the buffer starts zeroed, so 0 is never used
-        if (++ctx->split_epoch == 0) ctx->split_epoch = 1;
-        epoch = ctx->split_epoch;
+        const size_t wbytes = (size_t)p.splits * M * N * sizeof(uint64_t), ncnt = (size_t)p.tiles_m * p.tiles_n;
+        if (wk) {
+            if (wbytes > wk->words_bytes || ncnt > wk->ncnt)
+                return vxm_fail(ctx, VXM_ERR_INVALID_ARG,
+                                "mul_mat: %lld x %d x %d needs %zu B of split partials and %zu counters; the "
+                                "workspace holds %zu B and %zu",
+                                (long long)M, N, K, wbytes, ncnt, wk->words_bytes, wk->ncnt);
+            part = wk->words;
+            cnt = wk->cnt;
+            do epoch = ++*wk->epoch;
+            while (epoch == 0);   // the words start zeroed: tag 0 is never live
+            // the counters start this launch at zero whatever an earlier call left
+            const int64_t n16 = (int64_t)((ncnt * sizeof(int) + 15) / 16);
+            hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, ctx->stream,
+                               (uint4 *)cnt, n16);
+        } else {
+            int rc = vxm_ensure_split(ctx, wbytes, ncnt);
+            if (rc) return rc;
+            part = (uint64_t *)ctx->split_buf;
+            cnt = ctx->split_cnt;
+            // tag of this launch's partial words; the buffer starts zeroed, so 0 is never used
+            if (++ctx->split_epoch == 0) ctx->split_epoch = 1;
+            epoch = ctx->split_epoch;
+        }
         ctx->split_launched = true;
     }
     if (p.ks == 16) launch_gemm_ks<16>(ctx, w, xq, xd, M, y, p, part, cnt, epoch);
@@ -933,16 +970,26 @@ static void launch_small(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, co
 // Public entry: a split product goes through the context's scratch and one
 // fix-up launch that adds the slices in order.
 static int launch_gemm_small(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
-                             float *y, const SmallPlan &p) {
+                             float *y, const SmallPlan &p, const MmWork *wk = nullptr) {
     if (p.splits == 1) {
         launch_small(ctx, w, xq, xd, M, y, p);
         VXM_CHECK_LAUNCH(ctx);
         return VXM_OK;
     }
     const int64_t count = M * w->n;
-    int rc = vxm_ensure_parts(ctx, (size_t)p.splits * count * sizeof(float));
-    if (rc) return rc;
-    float *scratch = (float *)ctx->parts_buf;
+    const size_t pbytes = (size_t)p.splits * count * sizeof(float);
+    float *scratch;
+    if (wk) {
+        if (pbytes > wk->parts_bytes)
+            return vxm_fail(ctx, VXM_ERR_INVALID_ARG,
+                            "mul_mat: %lld x %lld x %lld needs %zu B of K-split slices; the workspace holds %zu B",
+                            (long long)M, (long long)w->n, (long long)w->k, pbytes, wk->parts_bytes);
+        scratch = wk->parts;
+    } else {
+        int rc = vxm_ensure_parts(ctx, pbytes);
+        if (rc) return rc;
+        scratch = (float *)ctx->parts_buf;
+    }
     launch_small(ctx, w, xq, xd, M, scratch, p);
     VXM_CHECK_LAUNCH(ctx);
     const int64_t threads = count / 4;   // N % 64 == 0
@@ -1025,18 +1072,23 @@ static bool use_mfma(const vxm_ctx *ctx, int64_t M) {
            (ctx->path == VXM_PATH_AUTO && M >= kMfmaMinRows);
 }
 
-int vxm_launch_mul_mat(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd,
-                       int64_t M, float *y) {
+static int launch_mul_mat(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                          float *y, const MmWork *wk) {
     if (M <= 0) return VXM_OK;
     if (use_mfma(ctx, M)) {
         SmallPlan sp;
         if (ctx->path != VXM_PATH_MFMA_TILED && small_plan(ctx, M, w->n, w->k, VXM_MAX_PARTS, sp))
-            return launch_gemm_small(ctx, w, xq, xd, M, y, sp);
-        return launch_gemm(ctx, w, xq, xd, M, y);
+            return launch_gemm_small(ctx, w, xq, xd, M, y, sp, wk);
+        return launch_gemm(ctx, w, xq, xd, M, y, wk);
     }
     launch_gemv(ctx, w, xq, xd, M, y, nullptr);
     VXM_CHECK_LAUNCH(ctx);
     return VXM_OK;
+}
+
+int vxm_launch_mul_mat(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd,
+                       int64_t M, float *y) {
+    return launch_mul_mat(ctx, w, xq, xd, M, y, nullptr);
 }
 
 // int32 block sums from the kernel vxm_launch_mul_mat picks for this M and path,
@@ -1115,4 +1167,82 @@ extern "C" int vxm_block_dots_q8_0(vxm_ctx *ctx, const vxm_weight *w, const int8
     const int64_t total = M * w->n * (w->k / VXM_QK);
     if (total == 0) return VXM_OK;
     return launch_block_dots(ctx, w, xq_dev, xd_dev, M, out_dev);
+}
+
+// ---- the allocation-free matmul ---------------------------------------------
+// vxm_mul_mat_q8_0_noalloc runs the kernels of vxm_mul_mat_q8_0, with the same
+// plans, but takes every buffer beyond x and y from `scratch`, a file-scope
+// device array that the code object carries: no call allocates.  Layout:
+//   [0, kScrCnt)                 per-tile arrival counters of the tiled GEMM's
+//                                K splits (zeroed by each call that splits)
+//   [kScrCnt, +kScrWords)        its tagged partial words, and nothing else, so
+//                                no leftover of another use can carry a live tag
+//   [kScrCnt + kScrWords, end)   the quantized activation, then the small-M
+//                                GEMM's K-split slices
+// Every call on a device shares that device's copy of the array: calls that
+// overlap on one device (two streams, two threads) race.
+constexpr size_t kScrCnt = 64 << 10, kScrWords = 16 << 20, kScrGeneral = 32 << 20;
+constexpr size_t kScratchBytes = kScrCnt + kScrWords + kScrGeneral;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// The device address of `scratch` on each device (the host-side name is a
+// stand-in, never a device address), set once per device with that device
+// current, and each device's tag source for the split words.
+constexpr int kScrMaxDev = 64;
+static std::mutex g_scr_mu;
+static unsigned char *g_scr_ptr[kScrMaxDev];
+static std::atomic<uint32_t> g_scr_epoch[kScrMaxDev];
+
+int vxm_scratch_setup(vxm_ctx *ctx) {
+    ctx->scratch = nullptr;
+    if (ctx->device < 0 || ctx->device >= kScrMaxDev) {
+        ctx->scratch_err = "device index beyond the scratch table";
+        return VXM_OK;
+    }
+    std::lock_guard<std::mutex> lock(g_scr_mu);
+    if (!g_scr_ptr[ctx->device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            ctx->scratch_err = std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e);
+            return VXM_OK;   // only the allocation-free entry reports it
+        }
+        // all zero once, so the split words hold tag 0, which no launch uses
+        const int64_t n16 = (int64_t)(kScratchBytes / 16);
+        hipLaunchKernelGGL(k_fill_zero, dim3(1024), dim3(256), 0, ctx->stream, (uint4 *)p, n16);
+        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess) {
+            (void)hipGetLastError();
+            ctx->scratch_err = "clearing the scratch array failed";
+            return VXM_OK;
+        }
+        g_scr_ptr[ctx->device] = (unsigned char *)p;
+    }
+    ctx->scratch = g_scr_ptr[ctx->device];
+    return VXM_OK;
+}
+
+extern "C" size_t vxm_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int vxm_mul_mat_q8_0_noalloc(vxm_ctx *ctx, const vxm_weight *w, const float *x_dev, int64_t M,
+                                        float *y_dev) {
+    int rc = check_mm(ctx, w, x_dev, x_dev, M, y_dev);
+    if (rc) return rc;
+    if (!ctx->scratch) return vxm_fail(ctx, VXM_ERR_BACKEND, "mul_mat_noalloc: no scratch (%s)", ctx->scratch_err.c_str());
+    const int64_t K = w->k;
+    const size_t qbytes = ((size_t)M * K + 255) & ~(size_t)255;
+    const size_t abytes = qbytes + (((size_t)M * (K / VXM_QK) * 2 + 255) & ~(size_t)255);
+    if (abytes > kScrGeneral)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG,
+                        "mul_mat_noalloc: the quantized %lld x %lld activation needs %zu B; the scratch holds %zu B",
+                        (long long)M, (long long)K, abytes, kScrGeneral);
+    unsigned char *base = ctx->scratch;
+    unsigned char *gen = base + kScrCnt + kScrWords;
+    int8_t *xq = (int8_t *)gen;
+    uint16_t *xd = (uint16_t *)(gen + qbytes);
+    const MmWork wk{(uint64_t *)(base + kScrCnt), kScrWords, (int *)base, kScrCnt / sizeof(int),
+                    (float *)(gen + abytes), kScrGeneral - abytes, &g_scr_epoch[ctx->device]};
+    rc = vxm_launch_quantize(ctx, x_dev, M, K, ctx->quant_variant, xq, xd);
+    if (rc) return rc;
+    return launch_mul_mat(ctx, w, xq, xd, M, y_dev, &wk);
 }

@@ -62,6 +62,7 @@ extern "C" int vxm_open(int device, vxm_ctx **out) {
         g_open_err = "device error word allocation failed";
         return VXM_ERR_BACKEND;
     }
+    vxm_scratch_setup(ctx);   // a failure is reported by the allocation-free entry only
     *out = ctx;
     return VXM_OK;
 }

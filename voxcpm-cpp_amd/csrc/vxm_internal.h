@@ -41,6 +41,10 @@ struct vxm_ctx {
     // (a graph would replay stale tags) and an eager run must add in the same
     // order as the replays
     bool no_split_tags = false;
+    // this device's copy of the allocation-free matmul's scratch array (its
+    // device address), or null with the reason in scratch_err
+    unsigned char *scratch = nullptr;
+    std::string scratch_err;
 };
 
 // Device layout of a Q8_0 matrix (n_rows x k).  The GGUF row of k/32 34-byte
@@ -147,5 +151,7 @@ int vxm_launch_mul_mat_parts(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq
 bool vxm_launch_gate_up_swiglu(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                                int8_t *sq, uint16_t *sd, int variant, int *rc);
 int vxm_ensure_act(vxm_ctx *ctx, size_t bytes);
+// Finds the allocation-free matmul's scratch array on ctx's (current) device.
+int vxm_scratch_setup(vxm_ctx *ctx);
 int vxm_ensure_parts(vxm_ctx *ctx, size_t bytes);
 int vxm_ensure_split(vxm_ctx *ctx, size_t bytes, size_t n_counters);

@@ -72,6 +72,8 @@ _SIGS = {
     "vxm_quantize_q8_0": (_I, [_P, _P, _I64, _I64, _I, _P, _P]),
     "vxm_mul_mat_q8_0": (_I, [_P, _P, _P, _I64, _P]),
     "vxm_mul_mat_q8_0_q8_0": (_I, [_P, _P, _P, _P, _I64, _P]),
+    "vxm_mul_mat_q8_0_noalloc": (_I, [_P, _P, _P, _I64, _P]),
+    "vxm_noalloc_scratch_bytes": (C.c_size_t, []),
     "vxm_block_dots_q8_0": (_I, [_P, _P, _P, _P, _I64, _P]),
     "vxm_rms_norm": (_I, [_P, _P, _P, _I64, _I64, _F, _P, _P, _P]),
     "vxm_minicpm4_create": (_I, [_P, _P, _P, _P, C.POINTER(_P)]),
@@ -233,6 +235,11 @@ class Context:
         M = x.shape[0]
         y = torch.empty((M, w.n), dtype=torch.float32, device=x.device) if y is None else y
         self.check(lib().vxm_mul_mat_q8_0(self.h, w.h, _ptr(x), M, _ptr(y)))
+        return y
+
+    def mul_mat_noalloc(self, w, x, y):
+        """ggml_mul_mat(W, x) through the allocation-free entry: y must be given."""
+        self.check(lib().vxm_mul_mat_q8_0_noalloc(self.h, w.h, _ptr(x), x.shape[0], _ptr(y)))
         return y
 
     def mul_mat_q8(self, w, xq, xd, y=None):
