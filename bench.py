@@ -147,24 +147,65 @@ def bench_gemv(ctx, torch, vxm, N, K, copies, reps):
     return us
 
 
-def bench_copy_floor(torch, nbytes, copies, reps):
-    """Per-launch time of a device copy moving nbytes (nbytes/2 read + nbytes/2 written), back to back
-    over `copies` rotated buffer pairs: what one launch of that much traffic costs on this device."""
-    n = nbytes // 8
-    src = [torch.ones(n, dtype=torch.float32, device="cuda:0") for _ in range(copies)]
-    dst = [torch.empty_like(a) for a in src]
-    for a, b in zip(src, dst):
-        b.copy_(a)
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
+def bench_gemv_multi(ctx, torch, vxm, N, K, copies, reps):
+    """`copies` rotated copies of one GEMV in ONE launch (vxm_mul_mat_q8_0_q8_0_multi), launches back to
+    back: us per launch (all copies)."""
+    import ctypes as C
+
+    import numpy as np
+
+    w32 = vxm.host_randn(0, N * K, 0.0, 0.02).reshape(N, K)
+    x = vxm.host_randn(0, K, 0.0, 1.0, offset=N * K).reshape(1, K)
+    wq = vxm.host_quantize_q8_0(w32)
+    ws = [ctx.upload_q8_0(wq, N, K) for _ in range(copies)]
+    xq, xs = ctx.quantize_q8_0(torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0"), vxm.QUANT_X86)
+    ys = [torch.empty((1, N), dtype=torch.float32, device="cuda:0") for _ in range(copies)]
+    arr = C.c_void_p * copies
+    a_w = arr(*[w.h.value for w in ws])
+    a_q = arr(*[xq.data_ptr()] * copies)
+    a_s = arr(*[xs.data_ptr()] * copies)
+    a_y = arr(*[y.data_ptr() for y in ys])
+    L_ = vxm.lib()
+    ctx.check(L_.vxm_mul_mat_q8_0_q8_0_multi(ctx.h, copies, a_w, a_q, a_s, 1, a_y))
+    ctx.sync()
+    ref = ctx.mul_mat_q8(ws[0], xq, xs)
+    same = all(bool(torch.equal(y, ref)) for y in ys)
+    t = Timer(torch, ctx)
+    t.start()
     for _ in range(reps):
-        for a, b in zip(src, dst):
-            b.copy_(a)
-    e1.record()
-    e1.synchronize()
-    return e0.elapsed_time(e1) * 1000.0 / (reps * copies)
+        L_.vxm_mul_mat_q8_0_q8_0_multi(ctx.h, copies, a_w, a_q, a_s, 1, a_y)
+    us = t.stop_ms() * 1000.0 / reps
+    for w in ws:
+        w.free()
+    return us, same
+
+
+def bench_read_floor(ctx, torch, vxm, nbytes, copies, reps, per_launch):
+    """vxm_stream_read over `copies` buffers of nbytes: `per_launch` buffers per launch, launches back to
+    back over the rotation.  Returns us per buffer read."""
+    import ctypes as C
+
+    n16 = (nbytes + 15) // 16
+    bufs = [torch.ones(n16 * 4, dtype=torch.int32, device="cuda:0") for _ in range(copies)]
+    groups = [bufs[i:i + per_launch] for i in range(0, copies, per_launch)]
+    args = []
+    for g in groups:
+        args.append((len(g), (C.c_void_p * len(g))(*[b.data_ptr() for b in g]),
+                     (C.c_int64 * len(g))(*[n16 * 16] * len(g))))
+    L_ = vxm.lib()
+    words = max(L_.vxm_stream_read_sink_words(n, b) for n, _, b in args)
+    sink = torch.zeros(words, dtype=torch.int32, device="cuda:0")
+    for n, p, b in args:
+        ctx.check(L_.vxm_stream_read(ctx.h, n, p, b, C.c_void_p(sink.data_ptr())))
+    ctx.sync()
+    t = Timer(torch, ctx)
+    t.start()
+    for _ in range(reps):
+        for n, p, b in args:
+            L_.vxm_stream_read(ctx.h, n, p, b, C.c_void_p(sink.data_ptr()))
+    us = t.stop_ms() * 1000.0 / (reps * copies)
+    del bufs
+    return us
 
 
 def bench_decode(ctx, torch, vxm, layers, n_layers, copies, ctx0, steps, warmup, mode):
@@ -543,18 +584,31 @@ def main():
             return
     if not args.decode_only and not args.lm_update_only:
         for (N, K) in ((6144, 2048), (2048, 6144)):
+            gb = gemv_bytes(N, K)
             us = bench_gemv(ctx, torch, vxm, N, K, 64, 10)
-            gbs = gemv_bytes(N, K) / (us * 1e-6) / 1e9
-            cus = bench_copy_floor(torch, gemv_bytes(N, K), 64, 10)
-            cgbs = gemv_bytes(N, K) / (cus * 1e-6) / 1e9
+            gbs = gb / (us * 1e-6) / 1e9
+            us_m, same = bench_gemv_multi(ctx, torch, vxm, N, K, 64, 10)
+            mgbs = 64 * gb / (us_m * 1e-6) / 1e9
+            rus1 = bench_read_floor(ctx, torch, vxm, gb, 64, 10, 1)
+            rus64 = bench_read_floor(ctx, torch, vxm, gb, 64, 10, 64)
             res[f"{N}x{K}"] = {"us_per_launch": round(us, 3), "GBs": round(gbs, 1),
                                "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                               "copy_floor_us_per_launch": round(cus, 3), "copy_floor_GBs": round(cgbs, 1),
-                               "note": "one launch per GEMV, back to back over 64 rotated weight copies; "
-                                       "copy_floor: a device copy moving the same bytes, back to back over 64 "
-                                       "rotated buffers"}
+                               "read_floor_us_per_launch": round(rus1, 3),
+                               "read_floor_GBs": round(gb / (rus1 * 1e-6) / 1e9, 1),
+                               "multi": {"gemvs_per_launch": 64, "us_per_launch": round(us_m, 2),
+                                         "us_per_gemv": round(us_m / 64, 3), "GBs": round(mgbs, 1),
+                                         "hbm_frac": round(mgbs / HBM_PEAK_GBS, 4),
+                                         "bit_identical_to_single": same,
+                                         "read_floor_GBs": round(gb / (rus64 * 1e-6) / 1e9, 1),
+                                         "read_floor_hbm_frac": round(gb / (rus64 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+                               "note": "us_per_launch: one launch per GEMV, back to back over 64 rotated weight "
+                                       "copies (855 MB, beyond the 256 MB Infinity Cache); multi: the 64 copies "
+                                       "in one launch; read_floor: vxm_stream_read of the same bytes, one buffer "
+                                       "per launch / 64 per launch"}
             log(f"gemv {N}x{K}: {us:.3f} us/launch, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM); "
-                f"copy of the same bytes {cus:.3f} us/launch, {cgbs:.1f} GB/s")
+                f"64 per launch {us_m / 64:.3f} us/GEMV, {mgbs:.1f} GB/s ({100 * mgbs / HBM_PEAK_GBS:.1f}%), "
+                f"bit-identical={same}; read floor {gb / (rus1 * 1e-6) / 1e9:.1f} GB/s single, "
+                f"{gb / (rus64 * 1e-6) / 1e9:.1f} GB/s 64 per launch")
         if args.gemv_only:
             print(json.dumps({"gemv": res}))
             ctx.close()

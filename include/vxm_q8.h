@@ -98,6 +98,27 @@ int vxm_mul_mat_q8_0(vxm_ctx *ctx, const vxm_weight *w, const float *x_dev, int6
 /* y = W . x for an already quantized activation. */
 int vxm_mul_mat_q8_0_q8_0(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq_dev,
                           const uint16_t *xd_dev, int64_t M, float *y_dev);
+/* n independent products y_i = W_i . x_i of already quantized activations
+ * (M rows each, every W_i of the same K) in one launch per 64 products.  They
+ * are the mul_mat nodes of one reference graph that share no dependency (the
+ * q/k/v projections, src/minicpm4.c:270-279; gate and up, src/minicpm4.c:
+ * 441-458), which ggml runs one after another inside vcpm_backend_compute_graph
+ * (src/ggml_backend.c:557-599).  Every y_i is bit-identical to
+ * vxm_mul_mat_q8_0_q8_0's for the same operands.  Shapes that the chunked GEMV
+ * does not take (M >= 8, K / 1024 not in {1, 2, 4, 6}) run one product per
+ * launch on the kernel vxm_mul_mat_q8_0_q8_0 picks. */
+int vxm_mul_mat_q8_0_q8_0_multi(vxm_ctx *ctx, int32_t n, const vxm_weight *const *w,
+                                const int8_t *const *xq_dev, const uint16_t *const *xd_dev, int64_t M,
+                                float *const *y_dev);
+/* Measurement helper, no counterpart in the reference: reads n <= 128 device
+ * ranges (16-byte aligned, sizes multiples of 16 B) once, in one launch, with
+ * the GEMV's 128-bit streaming loads, and writes one XOR of 32-bit words per
+ * wave to sink_dev, which holds vxm_stream_read_sink_words(n, bytes) words
+ * (their XOR is the XOR of every word read).  The HBM read floor of a launch
+ * that moves the same bytes. */
+int vxm_stream_read(vxm_ctx *ctx, int32_t n, const void *const *ranges_dev, const int64_t *bytes,
+                    uint32_t *sink_dev);
+int64_t vxm_stream_read_sink_words(int32_t n, const int64_t *bytes);
 /* vxm_mul_mat_q8_0 without any allocation: no counterpart in the reference.
  * For callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same

@@ -279,3 +279,92 @@ def test_auto_path_switches_at_eight_rows(vxm_ctx, orc):
         _assert_close(y_gemv, ref)
         _assert_close(y_mfma, ref)
         w.free()
+
+
+# (K, [N of each product], M): products of one K in one launch
+_MULTI = [
+    (2048, [2048, 256, 256, 6144, 12288], 1),   # q, k, v, gate, gate/up-sized
+    (6144, [2048, 2048, 64], 1),                # down-sized
+    (1024, [1024, 37, 3072], 2),                # GEMV <1, 4> with a ragged N
+    (4096, [1024, 5], 3),                       # GEMV <4, 1>, three rows
+    (96, [7, 5], 2),                            # K outside the chunked GEMV: one launch each
+]
+
+
+@pytest.mark.parametrize("K,Ns,M", _MULTI)
+def test_mul_mat_multi_bit_identical_to_single(vxm_ctx, orc, K, Ns, M):
+    """Every output of the one-launch GEMV batch equals the single GEMV's bit for
+    bit (the same per-wave code), and the single GEMV's block sums are pinned."""
+    import torch
+
+    ws, xqs, xds, singles, refs = [], [], [], [], []
+    for i, N in enumerate(Ns):
+        _, x, wq = _case(orc, N, K, M, 1000 + 17 * i + K + M)
+        w = vxm_ctx.upload_q8_0(wq, N, K)
+        xq, xd = vxm_ctx.quantize_q8_0(_dev(x), 1)
+        ws.append(w); xqs.append(xq); xds.append(xd)
+        singles.append(_np(vxm_ctx.mul_mat_q8(w, xq, xd)))
+        refs.append(orc.mul_mat_f64(wq, orc.quantize_rows(x, 1), N, K, M))
+    ys = [torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda:0") for N in Ns]
+    vxm_ctx.mul_mat_q8_multi(ws, xqs, xds, ys)
+    for y, s, r in zip(ys, singles, refs):
+        got = _np(y)
+        assert np.array_equal(got.view(np.uint32), s.view(np.uint32))
+        _assert_close(got, r)
+    for w in ws:
+        w.free()
+
+
+def test_mul_mat_multi_more_than_one_launch(vxm_ctx, orc):
+    """70 products (a launch takes 64): every output still equals the single GEMV's."""
+    import torch
+
+    N, K, M = 128, 2048, 1
+    _, x, _ = _case(orc, 1, K, M, 5)
+    xq, xd = vxm_ctx.quantize_q8_0(_dev(x), 1)
+    ws, ys, singles = [], [], []
+    for i in range(70):
+        _, _, wq = _case(orc, N, K, 1, 300 + i)
+        w = vxm_ctx.upload_q8_0(wq, N, K)
+        ws.append(w)
+        singles.append(_np(vxm_ctx.mul_mat_q8(w, xq, xd)))
+        ys.append(torch.empty((M, N), dtype=torch.float32, device="cuda:0"))
+    vxm_ctx.mul_mat_q8_multi(ws, [xq] * 70, [xd] * 70, ys)
+    for y, s in zip(ys, singles):
+        assert np.array_equal(_np(y).view(np.uint32), s.view(np.uint32))
+    for w in ws:
+        w.free()
+
+
+def test_mul_mat_multi_rejects_mixed_k(vxm_ctx, orc):
+    import vxm
+
+    _, x, wq1 = _case(orc, 64, 1024, 1, 1)
+    _, _, wq2 = _case(orc, 64, 2048, 1, 2)
+    w1, w2 = vxm_ctx.upload_q8_0(wq1, 64, 1024), vxm_ctx.upload_q8_0(wq2, 64, 2048)
+    xq, xd = vxm_ctx.quantize_q8_0(_dev(x), 1)
+    import torch
+
+    ys = [torch.empty((1, 64), dtype=torch.float32, device="cuda:0") for _ in range(2)]
+    with pytest.raises(vxm.VxmError) as e:
+        vxm_ctx.mul_mat_q8_multi([w1, w2], [xq, xq], [xd, xd], ys)
+    assert e.value.code == 1
+    w1.free()
+    w2.free()
+
+
+def test_stream_read_checksum(vxm_ctx):
+    """The read floor kernel reads every byte once: its XOR of all 32-bit words
+    equals numpy's over the same ranges (ragged sizes, several ranges)."""
+    import torch
+
+    rng = np.random.default_rng(9)
+    sizes = [16, 16384, 16400, 1 << 20, 13369344 + 16 * 7]
+    hs = [rng.integers(0, 2 ** 32, n // 4, dtype=np.uint32) for n in sizes]
+    ds = [torch.from_numpy(h.view(np.int32)).to("cuda:0") for h in hs]
+    sink = vxm_ctx.stream_read(ds)
+    vxm_ctx.sync()
+    ref = np.uint32(0)
+    for h in hs:
+        ref ^= np.bitwise_xor.reduce(h)
+    assert int(np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))) == int(ref)

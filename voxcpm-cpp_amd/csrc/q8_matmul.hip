@@ -97,15 +97,13 @@ int vxm_launch_quantize(vxm_ctx *ctx, const float *x, int64_t M, int64_t K, int 
 // lane-pair exchange) to dots[(m*N + n)*(K/32) + b] instead of y.
 // ---------------------------------------------------------------------------
 template <int C, int R, bool DOTS>
-__global__ __launch_bounds__(256) void k_gemv_q8_0(const int8_t *__restrict__ qs,
-                                                   const uint16_t *__restrict__ dg,
-                                                   const int8_t *__restrict__ xq,
-                                                   const uint16_t *__restrict__ xd, float *__restrict__ y,
-                                                   int N, int M, int32_t *__restrict__ dots) {
+__device__ __forceinline__ void gemv_wave(const int8_t *__restrict__ qs, const uint16_t *__restrict__ dg,
+                                          const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd,
+                                          float *__restrict__ y, int N, int M, int32_t *__restrict__ dots,
+                                          int wave) {
     constexpr int K = C * 1024;
     constexpr int NB = K / 32;
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int row0 = wave * R;
     if (row0 >= N) return;
     const int pair = lane >> 1;
@@ -167,6 +165,99 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0(const int8_t *__restrict__ qs
                 if (row0 + r < N) y[(int64_t)m * N + row0 + r] = acc[r];
         }
     }
+}
+
+template <int C, int R, bool DOTS>
+__global__ __launch_bounds__(256) void k_gemv_q8_0(const int8_t *__restrict__ qs,
+                                                   const uint16_t *__restrict__ dg,
+                                                   const int8_t *__restrict__ xq,
+                                                   const uint16_t *__restrict__ xd, float *__restrict__ y,
+                                                   int N, int M, int32_t *__restrict__ dots) {
+    gemv_wave<C, R, DOTS>(qs, dg, xq, xd, y, N, M, dots, blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+}
+
+// ---------------------------------------------------------------------------
+// Many independent GEMVs of one K in one launch (the decode projections that
+// share no dependency, or a stream of them).  A single GEMV of 13 MB cannot
+// keep HBM busy: the launch ramp and the first loads' latency are a fixed
+// ~2 us against 1.7 us of streaming at 8 TB/s.  Here the workgroups of all
+// products form one grid; workgroup b runs wave (b - wg0) * 4 + w of the item
+// with the largest wg0 <= b, with exactly the single GEMV's per-wave code, so
+// every output is bit-identical to k_gemv_q8_0's.  The item table is a kernel
+// argument (read with scalar loads through the kernarg pointer).
+// ---------------------------------------------------------------------------
+constexpr int kMultiMax = 64;
+struct GemvItem {
+    const int8_t *qs;
+    const uint16_t *dg;
+    const int8_t *xq;
+    const uint16_t *xd;
+    float *y;
+    int n, wg0;
+};
+struct GemvBatch {
+    GemvItem it[kMultiMax];
+    int n_items;
+};
+
+template <int C, int R>
+__global__ __launch_bounds__(256) void k_gemv_q8_0_multi(const GemvBatch b, int M) {
+    const int bid = blockIdx.x;
+    int lo = 0, hi = b.n_items - 1;
+    while (lo < hi) {   // uniform binary search: the last item starting at or before bid
+        const int mid = (lo + hi + 1) >> 1;
+        if (b.it[mid].wg0 <= bid) lo = mid;
+        else hi = mid - 1;
+    }
+    const GemvItem &t = b.it[lo];
+    gemv_wave<C, R, false>(t.qs, t.dg, t.xq, t.xd, t.y, t.n, M, nullptr, (bid - t.wg0) * 4 + (threadIdx.x >> 6));
+}
+
+// ---------------------------------------------------------------------------
+// Read-only stream (a measurement helper): n device ranges read once in one
+// launch with the GEMV's loads, every 32-bit word XOR-folded into one word
+// per wave.  It is the floor a launch of the same bytes can reach on this
+// device.  Workgroup b reads 16 KiB of the range with the largest wg0 <= b;
+// as in the GEMV, each wave reads 4 contiguous KiB (one KiB per load
+// instruction, non-temporal) and ends with one plain store: atomics from every
+// wave into shared words serialised (6.1 against 7.1 TB/s measured), and
+// spreading a wave's loads over the workgroup's 16 KiB cost as much.
+// ---------------------------------------------------------------------------
+constexpr int kReadMax = 128;
+constexpr int kReadWgBytes = 16384;
+struct ReadRange {
+    const uint4 *p;
+    int64_t n16;   // 16-byte words
+    int wg0;
+};
+struct ReadBatch {
+    ReadRange r[kReadMax];
+    int n;
+};
+
+__global__ __launch_bounds__(256) void k_stream_read(const ReadBatch b, uint32_t *__restrict__ sink) {
+    const int bid = blockIdx.x;
+    int lo = 0, hi = b.n - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (b.r[mid].wg0 <= bid) lo = mid;
+        else hi = mid - 1;
+    }
+    const ReadRange &t = b.r[lo];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t w0 = (int64_t)(bid - t.wg0) * (kReadWgBytes / 16) + wave * 256 + lane;
+    v4i v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int64_t w = w0 + i * 64;
+        v[i] = w < t.n16 ? __builtin_nontemporal_load((const v4i *)(t.p + w)) : v4i{0, 0, 0, 0};
+    }
+    uint32_t x = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) x ^= (uint32_t)(v[i].x ^ v[i].y ^ v[i].z ^ v[i].w);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) x ^= __shfl_xor(x, m, 64);
+    if (lane == 0) sink[(int64_t)bid * 4 + wave] = x;
 }
 
 // ---------------------------------------------------------------------------
@@ -1245,4 +1336,90 @@ extern "C" int vxm_mul_mat_q8_0_noalloc(vxm_ctx *ctx, const vxm_weight *w, const
     rc = vxm_launch_quantize(ctx, x_dev, M, K, ctx->quant_variant, xq, xd);
     if (rc) return rc;
     return launch_mul_mat(ctx, w, xq, xd, M, y_dev, &wk);
+}
+
+// ---- many GEMVs in one launch, and the read floor ---------------------------
+template <int C, int R>
+static int launch_gemv_multi(vxm_ctx *ctx, int n, const vxm_weight *const *w, const int8_t *const *xq,
+                             const uint16_t *const *xd, int64_t M, float *const *y) {
+    GemvBatch b;
+    int wg = 0;
+    for (int i = 0; i < n; i++) {
+        const int waves = (int)((w[i]->n + R - 1) / R);
+        b.it[i] = GemvItem{w[i]->qs, w[i]->dg, xq[i], xd[i], y[i], (int)w[i]->n, wg};
+        wg += (waves + 3) / 4;
+    }
+    b.n_items = n;
+    hipLaunchKernelGGL((k_gemv_q8_0_multi<C, R>), dim3(wg), dim3(256), 0, ctx->stream, b, (int)M);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}
+
+extern "C" int vxm_mul_mat_q8_0_q8_0_multi(vxm_ctx *ctx, int32_t n, const vxm_weight *const *w,
+                                           const int8_t *const *xq_dev, const uint16_t *const *xd_dev, int64_t M,
+                                           float *const *y_dev) {
+    if (!ctx) return VXM_ERR_INVALID_ARG;
+    if (n < 0 || (n > 0 && (!w || !xq_dev || !xd_dev || !y_dev)) || M < 0)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "mul_mat_multi: bad arguments (n=%d M=%lld)", n, (long long)M);
+    for (int i = 0; i < n; i++) {
+        int rc = check_mm(ctx, w[i], xq_dev[i], xd_dev[i], M, y_dev[i]);
+        if (rc) return rc;
+        if (w[i]->k != w[0]->k)
+            return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "mul_mat_multi: product %d has K %lld, product 0 has %lld", i,
+                            (long long)w[i]->k, (long long)w[0]->k);
+    }
+    if (n == 0 || M == 0) return VXM_OK;
+    // one launch per 64 products where the chunked GEMV takes the shape; else each
+    // product on the kernel vxm_mul_mat_q8_0_q8_0 picks
+    const int64_t K = w[0]->k;
+    bool chunked = !use_mfma(ctx, M) && (K / 1024 == 1 || K / 1024 == 2 || K / 1024 == 4 || K / 1024 == 6) &&
+                   K % 1024 == 0;
+    for (int i = 0; chunked && i < n; i++) chunked = w[i]->dg != nullptr;
+    if (!chunked) {
+        for (int i = 0; i < n; i++) {
+            int rc = vxm_launch_mul_mat(ctx, w[i], xq_dev[i], xd_dev[i], M, y_dev[i]);
+            if (rc) return rc;
+        }
+        return VXM_OK;
+    }
+    for (int i0 = 0; i0 < n; i0 += kMultiMax) {
+        const int c = n - i0 < kMultiMax ? n - i0 : kMultiMax;
+        int rc = VXM_OK;
+        switch (K / 1024) {
+            case 1: rc = launch_gemv_multi<1, 4>(ctx, c, w + i0, xq_dev + i0, xd_dev + i0, M, y_dev + i0); break;
+            case 2: rc = launch_gemv_multi<2, 2>(ctx, c, w + i0, xq_dev + i0, xd_dev + i0, M, y_dev + i0); break;
+            case 4: rc = launch_gemv_multi<4, 1>(ctx, c, w + i0, xq_dev + i0, xd_dev + i0, M, y_dev + i0); break;
+            default: rc = launch_gemv_multi<6, 1>(ctx, c, w + i0, xq_dev + i0, xd_dev + i0, M, y_dev + i0); break;
+        }
+        if (rc) return rc;
+    }
+    return VXM_OK;
+}
+
+extern "C" int64_t vxm_stream_read_sink_words(int32_t n, const int64_t *bytes) {
+    int64_t wg = 0;
+    for (int i = 0; i < n; i++) wg += (bytes[i] + kReadWgBytes - 1) / kReadWgBytes;
+    return 4 * wg;
+}
+
+extern "C" int vxm_stream_read(vxm_ctx *ctx, int32_t n, const void *const *ranges_dev, const int64_t *bytes,
+                               uint32_t *sink_dev) {
+    if (!ctx) return VXM_ERR_INVALID_ARG;
+    if (n < 0 || n > kReadMax || (n > 0 && (!ranges_dev || !bytes)) || !sink_dev)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "stream_read: bad arguments (n=%d, at most %d ranges)", n, kReadMax);
+    ReadBatch b;
+    int64_t wg = 0;
+    for (int i = 0; i < n; i++) {
+        if (!ranges_dev[i] || bytes[i] < 0 || bytes[i] % 16 || ((uintptr_t)ranges_dev[i] & 15))
+            return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "stream_read: range %d must be 16-byte aligned, a multiple of 16 B", i);
+        b.r[i] = ReadRange{(const uint4 *)ranges_dev[i], bytes[i] / 16, (int)wg};
+        // (sink: 4 words per workgroup, vxm_stream_read_sink_words)
+        wg += (bytes[i] + kReadWgBytes - 1) / kReadWgBytes;
+        if (wg >= INT32_MAX) return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "stream_read: too many bytes in one launch");
+    }
+    b.n = n;
+    if (wg == 0) return VXM_OK;
+    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)wg), dim3(256), 0, ctx->stream, b, sink_dev);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
 }

@@ -74,6 +74,9 @@ _SIGS = {
     "vxm_mul_mat_q8_0_q8_0": (_I, [_P, _P, _P, _P, _I64, _P]),
     "vxm_mul_mat_q8_0_noalloc": (_I, [_P, _P, _P, _I64, _P]),
     "vxm_noalloc_scratch_bytes": (C.c_size_t, []),
+    "vxm_mul_mat_q8_0_q8_0_multi": (_I, [_P, C.c_int32, _P, _P, _P, _I64, _P]),
+    "vxm_stream_read": (_I, [_P, C.c_int32, _P, _P, _P]),
+    "vxm_stream_read_sink_words": (_I64, [C.c_int32, _P]),
     "vxm_block_dots_q8_0": (_I, [_P, _P, _P, _P, _I64, _P]),
     "vxm_rms_norm": (_I, [_P, _P, _P, _I64, _I64, _F, _P, _P, _P]),
     "vxm_minicpm4_create": (_I, [_P, _P, _P, _P, C.POINTER(_P)]),
@@ -241,6 +244,32 @@ class Context:
         """ggml_mul_mat(W, x) through the allocation-free entry: y must be given."""
         self.check(lib().vxm_mul_mat_q8_0_noalloc(self.h, w.h, _ptr(x), x.shape[0], _ptr(y)))
         return y
+
+    def mul_mat_q8_multi(self, ws, xqs, xds, ys):
+        """y_i = W_i . x_i for quantized x_i (M rows each, one K) in one launch per 64."""
+        n = len(ws)
+        M = xqs[0].shape[0] if n else 0
+
+        def arr(ptrs):
+            return (C.c_void_p * max(n, 1))(*[p.value for p in ptrs])
+
+        self.check(lib().vxm_mul_mat_q8_0_q8_0_multi(
+            self.h, n, arr([C.c_void_p(w.h.value) for w in ws]), arr([_ptr(t) for t in xqs]),
+            arr([_ptr(t) for t in xds]), M, arr([_ptr(t) for t in ys])))
+        return ys
+
+    def stream_read(self, tensors):
+        """Read every tensor once in one launch; returns the device words (one per wave) whose XOR
+        is the XOR of all 32-bit words read."""
+        import torch
+
+        n = len(tensors)
+        ptrs = (C.c_void_p * max(n, 1))(*[_ptr(t).value for t in tensors])
+        sizes = (C.c_int64 * max(n, 1))(*[t.numel() * t.element_size() for t in tensors])
+        words = lib().vxm_stream_read_sink_words(n, sizes)
+        sink = torch.zeros(max(words, 1), dtype=torch.int32, device=f"cuda:{self.device}")
+        self.check(lib().vxm_stream_read(self.h, n, ptrs, sizes, _ptr(sink)))
+        return sink
 
     def mul_mat_q8(self, w, xq, xd, y=None):
         import torch
