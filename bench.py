@@ -239,6 +239,38 @@ def bench_decode(ctx, torch, vxm, layers, n_layers, copies, ctx0, steps, warmup,
     return ms * 1000.0 / steps, ok
 
 
+def bench_decode_long(ctx, torch, vxm, layers, copies, contexts, steps, mode):
+    """28-layer decode at long contexts: one cache of capacity max(contexts) + steps filled once,
+    `steps` tokens timed from each context.  Returns {context: us per token}."""
+    cfg = dict(hidden_size=H, n_layers=L, n_heads=NH, n_kv_heads=NKV, head_dim=HD, intermediate_size=F,
+               rms_norm_eps=1e-6, rope_theta=10000)
+    fn = vxm.host_randn(11, H, 1.0, 0.02)
+    models = [vxm.MiniCPM4(ctx, cfg, layers, final_norm=fn) for _ in range(copies)]
+    for m in models:
+        m.set_decode_mode(mode)
+    kv = vxm.KVCache(ctx, L, NKV, HD, max(contexts) + steps)
+    kv_prefill(vxm, kv, L, max(contexts), 5)
+    x = torch.from_numpy(vxm.host_randn(3, H, 0.0, 1.0).reshape(1, H)).to("cuda:0")
+    out = {}
+    for c0 in contexts:
+        kv.set_used(c0)
+        for i in range(2):
+            models[i % copies].forward(kv, x, c0 + i)
+        ctx.sync()
+        kv.set_used(c0)
+        t = Timer(torch, ctx)
+        t.start()
+        for i in range(steps):
+            models[i % copies].forward(kv, x, c0 + i)
+        out[c0] = t.stop_ms() * 1000.0 / steps
+    for m in models:
+        m.check()
+    kv.free()
+    for m in models:
+        m.free()
+    return out
+
+
 def bench_gemm(ctx, torch, vxm, N, K, M, reps):
     """One Q8_0 x Q8_0 matmul of M activation rows (the MFMA GEMM), back to back."""
     import numpy as np
@@ -518,6 +550,8 @@ def main():
     ap.add_argument("--cfm-only", action="store_true", help="time only the CFM solve leg")
     ap.add_argument("--gemv-only", action="store_true", help="time only the isolated Q8_0 GEMV leg")
     ap.add_argument("--lm-update-only", action="store_true", help="time only the per-token LM update leg")
+    ap.add_argument("--long-context-only", action="store_true",
+                    help="time only the 28-layer decode at long contexts (single-launch and per-op paths)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 device copies of 256 MiB (a known-traffic kernel for HBM counter scaling)")
     args = ap.parse_args()
@@ -541,7 +575,7 @@ def main():
     res = {}
     pre = None
     cfm = None
-    if not args.decode_only and not args.prefill_only and not args.gemv_only and not args.lm_update_only:
+    if not (args.decode_only or args.prefill_only or args.gemv_only or args.lm_update_only or args.long_context_only):
         us_cfm, evals, fin = bench_cfm(ctx, torch, vxm, 5)
         eb = locdit_eval_bytes()
         ops = 2 * 2 * (3 + DIT["PC"] + DIT["P"]) * (eb * 32 // 34)
@@ -556,7 +590,7 @@ def main():
             print(json.dumps({"cfm": cfm}))
             ctx.close()
             return
-    if not args.decode_only and not args.gemv_only and not args.lm_update_only:
+    if not (args.decode_only or args.gemv_only or args.lm_update_only or args.long_context_only):
         M = args.prefill_tokens
         gemms = {}
         for name, (N, K) in (("qkv", (NH * HD + 2 * NKV * HD, H)), ("o", (H, NH * HD)), ("gate_up", (2 * F, H)),
@@ -582,7 +616,7 @@ def main():
             print(json.dumps({"prefill": pre}))
             ctx.close()
             return
-    if not args.decode_only and not args.lm_update_only:
+    if not (args.decode_only or args.lm_update_only or args.long_context_only):
         for (N, K) in ((6144, 2048), (2048, 6144)):
             gb = gemv_bytes(N, K)
             us = bench_gemv(ctx, torch, vxm, N, K, 64, 10)
@@ -619,11 +653,31 @@ def main():
     log(f"generated {L} Q8_0 layers in {time.time() - t0:.1f} s")
 
     us1 = None
-    if not args.decode_only and not args.lm_update_only:
+    if not (args.decode_only or args.lm_update_only or args.long_context_only):
         # one decoder layer, context 512 (8 rotated copies of the layer)
         us1, _ = bench_decode(ctx, torch, vxm, layers[:1], 1, 8, 512, 64, 4, mode)
         layer_b = step_bytes(512, 1)
         log(f"one layer decode @ctx512: {us1:.2f} us, {layer_b / (us1 * 1e-6) / 1e9:.1f} GB/s")
+
+    longc = None
+    if args.long_context_only or not (args.decode_only or args.lm_update_only):
+        contexts = (1024, 2048, 4096, 8000) if args.long_context_only else (4096, 8000)
+        lc = bench_decode_long(ctx, torch, vxm, layers, args.copies, contexts, 16, 2)
+        longc = {"contexts": {str(c): {"us_per_token": round(u, 1),
+                                       "GBs": round(step_bytes(c + 7.5) / (u * 1e-6) / 1e9, 1)}
+                              for c, u in lc.items()},
+                 "note": "single-launch decode, 16 tokens from each context, cache capacity 8016; the keys of "
+                         "each head are split over up to 16 workgroups beyond 640"}
+        log("long-context decode (single launch): " +
+            ", ".join(f"ctx {c} {u:.1f} us" for c, u in lc.items()))
+        if args.long_context_only:
+            lk = bench_decode_long(ctx, torch, vxm, layers, args.copies, contexts, 8, 1)
+            longc["per_op_us_per_token"] = {str(c): round(u, 1) for c, u in lk.items()}
+            log("long-context decode (per-op kernels): " +
+                ", ".join(f"ctx {c} {u:.1f} us" for c, u in lk.items()))
+            print(json.dumps({"long_context": longc}))
+            ctx.close()
+            return
 
     mean_ctx = 256 + (args.steps - 1) / 2.0
     if args.lm_update_only:
@@ -701,6 +755,7 @@ def main():
         "prefill": pre,
         "cfm": cfm,
         "lm_update": lmu,
+        "long_context": longc,
         "roofline": roof,
         "cpu_baseline": cpu,
     }

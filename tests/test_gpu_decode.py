@@ -37,7 +37,7 @@ SHAPES = {
 }
 
 
-def _setup(orc, vxm, vxm_ctx, shape, L, cap, ctx0, seed, no_rope=0):
+def _setup(orc, vxm, vxm_ctx, shape, L, cap, ctx0, seed, no_rope=0, kscale=1.0):
     s = SHAPES[shape]
     rng = np.random.default_rng(seed)
     lws = [rand_layer(orc, rng, s["H"], s["nh"], s["nkv"], s["hd"], s["F"]) for _ in range(L)]
@@ -53,7 +53,7 @@ def _setup(orc, vxm, vxm_ctx, shape, L, cap, ctx0, seed, no_rope=0):
     for l in range(L):
         k = np.zeros((s["nkv"], cap, s["hd"]), np.uint16)
         v = np.zeros_like(k)
-        k[:, :ctx0] = orc.fp32_to_fp16_bits(orc.bf16_round(rng.normal(0, 1, (s["nkv"], ctx0, s["hd"])).astype(np.float32)))
+        k[:, :ctx0] = orc.fp32_to_fp16_bits(orc.bf16_round(rng.normal(0, kscale, (s["nkv"], ctx0, s["hd"])).astype(np.float32)))
         v[:, :ctx0] = orc.fp32_to_fp16_bits(orc.bf16_round(rng.normal(0, 1, (s["nkv"], ctx0, s["hd"])).astype(np.float32)))
         for mode in (1, 2):
             kvs[mode].upload(l, k, v)
@@ -213,3 +213,117 @@ def test_persistent_decode_after_cache_free_and_recreate(vxm_ctx, orc):
             kv.free()
     finally:
         m.free()
+
+
+@pytest.mark.parametrize("ctx0,steps", [
+    (382, 4),     # 383, 384 keys on one workgroup per head, then 385, 386 split in two chunks
+    (2047, 2),    # 2048 keys: 8 chunks per head, 2049: 9
+    (4095, 2),    # 4096 keys: 16 chunks of 256, 4097: 16 of 257
+    (8190, 2),    # 8191, 8192 keys: 16 chunks of 512
+])
+def test_persistent_long_context_matches_oracle(vxm_ctx, orc, ctx0, steps):
+    """Long contexts stay on the single-launch kernel, which splits each head's keys
+    over up to 16 workgroups and merges the chunk softmaxes in chunk order: two
+    full-width layers against the oracle and the per-op path, appended KV rows too."""
+    import vxm
+
+    cap, L = 8192, 2
+    print(f"long context ctx0={ctx0} steps={steps}", flush=True)
+    s, rng, c, lws, fn, models, kvs, kcs, vcs = _setup(orc, vxm, vxm_ctx, "tslm", L, cap, ctx0, 17 + ctx0)
+    oc = orc_cfg(orc, c)
+    ol = [to_orc(orc, l) for l in lws]
+    for t in range(steps):
+        x = rng.normal(0, 1, (1, s["H"])).astype(np.float32)
+        outs = {}
+        for mode in (1, 2):
+            xd = _dev(x)
+            models[mode].forward(kvs[mode], xd, ctx0 + t)
+            vxm_ctx.sync()
+            outs[mode] = xd.cpu().numpy()
+        models[2].check()
+        ref = orc.minicpm4_forward(oc, ol, fn, x, kcs, vcs, cap, ctx0 + t)
+        assert_stack_close(outs[2], ref, what=f"persistent ctx {ctx0 + t + 1} keys")
+        assert_stack_close(outs[1], ref, what=f"kernels ctx {ctx0 + t + 1} keys")
+    for l in range(L):
+        k2, v2 = kvs[2].download(l)
+        rows = slice(ctx0, ctx0 + steps)
+        for got, want in ((k2, kcs[l]), (v2, vcs[l])):
+            g = orc.fp16_bits_to_fp32(got)[:, rows]
+            w = orc.fp16_bits_to_fp32(want).reshape(got.shape)[:, rows]
+            if l == 0:
+                assert np.array_equal(g[:, 0], w[:, 0])
+            assert np.linalg.norm(g - w) / np.linalg.norm(w) <= 2e-2
+        # rows before ctx0 are untouched
+        assert np.array_equal(k2[:, :ctx0], kcs[l].reshape(k2.shape)[:, :ctx0])
+    for m in models.values():
+        m.free()
+    for kv in kvs.values():
+        kv.free()
+
+
+def test_persistent_long_context_repeatable(vxm_ctx, orc):
+    """The chunk merge adds in chunk order: the same token at 4096 keys twice is
+    bit-identical."""
+    import vxm
+
+    s, rng, c, lws, fn, models, kvs, kcs, vcs = _setup(orc, vxm, vxm_ctx, "tslm", 2, 4200, 4095, 6)
+    x = rng.normal(0, 1, (1, s["H"])).astype(np.float32)
+    outs = []
+    for _ in range(3):
+        xd = _dev(x)
+        models[2].forward(kvs[2], xd, 4095)
+        vxm_ctx.sync()
+        outs.append(xd.cpu().numpy())
+    models[2].check()
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
+    for m in models.values():
+        m.free()
+    for kv in kvs.values():
+        kv.free()
+
+
+@pytest.mark.parametrize("ctx0", [384, 2047, 4095, 8191])
+def test_persistent_long_context_peaked_attention(vxm_ctx, orc, ctx0):
+    """One full-width layer at long context with keys of standard deviation 6: each
+    head's softmax is dominated by a few keys and the attention output is as large as
+    the residual, so the attention, and the merge of its key chunks, shows in the
+    layer output.  The single-launch kernel sums a score's 128 products in another
+    fp32 order than the oracle (parity unpinned), and with outputs this large one ulp
+    can flip a Q8_0 or BF16 rounding that the rest of the layer spreads (a build that
+    never splits the keys gives the same output at 2048 keys), so the bar is the
+    stack bar.  Planted in the oracle on the CPU, an attention that loses its output
+    (V = 0) or weights the chunks past the first wrongly (their V doubled) misses
+    that bar many times over."""
+    import vxm
+    from test_gpu_minicpm4 import layer_stats
+
+    cap, L = 8192, 1
+    print(f"peaked attention ctx0={ctx0}", flush=True)
+    s, rng, c, lws, fn, models, kvs, kcs, vcs = _setup(orc, vxm, vxm_ctx, "tslm", L, cap, ctx0, 91 + ctx0, kscale=6.0)
+    oc, ol = orc_cfg(orc, c), [to_orc(orc, l) for l in lws]
+    x = rng.normal(0, 1, (1, s["H"])).astype(np.float32)
+    xd = _dev(x)
+    models[2].forward(kvs[2], xd, ctx0)
+    vxm_ctx.sync()
+    models[2].check()
+    got = xd.cpu().numpy()
+    k0, v0 = kcs[0].copy(), vcs[0].copy()
+    ref = orc.minicpm4_forward(oc, ol, fn, x, kcs, vcs, cap, ctx0)
+    assert_stack_close(got, ref, what=f"persistent 1 layer, {ctx0 + 1} keys")
+
+    kv_len = ctx0 + 1
+    n = 1 if kv_len <= 384 else min(16, (kv_len + 255) // 256)
+    chl = (kv_len + n - 1) // n
+    v_bad = orc.fp16_bits_to_fp32(v0).reshape(s["nkv"], cap, s["hd"])
+    v_bad[:, chl:ctx0] *= 2.0
+    plants = {"V = 0": np.zeros_like(v0),
+              "V doubled past the first chunk": orc.fp32_to_fp16_bits(v_bad.astype(np.float32)).reshape(-1)}
+    for what, vp in plants.items():
+        bad = orc.minicpm4_forward(oc, ol, fn, x, [k0.copy()], [vp], cap, ctx0)
+        st = layer_stats(got, bad)
+        print(f"planted {what}: {st}")
+        assert st["rel_l2"] >= 0.1, (what, st)   # the stack bar is rel_l2 <= 2e-2
+    for m in models.values():
+        m.free()
+    for kv in kvs.values():
+        kv.free()

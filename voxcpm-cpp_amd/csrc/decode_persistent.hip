@@ -93,7 +93,13 @@ __host__ __device__ constexpr int rep_stride(int words) { return words + kPad; }
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
-enum Phase { PH_X = 0, PH_QKV = 1, PH_ATT = 2, PH_H1 = 3, PH_P = 4 };
+enum Phase { PH_X = 0, PH_QKV = 1, PH_ATT = 2, PH_H1 = 3, PH_P = 4, PH_ATTP = 5 };
+
+// Long contexts split each head's keys over up to kAttSplitMax workgroups
+// (chunks); every chunk publishes its softmax-normalised output with its
+// score max m and exp sum l as kAttpWords tagged words (o[HD], m, l).
+constexpr int kAttSplitMax = 16;
+constexpr int kAttpWords = 132;
 
 template <int H_, int NH_, int NKV_, int HD_, int F_>
 struct Shape {
@@ -127,6 +133,7 @@ struct Shape {
     static_assert(H <= 4 * kThreads && (H & (H - 1)) == 0, "hidden: one norm pass, power of two");
     static_assert(HD == 128 && NH % NKV == 0, "heads: the attention maps one key to a row of 16 lanes");
     static_assert(NH <= kG && QPK * 8 <= kG && NH <= 64, "attention workgroups");
+    static_assert(((NKV * kAttSplitMax - 1) / 8 * QPK + QPK - 1) * 8 + 7 < kG, "attention chunk workgroups");
     // LDS layout, in floats (the int8 quants go last, 16-byte aligned)
     static constexpr int L_XS = 0;                  // layer input x              [H]
     static constexpr int L_H1 = L_XS + H;           // h1                         [H]
@@ -141,7 +148,10 @@ struct Shape {
     static constexpr int XQ_OFF = (L_END * 4 + 15) & ~15;          // int8 quants [KMAX]
     static constexpr int RING_OFF = XQ_OFF + KMAX;                   // 16-byte aligned
     static constexpr int BYTES = RING_OFF + RING_BYTES;
-    static constexpr int MAX_CAP = BIG - 1;                          // scores fit BIG
+    // a chunk's scores fit BIG; the chunk-0 workgroup gathers every chunk's
+    // (o, m, l) in the same space
+    static constexpr int MAX_CAP = kAttSplitMax * BIG - 1;
+    static_assert(kAttSplitMax * (HD + 2) <= BIG && HD + 2 <= kAttpWords, "chunk partials fit the score space");
 };
 
 // workgroup that runs the attention of query head h: the heads of one kv
@@ -149,6 +159,17 @@ struct Shape {
 // XCDs), so the group's K/V rows are shared through that XCD's L2.
 template <class S>
 __device__ __forceinline__ int attn_wg(int h) { return (h % S::QPK) * 8 + h / S::QPK; }
+
+// Workgroup of chunk c of query head h: (kv group g, chunk c) is combination
+// k = c * NKV + g, whose QPK heads share one XCD (x = k % 8) and so read the
+// chunk's K/V rows through one L2; chunk 0 is attn_wg(h).  Injective over
+// h < NH, c < kAttSplitMax: workgroup (sb * QPK + h % QPK) * 8 + x with
+// sb = k / 8.
+template <class S>
+__device__ __forceinline__ int attn_wg_chunk(int h, int c) {
+    const int k = c * S::NKV + h / S::QPK;
+    return ((k / 8) * S::QPK + h % S::QPK) * 8 + k % 8;
+}
 
 __device__ __forceinline__ uint32_t make_tag(uint32_t epoch, int layer, int phase) {
     return (epoch << 12) | ((uint32_t)layer << 3) | (uint32_t)phase;
@@ -312,6 +333,8 @@ struct vxm_pparams {
     uint64_t *attb;    // [QD] attention output (fp32)
     uint64_t *h1b;     // [H/2] BF16 pairs
     uint64_t *pb;      // [F/2] BF16 pairs
+    uint64_t *attp;    // [NH][kAttSplitMax][kAttpWords] chunk partials (fp32), long contexts only
+    int att_split;     // key chunks per head (1: one workgroup per head)
     const int8_t *dummy_q;     // 2 KiB of zeros: loads of units a wave does not own
     const uint16_t *dummy_d;   // 64 zero scales
     int *err;
@@ -709,15 +732,16 @@ __device__ __forceinline__ void ring_refill(const vxm_pparams &p, const UnitBase
 // and publish the 128 fp32 outputs.  The group's first head appends k, v.
 // K or V rows of one attention batch: lane (kin, sub) of wave w loads dims
 // sub*8..+8 of key jb + (k * kWaves + w) * KPW + kin for k < KB; keys at or
-// past pos (the current token comes from LDS) load nothing.
+// past lim (the current token, which comes from LDS, or the chunk's end)
+// load nothing.
 template <int KB, int HD>
-__device__ __forceinline__ void attn_load(const uint16_t *base, int jb, int pos, uint4 (&r)[KB]) {
+__device__ __forceinline__ void attn_load(const uint16_t *base, int jb, int lim, uint4 (&r)[KB]) {
     constexpr int LPK = HD / 8, KPW = 64 / LPK;
     const int tid = tid_now(), wave = tid >> 6, lane = tid & 63, sub = lane % LPK, kin = lane / LPK;
 #pragma unroll
     for (int k = 0; k < KB; k++) {
         const int j = jb + (k * kWaves + wave) * KPW + kin;
-        r[k] = j < pos ? *(const uint4 *)(base + (int64_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
+        r[k] = j < lim ? *(const uint4 *)(base + (int64_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
     }
 }
 
@@ -727,8 +751,17 @@ __device__ __forceinline__ void attn_load(const uint16_t *base, int jb, int pos,
 // batch (up to 320 keys) before wave 0 reads q_h, k_g, v_g: the cache fetch
 // overlaps the QKV exchange.  The current token's k, v come from LDS; the
 // group's first head appends them to the cache.  Output: 128 fp32.
+//
+// With p.att_split = S > 1 (long contexts) this workgroup takes chunk c of
+// the keys, [c CH, (c + 1) CH) with CH = ceil((pos + 1) / S): a softmax
+// within the chunk, its normalised output o_c, max m_c and exp sum l_c.
+// Chunks c > 0 publish (o_c, m_c, l_c); chunk 0 gathers them and combines in
+// chunk order, o = sum_c w_c o_c / sum_c w_c with w_c = l_c exp(m_c - m),
+// m = max_c m_c (the softmax over all keys, regrouped).  With S = 1 this is
+// the unsplit attention, unchanged.
 template <class S>
-__device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int h, float *lds, int *bail) {
+__device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int h, int chunk, float *lds,
+                                                int *bail) {
     constexpr int QD = S::QD, KVD = S::KVD, HD = S::HD;
     constexpr int SQ = rep_stride(S::NQKV / 2), SAT = rep_stride(QD);
     constexpr int LPK = HD / 8, KPW = 64 / LPK;                  // lanes per key, keys per wave
@@ -742,9 +775,12 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     uint16_t *const kc = Ly->kc, *const vc = Ly->vc;
     const uint16_t *kb = kc + (int64_t)g * p.cap * HD;
     const uint16_t *vb = vc + (int64_t)g * p.cap * HD;
+    const int kv_len = pos + 1, nsplit = p.att_split;
+    const int chl = (kv_len + nsplit - 1) / nsplit;
+    const int j0 = chunk * chl, j1 = min(kv_len, j0 + chl), lim = min(j1, pos);
     uint4 kr[KB], vr[KB];
-    attn_load<KB, HD>(kb, 0, pos, kr);
-    attn_load<KB, HD>(vb, 0, pos, vr);
+    attn_load<KB, HD>(kb, j0, lim, kr);
+    attn_load<KB, HD>(vb, j0, lim, vr);
     if (wave == 0) {
         // q_h and k_g (pair-interleaved: word w = dims w, w + HD/2) and v_g
         // (natural pairs) -> aq[0..3HD) in natural order; lane l owns word w = l
@@ -784,7 +820,7 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     VXM_TS(tid_now() == 0, 3);
     const float *qh = aq, *kcur = aq + HD, *vcur = aq + 2 * HD;
     // KV append: the first query head of each group writes the f16 rows at pos
-    if (h % S::QPK == 0) {
+    if (h % S::QPK == 0 && chunk == 0) {
         uint16_t *kw = kc + ((int64_t)g * p.cap + pos) * HD;
         uint16_t *vw = vc + ((int64_t)g * p.cap + pos) * HD;
         for (int d = tid; d < HD; d += kThreads) {
@@ -792,7 +828,6 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
             vw[d] = vxm_f2h(vcur[d]);
         }
     }
-    const int kv_len = pos + 1;
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
     const int sub = lane % LPK, kin = lane / LPK;
     // q_h as f16 pairs: q is BF16-valued (8 mantissa bits), so f16 holds it
@@ -804,8 +839,8 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     for (int i = 0; i < 4; i++) q2[i] = half2_t{(_Float16)qh[sub * 8 + 2 * i], (_Float16)qh[sub * 8 + 2 * i + 1]};
     // scores: batch jb covers keys jb + (k * kWaves + wave) * KPW + kin
     float mx = -INFINITY;
-    for (int jb = 0; jb < kv_len; jb += PERB) {
-        if (jb > 0) attn_load<KB, HD>(kb, jb, pos, kr);
+    for (int jb = j0; jb < j1; jb += PERB) {
+        if (jb > j0) attn_load<KB, HD>(kb, jb, lim, kr);
 #pragma unroll
         for (int k = 0; k < KB; k++) {
             const int j = jb + (k * kWaves + wave) * KPW + kin;
@@ -819,33 +854,33 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
 #pragma unroll
             for (int i = 0; i < 4; i++) pt = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, wv[i]), q2[i], pt, false);
             pt = row16_sum_15(pt);
-            if (j < kv_len && sub == LPK - 1) {
+            if (j < j1 && sub == LPK - 1) {
                 const float s2 = pt * scale;
-                sc[j] = s2;
+                sc[j - j0] = s2;
                 mx = fmaxf(mx, s2);
             }
         }
     }
     mx = wg_max_f(mx, red);
     double sum = 0.0;
-    for (int j = tid; j < kv_len; j += kThreads) {
+    for (int j = tid; j < j1 - j0; j += kThreads) {
         const float e = expf(sc[j] - mx);
         sc[j] = e;
         sum += (double)e;
     }
     sum = wg_sum_d(sum, red);
     const float inv = (float)(1.0 / sum);
-    for (int j = tid; j < kv_len; j += kThreads) sc[j] = sc[j] * inv;
+    for (int j = tid; j < j1 - j0; j += kThreads) sc[j] = sc[j] * inv;
     lds_barrier();
     // out[d] = sum_j p_j v_j[d]: lane (kin, sub) accumulates dims sub*8..+8 over its keys
     float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int jb = 0; jb < kv_len; jb += PERB) {
-        if (jb > 0) attn_load<KB, HD>(vb, jb, pos, vr);
+    for (int jb = j0; jb < j1; jb += PERB) {
+        if (jb > j0) attn_load<KB, HD>(vb, jb, lim, vr);
 #pragma unroll
         for (int k = 0; k < KB; k++) {
             const int j = jb + (k * kWaves + wave) * KPW + kin;
-            if (j >= kv_len) continue;
-            const float pj = sc[j];
+            if (j >= j1) continue;
+            const float pj = sc[j - j0];
             uint32_t wv[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
             if (j == pos) {
 #pragma unroll
@@ -878,15 +913,70 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     lds_barrier();
     const uint32_t tg = make_tag(ep, l, PH_ATT);
     static_assert(kThreads % HD == 0 && kRep % (kThreads / HD) == 0, "attention output replicas");
-    {
-        // thread t owns dim t % HD; the wave partials are summed once, in a
-        // fixed order, and stored to kRep / (kThreads / HD) replicas
-        const int d = tid % HD;
-        float v = 0.0f;
+    // thread t owns dim t % HD; the wave partials are summed once, in a fixed order
+    const int d = tid % HD;
+    float v = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) v += red[w * HD + d];
-        for (int r = tid / HD; r < kRep; r += kThreads / HD) put_word(p.attb + r * SAT + h * HD + d, __float_as_uint(v), tg);
+    for (int w = 0; w < kWaves; w++) v += red[w * HD + d];
+    if (nsplit > 1) {
+        constexpr int CW = HD + 2;   // o[HD], m, l of one chunk in LDS
+        const uint32_t tp = make_tag(ep, l, PH_ATTP);
+        uint64_t *mine = p.attp + ((int64_t)h * kAttSplitMax + chunk) * kAttpWords;
+        if (chunk > 0) {
+            if (tid < HD) put_word(mine + d, __float_as_uint(v), tp);
+            else if (tid == HD) put_word(mine + HD, __float_as_uint(mx), tp);
+            else if (tid == HD + 1) put_word(mine + HD + 1, __float_as_uint((float)sum), tp);
+            VXM_TS(tid_now() == 0, 4);
+            return;
+        }
+        // chunk 0: its own (o, m, l) at sc[0..CW), the other chunks' words to sc[CW c ..]
+        // (the scores are dead: every P.V read of sc precedes the barrier above)
+        if (tid < HD) sc[d] = v;
+        else if (tid == HD) sc[HD] = mx;
+        else if (tid == HD + 1) sc[HD + 1] = (float)sum;
+        const int nw = (nsplit - 1) * CW;
+        constexpr int NPT = cdiv((kAttSplitMax - 1) * CW, kThreads);
+        const uint64_t *base = p.attp + (int64_t)h * kAttSplitMax * kAttpWords;
+        uint32_t pend = 0;
+#pragma unroll
+        for (int k = 0; k < NPT; k++)
+            if (tid + k * kThreads < nw) pend |= 1u << k;
+        int it = 0;
+        while (true) {
+            uint64_t w[NPT];
+#pragma unroll
+            for (int k = 0; k < NPT; k++) {
+                const int i = tid + k * kThreads;
+                if (pend & (1u << k)) w[k] = get_word(base + (int64_t)(1 + i / CW) * kAttpWords + i % CW);
+            }
+#pragma unroll
+            for (int k = 0; k < NPT; k++) {
+                if ((pend & (1u << k)) && (uint32_t)(w[k] >> 32) == tp) {
+                    sc[CW + tid + k * kThreads] = __uint_as_float((uint32_t)w[k]);
+                    pend &= ~(1u << k);
+                }
+            }
+            if (__all(pend == 0)) break;
+            if (give_up(p, it, bail)) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        lds_barrier();
+        if (*bail) return;
+        float m = -INFINITY;
+        for (int c = 0; c < nsplit; c++) m = fmaxf(m, sc[c * CW + HD]);
+        double num = 0.0, den = 0.0;
+        for (int c = 0; c < nsplit; c++) {
+            const double wc = (double)sc[c * CW + HD + 1] * (double)expf(sc[c * CW + HD] - m);
+            den += wc;
+            num += wc * (double)sc[c * CW + d];
+        }
+        v = (float)(num / den);
+        // every wave's reads of the gathered partials end before any wave moves on:
+        // the next phase's input lands in the same LDS
+        lds_barrier();
     }
+    // stored to kRep / (kThreads / HD) replicas
+    for (int r = tid / HD; r < kRep; r += kThreads / HD) put_word(p.attb + r * SAT + h * HD + d, __float_as_uint(v), tg);
     VXM_TS(tid_now() == 0, 4);
 }
 
@@ -911,9 +1001,13 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
     const int pos = p.pos;
     const uint32_t ep = p.epoch;
     // the query head this workgroup attends for, or -1
-    int head = -1;
+    int head = -1, chunk = 0;
     for (int h = 0; h < NH; h++)
-        if (attn_wg<S>(h) == wg) head = h;
+        for (int c = 0; c < p.att_split; c++)
+            if (attn_wg_chunk<S>(h, c) == wg) {
+                head = h;
+                chunk = c;
+            }
 
     // rope cos/sin of this token's position (ggml_rope_ext NEOX angles, host table)
     if (!p.no_rope) {
@@ -988,7 +1082,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         if (!reader) ring_refill<S, S::OA, S::SA>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         // ---------------- B: attention, one workgroup per query head ----------------
         if (head >= 0) {
-            attention_phase<S>(p, l, head, lds, bail);
+            attention_phase<S>(p, l, head, chunk, lds, bail);
             if (*bail) return;
         }
         // ---------------- C: O rows + residual ----------------
@@ -1143,7 +1237,7 @@ using ShapeTslm = Shape<2048, 16, 2, 128, 6144>;
 struct vxm_persistent_state {
     void *base = nullptr;
     vxm_player *layers = nullptr;
-    uint64_t *xb = nullptr, *qkvb = nullptr, *attb = nullptr, *h1b = nullptr, *pb = nullptr;
+    uint64_t *xb = nullptr, *qkvb = nullptr, *attb = nullptr, *h1b = nullptr, *pb = nullptr, *attp = nullptr;
     int8_t *dummy_q = nullptr;
     uint16_t *dummy_d = nullptr;
     int *err = nullptr;
@@ -1177,10 +1271,34 @@ static bool persistent_shape(const vxm_block_dims &d, int n_cu) {
     return false;
 }
 
-// Largest cache capacity whose attention scores fit the LDS.
+// Largest cache capacity: kAttSplitMax key chunks whose scores each fit the LDS.
 int vxm_persistent_max_cap(const vxm_block_dims &d) {
     (void)d;
     return ShapeTslm::MAX_CAP;
+}
+
+// Key chunks per head for kv_len keys.  One workgroup per head up to
+// kAttSplitFrom keys; beyond, about kAttChunk keys per chunk, never more than
+// kAttSplitMax chunks, each at most BIG keys and none empty.  The merge costs
+// one more exchange, which pays once a workgroup's key stream is longer:
+// measured over the 28-layer stack, splitting 256-320 keys in chunks of 64-192
+// took 759-771 us per token against 746 unsplit, while at 512 keys two chunks
+// took 777 us against 851 and at 1024 keys four took 789 against 860.
+#ifndef VXM_ATT_SPLIT_FROM
+#define VXM_ATT_SPLIT_FROM 384
+#endif
+#ifndef VXM_ATT_CHUNK
+#define VXM_ATT_CHUNK 256
+#endif
+constexpr int kAttSplitFrom = VXM_ATT_SPLIT_FROM;
+constexpr int kAttChunk = VXM_ATT_CHUNK;
+template <class S>
+static int att_split_for(int kv_len) {
+    if (kv_len <= kAttSplitFrom) return 1;
+    int n = (kv_len + kAttChunk - 1) / kAttChunk;
+    if (n > kAttSplitMax) n = kAttSplitMax;
+    while (n < kAttSplitMax && (kv_len + n - 1) / n > S::BIG) n++;
+    return n;
 }
 
 bool vxm_persistent_supported(const vxm_minicpm4 *m, const vxm_kv_cache *kv) {
@@ -1212,7 +1330,7 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
         const size_t tab = ((size_t)L * sizeof(vxm_player) + 255) & ~(size_t)255;
         const int nx = rep_stride((int)d.H / 2), nq = rep_stride((int)(qd + 2 * kvd) / 2),
                   na = rep_stride((int)qd), np_ = rep_stride((int)d.F / 2);
-        const size_t words = (size_t)kRep * (2 * nx + nq + na + nx + np_);
+        const size_t words = (size_t)kRep * (2 * nx + nq + na + nx + np_) + (size_t)d.nh * kAttSplitMax * kAttpWords;
         const size_t dummy = kUnit + 256;
         const size_t total = tab + words * 8 + dummy + 256;
         if (hipMalloc(&s.base, total) != hipSuccess) {
@@ -1227,6 +1345,7 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
         s.attb = (uint64_t *)b; b += (size_t)kRep * na * 8;
         s.h1b = (uint64_t *)b; b += (size_t)kRep * nx * 8;
         s.pb = (uint64_t *)b; b += (size_t)kRep * np_ * 8;
+        s.attp = (uint64_t *)b; b += (size_t)d.nh * kAttSplitMax * kAttpWords * 8;
         s.dummy_q = (int8_t *)b; b += kUnit;
         s.dummy_d = (uint16_t *)b; b += 256;
         s.err = (int *)b;
@@ -1261,6 +1380,13 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
     prm.attb = s.attb;
     prm.h1b = s.h1b;
     prm.pb = s.pb;
+    prm.attp = s.attp;
+    prm.att_split = att_split_for<ShapeTslm>(pos + 1);
+    {
+        const int n = prm.att_split, chl = (pos + 1 + n - 1) / n;
+        if (chl > ShapeTslm::BIG || (n - 1) * chl >= pos + 1)
+            return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "persistent decode: %d keys do not split into %d chunks", pos + 1, n);
+    }
     prm.dummy_q = s.dummy_q;
     prm.dummy_d = s.dummy_d;
     prm.err = s.err;
