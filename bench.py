@@ -412,7 +412,7 @@ def lm_update_bytes(ctx_len):
     return step_bytes(ctx_len) + step_bytes(ctx_len, RALM_L) + e["L"] * enc_blk + proj
 
 
-def bench_lm_update(ctx, torch, vxm, tslm_layers, ctx0, steps, warmup):
+def bench_lm_update(ctx, torch, vxm, tslm_layers, ctx0, steps, warmup, prompt_tokens=0):
     """gen_lm_update per generated patch: LocEnc + enc_to_lm, the 28-layer TSLM step, FSQ, the fusion
     projection and the 8-layer RALM step, one stream-ordered call per token."""
     e = ENC
@@ -462,10 +462,27 @@ def bench_lm_update(ctx, torch, vxm, tslm_layers, ctx0, steps, warmup):
     tslm.check()
     ralm.check()
     ok = all(bool(torch.isfinite(o).all().item()) for o in outs)
+    prompt = None
+    if prompt_tokens:
+        # gen_prompt_eval_range: the prompt through the TSLM, the fusion projection and the RALM
+        n = prompt_tokens
+        x0 = torch.from_numpy(vxm.host_randn(35, n * H, 0.0, 1.0).reshape(n, H)).to("cuda:0")
+        x = x0.clone()
+        rh = torch.empty((n, H), dtype=torch.float32, device="cuda:0")
+        u.prompt_prefill(tkv, rkv, x, 0, rh)
+        ctx.sync()
+        pms = 0.0
+        for _ in range(3):
+            x.copy_(x0)
+            torch.cuda.synchronize()
+            t.start()
+            u.prompt_prefill(tkv, rkv, x, 0, rh)
+            pms += t.stop_ms()
+        prompt = (pms * 1000.0 / 3, bool(torch.isfinite(x).all().item() and torch.isfinite(rh).all().item()))
     u.free()
     for o in (enc, tslm, ralm, tkv, rkv):
         o.free()
-    return ms * 1000.0 / steps, ok
+    return ms * 1000.0 / steps, ok, prompt
 
 
 def host_cores():
@@ -681,7 +698,7 @@ def main():
 
     mean_ctx = 256 + (args.steps - 1) / 2.0
     if args.lm_update_only:
-        us_u, fin_u = bench_lm_update(ctx, torch, vxm, layers, 256, args.steps, args.warmup)
+        us_u, fin_u, _ = bench_lm_update(ctx, torch, vxm, layers, 256, args.steps, args.warmup)
         log(f"lm update (LocEnc + TSLM + FSQ + RALM): {us_u:.1f} us/token, finite={fin_u}")
         print(json.dumps({"lm_update": {"us_per_update": round(us_u, 1), "finite": fin_u}}))
         ctx.close()
@@ -693,13 +710,22 @@ def main():
         f"finite={finite}")
     lmu = None
     if not args.decode_only:
-        us_u, fin_u = bench_lm_update(ctx, torch, vxm, layers, 256, args.steps, args.warmup)
+        us_u, fin_u, prm = bench_lm_update(ctx, torch, vxm, layers, 256, args.steps, args.warmup,
+                                           prompt_tokens=args.prefill_tokens)
         ub = lm_update_bytes(mean_ctx)
         lmu = {"us_per_update": round(us_u, 1), "bytes": int(ub), "GBs": round(ub / (us_u * 1e-6) / 1e9, 1),
                "hbm_frac": round(ub / (us_u * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "finite": fin_u,
                "note": f"LocEnc 12 x hidden 1024 on a 4-position patch + 28-layer TSLM step + FSQ 512 + fusion + "
                        f"{RALM_L}-layer RALM step, ctx 256->{256 + args.steps}, one call per token, no host sync"}
         log(f"lm update (LocEnc + TSLM + FSQ + RALM): {us_u:.1f} us/token, {lmu['GBs']} GB/s, finite={fin_u}")
+        if prm:
+            lmu["prompt_prefill"] = {"tokens": args.prefill_tokens, "us": round(prm[0], 1),
+                                     "tokens_per_s": round(args.prefill_tokens / (prm[0] * 1e-6), 1),
+                                     "finite": prm[1],
+                                     "note": "gen_prompt_eval_range: 28-layer TSLM + fusion_concat (4096 -> 2048) + "
+                                             f"{RALM_L}-layer RALM over the prompt, one stream-ordered call"}
+            log(f"prompt prefill ({args.prefill_tokens} tokens, TSLM + fusion + RALM): {prm[0]:.1f} us, "
+                f"finite={prm[1]}")
     ctx.close()
 
     cpu = None

@@ -365,6 +365,26 @@ int vxm_lm_update_step(vxm_lm_update *u, vxm_kv_cache *tslm_kv, vxm_kv_cache *ra
                        const float *prev_patch_dev, int32_t P, int32_t pos, float *audio_embed_dev,
                        float *base_hidden_dev, float *fsq_dev, float *ralm_hidden_dev);
 
+/* gen_prompt_eval_range (src/gen_prompt.c:186-272) for n_tokens text tokens at
+ * sequence positions [pos, pos + n_tokens), on the update's TSLM and RALM:
+ *   base_hidden = TSLM(x), cache rows [pos, pos + n)                 [n][lm_hidden]
+ *   ralm_hidden = RALM(fusion_concat([base_hidden ; 0])), same rows   [n][res_hidden]
+ * The prompt carries no audio features, so the second half of every fusion
+ * input row is zero (src/gen_prompt.c:206-217).  x_dev holds the n token
+ * embeddings (vxm_embed_rows_q8_0) and receives base_hidden in place; the
+ * last rows of the two outputs are the reference's lm_hidden_state and
+ * residual_hidden_state (src/gen_prompt.c:247-270).  Stream-ordered, no host
+ * synchronisation (the reference reads both outputs back after one graph). */
+int vxm_prompt_prefill(vxm_lm_update *u, vxm_kv_cache *tslm_kv, vxm_kv_cache *ralm_kv, float *x_dev,
+                       int32_t n_tokens, int32_t pos, float *ralm_hidden_dev);
+
+/* The text embedding rows of gen_forward_text for a Q8_0 embed_tokens table
+ * (src/gen_prompt.c:106-125): out[i] = dequantized row ids[i] of table (an id
+ * outside [0, rows) reads row 0, src/gen_prompt.c:113-114).  ids_dev: n int32
+ * on the device (the reference indexes token_ids[pos_start + i]: pass the
+ * pointer at pos_start); out_dev: [n][cols] F32. */
+int vxm_embed_rows_q8_0(vxm_ctx *ctx, const vxm_weight *table, const int32_t *ids_dev, int32_t n, float *out_dev);
+
 /* ---- GGUF reader (host only) ----------------------------------------------
  * A read-only, memory-mapped GGUF v2/v3 file: tensor directory, key/value
  * metadata and tensor bytes in place.  Stands in for ggml's

@@ -492,3 +492,32 @@ def lm_update(enc_cfg, enc_w, tslm, ralm, pw, prev_patch, pos, fsq_scale=9.0, va
     ralm_h = minicpm4_forward(ralm["cfg"], ralm["layers"], ralm["norm"], ralm_in[None], ralm["k"], ralm["v"],
                               ralm["cap"], pos)[0]
     return audio, base, fsq, ralm_h
+
+
+def prompt_prefill(tslm, ralm, pw, x, pos, variant=QUANT_X86):
+    """gen_prompt_eval_range (src/gen_prompt.c:186-272) composed from the oracle pieces: the base LM over
+    the n text embeddings x [n][L] at positions [pos, pos + n) (:197-200), the RALM input
+    fusion_concat([base ; 0]) with a zero second half for every prompt row (:204-217), and the RALM over
+    the same positions (:219-223).  tslm / ralm as in lm_update (caches updated in place).
+    Returns (base_hidden [n][L], ralm_hidden [n][R])."""
+    L, R = pw["L"], pw["R"]
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.shape[0]
+    base = minicpm4_forward(tslm["cfg"], tslm["layers"], tslm["norm"], x, tslm["k"], tslm["v"], tslm["cap"], pos)
+    cat = np.concatenate([base, np.zeros((n, L), np.float32)], axis=1)
+    ralm_in = linear(pw["fusion"], cat, R, 2 * L, None, variant)
+    ralm_h = minicpm4_forward(ralm["cfg"], ralm["layers"], ralm["norm"], ralm_in, ralm["k"], ralm["v"],
+                              ralm["cap"], pos)
+    return base, ralm_h
+
+
+def embed_rows_q8_0(table, n_rows, k, ids):
+    """The Q8_0 branch of gen_forward_text's embedding rows (src/gen_prompt.c:106-125): row ids[i] of the
+    GGUF Q8_0 table dequantized; an id outside [0, n_rows) reads row 0 (:113-114)."""
+    ids = np.asarray(ids, np.int64)
+    rb = k // 32 * 34
+    out = np.empty((ids.size, k), np.float32)
+    for i, r in enumerate(ids):
+        r = int(r) if 0 <= r < n_rows else 0
+        out[i] = dequantize_rows(table[r * rb:(r + 1) * rb], 1, k)[0]
+    return out

@@ -151,13 +151,13 @@ def _build_update(vxm, vxm_ctx, orc, seed, with_fsq, dims):
     return (e, eow, eocfg), (tm, tkv, tslm), (rm, rkv, ralm), pw, u
 
 
-def _check_update(orc, vxm_ctx, enc, tsl, ral, pw, u, steps, patch_seed, stack_bar):
+def _check_update(orc, vxm_ctx, enc, tsl, ral, pw, u, steps, patch_seed, stack_bar, pos0=0):
     e, eow, eocfg = enc
     tm, tkv, tslm = tsl
     rm, rkv, ralm = ral
     L, E, R = pw["L"], pw["E"], pw["R"]
     rng = np.random.default_rng(patch_seed)
-    for pos in range(steps):
+    for pos in range(pos0, pos0 + steps):
         patch = rng.normal(0, 1, (4, 64)).astype(np.float32)
         _sync_caches(tkv, tslm)
         _sync_caches(rkv, ralm)
@@ -226,3 +226,85 @@ def test_lm_update_full_width_persistent(vxm_ctx, orc):
     u.free()
     for o in (enc[0], tsl[0], ral[0], tsl[1], ral[1]):
         o.free()
+
+
+def _check_prompt(orc, tsl, ral, pw, u, x, pos, stack_bar, what):
+    """gen_prompt_eval_range on the device, stage by stage: the base LM on x against the oracle's on the
+    device's caches, the RALM on the device's own fusion input of [base ; 0]."""
+    tm, tkv, tslm = tsl
+    rm, rkv, ralm = ral
+    L, R = pw["L"], pw["R"]
+    n = x.shape[0]
+    _sync_caches(tkv, tslm)
+    _sync_caches(rkv, ralm)
+    b, r = u.prompt_prefill(tkv, rkv, _dev(x), pos)
+    b, r = _np(b), _np(r)
+    assert b.shape == (n, L) and r.shape == (n, R)
+    assert tkv.used == pos + n and rkv.used == pos + n
+    b_ref = orc.minicpm4_forward(tslm["cfg"], tslm["layers"], tslm["norm"], x, tslm["k"], tslm["v"], tslm["cap"], pos)
+    stack_bar(b, b_ref, what=f"{what} base_hidden")
+    ralm_in = orc.linear(pw["fusion"], np.concatenate([b, np.zeros_like(b)], axis=1), R, 2 * L)
+    r_ref = orc.minicpm4_forward(ralm["cfg"], ralm["layers"], ralm["norm"], ralm_in, ralm["k"], ralm["v"],
+                                 ralm["cap"], pos)
+    stack_bar(r, r_ref, what=f"{what} ralm_hidden")
+
+
+def test_prompt_prefill_small_then_update(vxm_ctx, orc):
+    """Prompt of 7 tokens in two ranges (gen_prompt_eval_range's pos_start), then two LM updates that
+    attend to the prompt's cache rows."""
+    import vxm
+
+    small = dict(SMALL, sizes=dict(SMALL["sizes"], cap=24))
+    enc, tsl, ral, pw, u = _build_update(vxm, vxm_ctx, orc, 110, True, small)
+    x = np.random.default_rng(111).normal(0, 1, (7, 128)).astype(np.float32)
+
+    def bar(y, ref, what):
+        assert_layer_close(y, ref, what=what)
+
+    _check_prompt(orc, tsl, ral, pw, u, x[:4], 0, bar, "prompt rows 0-3")
+    _check_prompt(orc, tsl, ral, pw, u, x[4:], 4, bar, "prompt rows 4-6")
+    _check_update(orc, vxm_ctx, enc, tsl, ral, pw, u, 2, 112, bar, pos0=7)
+    u.free()
+    for o in (enc[0], tsl[0], ral[0], tsl[1], ral[1]):
+        o.free()
+
+
+@pytest.mark.parametrize("n,chunks", [(40, 1), (96, 1), (160, 2)])
+def test_prompt_prefill_full_width(vxm_ctx, orc, n, chunks):
+    """The prompt prefill at the TSLM / RALM block shape (hidden 2048, 16 / 2 heads x 128, FFN 6144, 2 layers
+    each, RALM without rope; fusion 4096 -> 2048): 40 tokens take the small-M GEMM, 96 and 80 the tiled MFMA
+    GEMM and the MFMA attention."""
+    import vxm
+
+    full = dict(sizes=dict(L=2048, E=1024, Fq=512, R=2048, cap=192,
+                           enc_kw=dict(L=1, nh=16, nkv=2, hd=128, F=4096),
+                           lm_kw=dict(n_layers=2, nh=16, nkv=2, hd=128, F=6144)),
+                tslm=dict(hidden_size=2048, n_layers=2, n_heads=16, n_kv_heads=2, head_dim=128,
+                          intermediate_size=6144, rms_norm_eps=1e-6, rope_theta=10000, no_rope=0),
+                ralm=dict(hidden_size=2048, n_layers=2, n_heads=16, n_kv_heads=2, head_dim=128,
+                          intermediate_size=6144, rms_norm_eps=1e-6, rope_theta=10000, no_rope=1))
+    print(f"prompt prefill full width n={n} chunks={chunks}", flush=True)
+    enc, tsl, ral, pw, u = _build_update(vxm, vxm_ctx, orc, 120 + n, False, full)
+    x = np.random.default_rng(121 + n).normal(0, 1, (n, 2048)).astype(np.float32)
+    step = n // chunks
+    for c in range(chunks):
+        _check_prompt(orc, tsl, ral, pw, u, x[c * step:(c + 1) * step], c * step, assert_stack_close,
+                      f"prompt rows {c * step}-{(c + 1) * step - 1}")
+    u.free()
+    for o in (enc[0], tsl[0], ral[0], tsl[1], ral[1]):
+        o.free()
+
+
+def test_embed_rows_q8_0_bit_exact(vxm_ctx, orc):
+    """Q8_0 text-embedding rows gathered and dequantized on the device equal the oracle's, ids outside
+    the table reading row 0."""
+    import torch
+
+    rng = np.random.default_rng(130)
+    rows, k = 1000, 2048
+    table = orc.quantize_rows(rng.normal(0, 0.05, (rows, k)).astype(np.float32), orc.QUANT_REF)
+    w = vxm_ctx.upload_q8_0(table, rows, k)
+    ids = np.array([5, 999, 0, -3, 1000, 123, 123, 77] + list(rng.integers(0, rows, 56)), np.int32)
+    out = _np(vxm_ctx.embed_rows_q8_0(w, torch.from_numpy(ids).to("cuda:0")))
+    assert np.array_equal(out, orc.embed_rows_q8_0(table, rows, k, ids))
+    w.free()

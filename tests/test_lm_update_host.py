@@ -179,3 +179,73 @@ def test_lm_update_without_fsq_passes_the_hidden(orc):
     patch = np.random.default_rng(31).normal(0, 1, (4, 64)).astype(np.float32)
     audio, base, fsq, rh = orc.lm_update(enc[3], enc[2], tslm, ralm, pw, patch, 0)
     assert np.array_equal(fsq, base)
+
+
+def _fresh_caches(lm):
+    for k in lm["k"] + lm["v"]:
+        k[...] = 0
+
+
+def test_prompt_prefill_structure(orc):
+    """gen_prompt_eval_range's composition: caches are written at rows [pos, pos + n) only; the RALM input
+    is the fusion of [base ; 0] -- the fusion's second-half columns cannot matter, its first half must."""
+    enc, tslm, ralm, pw = make_lm_update(orc, 40, with_fsq=False, cap=24)
+    rng = np.random.default_rng(41)
+    x = rng.normal(0, 1, (6, 128)).astype(np.float32)
+    pos = 3
+    base, rh = orc.prompt_prefill(tslm, ralm, pw, x, pos)
+    assert base.shape == (6, 128) and rh.shape == (6, 128)
+    for lm in (tslm, ralm):
+        for k in lm["k"]:
+            rows = np.nonzero(k.reshape(k.shape[0], k.shape[1], -1).any(axis=(0, 2)))[0] if k.ndim == 3 else \
+                np.nonzero(k.reshape(2, lm["cap"], -1).any(axis=(0, 2)))[0]
+            assert list(rows) == list(range(pos, pos + 6))
+    # the second half of every fusion row (rows of 2L inputs) multiplies zeros
+    R, L = pw["R"], pw["L"]
+    rb = 2 * L // 32 * 34
+    fus = pw["fusion"].reshape(R, rb).copy()
+    fus[:, rb // 2:] = orc.quantize_rows(rng.normal(0, 1, (R, L)).astype(np.float32), orc.QUANT_REF).reshape(R, -1)
+    pw2 = dict(pw, fusion=fus.reshape(-1))
+    for lm in (tslm, ralm):
+        _fresh_caches(lm)
+    base2, rh2 = orc.prompt_prefill(tslm, ralm, pw2, x, pos)
+    assert np.array_equal(base2, base) and np.array_equal(rh2, rh)
+    # ... and the first half does
+    fus3 = pw["fusion"].reshape(R, rb).copy()
+    fus3[:, :rb // 2] = fus[:, rb // 2:]
+    for lm in (tslm, ralm):
+        _fresh_caches(lm)
+    _, rh3 = orc.prompt_prefill(tslm, ralm, dict(pw, fusion=fus3.reshape(-1)), x, pos)
+    assert not np.allclose(rh3, rh, atol=1e-3)
+
+
+def test_prompt_prefill_in_chunks_equals_whole(orc):
+    """A prompt evaluated in two ranges (gen_prompt_eval_range's pos_start) gives the same hidden states
+    and caches as in one: the base LM and the RALM are causal over positions."""
+    enc, tslm, ralm, pw = make_lm_update(orc, 50, with_fsq=False, cap=24)
+    x = np.random.default_rng(51).normal(0, 1, (9, 128)).astype(np.float32)
+    base, rh = orc.prompt_prefill(tslm, ralm, pw, x, 0)
+    caches = [a.copy() for lm in (tslm, ralm) for a in lm["k"] + lm["v"]]
+    for lm in (tslm, ralm):
+        _fresh_caches(lm)
+    b1, r1 = orc.prompt_prefill(tslm, ralm, pw, x[:4], 0)
+    b2, r2 = orc.prompt_prefill(tslm, ralm, pw, x[4:], 4)
+    assert np.array_equal(np.concatenate([b1, b2]), base) and np.array_equal(np.concatenate([r1, r2]), rh)
+    for a, b in zip(caches, [a for lm in (tslm, ralm) for a in lm["k"] + lm["v"]]):
+        assert np.array_equal(a, b)
+
+
+def test_embed_rows_q8_0_closed_form(orc):
+    """The Q8_0 embedding rows: each element is int8 q times the block's fp16 scale, read straight from
+    the 34-byte blocks; ids outside the table read row 0."""
+    rng = np.random.default_rng(60)
+    rows, k = 11, 96
+    table = orc.quantize_rows(rng.normal(0, 0.5, (rows, k)).astype(np.float32), orc.QUANT_REF)
+    ids = np.array([3, 0, 10, -1, 11, 7, 1 << 20], np.int32)
+    got = orc.embed_rows_q8_0(table, rows, k, ids)
+    blocks = table.reshape(rows, k // 32, 34)
+    d = blocks[:, :, :2].copy().view(np.float16)[..., 0].astype(np.float32)
+    q = blocks[:, :, 2:].view(np.int8).astype(np.float32)
+    full = (q * d[:, :, None]).reshape(rows, k)
+    want = full[[3, 0, 10, 0, 0, 7, 0]]
+    assert np.array_equal(got, want)

@@ -47,6 +47,9 @@ struct vxm_lm_update {
     float *fh = nullptr;     // raw fsq.in_proj output [fsq_dim]
     int8_t *aq = nullptr;    // Q8_0 of the widest input (2 lm_hidden)
     uint16_t *ad = nullptr;
+    // prompt prefill: [n][2 lm_hidden] fusion input and its Q8_0, grown on demand
+    void *pbuf = nullptr;
+    size_t pbytes = 0;
 };
 
 // ---------------------------------------------------------------------------
@@ -92,6 +95,31 @@ __global__ void k_fsq(const float *__restrict__ x, const float *__restrict__ b, 
     if (b) v = v + b[i];
     if (s > 0.0f) v = roundf(tanhf(v) * s) * inv_s;
     y[i] = v;
+}
+
+// Prompt fusion input (src/gen_prompt.c:206-217): row i = [base_hidden[i] ;
+// zeros] -- the prompt carries no audio features.
+__global__ void k_prompt_fusion_in(const float *__restrict__ base, float *__restrict__ cat, int n, int H) {
+    const int row = blockIdx.x;
+    if (row >= n) return;
+    const float *src = base + (int64_t)row * H;
+    float *dst = cat + (int64_t)row * 2 * H;
+    for (int i = threadIdx.x; i < 2 * H; i += blockDim.x) dst[i] = i < H ? src[i] : 0.0f;
+}
+
+// Q8_0 embedding rows (the Q8_0 branch of gen_forward_text, src/gen_prompt.c:
+// 106-125): out[i][j] = (float)qs[j] * fp16(d[j/32]) of row ids[i]; an id outside
+// [0, n_rows) takes row 0 (src/gen_prompt.c:113-114).
+__global__ void k_embed_rows_q8_0(const int8_t *__restrict__ qs, const uint16_t *__restrict__ d,
+                                  const int32_t *__restrict__ ids, int64_t n_rows, int64_t k,
+                                  float *__restrict__ out) {
+    const int i = blockIdx.x;
+    int64_t r = ids[i];
+    if (r < 0 || r >= n_rows) r = 0;
+    const int8_t *q = qs + r * k;
+    const uint16_t *dr = d + r * (k / 32);
+    float *o = out + (int64_t)i * k;
+    for (int64_t j = threadIdx.x; j < k; j += blockDim.x) o[j] = (float)q[j] * vxm_h2f(dr[j / 32]);
 }
 
 static unsigned grid_of(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -253,6 +281,7 @@ extern "C" int vxm_lm_update_free(vxm_lm_update *u) {
     for (float *p : {u->enc_to_lm_bias, u->fsq_in_bias, u->fsq_out_bias})
         if (p) (void)hipFree(p);
     if (u->buf) (void)hipFree(u->buf);
+    if (u->pbuf) (void)hipFree(u->pbuf);
     delete u;
     return VXM_OK;
 }
@@ -359,4 +388,56 @@ extern "C" int vxm_lm_update_step(vxm_lm_update *u, vxm_kv_cache *tslm_kv, vxm_k
     if ((rc = vxm_launch_quantize(ctx, u->cat, 1, 2 * L, var, u->aq, u->ad))) return rc;
     if ((rc = vxm_launch_mul_mat(ctx, u->fusion, u->aq, u->ad, 1, ralm_hidden_dev))) return rc;
     return vxm_minicpm4_forward(u->ralm, ralm_kv, ralm_hidden_dev, 1, pos);
+}
+
+// ---------------------------------------------------------------------------
+// prompt prefill and the embedding rows
+// ---------------------------------------------------------------------------
+extern "C" int vxm_embed_rows_q8_0(vxm_ctx *ctx, const vxm_weight *table, const int32_t *ids_dev, int32_t n,
+                                   float *out_dev) {
+    if (!ctx) return VXM_ERR_INVALID_ARG;
+    if (!table || (n > 0 && (!ids_dev || !out_dev)) || n < 0)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "embed_rows: bad table / ids / out / n");
+    if (n == 0) return VXM_OK;
+    hipLaunchKernelGGL(k_embed_rows_q8_0, dim3((unsigned)n), dim3(256), 0, ctx->stream, table->qs, table->d, ids_dev,
+                       table->n, table->k, out_dev);
+    VXM_CHECK_LAUNCH(ctx);
+    return VXM_OK;
+}
+
+extern "C" int vxm_prompt_prefill(vxm_lm_update *u, vxm_kv_cache *tslm_kv, vxm_kv_cache *ralm_kv, float *x_dev,
+                                  int32_t n_tokens, int32_t pos, float *ralm_hidden_dev) {
+    if (!u) return VXM_ERR_INVALID_ARG;
+    vxm_ctx *ctx = u->ctx;
+    if (!x_dev || !ralm_hidden_dev || !tslm_kv || !ralm_kv || pos < 0 || n_tokens < 0)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "prompt_prefill: bad x / outputs / caches / pos / n_tokens");
+    if (n_tokens == 0) return VXM_OK;
+    const int64_t L = u->cfg.lm_hidden, n = n_tokens;
+    const int var = ctx->quant_variant;
+    int rc;
+    // base LM over the n text tokens, in place (src/gen_prompt.c:197-200)
+    if ((rc = vxm_minicpm4_forward(u->tslm, tslm_kv, x_dev, n, pos))) return rc;
+    // RALM input = fusion_concat_proj([base_hidden ; 0]) (src/gen_prompt.c:204-217)
+    const size_t cat_b = ((size_t)n * 2 * L * 4 + 255) & ~(size_t)255, q_b = ((size_t)n * 2 * L + 255) & ~(size_t)255,
+                 d_b = (size_t)n * (2 * L / 32) * 2;
+    if (u->pbytes < cat_b + q_b + d_b) {
+        VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (u->pbuf) VXM_HIP(ctx, hipFree(u->pbuf));
+        u->pbuf = nullptr;
+        u->pbytes = 0;
+        if (hipMalloc(&u->pbuf, cat_b + q_b + d_b) != hipSuccess) {
+            (void)hipGetLastError();
+            return vxm_fail(ctx, VXM_ERR_OOM, "prompt_prefill: %zu bytes of fusion buffers", cat_b + q_b + d_b);
+        }
+        u->pbytes = cat_b + q_b + d_b;
+    }
+    float *cat = (float *)u->pbuf;
+    int8_t *cq = (int8_t *)((char *)u->pbuf + cat_b);
+    uint16_t *cd = (uint16_t *)((char *)u->pbuf + cat_b + q_b);
+    hipLaunchKernelGGL(k_prompt_fusion_in, dim3((unsigned)n), dim3(256), 0, ctx->stream, x_dev, cat, (int)n, (int)L);
+    VXM_CHECK_LAUNCH(ctx);
+    if ((rc = vxm_launch_quantize(ctx, cat, n, 2 * L, var, cq, cd))) return rc;
+    if ((rc = vxm_launch_mul_mat(ctx, u->fusion, cq, cd, n, ralm_hidden_dev))) return rc;
+    // RALM over the same positions (src/gen_prompt.c:219-223)
+    return vxm_minicpm4_forward(u->ralm, ralm_kv, ralm_hidden_dev, n, pos);
 }

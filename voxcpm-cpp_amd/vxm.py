@@ -108,6 +108,8 @@ _SIGS = {
     "vxm_lm_update_create": (_I, [_P, _P, _P, _P, _P, _P, C.POINTER(_P)]),
     "vxm_lm_update_free": (_I, [_P]),
     "vxm_lm_update_step": (_I, [_P, _P, _P, _P, C.c_int32, C.c_int32, _P, _P, _P, _P]),
+    "vxm_prompt_prefill": (_I, [_P, _P, _P, _P, C.c_int32, C.c_int32, _P]),
+    "vxm_embed_rows_q8_0": (_I, [_P, _P, _P, C.c_int32, _P]),
     "vxm_gguf_open": (_I, [C.c_char_p, C.POINTER(_P), C.c_char_p, C.c_size_t]),
     "vxm_gguf_close": (_I, [_P]),
     "vxm_gguf_last_error": (C.c_char_p, [_P]),
@@ -270,6 +272,15 @@ class Context:
         sink = torch.zeros(max(words, 1), dtype=torch.int32, device=f"cuda:{self.device}")
         self.check(lib().vxm_stream_read(self.h, n, ptrs, sizes, _ptr(sink)))
         return sink
+
+    def embed_rows_q8_0(self, table, ids, out=None):
+        """Dequantized Q8_0 rows ids (int32 device tensor) of table -> [n][cols] F32."""
+        import torch
+
+        n = ids.shape[0]
+        out = torch.empty((n, table.k), dtype=torch.float32, device=ids.device) if out is None else out
+        self.check(lib().vxm_embed_rows_q8_0(self.h, table.h, _ptr(ids), n, _ptr(out)))
+        return out
 
     def mul_mat_q8(self, w, xq, xd, y=None):
         import torch
@@ -743,6 +754,17 @@ class LMUpdate:
                                                 pos, _ptr(audio_embed), _ptr(base_hidden), _ptr(fsq),
                                                 _ptr(ralm_hidden)))
         return audio_embed, base_hidden, fsq, ralm_hidden
+
+    def prompt_prefill(self, tslm_kv, ralm_kv, x, pos, ralm_hidden=None):
+        """gen_prompt_eval_range: x [n][lm_hidden] text embeddings (device) -> base_hidden in place;
+        returns (x, ralm_hidden [n][res_hidden])."""
+        import torch
+
+        n = x.shape[0]
+        if ralm_hidden is None:
+            ralm_hidden = torch.empty((n, self.cfg["res_hidden"]), dtype=torch.float32, device=x.device)
+        self.ctx.check(lib().vxm_prompt_prefill(self.h, tslm_kv.h, ralm_kv.h, _ptr(x), n, pos, _ptr(ralm_hidden)))
+        return x, ralm_hidden
 
     def free(self):
         if self.h:
