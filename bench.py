@@ -329,12 +329,15 @@ def bench_prefill(ctx, torch, vxm, layers, n_layers, M, reps):
     return ms * 1000.0 / reps, ok
 
 
-DIT = dict(H=1024, L=12, NH=16, HD=64, F=4096, FEAT=64, P=4, PC=17)
+DIT = dict(H=1024, L=12, NH=16, NKV=16, HD=64, F=4096, FEAT=64, P=4, PC=17)
+# the reference's own LocDiT (src/gen_init.c:280-283,424-441): 16 query / 2 KV heads of 128, and per CFG
+# branch mu (2) + t (1) + the previous patch as cond (4) + the latent patch (4) = 11 rows
+DIT_REF = dict(H=1024, L=12, NH=16, NKV=2, HD=128, F=4096, FEAT=64, P=4, PC=4)
 
 
-def make_locdit(vxm, seed):
-    """Seeded synthetic LocDiT (hidden 1024, 12 blocks, 16 x 64 MHA, FFN 4096), Q8_0 N(0, 0.02)."""
-    H, F, FEAT, NHD = DIT["H"], DIT["F"], DIT["FEAT"], DIT["NH"] * DIT["HD"]
+def make_locdit(vxm, seed, d=DIT):
+    """Seeded synthetic LocDiT (hidden 1024, 12 blocks, FFN 4096, the heads of d), Q8_0 N(0, 0.02)."""
+    H, F, FEAT, NHD, KVD = d["H"], d["F"], d["FEAT"], d["NH"] * d["HD"], d["NKV"] * d["HD"]
     off = [0]
 
     def q8(n, k):
@@ -347,30 +350,32 @@ def make_locdit(vxm, seed):
         off[0] += n
         return v
 
-    layers = [dict(q_proj=q8(NHD, H), k_proj=q8(NHD, H), v_proj=q8(NHD, H), o_proj=q8(H, NHD),
+    layers = [dict(q_proj=q8(NHD, H), k_proj=q8(KVD, H), v_proj=q8(KVD, H), o_proj=q8(H, NHD),
                    gate_proj=q8(F, H), up_proj=q8(F, H), down_proj=q8(H, F), input_layernorm=vec(H, 1.0),
-                   post_attention_layernorm=vec(H, 1.0)) for _ in range(DIT["L"])]
+                   post_attention_layernorm=vec(H, 1.0)) for _ in range(d["L"])]
     w = dict(layers=layers, in_proj=q8(H, FEAT), in_bias=vec(H), cond_proj=q8(H, FEAT), cond_bias=vec(H),
              out_proj=q8(FEAT, H), out_bias=vec(FEAT), norm=vec(H, 1.0), t_w1=q8(H, H), t_w2=q8(H, H),
              dt_w1=q8(H, H), dt_w2=q8(H, H), t_b1=vec(H), t_b2=vec(H), dt_b1=vec(H), dt_b2=vec(H))
-    cfg = dict(hidden_size=H, n_layers=DIT["L"], n_heads=DIT["NH"], n_kv_heads=DIT["NH"], head_dim=DIT["HD"],
+    cfg = dict(hidden_size=H, n_layers=d["L"], n_heads=d["NH"], n_kv_heads=d["NKV"], head_dim=d["HD"],
                intermediate_size=F, feat_dim=FEAT, cond_dim=FEAT, rms_norm_eps=1e-6, rope_theta=10000)
     return cfg, w
 
 
-def locdit_eval_bytes():
+def locdit_eval_bytes(d=DIT):
     """Q8_0 bytes of one LocDiT evaluation: 12 blocks + in/out/cond projections."""
-    H, F, FEAT, NHD = DIT["H"], DIT["F"], DIT["FEAT"], DIT["NH"] * DIT["HD"]
-    blk = q8_bytes(3 * NHD, H) + q8_bytes(H, NHD) + 2 * q8_bytes(F, H) + q8_bytes(H, F)
-    return DIT["L"] * blk + 2 * q8_bytes(H, FEAT) + q8_bytes(FEAT, H)
+    H, F, FEAT, NHD, KVD = d["H"], d["F"], d["FEAT"], d["NH"] * d["HD"], d["NKV"] * d["HD"]
+    blk = q8_bytes(NHD + 2 * KVD, H) + q8_bytes(H, NHD) + 2 * q8_bytes(F, H) + q8_bytes(H, F)
+    return d["L"] * blk + 2 * q8_bytes(H, FEAT) + q8_bytes(FEAT, H)
 
 
-def bench_cfm(ctx, torch, vxm, reps, n_steps=10):
-    """CFM solves: n_steps uniform Euler steps, CFG 2.0 with CFG-Zero* (both branches in one
-    batch of 2 x 24 rows per LocDiT evaluation), latent 4 x 64, 17 cond tokens."""
-    cfg, w = make_locdit(vxm, 21)
+def bench_cfm(ctx, torch, vxm, reps, n_steps=10, d=DIT, schedule=None):
+    """CFM solves: n_steps Euler steps (uniform unless schedule says otherwise), CFG 2.0 with CFG-Zero*
+    (both branches in one batch of 2 x (3 + PC + P) rows per LocDiT evaluation), latent P x 64, PC cond
+    tokens."""
+    cfg, w = make_locdit(vxm, 21, d)
     m = vxm.LocDiT(ctx, cfg, w)
-    P, PC, H, FEAT = DIT["P"], DIT["PC"], DIT["H"], DIT["FEAT"]
+    P, PC, H, FEAT = d["P"], d["PC"], d["H"], d["FEAT"]
+    schedule = vxm.CFM_UNIFORM if schedule is None else schedule
     x0 = torch.from_numpy(vxm.host_randn(22, P * FEAT).reshape(P, FEAT)).to("cuda:0")
     cond = torch.from_numpy(vxm.host_randn(23, PC * FEAT).reshape(PC, FEAT)).to("cuda:0")
     mu = torch.from_numpy(vxm.host_randn(24, 2 * H).reshape(2, H)).to("cuda:0")
@@ -378,7 +383,7 @@ def bench_cfm(ctx, torch, vxm, reps, n_steps=10):
     # two untimed solves: the first runs eagerly, the second records the Euler loop as a graph
     for _ in range(2):
         x.copy_(x0)
-        m.cfm_solve(x, cond, mu, n_steps, 2.0, vxm.CFM_UNIFORM, True)
+        m.cfm_solve(x, cond, mu, n_steps, 2.0, schedule, True)
     ctx.sync()
     t = Timer(torch, ctx)
     ms = 0.0
@@ -386,7 +391,7 @@ def bench_cfm(ctx, torch, vxm, reps, n_steps=10):
         x.copy_(x0)
         torch.cuda.synchronize()
         t.start()
-        m.cfm_solve(x, cond, mu, n_steps, 2.0, vxm.CFM_UNIFORM, True)
+        m.cfm_solve(x, cond, mu, n_steps, 2.0, schedule, True)
         ms += t.stop_ms()
     ok = bool(torch.isfinite(x).all().item())
     m.free()
@@ -603,6 +608,17 @@ def main():
                        "(M = 2 x 24); weights 214 MB per evaluation, Infinity-Cache resident"}
         log(f"cfm solve: {us_cfm:.1f} us for {evals} evaluations ({us_cfm / evals:.1f} us each), "
             f"{cfm['weight_GBs']} GB/s of weights, finite={fin}")
+        us_r, evals_r, fin_r = bench_cfm(ctx, torch, vxm, 5, 10, DIT_REF, vxm.CFM_SWAY)
+        ebr = locdit_eval_bytes(DIT_REF)
+        rows_r = 2 * (3 + DIT_REF["PC"] + DIT_REF["P"])
+        cfm["reference_shape"] = {
+            "us_per_solve": round(us_r, 1), "evals": evals_r, "us_per_eval": round(us_r / evals_r, 1),
+            "weight_GBs": round(evals_r * ebr / (us_r * 1e-6) / 1e9, 1),
+            "int8_TOPs": round(evals_r * 2 * rows_r * (ebr * 32 // 34) / (us_r * 1e-6) / 1e12, 2), "finite": fin_r,
+            "note": "the reference's LocDiT: 16 q / 2 kv heads x 128, 2 x 11 rows, 10 sway steps, CFG 2.0 + "
+                    f"CFG-Zero*; weights {ebr / 1e6:.0f} MB per evaluation"}
+        log(f"cfm solve, reference shape: {us_r:.1f} us for {evals_r} evaluations ({us_r / evals_r:.1f} us each), "
+            f"finite={fin_r}")
         if args.cfm_only:
             print(json.dumps({"cfm": cfm}))
             ctx.close()

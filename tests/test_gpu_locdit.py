@@ -286,3 +286,83 @@ def test_locdit_rejects_bad_sizes(vxm_ctx, orc):
     with pytest.raises(vxm.VxmError):
         m.cfm_solve(_dev(np.zeros((2, 64), np.float32)), None, None, 4, 2.0, 7, True)
     m.free()
+
+
+# The reference's own LocDiT (src/gen_init.c:280-283,424-441; src/gen_step.c:442-649): hidden 1024,
+# 12 layers, 16 query heads and 2 KV heads of 128 (LongRoPE short factors), FFN 4 x hidden; per CFG
+# branch mu (2 rows) + t (1) + the previous patch as cond (4) + the latent patch (4) = 11 rows; 10 sway
+# steps with CFG-Zero* at CFG 2.0.
+REF = dict(H=1024, L=12, nh=16, nkv=2, hd=128, F=4096, feat=64)
+
+
+def test_locdit_reference_shape_forward(vxm_ctx, orc):
+    """Every block of the reference-shape LocDiT (GQA 16 / 2 x 128, 11 rows per branch) meets the block
+    sensitivity bar against the oracle's input to it; the velocity meets the gross bar."""
+    import vxm
+
+    keep = {}
+    m, ow, ocfg = _model(vxm_ctx, orc, 71, **REF, keep=keep)
+    x, cond, mu = make_inputs(72, 4, 4, 64, 1024)
+    v = m.forward(_dev(x), _dev(cond), 0.6, 0.0, _dev(mu)).cpu().numpy()
+    ref, states = orc.locdit_states(ocfg, ow, x, cond, 0.6, 0.0, mu)
+    assert states[0].shape[0] == 11
+    c = keep["cfg"]
+    blocks = vxm.MiniCPM4(vxm_ctx, dict(hidden_size=1024, n_layers=12, n_heads=16, n_kv_heads=2, head_dim=128,
+                                        intermediate_size=4096, rms_norm_eps=1e-6, rope_theta=10000),
+                          keep["w"]["layers"])
+    for l in range(c["n_layers"]):
+        h = _dev(states[l])
+        blocks.block(None, l, h, 0, 1)
+        assert_sensitivity_close(h.cpu().numpy(), states[l + 1], what=f"reference locdit block {l}")
+    blocks.free()
+    rel = np.linalg.norm(v.astype(np.float64) - ref) / np.linalg.norm(ref)
+    print(f"reference-shape velocity rel_l2 {rel:.3e}")
+    assert np.isfinite(v).all() and rel < 5e-2
+    m.free()
+
+
+@pytest.mark.parametrize("path", ["auto", "tiled"])
+def test_cfm_reference_shape_one_block_sway(vxm_ctx, orc, path):
+    """The reference's solve at full width with one block: 10 sway steps, CFG 2.0, CFG-Zero* (its zero
+    first step), both branches of 11 rows in one batch, against the oracle's loop."""
+    import vxm
+
+    m, ow, ocfg = _model(vxm_ctx, orc, 73, **dict(REF, L=1))
+    x0, cond, mu = make_inputs(74, 4, 4, 64, 1024)
+    x = _dev(x0)
+    code = {"auto": vxm.PATH_AUTO, "tiled": vxm.PATH_MFMA_TILED}[path]
+    try:
+        vxm_ctx.set_path(code)
+        m.cfm_solve(x, _dev(cond), _dev(mu), 10, 2.0, vxm.CFM_SWAY, True)
+        vxm_ctx.sync()
+    finally:
+        vxm_ctx.set_path(vxm.PATH_AUTO)
+    assert_trajectory_close(x.cpu().numpy(), orc.cfm_solve(ocfg, ow, x0, cond, mu, 10, 2.0, 0, 1),
+                            what=f"reference cfm L=1 sway 10 steps ({path})")
+    m.free()
+
+
+def test_cfm_reference_shape_full_depth(vxm_ctx, orc):
+    """The 12-block reference solve: its first non-zero step (sway, CFG-Zero*) within the deep-stack gross
+    bar, and the full 10-step solve finite, moved and bit-identical across runs (eager then graph replays)."""
+    import torch
+    import vxm
+
+    m, ow, ocfg = _model(vxm_ctx, orc, 75, **REF)
+    x0, cond, mu = make_inputs(76, 4, 4, 64, 1024)
+    cd, md = _dev(cond), _dev(mu)
+    x = _dev(x0)
+    m.cfm_solve(x, cd, md, 2, 2.0, vxm.CFM_SWAY, True)
+    ref = orc.cfm_solve(ocfg, ow, x0, cond, mu, 2, 2.0, 0, 1)
+    rel = np.linalg.norm(x.cpu().numpy().astype(np.float64) - ref) / np.linalg.norm(ref)
+    print(f"reference cfm 12 blocks, 2 sway steps: rel_l2 {rel:.3e}")
+    assert rel < 1e-1
+    outs = []
+    for _ in range(3):
+        x = _dev(x0)
+        m.cfm_solve(x, cd, md, 10, 2.0, vxm.CFM_SWAY, True)
+        torch.cuda.synchronize()
+        outs.append(x.cpu().numpy())
+    assert np.isfinite(outs[0]).all() and not np.array_equal(outs[0], x0)
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
+    m.free()
