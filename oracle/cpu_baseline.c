@@ -17,6 +17,7 @@
 #include <string.h>
 
 #define ORC_MUL_MAT_HOOK 1
+#define ORC_ATTN_PAR_MIN 1
 #include "vxm_oracle.c"
 
 static int g_threads = 1;
@@ -110,12 +111,53 @@ static void cb_mul_mat_f32_in(const uint8_t *w, const float *x, int64_t N, int64
     free(xq);
 }
 
+/* One query head's attention over an f16 cache as ggml-cpu computes it with
+ * F16C + FMA: f16 keys widened 8 at a time for the scores, the softmax of
+ * ggml_soft_max_ext (max, expf, a double sum), then P.V accumulated row by row
+ * over the f16 values.  hd % 8 == 0. */
+__attribute__((target("avx2,fma,f16c")))
+static void attend_one_f16c(const float *q, const uint16_t *k, const uint16_t *v, int64_t kv_len, int64_t hd,
+                            int64_t stride, float *out, float *scratch) {
+    const float sc = 1.0f / sqrtf((float)hd);
+    float mx = -INFINITY;
+    for (int64_t j = 0; j < kv_len; j++) {
+        __m256 acc = _mm256_setzero_ps();
+        for (int64_t d = 0; d < hd; d += 8) {
+            const __m256 kf = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(k + j * stride + d)));
+            acc = _mm256_fmadd_ps(kf, _mm256_loadu_ps(q + d), acc);
+        }
+        __m128 lo = _mm_add_ps(_mm256_castps256_ps128(acc), _mm256_extractf128_ps(acc, 1));
+        lo = _mm_add_ps(lo, _mm_movehl_ps(lo, lo));
+        lo = _mm_add_ss(lo, _mm_movehdup_ps(lo));
+        const float s = _mm_cvtss_f32(lo) * sc;
+        scratch[j] = s;
+        if (s > mx) mx = s;
+    }
+    double sum = 0.0;
+    for (int64_t j = 0; j < kv_len; j++) {
+        const float e = expf(scratch[j] - mx);
+        scratch[j] = e;
+        sum += (double)e;
+    }
+    const float inv = (float)(1.0 / sum);
+    for (int64_t d = 0; d < hd; d++) out[d] = 0.0f;
+    for (int64_t j = 0; j < kv_len; j++) {
+        const __m256 p = _mm256_set1_ps(scratch[j] * inv);
+        for (int64_t d = 0; d < hd; d += 8) {
+            const __m256 vf = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(v + j * stride + d)));
+            _mm256_storeu_ps(out + d, _mm256_fmadd_ps(p, vf, _mm256_loadu_ps(out + d)));
+        }
+    }
+}
+
 int cb_minicpm4_forward(const orc_cfg *cfg, const orc_layer *layers, int32_t n_layers,
                         const float *final_norm, float *x, int64_t M, uint16_t **k_caches,
                         uint16_t **v_caches, int64_t capacity, int32_t pos) {
     g_mul_mat_hook = cb_mul_mat_f32_in;
+    if (cfg->head_dim % 8 == 0) g_attend_hook = attend_one_f16c;
     int rc = orc_minicpm4_forward(cfg, layers, n_layers, final_norm, x, M, k_caches, v_caches,
                                   capacity, pos);
     g_mul_mat_hook = NULL;
+    g_attend_hook = NULL;
     return rc;
 }

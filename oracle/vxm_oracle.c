@@ -224,10 +224,17 @@ void orc_mul_mat_q8_0_f64(const uint8_t *w, const uint8_t *xq, int64_t N, int64_
 }
 
 /* When this file is included by the timed CPU baseline, the baseline swaps in
- * its SIMD mul_mat through this pointer; the oracle build leaves it NULL. */
+ * its SIMD mul_mat and attention through these pointers and threads the
+ * attention heads of a single token; the oracle build leaves the pointers NULL
+ * and threads only multi-token attention (its results do not depend on it). */
 #ifdef ORC_MUL_MAT_HOOK
 static void (*g_mul_mat_hook)(const uint8_t *, const float *, int64_t, int64_t, int64_t, float *,
                               int) = NULL;
+static void (*g_attend_hook)(const float *, const uint16_t *, const uint16_t *, int64_t, int64_t, int64_t,
+                             float *, float *) = NULL;
+#endif
+#ifndef ORC_ATTN_PAR_MIN
+#define ORC_ATTN_PAR_MIN 16
 #endif
 
 /* ggml_mul_mat(W_q8_0, x_f32): quantize each x row (activation variant), then
@@ -391,7 +398,7 @@ int orc_attention(const orc_cfg *cfg, const orc_layer *w, const float *xn, int64
                 vc[(hh * kvcap + base + t) * hd + d] = orc_fp32_to_fp16(v[t * kvd + hh * hd + d]);
             }
     /* every (token, head) output is formed by one thread with its own scores */
-#pragma omp parallel if (M * nh > 16)
+#pragma omp parallel if (M * nh > ORC_ATTN_PAR_MIN)
     {
         float *sc = (float *)malloc(sizeof(float) * (size_t)(kvcap + 1));
 #pragma omp for collapse(2) schedule(dynamic, 4)
@@ -399,6 +406,13 @@ int orc_attention(const orc_cfg *cfg, const orc_layer *w, const float *xn, int64
             for (int64_t h = 0; h < nh; h++) {
                 const int64_t kv_len = no_causal ? M : pos + t + 1;
                 const int64_t gi = h / qpk;
+#ifdef ORC_MUL_MAT_HOOK
+                if (g_attend_hook) {
+                    g_attend_hook(q + t * qd + h * hd, kc + gi * kvcap * hd, vc + gi * kvcap * hd, kv_len, hd, hd,
+                                  att + t * qd + h * hd, sc);
+                    continue;
+                }
+#endif
                 attend_one(q + t * qd + h * hd, kc + gi * kvcap * hd, vc + gi * kvcap * hd, kv_len, hd,
                            hd, att + t * qd + h * hd, sc);
             }
