@@ -29,7 +29,7 @@
 // a unit's dot product is 8 sdot4 per lane and one wave sum.  The partials of
 // a row are added in unit order from LDS.
 //
-// Weight streaming.  Wave 0 only reads the phase inputs; waves 1..7 stream
+// Weight streaming.  Wave 0 issues no weight loads; waves 1..7 stream
 // weights with direct-to-LDS loads (global_load_lds_dwordx4) into a ring of
 // RING unit slots per wave, with a fixed lookahead of P units: after
 // consuming the unit at stream position j the wave issues the loads of
@@ -77,6 +77,29 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 namespace {
 
 constexpr int kWaves = 8;              // waves per workgroup: 1 reader + 7 compute
+// Waves that read each exchanged input: x (phase A), the attention output
+// (phase C), h1 (phase D) and p (phase E).  An exchange read is a round of
+// agent-scope loads whose cost is their issue and their trip to the memory
+// side, so spreading a round over more waves shortens it, even over compute
+// waves whose own refill loads are still in flight (their loads retire in
+// issue order).  Measured over the 28-layer decode (us per token): x / att /
+// h1 / p read by 2 / 2 / 1 / 4 waves 741-748; p by 1 wave 832; everything by
+// wave 0 alone 863; 8 / 8 / 1 / 8 waves 722; 8 / 8 / 4 / 8 692; 8 / 8 / 8 / 8 694;
+// 4 / 8 / 4 / 8 707; 8 / 4 / 4 / 8 698; 8 / 8 / 4 / 6 706.
+#ifndef VXM_X_READERS
+#define VXM_X_READERS 8
+#endif
+#ifndef VXM_ATT_READERS
+#define VXM_ATT_READERS 8
+#endif
+#ifndef VXM_P_READERS
+#define VXM_P_READERS 8
+#endif
+#ifndef VXM_H1_READERS
+#define VXM_H1_READERS 4
+#endif
+constexpr int kXReaders = VXM_X_READERS, kAttReaders = VXM_ATT_READERS, kPReaders = VXM_P_READERS;
+constexpr int kH1Readers = VXM_H1_READERS;
 constexpr int kCW = kWaves - 1;
 constexpr int kThreads = kWaves * 64;
 constexpr int kG = 256;                // workgroups: one per CU
@@ -980,10 +1003,10 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     VXM_TS(tid_now() == 0, 4);
 }
 
-// The whole decode.  Wave 0 reads the inputs of each phase (and forms
-// RMSNorm's sum of squares on the way); waves 1..7 stream weights and
-// publish the outputs.  All waves walk the same phase schedule and barrier
-// sequence.
+// The whole decode.  The inputs of each phase are read by the waves named by
+// k*Readers (each forming its share of RMSNorm's sum of squares on the way);
+// waves 1..7 also stream weights and publish the outputs.  All waves walk
+// the same phase schedule and barrier sequence.
 template <class S>
 __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int *bail) {
     constexpr int H = S::H, QD = S::QD, KVD = S::KVD, HD = S::HD, F = S::F, NH = S::NH;
@@ -1028,32 +1051,36 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         vxm_ptab Ly = layer_at(p, l);
         const UnitBases nxt = unit_bases(p, l + 1);
         // ---------------- A: norm + QKV + rope ----------------
-        if (reader) {
-            stage_f32(Ly->g_in, H, gn);
+        static_assert((H / 2) % (64 * kXReaders) == 0 && H / 2 / kXReaders <= 64 * 64, "x readers");
+        if (reader) stage_f32(Ly->g_in, H, gn);
+        if (wave < kXReaders) {
+            // waves 0 .. kXReaders-1 each read a share of x (and its sum of squares)
+            constexpr int XW = H / 2 / kXReaders;   // words per reading wave
             double ss = 0.0;
             if (l == 0) {
-                for (int i = lane * 4; i < H; i += 256) {
-                    const float4 v = *(const float4 *)(p.x + i);
-                    *(float4 *)(xs + i) = v;
-                    ss += (double)(v.x * v.x) + (double)(v.y * v.y) + (double)(v.z * v.z) + (double)(v.w * v.w);
+                if (reader) {
+                    for (int i = lane * 4; i < H; i += 256) {
+                        const float4 v = *(const float4 *)(p.x + i);
+                        *(float4 *)(xs + i) = v;
+                        ss += (double)(v.x * v.x) + (double)(v.y * v.y) + (double)(v.z * v.z) + (double)(v.w * v.w);
+                    }
                 }
             } else {
-                ss = read_words<cdiv(H / 4, 64), true>(p, p.xb + ((l & 1) * kRep + rp) * SX, H / 4,
-                                                       make_tag(ep, l, PH_X), xs, bail);
+                ss = read_words<XW / 64, true>(p, p.xb + ((l & 1) * kRep + rp) * SX + wave * XW, XW,
+                                               make_tag(ep, l, PH_X), xs + 2 * wave * XW, bail);
             }
             ss = wave_sum_63_d(ss);
-            if (lane == 63) ssq[0] = ss;
-        } else if (wave == 1 && l > 0) {
-            // the second half of x, read in parallel with wave 0's
-            double ss = read_words<cdiv(H / 4, 64), true>(p, p.xb + ((l & 1) * kRep + rp) * SX + H / 4, H / 4,
-                                                          make_tag(ep, l, PH_X), xs + H / 2, bail);
-            ss = wave_sum_63_d(ss);
-            if (lane == 63) ssq[1] = ss;
+            if (lane == 63) ssq[wave] = ss;
         }
         lds_barrier();
         if (*bail) return;
         VXM_TS(tid_now() == 0, 0);
-        norm_quant<H>(xs, gn, l > 0 ? ssq[0] + ssq[1] : ssq[0], p.eps, xq, xd);
+        {
+            double sst = 0.0;
+#pragma unroll
+            for (int w = 0; w < kXReaders; w++) sst += ssq[w];
+            norm_quant<H>(xs, gn, sst, p.eps, xq, xd);
+        }
         lds_barrier();
         if (!reader) ring_phase<S, S::OA, S::SA>(ring, l, ci, lane, xq, xd, part);
         lds_barrier();
@@ -1086,15 +1113,15 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             if (*bail) return;
         }
         // ---------------- C: O rows + residual ----------------
-        if (wave < 2) {
-            // waves 0 and 1 (idle until this input arrives) each read one half:
-            // the two rounds of loads are in flight together
+        if (wave < kAttReaders) {
+            // waves 0 .. kAttReaders-1 each read a share; their rounds of loads are in flight together
             const uint64_t *src = p.attb + rp * SAT;
             const uint32_t tag = make_tag(ep, l, PH_ATT);
             wait_sentinels(p, src, NH, HD, tag, bail);
-            static_assert(QD % 128 == 0 && QD / 128 <= 24, "attention channel halves");
-            const int hf = wave * (QD / 2);
-            if (!*bail) read_words<QD / 128, false>(p, src + hf, QD / 2, tag, big + hf, bail);
+            constexpr int AW = QD / kAttReaders;
+            static_assert(AW % 64 == 0 && AW / 64 <= 64, "attention channel shares");
+            const int hf = wave * AW;
+            if (!*bail) read_words<AW / 64, false>(p, src + hf, AW, tag, big + hf, bail);
         }
         lds_barrier();
         if (*bail) return;
@@ -1121,18 +1148,24 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         }
         if (!reader) ring_refill<S, S::OC, S::SC>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         // ---------------- D: post norm + gate/up + SwiGLU ----------------
-        if (reader) {
-            // the reader alone: a compute wave's loads would wait (in-order
-            // vmcnt) for the D units it has just put in flight
-            stage_f32(Ly->g_post, H, gn);
-            double ss = read_words<cdiv(H / 2, 64), true>(p, p.h1b + rp * SX, H / 2, make_tag(ep, l, PH_H1), h1s, bail);
+        if (reader) stage_f32(Ly->g_post, H, gn);
+        if (wave < kH1Readers) {
+            constexpr int HW = H / 2 / kH1Readers;   // words per reading wave
+            static_assert(HW % 64 == 0 && HW / 64 <= 64, "h1 readers");
+            double ss = read_words<HW / 64, true>(p, p.h1b + rp * SX + wave * HW, HW, make_tag(ep, l, PH_H1),
+                                                  h1s + 2 * wave * HW, bail);
             ss = wave_sum_63_d(ss);
-            if (lane == 63) ssq[0] = ss;
+            if (lane == 63) ssq[wave] = ss;
         }
         lds_barrier();
         if (*bail) return;
         VXM_TS(tid_now() == 0, 7);
-        norm_quant<H>(h1s, gn, ssq[0], p.eps, xq, xd);
+        {
+            double sst = 0.0;
+#pragma unroll
+            for (int w = 0; w < kH1Readers; w++) sst += ssq[w];
+            norm_quant<H>(h1s, gn, sst, p.eps, xq, xd);
+        }
         lds_barrier();
         if (!reader) ring_phase<S, S::OD, S::SD>(ring, l, ci, lane, xq, xd, part);
         lds_barrier();
@@ -1152,10 +1185,10 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         }
         if (!reader) ring_refill<S, S::OD, S::SD>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         // ---------------- E: down rows + residual ----------------
-        if (wave < 4) {
-            // waves 0..3 (idle until this input arrives) each read one quarter
-            constexpr int QW = F / 8;
-            static_assert(QW % 64 == 0 && QW / 64 <= 24, "p channel quarters");
+        if (wave < kPReaders) {
+            // waves 0 .. kPReaders-1 each read a share of p
+            constexpr int QW = F / 2 / kPReaders;
+            static_assert(QW % 64 == 0 && QW / 64 <= 64, "p channel shares");
             const uint32_t tag = make_tag(ep, l, PH_P);
             read_words<QW / 64, true, true>(p, p.pb + rp * SP + wave * QW, QW, tag, big + wave * QW, bail);
         }

@@ -15,7 +15,8 @@ import os
 import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libvxm_q8.so")
+# the in-tree library; VXM_LIB names another build of it (the profiling build, libvxm_q8_trace.so)
+LIB_PATH = os.environ.get("VXM_LIB") or os.path.join(HERE, "libvxm_q8.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "vxm_q8.h")
 
 QUANT_REF = 0
