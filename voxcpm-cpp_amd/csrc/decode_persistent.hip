@@ -82,10 +82,12 @@ constexpr int kWaves = 8;              // waves per workgroup: 1 reader + 7 comp
 // agent-scope loads whose cost is their issue and their trip to the memory
 // side, so spreading a round over more waves shortens it, even over compute
 // waves whose own refill loads are still in flight (their loads retire in
-// issue order).  Measured over the 28-layer decode (us per token): x / att /
-// h1 / p read by 2 / 2 / 1 / 4 waves 741-748; p by 1 wave 832; everything by
-// wave 0 alone 863; 8 / 8 / 1 / 8 waves 722; 8 / 8 / 4 / 8 692; 8 / 8 / 8 / 8 694;
-// 4 / 8 / 4 / 8 707; 8 / 4 / 4 / 8 698; 8 / 8 / 4 / 6 706.
+// issue order).  Measured over the 28-layer decode (us per token), with 16
+// channel replicas: x / att / h1 / p read by 2 / 2 / 1 / 4 waves 741-748; p by
+// 1 wave 832; everything by wave 0 alone 863; 8 / 8 / 1 / 8 waves 722;
+// 8 / 8 / 4 / 8 692; 8 / 8 / 8 / 8 694; 4 / 8 / 4 / 8 707; 8 / 4 / 4 / 8 698.
+// With 4 replicas: 8 / 8 / 8 / 8 664; 8 / 8 / 4 / 8 667; 8 / 8 / 2 / 8 671;
+// 4 / 8 / 4 / 8 676; 8 / 4 / 4 / 8 672; 8 / 8 / 4 / 4 680.
 #ifndef VXM_X_READERS
 #define VXM_X_READERS 8
 #endif
@@ -96,7 +98,7 @@ constexpr int kWaves = 8;              // waves per workgroup: 1 reader + 7 comp
 #define VXM_P_READERS 8
 #endif
 #ifndef VXM_H1_READERS
-#define VXM_H1_READERS 4
+#define VXM_H1_READERS 8
 #endif
 constexpr int kXReaders = VXM_X_READERS, kAttReaders = VXM_ATT_READERS, kPReaders = VXM_P_READERS;
 constexpr int kH1Readers = VXM_H1_READERS;
@@ -108,8 +110,13 @@ constexpr int kLook = 7;               // 2 KiB weight units in the LDS ring per
 constexpr int kUnit = 2048;            // quant bytes per unit (64 blocks)
 constexpr int kSlot = kUnit + 128;     // LDS bytes per ring slot: quants, then 64 fp16 scales
 // Every channel is written as kRep replicas; workgroup b reads replica
-// b % kRep, so the coherent loads of 256 workgroups spread over many lines.
-constexpr int kRep = 16;
+// b % kRep, so the coherent loads of 256 workgroups spread over more lines.
+// Each replica costs its producer one more agent-scope store per word:
+// measured (us per token) 32 replicas 741, 16 693, 8 677, 4 667, 2 666, 1 672.
+#ifndef VXM_REPLICAS
+#define VXM_REPLICAS 4
+#endif
+constexpr int kRep = VXM_REPLICAS;
 constexpr int kPad = 64;               // words between replicas
 
 __host__ __device__ constexpr int rep_stride(int words) { return words + kPad; }
@@ -935,7 +942,8 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     }
     lds_barrier();
     const uint32_t tg = make_tag(ep, l, PH_ATT);
-    static_assert(kThreads % HD == 0 && kRep % (kThreads / HD) == 0, "attention output replicas");
+    static_assert(kThreads % HD == 0 && (kRep % (kThreads / HD) == 0 || kRep < kThreads / HD),
+                  "attention output replicas");
     // thread t owns dim t % HD; the wave partials are summed once, in a fixed order
     const int d = tid % HD;
     float v = 0.0f;
