@@ -102,6 +102,7 @@ constexpr int kWaves = 8;              // waves per workgroup: 1 reader + 7 comp
 #endif
 constexpr int kXReaders = VXM_X_READERS, kAttReaders = VXM_ATT_READERS, kPReaders = VXM_P_READERS;
 constexpr int kH1Readers = VXM_H1_READERS;
+
 constexpr int kCW = kWaves - 1;
 constexpr int kThreads = kWaves * 64;
 constexpr int kG = 256;                // workgroups: one per CU
@@ -1191,7 +1192,15 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             const float p0 = swiglu(v[0], v[1]), p1 = swiglu(v[2], v[3]);
             put_word(p.pb + r * SP + wg * (S::RD / 4) + wi, pack_bf16x2(p0, p1), make_tag(ep, l, PH_P));
         }
-        if (!reader) ring_refill<S, S::OD, S::SD>(p, cur, nxt, ring_lds, l, wg, ci, lane);
+        // D's refills in two parts.  The units of E (the positions before the
+        // layer's end) go out now; the next layer's A / C units only after the
+        // p read below, which would otherwise retire behind them in each reading
+        // wave: 667 -> 649 us per token.  Holding back more measured slower (the
+        // units then arrive late for their phase): E's refills after the next
+        // layer's x read 709, the part of them that lands on D 684, C's refills
+        // after the h1 read 700.
+        constexpr int kDE = S::NS - S::OD - S::P > 0 ? S::NS - S::OD - S::P : 0;
+        if (!reader) ring_refill<S, S::OD, kDE>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         // ---------------- E: down rows + residual ----------------
         if (wave < kPReaders) {
             // waves 0 .. kPReaders-1 each read a share of p
@@ -1203,6 +1212,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         lds_barrier();
         if (*bail) return;
         VXM_TS(tid_now() == 0, 9);
+        if (!reader) ring_refill<S, S::OD, S::SD, kDE>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         quantize_lds_bf16x2((const uint32_t *)big, F, xq, xd);
         lds_barrier();
         if (!reader) ring_phase<S, S::OE, S::SE>(ring, l, ci, lane, xq, xd, part);
