@@ -327,3 +327,67 @@ def test_persistent_long_context_peaked_attention(vxm_ctx, orc, ctx0):
         m.free()
     for kv in kvs.values():
         kv.free()
+
+
+def test_persistent_decode_two_streams_interleaved(vxm_ctx, orc):
+    """Single-launch decodes from two contexts (two streams) of one device, issued
+    alternately with no host synchronisation: each launch needs all 256 workgroups
+    resident, and the library orders decode launches on a device across streams, so
+    both sequences complete and equal their runs one token at a time bit for bit."""
+    import vxm
+
+    s = SHAPES["tslm"]
+    L, cap, ctx0, steps = 2, 256, 50, 3
+    rng = np.random.default_rng(777)
+    lws = [rand_layer(orc, rng, s["H"], s["nh"], s["nkv"], s["hd"], s["F"]) for _ in range(L)]
+    fn = (1 + rng.normal(0, 0.02, s["H"])).astype(np.float32)
+    c = cfg_dict(s["H"], L, s["nh"], s["nkv"], s["hd"], s["F"])
+    xs = [[rng.normal(0, 1, (1, s["H"])).astype(np.float32) for _ in range(steps)] for _ in range(2)]
+    kh = orc.fp32_to_fp16_bits(orc.bf16_round(rng.normal(0, 1, (s["nkv"], cap, s["hd"])).astype(np.float32)))
+    ctx2 = vxm.Context(0)
+    contexts = (vxm_ctx, ctx2)
+
+    def setup():
+        ms, kvs = [], []
+        for cx in contexts:
+            m = vxm.MiniCPM4(cx, c, lws, final_norm=fn)
+            m.set_decode_mode(2)
+            kv = vxm.KVCache(cx, L, s["nkv"], s["hd"], cap)
+            for l in range(L):
+                kv.upload(l, kh, kh)
+            kv.set_used(ctx0)
+            ms.append(m)
+            kvs.append(kv)
+        return ms, kvs
+
+    def teardown(ms, kvs):
+        for m in ms:
+            m.check()
+            m.free()
+        for kv in kvs:
+            kv.free()
+
+    try:
+        # interleaved: token t of stream 0, token t of stream 1, ... no host sync
+        ms, kvs = setup()
+        dev = {}
+        for t in range(steps):
+            for j in range(2):
+                xd = _dev(xs[j][t])
+                ms[j].forward(kvs[j], xd, ctx0 + t)
+                dev[(j, t)] = xd
+        for cx in contexts:
+            cx.sync()
+        both = {k: v.cpu().numpy() for k, v in dev.items()}
+        teardown(ms, kvs)
+        # one token at a time, synchronised after each
+        ms, kvs = setup()
+        for j in range(2):
+            for t in range(steps):
+                xd = _dev(xs[j][t])
+                ms[j].forward(kvs[j], xd, ctx0 + t)
+                contexts[j].sync()
+                assert np.array_equal(xd.cpu().numpy(), both[(j, t)]), (j, t)
+        teardown(ms, kvs)
+    finally:
+        ctx2.close()

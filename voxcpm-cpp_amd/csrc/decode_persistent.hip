@@ -1,6 +1,6 @@
 // decode_persistent.hip -- one decode token through the whole MiniCPM4 stack
 // (vcpm_minicpm4_forward with n_tokens = 1, src/minicpm4.c:536-572) in ONE
-// cooperative launch of one 512-thread workgroup per CU.
+// launch of one 512-thread workgroup per CU, all resident at once.
 //
 // Why one launch: on MI355X a dependent kernel boundary costs ~2.7 us (1.6 us
 // in a HIP graph) against ~6.3 us of HBM streaming per layer; one launch per
@@ -54,6 +54,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <mutex>
 #include <utility>
 
 #include "vxm_model.h"
@@ -1302,16 +1303,43 @@ struct vxm_persistent_state {
 
 static constexpr int kMaxLds = 160 * 1024;
 
+// Every workgroup of the decode waits on words the others publish, so all 256
+// must be resident at once: one per CU, since the LDS layout takes more than
+// half of a CU's 160 KB.  A plain launch of 256 workgroups places them all on
+// a device whose other work finishes on its own.  hipLaunchCooperativeKernel
+// guarantees it, but measured 19 us more per token (649 against 630).  Other
+// work on the device can only delay the waits, and every wait is bounded
+// (kSpin rounds, then the error word): an error, never a hang.  Two decodes on
+// different streams of one device could interleave their workgroups and wait
+// on each other until that bound.  So every decode launch on a device is
+// ordered after the previous one there: one event per device, waited on when
+// the stream changes.
+namespace {
+struct LaunchOrder {
+    std::mutex mu;
+    hipEvent_t ev = nullptr;
+    hipStream_t last = nullptr;
+};
+LaunchOrder g_launch_order[64];
+}  // namespace
+
 template <class S>
 static int launch_decode(vxm_ctx *ctx, const vxm_pparams &prm) {
     const int lds = S::BYTES + 16;   // the layout + the bail flag
     auto kern = k_decode_persistent<S>;
     if (lds > kMaxLds)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "persistent decode: kv capacity %d needs %d B of LDS", prm.cap, lds);
+    if (ctx->device < 0 || ctx->device >= 64)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "persistent decode: device %d beyond the launch table", ctx->device);
     VXM_HIP(ctx, hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
-    void *args[] = {(void *)&prm};
-    VXM_HIP(ctx, hipLaunchCooperativeKernel((const void *)kern, dim3(kG), dim3(kThreads), args, (unsigned)lds,
-                                            ctx->stream));
+    LaunchOrder &o = g_launch_order[ctx->device];
+    std::lock_guard<std::mutex> lock(o.mu);
+    if (!o.ev) VXM_HIP(ctx, hipEventCreateWithFlags(&o.ev, hipEventDisableTiming));
+    if (o.last && o.last != ctx->stream) VXM_HIP(ctx, hipStreamWaitEvent(ctx->stream, o.ev, 0));
+    hipLaunchKernelGGL(kern, dim3(kG), dim3(kThreads), (unsigned)lds, ctx->stream, prm);
+    VXM_CHECK_LAUNCH(ctx);
+    VXM_HIP(ctx, hipEventRecord(o.ev, ctx->stream));
+    o.last = ctx->stream;
     return VXM_OK;
 }
 
