@@ -53,6 +53,24 @@ def phases(t, L):
     return out
 
 
+def exchanges(t, L):
+    """Per exchange and layer, in ticks: the spread of the producers' finish (last minus median
+    workgroup), and the time from the LAST producer's finish to the median consumer having every
+    input (the transit seen by the critical path)."""
+    s = lambda k: t[:, 2 + np.arange(L) * 12 + k].astype(np.float64)
+    att = s(3) > 0
+    ends_next = [("A -> attention", s(1), np.where(att, s(3), np.nan)),
+                 ("attention -> C", np.where(att, s(4), np.nan), s(5)),
+                 ("C -> D", s(6), s(7)),
+                 ("D -> E", s(8), s(9)),
+                 ("E -> next A", s(10)[:, :-1], s(0)[:, 1:])]
+    out = {}
+    for name, end, ready in ends_next:
+        last = np.nanmax(end, axis=0)
+        out[name] = (last - np.nanmedian(end, axis=0), np.nanmedian(ready, axis=0) - last)
+    return out
+
+
 def main(argv):
     d = argv[1]
     skip = int(argv[argv.index("--skip") + 1]) if "--skip" in argv else 4
@@ -74,6 +92,19 @@ def main(argv):
     for k, parts in acc.items():
         v = np.concatenate(parts) * TICK_US
         print(f"| {k} | {np.median(v):.2f} | {np.percentile(v, 90):.2f} |")
+    ex = {}
+    for f in files:
+        t, L = load(f)
+        for k, (skew, transit) in exchanges(t, L).items():
+            ex.setdefault(k, ([], []))
+            ex[k][0].append(skew)
+            ex[k][1].append(transit)
+    print()
+    print("| exchange | producers' finish: last - median, us | last producer -> median consumer ready, us |")
+    print("|---|---|---|")
+    for k, (skew, transit) in ex.items():
+        print(f"| {k} | {np.median(np.concatenate(skew)) * TICK_US:.2f} | "
+              f"{np.median(np.concatenate(transit)) * TICK_US:.2f} |")
 
 
 if __name__ == "__main__":
