@@ -127,7 +127,8 @@ def test_decode_gemv_full_size_seed0(vxm_ctx, orc, N, K):
 # (path, N, K, M): the kernel vxm_mul_mat_q8_0_q8_0 runs for each is the one whose
 # int32 block sums vxm_block_dots_q8_0 returns -- chunked GEMV <C, R> (M < 8, K a
 # multiple of 1024 in {1, 2, 4, 6} KiB), generic GEMV, small-M MFMA (one or two wave
-# groups, K splits), tiled MFMA (16- or 8-block stages, K splits)
+# groups, K splits), the DMA-fed tile GEMM (64 x 64 or 64 x 128 tiles, K % 256 == 0,
+# K splits), the register-staged tiled GEMM (16- or 8-block stages, K splits)
 _PRODUCTION_DOTS = [
     (0, 6144, 2048, 1),     # decode gate/up GEMV <2, 2>
     (0, 2048, 6144, 1),     # decode down GEMV <6, 1>
@@ -139,9 +140,13 @@ _PRODUCTION_DOTS = [
     (0, 3072, 1024, 48),    # CFM QKV: small-M
     (0, 1024, 4096, 48),    # CFM down: small-M, K split
     (2, 1024, 4096, 5),     # small-M at 5 rows (the block pipeline's choice)
-    (0, 2048, 2048, 512),   # prefill O: tiled, 8-block stages
+    (0, 2048, 2048, 512),   # prefill O: tile GEMM, 64 x 64 tiles
+    (0, 2560, 1024, 512),   # tile GEMM, 64 x 128 tiles (the prefill QKV choice)
+    (0, 256, 8192, 128),    # tile GEMM, four K splits (more blocks than one activation scale panel holds)
+    (0, 1001, 512, 100),    # tile GEMM, ragged M and N (N % 4 != 0: no 16-byte stores)
     (3, 2048, 2048, 33),    # tiled, 16-block stages, K split
-    (0, 2560, 2048, 100),   # tiled, ragged M tile
+    (0, 2560, 2048, 100),   # tile GEMM, ragged M tile
+    (0, 2560, 2080, 100),   # register-staged tiled GEMM (K % 256 != 0)
 ]
 
 
@@ -167,6 +172,26 @@ def test_block_dots_of_the_kernel_that_runs(vxm_ctx, orc, path, N, K, M):
     scale = (dx.view(np.float16).astype(np.float32)[:, None, :] * dw.view(np.float16).astype(np.float32)[None, :, :])
     terms = (sums.astype(np.float32) * scale).astype(np.float64)
     _assert_close(y, terms.sum(axis=2))
+    w.free()
+
+
+def test_tile_gemm_unaligned_output(vxm_ctx, orc):
+    """An output pointer that is 4- but not 16-byte aligned takes the tile GEMM's
+    scalar stores: the same bits as into an aligned buffer."""
+    import torch
+
+    N, K, M = 640, 1024, 256
+    _, x, wq = _case(orc, N, K, M, 91)
+    w = vxm_ctx.upload_q8_0(wq, N, K)
+    xq, xd = vxm_ctx.quantize_q8_0(_dev(x), 1)
+    y_al = vxm_ctx.mul_mat_q8(w, xq, xd)
+    buf = torch.full((M * N + 1,), float("nan"), dtype=torch.float32, device=xq.device)
+    y_un = buf[1:].view(M, N)
+    assert y_un.data_ptr() % 16 != 0
+    vxm_ctx.mul_mat_q8(w, xq, xd, y_un)
+    vxm_ctx.sync()
+    assert torch.equal(y_al, y_un)
+    assert torch.isnan(buf[0])   # nothing written before the output
     w.free()
 
 

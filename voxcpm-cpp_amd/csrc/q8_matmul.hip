@@ -8,6 +8,7 @@
 // Every kernel here forms exactly these per-block fp32 terms; only the order
 // of the fp32 additions over b differs from ggml's (a tree over lanes).
 #include <atomic>
+#include <cstdint>
 #include <mutex>
 
 #include "vxm_internal.h"
@@ -363,6 +364,116 @@ struct GemmLds {
     float bd[2][KS][GN];
 };
 
+// The end of a tiled-GEMM workgroup, shared by both tiled kernels: acc holds
+// this wave's 32 x 64 strip of K quarter kq (8 waves: wm = wave & 1, kq =
+// wave >> 1).  The four quarters are added in order through LDS (red: 64 KiB,
+// free), then y is written, or with K splits the partial tile is published
+// as tagged words and the last workgroup of the tile adds the splits in order.
+__device__ __forceinline__ void gemm_finish(float (&acc)[2][16], float *red, int *last_sh, float *__restrict__ y,
+                                            uint64_t *__restrict__ part, int *__restrict__ cnt, int M, int N,
+                                            int m0, int n0, int tm, int tn, int tiles_n, int z, int splits,
+                                            uint32_t epoch, int *__restrict__ err) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, kq = wave >> 1;
+    const int lr = lane & 31, lh = lane >> 5;
+    // add the K quarters in order (quarter 0 + 1 + 2 + 3): every quarter hands its strips to
+    // LDS, then quarter group kq finalizes result registers v = 4 kq .. 4 kq + 3 of both
+    // strips (rows m0 + 32 wm + 8 kq + 4 lh + vv)
+    // red: [4 quarters][2 strips][32 values][64 lanes]
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        red[((kq * 2 + wm) * 32 + v) * 64 + lane] = acc[0][v];
+        red[((kq * 2 + wm) * 32 + 16 + v) * 64 + lane] = acc[1][v];
+    }
+    __syncthreads();
+    float fin[2][4];
+#pragma unroll
+    for (int half = 0; half < 2; half++)
+#pragma unroll
+        for (int vv = 0; vv < 4; vv++) {
+            const int v = 4 * kq + vv;
+            float t = red[((0 * 2 + wm) * 32 + 16 * half + v) * 64 + lane];
+#pragma unroll
+            for (int q = 1; q < 4; q++) t = t + red[((q * 2 + wm) * 32 + 16 * half + v) * 64 + lane];
+            fin[half][vv] = t;
+        }
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+        const int n = n0 + half * 32 + lr;
+        if (n >= N) continue;
+#pragma unroll
+        for (int vv = 0; vv < 4; vv++) {
+            const int m = m0 + wm * 32 + 8 * kq + 4 * lh + vv;
+            if (m >= M) continue;
+            const int64_t idx = (int64_t)m * N + n;
+            if (splits == 1) {
+                y[idx] = fin[half][vv];
+            } else {
+                const uint64_t word = ((uint64_t)epoch << 32) | __float_as_uint(fin[half][vv]);
+                __hip_atomic_store(part + (int64_t)z * M * N + idx, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+    if (splits == 1) return;
+    // split fix-up: count arrivals; the last one reduces the tagged partials in split order
+    __syncthreads();
+    const int tile = tm * tiles_n + tn;
+    if (tid == 0) {
+        const int prev = __hip_atomic_fetch_add(cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        (*last_sh) = prev == splits - 1;
+        if ((*last_sh)) __hip_atomic_store(cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!(*last_sh)) return;
+    // thread t reduces elements t + 512 j, j < 8, four at a time: all 4 x splits words
+    // are requested before any tag is checked
+    constexpr int EPT = GM * GN / kGemmThreads, EPP = 4;
+    const int64_t MN = (int64_t)M * N;
+#pragma unroll
+    for (int j0 = 0; j0 < EPT; j0 += EPP) {
+        uint64_t w[EPP][kGemmMaxSplits];
+#pragma unroll
+        for (int j = 0; j < EPP; j++) {
+            const int e = tid + kGemmThreads * (j0 + j), m = m0 + e / GN, nn = n0 + e % GN;
+            const bool live = m < M && nn < N;
+            const int64_t i = live ? (int64_t)m * N + nn : 0;
+#pragma unroll
+            for (int zz = 0; zz < kGemmMaxSplits; zz++)
+                w[j][zz] = (live && zz < splits)
+                               ? __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                               : ((uint64_t)epoch << 32);
+        }
+#pragma unroll
+        for (int j = 0; j < EPP; j++) {
+            const int e = tid + kGemmThreads * (j0 + j), m = m0 + e / GN, nn = n0 + e % GN;
+            if (m >= M || nn >= N) continue;
+            const int64_t i = (int64_t)m * N + nn;
+            float s = 0.0f;
+            bool stale = false;
+#pragma unroll
+            for (int zz = 0; zz < kGemmMaxSplits; zz++) {
+                if (zz >= splits) break;
+                uint64_t v = w[j][zz];
+                for (int spin = 0; (uint32_t)(v >> 32) != epoch && spin < kGemmSpin; spin++) {
+                    __builtin_amdgcn_s_sleep(1);
+                    v = __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                stale |= (uint32_t)(v >> 32) != epoch;
+                const float p = __uint_as_float((uint32_t)v);
+                s = zz ? s + p : p;
+            }
+            // a partial that never arrived: a visible NaN and the context's error word
+            // (reported by vxm_sync), never a plausible-looking stale sum
+            if (stale) {
+                s = __builtin_nanf("");
+                __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            y[i] = s;
+        }
+    }
+}
+
 template <int KS, bool DOTS>
 #ifndef VXM_GEMM_PIPE
 #define VXM_GEMM_PIPE 1
@@ -514,46 +625,374 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
         __syncthreads();
     }
     if (DOTS) return;
-    // add the K quarters in order (quarter 0 + 1 + 2 + 3): every quarter hands its strips to
-    // LDS, then quarter group kq finalizes result registers v = 4 kq .. 4 kq + 3 of both
-    // strips (rows m0 + 32 wm + 8 kq + 4 lh + vv)
-    float *red = (float *)&L;   // [4 quarters][2 strips][32 values][64 lanes], free after the last barrier
+    gemm_finish(acc, (float *)&L, &last_sh, y, part, cnt, M, N, m0, n0, tm, tn, tiles_n, z, splits, epoch, err);
+}
+
+// ---------------------------------------------------------------------------
+// Tiled Q8_0 x Q8_0 GEMM for prefill-sized M (> 64): one 64 x TN output tile
+// per workgroup (TN = 64 or 128, 512 threads), every operand byte brought
+// into LDS by direct HBM -> LDS loads (global_load_lds_dwordx4: lane l of an
+// instruction writes 16 bytes at M0 + 16 l) into a ring of kTileSlots stages,
+// three of them in flight while one is multiplied.
+//
+// Waves: wave w owns the 32-row strip sm = w & 1 and the 64-column half
+// h = (w >> 1) & (H - 1) of the tile (H = TN / 64) for K part kp (KP = 4 / H
+// parts): the two blocks 2 kp, 2 kp + 1 of every SB-block stage (SB = 8 / H,
+// so a stage holds RB = 32 SB bytes of each operand row).  The K parts are
+// added in order through LDS at the end.
+//
+// Per block a wave issues two v_mfma_i32_32x32x32_i8 (its 32 x 64 integer
+// block sums) and one two-block f32 outer product (the 2 x 32 x 32 scale
+// products d_x[m] d_w[n], exact in fp32), then converts and accumulates:
+// acc += float(sum) * scale.  The MFMAs of the next block are always issued
+// before the conversion of the current one, so the matrix core runs under
+// the VALU work and no result is waited for.
+//
+// Scales: the weight scales come from the tile-blocked copy dt (groups of 64
+// rows x 4 blocks, 512 contiguous bytes; rows past N hold zeros), so a
+// stage's TN x SB scales are one DMA instruction.  The activation scales of
+// the tile's 64 rows over the split's K range are one LDS panel loaded with
+// the first stages (rows of 2 (b1 - b0) bytes + 16 bytes of padding, which
+// spreads the 32 rows a wave reads over the banks).  Operand rows past M or
+// N load the clamped last row; past-N columns have zero scales and past-M
+// rows are never stored.
+//
+// Operand rows are RB bytes in LDS with the 16-byte piece p of row r stored
+// at p ^ (r % R16) (R16 = RB / 16 pieces), so the 32 rows of an MFMA operand
+// read fall on distinct banks; each DMA lane simply loads the piece its LDS
+// position holds.  Each wave issues the same number of stage loads (wave 0
+// one more: the weight scales), so its own in-order load counter tells when
+// its part of a stage has landed; a barrier then publishes all parts and
+// frees the slot of the stage before.
+//
+// K splits (blockIdx.y) end as in gemm_finish: tagged partial words, the last
+// workgroup of a tile adds them in split order.  DOTS = true writes the int32
+// block sums to dots[(m*N + n)*nb + b] instead (no scaling, no split fix-up).
+// ---------------------------------------------------------------------------
+constexpr int kTileSlots = 4;
+constexpr int kTileMaxBps = 192;      // K blocks per split (activation scale panel <= 25 KiB)
+constexpr int kTileThreads = 512;
+
+#ifdef VXM_TILE_TRACE
+// per-stage timestamps (s_memtime) of every wave of the first 256 workgroups:
+// [workgroup][wave][stage < 62][top, compute done, loads landed, barrier passed];
+// stage 62: entry, loop end, stores done
+__device__ uint64_t vxm_tile_trace[256 * 8 * 64 * 4];
+#define VXM_TILE_TS(st, k)                                                                         \
+    do {                                                                                           \
+        if (lane == 0 && blockIdx.x < 256 && blockIdx.y == 0 && (st) < 64)                         \
+            vxm_tile_trace[((blockIdx.x * 8 + wave) * 64 + (st)) * 4 + (k)] = __builtin_amdgcn_s_memtime(); \
+    } while (0)
+#else
+#define VXM_TILE_TS(st, k) \
+    do {                   \
+    } while (0)
+#endif
+
+template <int TN>
+struct TileCfg {
+    static constexpr int H = TN / 64;                  // 64-column halves
+    static constexpr int KP = 4 / H;                   // K parts
+    static constexpr int SB = 8 / H;                   // blocks per stage
+    static constexpr int RB = SB * 32;                 // operand row bytes per stage
+    static constexpr int R16 = RB / 16;                // 16-byte pieces per row
+    static constexpr int ABytes = GM * RB, BBytes = TN * RB;
+    static constexpr int Slot = ABytes + BBytes + 1024;   // + TN x SB weight scales
+    static constexpr int LoadsAB = (ABytes + BBytes) / 1024 / 8;   // operand loads per wave and stage
+    static constexpr int Red = KP * 2 * H * 32 * 64;   // floats of the K-part reduction
+    static_assert((ABytes + BBytes) % 8192 == 0, "operand loads must split evenly over the waves");
+    static_assert(Red * 4 <= kTileSlots * Slot, "the reduction reuses the ring");
+};
+
+static size_t tile_lds_bytes(int tn, int bps) {
+    const int slot = tn == 128 ? TileCfg<128>::Slot : TileCfg<64>::Slot;
+    return (size_t)kTileSlots * slot + 1024 * (size_t)(bps / 8 + 1);
+}
+
+// 16 bytes per lane from src into LDS at lds_base + 16 lane.
+__device__ __forceinline__ void lds_dma16(uint32_t lds_base, const void *src) {
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_base);
+    uint32_t saved_m0;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %2, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved_m0)
+        : "s"(m0v), "v"(src)
+        : "memory");
+}
+
+// 16 bytes per lane of lanes 0..7 only (exec = 0xff), into LDS at lds_base + 16 lane.
+__device__ __forceinline__ void lds_dma16_8(uint32_t lds_base, const void *src) {
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_base);
+    uint64_t saved;
+    uint32_t saved_m0;
+    asm volatile(
+        "s_mov_b32 %1, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, 0xff\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %3, off\n\t"
+        "s_mov_b64 exec, %0\n\t"
+        "s_mov_b32 m0, %1"
+        : "=&s"(saved), "=&s"(saved_m0)
+        : "s"(m0v), "v"(src)
+        : "memory", "scc");
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// wait until at most `stages` later stages of this wave's loads (L per stage) are in flight
+template <int L>
+__device__ __forceinline__ void vm_wait_stages(int stages) {
+    if (stages >= 2) vm_wait<2 * L>();
+    else if (stages == 1) vm_wait<L>();
+    else vm_wait<0>();
+}
+
+__device__ __forceinline__ void ring_barrier() {   // orders LDS only: loads in flight stay in flight
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int TN, bool DOTS>
+__global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
+    const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd, const int8_t *__restrict__ wq,
+    const uint16_t *__restrict__ wt, float *__restrict__ y, uint64_t *__restrict__ part, int *__restrict__ cnt,
+    int32_t *__restrict__ dots, int M, int N, int K, int tiles_m, int tiles_n, int bps, int splits,
+    uint32_t epoch, int *__restrict__ err) {
+    using C = TileCfg<TN>;
+    extern __shared__ __attribute__((aligned(16))) int8_t ring[];
+    __shared__ int last_sh;
+    const int id = blockIdx.x, xcd = id % 8, k8 = id / 8;
+    const int tn = (k8 / tiles_m) * 8 + xcd, tm = k8 % tiles_m;
+    if (tn >= tiles_n) return;
+    const int m0 = tm * GM, n0 = tn * TN;
+    const int nb = K / 32, nb4 = nb / 4;
+    const int z = blockIdx.y;
+    const int b0 = z * bps, b1 = min(nb, b0 + bps);
+    const int ns = (b1 - b0) / C::SB;   // whole stages
+    const int P = (b1 - b0) / 8;        // 16-byte pieces of a panel row
+    const int pitch = 16 * (P + 1);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int sm = wave & 1, h = (wave >> 1) & (C::H - 1), kp = wave >> (C::H == 2 ? 2 : 1);
+    const int lr = lane & 31, lh = lane >> 5;
+    const int j0 = 2 * kp;   // this wave's first block of a stage
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
+    const int8_t *panel = ring + kTileSlots * C::Slot;
+    VXM_TILE_TS(62, 0);
+
+    // activation scale panel: piece f = 64 i + lane of instruction i is row f / (P + 1),
+    // piece f % (P + 1) (the last piece of a row is padding and loads a valid dummy)
+    for (int i = wave; i <= P; i += 8) {
+        const int f = 64 * i + lane, row = f / (P + 1), pc = f % (P + 1);
+        const int r = min(m0 + row, M - 1), q = pc < P ? pc : 0;
+        lds_dma16(ring_lds + kTileSlots * C::Slot + 1024 * i, xd + (int64_t)r * nb + b0 + 8 * q);
+    }
+    // this wave's loads of stage st: operand instruction i < LoadsAB is instruction
+    // wave * LoadsAB + i of the stage's A | B rows; i == LoadsAB is the wave's
+    // eighth (128 bytes, 8 lanes) of the TN x SB weight scales
+    auto issue_one = [&](int st, int i) {
+        const uint32_t base = ring_lds + (st % kTileSlots) * C::Slot;
+        const int kb0 = b0 + C::SB * st;
+        if (i < C::LoadsAB) {
+            const int q = wave * C::LoadsAB + i;
+            const int rr = q * (64 / C::R16) + lane / C::R16;   // row of A (< 64) then B
+            const int pg = (lane % C::R16) ^ (rr % C::R16);
+            const int8_t *src = rr < GM ? xq + (int64_t)min(m0 + rr, M - 1) * K
+                                        : wq + (int64_t)min(n0 + rr - GM, N - 1) * K;
+            lds_dma16(base + q * 1024, src + kb0 * 32 + pg * 16);
+        } else {
+            // 16-byte piece p = 8 wave + lane of the stage's 1 KiB: 64-row group
+            // p >> 5 (TN = 128) or 4-block step p >> 5 (TN = 64), rows 2 (p & 31) ..
+            const int p = 8 * wave + (lane & 7), g = C::H == 2 ? 2 * tn + (p >> 5) : tn,
+                      c = C::H == 2 ? 0 : p >> 5;
+            lds_dma16_8(base + C::ABytes + C::BBytes + 128 * wave,
+                        wt + ((int64_t)g * nb4 + kb0 / 4 + c) * 256 + (p & 31) * 8);
+        }
+    };
+    auto issue = [&](int st) {
+#pragma unroll
+        for (int i = 0; i <= C::LoadsAB; i++) issue_one(st, i);
+    };
+
+    float acc[2][16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[0][v] = acc[1][v] = 0.0f;
+    // LDS offsets of this lane's operand rows and scales
+    const int ar = 32 * sm + lr, br0 = 64 * h + lr, br1 = br0 + 32, sr = 64 * h + 32 * lh + lr;
+    const int a_off = ar * C::RB, b0_off = C::ABytes + br0 * C::RB, b1_off = C::ABytes + br1 * C::RB;
+    const int s_off = C::ABytes + C::BBytes +
+                      (C::H == 2 ? (sr >> 6) * 512 + (sr & 63) * 8 + j0 * 2 : (j0 >> 2) * 512 + sr * 8 + (j0 & 3) * 2);
+    const int8_t *pa_row = panel + ar * pitch;
+
+    // operands of block j of a stage: this lane's 16 bytes of its A row and of its two B rows
+    auto operands = [&](const int8_t *sb, int j, v4i &a, v4i &w0, v4i &w1) {
+        const int pc = 2 * j + lh;
+        a = *(const v4i *)(sb + a_off + ((pc ^ (ar % C::R16)) * 16));
+        w0 = *(const v4i *)(sb + b0_off + ((pc ^ (br0 % C::R16)) * 16));
+        w1 = *(const v4i *)(sb + b1_off + ((pc ^ (br1 % C::R16)) * 16));
+    };
+    // conversion of values v0 <= v < v1 of a block's sums (both column halves)
+    auto epi_part = [&](const v16i &c0, const v16i &c1, const v32f &sc, int v0, int v1) {
+#pragma unroll
+        for (int v = v0; v < v1; v++) {
+            acc[0][v] = __builtin_fmaf((float)c0[v], sc[v], acc[0][v]);
+            acc[1][v] = __builtin_fmaf((float)c1[v], sc[16 + v], acc[1][v]);
+        }
+    };
+    auto dots_out = [&](const v16i &c0, const v16i &c1, int kb) {
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            const int n = n0 + 64 * h + 32 * half + lr;
+            const v16i &c = half ? c1 : c0;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int m = m0 + 32 * sm + 8 * (v >> 2) + 4 * lh + (v & 3);
+                if (m < M && n < N) dots[((int64_t)m * N + n) * nb + kb] = c[v];
+            }
+        }
+    };
+
+    constexpr int L = C::LoadsAB + 1;   // loads per wave and stage
+#pragma unroll
+    for (int st = 0; st < kTileSlots - 1; st++)
+        if (st < ns) issue(st);
+    vm_wait_stages<L>(min(2, ns - 1));
+    ring_barrier();   // the panel and stage 0 are in LDS
+
+    // Block pipeline: X = this stage's first block, Y = its second.  Each MFMA is
+    // followed by a third of the conversion of the other block -- Y of the stage
+    // before while X's MFMAs run, X while Y's run -- so the matrix core works
+    // under the VALU and no conversion waits for a product (scheduling fences
+    // keep that order).  Y starts as zeros, whose conversion adds nothing.  The
+    // loads of stage st + 3 go out first, into the slot that stage st - 1 freed
+    // at the last barrier.
+    v16i xc0, xc1, yc0 = {}, yc1 = {};
+    v32f xs, ys = {};
+#define VXM_FENCE __builtin_amdgcn_sched_barrier(0)
+    for (int st = 0; st < ns; st++) {
+        VXM_TILE_TS(st, 0);
+        const int8_t *sb = ring + (st % kTileSlots) * C::Slot;
+        const uint32_t pa = *(const uint32_t *)(pa_row + 2 * (C::SB * st + j0));
+        const uint32_t pw = *(const uint32_t *)(sb + s_off);
+        const int kb = b0 + C::SB * st + j0;
+        const bool more = st + kTileSlots - 1 < ns;
+        if (more) issue(st + kTileSlots - 1);
+        v4i xa, xw0, xw1, ya, yw0, yw1;
+        operands(sb, j0, xa, xw0, xw1);
+        operands(sb, j0 + 1, ya, yw0, yw1);
+        if (DOTS) {
+            xc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, xw0, v16i{}, 0, 0, 0);
+            xc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, xw1, v16i{}, 0, 0, 0);
+            yc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ya, yw0, v16i{}, 0, 0, 0);
+            yc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ya, yw1, v16i{}, 0, 0, 0);
+            dots_out(xc0, xc1, kb);
+            dots_out(yc0, yc1, kb + 1);
+        } else {
+            const float dax = vxm_h2f((uint16_t)pa), dwx = vxm_h2f((uint16_t)pw);
+            const float day = vxm_h2f((uint16_t)(pa >> 16)), dwy = vxm_h2f((uint16_t)(pw >> 16));
+            VXM_FENCE;
+            xs = __builtin_amdgcn_mfma_f32_32x32x1f32(dax, dwx, v32f{}, 0, 0, 0);
+            VXM_FENCE;
+            epi_part(yc0, yc1, ys, 0, 6);
+            VXM_FENCE;
+            xc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, xw0, v16i{}, 0, 0, 0);
+            VXM_FENCE;
+            epi_part(yc0, yc1, ys, 6, 11);
+            VXM_FENCE;
+            xc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, xw1, v16i{}, 0, 0, 0);
+            VXM_FENCE;
+            epi_part(yc0, yc1, ys, 11, 16);
+            VXM_FENCE;
+            ys = __builtin_amdgcn_mfma_f32_32x32x1f32(day, dwy, v32f{}, 0, 0, 0);
+            VXM_FENCE;
+            epi_part(xc0, xc1, xs, 0, 6);
+            VXM_FENCE;
+            yc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ya, yw0, v16i{}, 0, 0, 0);
+            VXM_FENCE;
+            epi_part(xc0, xc1, xs, 6, 11);
+            VXM_FENCE;
+            yc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ya, yw1, v16i{}, 0, 0, 0);
+            VXM_FENCE;
+            epi_part(xc0, xc1, xs, 11, 16);
+            VXM_FENCE;
+            // the sums are needed here, not after the stage wait: keep the conversions
+            // in this block (otherwise they sink past the barrier, behind the MFMAs)
+#pragma unroll
+            for (int v = 0; v < 16; v++) asm volatile("" ::"v"(acc[0][v]), "v"(acc[1][v]));
+        }
+        VXM_TILE_TS(st, 1);
+        if (st + 1 < ns) {
+            // stage st + 1 has landed once at most the stages after it remain in flight
+            vm_wait_stages<L>(min(2, ns - 2 - st));
+            VXM_TILE_TS(st, 2);
+            ring_barrier();   // every wave's part of stage st + 1 is visible; slot st is free
+            VXM_TILE_TS(st, 3);
+        }
+    }
+#undef VXM_FENCE
+    if (DOTS) return;
+    if (ns > 0) epi_part(yc0, yc1, ys, 0, 16);
+    VXM_TILE_TS(62, 1);
+
+    // K parts in order through LDS: red[kp][wave of the part][32 values][64 lanes]
+    __syncthreads();   // every wave is done with the ring
+    float *red = (float *)ring;
+    const int wi = wave & (2 * C::H - 1);
 #pragma unroll
     for (int v = 0; v < 16; v++) {
-        red[((kq * 2 + wm) * 32 + v) * 64 + lane] = acc[0][v];
-        red[((kq * 2 + wm) * 32 + 16 + v) * 64 + lane] = acc[1][v];
+        red[((kp * 2 * C::H + wi) * 32 + v) * 64 + lane] = acc[0][v];
+        red[((kp * 2 * C::H + wi) * 32 + 16 + v) * 64 + lane] = acc[1][v];
     }
     __syncthreads();
-    float fin[2][4];
+    // four neighbouring lanes = four neighbouring columns of one row: 16-byte LDS
+    // reads and (N % 4 == 0, the usual case) 16-byte stores
+    constexpr int PER = 2 * C::H * 32 * 64;   // floats of one K part
+    const int64_t MN = (int64_t)M * N;
+    const bool vec = (N & 3) == 0 && splits == 1 && ((uintptr_t)y & 15) == 0;
+#pragma unroll 2
+    for (int f = 4 * tid; f < PER; f += 4 * kTileThreads) {
+        float4 s = *(const float4 *)(red + f);
 #pragma unroll
-    for (int half = 0; half < 2; half++)
-#pragma unroll
-        for (int vv = 0; vv < 4; vv++) {
-            const int v = 4 * kq + vv;
-            float t = red[((0 * 2 + wm) * 32 + 16 * half + v) * 64 + lane];
-#pragma unroll
-            for (int q = 1; q < 4; q++) t = t + red[((q * 2 + wm) * 32 + 16 * half + v) * 64 + lane];
-            fin[half][vv] = t;
+        for (int q = 1; q < C::KP; q++) {
+            const float4 t = *(const float4 *)(red + q * PER + f);
+            s.x = s.x + t.x; s.y = s.y + t.y; s.z = s.z + t.z; s.w = s.w + t.w;
         }
+        const int fw = f >> 11, v = (f >> 6) & 31, fl = f & 63;
+        const int vv = v & 15;
+        const int m = m0 + 32 * (fw & 1) + 8 * (vv >> 2) + 4 * (fl >> 5) + (vv & 3);
+        const int n = n0 + 64 * (fw >> 1) + 32 * (v >> 4) + (fl & 31);
+        if (m >= M) continue;
+        const int64_t idx = (int64_t)m * N + n;
+        if (vec && n + 3 < N) {
+            *(float4 *)(y + idx) = s;
+            continue;
+        }
+        const float sv[4] = {s.x, s.y, s.z, s.w};
 #pragma unroll
-    for (int half = 0; half < 2; half++) {
-        const int n = n0 + half * 32 + lr;
-        if (n >= N) continue;
-#pragma unroll
-        for (int vv = 0; vv < 4; vv++) {
-            const int m = m0 + wm * 32 + 8 * kq + 4 * lh + vv;
-            if (m >= M) continue;
-            const int64_t idx = (int64_t)m * N + n;
+        for (int e = 0; e < 4; e++) {
+            if (n + e >= N) break;
             if (splits == 1) {
-                y[idx] = fin[half][vv];
+                y[idx + e] = sv[e];
             } else {
-                const uint64_t word = ((uint64_t)epoch << 32) | __float_as_uint(fin[half][vv]);
-                __hip_atomic_store(part + (int64_t)z * M * N + idx, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t word = ((uint64_t)epoch << 32) | __float_as_uint(sv[e]);
+                __hip_atomic_store(part + (int64_t)z * MN + idx + e, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     }
+    VXM_TILE_TS(62, 2);
     if (splits == 1) return;
-    // split fix-up: count arrivals; the last one reduces the tagged partials in split order
+    // split fix-up: count arrivals; the last one adds the tagged partials in split order
     __syncthreads();
     const int tile = tm * tiles_n + tn;
     if (tid == 0) {
@@ -563,52 +1002,35 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
     }
     __syncthreads();
     if (!last_sh) return;
-    // thread t reduces elements t + 512 j, j < 8, four at a time: all 4 x splits words
-    // are requested before any tag is checked
-    constexpr int EPT = GM * GN / kGemmThreads, EPP = 4;
-    const int64_t MN = (int64_t)M * N;
+    bool stale = false;
+    for (int e = tid; e < GM * TN; e += kTileThreads) {
+        const int m = m0 + e / TN, n = n0 + e % TN;
+        if (m >= M || n >= N) continue;
+        const int64_t i = (int64_t)m * N + n;
+        uint64_t w[kGemmMaxSplits];
 #pragma unroll
-    for (int j0 = 0; j0 < EPT; j0 += EPP) {
-        uint64_t w[EPP][kGemmMaxSplits];
+        for (int zz = 0; zz < kGemmMaxSplits; zz++)
+            w[zz] = zz < splits ? __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                : ((uint64_t)epoch << 32);
+        float s = 0.0f;
+        bool st_e = false;
 #pragma unroll
-        for (int j = 0; j < EPP; j++) {
-            const int e = tid + kGemmThreads * (j0 + j), m = m0 + e / GN, nn = n0 + e % GN;
-            const bool live = m < M && nn < N;
-            const int64_t i = live ? (int64_t)m * N + nn : 0;
-#pragma unroll
-            for (int zz = 0; zz < kGemmMaxSplits; zz++)
-                w[j][zz] = (live && zz < splits)
-                               ? __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                               : ((uint64_t)epoch << 32);
-        }
-#pragma unroll
-        for (int j = 0; j < EPP; j++) {
-            const int e = tid + kGemmThreads * (j0 + j), m = m0 + e / GN, nn = n0 + e % GN;
-            if (m >= M || nn >= N) continue;
-            const int64_t i = (int64_t)m * N + nn;
-            float s = 0.0f;
-            bool stale = false;
-#pragma unroll
-            for (int zz = 0; zz < kGemmMaxSplits; zz++) {
-                if (zz >= splits) break;
-                uint64_t v = w[j][zz];
-                for (int spin = 0; (uint32_t)(v >> 32) != epoch && spin < kGemmSpin; spin++) {
-                    __builtin_amdgcn_s_sleep(1);
-                    v = __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-                stale |= (uint32_t)(v >> 32) != epoch;
-                const float p = __uint_as_float((uint32_t)v);
-                s = zz ? s + p : p;
+        for (int zz = 0; zz < kGemmMaxSplits; zz++) {
+            if (zz >= splits) break;
+            uint64_t v = w[zz];
+            for (int spin = 0; (uint32_t)(v >> 32) != epoch && spin < kGemmSpin; spin++) {
+                __builtin_amdgcn_s_sleep(1);
+                v = __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            // a partial that never arrived: a visible NaN and the context's error word
-            // (reported by vxm_sync), never a plausible-looking stale sum
-            if (stale) {
-                s = __builtin_nanf("");
-                __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            y[i] = s;
+            st_e |= (uint32_t)(v >> 32) != epoch;
+            const float p = __uint_as_float((uint32_t)v);
+            s = zz ? s + p : p;
         }
+        // a partial that never arrived: a visible NaN and the context's error word
+        y[i] = st_e ? __builtin_nanf("") : s;
+        stale |= st_e;
     }
+    if (stale) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -890,17 +1312,21 @@ __global__ void k_sum_parts(const float *__restrict__ p, int n, int64_t stride, 
     *(float4 *)(y + i) = s;
 }
 
-// Tile grid, stage depth and K split.  Single-row-tile GEMMs (M <= 64) take
-// 16-block stages, the others 8-block stages (two workgroups per CU); the K split (at most 4 ways, each part at least 2 stages)
-// brings the grid towards one workgroup per CU.
+// Tile grid, stage depth and K split of the register-staged GEMM
+// (k_gemm_q8_0_mfma).  Single-row-tile GEMMs (M <= 64) take 16-block stages,
+// the others 8-block stages (two workgroups per CU); the K split (at most 4
+// ways, each part at least 2 stages) brings the grid towards one workgroup per
+// CU.  tile_n > 0: k_gemm_q8_0_tile with 64 x tile_n tiles instead.
 struct GemmPlan {
     int tiles_m, tiles_n, splits, bps, ks;
+    int tile_n;
 };
 
 static GemmPlan gemm_plan(vxm_ctx *ctx, int64_t M, int N, int nb) {
     GemmPlan p;
     p.tiles_m = (int)((M + GM - 1) / GM);
     p.tiles_n = (N + GN - 1) / GN;
+    p.tile_n = 0;
     p.ks = p.tiles_m == 1 ? 16 : 8;
     int s = 1;
     // no split under graph capture: the split tags are per launch
@@ -910,6 +1336,74 @@ static GemmPlan gemm_plan(vxm_ctx *ctx, int64_t M, int N, int nb) {
     p.bps = (nb + s - 1) / s;
     p.splits = (nb + p.bps - 1) / p.bps;   // every split then owns at least one block
     return p;
+}
+
+#ifndef VXM_GEMM_TILE
+#define VXM_GEMM_TILE 1
+#endif
+
+// k_gemm_q8_0_tile plan: the tile width (64 or 128 columns) and K split with the
+// fewest block steps on the busiest CU, one workgroup per CU: rounds of the grid
+// x blocks per split x tile width (a 64 x 128 step costs twice a 64 x 64 one:
+// the per-block conversion work is per output), plus a fix-up charge per round
+// when the K is split.  Ties go to the wider tile (fewer operand bytes per
+// output).  Splits keep whole 8-block steps and at most kTileMaxBps blocks (the
+// activation scale panel); their partial words must fit max_split_bytes.
+// Returns false when the shape is not the tile kernel's (K % 256, alignment).
+static bool tile_plan(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                      size_t max_split_bytes, GemmPlan &best) {
+    const int N = (int)w->n, nb = (int)(w->k / 32);
+    if (!VXM_GEMM_TILE || !w->dt || nb % 8 != 0 || ((uintptr_t)xq & 15) || ((uintptr_t)xd & 15)) return false;
+    int64_t best_cost = -1;
+    for (int tn : {128, 64}) {
+        for (int s = 1; s <= kGemmMaxSplits; s++) {
+            const int bps = ((nb + s - 1) / s + 7) / 8 * 8;
+            const int splits = (nb + bps - 1) / bps;
+            if (bps > kTileMaxBps || splits != s) continue;
+            if (splits > 1 && (ctx->no_split_tags || (size_t)splits * M * N * sizeof(uint64_t) > max_split_bytes))
+                continue;
+            const int tiles_m = (int)((M + GM - 1) / GM), tiles_n = (N + tn - 1) / tn;
+            const int64_t wgs = (int64_t)tiles_m * tiles_n * splits, rounds = (wgs + ctx->n_cu - 1) / ctx->n_cu;
+            const int64_t cost = rounds * (bps + (splits > 1 ? 24 : 0)) * tn;
+            if (best_cost < 0 || cost < best_cost) {
+                best_cost = cost;
+                best.tiles_m = tiles_m;
+                best.tiles_n = tiles_n;
+                best.splits = splits;
+                best.bps = bps;
+                best.ks = 0;
+                best.tile_n = tn;
+            }
+        }
+    }
+    return best_cost >= 0;
+}
+
+// The tile kernel's dynamic LDS (4 stages + the scale panel, up to 157 KiB) is
+// above the default limit: raise it once per device for each instantiation.
+template <int TN, bool DOTS>
+static int launch_gemm_tile_t(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                              float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, uint32_t epoch) {
+    static std::atomic<uint64_t> attr_done{0};
+    const uint64_t bit = 1ull << (ctx->device & 63);
+    if (!(attr_done.load() & bit)) {
+        VXM_HIP(ctx, hipFuncSetAttribute((const void *)k_gemm_q8_0_tile<TN, DOTS>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)tile_lds_bytes(TN, kTileMaxBps)));
+        attr_done.fetch_or(bit);
+    }
+    const int grid_x = 8 * p.tiles_m * ((p.tiles_n + 7) / 8);
+    hipLaunchKernelGGL((k_gemm_q8_0_tile<TN, DOTS>), dim3(grid_x, p.splits), dim3(kTileThreads),
+                       (unsigned)tile_lds_bytes(TN, p.bps), ctx->stream, xq, xd, w->qs, w->dt, y, part, cnt, dots,
+                       (int)M, (int)w->n, (int)w->k, p.tiles_m, p.tiles_n, p.bps, p.splits, epoch, ctx->dev_err);
+    return VXM_OK;
+}
+
+template <bool DOTS>
+static int launch_gemm_tile(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                            float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, uint32_t epoch) {
+    return p.tile_n == 128 ? launch_gemm_tile_t<128, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch)
+                           : launch_gemm_tile_t<64, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch);
 }
 
 template <int KS>
@@ -959,7 +1453,8 @@ static int launch_gemm(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, cons
     if (!gemm_fits(M, N, K))
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "mul_mat: %lld x %d x %d exceeds the GEMM's 2 GiB operand range",
                         (long long)M, N, K);
-    const GemmPlan p = gemm_plan(ctx, M, N, nb);
+    GemmPlan p;
+    if (!tile_plan(ctx, w, xq, xd, M, wk ? wk->words_bytes : SIZE_MAX, p)) p = gemm_plan(ctx, M, N, nb);
     uint64_t *part = nullptr;
     int *cnt = nullptr;
     uint32_t epoch = 0;
@@ -990,8 +1485,14 @@ static int launch_gemm(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, cons
         }
         ctx->split_launched = true;
     }
-    if (p.ks == 16) launch_gemm_ks<16>(ctx, w, xq, xd, M, y, p, part, cnt, epoch);
-    else launch_gemm_ks<8>(ctx, w, xq, xd, M, y, p, part, cnt, epoch);
+    if (p.tile_n) {
+        int rc = launch_gemm_tile<false>(ctx, w, xq, xd, M, y, nullptr, p, part, cnt, epoch);
+        if (rc) return rc;
+    } else if (p.ks == 16) {
+        launch_gemm_ks<16>(ctx, w, xq, xd, M, y, p, part, cnt, epoch);
+    } else {
+        launch_gemm_ks<8>(ctx, w, xq, xd, M, y, p, part, cnt, epoch);
+    }
     VXM_CHECK_LAUNCH(ctx);
     return VXM_OK;
 }
@@ -1195,9 +1696,16 @@ static int launch_block_dots(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq
             if (!gemm_fits(M, N, K))
                 return vxm_fail(ctx, VXM_ERR_INVALID_ARG,
                                 "block_dots: %lld x %d x %d exceeds the GEMM's 2 GiB operand range", (long long)M, N, K);
-            const GemmPlan p = gemm_plan(ctx, M, N, K / 32);
-            if (p.ks == 16) launch_gemm_dots_ks<16>(ctx, w, xq, xd, M, out, p);
-            else launch_gemm_dots_ks<8>(ctx, w, xq, xd, M, out, p);
+            GemmPlan p;
+            if (!tile_plan(ctx, w, xq, xd, M, SIZE_MAX, p)) p = gemm_plan(ctx, M, N, K / 32);
+            if (p.tile_n) {
+                int rc = launch_gemm_tile<true>(ctx, w, xq, xd, M, nullptr, out, p, nullptr, nullptr, 0u);
+                if (rc) return rc;
+            } else if (p.ks == 16) {
+                launch_gemm_dots_ks<16>(ctx, w, xq, xd, M, out, p);
+            } else {
+                launch_gemm_dots_ks<8>(ctx, w, xq, xd, M, out, p);
+            }
         }
     } else {
         launch_gemv(ctx, w, xq, xd, M, nullptr, out);

@@ -212,10 +212,11 @@ int vxm_ensure_split(vxm_ctx *ctx, size_t bytes, size_t n_counters) {
 
 // ---- weight repack --------------------------------------------------------
 
-// One thread per 34-byte block: split into quants / scales / GEMV scales.
+// One thread per 34-byte block: split into quants / scales / GEMV scales /
+// tile-blocked GEMM scales.
 __global__ void k_repack_q8_0(const uint16_t *__restrict__ src, int64_t nblocks, int64_t nb,
                               int C, int8_t *__restrict__ qs, uint16_t *__restrict__ d,
-                              uint16_t *__restrict__ dg) {
+                              uint16_t *__restrict__ dg, uint16_t *__restrict__ dt) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblocks) return;
     const uint16_t *blk = src + i * 17;   // 34 bytes = 17 half-words, 2-byte aligned
@@ -230,6 +231,10 @@ __global__ void k_repack_q8_0(const uint16_t *__restrict__ src, int64_t nblocks,
         int64_t row = i / nb, b = i % nb;
         int64_t c = b / 32, p = b % 32;
         dg[row * nb + p * C + c] = blk[0];
+    }
+    if (dt) {
+        const int64_t row = i / nb, b = i % nb;
+        dt[(((row >> 6) * (nb >> 2) + (b >> 2)) * 64 + (row & 63)) * 4 + (b & 3)] = blk[0];
     }
 }
 
@@ -262,9 +267,11 @@ extern "C" int vxm_upload_q8_0(vxm_ctx *ctx, const void *gguf_rows, int64_t n_ro
     const int64_t nb = k / VXM_QK, nblocks = n_rows * nb;
     const size_t raw = (size_t)nblocks * VXM_BLOCK_BYTES;
     const bool gemv_perm = (k % 1024) == 0;
+    const bool tile_scales = (k % 256) == 0;
     const size_t qs_b = align256((size_t)n_rows * k);
     const size_t d_b = align256((size_t)nblocks * 2);
-    const size_t total = qs_b + d_b + (gemv_perm ? d_b : 0);
+    const size_t dt_b = tile_scales ? align256((size_t)((n_rows + 127) / 128) * 128 * nb * 2) : 0;
+    const size_t total = qs_b + d_b + (gemv_perm ? d_b : 0) + dt_b;
     vxm_weight *w = new vxm_weight();
     w->n = n_rows;
     w->k = k;
@@ -277,6 +284,7 @@ extern "C" int vxm_upload_q8_0(vxm_ctx *ctx, const void *gguf_rows, int64_t n_ro
     w->qs = (int8_t *)w->base;
     w->d = (uint16_t *)((char *)w->base + qs_b);
     w->dg = gemv_perm ? (uint16_t *)((char *)w->base + qs_b + d_b) : nullptr;
+    w->dt = tile_scales ? (uint16_t *)((char *)w->base + qs_b + d_b + (gemv_perm ? d_b : 0)) : nullptr;
     void *tmp = nullptr;
     if (hipMalloc(&tmp, raw) != hipSuccess) {
         (void)hipGetLastError();
@@ -285,13 +293,14 @@ extern "C" int vxm_upload_q8_0(vxm_ctx *ctx, const void *gguf_rows, int64_t n_ro
         return vxm_fail(ctx, VXM_ERR_OOM, "staging allocation of %zu bytes failed", raw);
     }
     int rc = VXM_OK;
-    if (hipMemcpyAsync(tmp, gguf_rows, raw, hipMemcpyHostToDevice, ctx->stream) != hipSuccess) {
+    if (hipMemcpyAsync(tmp, gguf_rows, raw, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        (w->dt && hipMemsetAsync(w->dt, 0, dt_b, ctx->stream) != hipSuccess)) {   // rows past n: zero scales
         rc = vxm_fail(ctx, VXM_ERR_BACKEND, "weight upload copy failed");
     } else {
         const int threads = 256;
         const int64_t grid = (nblocks + threads - 1) / threads;
         hipLaunchKernelGGL(k_repack_q8_0, dim3((unsigned)grid), dim3(threads), 0, ctx->stream,
-                           (const uint16_t *)tmp, nblocks, nb, (int)(k / 1024), w->qs, w->d, w->dg);
+                           (const uint16_t *)tmp, nblocks, nb, (int)(k / 1024), w->qs, w->d, w->dg, w->dt);
         if (hipGetLastError() != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess)
             rc = vxm_fail(ctx, VXM_ERR_BACKEND, "weight repack failed");
     }

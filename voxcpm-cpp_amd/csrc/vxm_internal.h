@@ -62,7 +62,10 @@ struct vxm_weight {
     int8_t *qs = nullptr;
     uint16_t *d = nullptr;
     uint16_t *dg = nullptr;
-    void *base = nullptr;   // single allocation holding qs, d, dg
+    // tile-blocked scales for the prefill GEMM (K % 256 == 0): 64-row groups
+    // g < 2 ceil(n / 128), each [k/128 steps][64 rows][4 blocks]; rows past n are zero
+    uint16_t *dt = nullptr;
+    void *base = nullptr;   // single allocation holding qs, d, dg, dt
     size_t bytes = 0;
 };
 
