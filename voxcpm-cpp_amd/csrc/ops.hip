@@ -320,37 +320,67 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ q, 
 // The same attention for many queries of one segment (prefill), on f16 MFMA
 // (v_mfma_f32_32x32x16_f16: lane l supplies A[l%32][8(l/32)..+8] and
 // B[8(l/32)..+8][l%32]; result register v of lane l is row 8(v/4) + 4(l/32)
-// + v%4, column l%32).  One workgroup (4 waves) per (query head, tile of
-// AQ = 32 consecutive tokens):
-//   scores  S = Q K^T * scale over the tile's key span [0, kv_end): the
-//           queries are BF16 values and the cache holds f16, both exact in
-//           f16, so every product is exact and only the fp32 summation order
-//           differs from the reference's; wave w takes key block w of each
-//           128-key stage;
-//   softmax per query row over its own kv_len (8 threads per row: max, expf,
-//           sum in double), p = e * (float)(1 / sum), 0 past kv_len;
-//   output  O = P V: wave w owns output dims [32w, 32w + 32); P enters the
-//           MFMA as f16 hi + lo halves (two products, ~22 bits of p), V as
-//           a transposed f16 tile.
+// + v%4, column l%32).  One workgroup of 8 waves (2 per SIMD) per (query
+// head, tile of AQ = 32 consecutive tokens).  Every phase is a chain of
+// dependent loads and products, so the work is cut into as many independent
+// chains as the waves:
+//   scores  S = Q K^T * scale, the tile's 32-key blocks of [0, kv_end) split
+//           into 8 contiguous runs, one per wave.  The queries are BF16 values
+//           and the cache holds f16, both exact in f16, so every product is
+//           exact and only the fp32 summation order differs from the
+//           reference's.  A lane's B operands (16 bytes of a key row) come
+//           straight from the cache; every load of a wave (Q, K and its V
+//           rows) is issued at once;
+//   softmax per query row over its own kv_len, on the scores in registers
+//           (computed as S^T = K Q^T, so a lane holds 16 keys of one query per
+//           block): max over the lane's keys, its partner lane's and the 8
+//           waves', e = expf(s - max), sums in double the same way, p = e *
+//           (float)(1 / sum), 0 past kv_len;
+//   output  wave (kq, dh) = (w % 4, w / 4) forms the partial P V of key quarter
+//           kq for dims [64 dh, 64 dh + 64): P enters the MFMA as f16 hi + lo
+//           halves (two products, ~22 bits of p), V through the wave's own LDS
+//           buffer, transposed as key-pair words; the four key quarters are
+//           added in order at the end.
 // The score buffer holds AKV keys: longer spans take k_attention.
 // ---------------------------------------------------------------------------
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
-constexpr int AQ = 32, AKV = 512, ATH = 256;
+constexpr int AQ = 32, AKV = 512, ATH = 512;
+
+#ifdef VXM_ATTN_TRACE
+// per-workgroup timestamps (s_memtime) of wave 0: [workgroup][entry, scores, softmax, P V, end]
+__device__ uint64_t vxm_attn_trace[4096 * 8];
+#define VXM_ATTN_TS(k)                                                                                        \
+    do {                                                                                                      \
+        if (tid == 0 && blockIdx.x * gridDim.y + blockIdx.y < 4096)                                           \
+            vxm_attn_trace[(blockIdx.x * gridDim.y + blockIdx.y) * 8 + (k)] = __builtin_amdgcn_s_memtime(); \
+    } while (0)
+#else
+#define VXM_ATTN_TS(k) \
+    do {               \
+    } while (0)
+#endif
 
 template <int HD>
 __global__ __launch_bounds__(ATH) void k_attention_mfma(const float *__restrict__ q, const uint16_t *__restrict__ kc,
                                                         const uint16_t *__restrict__ vc, float *__restrict__ out,
                                                         int M, int nh, int nkv, int cap, int kv_base, int causal) {
-    constexpr int QP = HD + 8;      // f16 row pitch of Q and K tiles (16-byte pad)
-    constexpr int KS = 128;         // keys per K stage (one 32-key block per wave)
-    constexpr int VS = 64;          // keys per V stage
-    constexpr int VP = VS + 8;      // f16 row pitch of the transposed V tile
-    constexpr int SP = AKV + 4;     // fp32 score row pitch
-    __shared__ __align__(16) _Float16 Qh[AQ * QP];
-    __shared__ __align__(16) _Float16 Kh[KS * QP];
-    __shared__ __align__(16) _Float16 Vt[HD * VP];
+    constexpr int NW = ATH / 64;       // waves
+    constexpr int SP = AKV + 4;        // fp32 P row pitch
+    constexpr int KSTEPS = HD / 16;    // MFMA steps over the head dimension
+    constexpr int HDH = HD / 2;        // dims of one output half
+    constexpr int DT = HDH / 32;       // 32-dim output tiles per wave
+    constexpr int VP = 32 + 8;         // f16 pitch of a wave's transposed V block (32 keys + pad)
+    constexpr int VITEMS = 16 * (HDH / 8) / 64;   // (key pair, 8-dim chunk) items per lane and block
+    constexpr int SB = AKV / 32 / NW;  // most score blocks of one wave
+    constexpr int VB = AKV / 32 / 4;   // most P V blocks of one key quarter
     __shared__ __align__(16) float Sc[AQ * SP];
+    __shared__ __align__(16) _Float16 Vt[NW][HDH * VP];
+    __shared__ float smax[AQ][NW];
+    __shared__ double ssum[AQ][NW];
+    constexpr int QP = HD + 8;         // f16 pitch of the query tile (16-byte pad)
+    __shared__ __align__(16) _Float16 Qh[AQ * QP];
+    static_assert(NW == 8 && VITEMS >= 1 && 4 * AQ * HD <= AQ * SP, "8 waves; the key-quarter sums reuse P's buffer");
     const int h = blockIdx.x, t0 = blockIdx.y * AQ, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kvh = h / (nh / nkv);
@@ -360,128 +390,188 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma(const float *__restrict_
     const int kv_end = causal ? kv_base + t0 + nq : M;
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
     const int lr = lane & 31, lh = lane >> 5;
-    for (int i = tid; i < AQ * HD; i += ATH) {
-        const int r = i / HD, d = i % HD;
-        Qh[r * QP + d] = (_Float16)(r < nq ? q[(int64_t)(t0 + r) * nh * HD + h * HD + d] : 0.0f);
+    const int nblk = (kv_end + 31) / 32;
+    const int bw0 = nblk * wave / NW, nbw = nblk * (wave + 1) / NW - bw0;   // this wave's score blocks
+    const int kq = wave & 3, dh = wave >> 2;
+    const int bq0 = nblk * kq / 4, nbq = nblk * (kq + 1) / 4 - bq0;        // its P V blocks
+    VXM_ATTN_TS(0);
+
+    // loads in the order they are needed: the query tile (once per workgroup, 4 values
+    // per thread and round, into LDS as f16) and the rows of the wave's score blocks'
+    // keys (A operands: 16 bytes of key 32 b + lr's row per step); after the scores, the
+    // V rows of its P V blocks (item (key pair p, dims 8c .. 8c+7 of its half), p = item
+    // % 16 fastest).
+    // Every load is unconditional (rows past the span, and blocks past a wave's share,
+    // read the clamped last row, whose values are masked or multiplied by p = 0), so the
+    // loads stay in one straight-line block and each product waits only for its own.
+    constexpr int QL = AQ * HD / 4 / ATH;   // float4 query loads per thread
+    float4 qf[QL];
+#pragma unroll
+    for (int u = 0; u < QL; u++) {
+        const int i = (u * ATH + tid) * 4, r = i / HD, d = i % HD;
+        qf[u] = *(const float4 *)(q + (int64_t)(t0 + min(r, nq - 1)) * nh * HD + h * HD + d);
     }
-    // pass 1: scores, 128 keys per stage; the next stage's keys are loaded during this
-    // stage's products
-    constexpr int NKL = KS * HD / (ATH * 8);                // 16-byte key loads per thread
-    constexpr int NVL = (VS / 2) * (HD / 8) / ATH;          // (key pair, 8-dim chunk) items per thread
-    static_assert(KS * HD % (ATH * 8) == 0 && (VS / 2) * (HD / 8) % ATH == 0 && VS == 64,
-                  "whole rounds of loads; 32 key pairs per V stage");
-    uint4 kreg[NKL];
-    auto load_k = [&](int k0) {
+    uint4 kr[SB][KSTEPS];
 #pragma unroll
-        for (int u = 0; u < NKL; u++) {
-            const int i = (u * ATH + tid) * 8, r = i / HD, d = i % HD;
-            kreg[u] = k0 + r < kv_end ? *(const uint4 *)(kb + (int64_t)(k0 + r) * HD + d) : make_uint4(0, 0, 0, 0);
-        }
-    };
-    load_k(0);
-    for (int k0 = 0; k0 < kv_end; k0 += KS) {
-        __syncthreads();
+    for (int i = 0; i < SB; i++) {
+        const int key = min(32 * (bw0 + i) + lr, kv_end - 1);
 #pragma unroll
-        for (int u = 0; u < NKL; u++) {
-            const int i = (u * ATH + tid) * 8, r = i / HD, d = i % HD;
-            *(uint4 *)(Kh + r * QP + d) = kreg[u];
-        }
-        __syncthreads();
-        if (k0 + KS < kv_end) load_k(k0 + KS);
-        const int kblk = k0 + 32 * wave;
-        if (kblk < kv_end) {
-            v16f c = v16f{};
+        for (int kk = 0; kk < KSTEPS; kk++) kr[i][kk] = *(const uint4 *)(kb + (int64_t)key * HD + 16 * kk + 8 * lh);
+    }
 #pragma unroll
-            for (int kk = 0; kk < HD / 16; kk++) {
-                const v8h a = *(const v8h *)(Qh + lr * QP + 16 * kk + 8 * lh);
-                const v8h b = *(const v8h *)(Kh + (32 * wave + lr) * QP + 16 * kk + 8 * lh);
-                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-            }
-#pragma unroll
-            for (int v = 0; v < 16; v++) Sc[(8 * (v >> 2) + 4 * lh + (v & 3)) * SP + kblk + lr] = c[v] * scale;
-        }
+    for (int u = 0; u < QL; u++) {
+        const int i = (u * ATH + tid) * 4, r = i / HD, d = i % HD;
+        const bool qlive = r < nq;
+        _Float16 *dst = Qh + r * QP + d;
+        dst[0] = (_Float16)(qlive ? qf[u].x : 0.0f);
+        dst[1] = (_Float16)(qlive ? qf[u].y : 0.0f);
+        dst[2] = (_Float16)(qlive ? qf[u].z : 0.0f);
+        dst[3] = (_Float16)(qlive ? qf[u].w : 0.0f);
     }
     __syncthreads();
-    // pass 2: softmax of each row over its kv_len (8 threads per row)
-    {
-        const int qi = tid >> 3, sub = tid & 7;
-        const int kvl = qi < nq ? (causal ? kv_base + t0 + qi + 1 : M) : 0;
-        float *row = Sc + qi * SP;
-        float mx = -INFINITY;
-        for (int j = sub; j < kvl; j += 8) mx = fmaxf(mx, row[j]);
+
+    // pass 1: scores of this wave's blocks in registers, as S^T = K Q^T (the key rows are
+    // the A operands, the queries the B operands): value v of block i in lane (lr, lh) is
+    // query t0 + lr, key 32 (bw0 + i) + kr(v) with kr(v) = 8 (v / 4) + 4 lh + v % 4
+    v8h qa[KSTEPS];   // B operands: query t0 + lr, dims 16 kk + 8 lh .. + 8
 #pragma unroll
-        for (int m = 4; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 8));
-        double sum = 0.0;
-        for (int j = sub; j < kvl; j += 8) {
-            const float e = expf(row[j] - mx);
-            row[j] = e;
-            sum += (double)e;
+    for (int kk = 0; kk < KSTEPS; kk++) qa[kk] = *(const v8h *)(Qh + lr * QP + 16 * kk + 8 * lh);
+    v16f sc[SB];
+#pragma unroll
+    for (int i = 0; i < SB; i++) {
+        v16f c = v16f{};
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; kk++) {
+            v8h av;
+            __builtin_memcpy(&av, &kr[i][kk], 16);
+            c = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qa[kk], c, 0, 0, 0);
         }
 #pragma unroll
-        for (int m = 4; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 8);
-        const float inv = kvl > 0 ? (float)(1.0 / sum) : 0.0f;
-        const int span = (kv_end + VS - 1) / VS * VS;
-        for (int j = sub; j < span; j += 8) row[j] = j < kvl ? row[j] * inv : 0.0f;
+        for (int v = 0; v < 16; v++) sc[i][v] = c[v] * scale;
     }
-    // pass 3: O = P V, 64 keys per stage; wave w < HD/32 owns dims [32w, 32w + 32)
-    v16f o = v16f{};
-    // V item (key pair p, dims 8c .. 8c+7), p = item % 32 fastest: the transposing 32-bit
-    // LDS writes of a wave land on distinct banks
-    uint4 vreg[NVL][2];
-    auto load_v = [&](int v0) {
+    // the V rows of the wave's P V blocks, in flight during the softmax
+    const uint16_t *vbh = vb + HDH * dh;
+    uint4 vr[VB][VITEMS][2];
 #pragma unroll
-        for (int u = 0; u < NVL; u++) {
-            const int item = u * ATH + tid, r = 2 * (item % 32), d = 8 * (item / 32);
+    for (int i = 0; i < VB; i++)
+#pragma unroll
+        for (int u = 0; u < VITEMS; u++) {
+            const int item = u * 64 + lane, r = 32 * (bq0 + i) + 2 * (item % 16), d = 8 * (item / 16);
 #pragma unroll
             for (int e = 0; e < 2; e++)
-                vreg[u][e] = v0 + r + e < kv_end ? *(const uint4 *)(vb + (int64_t)(v0 + r + e) * HD + d)
-                                                 : make_uint4(0, 0, 0, 0);
+                vr[i][u][e] = *(const uint4 *)(vbh + (int64_t)min(r + e, kv_end - 1) * HD + d);
         }
-    };
-    load_v(0);
-    for (int v0 = 0; v0 < kv_end; v0 += VS) {
-        __syncthreads();
-        // transpose: dims d .. d+7 of keys r, r+1 become 8 words (key r low, key r+1 high)
-        // in rows d .. d+7 of Vt
+    VXM_ATTN_TS(1);
+    // pass 2: softmax of query t0 + lr over its kv_len: max over the lane's keys, its
+    // partner lane's (lr + 32: the other half of every block) and the 8 waves' (through
+    // LDS); e = exp(s - max), the double sums the same way; p = e * (float)(1 / sum),
+    // 0 past kv_len
+    const int kvl = lr < nq ? (causal ? kv_base + t0 + lr + 1 : M) : 0;
+    auto live = [&](int i, int v) { return i < nbw && 32 * (bw0 + i) + 8 * (v >> 2) + 4 * lh + (v & 3) < kvl; };
+    float m = -INFINITY;
 #pragma unroll
-        for (int u = 0; u < NVL; u++) {
-            const int item = u * ATH + tid, r = 2 * (item % 32), d = 8 * (item / 32);
-            const uint32_t a[4] = {vreg[u][0].x, vreg[u][0].y, vreg[u][0].z, vreg[u][0].w};
-            const uint32_t b[4] = {vreg[u][1].x, vreg[u][1].y, vreg[u][1].z, vreg[u][1].w};
+    for (int i = 0; i < SB; i++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                *(uint32_t *)(Vt + (d + 2 * e) * VP + r) = (a[e] & 0xffffu) | (b[e] << 16);
-                *(uint32_t *)(Vt + (d + 2 * e + 1) * VP + r) = (a[e] >> 16) | (b[e] & 0xffff0000u);
-            }
-        }
-        __syncthreads();
-        if (v0 + VS < kv_end) load_v(v0 + VS);
-        if (wave < HD / 32) {
+        for (int v = 0; v < 16; v++)
+            if (live(i, v)) m = fmaxf(m, sc[i][v]);
+    m = fmaxf(m, __shfl_xor(m, 32));
+    if (lh == 0) smax[lr][wave] = m;
+    __syncthreads();
+    m = smax[lr][0];
 #pragma unroll
-            for (int ks = 0; ks < VS; ks += 16) {
-                const float *pr = Sc + lr * SP + v0 + ks + 8 * lh;
-                const float4 p0 = *(const float4 *)pr, p1 = *(const float4 *)(pr + 4);
-                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-                v8h ahi, alo;
+    for (int w = 1; w < NW; w++) m = fmaxf(m, smax[lr][w]);
+    double sum = 0.0;
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const _Float16 hi = (_Float16)pv[e];
-                    ahi[e] = hi;
-                    alo[e] = (_Float16)(pv[e] - (float)hi);
-                }
-                const v8h b = *(const v8h *)(Vt + (32 * wave + lr) * VP + ks + 8 * lh);
-                o = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, b, o, 0, 0, 0);
-                o = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, b, o, 0, 0, 0);
-            }
-        }
-    }
-    if (wave < HD / 32) {
+    for (int i = 0; i < SB; i++)
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            const int qi = 8 * (v >> 2) + 4 * lh + (v & 3);
-            if (qi < nq) out[(int64_t)(t0 + qi) * nh * HD + h * HD + 32 * wave + lr] = o[v];
+            const float e = live(i, v) ? expf(sc[i][v] - m) : 0.0f;
+            sc[i][v] = e;
+            sum += (double)e;
+        }
+    sum += __shfl_xor(sum, 32);
+    if (lh == 0) ssum[lr][wave] = sum;
+    __syncthreads();
+    sum = ssum[lr][0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) sum += ssum[lr][w];
+    const float inv = kvl > 0 ? (float)(1.0 / sum) : 0.0f;
+    // P rows in LDS: the lane's 4 runs of 4 consecutive keys per block
+#pragma unroll
+    for (int i = 0; i < SB; i++) {
+        if (i >= nbw) break;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; r4++)
+            *(float4 *)(Sc + lr * SP + 32 * (bw0 + i) + 8 * r4 + 4 * lh) =
+                make_float4(sc[i][4 * r4] * inv, sc[i][4 * r4 + 1] * inv, sc[i][4 * r4 + 2] * inv,
+                            sc[i][4 * r4 + 3] * inv);
+    }
+    __syncthreads();
+    VXM_ATTN_TS(2);
+    // pass 3: partial O = P V of key quarter kq, dims [64 dh, 64 dh + 64); each block's V
+    // goes to this wave's LDS buffer as key-pair words, dims as rows
+    v16f o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) o[dt] = v16f{};
+    _Float16 *vt = Vt[wave];
+#pragma unroll
+    for (int i = 0; i < VB; i++) {
+        if (i >= nbq) break;
+        const int b = bq0 + i;
+#pragma unroll
+        for (int u = 0; u < VITEMS; u++) {
+            const int item = u * 64 + lane, r = 2 * (item % 16), d = 8 * (item / 16);
+            const uint32_t a[4] = {vr[i][u][0].x, vr[i][u][0].y, vr[i][u][0].z, vr[i][u][0].w};
+            const uint32_t bb[4] = {vr[i][u][1].x, vr[i][u][1].y, vr[i][u][1].z, vr[i][u][1].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                *(uint32_t *)(vt + (d + 2 * e) * VP + r) = (a[e] & 0xffffu) | (bb[e] << 16);
+                *(uint32_t *)(vt + (d + 2 * e + 1) * VP + r) = (a[e] >> 16) | (bb[e] & 0xffff0000u);
+            }
+        }
+        // the wave's own LDS writes are seen by its later reads (one wave, in order)
+#pragma unroll
+        for (int ks = 0; ks < 32; ks += 16) {
+            const float *pr = Sc + lr * SP + 32 * b + ks + 8 * lh;
+            const float4 p0 = *(const float4 *)pr, p1 = *(const float4 *)(pr + 4);
+            const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+            v8h ahi, alo;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const _Float16 hi = (_Float16)pv[e];
+                ahi[e] = hi;
+                alo[e] = (_Float16)(pv[e] - (float)hi);
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                const v8h bv = *(const v8h *)(vt + (32 * dt + lr) * VP + ks + 8 * lh);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, bv, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, bv, o[dt], 0, 0, 0);
+            }
         }
     }
+    // the key quarters in order through LDS (P's buffer is free)
+    __syncthreads();
+    VXM_ATTN_TS(3);
+    float *red = Sc;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+            red[(kq * AQ + 8 * (v >> 2) + 4 * lh + (v & 3)) * HD + HDH * dh + 32 * dt + lr] = o[dt][v];
+    __syncthreads();
+    for (int i = 4 * tid; i < AQ * HD; i += 4 * ATH) {
+        const int qi = i / HD, d = i % HD;
+        if (qi >= nq) continue;
+        float4 s = *(const float4 *)(red + i);
+#pragma unroll
+        for (int w = 1; w < 4; w++) {
+            const float4 t = *(const float4 *)(red + w * AQ * HD + i);
+            s.x = s.x + t.x; s.y = s.y + t.y; s.z = s.z + t.z; s.w = s.w + t.w;
+        }
+        *(float4 *)(out + (int64_t)(t0 + qi) * nh * HD + h * HD + d) = s;
+    }
+    VXM_ATTN_TS(4);
 }
 
 int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
