@@ -274,6 +274,38 @@ def test_block_prefill_tiled_attention(vxm_ctx, orc, M, pos, hd):
     model.free()
 
 
+@pytest.mark.parametrize("M,F", [(100, 512), (512, 768)])
+def test_block_prefill_fused_swiglu_bit_identical(vxm_ctx, orc, M, F):
+    """Above 64 rows the gate/up GEMM applies SwiGLU and quantizes the down projection's
+    input in its own epilogue; PATH_MFMA_TILED runs the same GEMM followed by
+    k_swiglu_quant.  The block outputs and the appended KV rows are identical bit for bit."""
+    import vxm
+
+    rng = np.random.default_rng(41 + M)
+    H, nh, nkv, hd = 256, 4, 2, 64
+    lw = rand_layer(orc, rng, H, nh, nkv, hd, F)
+    c = cfg_dict(H, 1, nh, nkv, hd, F)
+    cap = 512
+    x = rng.normal(0, 1, (M, H)).astype(np.float32)
+    outs = []
+    for path in (vxm.PATH_AUTO, vxm.PATH_MFMA_TILED):
+        vxm_ctx.set_path(path)
+        try:
+            model = vxm.MiniCPM4(vxm_ctx, c, [lw])
+            kv = vxm.KVCache(vxm_ctx, 1, nkv, hd, cap)
+            xd = _dev(x)
+            model.block(kv, 0, xd, 0)
+            vxm_ctx.sync()
+            outs.append((xd.cpu().numpy(), kv.download(0)))
+            kv.free()
+            model.free()
+        finally:
+            vxm_ctx.set_path(vxm.PATH_AUTO)
+    (y0, kv0), (y1, kv1) = outs
+    assert np.array_equal(y0, y1)
+    assert all(np.array_equal(a, b) for a, b in zip(kv0, kv1))
+
+
 def test_block_noncausal_tiled_attention(vxm_ctx, orc):
     import vxm
 

@@ -33,32 +33,6 @@ __device__ __forceinline__ float block_max_f32(float v, float *sh) {
     return t;
 }
 
-// Quantize 32 values held 8 per lane by 4 consecutive lanes (lane & 3 = part)
-// with the x86 rule (id = 127/amax, round half even) or the _ref rule.
-__device__ __forceinline__ void quant_block_4lanes(const float v[8], int variant, int8_t *q8,
-                                                   uint16_t *dout, bool write_d) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    const float d = __fdiv_rn(amax, 127.0f);
-    float id;
-    if (variant == VXM_QUANT_X86) id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-    else id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        float q = variant == VXM_QUANT_X86 ? rintf(v[i] * id) : roundf(v[i] * id);
-        q = fminf(fmaxf(q, -128.0f), 127.0f);
-        const uint32_t b = (uint32_t)(uint8_t)(int8_t)(int)q;
-        if (i < 4) lo |= b << (8 * i);
-        else hi |= b << (8 * (i - 4));
-    }
-    *(uint2 *)q8 = make_uint2(lo, hi);
-    if (write_d) *dout = vxm_f2h(d);
-}
-
 // ---------------------------------------------------------------------------
 // [h = bf16(h + scale * bf16(delta))]; y = vcpm_rms_norm(h) (src/minicpm4.c:132-152):
 // ggml_rms_norm (sum of fp32 squares in double, mean = (float)(sum/n),

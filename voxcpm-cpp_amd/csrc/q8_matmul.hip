@@ -768,7 +768,7 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd, const int8_t *__restrict__ wq,
     const uint16_t *__restrict__ wt, float *__restrict__ y, uint64_t *__restrict__ part, int *__restrict__ cnt,
     int32_t *__restrict__ dots, int M, int N, int K, int tiles_m, int tiles_n, int bps, int splits,
-    uint32_t epoch, int *__restrict__ err) {
+    uint32_t epoch, int *__restrict__ err, int8_t *__restrict__ sq, uint16_t *__restrict__ sd, int variant) {
     using C = TileCfg<TN>;
     extern __shared__ __attribute__((aligned(16))) int8_t ring[];
     __shared__ int last_sh;
@@ -955,9 +955,40 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
         red[((kp * 2 * C::H + wi) * 32 + 16 + v) * 64 + lane] = acc[1][v];
     }
     __syncthreads();
+    constexpr int PER = 2 * C::H * 32 * 64;   // floats of one K part
+    if (sq) {
+        // gate/up with SwiGLU and Q8_0 (one split): columns 2n and 2n + 1 are gate n and
+        // up n, so the 64 columns of a row in one wave half are one 32-value block of
+        // p = vxm_swiglu(gate, up).  Four threads per (row, half): 16 columns each
+        const int F = N / 2;
+        if (tid < 4 * GM * C::H) {
+            const int bi = tid >> 2, part = tid & 3, mi = bi % GM, g = bi / GM;
+            const int r32 = mi & 31;
+            const int v = 16 * (part >> 1) + 4 * (r32 >> 3) + (r32 & 3);
+            const int f = (((mi >> 5) + 2 * g) * 32 + v) * 64 + 32 * ((r32 >> 2) & 1) + 16 * (part & 1);
+            float gu[16];
+#pragma unroll
+            for (int c4 = 0; c4 < 4; c4++) {
+                float4 t = *(const float4 *)(red + f + 4 * c4);
+#pragma unroll
+                for (int q = 1; q < C::KP; q++) {
+                    const float4 u = *(const float4 *)(red + q * PER + f + 4 * c4);
+                    t.x = t.x + u.x; t.y = t.y + u.y; t.z = t.z + u.z; t.w = t.w + u.w;
+                }
+                gu[4 * c4] = t.x; gu[4 * c4 + 1] = t.y; gu[4 * c4 + 2] = t.z; gu[4 * c4 + 3] = t.w;
+            }
+            float pv[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) pv[e] = vxm_swiglu(gu[2 * e], gu[2 * e + 1]);
+            const int m = m0 + mi;
+            const int64_t o = (int64_t)min(m, M - 1) * F + (n0 + 64 * g) / 2 + 8 * part;
+            // rows past M quantize too (the amax exchange needs all four lanes) but store nothing
+            quant_block_4lanes(pv, variant, sq + o, sd + o / 32, part == 0, m < M);
+        }
+        return;
+    }
     // four neighbouring lanes = four neighbouring columns of one row: 16-byte LDS
     // reads and (N % 4 == 0, the usual case) 16-byte stores
-    constexpr int PER = 2 * C::H * 32 * 64;   // floats of one K part
     const int64_t MN = (int64_t)M * N;
     const bool vec = (N & 3) == 0 && splits == 1 && ((uintptr_t)y & 15) == 0;
 #pragma unroll 2
@@ -1383,7 +1414,8 @@ static bool tile_plan(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const
 // above the default limit: raise it once per device for each instantiation.
 template <int TN, bool DOTS>
 static int launch_gemm_tile_t(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
-                              float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, uint32_t epoch) {
+                              float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, uint32_t epoch,
+                              int8_t *sq, uint16_t *sd, int variant) {
     static std::atomic<uint64_t> attr_done{0};
     const uint64_t bit = 1ull << (ctx->device & 63);
     if (!(attr_done.load() & bit)) {
@@ -1395,15 +1427,20 @@ static int launch_gemm_tile_t(vxm_ctx *ctx, const vxm_weight *w, const int8_t *x
     const int grid_x = 8 * p.tiles_m * ((p.tiles_n + 7) / 8);
     hipLaunchKernelGGL((k_gemm_q8_0_tile<TN, DOTS>), dim3(grid_x, p.splits), dim3(kTileThreads),
                        (unsigned)tile_lds_bytes(TN, p.bps), ctx->stream, xq, xd, w->qs, w->dt, y, part, cnt, dots,
-                       (int)M, (int)w->n, (int)w->k, p.tiles_m, p.tiles_n, p.bps, p.splits, epoch, ctx->dev_err);
+                       (int)M, (int)w->n, (int)w->k, p.tiles_m, p.tiles_n, p.bps, p.splits, epoch, ctx->dev_err,
+                       sq, sd, variant);
     return VXM_OK;
 }
 
+// sq != nullptr: SwiGLU + Q8_0 epilogue (gate/up weight with interleaved rows, one
+// split, N % 64 == 0) into sq [M][N/2], sd [M][N/64] instead of y
 template <bool DOTS>
 static int launch_gemm_tile(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
-                            float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, uint32_t epoch) {
-    return p.tile_n == 128 ? launch_gemm_tile_t<128, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch)
-                           : launch_gemm_tile_t<64, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch);
+                            float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, uint32_t epoch,
+                            int8_t *sq = nullptr, uint16_t *sd = nullptr, int variant = 0) {
+    return p.tile_n == 128
+               ? launch_gemm_tile_t<128, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant)
+               : launch_gemm_tile_t<64, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant);
 }
 
 template <int KS>
@@ -1606,19 +1643,28 @@ int vxm_launch_mul_mat_parts(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq
 }
 
 // The gate/up projection with SwiGLU and the Q8_0 of its output fused into the
-// small-M GEMM's epilogue (rows of w interleave gate n = row 2n and up n = row
-// 2n+1): sq [M][N/2] and sd [M][N/64] are the down projection's input.  Returns
-// false without launching when the small-M kernel does not take the product (the
-// tiled GEMM plus k_swiglu_quant are faster than a fused tiled epilogue at M = 512).
+// GEMM's epilogue (rows of w interleave gate n = row 2n and up n = row 2n+1): sq
+// [M][N/2] and sd [M][N/64] are the down projection's input.  The small-M kernel
+// takes M <= 64, the tile GEMM larger M when its plan needs no K split.  Returns
+// false without launching otherwise (and under PATH_MFMA_TILED, which keeps the
+// unfused GEMM + k_swiglu_quant as the reference of the fused epilogue).
 bool vxm_launch_gate_up_swiglu(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                                int8_t *sq, uint16_t *sd, int variant, int *rc) {
     *rc = VXM_OK;
     const int64_t N = w->n, K = w->k;
     const bool mfma = ctx->path == VXM_PATH_MFMA || (ctx->path == VXM_PATH_AUTO && M >= kSmallPartsMinRows);
+    if (!mfma || M <= 0 || N % 64) return false;
     SmallPlan sp;
-    if (!mfma || M <= 0 || N % 64 || !small_plan(ctx, M, N, K, 1, sp)) return false;
-    // unsplit: each workgroup holds whole 32-pair blocks over all of K
-    launch_small(ctx, w, xq, xd, M, nullptr, sp, sq, sd, variant);
+    if (small_plan(ctx, M, N, K, 1, sp)) {
+        // unsplit: each workgroup holds whole 32-pair blocks over all of K
+        launch_small(ctx, w, xq, xd, M, nullptr, sp, sq, sd, variant);
+    } else {
+        GemmPlan p;
+        if (!tile_plan(ctx, w, xq, xd, M, 0, p) || p.splits != 1) return false;
+        if ((*rc = launch_gemm_tile<false>(ctx, w, xq, xd, M, nullptr, nullptr, p, nullptr, nullptr, 0u, sq, sd,
+                                           variant)))
+            return true;
+    }
     if (hipGetLastError() != hipSuccess) *rc = vxm_fail(ctx, VXM_ERR_BACKEND, "gate/up + SwiGLU launch failed");
     return true;
 }

@@ -104,6 +104,43 @@ __device__ __forceinline__ uint16_t vxm_f2h(float f) {
 // (its payload bits may differ from the reference's).
 __device__ __forceinline__ float vxm_bf16(float f) { return (float)(__bf16)f; }
 
+// p = bf16(bf16(silu(bf16(g))) * bf16(u)): the SwiGLU product of vcpm_mlp
+// (src/minicpm4.c:432-463) with the reference's BF16 rounding points.
+__device__ __forceinline__ float vxm_swiglu(float g, float u) {
+    const float gb = vxm_bf16(g);
+    const float s = vxm_bf16(__fdiv_rn(gb, 1.0f + expf(-gb)));
+    return vxm_bf16(s * vxm_bf16(u));
+}
+
+// Q8_0 of one 32-value block held 8 per lane by four consecutive lanes (lane & 3
+// = part) with the x86 rule (id = 127/amax, round half even) or the _ref rule;
+// the lane with write_d set stores d.  write = false: compute (every lane of the
+// four takes part in the amax exchange) but store nothing.
+__device__ __forceinline__ void quant_block_4lanes(const float v[8], int variant, int8_t *q8,
+                                                   uint16_t *dout, bool write_d, bool write = true) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    const float d = __fdiv_rn(amax, 127.0f);
+    float id;
+    if (variant == VXM_QUANT_X86) id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    else id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        float q = variant == VXM_QUANT_X86 ? rintf(v[i] * id) : roundf(v[i] * id);
+        q = fminf(fmaxf(q, -128.0f), 127.0f);
+        const uint32_t b = (uint32_t)(uint8_t)(int8_t)(int)q;
+        if (i < 4) lo |= b << (8 * i);
+        else hi |= b << (8 * (i - 4));
+    }
+    if (!write) return;
+    *(uint2 *)q8 = make_uint2(lo, hi);
+    if (write_d) *dout = vxm_f2h(d);
+}
+
 // sum of 16 int8 x int8 products held as 4 packed dwords each
 __device__ __forceinline__ int vxm_dot16(const int4 a, const int4 b, int acc) {
     acc = __builtin_amdgcn_sdot4(a.x, b.x, acc, false);
