@@ -362,7 +362,7 @@ struct vxm_pparams {
     // tagged channels, each kRep replicas of rep_stride(words) words
     uint64_t *xb;      // 2 x [H/2] layer inputs (BF16 pairs), by layer parity
     uint64_t *qkvb;    // [NQKV/2] q, k (rope'd, pair-interleaved per head) and v (BF16 pairs)
-    uint64_t *attb;    // [QD] attention output (fp32)
+    uint64_t *attb;    // Q8_0 attention output: [NH][HD/4] quant words, then [NH][HD/32] scales (room for QD words)
     uint64_t *h1b;     // [H/2] BF16 pairs
     uint64_t *pb;      // [F/2] BF16 pairs
     uint64_t *attp;    // [NH][kAttSplitMax][kAttpWords] chunk partials (fp32), long contexts only
@@ -453,6 +453,40 @@ __device__ double read_words(const vxm_pparams &p, const uint64_t *src, int n, u
     return ss;
 }
 
+// Words [i0, i0 + n) of a Q8_0 channel: words below nq hold four quants each
+// (stored to xq as they are), the words from nq on one block scale each (to
+// xd[i - nq]).  Polls until every word carries tag.
+template <int NPL>
+__device__ void read_q8_words(const vxm_pparams &p, const uint64_t *src, int i0, int n, int nq, uint32_t tag,
+                              int8_t *xq, float *xd, int *bail) {
+    static_assert(NPL <= 64, "words per lane");
+    const int lane = tid_now() & 63;
+    uint64_t pending = 0;
+#pragma unroll
+    for (int k = 0; k < NPL; k++)
+        if (lane + 64 * k < n) pending |= 1ull << k;
+    int it = 0;
+    while (true) {
+        uint64_t w[NPL];
+#pragma unroll
+        for (int k = 0; k < NPL; k++)
+            if (pending & (1ull << k)) w[k] = get_word(src + i0 + lane + 64 * k);
+#pragma unroll
+        for (int k = 0; k < NPL; k++) {
+            if ((pending & (1ull << k)) && (uint32_t)(w[k] >> 32) == tag) {
+                const uint32_t v = (uint32_t)w[k];
+                const int i = i0 + lane + 64 * k;
+                if (i < nq) ((uint32_t *)xq)[i] = v;
+                else xd[i - nq] = __uint_as_float(v);
+                pending &= ~(1ull << k);
+            }
+        }
+        if (__all(pending == 0)) break;
+        if (give_up(p, it, bail)) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // Wave 0: wait until the first word of each of the n producers (word i * stride)
 // carries tag.  Used where the wait is long (the attention output), so that
 // 240 waiting workgroups read 16 words per round instead of 2048.
@@ -501,28 +535,28 @@ __device__ __forceinline__ float wg_max_f(float v, float *red) {
 // Q8_0 (x86 rule: id = 127/amax, round half even) of 4 values held by each
 // lane of an aligned group of 8 lanes (one 32-value block); writes the four
 // quants and, from the group's first lane, the fp16-rounded block scale.
-__device__ __forceinline__ void quant4(const float v[4], int8_t *xq4, float *xd1, bool first) {
+// The same in registers: the four quants packed low byte first, and the block
+// scale as the consumer uses it (fp16-rounded, as float).
+__device__ __forceinline__ void quant4_reg(const float v[4], uint32_t &w, float &dsc) {
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     amax = max8(amax);
     const float d = __fdiv_rn(amax, 127.0f);
     const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-    uint32_t w = 0;
+    w = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const float q = fminf(fmaxf(rintf(v[i] * id), -128.0f), 127.0f);
         w |= (uint32_t)(uint8_t)(int8_t)(int)q << (8 * i);
     }
-    *(uint32_t *)xq4 = w;
-    if (first) *xd1 = vxm_h2f(vxm_f2h(d));
+    dsc = vxm_h2f(vxm_f2h(d));
 }
 
-// Q8_0 of n values in LDS (n % 32 == 0), 4 values per thread.
-__device__ void quantize_lds(const float *src, int n, int8_t *xq, float *xd) {
-    for (int base = tid_now() * 4; base < n; base += kThreads * 4) {
-        const float4 a = *(const float4 *)(src + base);
-        const float v[4] = {a.x, a.y, a.z, a.w};
-        quant4(v, xq + base, xd + base / 32, (tid_now() & 7) == 0);
-    }
+__device__ __forceinline__ void quant4(const float v[4], int8_t *xq4, float *xd1, bool first) {
+    uint32_t w;
+    float dsc;
+    quant4_reg(v, w, dsc);
+    *(uint32_t *)xq4 = w;
+    if (first) *xd1 = dsc;
 }
 
 // Q8_0 of n BF16 values stored as pairs (low half first) in LDS, 4 values per thread.
@@ -1008,8 +1042,31 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
         // the next phase's input lands in the same LDS
         lds_barrier();
     }
-    // stored to kRep / (kThreads / HD) replicas
-    for (int r = tid / HD; r < kRep; r += kThreads / HD) put_word(p.attb + r * SAT + h * HD + d, __float_as_uint(v), tg);
+    // Q8_0 of the head's HD outputs, the quantization the O projection applies to
+    // its input (quant4 over aligned 32-value blocks, which never cross a head):
+    // word h HD/4 + i holds the quants of dims 4i .. 4i + 3 of head h, word
+    // NH HD/4 + h HD/32 + b the scale of its block b.  A quarter of the words of
+    // fp32 outputs, so each of the 256 readers of phase C loads a quarter of the
+    // bytes.  aq's q, k, v are dead here (their last reads precede the barriers
+    // above).
+    static_assert(HD % 32 == 0 && HD / 4 <= 64, "one wave quantizes a head");
+    if (tid < HD) aq[tid] = v;
+    lds_barrier();
+    if (wave == 0) {
+        const int i = lane % (HD / 4);   // lanes past HD / 4 repeat the first ones
+        const float4 a = *(const float4 *)(aq + 4 * i);
+        const float q4[4] = {a.x, a.y, a.z, a.w};
+        uint32_t w;
+        float dsc;
+        quant4_reg(q4, w, dsc);
+        if (lane < HD / 4) {
+#pragma unroll
+            for (int r = 0; r < kRep; r++) {
+                put_word(p.attb + r * SAT + h * (HD / 4) + i, w, tg);
+                if ((i & 7) == 0) put_word(p.attb + r * SAT + S::NH * (HD / 4) + h * (HD / 32) + i / 8, __float_as_uint(dsc), tg);
+            }
+        }
+    }
     VXM_TS(tid_now() == 0, 4);
 }
 
@@ -1124,20 +1181,20 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         }
         // ---------------- C: O rows + residual ----------------
         if (wave < kAttReaders) {
-            // waves 0 .. kAttReaders-1 each read a share; their rounds of loads are in flight together
+            // waves 0 .. kAttReaders-1 each read a share of the Q8_0 attention output
+            // (quants and scales straight into xq / xd); their rounds of loads are in
+            // flight together
             const uint64_t *src = p.attb + rp * SAT;
             const uint32_t tag = make_tag(ep, l, PH_ATT);
-            wait_sentinels(p, src, NH, HD, tag, bail);
-            constexpr int AW = QD / kAttReaders;
-            static_assert(AW % 64 == 0 && AW / 64 <= 64, "attention channel shares");
-            const int hf = wave * AW;
-            if (!*bail) read_words<AW / 64, false>(p, src + hf, AW, tag, big + hf, bail);
+            constexpr int NQW = NH * (HD / 4), NW = NQW + NH * (HD / 32), AW = cdiv(NW, kAttReaders);
+            static_assert(AW <= 64 * 64, "attention channel shares");
+            wait_sentinels(p, src, NH, HD / 4, tag, bail);
+            const int i0 = wave * AW;
+            if (!*bail) read_q8_words<cdiv(AW, 64)>(p, src, i0, min(AW, NW - i0), NQW, tag, xq, xd, bail);
         }
         lds_barrier();
         if (*bail) return;
         VXM_TS(tid_now() == 0, 5);
-        quantize_lds(big, QD, xq, xd);
-        lds_barrier();
         if (!reader) ring_phase<S, S::OC, S::SC>(ring, l, ci, lane, xq, xd, part);
         lds_barrier();
         VXM_TS(tid_now() == 0, 6);

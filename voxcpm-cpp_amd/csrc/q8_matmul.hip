@@ -658,7 +658,7 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
 // rows are never stored.
 //
 // Operand rows are RB bytes in LDS with the 16-byte piece p of row r stored
-// at p ^ (r % R16) (R16 = RB / 16 pieces), so the 32 rows of an MFMA operand
+// at p ^ swz(r) (R16 = RB / 16 pieces per row), so the 32 rows of an MFMA operand
 // read fall on distinct banks; each DMA lane simply loads the piece its LDS
 // position holds.  Each wave issues the same number of stage loads (wave 0
 // one more: the weight scales), so its own in-order load counter tells when
@@ -696,6 +696,12 @@ struct TileCfg {
     static constexpr int SB = 8 / H;                   // blocks per stage
     static constexpr int RB = SB * 32;                 // operand row bytes per stage
     static constexpr int R16 = RB / 16;                // 16-byte pieces per row
+    // LDS position of piece p of row r: p ^ swz(r).  An operand read of 16 bytes per
+    // lane is served 16 lanes (16 consecutive rows, one piece each) per 256 bytes of
+    // banks; 128-byte rows (TN = 128) put two rows in that span, so the even rows and
+    // the odd rows of any 16 must each take 8 distinct pieces, and any 8 consecutive
+    // rows too (the same reads served 8 lanes per 128 bytes)
+    static __device__ __forceinline__ int swz(int r) { return R16 == 8 ? (r & 7) ^ ((r >> 3) & 1) : r & 15; }
     static constexpr int ABytes = GM * RB, BBytes = TN * RB;
     static constexpr int Slot = ABytes + BBytes + 1024;   // + TN x SB weight scales
     static constexpr int LoadsAB = (ABytes + BBytes) / 1024 / 8;   // operand loads per wave and stage
@@ -807,7 +813,7 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
         if (i < C::LoadsAB) {
             const int q = wave * C::LoadsAB + i;
             const int rr = q * (64 / C::R16) + lane / C::R16;   // row of A (< 64) then B
-            const int pg = (lane % C::R16) ^ (rr % C::R16);
+            const int pg = (lane % C::R16) ^ C::swz(rr);
             const int8_t *src = rr < GM ? xq + (int64_t)min(m0 + rr, M - 1) * K
                                         : wq + (int64_t)min(n0 + rr - GM, N - 1) * K;
             lds_dma16(base + q * 1024, src + kb0 * 32 + pg * 16);
@@ -838,9 +844,9 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     // operands of block j of a stage: this lane's 16 bytes of its A row and of its two B rows
     auto operands = [&](const int8_t *sb, int j, v4i &a, v4i &w0, v4i &w1) {
         const int pc = 2 * j + lh;
-        a = *(const v4i *)(sb + a_off + ((pc ^ (ar % C::R16)) * 16));
-        w0 = *(const v4i *)(sb + b0_off + ((pc ^ (br0 % C::R16)) * 16));
-        w1 = *(const v4i *)(sb + b1_off + ((pc ^ (br1 % C::R16)) * 16));
+        a = *(const v4i *)(sb + a_off + ((pc ^ C::swz(ar)) * 16));
+        w0 = *(const v4i *)(sb + b0_off + ((pc ^ C::swz(br0)) * 16));
+        w1 = *(const v4i *)(sb + b1_off + ((pc ^ C::swz(br1)) * 16));
     };
     // conversion of values v0 <= v < v1 of a block's sums (both column halves)
     auto epi_part = [&](const v16i &c0, const v16i &c1, const v32f &sc, int v0, int v1) {
