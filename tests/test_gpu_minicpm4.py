@@ -306,6 +306,42 @@ def test_block_prefill_fused_swiglu_bit_identical(vxm_ctx, orc, M, F):
     assert all(np.array_equal(a, b) for a, b in zip(kv0, kv1))
 
 
+def test_block_prefill_fused_rope_and_attention_quant_bit_identical(vxm_ctx, orc):
+    """At the TSLM width and 512 tokens the QKV GEMM runs without a K split and takes
+    k_rope_kv's work (BF16 rounding, NEOX rope, q out, f16 K/V append) into its epilogue;
+    PATH_MFMA_TILED runs the same GEMM and then k_rope_kv.  Two chunks (cache rows 0 and
+    512 on): the block outputs and every cache row are identical bit for bit.  Both
+    paths quantize the attention output inside the MFMA attention kernel."""
+    import vxm
+
+    rng = np.random.default_rng(77)
+    H, nh, nkv, hd, F, M = 2048, 16, 2, 128, 6144, 512
+    lw = rand_layer(orc, rng, H, nh, nkv, hd, F)
+    c = cfg_dict(H, 1, nh, nkv, hd, F)
+    x = rng.normal(0, 1, (2, M, H)).astype(np.float32)
+    outs = []
+    for path in (vxm.PATH_AUTO, vxm.PATH_MFMA_TILED):
+        vxm_ctx.set_path(path)
+        try:
+            model = vxm.MiniCPM4(vxm_ctx, c, [lw])
+            kv = vxm.KVCache(vxm_ctx, 1, nkv, hd, 2 * M)
+            ys = []
+            for chunk in range(2):
+                xd = _dev(x[chunk])
+                model.block(kv, 0, xd, chunk * M)
+                vxm_ctx.sync()
+                ys.append(xd.cpu().numpy())
+            outs.append((ys, kv.download(0)))
+            kv.free()
+            model.free()
+        finally:
+            vxm_ctx.set_path(vxm.PATH_AUTO)
+    (y0, kv0), (y1, kv1) = outs
+    assert all(np.array_equal(a, b) for a, b in zip(y0, y1))
+    assert all(np.array_equal(a, b) for a, b in zip(kv0, kv1))
+    assert all(np.isfinite(a).all() for a in y0)
+
+
 def test_block_noncausal_tiled_attention(vxm_ctx, orc):
     import vxm
 

@@ -207,9 +207,18 @@ int vxm_block_run(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_block &b, vxm
     const int64_t qd = (int64_t)d.nh * d.hd, kvd = (int64_t)d.nkv * d.hd;
     const int var = ctx->quant_variant;
     int rc, np;
-    if ((rc = vxm_launch_mul_mat_parts(ctx, b.wqkv, ws.xq, ws.xd, M, ws.qkv, ws.max_parts, &np))) return rc;
     const bool local = !site.causal && site.cache_pos0 == 0 && site.S > 0 && M % site.S == 0 &&
                        vxm_attention_local_fits(site.S, d.hd);
+    // many tokens: k_rope_kv's work in the QKV GEMM's epilogue where its plan allows
+    bool fused_rope = false;
+    if (!local) {
+        const vxm_qkv_epi qe{ws.q, site.kc, site.vc, d.rope_cs, site.seg_stride, d.nh, d.nkv, (int)d.hd,
+                             site.pos0, site.S, d.no_rope, site.cap, site.cache_pos0};
+        fused_rope = vxm_launch_qkv_rope(ctx, b.wqkv, ws.xq, ws.xd, M, qe, d.rope_rows, &rc);
+        if (rc) return rc;
+    }
+    if (!fused_rope && (rc = vxm_launch_mul_mat_parts(ctx, b.wqkv, ws.xq, ws.xd, M, ws.qkv, ws.max_parts, &np)))
+        return rc;
     if (local) {
         // fresh K/V within each segment: RoPE, attention and the output's Q8_0 in one launch
         if ((rc = vxm_launch_attention_local(ctx, vxm_parts{ws.qkv, np, M * (qd + 2 * kvd)}, M, d.nh, d.nkv, d.hd,
@@ -217,14 +226,15 @@ int vxm_block_run(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_block &b, vxm
                                              var)))
             return rc;
     } else {
-        if ((rc = vxm_launch_rope_kv(ctx, vxm_parts{ws.qkv, np, M * (qd + 2 * kvd)}, M, d.nh, d.nkv, d.hd,
+        if (!fused_rope &&
+            (rc = vxm_launch_rope_kv(ctx, vxm_parts{ws.qkv, np, M * (qd + 2 * kvd)}, M, d.nh, d.nkv, d.hd,
                                      site.pos0, site.S, d.rope_cs, d.rope_rows, d.no_rope, ws.q, site.kc, site.vc,
                                      site.cap, site.seg_stride, site.cache_pos0)))
             return rc;
+        // attention with the Q8_0 of its output rows (the O projection's input)
         if ((rc = vxm_launch_attention(ctx, ws.q, site.kc, site.vc, ws.att, M, d.nh, d.nkv, d.hd, site.cap,
-                                       site.seg_stride, site.S, site.cache_pos0, site.causal)))
+                                       site.seg_stride, site.S, site.cache_pos0, site.causal, ws.xq, ws.xd, var)))
             return rc;
-        if ((rc = vxm_launch_quantize(ctx, ws.att, M, qd, var, ws.xq, ws.xd))) return rc;
     }
     if ((rc = vxm_launch_mul_mat_parts(ctx, b.wo, ws.xq, ws.xd, M, ws.o, ws.max_parts, &np))) return rc;
     // x = bf16(x + scale*bf16(o)); post-attention norm -> Q8_0

@@ -338,7 +338,9 @@ __device__ uint64_t vxm_attn_trace[4096 * 8];
 template <int HD>
 __global__ __launch_bounds__(ATH) void k_attention_mfma(const float *__restrict__ q, const uint16_t *__restrict__ kc,
                                                         const uint16_t *__restrict__ vc, float *__restrict__ out,
-                                                        int M, int nh, int nkv, int cap, int kv_base, int causal) {
+                                                        int M, int nh, int nkv, int cap, int kv_base, int causal,
+                                                        int8_t *__restrict__ xq, uint16_t *__restrict__ xd,
+                                                        int variant) {
     constexpr int NW = ATH / 64;       // waves
     constexpr int SP = AKV + 4;        // fp32 P row pitch
     constexpr int KSTEPS = HD / 16;    // MFMA steps over the head dimension
@@ -534,23 +536,45 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma(const float *__restrict_
         for (int v = 0; v < 16; v++)
             red[(kq * AQ + 8 * (v >> 2) + 4 * lh + (v & 3)) * HD + HDH * dh + 32 * dt + lr] = o[dt][v];
     __syncthreads();
-    for (int i = 4 * tid; i < AQ * HD; i += 4 * ATH) {
-        const int qi = i / HD, d = i % HD;
-        if (qi >= nq) continue;
-        float4 s = *(const float4 *)(red + i);
+    if (xq) {
+        // Q8_0 of the output rows (the O projection's input; the arithmetic of
+        // k_quantize_q8_0): 8 values per lane, 4 lanes per 32-value block, the
+        // blocks of a row never crossing a head
+        for (int i = 8 * tid; i < AQ * HD; i += 8 * ATH) {
+            const int qi = i / HD, d = i % HD;
+            float v[8];
 #pragma unroll
-        for (int w = 1; w < 4; w++) {
-            const float4 t = *(const float4 *)(red + w * AQ * HD + i);
-            s.x = s.x + t.x; s.y = s.y + t.y; s.z = s.z + t.z; s.w = s.w + t.w;
+            for (int hf = 0; hf < 2; hf++) {
+                float4 s = *(const float4 *)(red + i + 4 * hf);
+#pragma unroll
+                for (int w = 1; w < 4; w++) {
+                    const float4 t = *(const float4 *)(red + w * AQ * HD + i + 4 * hf);
+                    s.x = s.x + t.x; s.y = s.y + t.y; s.z = s.z + t.z; s.w = s.w + t.w;
+                }
+                v[4 * hf] = s.x; v[4 * hf + 1] = s.y; v[4 * hf + 2] = s.z; v[4 * hf + 3] = s.w;
+            }
+            const int64_t o = (int64_t)(t0 + min(qi, nq - 1)) * nh * HD + h * HD + d;
+            quant_block_4lanes(v, variant, xq + o, xd + o / 32, (tid & 3) == 0, qi < nq);
         }
-        *(float4 *)(out + (int64_t)(t0 + qi) * nh * HD + h * HD + d) = s;
+    } else {
+        for (int i = 4 * tid; i < AQ * HD; i += 4 * ATH) {
+            const int qi = i / HD, d = i % HD;
+            if (qi >= nq) continue;
+            float4 s = *(const float4 *)(red + i);
+#pragma unroll
+            for (int w = 1; w < 4; w++) {
+                const float4 t = *(const float4 *)(red + w * AQ * HD + i);
+                s.x = s.x + t.x; s.y = s.y + t.y; s.z = s.z + t.z; s.w = s.w + t.w;
+            }
+            *(float4 *)(out + (int64_t)(t0 + qi) * nh * HD + h * HD + d) = s;
+        }
     }
     VXM_ATTN_TS(4);
 }
 
 int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
                          int64_t M, int nh, int nkv, int hd, int cap, int64_t seg_stride, int S, int kv_base,
-                         int causal) {
+                         int causal, int8_t *xq, uint16_t *xd, int variant) {
     if (M <= 0) return VXM_OK;
     if (hd > 256 || hd <= 0 || nkv <= 0 || nh % nkv)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "attention: head_dim %d / heads %d,%d unsupported", hd, nh, nkv);
@@ -560,10 +584,10 @@ int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const
         const dim3 grid(nh, (unsigned)((M + AQ - 1) / AQ));
         if (hd == 128)
             hipLaunchKernelGGL(k_attention_mfma<128>, grid, dim3(ATH), 0, ctx->stream, q, kc, vc, out, (int)M, nh,
-                               nkv, cap, kv_base, causal);
+                               nkv, cap, kv_base, causal, xq, xd, variant);
         else
             hipLaunchKernelGGL(k_attention_mfma<64>, grid, dim3(ATH), 0, ctx->stream, q, kc, vc, out, (int)M, nh,
-                               nkv, cap, kv_base, causal);
+                               nkv, cap, kv_base, causal, xq, xd, variant);
         VXM_CHECK_LAUNCH(ctx);
         return VXM_OK;
     }
@@ -573,7 +597,7 @@ int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const
     hipLaunchKernelGGL(k_attention, dim3(nh, (unsigned)M), dim3(256), lds, ctx->stream, q, kc, vc, out, nh, nkv,
                        hd, cap, seg_stride, S, kv_base, causal);
     VXM_CHECK_LAUNCH(ctx);
-    return VXM_OK;
+    return xq ? vxm_launch_quantize(ctx, out, M, (int64_t)nh * hd, variant, xq, xd) : VXM_OK;
 }
 
 // ---------------------------------------------------------------------------

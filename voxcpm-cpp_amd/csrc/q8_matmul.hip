@@ -774,7 +774,8 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd, const int8_t *__restrict__ wq,
     const uint16_t *__restrict__ wt, float *__restrict__ y, uint64_t *__restrict__ part, int *__restrict__ cnt,
     int32_t *__restrict__ dots, int M, int N, int K, int tiles_m, int tiles_n, int bps, int splits,
-    uint32_t epoch, int *__restrict__ err, int8_t *__restrict__ sq, uint16_t *__restrict__ sd, int variant) {
+    uint32_t epoch, int *__restrict__ err, int8_t *__restrict__ sq, uint16_t *__restrict__ sd, int variant,
+    const vxm_qkv_epi qe) {
     using C = TileCfg<TN>;
     extern __shared__ __attribute__((aligned(16))) int8_t ring[];
     __shared__ int last_sh;
@@ -1010,6 +1011,45 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
         const int m = m0 + 32 * (fw & 1) + 8 * (vv >> 2) + 4 * (fl >> 5) + (vv & 3);
         const int n = n0 + 64 * (fw >> 1) + 32 * (v >> 4) + (fl & 31);
         if (m >= M) continue;
+        if (qe.q_out) {
+            // k_rope_kv on columns n .. n + 3 of token m (one split, N % 4 == 0): two
+            // rope pairs of q or k (rows 2i, 2i + 1 of a head are dims i, i + hd/2),
+            // or four values of v
+            const int qd = qe.nh * qe.hd, kvd = qe.nkv * qe.hd, half = qe.hd / 2;
+            const int seg = m / qe.S, ti = m % qe.S, cpos = qe.cache_pos0 + ti;
+            const float sv[4] = {s.x, s.y, s.z, s.w};
+            if (n < qd + kvd) {
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                    const int c = n + e;
+                    const bool isq = c < qd;
+                    const int cc = isq ? c : c - qd, head = cc / qe.hd, i = (cc % qe.hd) / 2;
+                    const float x0 = vxm_bf16(sv[e]), x1 = vxm_bf16(sv[e + 1]);
+                    float y0 = x0, y1 = x1;
+                    if (!qe.no_rope) {
+                        const float2 r = qe.cs[(int64_t)(qe.pos0 + ti) * half + i];
+                        y0 = vxm_bf16(x0 * r.x - x1 * r.y);
+                        y1 = vxm_bf16(x0 * r.y + x1 * r.x);
+                    }
+                    if (isq) {
+                        float *qo = qe.q_out + (int64_t)m * qd + head * qe.hd;
+                        qo[i] = y0;
+                        qo[i + half] = y1;
+                    } else {
+                        uint16_t *kd = qe.kc + seg * qe.seg_stride + ((int64_t)head * qe.cap + cpos) * qe.hd;
+                        kd[i] = vxm_f2h(y0);
+                        kd[i + half] = vxm_f2h(y1);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int c = n + e - qd - kvd, kh = c / qe.hd, dd = c % qe.hd;
+                    qe.vc[seg * qe.seg_stride + ((int64_t)kh * qe.cap + cpos) * qe.hd + dd] = vxm_f2h(vxm_bf16(sv[e]));
+                }
+            }
+            continue;
+        }
         const int64_t idx = (int64_t)m * N + n;
         if (vec && n + 3 < N) {
             *(float4 *)(y + idx) = s;
@@ -1421,7 +1461,7 @@ static bool tile_plan(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const
 template <int TN, bool DOTS>
 static int launch_gemm_tile_t(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                               float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, uint32_t epoch,
-                              int8_t *sq, uint16_t *sd, int variant) {
+                              int8_t *sq, uint16_t *sd, int variant, const vxm_qkv_epi &qe) {
     static std::atomic<uint64_t> attr_done{0};
     const uint64_t bit = 1ull << (ctx->device & 63);
     if (!(attr_done.load() & bit)) {
@@ -1434,19 +1474,21 @@ static int launch_gemm_tile_t(vxm_ctx *ctx, const vxm_weight *w, const int8_t *x
     hipLaunchKernelGGL((k_gemm_q8_0_tile<TN, DOTS>), dim3(grid_x, p.splits), dim3(kTileThreads),
                        (unsigned)tile_lds_bytes(TN, p.bps), ctx->stream, xq, xd, w->qs, w->dt, y, part, cnt, dots,
                        (int)M, (int)w->n, (int)w->k, p.tiles_m, p.tiles_n, p.bps, p.splits, epoch, ctx->dev_err,
-                       sq, sd, variant);
+                       sq, sd, variant, qe);
     return VXM_OK;
 }
 
 // sq != nullptr: SwiGLU + Q8_0 epilogue (gate/up weight with interleaved rows, one
 // split, N % 64 == 0) into sq [M][N/2], sd [M][N/64] instead of y
+// qe.q_out != nullptr: the QKV epilogue (k_rope_kv's work, one split) instead of y
 template <bool DOTS>
 static int launch_gemm_tile(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                             float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, uint32_t epoch,
-                            int8_t *sq = nullptr, uint16_t *sd = nullptr, int variant = 0) {
+                            int8_t *sq = nullptr, uint16_t *sd = nullptr, int variant = 0,
+                            const vxm_qkv_epi &qe = vxm_qkv_epi{}) {
     return p.tile_n == 128
-               ? launch_gemm_tile_t<128, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant)
-               : launch_gemm_tile_t<64, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant);
+               ? launch_gemm_tile_t<128, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant, qe)
+               : launch_gemm_tile_t<64, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant, qe);
 }
 
 template <int KS>
@@ -1672,6 +1714,34 @@ bool vxm_launch_gate_up_swiglu(vxm_ctx *ctx, const vxm_weight *w, const int8_t *
             return true;
     }
     if (hipGetLastError() != hipSuccess) *rc = vxm_fail(ctx, VXM_ERR_BACKEND, "gate/up + SwiGLU launch failed");
+    return true;
+}
+
+// The QKV projection with k_rope_kv's work in the tile GEMM's epilogue (qe):
+// taken where vxm_launch_mul_mat_parts would run the tile GEMM without a K
+// split (M > 64 and a plan of one split), so the products are the same.
+// Returns false without launching otherwise, and under PATH_MFMA_TILED (which
+// keeps the GEMM + k_rope_kv pair as the reference of the fused epilogue).
+static bool use_mfma(const vxm_ctx *ctx, int64_t M);
+
+bool vxm_launch_qkv_rope(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                         const vxm_qkv_epi &qe, int cs_rows, int *rc) {
+    *rc = VXM_OK;
+    if (M <= VXM_SMALL_MAX_ROWS || !use_mfma(ctx, M) || ctx->path == VXM_PATH_MFMA_TILED || !qe.q_out) return false;
+    const int64_t N = w->n;
+    if (qe.hd % 4 || N != (int64_t)(qe.nh + 2 * qe.nkv) * qe.hd || qe.S <= 0) return false;
+    if (!gemm_fits(M, (int)N, (int)w->k)) return false;
+    GemmPlan p;
+    if (!tile_plan(ctx, w, xq, xd, M, SIZE_MAX, p) || p.splits != 1) return false;
+    if (!qe.no_rope && (!qe.cs || qe.pos0 + std::min<int64_t>(M, qe.S) > cs_rows)) {
+        *rc = vxm_fail(ctx, VXM_ERR_BACKEND, "rope: table holds %d positions, %lld needed", cs_rows,
+                       (long long)(qe.pos0 + std::min<int64_t>(M, qe.S)));
+        return true;
+    }
+    if ((*rc = launch_gemm_tile<false>(ctx, w, xq, xd, M, nullptr, nullptr, p, nullptr, nullptr, 0u, nullptr, nullptr,
+                                       0, qe)))
+        return true;
+    if (hipGetLastError() != hipSuccess) *rc = vxm_fail(ctx, VXM_ERR_BACKEND, "QKV + rope launch failed");
     return true;
 }
 

@@ -190,6 +190,18 @@ int vxm_launch_mul_mat_parts(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq
                              int64_t M, float *y, int max_parts, int *parts);
 bool vxm_launch_gate_up_swiglu(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                                int8_t *sq, uint16_t *sd, int variant, int *rc);
+// What k_rope_kv does with the QKV projection's rows (BF16 rounding, NEOX rope
+// of the pair-interleaved q and k rows, q out as fp32, k and v into the f16
+// cache), done instead by the GEMM's epilogue.  q_out == nullptr: off.
+struct vxm_qkv_epi {
+    float *q_out;             // [M][nh*hd]
+    uint16_t *kc, *vc;        // cache of the layer: [seg][nkv][cap][hd]
+    const float2 *cs;         // rope (cos, sin) table [pos][hd/2]
+    int64_t seg_stride;
+    int nh, nkv, hd, pos0, S, no_rope, cap, cache_pos0;
+};
+bool vxm_launch_qkv_rope(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                         const vxm_qkv_epi &qe, int cs_rows, int *rc);
 int vxm_ensure_act(vxm_ctx *ctx, size_t bytes);
 // Finds the allocation-free matmul's scratch array on ctx's (current) device.
 int vxm_scratch_setup(vxm_ctx *ctx);
