@@ -401,7 +401,10 @@ __device__ __forceinline__ vxm_ptab layer_at(const vxm_pparams &p, int l) {
 }
 
 __device__ __forceinline__ bool give_up(const vxm_pparams &p, int &it, int *bail) {
-    if (++it > kSpin || __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+    // the error word (another workgroup gave up) is polled every 32nd round:
+    // each read of it is one more round trip to the memory side (631 -> 628 us
+    // per token)
+    if (++it > kSpin || ((it & 31) == 0 && __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
         __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *bail = 1;
         return true;
@@ -609,7 +612,10 @@ struct Slot {
 };
 
 // The ring's loads: direct-to-LDS DMA issued as inline asm.  Lane l of
-// global_load_lds_dwordx4 writes its 16 bytes at M0 + 16 l.  A unit is three
+// global_load_lds_dwordx4 writes its 16 bytes at M0 + 16 l.  The loads are
+// non-temporal (nt): each weight byte is read once per token, and keeping it
+// out of the caches leaves them to the exchanged words: 635 -> 631 us per
+// token.  A unit is three
 // instructions: quants [0, 1024) and [1024, 2048) by all lanes, and the 128
 // bytes of scales by lanes 0..7 (exec narrowed inside the asm and restored).
 // Before the DMA overwrites a slot, lgkmcnt(0) guarantees that the wave's
@@ -628,15 +634,15 @@ __device__ __forceinline__ void dma_unit(uint32_t lds_slot, const int8_t *q, con
         "s_mov_b32 %1, m0\n\t"
         "s_mov_b32 m0, %2\n\t"
         "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %3, off\n\t"
+        "global_load_lds_dwordx4 %3, off nt\n\t"
         "s_add_u32 m0, m0, 1024\n\t"
         "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %4, off\n\t"
+        "global_load_lds_dwordx4 %4, off nt\n\t"
         "s_add_u32 m0, m0, 1024\n\t"
         "s_mov_b64 %0, exec\n\t"
         "s_mov_b64 exec, 0xff\n\t"
         "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %5, off\n\t"
+        "global_load_lds_dwordx4 %5, off nt\n\t"
         "s_mov_b64 exec, %0\n\t"
         "s_mov_b32 m0, %1"
         : "=&s"(saved), "=&s"(saved_m0)
@@ -927,6 +933,7 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
             }
         }
     }
+    VXM_TS(tid_now() == 0, 2);
     mx = wg_max_f(mx, red);
     double sum = 0.0;
     for (int j = tid; j < j1 - j0; j += kThreads) {
@@ -938,6 +945,7 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     const float inv = (float)(1.0 / sum);
     for (int j = tid; j < j1 - j0; j += kThreads) sc[j] = sc[j] * inv;
     lds_barrier();
+    VXM_TS(tid_now() == 0, 11);
     // out[d] = sum_j p_j v_j[d]: lane (kin, sub) accumulates dims sub*8..+8 over its keys
     float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int jb = j0; jb < j1; jb += PERB) {

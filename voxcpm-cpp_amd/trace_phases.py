@@ -6,6 +6,7 @@ of 2 + 12 * layers 64-bit values of the 100 MHz real-time counter -- [0] the wor
 l at 2 + 12 l + k:
   k = 0  layer input x read (phase A may start)     k = 1  A's QKV rows computed
   k = 3  attention inputs read (attention workgroups) k = 4 attention output published
+  k = 2  scores computed (attention workgroups)      k = 11 softmax done, P.V starts
   k = 5  attention output read (C may start)        k = 6  C's O rows computed
   k = 7  h1 read (D may start)                      k = 8  D's gate / up rows computed
   k = 9  p read (E may start)                       k = 10 E's down rows computed
@@ -39,6 +40,9 @@ def phases(t, L):
         "A: norm + QKV rows": s(1) - s(0),
         "hop A -> attention inputs": np.where(att, s(3) - s(1), nan),
         "attention (incl. chunk merge)": np.where(att, s(4) - s(3), nan),
+        "  scores (K rows landed + q.k)": np.where(att, s(2) - s(3), nan),
+        "  softmax": np.where(att, s(11) - s(2), nan),
+        "  P.V + reduction + Q8_0 + publish": np.where(att, s(4) - s(11), nan),
         "hop attention -> C inputs": np.where(att, s(5) - s(4), nan),
         "A end -> C inputs (every workgroup)": s(5) - s(1),
         "C: O rows + residual": s(6) - s(5),
