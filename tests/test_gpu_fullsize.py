@@ -39,6 +39,11 @@ H, NH, NKV, HD, F, L = 2048, 16, 2, 128, 6144, 28
 LAYER_REL, LAYER_ROW = 1e-2, 2.0 ** -5      # one layer fed identical inputs
 STACK_COS, STACK_REL = 0.995, 0.1           # 28 layers
 KV_EQ, KV_REL = 0.99, 1e-3                  # K / V rows from identical inputs
+# A K / V element from identical inputs can differ only by the fp32 order of its
+# projection's block terms: at most one BF16 ulp (2^-7 of the value) before the
+# rotary pair mixes it into two elements of at most sqrt(2) times the row max,
+# plus the f16 rounding of the cache
+KV_ULP = 2.0 ** -6
 
 
 def assert_one_layer(y, ref, what):
@@ -103,6 +108,13 @@ def _kv_rel(orc, got_bits, want_bits, rows, what):
     eq = float((got_bits[:, rows] == want_bits[:, rows]).mean())
     print(f"{what}: rel-L2 {rel:.3g}, identical {eq:.4f}")
     return rel, eq
+
+
+def _kv_worst(orc, got_bits, want_bits, rows):
+    """Largest |got - want| over each head's row, relative to the row's max |want|."""
+    g = orc.fp16_bits_to_fp32(got_bits)[:, rows].astype(np.float64)
+    w = orc.fp16_bits_to_fp32(want_bits)[:, rows].astype(np.float64)
+    return float((np.abs(g - w) / np.abs(w).max(axis=-1, keepdims=True)).max())
 
 
 def _oracle_sensitivity(orc, oc, ol, fn, x, kcs, vcs, cap, pos, ref):
@@ -217,9 +229,10 @@ def test_decode_every_layer_teacher_forced(vxm_ctx, orc, stack28):
             exact += rel == 0.0
             # the appended row comes from identical inputs: only the projection's fp32 order differs
             for got, want, nm in ((kvrows[mode][0], kc, "K"), (kvrows[mode][1], vc, "V")):
-                rel_kv, eq = _kv_rel(orc, got, want.reshape(NKV, cap, HD), slice(ctx0, ctx0 + 1),
-                                     f"layer {l} mode {mode} {nm} row")
-                assert rel_kv <= KV_REL and eq >= KV_EQ - 0.02, (l, mode, nm, rel_kv, eq)
+                rows = slice(ctx0, ctx0 + 1)
+                rel_kv, eq = _kv_rel(orc, got, want.reshape(NKV, cap, HD), rows, f"layer {l} mode {mode} {nm} row")
+                worst_kv = _kv_worst(orc, got, want.reshape(NKV, cap, HD), rows)
+                assert worst_kv <= KV_ULP and eq >= KV_EQ - 0.02, (l, mode, nm, rel_kv, worst_kv, eq)
                 assert np.array_equal(got[:, :ctx0], want.reshape(NKV, cap, HD)[:, :ctx0])
         x = outs[2]
     print(f"28 layers x 2 paths: worst rel-L2 {worst:.3g}, {exact} of 56 bit-identical")

@@ -65,11 +65,12 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 // Phase timestamps for profiling builds (-DVXM_PERSISTENT_TRACE): slot k of
 // layer l of this workgroup gets the 100 MHz real-time counter.  Compiled
 // out of the library.
+constexpr int kTraceSlots = 16;
 #ifdef VXM_PERSISTENT_TRACE
 #define VXM_TS(cond, k)                                                                              \
     do {                                                                                             \
         if ((cond) && p.trace)                                                                       \
-            p.trace[(size_t)blockIdx.x * p.trace_stride + 2 + l * 12 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+            p.trace[(size_t)blockIdx.x * p.trace_stride + 2 + l * kTraceSlots + (k)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 #else
 #define VXM_TS(cond, k) do { } while (0)
@@ -562,13 +563,40 @@ __device__ __forceinline__ void quant4(const float v[4], int8_t *xq4, float *xd1
     if (first) *xd1 = dsc;
 }
 
-// Q8_0 of n BF16 values stored as pairs (low half first) in LDS, 4 values per thread.
+// Q8_0 of n BF16 values stored as pairs (low half first) in LDS.  Two lanes
+// (an even lane and the next) take one 32-value block, 16 values each, in a
+// single pass for n <= 32 kThreads: the block max is one DPP step and the two
+// divisions of the scale are issued once per 16 values instead of once per 4
+// (the activation of the down projection: 1.76 -> 0.3 us per layer).  The
+// arithmetic per value is quant4_reg's.
 __device__ void quantize_lds_bf16x2(const uint32_t *src, int n, int8_t *xq, float *xd) {
-    for (int base = tid_now() * 4; base < n; base += kThreads * 4) {
-        const uint2 w = *(const uint2 *)(src + base / 2);
-        const float v[4] = {__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
-                            __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u)};
-        quant4(v, xq + base, xd + base / 32, (tid_now() & 7) == 0);
+    const int t = tid_now();
+    for (int base = t * 16; base < n; base += kThreads * 16) {
+        const uint4 a = *(const uint4 *)(src + base / 2), b = *(const uint4 *)(src + base / 2 + 4);
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        float v[16];
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+            amax = fmaxf(amax, fmaxf(fabsf(v[2 * i]), fabsf(v[2 * i + 1])));
+        }
+        amax = fmaxf(amax, dpp_f<kDppXor1>(amax));   // the other half of the block
+        const float d = __fdiv_rn(amax, 127.0f);
+        const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+        uint32_t q4[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            q4[j] = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float q = fminf(fmaxf(rintf(v[4 * j + i] * id), -128.0f), 127.0f);
+                q4[j] |= (uint32_t)(uint8_t)(int8_t)(int)q << (8 * i);
+            }
+        }
+        *(uint4 *)(xq + base) = make_uint4(q4[0], q4[1], q4[2], q4[3]);
+        if ((t & 1) == 0) xd[base / 32] = vxm_h2f(vxm_f2h(d));
     }
 }
 
@@ -620,11 +648,16 @@ struct Slot {
 // bytes of scales by lanes 0..7 (exec narrowed inside the asm and restored).
 // Before the DMA overwrites a slot, lgkmcnt(0) guarantees that the wave's
 // LDS reads of the slot's previous unit have completed.
-__device__ __forceinline__ void dma_unit(uint32_t lds_slot, const int8_t *q, const uint16_t *d, int lane) {
+__device__ __forceinline__ void dma_unit(uint32_t lds_slot, const int8_t *q, const uint16_t *d, int lane, bool live) {
     const int8_t *q0 = q + lane * 16;
     const int8_t *q1 = q0 + 1024;
     const char *dd = (const char *)d + (lane & 7) * 16;
     const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_slot);
+    // a unit the wave does not own (15 of the 105 slots of a layer at the
+    // TSLM shape) loads with one lane: the instructions still count in vmcnt,
+    // which the ring's waits rely on, but cost the address unit and the
+    // memory side almost nothing (627 -> 622 us per token)
+    const uint64_t mq = live ? ~0ull : 1ull, md = live ? 0xffull : 1ull;
     uint64_t saved;
     uint32_t saved_m0;
     // m0 and exec are saved and restored inside the statement, so the
@@ -633,20 +666,21 @@ __device__ __forceinline__ void dma_unit(uint32_t lds_slot, const int8_t *q, con
         "s_waitcnt lgkmcnt(0)\n\t"
         "s_mov_b32 %1, m0\n\t"
         "s_mov_b32 m0, %2\n\t"
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %6\n\t"
         "s_nop 0\n\t"
         "global_load_lds_dwordx4 %3, off nt\n\t"
         "s_add_u32 m0, m0, 1024\n\t"
         "s_nop 0\n\t"
         "global_load_lds_dwordx4 %4, off nt\n\t"
         "s_add_u32 m0, m0, 1024\n\t"
-        "s_mov_b64 %0, exec\n\t"
-        "s_mov_b64 exec, 0xff\n\t"
+        "s_mov_b64 exec, %7\n\t"
         "s_nop 0\n\t"
         "global_load_lds_dwordx4 %5, off nt\n\t"
         "s_mov_b64 exec, %0\n\t"
         "s_mov_b32 m0, %1"
         : "=&s"(saved), "=&s"(saved_m0)
-        : "s"(m0v), "v"(q0), "v"(q1), "v"(dd)
+        : "s"(m0v), "v"(q0), "v"(q1), "v"(dd), "s"(mq), "s"(md)
         : "memory", "scc");
 }
 
@@ -685,12 +719,13 @@ __device__ __forceinline__ UnitBases unit_bases(const vxm_pparams &p, int l) {
 // wave issues the same count of loads).
 template <class S, int s>
 __device__ __forceinline__ void unit_addr(const vxm_pparams &p, const UnitBases &B, int wg, int ci,
-                                          const int8_t *&q, const uint16_t *&d) {
+                                          const int8_t *&q, const uint16_t *&d, bool &live) {
     using T = Slot<S, s>;
     const int u = ci + kCW * T::k;
     q = p.dummy_q;
     d = p.dummy_d;
-    if (u < T::U && B.valid) {
+    live = u < T::U && B.valid;
+    if (live) {
         const int row = wg * T::R + u / T::C, c = u % T::C;
         constexpr int K = T::C * kUnit;
         q = B.q[T::ph] + (int64_t)row * K + c * kUnit;
@@ -710,8 +745,9 @@ __device__ __forceinline__ void ring_issue(const vxm_pparams &p, const UnitBases
                                            int ci, int lane) {
     const int8_t *q;
     const uint16_t *d;
-    unit_addr<S, s>(p, B, wg, ci, q, d);
-    dma_unit(ring_lds + ring_slot<S, s>(l) * kSlot, q, d, lane);
+    bool live;
+    unit_addr<S, s>(p, B, wg, ci, q, d, live);
+    dma_unit(ring_lds + ring_slot<S, s>(l) * kSlot, q, d, lane, live);
 }
 
 template <class S, int... ss>
@@ -720,68 +756,103 @@ __device__ __forceinline__ void ring_prime(const vxm_pparams &p, const UnitBases
     (ring_issue<S, ss>(p, B0, ring_lds, 0, wg, ci, lane), ...);
 }
 
-// Consume the K slots of one phase starting at slot OFF: dot product of each
-// unit (lane l: block l) with the quantized activation in LDS, partial to
-// part[u]; after each unit, the loads P positions ahead are issued.  Units go
-// two at a time: both are waited for, read and reduced together (two
-// independent dependency chains), then both refills are issued.
+// The operands of one ring unit for lane l (block l of the unit): its 32
+// weight quants and scale, and the activation's block of the unit's K chunk.
+struct UnitOps {
+    v4i w0, w1, x0, x1;
+    float xs;
+    uint32_t dw;
+};
+
 template <class S, int s>
-__device__ __forceinline__ float unit_dot(const int8_t *ring, int l, int ci, int lane, const int8_t *xq,
-                                          const float *xd) {
+__device__ __forceinline__ UnitOps unit_load(const int8_t *ring, int l, int ci, int lane, const int8_t *xq,
+                                             const float *xd) {
     using T = Slot<S, s>;
     const int u = ci + kCW * T::k;
     const int c = u % T::C;
-    const v4i x0 = *(const v4i *)(xq + c * kUnit + lane * 32);
-    const v4i x1 = *(const v4i *)(xq + c * kUnit + lane * 32 + 16);
-    const float xs = xd[c * (kUnit / 32) + lane];
     const int8_t *slot = ring + ring_slot<S, s>(l) * kSlot;
-    const v4i w0 = *(const v4i *)(slot + lane * 32);
-    const v4i w1 = *(const v4i *)(slot + lane * 32 + 16);
-    const uint16_t dw = *(const uint16_t *)(slot + kUnit + lane * 2);
-    const int si = dot16(w1, x1) + dot16(w0, x0);   // exact int32 block sum
-    return (float)si * (vxm_h2f(dw) * xs);
+    UnitOps o;
+    o.x0 = *(const v4i *)(xq + c * kUnit + lane * 32);
+    o.x1 = *(const v4i *)(xq + c * kUnit + lane * 32 + 16);
+    o.xs = xd[c * (kUnit / 32) + lane];
+    o.w0 = *(const v4i *)(slot + lane * 32);
+    o.w1 = *(const v4i *)(slot + lane * 32 + 16);
+    o.dw = *(const uint16_t *)(slot + kUnit + lane * 2);
+    return o;
 }
 
-// Consume the K slots of one phase starting at slot OFF: dot product of each
-// unit (lane l: block l) with the quantized activation in LDS, partial to
-// part[u].  Units go two at a time: both are waited for, read and reduced
-// together (two independent dependency chains).  No loads are issued here:
-// the refills of the phase's slots go out after its outputs are published
-// (ring_refill), while the workgroup waits for the next phase's inputs.  All
-// 7 compute waves issuing DMAs at once saturate the CU's address unit, and a
-// wave's load issue blocks until it is accepted, so refills issued between
-// units stalled the compute by about as long as the compute itself.
-// At phase start every slot of the phase is in flight or landed, and the
-// only ring loads issued after slot k's are those of the phase's later
-// slots: 3 (P - 1 - k) of them, so vmcnt(3 (P - 1 - k)) means slot k is in
-// LDS.  (Other vector memory instructions of the wave are issued later and
-// only make the wait stricter.)
-template <class S, int OFF, int K, int k = 0>
+// This lane's term of the unit's partial: the exact int32 block sum times
+// d_w * d_x.
+__device__ __forceinline__ float unit_term(const UnitOps &o) {
+    const int si = dot16(o.w1, o.x1) + dot16(o.w0, o.x0);   // exact int32 block sum
+    return (float)si * (vxm_h2f((uint16_t)o.dw) * o.xs);
+}
+
+// Makes every operand of a group live at one point, so all of the group's LDS
+// reads are issued before its first product (the compiler otherwise reuses one
+// register set and serialises the units on the LDS latency).
+// The activation's operands are left out: a phase whose K is one unit reads
+// the same block for every unit, which the compiler loads once.
+__device__ __forceinline__ void ops_ready(UnitOps &o) {
+    asm volatile("" : "+v"(o.w0), "+v"(o.w1), "+v"(o.dw));
+}
+
+// Sums of four values over the 64 lanes, transposed: one permlane32 swap per
+// pair folds lanes 32..63 onto 0..31 for two values at once, one permlane16
+// swap folds the result to a 16-lane row per value, and a row sum ends the
+// total in lane 15 of row r: v[0], v[2], v[1], v[3] for r = 0, 1, 2, 3.
+// 10 instructions for four values; a 64-lane DPP sum takes 6 (and two
+// broadcasts across rows) per value.
+__device__ __forceinline__ float wave_sum4_rows(const float (&v)[4]) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0]), __float_as_uint(v[1]), false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[2]), __float_as_uint(v[3]), false, false);
+    const float r01 = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const float r23 = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+    const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(r01), __float_as_uint(r23), false, false);
+    return row16_sum_15(__uint_as_float(c[0]) + __uint_as_float(c[1]));
+}
+
+// Consume slots OFF + G .. OFF + G + 3 (at most K - G of them) of one phase:
+// wait until they are in LDS, read every operand of the group, form the four
+// units' terms, and reduce them together (wave_sum4_rows); partials to
+// part[u].  The ring's waits count loads: at phase start every slot of the
+// phase is in flight or landed, and the only ring loads issued after slot k's
+// are those of the next P - 1 - k stream positions, 3 instructions each, so
+// vmcnt(3 (P - G - n)) means slots G .. G + n - 1 are in LDS.  (Other vector
+// memory instructions of the wave are issued later and only make the wait
+// stricter.)  No loads are issued here: the refills of the phase's slots go
+// out after its outputs are published (ring_refill), while the workgroup
+// waits for the next phase's inputs.  All 7 compute waves issuing DMAs at
+// once saturate the CU's address unit, and a wave's load issue blocks until
+// it is accepted, so refills issued between units stalled the compute by
+// about as long as the compute itself.
+template <class S, int OFF, int K, int G = 0>
 __device__ __forceinline__ void ring_phase(const int8_t *ring, int l, int ci, int lane, const int8_t *xq,
                                            const float *xd, float *part) {
     static_assert(K <= S::P, "a phase's slots are all in the ring at its start");
-    if constexpr (k + 1 < K) {
-        constexpr int s = OFF + k;
-        using T0 = Slot<S, s>;
-        using T1 = Slot<S, s + 1>;
-        const int u0 = ci + kCW * T0::k, u1 = ci + kCW * T1::k;
-        ring_wait<3 * (S::P - 2 - k)>();   // slots k and k + 1 are in LDS
-        float a = unit_dot<S, s>(ring, l, ci, lane, xq, xd);
-        float b = unit_dot<S, s + 1>(ring, l, ci, lane, xq, xd);
-        wave_sum_63_x2(a, b);
-        if (lane == 63) {
-            if (u0 < T0::U) part[u0] = a;
-            if (u1 < T1::U) part[u1] = b;
+    if constexpr (G < K) {
+        constexpr int n = K - G < 4 ? K - G : 4;
+        ring_wait<3 * (S::P - G - n)>();
+        UnitOps o[4];
+        o[0] = unit_load<S, OFF + G>(ring, l, ci, lane, xq, xd);
+        if constexpr (n > 1) o[1] = unit_load<S, OFF + G + 1>(ring, l, ci, lane, xq, xd);
+        if constexpr (n > 2) o[2] = unit_load<S, OFF + G + 2>(ring, l, ci, lane, xq, xd);
+        if constexpr (n > 3) o[3] = unit_load<S, OFF + G + 3>(ring, l, ci, lane, xq, xd);
+#pragma unroll
+        for (int i = 0; i < n; i++) ops_ready(o[i]);
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < n; i++) v[i] = unit_term(o[i]);
+        const float tot = wave_sum4_rows(v);
+        if ((lane & 15) == 15) {
+            const int r = lane >> 4;
+            const int i = r == 1 ? 2 : r == 2 ? 1 : r;   // rows hold v[0], v[2], v[1], v[3]
+            int u = -1;
+            if (i < n) u = ci + kCW * (Slot<S, OFF + G>::k + i);
+            // units past the phase's (or a wave's dummy units) are not stored
+            if (u >= 0 && u < Slot<S, OFF + G>::U) part[u] = tot;
         }
-        ring_phase<S, OFF, K, k + 2>(ring, l, ci, lane, xq, xd, part);
-    } else if constexpr (k < K) {
-        constexpr int s = OFF + k;
-        using T = Slot<S, s>;
-        const int u = ci + kCW * T::k;
-        ring_wait<3 * (S::P - 1 - k)>();
-        const float a = wave_sum_63(unit_dot<S, s>(ring, l, ci, lane, xq, xd));
-        if (lane == 63 && u < T::U) part[u] = a;
-        ring_phase<S, OFF, K, k + 1>(ring, l, ci, lane, xq, xd, part);
+        ring_phase<S, OFF, K, G + 4>(ring, l, ci, lane, xq, xd, part);
     }
 }
 
@@ -1157,6 +1228,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             norm_quant<H>(xs, gn, sst, p.eps, xq, xd);
         }
         lds_barrier();
+        VXM_TS(tid_now() == 0, 12);
         if (!reader) ring_phase<S, S::OA, S::SA>(ring, l, ci, lane, xq, xd, part);
         lds_barrier();
         VXM_TS(tid_now() == 0, 1);
@@ -1242,6 +1314,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             norm_quant<H>(h1s, gn, sst, p.eps, xq, xd);
         }
         lds_barrier();
+        VXM_TS(tid_now() == 0, 13);
         if (!reader) ring_phase<S, S::OD, S::SD>(ring, l, ci, lane, xq, xd, part);
         lds_barrier();
         VXM_TS(tid_now() == 0, 8);
@@ -1279,8 +1352,10 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         if (*bail) return;
         VXM_TS(tid_now() == 0, 9);
         if (!reader) ring_refill<S, S::OD, S::SD, kDE>(p, cur, nxt, ring_lds, l, wg, ci, lane);
+        VXM_TS(tid_now() == 0, 15);
         quantize_lds_bf16x2((const uint32_t *)big, F, xq, xd);
         lds_barrier();
+        VXM_TS(tid_now() == 0, 14);
         if (!reader) ring_phase<S, S::OE, S::SE>(ring, l, ci, lane, xq, xd, part);
         lds_barrier();
         VXM_TS(tid_now() == 0, 10);
@@ -1546,7 +1621,7 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
     static uint64_t *tbuf = nullptr;
     static size_t tcap = 0;
     static int ncall = 0;
-    const int stride = 2 + L * 12;
+    const int stride = 2 + L * kTraceSlots;
     const size_t tbytes = (size_t)kG * stride * 8;
     if (tbytes > tcap) {
         VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
