@@ -248,14 +248,17 @@ def bench_decode_long(ctx, torch, vxm, layers, copies, contexts, steps, mode):
     models = [vxm.MiniCPM4(ctx, cfg, layers, final_norm=fn) for _ in range(copies)]
     for m in models:
         m.set_decode_mode(mode)
-    kv = vxm.KVCache(ctx, L, NKV, HD, max(contexts) + steps)
+    warm = max(24, copies)
+    kv = vxm.KVCache(ctx, L, NKV, HD, max(contexts) + max(steps, warm))
     kv_prefill(vxm, kv, L, max(contexts), 5)
     x = torch.from_numpy(vxm.host_randn(3, H, 0.0, 1.0).reshape(1, H)).to("cuda:0")
     out = {}
     for c0 in contexts:
         kv.set_used(c0)
-        # every copy decodes once before the timed tokens (its first call sets up its launch state)
-        for i in range(max(2, copies)):
+        # every copy decodes before the timed tokens (its first call sets up its launch state), 24
+        # tokens in all: after the host-side cache fill the first timed context otherwise ran at
+        # 1.5x its steady per-token time (the GPU had been idle)
+        for i in range(warm):
             models[i % copies].forward(kv, x, c0 + i)
         ctx.sync()
         kv.set_used(c0)
@@ -689,7 +692,9 @@ def main():
     us1 = None
     if not (args.decode_only or args.lm_update_only or args.long_context_only):
         # one decoder layer, context 512 (8 rotated copies of the layer)
-        us1, _ = bench_decode(ctx, torch, vxm, layers[:1], 1, 8, 512, 64, 4, mode)
+        # 200 untimed tokens (about 10 ms): with 4, the GPU's clocks had not come up after the
+        # previous leg's host work and the leg read 52-123 us from run to run
+        us1, _ = bench_decode(ctx, torch, vxm, layers[:1], 1, 8, 512, 64, 200, mode)
         layer_b = step_bytes(512, 1)
         log(f"one layer decode @ctx512: {us1:.2f} us, {layer_b / (us1 * 1e-6) / 1e9:.1f} GB/s")
 
@@ -700,7 +705,8 @@ def main():
         longc = {"contexts": {str(c): {"us_per_token": round(u, 1),
                                        "GBs": round(step_bytes(c + 7.5) / (u * 1e-6) / 1e9, 1)}
                               for c, u in lc.items()},
-                 "note": f"single-launch decode, 16 tokens from each context, cache capacity {max(contexts) + 16}; "
+                 "note": f"single-launch decode, 16 tokens from each context after 24 untimed ones, cache capacity "
+                         f"{max(contexts) + 24}; "
                          "the keys of each head are split over up to 16 workgroups beyond 384"}
         log("long-context decode (single launch): " +
             ", ".join(f"ctx {c} {u:.1f} us" for c, u in lc.items()))
