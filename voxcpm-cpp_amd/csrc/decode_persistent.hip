@@ -1253,11 +1253,17 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             }
             put_word(p.qkvb + r * SQ + gw, pack_bf16x2(y0, y1), make_tag(ep, l, PH_QKV));
         }
-        if (!reader) ring_refill<S, S::OA, S::SA>(p, cur, nxt, ring_lds, l, wg, ci, lane);
+        // A's refills (the layer's D units 4 and 5, needed about 8 us later).  In an attention
+        // workgroup they go out after the attention: issued first, the K / V row loads of
+        // every wave retired behind them (loads retire in order).  593 -> 579 us per token.
+        // (The same deferral of E's refills, to after the next layer's A, measured 601 and
+        // 624 us: those loads then sit in front of the attention's and phase C's reads.)
+        if (!reader && head < 0) ring_refill<S, S::OA, S::SA>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         // ---------------- B: attention, one workgroup per query head ----------------
         if (head >= 0) {
             attention_phase<S>(p, l, head, chunk, lds, bail);
             if (*bail) return;
+            if (!reader) ring_refill<S, S::OA, S::SA>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         }
         // ---------------- C: O rows + residual ----------------
         if (wave < kAttReaders) {
