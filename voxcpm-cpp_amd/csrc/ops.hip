@@ -746,22 +746,28 @@ __global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, in
         P[i * SP + j] = sc * scale;
     }
     __syncthreads();
-    // 4. softmax: row max, exponentials, the row sum in double and (float)(1/sum)
-    if (tid < nq) {
-        float m = -INFINITY;
-        for (int j = 0; j < S; j++) m = fmaxf(m, P[tid * SP + j]);
-        mx[tid] = m;
-    }
-    __syncthreads();
-    for (int idx = tid; idx < nq * S; idx += 256) {
-        const int i = idx / S, j = idx % S;
-        P[i * SP + j] = expf(P[i * SP + j] - mx[i]);
-    }
-    __syncthreads();
-    if (tid < nq) {
-        double sum = 0.0;
-        for (int j = 0; j < S; j++) sum += (double)P[tid * SP + j];
-        inv[tid] = (float)(1.0 / sum);
+    // 4. softmax: row max, exponentials, the row sum in double and (float)(1/sum); wave i
+    //    takes query row i, lane j key j (S <= 64), so the max and the sum are wave
+    //    reductions.  The double sum of at most 64 exponentials of one row is exact
+    //    unless they span more than 2^29, so its order matches the serial sum's.
+    static_assert(kLocalRB <= 4 && kLocalMaxS <= 64, "one wave per query row, one lane per key");
+    {
+        const int i = tid >> 6, j = tid & 63;
+        if (i < nq) {
+            const float sj = j < S ? P[i * SP + j] : -INFINITY;
+            float m = sj;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            const float e = j < S ? expf(sj - m) : 0.0f;
+            if (j < S) P[i * SP + j] = e;
+            double sum = (double)e;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+            if (j == 0) {
+                mx[i] = m;
+                inv[i] = (float)(1.0 / sum);
+            }
+        }
     }
     __syncthreads();
     // 5. out[i][d] = sum_j v[j][d] p_ij, p_ij = e_ij * inv_i, over the j-slices of
