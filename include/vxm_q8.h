@@ -278,6 +278,20 @@ int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev, int32_t P,
                   const float *mu_dev, int32_t n_steps, float cfg_value, int32_t schedule,
                   int32_t use_zero_star);
 
+/* Block strategy of vxm_locdit_forward and vxm_cfm_solve (the VXM_DECODE_*
+ * values).  The persistent kernel runs every block of an evaluation in one
+ * launch; it supports hidden 1024, FFN 4096, 16 query heads of (16 kv x 64)
+ * or (2 kv x 128), at most 48 rows in segments of at most 32, on 256 CUs.
+ * AUTO takes it for the 2 kv x 128 layout, where it measured faster, and
+ * launches block by block otherwise; KERNELS always launches block by block;
+ * PERSISTENT fails with VXM_ERR_NOT_IMPLEMENTED where the kernel does not
+ * apply.  No reference counterpart (ggml evaluates one graph per call). */
+int vxm_locdit_set_block_mode(vxm_locdit *m, int mode);
+/* Synchronises the context's stream and reports a device-side failure of the
+ * persistent block kernel (a workgroup that timed out waiting for its inputs)
+ * as VXM_ERR_BACKEND, then clears it. */
+int vxm_locdit_check(vxm_locdit *m);
+
 /* ---- LocEnc and the per-token LM update ----------------------------------
  * Mirrors vcpm_locenc_config (src/locenc.h:49-60); max_seq_len and
  * patch_size are unused there and left out. */
@@ -317,6 +331,12 @@ int vxm_locenc_free(vxm_locenc *m);
  * special token's row [hidden]; without a special token it is every row
  * [P][hidden]. */
 int vxm_locenc_forward(vxm_locenc *m, const float *x_dev, int32_t P, float *out_dev);
+/* Block strategy of vxm_locenc_forward, as vxm_locdit_set_block_mode (the
+ * same persistent kernel; AUTO takes it for the 16 q / 2 kv x 128 layout), and
+ * the report of its device-side failures, as vxm_locdit_check.  No reference
+ * counterpart. */
+int vxm_locenc_set_block_mode(vxm_locenc *m, int mode);
+int vxm_locenc_check(vxm_locenc *m);
 
 /* The scalar quantizer core of the FSQ layer, vcpm_fsq_quantize
  * (src/fsq.c:16-29): y = round(tanh(x) * s) * (1/s) elementwise, round half

@@ -1,0 +1,201 @@
+"""GPU parity of the single-launch LocDiT / LocEnc blocks (k_locdit_persistent) against the oracle.
+
+The persistent kernel runs every block of an evaluation in one launch and
+hands each phase's output to the next through tagged words; its rounding
+steps are those of the launch-based kernels, the attention's P.V sum runs in
+the oracle's order and only the fp32 order of the matrix products differs.
+One full-width block meets the bars of test_gpu_locdit.py and
+test_gpu_lm_update.py through the whole driver: the LocDiT velocity (16 x 64
+heads) the block bar, the reference-shape solve (16 / 2 x 128) the trajectory
+bar, the encoder's hidden rows the block sensitivity bar.  The 12-block
+stacks meet the deep-stack gross bar against the oracle (relative L2 < 5e-2)
+and stay as close to the launch-based path as that path is to the oracle.
+Solves replayed from a recorded HIP graph are bit-identical to the eager solve.
+"""
+
+import numpy as np
+import pytest
+
+from locdit_case import make_inputs, make_locdit
+from test_gpu_minicpm4 import assert_layer_close
+
+pytestmark = pytest.mark.gpu
+
+MHA = dict(H=1024, L=12, nh=16, nkv=16, hd=64, F=4096, feat=64)   # 24 rows per branch
+GQA = dict(H=1024, L=12, nh=16, nkv=2, hd=128, F=4096, feat=64)   # the reference's LocDiT: 11 rows per branch
+PC = {"mha": 17, "gqa": 4}
+
+
+def _dev(a):
+    import torch
+
+    return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def _model(vxm_ctx, orc, seed, dims):
+    import vxm
+
+    cfg, w, ow, ocfg = make_locdit(orc, seed, dims["H"], dims["L"], dims["nh"], dims["nkv"], dims["hd"], dims["F"],
+                                   dims["feat"], True)
+    return vxm.LocDiT(vxm_ctx, cfg, w), ow, ocfg
+
+
+def _rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)
+
+
+def test_persistent_locdit_one_block_full_width_mha(vxm_ctx, orc):
+    """One 16 x 64 block at full width through the whole driver (time MLP, projections,
+    assembly, final norm, out_proj) in one persistent launch: the block bar (the inputs
+    of test_gpu_locdit.py::test_locdit_full_width_one_block)."""
+    import vxm
+
+    m, ow, ocfg = _model(vxm_ctx, orc, 51, dict(MHA, L=1))
+    m.set_block_mode(vxm.DECODE_PERSISTENT)
+    x, cond, mu = make_inputs(52, 4, 17, 64, 1024)
+    print("persistent locdit L=1 mha", flush=True)
+    v = m.forward(_dev(x), _dev(cond), 0.6, 0.0, _dev(mu)).cpu().numpy()
+    m.check()
+    assert_layer_close(v, orc.locdit_forward(ocfg, ow, x, cond, 0.6, 0.0, mu), what="persistent locdit L=1 mha")
+    m.free()
+
+
+def test_persistent_locdit_one_block_sway_gqa(vxm_ctx, orc):
+    """The reference's solve with one 16 / 2 x 128 block: 10 sway steps, CFG 2.0, CFG-Zero*,
+    both branches of 11 rows in one persistent launch per evaluation, against the oracle's
+    loop (the trajectory bar of test_gpu_locdit.py)."""
+    import vxm
+    from test_gpu_locdit import assert_trajectory_close
+
+    m, ow, ocfg = _model(vxm_ctx, orc, 73, dict(GQA, L=1))
+    m.set_block_mode(vxm.DECODE_PERSISTENT)
+    x0, cond, mu = make_inputs(74, 4, 4, 64, 1024)
+    x = _dev(x0)
+    print("persistent cfm L=1 gqa", flush=True)
+    m.cfm_solve(x, _dev(cond), _dev(mu), 10, 2.0, vxm.CFM_SWAY, True)
+    m.check()
+    assert_trajectory_close(x.cpu().numpy(), orc.cfm_solve(ocfg, ow, x0, cond, mu, 10, 2.0, 0, 1),
+                            what="persistent cfm L=1 gqa")
+    m.free()
+
+
+def _locenc(vxm_ctx, orc, seed, L, special):
+    import vxm
+    from test_lm_update_host import make_locenc
+
+    cfg, w, ow, ocfg = make_locenc(orc, seed, H=1024, L=L, nh=16, nkv=2, hd=128, F=4096, special=special)
+    return vxm.LocEnc(vxm_ctx, cfg, w), ow, ocfg
+
+
+@pytest.mark.parametrize("special", [True, False])
+def test_persistent_locenc_one_block(vxm_ctx, orc, special):
+    """The encoder's hidden rows after one full-width block (5 rows with the special token,
+    4 without) and the final norm, from one persistent launch: the block sensitivity bar."""
+    import vxm
+    from test_gpu_locdit import assert_sensitivity_close
+
+    enc, ow, ocfg = _locenc(vxm_ctx, orc, 141, 1, special)
+    enc.set_block_mode(vxm.DECODE_PERSISTENT)
+    x = np.random.default_rng(142).normal(0, 1, (4, 64)).astype(np.float32)
+    print(f"persistent locenc L=1 special={special}", flush=True)
+    out = enc.forward(_dev(x)).cpu().numpy()
+    enc.check()
+    assert_sensitivity_close(out.reshape(-1, 1024), orc.locenc_forward(ocfg, ow, x).reshape(-1, 1024),
+                             what="persistent locenc L=1")
+    enc.free()
+
+
+def test_persistent_locenc_full_size(vxm_ctx, orc):
+    """The 12-block encoder (5 rows): within the deep-stack bar of the oracle, and no farther
+    from the launch-based path than that path is from the oracle (plus the same bar)."""
+    import vxm
+
+    enc, ow, ocfg = _locenc(vxm_ctx, orc, 151, 12, True)
+    x = np.random.default_rng(152).normal(0, 1, (4, 64)).astype(np.float32)
+    ref = orc.locenc_forward(ocfg, ow, x)
+    print("persistent locenc L=12", flush=True)
+    enc.set_block_mode(vxm.DECODE_PERSISTENT)
+    op = enc.forward(_dev(x)).cpu().numpy()
+    enc.check()
+    enc.set_block_mode(vxm.DECODE_KERNELS)
+    ok = enc.forward(_dev(x)).cpu().numpy()
+    rp, rk, rpk = _rel(op, ref), _rel(ok, ref), _rel(op, ok)
+    print(f"locenc: persistent-oracle {rp:.3e}  kernels-oracle {rk:.3e}  persistent-kernels {rpk:.3e}")
+    assert np.isfinite(op).all() and rp < 5e-2
+    assert rpk < rk + 5e-2
+    enc.free()
+
+
+@pytest.mark.parametrize("shape", ["mha", "gqa"])
+def test_persistent_twelve_blocks_against_oracle_and_kernels(vxm_ctx, orc, shape):
+    """The 12-block velocity: within the deep-stack bar of the oracle, and no farther from
+    the launch-based path than that path is from the oracle (plus the same bar)."""
+    import vxm
+
+    dims = MHA if shape == "mha" else GQA
+    m, ow, ocfg = _model(vxm_ctx, orc, 111, dims)
+    x, cond, mu = make_inputs(112, 4, PC[shape], 64, 1024)
+    ref = orc.locdit_forward(ocfg, ow, x, cond, 0.6, 0.0, mu)
+    print(f"persistent L=12 {shape}", flush=True)
+    m.set_block_mode(vxm.DECODE_PERSISTENT)
+    vp = m.forward(_dev(x), _dev(cond), 0.6, 0.0, _dev(mu)).cpu().numpy()
+    m.check()
+    m.set_block_mode(vxm.DECODE_KERNELS)
+    vk = m.forward(_dev(x), _dev(cond), 0.6, 0.0, _dev(mu)).cpu().numpy()
+    rp, rk, rpk = _rel(vp, ref), _rel(vk, ref), _rel(vp, vk)
+    print(f"{shape}: persistent-oracle {rp:.3e}  kernels-oracle {rk:.3e}  persistent-kernels {rpk:.3e}")
+    assert np.isfinite(vp).all() and rp < 5e-2
+    assert rpk < rk + 5e-2
+    m.free()
+
+
+@pytest.mark.parametrize("shape", ["mha", "gqa"])
+def test_persistent_cfm_graph_replays(vxm_ctx, orc, shape):
+    """The CFM solve (both branches in one batch) on the persistent blocks: the first
+    non-zero step within the deep-stack bar of the oracle's loop; ten steps eager,
+    recorded and replayed (with eager forwards in between) bit-identical."""
+    import torch
+    import vxm
+
+    dims = MHA if shape == "mha" else GQA
+    m, ow, ocfg = _model(vxm_ctx, orc, 121, dims)
+    m.set_block_mode(vxm.DECODE_PERSISTENT)
+    x0, cond, mu = make_inputs(122, 4, PC[shape], 64, 1024)
+    cd, md = _dev(cond), _dev(mu)
+    sched = vxm.CFM_UNIFORM if shape == "mha" else vxm.CFM_SWAY
+    x = _dev(x0)
+    print(f"persistent cfm {shape}", flush=True)
+    m.cfm_solve(x, cd, md, 2, 2.0, sched, True)
+    m.check()
+    ref = orc.cfm_solve(ocfg, ow, x0, cond, mu, 2, 2.0, sched, 1)
+    rel = _rel(x.cpu().numpy(), ref)
+    print(f"{shape} cfm 2 steps: rel_l2 {rel:.3e}")
+    assert rel < 1e-1
+    x0d = _dev(x0)
+    other = _dev(x0[:1])
+    outs = []
+    for rep in range(4):   # eager, recorded + replayed, replayed, replayed
+        x = x0d.clone()
+        m.cfm_solve(x, cd, md, 10, 2.0, sched, True)
+        torch.cuda.synchronize()
+        outs.append(x.cpu().numpy())
+        m.forward(other, None, 0.25)
+        m.check()
+    assert np.isfinite(outs[0]).all() and not np.array_equal(outs[0], x0)
+    for rep in range(1, 4):
+        assert np.array_equal(outs[rep], outs[0]), f"run {rep}"
+    m.free()
+
+
+def test_persistent_mode_rejects_unsupported_shape(vxm_ctx, orc):
+    import vxm
+
+    m, _, _ = _model(vxm_ctx, orc, 131, dict(H=256, L=2, nh=4, nkv=2, hd=64, F=512, feat=64))
+    m.set_block_mode(vxm.DECODE_PERSISTENT)
+    x = _dev(np.zeros((4, 64), np.float32))
+    with pytest.raises(vxm.VxmError):
+        m.forward(x, None, 0.5)
+    m.set_block_mode(vxm.DECODE_AUTO)
+    assert np.isfinite(m.forward(x, None, 0.5).cpu().numpy()).all()
+    m.free()

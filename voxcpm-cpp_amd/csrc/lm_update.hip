@@ -31,6 +31,8 @@ struct vxm_locenc {
     float *seq = nullptr, *xh = nullptr;
     int8_t *aq = nullptr;
     uint16_t *ad = nullptr;
+    int block_mode = VXM_DECODE_AUTO;   // blocks launch by launch, or all in one persistent launch
+    vxm_lpersist *lp = nullptr;
 };
 
 struct vxm_lm_update {
@@ -176,6 +178,7 @@ extern "C" int vxm_locenc_free(vxm_locenc *m) {
     if (m->in_proj) vxm_weight_free(ctx, m->in_proj);
     for (float *p : {m->in_bias, m->special, m->norm})
         if (p) (void)hipFree(p);
+    vxm_locdit_persistent_free(m->lp);
     vxm_rope_free(m->dims);
     vxm_ws_free(m->ws);
     if (m->buf) (void)hipFree(m->buf);
@@ -243,19 +246,40 @@ extern "C" int vxm_locenc_forward(vxm_locenc *m, const float *x_dev, int32_t P, 
                        m->in_bias, (int)H);
     VXM_CHECK_LAUNCH(ctx);
     // bidirectional blocks over the S fresh rows, positions 0..S-1, no cache
-    const vxm_attn_site site{m->ws.lk, m->ws.lv, (int)S, (int64_t)d.nkv * S * d.hd, (int)S, 0, 0, 0};
-    for (int l = 0; l < m->cfg.n_layers; l++) {
-        const vxm_block &b = m->blocks[l];
-        if ((rc = vxm_launch_rmsnorm(ctx, m->seq, l ? m->ws.dn_out : vxm_parts{}, 1.0f, b.g_in, S, H, d.eps, nullptr,
-                                     m->ws.xq, m->ws.xd, var)))
-            return rc;
-        if ((rc = vxm_block_run(ctx, d, b, m->ws, m->seq, S, site))) return rc;
+    const bool persistent = m->cfg.n_layers > 0 && vxm_locdit_persistent_pick(ctx, d, S, (int)S, m->block_mode);
+    if (m->block_mode == VXM_DECODE_PERSISTENT && !persistent)
+        return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "locenc: no persistent block kernel for this shape / device");
+    if (persistent) {
+        // all blocks in one launch; seq then holds the last block's output, residual included
+        if ((rc = vxm_locdit_persistent_run(ctx, d, m->blocks, &m->lp, m->seq, S, (int)S))) return rc;
+    } else {
+        const vxm_attn_site site{m->ws.lk, m->ws.lv, (int)S, (int64_t)d.nkv * S * d.hd, (int)S, 0, 0, 0};
+        for (int l = 0; l < m->cfg.n_layers; l++) {
+            const vxm_block &b = m->blocks[l];
+            if ((rc = vxm_launch_rmsnorm(ctx, m->seq, l ? m->ws.dn_out : vxm_parts{}, 1.0f, b.g_in, S, H, d.eps,
+                                         nullptr, m->ws.xq, m->ws.xd, var)))
+                return rc;
+            if ((rc = vxm_block_run(ctx, d, b, m->ws, m->seq, S, site))) return rc;
+        }
     }
     // last residual + final RMSNorm of the rows that are returned: the
     // special token's row (src/locenc.c:118-128), or every row
     const int64_t rows = off ? 1 : S;
-    return vxm_launch_rmsnorm(ctx, m->seq, m->cfg.n_layers ? m->ws.dn_out : vxm_parts{}, 1.0f, m->norm, rows, H, d.eps,
-                              out_dev, nullptr, nullptr, var);
+    return vxm_launch_rmsnorm(ctx, m->seq, m->cfg.n_layers && !persistent ? m->ws.dn_out : vxm_parts{}, 1.0f, m->norm,
+                              rows, H, d.eps, out_dev, nullptr, nullptr, var);
+}
+
+extern "C" int vxm_locenc_set_block_mode(vxm_locenc *m, int mode) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    if (mode < VXM_DECODE_AUTO || mode > VXM_DECODE_PERSISTENT)
+        return vxm_fail(m->ctx, VXM_ERR_INVALID_ARG, "unknown block mode %d", mode);
+    m->block_mode = mode;
+    return VXM_OK;
+}
+
+extern "C" int vxm_locenc_check(vxm_locenc *m) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    return vxm_locdit_persistent_check(m->ctx, m->lp);
 }
 
 // ---------------------------------------------------------------------------

@@ -52,6 +52,8 @@ struct vxm_locdit {
     // arguments and device buffers (cfm_key); built on the second call with a key
     hipGraphExec_t cfm_exec = nullptr;
     std::vector<uint64_t> cfm_key, cfm_last_eager;
+    int block_mode = VXM_DECODE_AUTO;   // blocks launch by launch, or all in one persistent launch
+    vxm_lpersist *lp = nullptr;
 };
 
 // ---------------------------------------------------------------------------
@@ -284,20 +286,29 @@ static int dit_eval(vxm_locdit *m, const float *x, int P, int Pc, int n_seg, con
                        m->ch, m->cond_bias, m->xh, m->in_bias, (int)S, Pc, (int)H);
     VXM_CHECK_LAUNCH(ctx);
     // non-causal blocks, rope positions from 0 in each segment, fresh K/V per segment
-    const vxm_attn_site site{m->ws.lk, m->ws.lv, (int)S, (int64_t)d.nkv * S * d.hd, (int)S, 0, 0, 0};
-    for (int l = 0; l < m->cfg.n_layers; l++) {
-        const vxm_block &b = m->blocks[l];
-        if ((rc = vxm_launch_rmsnorm(ctx, m->seq, l ? m->ws.dn_out : vxm_parts{}, 1.0f, b.g_in, M, H, d.eps, nullptr,
-                                     m->ws.xq, m->ws.xd, var)))
-            return rc;
-        if ((rc = vxm_block_run(ctx, d, b, m->ws, m->seq, M, site))) return rc;
+    const bool persistent = m->cfg.n_layers > 0 && vxm_locdit_persistent_pick(ctx, d, M, (int)S, m->block_mode);
+    if (m->block_mode == VXM_DECODE_PERSISTENT && !persistent)
+        return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "locdit: no persistent block kernel for this shape / device");
+    if (persistent) {
+        // all blocks in one launch; seq then holds the last block's output, residual included
+        if ((rc = vxm_locdit_persistent_run(ctx, d, m->blocks, &m->lp, m->seq, M, (int)S))) return rc;
+    } else {
+        const vxm_attn_site site{m->ws.lk, m->ws.lv, (int)S, (int64_t)d.nkv * S * d.hd, (int)S, 0, 0, 0};
+        for (int l = 0; l < m->cfg.n_layers; l++) {
+            const vxm_block &b = m->blocks[l];
+            if ((rc = vxm_launch_rmsnorm(ctx, m->seq, l ? m->ws.dn_out : vxm_parts{}, 1.0f, b.g_in, M, H, d.eps,
+                                         nullptr, m->ws.xq, m->ws.xd, var)))
+                return rc;
+            if ((rc = vxm_block_run(ctx, d, b, m->ws, m->seq, M, site))) return rc;
+        }
     }
     // last residual + final RMSNorm of the x rows of each segment (src/locdit.c:373-390)
     // one launch over the P x rows of every segment (rows 3 + Pc .. S - 1 of each)
     {
         const int64_t r0 = 3 + Pc;
         const vxm_parts &dn = m->ws.dn_out;
-        const vxm_parts delta = m->cfg.n_layers ? vxm_parts{dn.p + r0 * H, dn.n, dn.stride} : vxm_parts{};
+        const vxm_parts delta =
+            m->cfg.n_layers && !persistent ? vxm_parts{dn.p + r0 * H, dn.n, dn.stride} : vxm_parts{};
         if ((rc = vxm_launch_rmsnorm(ctx, m->seq + r0 * H, delta, 1.0f, m->norm, (int64_t)n_seg * P, H, d.eps,
                                      nullptr, m->aq, m->ad, var, P, (int)S)))
             return rc;
@@ -376,6 +387,7 @@ extern "C" int vxm_locdit_free(vxm_locdit *m) {
     for (float *p : {m->in_bias, m->cond_bias, m->out_bias, m->norm, m->t_b1, m->t_b2, m->dt_b1, m->dt_b2})
         if (p) (void)hipFree(p);
     cfm_graph_drop(m);
+    vxm_locdit_persistent_free(m->lp);
     vxm_rope_free(m->dims);
     vxm_ws_free(m->ws);
     if (m->buf) (void)hipFree(m->buf);
@@ -441,6 +453,25 @@ extern "C" int vxm_locdit_create(vxm_ctx *ctx, const vxm_locdit_config *cfg, con
     }
     *out = m;
     return VXM_OK;
+}
+
+extern "C" int vxm_locdit_set_block_mode(vxm_locdit *m, int mode) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    if (mode < VXM_DECODE_AUTO || mode > VXM_DECODE_PERSISTENT)
+        return vxm_fail(m->ctx, VXM_ERR_INVALID_ARG, "unknown block mode %d", mode);
+    if (mode != m->block_mode) {
+        // a recorded Euler loop holds the other path's launches
+        (void)hipStreamSynchronize(m->ctx->stream);
+        cfm_graph_drop(m);
+        m->cfm_last_eager.clear();
+        m->block_mode = mode;
+    }
+    return VXM_OK;
+}
+
+extern "C" int vxm_locdit_check(vxm_locdit *m) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    return vxm_locdit_persistent_check(m->ctx, m->lp);
 }
 
 extern "C" int vxm_locdit_forward(vxm_locdit *m, const float *x_dev, const float *cond_dev, int32_t P, int32_t Pc,

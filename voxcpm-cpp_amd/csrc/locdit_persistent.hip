@@ -1,0 +1,1132 @@
+// locdit_persistent.hip -- every block of one LocDiT (or LocEnc) evaluation
+// in a single launch on gfx950: the M <= 48 rows of both CFG branches through
+// the blocks of vcpm_locdit_forward (src/locdit.c:300-372) / the encoder
+// (src/locenc.c:86-116), each block the non-causal MiniCPM4 block of
+// vcpm_minicpm4_block (src/minicpm4.c:467-532).
+//
+// Launch-based, a block is seven dependent kernels of a few microseconds each,
+// every one of them latency-bound (the weights of a whole evaluation stream in
+// 27 us at 8 TB/s).  Here 256 workgroups, one per CU, stay resident for all
+// blocks and hand each phase's output to the next phase's workgroups through
+// tagged 64-bit words (32-bit tag, 32-bit payload, written and read with
+// agent-scope relaxed atomics: a word is valid exactly when its tag is the
+// expected one, so no fences or grid barriers are needed).  Per block:
+//
+//   N1  row owners (one workgroup per row): x += the down projection's K-split
+//       partials of the previous block; RMSNorm(g_in) -> Q8_0 rows
+//   QKV 16-column tiles of W_qkv over all rows: MFMA, BF16, NEOX RoPE of the
+//       pair-interleaved q/k rows, f16 rounding of K and V -> BF16 pairs
+//   ATT one (head, segment, 8 query rows) per workgroup: softmax attention of
+//       vcpm_attention (src/minicpm4.c:232-248) -> Q8_0 of its head's columns
+//   O   (16-column tile, quarter of K) units: partial products
+//   N2  row owners: x += O; RMSNorm(g_post) -> Q8_0 rows
+//   GU  64-row tiles of the interleaved gate/up weight: MFMA, SwiGLU
+//       (src/minicpm4.c:441-456), Q8_0 of its 32 outputs
+//   D   (32-column tile, eighth of K) units: partial products
+//
+// The rounding steps are those of the launch-based kernels (k_rmsnorm,
+// k_attention_local, k_swiglu_quant); only the fp32 summation order of the
+// matrix products differs (blocks of K per wave, waves added in order).
+//
+// Every workgroup knows its weight tiles for all phases in advance, so wave 7
+// streams them into LDS with global_load_lds_dwordx4 one or more phases ahead
+// (its waits never delay the exchange reads of waves 0-6).  Weight tiles and
+// staged activations share one LDS layout per 32-byte Q8_0 block: 512 bytes
+// holding the 8-byte piece q of row r at 16 (16 (q >> 1) + r) + 8 (q & 1), which
+// is where lane (q, r) of v_mfma_i32_16x16x32_i8 reads it (conflict-free).
+#include <cstdio>
+#include <cstdlib>
+
+#include "vxm_model.h"
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 8, kThreads = kWaves * 64, kG = 256;
+constexpr int kPollThreads = 7 * 64;   // waves 0-6 read exchanged words; wave 7 streams weights
+constexpr int kSpin = 1 << 17;         // poll rounds before giving up
+constexpr int kMaxM = 48, kMT = 3, kMP = 48, kMaxS = 32, kRB = 8;
+constexpr int kH = 1024, kF = 4096, kNH = 16;
+constexpr int kXPitch = kH / 4 + kH / 32;   // words per row of a norm output (quants, then scales)
+constexpr int kPPitch = kF / 4 + kF / 32;   // words per row of the SwiGLU output
+constexpr int kOSplits = 4, kDSplits = 8, kDChunk = kF / kDSplits;
+enum { PH_X1, PH_QKV, PH_ATT, PH_O, PH_X2, PH_P, PH_D };
+
+template <int NKV_, int HD_>
+struct LShape {
+    static constexpr int NKV = NKV_, HD = HD_, HALF = HD / 2;
+    static constexpr int QD = kNH * HD, KVD = NKV * HD, NQKV = QD + 2 * KVD;
+    static constexpr int UQ = NQKV / 16;                  // QKV units
+    static constexpr int KO = QD / kOSplits, BO = KO / 32;  // O units: K bytes / blocks per split
+    static constexpr int APitch = QD / 4 + QD / 32;         // words per row of the attention output
+    // exchange channels, words (allocated for kMaxM rows)
+    static constexpr int WX = kMaxM * kXPitch, WQKV = kMaxM * NQKV / 2, WA = kMaxM * APitch;
+    static constexpr int WOP = kOSplits * kMaxM * kH, WP = kMaxM * kPPitch, WDP = kDSplits * kMaxM * kH;
+    // LDS layout (bytes; every region 1 KiB aligned)
+    static constexpr int RA = 0;                              // QKV (16 rows) / gate-up (64 rows) tile
+    static constexpr int RA_SC = RA + 64 * kH;                // its scales, f16 [rows][32]
+    static constexpr int RO = RA_SC + 64 * 32 * 2;            // O tile: 16 rows x KO
+    static constexpr int RO_SC = RO + 16 * KO;                // f16 [16][BO]
+    static constexpr int RD = RO_SC + 1024;                   // down tile: 32 rows x 512
+    static constexpr int RD_SC = RD + 32 * kDChunk;           // f16 [32][16]
+    static constexpr int ST = RD_SC + 1024;                   // staged activations [3][32 blocks][512]
+    static constexpr int ST_SC = ST + kMT * 32 * 512;         // their scales, f32 [32][kMP]
+    static constexpr int XR = ST_SC + 32 * kMP * 4;           // a row owner's x, f32 [1024]
+    static constexpr int GN = XR + kH * 4;                    // a row owner's norm gain, f32 [1024]
+    static constexpr int MISC = GN + kH * 4;                  // 8 doubles of reductions, then flags
+    static constexpr int BYTES = MISC + 128;
+    static_assert(16 * BO * 2 <= 1024, "O scales");
+    static_assert(BYTES <= 160 * 1024, "LDS");
+    // attention scratch inside the stage: k (rotated, f16-rounded) [S][HD+4], v [S][HD],
+    // q [kRB][HD+4], out [kRB][HD], p [kRB][S+1], row max and 1/sum [kRB] each
+    static_assert((kMaxS * (HD + 4) + kMaxS * HD + kRB * (HD + 4) + kRB * HD + kRB * (kMaxS + 1) + 2 * kRB) * 4 <=
+                      ST_SC - ST + 32 * kMP * 4,
+                  "attention scratch");
+};
+
+struct vxm_lblock {
+    const int8_t *qkv_q, *o_q, *gu_q, *dn_q;
+    const uint16_t *qkv_d, *o_d, *gu_d, *dn_d;
+    const float *g_in, *g_post;
+};
+
+struct vxm_lparams {
+    const vxm_lblock *blocks;
+    int L, M, S, nseg, qb;   // blocks, rows, rows per segment, segments, query blocks per (head, segment)
+    float eps;
+    int variant;
+    const float2 *cs;        // rope (cos, sin) [position][HD/2]
+    float *x;                // [M][1024]: block 0's input in, the last block's output out
+    uint64_t *x1, *qkv, *att, *op, *x2, *pp, *dp;   // exchange channels
+    int *err;
+    uint32_t *state;         // [0] epoch, [1] workgroups finished in this launch
+    uint64_t *trace;         // profiling build: per workgroup, the start and 16 timestamps per block
+};
+
+constexpr int kTraceSlots = 24;
+#ifdef VXM_PERSISTENT_TRACE
+#define VXM_LTS(k)                                                                                                 \
+    do {                                                                                                           \
+        if (threadIdx.x == 0 && p.trace)                                                                           \
+            p.trace[(size_t)blockIdx.x * (1 + kTraceSlots * p.L) + 1 + kTraceSlots * l + (k)] =                   \
+                __builtin_amdgcn_s_memrealtime();                                                                  \
+    } while (0)
+#else
+#define VXM_LTS(k) do { } while (0)
+#endif
+
+__device__ __forceinline__ uint32_t make_tag(uint32_t ep, int L, int l, int ph) {
+    return ((ep * (uint32_t)(8 * L) + (uint32_t)(8 * l + ph)) << 1) | 1u;   // odd: never a zeroed word
+}
+
+__device__ __forceinline__ void put_word(uint64_t *dst, uint32_t payload, uint32_t tag) {
+    __hip_atomic_store(dst, ((uint64_t)tag << 32) | (uint64_t)payload, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t get_word(const uint64_t *src) {
+    return __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float bf16r(float f) { return (float)(__bf16)f; }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xffff0000u);
+}
+
+// Workgroup barrier ordering LDS only: the weight loads of wave 7 stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ bool give_up(const vxm_lparams &p, int &it, int *bail) {
+    if (++it > kSpin || ((it & 31) == 0 && __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+        __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *bail = 1;
+        return true;
+    }
+    return false;
+}
+
+constexpr int kVmcnt0 = 0x0F70;   // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15)
+
+__device__ __forceinline__ int opaque_tid() {
+    int v;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "v"((int)threadIdx.x));
+    return v;
+}
+
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// A channel of exchanged words as a buffer resource (reads past `bytes` return zeros).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t chan_rsrc(const uint64_t *chan, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)chan, (short)0, (int)bytes, 0x00020000);
+}
+
+// Waves 0-6: thread t polls items t, t + 448, ... (< n, at most NPT per thread).  Item i
+// is the aligned pair of words at byte offset off(i) of channel rs, read with one
+// 16-byte load that bypasses the non-coherent caches like an agent-scope atomic load
+// (sc1; each 8-byte word is written by one atomic store, so each half is whole);
+// sink(i, a, b) stores the two payloads once both words carry `tag`.  The 16-byte
+// loads halve the address work of 8-byte ones, which sets the rate at which a CU
+// reads the words of a phase.
+template <int NPT, class A, class K>
+__device__ __forceinline__ void poll(const vxm_lparams &p, __amdgpu_buffer_rsrc_t rs, int n, uint32_t tag, A off,
+                                     K sink, int *bail) {
+    static_assert(NPT <= 32, "items per thread");
+    uint32_t pending = 0;
+    const int t0 = opaque_tid();
+#pragma unroll
+    for (int k = 0; k < NPT; k++)
+        if (t0 + kPollThreads * k < n) pending |= 1u << k;
+    int it = 0;
+    while (true) {
+        // the thread index through an opaque move: the items' offsets are recomputed
+        // in every round instead of being hoisted out of the block loop and held in
+        // registers across all phases
+        const int t = opaque_tid();
+        v4u w[NPT];
+#pragma unroll
+        for (int k = 0; k < NPT; k++)
+            if (pending & (1u << k)) w[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, off(t + kPollThreads * k), 0, 16);
+#pragma unroll
+        for (int k = 0; k < NPT; k++)
+            if ((pending & (1u << k)) && w[k].y == tag && w[k].w == tag) {
+                sink(t + kPollThreads * k, w[k].x, w[k].z);
+                pending &= ~(1u << k);
+            }
+        if (__all(pending == 0)) break;
+        if (give_up(p, it, bail)) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    // vmcnt(0) as the compiler's own wait: its wait insertion then knows that no load of
+    // this wave is outstanding, and inserts none after the phases' joins -- where wave 7
+    // would otherwise wait for its weight prefetches too
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+}
+
+__device__ __forceinline__ int slot_of(int q, int r) { return 16 * (16 * (q >> 1) + r) + 8 * (q & 1); }
+
+// Rows [0, M) x blocks [kb0, kb0 + nb) of a Q8_0 channel (row pitch `pitch` words:
+// qwords quant words, then one scale word per block; pitch, qwords, kb0 and nb even)
+// into the stage: quants in the block-slot layout [row tile][block][512], scales f32
+// [block][kMP].  A pair of quant words is one 8-byte piece of a block.
+template <int NPT>
+__device__ __forceinline__ void poll_stage(const vxm_lparams &p, __amdgpu_buffer_rsrc_t rs, int pitch, int qwords,
+                                           int kb0, int nb, int M, uint32_t tag, uint8_t *lds, int st, int st_sc,
+                                           int *bail) {
+    const int per = 4 * nb + nb / 2;   // pairs per row
+    poll<NPT>(
+        p, rs, M * per, tag,
+        [&](int i) {
+            const int m = i / per, j = i - m * per;
+            return (m * pitch + (j < 4 * nb ? 8 * kb0 + 2 * j : qwords + kb0 + 2 * (j - 4 * nb))) * 8;
+        },
+        [&](int i, uint32_t a, uint32_t b) {
+            const int m = i / per, j = i - m * per;
+            if (j < 4 * nb) {
+                const int blk = j >> 2, q = j & 3;
+                *(uint64_t *)(lds + st + ((m >> 4) * nb + blk) * 512 + slot_of(q, m & 15)) =
+                    (uint64_t)a | ((uint64_t)b << 32);
+            } else {
+                const int k = 2 * (j - 4 * nb);
+                *(float *)(lds + st_sc + (k * kMP + m) * 4) = __uint_as_float(a);
+                *(float *)(lds + st_sc + ((k + 1) * kMP + m) * 4) = __uint_as_float(b);
+            }
+        },
+        bail);
+}
+
+// Row owner: the ns partial rows [s][M][1024] of row `row` into the stage as f32 [ns][1024].
+template <int NPT>
+__device__ __forceinline__ void poll_partials(const vxm_lparams &p, __amdgpu_buffer_rsrc_t rs, int ns, int M, int row,
+                                              uint32_t tag, uint8_t *lds, int st, int *bail) {
+    poll<NPT>(
+        p, rs, ns * (kH / 2), tag, [&](int i) { return (((i >> 9) * M + row) * kH + 2 * (i & 511)) * 8; },
+        [&](int i, uint32_t a, uint32_t b) {
+            *(float2 *)(lds + st + ((i >> 9) * kH + 2 * (i & 511)) * 4) = make_float2(__uint_as_float(a), __uint_as_float(b));
+        },
+        bail);
+}
+
+// Lane l loads 16 bytes at g into LDS at lds_addr + 16 l (lanes outside mask load
+// nothing).  Called by wave 7 with all lanes active.
+__device__ __forceinline__ void dma16(uint32_t lds_addr, const void *g, uint64_t mask) {
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_addr);
+    uint64_t saved;
+    uint32_t saved_m0;
+    asm volatile(
+        "s_mov_b32 %1, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_mov_b64 %0, exec\n\t"
+        "s_and_b64 exec, exec, %4\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %3, off\n\t"
+        "s_mov_b64 exec, %0\n\t"
+        "s_mov_b32 m0, %1"
+        : "=&s"(saved), "=&s"(saved_m0)
+        : "s"(m0v), "v"(g), "s"(mask)
+        : "memory", "scc");
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// 16 weight rows [n0, n0 + 16) x blocks [kb0, kb0 + nb) (nb even) of a weight with
+// K bytes per row, as tile c of a region at `wt`: nb / 2 instructions, each two
+// blocks of the 16 rows.
+__device__ __forceinline__ void dma_tile(int wt, int c, const int8_t *wq, int K, int n0, int kb0, int nb, int lane) {
+    const int e = lane >> 5, j = (lane >> 4) & 1, r = lane & 15;
+    const int8_t *g = wq + (size_t)(n0 + r) * K + (kb0 + e) * 32 + 16 * j;
+    for (int k = 0; k < nb / 2; k++) dma16(wt + (c * (nb / 2) + k) * 1024, g + 64 * k, ~0ull);
+}
+
+// Scales of rows [n0, n0 + nrows) x blocks [kb0, kb0 + nb) (nb % 8 == 0): f16 [nrows][nb]
+// at `wsc`; ceil(nrows * nb / 512) instructions.
+__device__ __forceinline__ void dma_scales(int wsc, const uint16_t *wd, int nbk, int n0, int nrows, int kb0, int nb,
+                                           int lane) {
+    const int per = nb / 8, total = nrows * per;
+    for (int k0 = 0; k0 < total; k0 += 64) {
+        const int cnt = min(64, total - k0);
+        const int i = k0 + min(lane, cnt - 1);
+        const int row = i / per, part = i - row * per;
+        dma16(wsc + 16 * k0, wd + (size_t)(n0 + row) * nbk + kb0 + 8 * part, cnt == 64 ? ~0ull : ((1ull << cnt) - 1));
+    }
+}
+
+// acc[t][v] += products of tile rows 16 c + 4 q + v with stage rows 16 t + r (t < MT)
+// over the NB blocks from b0: weight tile (nbw blocks per row) at wt / wsc, stage
+// (nbs blocks) at st / st_sc.  MT and NB are compile-time: groups of up to 4 blocks
+// unroll, so each group's LDS reads are issued ahead of the products that need them.
+template <int MT, int NB, int G = (NB < 4 ? NB : 4)>
+__device__ __forceinline__ void mfma_run(const uint8_t *lds, int wt, int wsc, int nbw, int c, int st, int st_sc,
+                                         int nbs, int b0, int lane, float (&acc)[MT][4]) {
+    static_assert(NB % G == 0, "block groups");
+    const int q = lane >> 4, r = lane & 15, sl = slot_of(q, r);
+#pragma unroll 1
+    for (int i0 = 0; i0 < NB; i0 += G)
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+        const int b = b0 + i0 + i;
+        const long a = *(const long *)(lds + wt + (c * (nbw / 2) + (b >> 1)) * 1024 + (b & 1) * 512 + sl);
+        long bx[MT];
+        float dx[MT], dw[4];
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            bx[t] = *(const long *)(lds + st + (t * nbs + b) * 512 + sl);
+            dx[t] = *(const float *)(lds + st_sc + (b * kMP + 16 * t + r) * 4);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; v++) dw[v] = vxm_h2f(*(const uint16_t *)(lds + wsc + ((16 * c + 4 * q + v) * nbw + b) * 2));
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const v4i cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bx[t], v4i{}, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[t][v] = __builtin_fmaf((float)cc[v], dw[v] * dx[t], acc[t][v]);
+        }
+    }
+}
+
+// After mfma_run in every wave: the partial sums go to LDS (the stage, no longer
+// read) and out(ct, t, lane) = sum over kk of wave (ct + ncol * kk)'s partial, in kk order.
+template <int MT>
+__device__ __forceinline__ void red_store(uint8_t *lds, int st, int wave, int lane, const float (&acc)[MT][4]) {
+    float *red = (float *)(lds + st);
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) red[((wave * MT + t) * 4 + v) * 64 + lane] = acc[t][v];
+}
+
+template <int MT>
+__device__ __forceinline__ void red_sum(const uint8_t *lds, int st, int ncol, int ct, int t, int lane, float (&o)[4]) {
+    const float *red = (const float *)(lds + st);
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        float s = red[((ct * MT + t) * 4 + v) * 64 + lane];
+        for (int kk = 1; kk < kWaves / ncol; kk++) s = s + red[(((ct + ncol * kk) * MT + t) * 4 + v) * 64 + lane];
+        o[v] = s;
+    }
+}
+
+// Q8_0 rule of quant_block_4lanes for one value: x86 = id 127/amax, round half even;
+// otherwise id = 1/d, round half away.
+__device__ __forceinline__ uint32_t q8_byte(float v, float id, int variant) {
+    float q = variant == VXM_QUANT_X86 ? rintf(v * id) : roundf(v * id);
+    q = fminf(fmaxf(q, -128.0f), 127.0f);
+    return (uint32_t)(uint8_t)(int8_t)(int)q;
+}
+
+__device__ __forceinline__ void q8_scale(float amax, int variant, float &d, float &id) {
+    d = __fdiv_rn(amax, 127.0f);
+    if (variant == VXM_QUANT_X86) id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    else id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+}
+
+__device__ __forceinline__ double wg_sum_d(double v, uint8_t *lds, int misc) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    double *r = (double *)(lds + misc);
+    lds_barrier();
+    if ((threadIdx.x & 63) == 0) r[threadIdx.x >> 6] = v;
+    lds_barrier();
+    double t = 0.0;
+    for (int i = 0; i < kWaves; i++) t += r[i];
+    return t;
+}
+
+// Row owner: x = bf16(x + bf16(sum of ns partial rows, in order)) for row m (the
+// partials already in the stage as f32 [ns][1024]); with norm, the RMSNorm of
+// k_rmsnorm (gain staged in LDS at gn) and the Q8_0 of its output published as
+// row m of chan.
+__device__ __forceinline__ void row_update(uint8_t *lds, int st, int xr, int gn, int misc, int ns, float eps,
+                                           int variant, uint64_t *chan_row, uint32_t tag, bool norm) {
+    const int t = threadIdx.x, c = 2 * t;
+    const float *sum = (const float *)(lds + st);
+    float *x = (float *)(lds + xr);
+    float2 g = make_float2(1.0f, 1.0f);
+    if (norm) g = *(const float2 *)(lds + gn + 4 * c);
+    float xv[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        float dsum = sum[c + e];
+        for (int s = 1; s < ns; s++) dsum = dsum + sum[s * kH + c + e];
+        xv[e] = ns ? bf16r(x[c + e] + bf16r(dsum)) : x[c + e];
+        x[c + e] = xv[e];
+    }
+    if (!norm) return;
+    const double tot = wg_sum_d((double)(xv[0] * xv[0]) + (double)(xv[1] * xv[1]), lds, (int)misc);
+    const float mean = (float)(tot / (double)kH);
+    const float sc = __fdiv_rn(1.0f, __fsqrt_rn(mean + eps));
+    const float y0 = bf16r(bf16r(xv[0] * sc) * g.x), y1 = bf16r(bf16r(xv[1] * sc) * g.y);
+    // Q8_0: 16 threads per 32-value block
+    float amax = fmaxf(fabsf(y0), fabsf(y1));
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    float d, id;
+    q8_scale(amax, variant, d, id);
+    const uint32_t h = q8_byte(y0, id, variant) | (q8_byte(y1, id, variant) << 8);
+    const uint32_t ho = __shfl_xor(h, 1, 64);
+    if ((t & 1) == 0) put_word(chan_row + t / 2, h | (ho << 16), tag);
+    if ((t & 15) == 0) put_word(chan_row + kH / 4 + t / 16, __float_as_uint(vxm_h2f(vxm_f2h(d))), tag);
+}
+
+// One wave's program for all blocks.  DMA = wave 7: it streams the weight tiles and
+// computes with the others, but reads no exchanged words and loads nothing else, so
+// its only outstanding vector loads are its prefetches and the compiler, which sees
+// none of them, never makes it wait for one.  Waves 0-6 read the exchanged words.
+template <class LS, int MT, bool DMA>
+__device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, int *bail, uint32_t ep) {
+    const int wg = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int M = p.M, S = p.S, L = p.L;
+    const int row = wg < M ? wg : -1;
+    const int uq = wg - 64, n_att = kNH * p.nseg * p.qb;
+    const bool is_qkv = uq >= 0 && uq < LS::UQ, is_att = wg < n_att, is_gu = wg >= 128;
+    const int ugu = wg - 128;
+    const int oc = wg & 63, os = wg >> 6;   // O unit: 16-column tile, K quarter
+    const int dc = wg & 31, ds = wg >> 5;   // down unit: 32-column tile, K eighth
+    // loads per prefetch (16 rows x 2 blocks, or 64 f16 scale rows of 8 blocks, per instruction)
+    constexpr int nO = LS::BO / 2 + 1, nD = 17, nQKV = 17, nGA = 36;
+    const int dlane = threadIdx.x & 63;
+    // Wave 7 issues each prefetch at the start of a phase's wait, while waves 0-6 poll
+    // (an issue costs it ~50 ns per 1 KiB instruction when every CU streams at once).
+    // With Q = a QKV role, G = a gate/up role:
+    //   start:            O(0) and, with Q, QKV(0) (QKV first without G)
+    //   QKV(l) wait (Q):  D(l)
+    //   O(l) wait:        D(l) without Q; gate/up rows 0-31 (l) with G; QKV(l+1) with Q only
+    //   GU(l) wait (G):   gate/up rows 32-63 (l), O(l+1)
+    //   D(l) wait:        O(l+1) without G; QKV(l+1) with Q and G
+    // The waits before each phase's products count the loads issued after its own.
+    auto issue_o = [&](const vxm_lblock &b) {
+        dma_tile(LS::RO, 0, b.o_q, LS::QD, 16 * oc, LS::BO * os, LS::BO, dlane);
+        dma_scales(LS::RO_SC, b.o_d, LS::QD / 32, 16 * oc, 16, LS::BO * os, LS::BO, dlane);
+    };
+    auto issue_qkv = [&](const vxm_lblock &b) {
+        dma_tile(LS::RA, 0, b.qkv_q, kH, 16 * uq, 0, 32, dlane);
+        dma_scales(LS::RA_SC, b.qkv_d, kH / 32, 16 * uq, 16, 0, 32, dlane);
+    };
+    auto issue_d = [&](const vxm_lblock &b) {
+        for (int c = 0; c < 2; c++) dma_tile(LS::RD, c, b.dn_q, kF, 32 * dc + 16 * c, 16 * ds, 16, dlane);
+        dma_scales(LS::RD_SC, b.dn_d, kF / 32, 32 * dc, 32, 16 * ds, 16, dlane);
+    };
+    auto issue_gu_a = [&](const vxm_lblock &b) {
+        for (int c = 0; c < 2; c++) dma_tile(LS::RA, c, b.gu_q, kH, 64 * ugu + 16 * c, 0, 32, dlane);
+        dma_scales(LS::RA_SC, b.gu_d, kH / 32, 64 * ugu, 64, 0, 32, dlane);
+    };
+    auto issue_gu_b = [&](const vxm_lblock &b) {
+        for (int c = 2; c < 4; c++) dma_tile(LS::RA, c, b.gu_q, kH, 64 * ugu + 16 * c, 0, 32, dlane);
+    };
+    if (DMA) {
+        const vxm_lblock b0 = p.blocks[0];
+        if (is_qkv && !is_gu) {
+            issue_qkv(b0);
+            issue_o(b0);
+        } else {
+            issue_o(b0);
+            if (is_qkv) issue_qkv(b0);
+        }
+    }
+    // waves 0-6: a norm gain into LDS
+    auto stage_gain = [&](const float *g) {
+        const int t = opaque_tid();
+        for (int c = t * 4; c < kH; c += kPollThreads * 4) *(float4 *)(lds + LS::GN + 4 * c) = *(const float4 *)(g + c);
+    };
+    float acc[MT][4];
+    auto zero_acc = [&]() {
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[t][v] = 0.0f;
+    };
+
+    for (int l = 0; l < L; l++) {
+        const vxm_lblock blk = p.blocks[l];
+        const bool last = l == L - 1;
+        VXM_LTS(0);
+        // ---- N1: x += down partials of block l - 1; RMSNorm(g_in) -> Q8_0 ----
+        if (row >= 0) {
+            const int ns = l ? kDSplits : 0;
+            if (!DMA) {
+                stage_gain(blk.g_in);
+                if (ns)
+                    poll_partials<(kDSplits * kH / 2 + kPollThreads - 1) / kPollThreads>(
+                        p, chan_rsrc(p.dp, LS::WDP * 8), ns, M, row, make_tag(ep, L, l - 1, PH_D), lds, LS::ST, bail);
+            }
+            lds_barrier();
+            if (*bail) return;
+            VXM_LTS(1);
+            row_update(lds, LS::ST, LS::XR, LS::GN, LS::MISC, ns, p.eps, p.variant, p.x1 + (size_t)row * kXPitch,
+                       make_tag(ep, L, l, PH_X1), true);
+            lds_barrier();
+        }
+        VXM_LTS(2);
+        // ---- QKV ----
+        if (is_qkv) {
+            const int tid = opaque_tid(), lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
+            // the rope (cos, sin) of this thread's two output pairs, fetched before the wait
+            // (row 16 t + r16 at position row % S; pairs i, i + 1 of the head)
+            const int n0 = 16 * uq + 4 * q4, ip = (n0 % LS::HD) / 2, mrow = min(16 * (tid >> 6) + r16, M - 1);
+            float2 rc0 = make_float2(1.0f, 0.0f), rc1 = rc0;
+            if (!DMA && tid < MT * 64 && n0 < LS::QD + LS::KVD) {
+                rc0 = p.cs[(size_t)(mrow % S) * LS::HALF + ip];
+                rc1 = p.cs[(size_t)(mrow % S) * LS::HALF + ip + 1];
+            }
+            if (!DMA) {
+                const uint32_t tg = make_tag(ep, L, l, PH_X1);
+                poll_stage<(kMaxM * kXPitch / 2 + kPollThreads - 1) / kPollThreads>(
+                    p, chan_rsrc(p.x1, LS::WX * 8), kXPitch, kH / 4, 0, 32, M, tg, lds, LS::ST, LS::ST_SC, bail);
+            } else {
+                issue_d(blk);
+                vm_wait<nD>();
+            }
+            lds_barrier();
+            if (*bail) return;
+            VXM_LTS(3);
+            zero_acc();
+            mfma_run<MT, 4>(lds, LS::RA, LS::RA_SC, 32, 0, LS::ST, LS::ST_SC, 32, 4 * wave, lane, acc);
+            lds_barrier();
+            VXM_LTS(16);
+            red_store<MT>(lds, LS::ST, wave, lane, acc);
+            lds_barrier();
+            VXM_LTS(17);
+            if (!DMA && tid < MT * 64) {
+                const uint32_t tg = make_tag(ep, L, l, PH_QKV);
+                const int t = tid >> 6, m = 16 * t + r16;
+                float o[4];
+                red_sum<MT>(lds, LS::ST, 1, 0, t, lane, o);
+                if (m < M) {
+                    const int n = 16 * uq + 4 * q4;   // columns n .. n + 3: two pairs
+                    uint64_t *dst = p.qkv + (size_t)m * (LS::NQKV / 2) + n / 2;
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const int nc = n + 2 * e;
+                        float y0 = bf16r(o[2 * e]), y1 = bf16r(o[2 * e + 1]);
+                        if (nc < LS::QD + LS::KVD) {
+                            // pair (2i, 2i+1) of a q / k head row: dims i and i + HD/2
+                            const float2 r = e ? rc1 : rc0;
+                            const float z0 = bf16r(y0 * r.x - y1 * r.y), z1 = bf16r(y0 * r.y + y1 * r.x);
+                            y0 = z0;
+                            y1 = z1;
+                        }
+                        if (nc >= LS::QD) {
+                            y0 = vxm_h2f(vxm_f2h(y0));
+                            y1 = vxm_h2f(vxm_f2h(y1));
+                        }
+                        put_word(dst + e, pack_bf16x2(y0, y1), tg);
+                    }
+                }
+            }
+            lds_barrier();
+        }
+        VXM_LTS(4);
+        // ---- attention ----
+        if (is_att) {
+            const int tid = opaque_tid(), lane = tid & 63;
+            constexpr int HD = LS::HD, HALF = LS::HALF, HP = HD + 4;
+            const int h = wg % kNH, g = (wg / kNH) % p.nseg, qb = wg / (kNH * p.nseg);
+            const int kvh = h / (kNH / LS::NKV);
+            const int m0 = g * S, q0 = qb * kRB, nq = min(kRB, S - q0);
+            const int SP = S + 1;
+            float *Kf = (float *)(lds + LS::ST), *V = Kf + S * HP, *Q = V + S * HD, *O = Q + kRB * HP,
+                  *P = O + kRB * HD, *mx = P + kRB * SP, *inv = mx + kRB;
+            if (!DMA) {
+                // word pairs: a row of a head holds HALF words, so HP2 = HALF / 2 pairs
+                constexpr int W = LS::NQKV / 2, HP2 = HALF / 2;
+                const int nqp = nq * HP2, n = nqp + 2 * S * HP2;
+                poll<((kRB + 2 * kMaxS) * HP2 + kPollThreads - 1) / kPollThreads>(
+                    p, chan_rsrc(p.qkv, LS::WQKV * 8), n, make_tag(ep, L, l, PH_QKV),
+                    [&](int i) {
+                        if (i < nqp) return ((m0 + q0 + i / HP2) * W + h * HALF + 2 * (i % HP2)) * 8;
+                        const int e = i - nqp, part = e / (S * HP2), j = (e / HP2) % S, wi = 2 * (e % HP2);
+                        return ((m0 + j) * W + (part ? LS::QD + LS::KVD : LS::QD) / 2 + kvh * HALF + wi) * 8;
+                    },
+                    [&](int i, uint32_t a, uint32_t b) {
+                        // q / k word w: dims w and w + HD/2; v word w: dims 2w, 2w + 1
+                        const float a0 = __uint_as_float(a << 16), a1 = __uint_as_float(a & 0xffff0000u);
+                        const float b0 = __uint_as_float(b << 16), b1 = __uint_as_float(b & 0xffff0000u);
+                        float *d;
+                        if (i < nqp) {
+                            d = Q + (i / HP2) * HP + 2 * (i % HP2);
+                        } else {
+                            const int e = i - nqp, part = e / (S * HP2), j = (e / HP2) % S, wi = 2 * (e % HP2);
+                            if (part) {
+                                *(float4 *)(V + j * HD + 2 * wi) = make_float4(a0, a1, b0, b1);
+                                return;
+                            }
+                            d = Kf + j * HP + wi;
+                        }
+                        d[0] = a0;
+                        d[1] = b0;
+                        d[HALF] = a1;
+                        d[HALF + 1] = b1;
+                    },
+                    bail);
+            }
+            lds_barrier();
+            if (*bail) return;
+            VXM_LTS(21);
+            VXM_LTS(5);
+            // scores s_ij = (k_j . q_i) * scale, d in order
+            const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
+            for (int idx = tid; idx < nq * S; idx += kThreads) {
+                const int i = idx / S, j = idx % S;
+                const float4 *kr = (const float4 *)(Kf + j * HP), *qr = (const float4 *)(Q + i * HP);
+                float sc = 0.0f;
+#pragma unroll 8
+                for (int d4 = 0; d4 < HD / 4; d4++) {
+                    const float4 a = kr[d4], b = qr[d4];
+                    sc += a.x * b.x;
+                    sc += a.y * b.y;
+                    sc += a.z * b.z;
+                    sc += a.w * b.w;
+                }
+                P[i * SP + j] = sc * scale;
+            }
+            lds_barrier();
+            VXM_LTS(22);
+            // softmax: wave i takes query row i, lane j key j
+            {
+                const int i = wave, j = lane;
+                if (i < nq) {
+                    const float sj = j < S ? P[i * SP + j] : -INFINITY;
+                    float m = sj;
+#pragma unroll
+                    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+                    const float e = j < S ? expf(sj - m) : 0.0f;
+                    if (j < S) P[i * SP + j] = e;
+                    double sum = (double)e;
+#pragma unroll
+                    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+                    if (j == 0) {
+                        mx[i] = m;
+                        inv[i] = (float)(1.0 / sum);
+                    }
+                }
+            }
+            lds_barrier();
+            VXM_LTS(23);
+            // out[i][d] = sum_j v[j][d] p_ij, p_ij = e_ij * (1/sum_i), j in order (the
+            // oracle's attend_one): one output per thread
+            for (int idx = tid; idx < nq * HD; idx += kThreads) {
+                const int i = idx / HD, d = idx % HD;
+                const float iv = inv[i], *pr = P + i * SP;
+                float o = 0.0f;
+#pragma unroll 8
+                for (int j = 0; j < S; j++) o += V[j * HD + d] * (pr[j] * iv);
+                O[i * HD + d] = o;
+            }
+            lds_barrier();
+            // Q8_0 of the output rows: thread (i, c) holds dims 8c .. 8c+7, four threads a block
+            constexpr int CPR = HD / 8;
+            if (!DMA && tid < nq * CPR) {
+                const uint32_t tg = make_tag(ep, L, l, PH_ATT);
+                const int i = tid / CPR, c = tid % CPR;
+                float o[8], amax = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    o[e] = O[i * HD + 8 * c + e];
+                    amax = fmaxf(amax, fabsf(o[e]));
+                }
+                amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+                amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+                float d, id;
+                q8_scale(amax, p.variant, d, id);
+                uint32_t lo = 0, hi = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    lo |= q8_byte(o[e], id, p.variant) << (8 * e);
+                    hi |= q8_byte(o[4 + e], id, p.variant) << (8 * e);
+                }
+                uint64_t *dst = p.att + (size_t)(m0 + q0 + i) * LS::APitch;
+                const int col = h * HD + 8 * c;
+                put_word(dst + col / 4, lo, tg);
+                put_word(dst + col / 4 + 1, hi, tg);
+                if ((c & 3) == 0) put_word(dst + LS::QD / 4 + col / 32, __float_as_uint(vxm_h2f(vxm_f2h(d))), tg);
+            }
+            lds_barrier();
+        }
+        VXM_LTS(6);
+        // ---- O: 16-column tile oc over K quarter os ----
+        {
+            const int tid = opaque_tid(), lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
+            if (!DMA) {
+                const uint32_t tg = make_tag(ep, L, l, PH_ATT);
+                poll_stage<(kMaxM * 9 * LS::BO / 2 + kPollThreads - 1) / kPollThreads>(
+                    p, chan_rsrc(p.att, LS::WA * 8), LS::APitch, LS::QD / 4, LS::BO * os, LS::BO, M, tg, lds, LS::ST,
+                    LS::ST_SC, bail);
+            } else {
+                if (!is_qkv) issue_d(blk);
+                if (is_gu) issue_gu_a(blk);
+                else if (is_qkv && !last) issue_qkv(p.blocks[l + 1]);
+                if (is_gu && is_qkv)
+                    vm_wait<63>();
+                else if (is_gu)
+                    vm_wait<nD + nGA>();
+                else
+                    vm_wait<nD>();
+            }
+            lds_barrier();
+            if (*bail) return;
+            VXM_LTS(7);
+            zero_acc();
+            mfma_run<MT, LS::BO / kWaves>(lds, LS::RO, LS::RO_SC, LS::BO, 0, LS::ST, LS::ST_SC, LS::BO,
+                                          (LS::BO / kWaves) * wave, lane, acc);
+            lds_barrier();
+            red_store<MT>(lds, LS::ST, wave, lane, acc);
+            lds_barrier();
+            if (!DMA && tid < MT * 64) {
+                const uint32_t tg = make_tag(ep, L, l, PH_O);
+                const int t = tid >> 6, m = 16 * t + r16;
+                float o[4];
+                red_sum<MT>(lds, LS::ST, 1, 0, t, lane, o);
+                if (m < M) {
+                    uint64_t *dst = p.op + ((size_t)os * M + m) * kH + 16 * oc + 4 * q4;
+#pragma unroll
+                    for (int v = 0; v < 4; v++) put_word(dst + v, __float_as_uint(o[v]), tg);
+                }
+            }
+            lds_barrier();
+        }
+        VXM_LTS(8);
+        // ---- N2: x += O; RMSNorm(g_post) -> Q8_0 ----
+        if (row >= 0) {
+            if (!DMA) {
+                stage_gain(blk.g_post);
+                poll_partials<(kOSplits * kH / 2 + kPollThreads - 1) / kPollThreads>(
+                    p, chan_rsrc(p.op, LS::WOP * 8), kOSplits, M, row, make_tag(ep, L, l, PH_O), lds, LS::ST, bail);
+            }
+            lds_barrier();
+            if (*bail) return;
+            VXM_LTS(9);
+            row_update(lds, LS::ST, LS::XR, LS::GN, LS::MISC, kOSplits, p.eps, p.variant,
+                       p.x2 + (size_t)row * kXPitch, make_tag(ep, L, l, PH_X2), true);
+            lds_barrier();
+        }
+        VXM_LTS(10);
+        // ---- gate/up: 64 interleaved rows -> 32 SwiGLU outputs -> one Q8_0 block per row ----
+        if (is_gu) {
+            const int tid = opaque_tid(), lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
+            if (!DMA) {
+                const uint32_t tg = make_tag(ep, L, l, PH_X2);
+                poll_stage<(kMaxM * kXPitch / 2 + kPollThreads - 1) / kPollThreads>(
+                    p, chan_rsrc(p.x2, LS::WX * 8), kXPitch, kH / 4, 0, 32, M, tg, lds, LS::ST, LS::ST_SC, bail);
+            } else {
+                issue_gu_b(blk);
+                if (last) {
+                    vm_wait<0>();
+                } else {
+                    issue_o(p.blocks[l + 1]);
+                    vm_wait<nO>();
+                }
+            }
+            lds_barrier();
+            if (*bail) return;
+            VXM_LTS(11);
+            zero_acc();
+            const int ct = wave & 3, kh = wave >> 2;
+            mfma_run<MT, 16, 8>(lds, LS::RA, LS::RA_SC, 32, ct, LS::ST, LS::ST_SC, 32, 16 * kh, lane, acc);
+            lds_barrier();
+            VXM_LTS(18);
+            red_store<MT>(lds, LS::ST, wave, lane, acc);
+            lds_barrier();
+            VXM_LTS(19);
+            float *ps = (float *)(lds + LS::ST + kWaves * kMT * 4 * 64 * 4);   // [kMP][33]
+            for (int idx = tid; idx < 4 * MT * 64; idx += kThreads) {
+                const int ct2 = idx / (MT * 64), t = (idx / 64) % MT;
+                float o[4];
+                red_sum<MT>(lds, LS::ST, 4, ct2, t, lane, o);
+                const int m = 16 * t + r16;
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    // rows 2j (gate) and 2j + 1 (up) of the interleaved weight
+                    const float gb = bf16r(o[2 * e]);
+                    const float s = bf16r(__fdiv_rn(gb, 1.0f + expf(-gb)));
+                    ps[m * 33 + 8 * ct2 + 2 * q4 + e] = bf16r(s * bf16r(o[2 * e + 1]));
+                }
+            }
+            lds_barrier();
+            VXM_LTS(20);
+            if (!DMA && tid < 4 * M) {
+                const uint32_t tg = make_tag(ep, L, l, PH_P);
+                const int m = tid >> 2, part = tid & 3;
+                float o[8], amax = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    o[e] = ps[m * 33 + 8 * part + e];
+                    amax = fmaxf(amax, fabsf(o[e]));
+                }
+                amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+                amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+                float d, id;
+                q8_scale(amax, p.variant, d, id);
+                uint32_t lo = 0, hi = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    lo |= q8_byte(o[e], id, p.variant) << (8 * e);
+                    hi |= q8_byte(o[4 + e], id, p.variant) << (8 * e);
+                }
+                uint64_t *dst = p.pp + (size_t)m * kPPitch;
+                const int col = 32 * ugu + 8 * part;
+                put_word(dst + col / 4, lo, tg);
+                put_word(dst + col / 4 + 1, hi, tg);
+                if (part == 0) put_word(dst + kF / 4 + ugu, __float_as_uint(vxm_h2f(vxm_f2h(d))), tg);
+            }
+            lds_barrier();
+        }
+        VXM_LTS(12);
+        // ---- down: 32-column tile dc over K eighth ds ----
+        {
+            const int tid = opaque_tid(), lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
+            if (!DMA) {
+                const uint32_t tg = make_tag(ep, L, l, PH_P);
+                poll_stage<(kMaxM * 9 * 16 / 2 + kPollThreads - 1) / kPollThreads>(
+                    p, chan_rsrc(p.pp, LS::WP * 8), kPPitch, kF / 4, 16 * ds, 16, M, tg, lds, LS::ST, LS::ST_SC, bail);
+            } else {
+                if (!last && !is_gu) issue_o(p.blocks[l + 1]);
+                if (!last && is_gu && is_qkv) issue_qkv(p.blocks[l + 1]);
+                if (is_gu)
+                    vm_wait<63>();
+                else if (last)
+                    vm_wait<0>();
+                else if (is_qkv)
+                    vm_wait<nQKV + nO>();
+                else
+                    vm_wait<nO>();
+            }
+            lds_barrier();
+            if (*bail) return;
+            VXM_LTS(13);
+            zero_acc();
+            const int ct = wave & 1, kq = wave >> 1;
+            mfma_run<MT, 4>(lds, LS::RD, LS::RD_SC, 16, ct, LS::ST, LS::ST_SC, 16, 4 * kq, lane, acc);
+            lds_barrier();
+            red_store<MT>(lds, LS::ST, wave, lane, acc);
+            lds_barrier();
+            if (!DMA && tid < 2 * MT * 64) {
+                const uint32_t tg = make_tag(ep, L, l, PH_D);
+                const int ct2 = tid / (MT * 64), t = (tid / 64) % MT, m = 16 * t + r16;
+                float o[4];
+                red_sum<MT>(lds, LS::ST, 2, ct2, t, lane, o);
+                if (m < M) {
+                    uint64_t *dst = p.dp + ((size_t)ds * M + m) * kH + 32 * dc + 16 * ct2 + 4 * q4;
+#pragma unroll
+                    for (int v = 0; v < 4; v++) put_word(dst + v, __float_as_uint(o[v]), tg);
+                }
+            }
+            lds_barrier();
+        }
+        VXM_LTS(14);
+        // the last block: row owners add its down projection and write x out
+        if (last && row >= 0) {
+            if (!DMA)
+                poll_partials<(kDSplits * kH / 2 + kPollThreads - 1) / kPollThreads>(
+                    p, chan_rsrc(p.dp, LS::WDP * 8), kDSplits, M, row, make_tag(ep, L, l, PH_D), lds, LS::ST, bail);
+            lds_barrier();
+            if (*bail) return;
+            VXM_LTS(15);
+            row_update(lds, LS::ST, LS::XR, LS::GN, LS::MISC, kDSplits, 0.0f, p.variant, nullptr, 0, false);
+            lds_barrier();
+            const int tid = opaque_tid();
+            for (int c = tid * 4; c < kH; c += kThreads * 4)
+                *(float4 *)(p.x + (size_t)row * kH + c) = *(const float4 *)(lds + LS::XR + c * 4);
+        }
+    }
+}
+
+template <class LS, int MT>
+__global__ __launch_bounds__(kThreads, 1) void k_locdit_persistent(vxm_lparams p) {
+    // All of the workgroup's LDS is this one dynamic array, so it starts at address 0
+    // (the weight DMAs address it absolutely) and every layout offset is aligned.
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    int *bail = (int *)(lds + LS::MISC + 64);
+    uint32_t *ep_sh = (uint32_t *)(lds + LS::MISC + 68);
+    const int wg = blockIdx.x, tid = threadIdx.x;
+    if (tid == 0) {
+        *bail = 0;
+        *ep_sh = __hip_atomic_load(p.state, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#ifdef VXM_PERSISTENT_TRACE
+        if (p.trace) p.trace[(size_t)wg * (1 + kTraceSlots * p.L)] = __builtin_amdgcn_s_memrealtime();
+#endif
+    }
+    // block 0's input rows
+    if (wg < p.M)
+        for (int c = tid * 4; c < kH; c += kThreads * 4)
+            *(float4 *)(lds + LS::XR + c * 4) = *(const float4 *)(p.x + (size_t)wg * kH + c);
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    lds_barrier();
+    const uint32_t ep = *ep_sh;
+    if ((tid >> 6) == kWaves - 1) run_blocks<LS, MT, true>(p, lds, bail, ep);
+    else run_blocks<LS, MT, false>(p, lds, bail, ep);
+    // every weight load of wave 7 has landed before the workgroup ends
+    vm_wait<0>();
+    lds_barrier();
+    if (tid == 0) {
+        const uint32_t done = __hip_atomic_fetch_add(p.state + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == kG - 1) {
+            // the last workgroup: every workgroup has read the epoch; the next launch uses the next one
+            __hip_atomic_store(p.state + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p.state, ep + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+using ShapeDitMha = LShape<16, 64>;
+using ShapeDitGqa = LShape<2, 128>;
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+struct vxm_lpersist {
+    void *base = nullptr;
+    vxm_lblock *blocks = nullptr;
+    int L = 0;
+    std::vector<const void *> key;   // the weight pointers the table holds
+    uint64_t *chan[7] = {};
+    int *err = nullptr;
+    uint32_t *state = nullptr;
+};
+
+// Supported: hidden 1024, FFN 4096, 16 query heads of (16 kv heads x 64) or
+// (2 kv heads x 128), M <= 48 rows in segments of S <= 32, 256 CUs.
+bool vxm_locdit_persistent_fits(vxm_ctx *ctx, const vxm_block_dims &d, int64_t M, int S) {
+    if (ctx->n_cu != kG || d.H != kH || d.F != kF || d.nh != kNH || d.no_rope || d.res_scale != 1.0f) return false;
+    if (!((d.nkv == 16 && d.hd == 64) || (d.nkv == 2 && d.hd == 128))) return false;
+    if (M <= 0 || M > kMaxM || S <= 0 || S > kMaxS || M % S) return false;
+    if (!d.rope_cs || d.rope_rows < S) return false;
+    return true;
+}
+
+// AUTO takes the single launch where it measured faster than launch by launch: the
+// 16 q / 2 kv x 128 layout (the reference's LocDiT at 2 x 11 rows and the LocEnc), not
+// the 16 x 64 MHA layout at 2 x 24 rows, whose larger exchanges (every row's
+// activations to every tile of QKV and gate/up) cost more than the launches they save.
+bool vxm_locdit_persistent_pick(vxm_ctx *ctx, const vxm_block_dims &d, int64_t M, int S, int mode) {
+    if (mode == VXM_DECODE_KERNELS || !vxm_locdit_persistent_fits(ctx, d, M, S)) return false;
+    return mode == VXM_DECODE_PERSISTENT || d.hd == 128;
+}
+
+void vxm_locdit_persistent_free(vxm_lpersist *st) {
+    if (!st) return;
+    if (st->base) (void)hipFree(st->base);
+    delete st;
+}
+
+static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::vector<vxm_block> &blocks,
+                              vxm_lpersist **stp, float *x, int64_t M, int S) {
+    if (!vxm_locdit_persistent_fits(ctx, d, M, S))
+        return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "persistent blocks: unsupported shape (M=%lld S=%d)",
+                        (long long)M, S);
+    const int L = (int)blocks.size();
+    if (L <= 0) return VXM_OK;
+    std::vector<const void *> key;
+    for (const vxm_block &b : blocks) {
+        const vxm_weight *w[4] = {b.wqkv, b.wo, b.wgu, b.wd};
+        for (const vxm_weight *wi : w) {
+            if (!wi || !aligned16(wi->qs) || !aligned16(wi->d))
+                return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "persistent blocks: weights not 16-byte aligned");
+            key.push_back(wi->qs);
+            key.push_back(wi->d);
+        }
+        key.push_back(b.g_in);
+        key.push_back(b.g_post);
+    }
+    vxm_lpersist *st = *stp;
+    if (!st || st->L != L || st->key != key) {
+        vxm_locdit_persistent_free(st);
+        *stp = nullptr;
+        st = new vxm_lpersist();
+        st->L = L;
+        st->key = key;
+        const int qd = kNH * d.hd, nqkv = qd + 2 * d.nkv * d.hd;
+        const size_t words[7] = {(size_t)kMaxM * kXPitch,
+                                 (size_t)kMaxM * nqkv / 2,
+                                 (size_t)kMaxM * (qd / 4 + qd / 32),
+                                 (size_t)kOSplits * kMaxM * kH,
+                                 (size_t)kMaxM * kXPitch,
+                                 (size_t)kMaxM * kPPitch,
+                                 (size_t)kDSplits * kMaxM * kH};
+        size_t total = 0;
+        for (size_t w : words) total += (w * 8 + 255) & ~(size_t)255;
+        const size_t tab = ((size_t)L * sizeof(vxm_lblock) + 255) & ~(size_t)255;
+        const size_t bytes = total + tab + 256;
+        if (hipMalloc(&st->base, bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            delete st;
+            return vxm_fail(ctx, VXM_ERR_OOM, "persistent blocks: %zu bytes of exchange buffers", bytes);
+        }
+        char *b = (char *)st->base;
+        for (int c = 0; c < 7; c++) {
+            st->chan[c] = (uint64_t *)b;
+            b += (words[c] * 8 + 255) & ~(size_t)255;
+        }
+        st->blocks = (vxm_lblock *)b;
+        b += tab;
+        st->err = (int *)b;
+        st->state = (uint32_t *)(b + 64);
+        std::vector<vxm_lblock> th(L);
+        for (int l = 0; l < L; l++) {
+            const vxm_block &bl = blocks[l];
+            th[l] = vxm_lblock{bl.wqkv->qs, bl.wo->qs, bl.wgu->qs, bl.wd->qs, bl.wqkv->d, bl.wo->d,
+                               bl.wgu->d,   bl.wd->d,  bl.g_in,    bl.g_post};
+        }
+        // zeroed words carry an even tag, never a live (odd) one; epoch 1, no workgroup finished
+        const uint32_t st0[2] = {1u, 0u};
+        if (hipMemset(st->base, 0, bytes) != hipSuccess ||
+            hipMemcpy(st->blocks, th.data(), L * sizeof(vxm_lblock), hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(st->state, st0, sizeof st0, hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipGetLastError();
+            vxm_locdit_persistent_free(st);
+            return vxm_fail(ctx, VXM_ERR_BACKEND, "persistent blocks: buffer set-up failed");
+        }
+        // the kernels' LDS limit, set here rather than at a launch that may be under graph capture
+        const void *kern[6] = {(const void *)k_locdit_persistent<ShapeDitMha, 1>,
+                               (const void *)k_locdit_persistent<ShapeDitMha, 2>,
+                               (const void *)k_locdit_persistent<ShapeDitMha, 3>,
+                               (const void *)k_locdit_persistent<ShapeDitGqa, 1>,
+                               (const void *)k_locdit_persistent<ShapeDitGqa, 2>,
+                               (const void *)k_locdit_persistent<ShapeDitGqa, 3>};
+        bool attr_ok = true;
+        for (int i = 0; i < 6; i++)
+            attr_ok &= hipFuncSetAttribute(kern[i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           i < 3 ? ShapeDitMha::BYTES : ShapeDitGqa::BYTES) == hipSuccess;
+        if (!attr_ok) {
+            (void)hipGetLastError();
+            vxm_locdit_persistent_free(st);
+            return vxm_fail(ctx, VXM_ERR_BACKEND, "persistent blocks: LDS limit not accepted");
+        }
+        *stp = st;
+    }
+    vxm_lparams prm{};
+    prm.blocks = st->blocks;
+    prm.L = L;
+    prm.M = (int)M;
+    prm.S = S;
+    prm.nseg = (int)(M / S);
+    prm.qb = (S + kRB - 1) / kRB;
+    prm.eps = d.eps;
+    prm.variant = ctx->quant_variant;
+    prm.cs = d.rope_cs;
+    prm.x = x;
+    prm.x1 = st->chan[0];
+    prm.qkv = st->chan[1];
+    prm.att = st->chan[2];
+    prm.op = st->chan[3];
+    prm.x2 = st->chan[4];
+    prm.pp = st->chan[5];
+    prm.dp = st->chan[6];
+    prm.err = st->err;
+    prm.state = st->state;
+    if (kNH * prm.nseg * prm.qb > kG)
+        return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "persistent blocks: too many attention units");
+    // All 256 workgroups wait on each other's words, so all must be resident: one per CU
+    // (the LDS layout takes more than half of a CU's).  Every wait is bounded (kSpin
+    // rounds, then the error word), so other work on the device can only turn a launch
+    // into an error, never a hang.  Launches on one stream run one after another.
+#ifdef VXM_PERSISTENT_TRACE
+    // profiling build: timestamps of every launch into $VXM_TRACE_DIR/ltrace_L<blocks>_M<rows>_<n>.bin
+    const size_t tstride = 1 + (size_t)kTraceSlots * L, tbytes = (size_t)kG * tstride * 8;
+    static uint64_t *tbuf = nullptr;
+    static size_t tcap = 0;
+    static int ncall = 0;
+    if (tcap < tbytes) {
+        if (tbuf) (void)hipFree(tbuf);
+        tbuf = nullptr;
+        tcap = 0;
+        VXM_HIP(ctx, hipMalloc(&tbuf, tbytes));
+        tcap = tbytes;
+    }
+    VXM_HIP(ctx, hipMemset(tbuf, 0, tbytes));
+    prm.trace = tbuf;
+#endif
+    // row tiles of 16 as a template argument: the products' loops unroll completely
+    const int mt = (int)((M + 15) / 16);
+#define VXM_LP_LAUNCH(LS, MT)                                                                                \
+    hipLaunchKernelGGL((k_locdit_persistent<LS, MT>), dim3(kG), dim3(kThreads), (unsigned)LS::BYTES, ctx->stream, prm)
+    if (d.nkv == 16) {
+        if (mt == 1) VXM_LP_LAUNCH(ShapeDitMha, 1);
+        else if (mt == 2) VXM_LP_LAUNCH(ShapeDitMha, 2);
+        else VXM_LP_LAUNCH(ShapeDitMha, 3);
+    } else {
+        if (mt == 1) VXM_LP_LAUNCH(ShapeDitGqa, 1);
+        else if (mt == 2) VXM_LP_LAUNCH(ShapeDitGqa, 2);
+        else VXM_LP_LAUNCH(ShapeDitGqa, 3);
+    }
+#undef VXM_LP_LAUNCH
+    VXM_CHECK_LAUNCH(ctx);
+#ifdef VXM_PERSISTENT_TRACE
+    {
+        std::vector<uint64_t> th((size_t)kG * tstride);
+        VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        VXM_HIP(ctx, hipMemcpy(th.data(), tbuf, tbytes, hipMemcpyDeviceToHost));
+        const char *dir = getenv("VXM_TRACE_DIR");
+        char fn[512];
+        snprintf(fn, sizeof fn, "%s/ltrace_L%d_M%d_%04d.bin", dir ? dir : ".", L, (int)M, ncall++);
+        if (FILE *f = fopen(fn, "wb")) {
+            fwrite(th.data(), 8, th.size(), f);
+            fclose(f);
+        }
+    }
+#endif
+    return VXM_OK;
+}
+
+int vxm_locdit_persistent_check(vxm_ctx *ctx, vxm_lpersist *st) {
+    if (!st || !st->err) return VXM_OK;
+    int e = 0;
+    VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    VXM_HIP(ctx, hipMemcpy(&e, st->err, 4, hipMemcpyDeviceToHost));
+    if (e) {
+        VXM_HIP(ctx, hipMemset(st->err, 0, 4));
+        return vxm_fail(ctx, VXM_ERR_BACKEND, "persistent blocks: a workgroup timed out waiting for data");
+    }
+    return VXM_OK;
+}

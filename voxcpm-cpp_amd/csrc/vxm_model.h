@@ -94,3 +94,14 @@ void vxm_rope_free(vxm_block_dims &d);
 int vxm_upload_vec(vxm_ctx *ctx, const float *src, int64_t n, float **out);
 int vxm_block_run(vxm_ctx *ctx, const vxm_block_dims &d, const vxm_block &b, vxm_workspace &ws, float *x,
                   int64_t M, const vxm_attn_site &site);
+
+// every non-causal block of a LocDiT / LocEnc evaluation in one launch (locdit_persistent.hip):
+// x [M][H] holds block 0's input and receives the last block's output (its residual added)
+struct vxm_lpersist;
+bool vxm_locdit_persistent_fits(vxm_ctx *ctx, const vxm_block_dims &d, int64_t M, int S);
+// the block strategy (VXM_DECODE_*) resolved for one evaluation: true = the single launch
+bool vxm_locdit_persistent_pick(vxm_ctx *ctx, const vxm_block_dims &d, int64_t M, int S, int mode);
+int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::vector<vxm_block> &blocks,
+                              vxm_lpersist **st, float *x, int64_t M, int S);
+int vxm_locdit_persistent_check(vxm_ctx *ctx, vxm_lpersist *st);
+void vxm_locdit_persistent_free(vxm_lpersist *st);

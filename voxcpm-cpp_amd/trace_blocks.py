@@ -1,0 +1,77 @@
+"""Per-phase timeline of k_locdit_persistent from the profiling build's timestamps.
+
+Usage: python3 trace_blocks.py <dir with ltrace_L*_M*_*.bin> [first launch to use]
+
+Every workgroup writes the 100 MHz real-time counter at its start and, per
+block, at 16 points: 0 block start; then for each phase (N1, QKV, ATT, O, N2,
+GU, D) the moment its inputs are in LDS (odd slots 1..13, written only by the
+workgroups that have that phase) and the moment the workgroup leaves the phase
+(even slots 2..14); slot 15 = the last block's final inputs.  For each phase:
+  hop   = from the last producer leaving the previous phase to the median
+          consumer having all its inputs,
+  work  = from the median consumer's inputs to the last consumer leaving.
+"""
+import glob
+import os
+import sys
+
+import numpy as np
+
+SLOTS = 24
+PHASES = ["N1 (norm)", "QKV", "attention", "O", "N2 (norm)", "gate/up", "down"]
+
+
+def load(path):
+    base = os.path.basename(path)
+    L = int(base.split("_L")[1].split("_")[0])
+    a = np.fromfile(path, dtype=np.uint64).astype(np.int64)
+    return L, a.reshape(256, 1 + SLOTS * L)
+
+
+def main():
+    d = sys.argv[1]
+    skip = int(sys.argv[2]) if len(sys.argv) > 2 else 1
+    files = sorted(glob.glob(os.path.join(d, "ltrace_*.bin")))[skip:]
+    if not files:
+        sys.exit("no ltrace files")
+    rows = {p: ([], []) for p in PHASES}
+    totals = []
+    for f in files:
+        L, t = load(f)
+        start = t[:, 0]
+        totals.append((t[:, 1 + SLOTS * (L - 1) + 14].max() - start.min()) / 100.0)
+        for l in range(L):
+            m = t[:, 1 + SLOTS * l: 1 + SLOTS * (l + 1)]
+            prev_done = None if l == 0 else t[:, 1 + SLOTS * (l - 1) + 14]
+            for k, name in enumerate(PHASES):
+                ready, done = m[:, 2 * k + 1], m[:, 2 * k + 2]
+                who = ready > 0
+                if not who.any():
+                    continue
+                if k == 0:
+                    if prev_done is None:
+                        continue
+                    last_prod = prev_done.max()
+                else:
+                    pr = m[:, 2 * k - 1] > 0
+                    last_prod = m[pr, 2 * k].max()
+                hop = (np.median(ready[who]) - last_prod) / 100.0
+                work = (done[who].max() - np.median(ready[who])) / 100.0
+                rows[name][0].append(hop)
+                rows[name][1].append(work)
+    print(f"{len(files)} launches; launch start to last block's down: median {np.median(totals):.1f} us")
+    print("| phase | hop us (median) | work us (median) |")
+    print("|---|---|---|")
+    th = tw = 0.0
+    for name in PHASES:
+        h, w = rows[name]
+        if not h:
+            continue
+        th += np.median(h)
+        tw += np.median(w)
+        print(f"| {name} | {np.median(h):.2f} | {np.median(w):.2f} |")
+    print(f"| per block | {th:.2f} | {tw:.2f} |")
+
+
+if __name__ == "__main__":
+    main()

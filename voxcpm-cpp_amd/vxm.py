@@ -25,6 +25,9 @@ PATH_AUTO = 0
 PATH_GEMV = 1
 PATH_MFMA = 2
 PATH_MFMA_TILED = 3
+DECODE_AUTO = 0          # block strategies (vxm_minicpm4_set_decode_mode, vxm_locdit_set_block_mode)
+DECODE_KERNELS = 1
+DECODE_PERSISTENT = 2
 
 STATUS = {
     0: "VXM_OK",
@@ -98,6 +101,8 @@ _SIGS = {
     "vxm_locdit_free": (_I, [_P]),
     "vxm_locdit_forward": (_I, [_P, _P, _P, C.c_int32, C.c_int32, _F, _F, _P, _P]),
     "vxm_cfm_solve": (_I, [_P, _P, _P, C.c_int32, C.c_int32, _P, C.c_int32, _F, C.c_int32, C.c_int32]),
+    "vxm_locdit_set_block_mode": (_I, [_P, _I]),
+    "vxm_locdit_check": (_I, [_P]),
     "vxm_host_sinusoid_embed": (_I, [_F, C.c_int32, _P]),
     "vxm_host_cfm_t": (_F, [C.c_int32, C.c_int32, C.c_int32]),
     "vxm_host_cfm_zero_star_steps": (C.c_int32, [C.c_int32]),
@@ -105,6 +110,8 @@ _SIGS = {
     "vxm_locenc_create": (_I, [_P, _P, _P, C.POINTER(_P)]),
     "vxm_locenc_free": (_I, [_P]),
     "vxm_locenc_forward": (_I, [_P, _P, C.c_int32, _P]),
+    "vxm_locenc_set_block_mode": (_I, [_P, _I]),
+    "vxm_locenc_check": (_I, [_P]),
     "vxm_fsq_quantize": (_I, [_P, _P, _I64, _F, _P]),
     "vxm_lm_update_create": (_I, [_P, _P, _P, _P, _P, _P, C.POINTER(_P)]),
     "vxm_lm_update_free": (_I, [_P]),
@@ -536,6 +543,14 @@ class LocDiT:
                                            schedule, int(use_zero_star)))
         return x
 
+    def set_block_mode(self, mode):
+        """DECODE_AUTO / DECODE_KERNELS / DECODE_PERSISTENT: how the blocks of an evaluation launch."""
+        self.ctx.check(lib().vxm_locdit_set_block_mode(self.h, mode))
+
+    def check(self):
+        """Synchronise; raise if a persistent block launch timed out on the device."""
+        self.ctx.check(lib().vxm_locdit_check(self.h))
+
     def free(self):
         if self.h:
             self.ctx.check(lib().vxm_locdit_free(self.h))
@@ -691,6 +706,14 @@ class LocEnc:
             out = torch.empty(shape, dtype=torch.float32, device=x.device)
         self.ctx.check(lib().vxm_locenc_forward(self.h, _ptr(x), P, _ptr(out)))
         return out
+
+    def set_block_mode(self, mode):
+        """DECODE_AUTO / DECODE_KERNELS / DECODE_PERSISTENT: how the blocks launch."""
+        self.ctx.check(lib().vxm_locenc_set_block_mode(self.h, mode))
+
+    def check(self):
+        """Synchronise; raise if a persistent block launch timed out on the device."""
+        self.ctx.check(lib().vxm_locenc_check(self.h))
 
     def free(self):
         if self.h:
