@@ -372,12 +372,16 @@ def locdit_eval_bytes(d=DIT):
     return d["L"] * blk + 2 * q8_bytes(H, FEAT) + q8_bytes(FEAT, H)
 
 
-def bench_cfm(ctx, torch, vxm, reps, n_steps=10, d=DIT, schedule=None):
+BLOCK_MODES = {"auto": 0, "kernels": 1, "persistent": 2}   # vxm_locdit_set_block_mode
+
+
+def bench_cfm(ctx, torch, vxm, reps, n_steps=10, d=DIT, schedule=None, blocks="auto"):
     """CFM solves: n_steps Euler steps (uniform unless schedule says otherwise), CFG 2.0 with CFG-Zero*
     (both branches in one batch of 2 x (3 + PC + P) rows per LocDiT evaluation), latent P x 64, PC cond
-    tokens."""
+    tokens; blocks: the block strategy (launch by launch, one persistent launch, or the library's pick)."""
     cfg, w = make_locdit(vxm, 21, d)
     m = vxm.LocDiT(ctx, cfg, w)
+    m.set_block_mode(BLOCK_MODES[blocks])
     P, PC, H, FEAT = d["P"], d["PC"], d["H"], d["FEAT"]
     schedule = vxm.CFM_UNIFORM if schedule is None else schedule
     x0 = torch.from_numpy(vxm.host_randn(22, P * FEAT).reshape(P, FEAT)).to("cuda:0")
@@ -574,6 +578,8 @@ def main():
                     help="time only the prefill legs (MFMA GEMMs and the 512-token 28-layer prefill)")
     ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--cfm-only", action="store_true", help="time only the CFM solve leg")
+    ap.add_argument("--blocks", default="auto", choices=list(BLOCK_MODES),
+                    help="LocDiT block strategy of the CFM legs (auto: the library's pick per shape)")
     ap.add_argument("--gemv-only", action="store_true", help="time only the isolated Q8_0 GEMV leg")
     ap.add_argument("--lm-update-only", action="store_true", help="time only the per-token LM update leg")
     ap.add_argument("--long-context-only", action="store_true",
@@ -602,17 +608,18 @@ def main():
     pre = None
     cfm = None
     if not (args.decode_only or args.prefill_only or args.gemv_only or args.lm_update_only or args.long_context_only):
-        us_cfm, evals, fin = bench_cfm(ctx, torch, vxm, 5)
+        us_cfm, evals, fin = bench_cfm(ctx, torch, vxm, 5, blocks=args.blocks)
         eb = locdit_eval_bytes()
         ops = 2 * 2 * (3 + DIT["PC"] + DIT["P"]) * (eb * 32 // 34)
         cfm = {"us_per_solve": round(us_cfm, 1), "evals": evals, "us_per_eval": round(us_cfm / evals, 1),
                "weight_GBs": round(evals * eb / (us_cfm * 1e-6) / 1e9, 1),
                "int8_TOPs": round(evals * ops / (us_cfm * 1e-6) / 1e12, 2), "finite": fin,
+               "blocks": args.blocks,
                "note": "10 uniform steps, CFG 2.0 + CFG-Zero* (first step skipped), both branches batched "
                        "(M = 2 x 24); weights 214 MB per evaluation, Infinity-Cache resident"}
         log(f"cfm solve: {us_cfm:.1f} us for {evals} evaluations ({us_cfm / evals:.1f} us each), "
             f"{cfm['weight_GBs']} GB/s of weights, finite={fin}")
-        us_r, evals_r, fin_r = bench_cfm(ctx, torch, vxm, 5, 10, DIT_REF, vxm.CFM_SWAY)
+        us_r, evals_r, fin_r = bench_cfm(ctx, torch, vxm, 5, 10, DIT_REF, vxm.CFM_SWAY, blocks=args.blocks)
         ebr = locdit_eval_bytes(DIT_REF)
         rows_r = 2 * (3 + DIT_REF["PC"] + DIT_REF["P"])
         cfm["reference_shape"] = {

@@ -611,21 +611,26 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             if (*bail) return;
             VXM_LTS(21);
             VXM_LTS(5);
-            // scores s_ij = (k_j . q_i) * scale, d in order
+            // scores s_ij = (k_j . q_i) * scale: eight lanes per score, each a run of HD / 8
+            // dims in order, the eight partial sums added pairwise across the lanes
             const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
-            for (int idx = tid; idx < nq * S; idx += kThreads) {
-                const int i = idx / S, j = idx % S;
-                const float4 *kr = (const float4 *)(Kf + j * HP), *qr = (const float4 *)(Q + i * HP);
+            for (int idx = tid; idx < nq * S * 8; idx += kThreads) {
+                const int ij = idx >> 3, part = idx & 7, i = ij / S, j = ij % S;
+                const float4 *kr = (const float4 *)(Kf + j * HP) + part * (HD / 32),
+                             *qr = (const float4 *)(Q + i * HP) + part * (HD / 32);
                 float sc = 0.0f;
-#pragma unroll 8
-                for (int d4 = 0; d4 < HD / 4; d4++) {
+#pragma unroll
+                for (int d4 = 0; d4 < HD / 32; d4++) {
                     const float4 a = kr[d4], b = qr[d4];
                     sc += a.x * b.x;
                     sc += a.y * b.y;
                     sc += a.z * b.z;
                     sc += a.w * b.w;
                 }
-                P[i * SP + j] = sc * scale;
+                sc += __shfl_xor(sc, 1, 64);
+                sc += __shfl_xor(sc, 2, 64);
+                sc += __shfl_xor(sc, 4, 64);
+                if (part == 0) P[i * SP + j] = sc * scale;
             }
             lds_barrier();
             VXM_LTS(22);
@@ -1072,20 +1077,26 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
     // rounds, then the error word), so other work on the device can only turn a launch
     // into an error, never a hang.  Launches on one stream run one after another.
 #ifdef VXM_PERSISTENT_TRACE
-    // profiling build: timestamps of every launch into $VXM_TRACE_DIR/ltrace_L<blocks>_M<rows>_<n>.bin
+    // profiling build: timestamps of every eager launch into
+    // $VXM_TRACE_DIR/ltrace_L<blocks>_M<rows>_<n>.bin (launches recorded into a graph run untraced)
     const size_t tstride = 1 + (size_t)kTraceSlots * L, tbytes = (size_t)kG * tstride * 8;
     static uint64_t *tbuf = nullptr;
     static size_t tcap = 0;
     static int ncall = 0;
-    if (tcap < tbytes) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    VXM_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cap));
+    const bool traced = cap == hipStreamCaptureStatusNone;
+    if (traced && tcap < tbytes) {
         if (tbuf) (void)hipFree(tbuf);
         tbuf = nullptr;
         tcap = 0;
         VXM_HIP(ctx, hipMalloc(&tbuf, tbytes));
         tcap = tbytes;
     }
-    VXM_HIP(ctx, hipMemset(tbuf, 0, tbytes));
-    prm.trace = tbuf;
+    if (traced) {
+        VXM_HIP(ctx, hipMemset(tbuf, 0, tbytes));
+        prm.trace = tbuf;
+    }
 #endif
     // row tiles of 16 as a template argument: the products' loops unroll completely
     const int mt = (int)((M + 15) / 16);
@@ -1103,7 +1114,7 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
 #undef VXM_LP_LAUNCH
     VXM_CHECK_LAUNCH(ctx);
 #ifdef VXM_PERSISTENT_TRACE
-    {
+    if (traced) {
         std::vector<uint64_t> th((size_t)kG * tstride);
         VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
         VXM_HIP(ctx, hipMemcpy(th.data(), tbuf, tbytes, hipMemcpyDeviceToHost));

@@ -1,12 +1,14 @@
 """Per-phase timeline of k_locdit_persistent from the profiling build's timestamps.
 
-Usage: python3 trace_blocks.py <dir with ltrace_L*_M*_*.bin> [first launch to use]
+Usage: python3 trace_blocks.py <dir with ltrace_L*_M*_*.bin> [rows M] [launches to skip]
 
 Every workgroup writes the 100 MHz real-time counter at its start and, per
-block, at 16 points: 0 block start; then for each phase (N1, QKV, ATT, O, N2,
+block, at 24 points: 0 block start; then for each phase (N1, QKV, ATT, O, N2,
 GU, D) the moment its inputs are in LDS (odd slots 1..13, written only by the
 workgroups that have that phase) and the moment the workgroup leaves the phase
-(even slots 2..14); slot 15 = the last block's final inputs.  For each phase:
+(even slots 2..14); slot 15 = the last block's final inputs; 16..23 steps inside
+QKV (products, partial sums), the attention (scores, softmax, P.V) and gate/up
+(products, partial sums, SwiGLU).  For each phase:
   hop   = from the last producer leaving the previous phase to the median
           consumer having all its inputs,
   work  = from the median consumer's inputs to the last consumer leaving.
@@ -30,8 +32,9 @@ def load(path):
 
 def main():
     d = sys.argv[1]
-    skip = int(sys.argv[2]) if len(sys.argv) > 2 else 1
-    files = sorted(glob.glob(os.path.join(d, "ltrace_*.bin")))[skip:]
+    rows = sys.argv[2] if len(sys.argv) > 2 else "*"
+    skip = int(sys.argv[3]) if len(sys.argv) > 3 else 1
+    files = sorted(glob.glob(os.path.join(d, f"ltrace_L*_M{rows}_*.bin")))[skip:]
     if not files:
         sys.exit("no ltrace files")
     rows = {p: ([], []) for p in PHASES}
@@ -71,6 +74,26 @@ def main():
         tw += np.median(w)
         print(f"| {name} | {np.median(h):.2f} | {np.median(w):.2f} |")
     print(f"| per block | {th:.2f} | {tw:.2f} |")
+    # steps inside phases: median over the workgroups that run them of (slot b - slot a)
+    steps = [("QKV: products", 3, 16), ("QKV: partial sums to LDS", 16, 17), ("QKV: epilogue + publish", 17, 4),
+             ("attention: scores", 21, 22), ("attention: softmax", 22, 23), ("attention: P.V + Q8_0 + publish", 23, 6),
+             ("gate/up: products", 11, 18), ("gate/up: partial sums to LDS", 18, 19), ("gate/up: SwiGLU", 19, 20),
+             ("gate/up: Q8_0 + publish", 20, 12)]
+    sub = {n: [] for n, _, _ in steps}
+    for f in files:
+        L, t = load(f)
+        for l in range(L):
+            m = t[:, 1 + SLOTS * l: 1 + SLOTS * (l + 1)]
+            for n, a, b in steps:
+                w = (m[:, a] > 0) & (m[:, b] > 0)
+                if w.any():
+                    sub[n].append(np.median(m[w, b] - m[w, a]) / 100.0)
+    print()
+    print("| step inside a phase (one workgroup) | median us |")
+    print("|---|---|")
+    for n, _, _ in steps:
+        if sub[n]:
+            print(f"| {n} | {np.median(sub[n]):.2f} |")
 
 
 if __name__ == "__main__":
