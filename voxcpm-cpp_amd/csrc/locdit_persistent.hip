@@ -116,6 +116,19 @@ constexpr int kTraceSlots = 24;
 #define VXM_LTS(k) do { } while (0)
 #endif
 
+// Block l's table entry through the constant address space and a read-first-lane
+// address, so its fields are scalar (lgkmcnt) loads: a vector load here would make
+// wave 7 wait (vmcnt, which retires in order) for every weight prefetch it has in
+// flight before it could use the pointers.
+typedef const __attribute__((address_space(4))) vxm_lblock *vxm_lbtab;
+__device__ __forceinline__ vxm_lblock block_at(const vxm_lparams &p, int l) {
+    const uint64_t a = (uint64_t)(uintptr_t)(p.blocks + l);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    const vxm_lbtab t = (vxm_lbtab)(uintptr_t)(((uint64_t)hi << 32) | lo);
+    return vxm_lblock{t->qkv_q, t->o_q, t->gu_q, t->dn_q, t->qkv_d, t->o_d, t->gu_d, t->dn_d, t->g_in, t->g_post};
+}
+
 __device__ __forceinline__ uint32_t make_tag(uint32_t ep, int L, int l, int ph) {
     return ((ep * (uint32_t)(8 * L) + (uint32_t)(8 * l + ph)) << 1) | 1u;   // odd: never a zeroed word
 }
@@ -462,7 +475,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
         for (int c = 2; c < 4; c++) dma_tile(LS::RA, c, b.gu_q, kH, 64 * ugu + 16 * c, 0, 32, dlane);
     };
     if (DMA) {
-        const vxm_lblock b0 = p.blocks[0];
+        const vxm_lblock b0 = block_at(p, 0);
         if (is_qkv && !is_gu) {
             issue_qkv(b0);
             issue_o(b0);
@@ -485,7 +498,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
     };
 
     for (int l = 0; l < L; l++) {
-        const vxm_lblock blk = p.blocks[l];
+        const vxm_lblock blk = block_at(p, l);
         const bool last = l == L - 1;
         VXM_LTS(0);
         // ---- N1: x += down partials of block l - 1; RMSNorm(g_in) -> Q8_0 ----
@@ -611,25 +624,26 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             if (*bail) return;
             VXM_LTS(21);
             VXM_LTS(5);
-            // scores s_ij = (k_j . q_i) * scale: eight lanes per score, each a run of HD / 8
-            // dims in order, the eight partial sums added pairwise across the lanes
+            // scores s_ij = (k_j . q_i) * scale: LPS lanes per score (8 at HD = 128, where the
+            // serial 128-term sum was the longer wait; 1 at HD = 64), each a run of HD / LPS dims
+            // in order, the partial sums added pairwise across the lanes
+            constexpr int LPS = HD == 128 ? 8 : 1, RUN = HD / 4 / LPS;
             const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
-            for (int idx = tid; idx < nq * S * 8; idx += kThreads) {
-                const int ij = idx >> 3, part = idx & 7, i = ij / S, j = ij % S;
-                const float4 *kr = (const float4 *)(Kf + j * HP) + part * (HD / 32),
-                             *qr = (const float4 *)(Q + i * HP) + part * (HD / 32);
+            for (int idx = tid; idx < nq * S * LPS; idx += kThreads) {
+                const int ij = idx / LPS, part = idx % LPS, i = ij / S, j = ij % S;
+                const float4 *kr = (const float4 *)(Kf + j * HP) + part * RUN,
+                             *qr = (const float4 *)(Q + i * HP) + part * RUN;
                 float sc = 0.0f;
-#pragma unroll
-                for (int d4 = 0; d4 < HD / 32; d4++) {
+#pragma unroll 8
+                for (int d4 = 0; d4 < RUN; d4++) {
                     const float4 a = kr[d4], b = qr[d4];
                     sc += a.x * b.x;
                     sc += a.y * b.y;
                     sc += a.z * b.z;
                     sc += a.w * b.w;
                 }
-                sc += __shfl_xor(sc, 1, 64);
-                sc += __shfl_xor(sc, 2, 64);
-                sc += __shfl_xor(sc, 4, 64);
+#pragma unroll
+                for (int o = 1; o < LPS; o <<= 1) sc += __shfl_xor(sc, o, 64);
                 if (part == 0) P[i * SP + j] = sc * scale;
             }
             lds_barrier();
@@ -707,7 +721,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             } else {
                 if (!is_qkv) issue_d(blk);
                 if (is_gu) issue_gu_a(blk);
-                else if (is_qkv && !last) issue_qkv(p.blocks[l + 1]);
+                else if (is_qkv && !last) issue_qkv(block_at(p, l + 1));
                 if (is_gu && is_qkv)
                     vm_wait<63>();
                 else if (is_gu)
@@ -765,7 +779,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                 if (last) {
                     vm_wait<0>();
                 } else {
-                    issue_o(p.blocks[l + 1]);
+                    issue_o(block_at(p, l + 1));
                     vm_wait<nO>();
                 }
             }
@@ -832,8 +846,8 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                 poll_stage<(kMaxM * 9 * 16 / 2 + kPollThreads - 1) / kPollThreads>(
                     p, chan_rsrc(p.pp, LS::WP * 8), kPPitch, kF / 4, 16 * ds, 16, M, tg, lds, LS::ST, LS::ST_SC, bail);
             } else {
-                if (!last && !is_gu) issue_o(p.blocks[l + 1]);
-                if (!last && is_gu && is_qkv) issue_qkv(p.blocks[l + 1]);
+                if (!last && !is_gu) issue_o(block_at(p, l + 1));
+                if (!last && is_gu && is_qkv) issue_qkv(block_at(p, l + 1));
                 if (is_gu)
                     vm_wait<63>();
                 else if (last)
