@@ -381,9 +381,66 @@ __device__ __forceinline__ void q8_scale(float amax, int variant, float &d, floa
     else id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
 }
 
-__device__ __forceinline__ double wg_sum_d(double v, uint8_t *lds, int misc) {
+// Cross-lane steps on DPP (a few cycles) instead of ds_bpermute (an LDS round trip
+// each): quad_perm [1,0,3,2] and [2,3,0,1] (xor 1, xor 2), row_half_mirror (lane i of
+// 8 <- 7 - i) and row_mirror (lane i of 16 <- 15 - i).  After xor 1 and xor 2 a quad
+// is reduced, after the half mirror 8 lanes, after the mirror a row of 16, and every
+// lane holds the same bits (each step adds the same two values in either order).
+constexpr int kDppX1 = 0xB1, kDppX2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) { return __uint_as_float(dpp_u<CTRL>(__float_as_uint(v))); }
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint64_t r = (uint64_t)dpp_u<CTRL>((uint32_t)u) | ((uint64_t)dpp_u<CTRL>((uint32_t)(u >> 32)) << 32);
+    return __longlong_as_double((long long)r);
+}
+__device__ __forceinline__ float max4(float v) {
+    v = fmaxf(v, dpp_f<kDppX1>(v));
+    return fmaxf(v, dpp_f<kDppX2>(v));
+}
+__device__ __forceinline__ float max16(float v) {
+    v = max4(v);
+    v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    return fmaxf(v, dpp_f<kDppMirror>(v));
+}
+__device__ __forceinline__ float sum8(float v) {
+    v = v + dpp_f<kDppX1>(v);
+    v = v + dpp_f<kDppX2>(v);
+    return v + dpp_f<kDppHalfMirror>(v);
+}
+__device__ __forceinline__ double sum16_d(double v) {
+    v = v + dpp_d<kDppX1>(v);
+    v = v + dpp_d<kDppX2>(v);
+    v = v + dpp_d<kDppHalfMirror>(v);
+    return v + dpp_d<kDppMirror>(v);
+}
+// the four rows of a wave (all lanes active): row values read back as scalars
+__device__ __forceinline__ double rows_sum_d(double v) {
+    const long long b = __double_as_longlong(v);
+    double t = 0.0;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    for (int r = 0; r < 4; r++) {
+        const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)b, 16 * r);
+        const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)b >> 32), 16 * r);
+        t += __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+    }
+    return t;
+}
+__device__ __forceinline__ float rows_max(float v) {
+    float m = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+#pragma unroll
+    for (int r = 1; r < 4; r++) m = fmaxf(m, __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16 * r)));
+    return m;
+}
+
+__device__ __forceinline__ double wg_sum_d(double v, uint8_t *lds, int misc) {
+    v = rows_sum_d(sum16_d(v));   // the wave's sum (exact: sums of squares of BF16 values)
     double *r = (double *)(lds + misc);
     lds_barrier();
     if ((threadIdx.x & 63) == 0) r[threadIdx.x >> 6] = v;
@@ -419,12 +476,11 @@ __device__ __forceinline__ void row_update(uint8_t *lds, int st, int xr, int gn,
     const float y0 = bf16r(bf16r(xv[0] * sc) * g.x), y1 = bf16r(bf16r(xv[1] * sc) * g.y);
     // Q8_0: 16 threads per 32-value block
     float amax = fmaxf(fabsf(y0), fabsf(y1));
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    amax = max16(amax);
     float d, id;
     q8_scale(amax, variant, d, id);
     const uint32_t h = q8_byte(y0, id, variant) | (q8_byte(y1, id, variant) << 8);
-    const uint32_t ho = __shfl_xor(h, 1, 64);
+    const uint32_t ho = dpp_u<kDppX1>(h);
     if ((t & 1) == 0) put_word(chan_row + t / 2, h | (ho << 16), tag);
     if ((t & 15) == 0) put_word(chan_row + kH / 4 + t / 16, __float_as_uint(vxm_h2f(vxm_f2h(d))), tag);
 }
@@ -642,8 +698,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                     sc += a.z * b.z;
                     sc += a.w * b.w;
                 }
-#pragma unroll
-                for (int o = 1; o < LPS; o <<= 1) sc += __shfl_xor(sc, o, 64);
+                if (LPS == 8) sc = sum8(sc);
                 if (part == 0) P[i * SP + j] = sc * scale;
             }
             lds_barrier();
@@ -653,14 +708,11 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                 const int i = wave, j = lane;
                 if (i < nq) {
                     const float sj = j < S ? P[i * SP + j] : -INFINITY;
-                    float m = sj;
-#pragma unroll
-                    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+                    const float m = rows_max(max16(sj));
                     const float e = j < S ? expf(sj - m) : 0.0f;
                     if (j < S) P[i * SP + j] = e;
-                    double sum = (double)e;
-#pragma unroll
-                    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+                    // exact: at most 64 exponentials of one row, all in double
+                    const double sum = rows_sum_d(sum16_d((double)e));
                     if (j == 0) {
                         mx[i] = m;
                         inv[i] = (float)(1.0 / sum);
@@ -691,8 +743,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                     o[e] = O[i * HD + 8 * c + e];
                     amax = fmaxf(amax, fabsf(o[e]));
                 }
-                amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-                amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+                amax = max4(amax);
                 float d, id;
                 q8_scale(amax, p.variant, d, id);
                 uint32_t lo = 0, hi = 0;
@@ -819,8 +870,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                     o[e] = ps[m * 33 + 8 * part + e];
                     amax = fmaxf(amax, fabsf(o[e]));
                 }
-                amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-                amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+                amax = max4(amax);
                 float d, id;
                 q8_scale(amax, p.variant, d, id);
                 uint32_t lo = 0, hi = 0;
