@@ -347,24 +347,29 @@ __device__ __forceinline__ void mfma_run(const uint8_t *lds, int wt, int wsc, in
 
 // After mfma_run in every wave: the partial sums go to LDS (the stage, no longer
 // read) and out(ct, t, lane) = sum over kk of wave (ct + ncol * kk)'s partial, in kk order.
+// (The four sums of a lane are one 16-byte LDS word: one write and one read per row tile.)
 template <int MT>
 __device__ __forceinline__ void red_store(uint8_t *lds, int st, int wave, int lane, const float (&acc)[MT][4]) {
-    float *red = (float *)(lds + st);
+    float4 *red = (float4 *)(lds + st);
 #pragma unroll
-    for (int t = 0; t < MT; t++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) red[((wave * MT + t) * 4 + v) * 64 + lane] = acc[t][v];
+    for (int t = 0; t < MT; t++) red[(wave * MT + t) * 64 + lane] = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
 }
 
 template <int MT>
 __device__ __forceinline__ void red_sum(const uint8_t *lds, int st, int ncol, int ct, int t, int lane, float (&o)[4]) {
-    const float *red = (const float *)(lds + st);
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-        float s = red[((ct * MT + t) * 4 + v) * 64 + lane];
-        for (int kk = 1; kk < kWaves / ncol; kk++) s = s + red[(((ct + ncol * kk) * MT + t) * 4 + v) * 64 + lane];
-        o[v] = s;
+    const float4 *red = (const float4 *)(lds + st);
+    float4 s = red[(ct * MT + t) * 64 + lane];
+    for (int kk = 1; kk < kWaves / ncol; kk++) {
+        const float4 a = red[((ct + ncol * kk) * MT + t) * 64 + lane];
+        s.x = s.x + a.x;
+        s.y = s.y + a.y;
+        s.z = s.z + a.z;
+        s.w = s.w + a.w;
     }
+    o[0] = s.x;
+    o[1] = s.y;
+    o[2] = s.z;
+    o[3] = s.w;
 }
 
 // Q8_0 rule of quant_block_4lanes for one value: x86 = id 127/amax, round half even;
