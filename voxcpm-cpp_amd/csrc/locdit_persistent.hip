@@ -8,9 +8,11 @@
 // every one of them latency-bound (the weights of a whole evaluation stream in
 // 27 us at 8 TB/s).  Here 256 workgroups, one per CU, stay resident for all
 // blocks and hand each phase's output to the next phase's workgroups through
-// tagged 64-bit words (32-bit tag, 32-bit payload, written and read with
-// agent-scope relaxed atomics: a word is valid exactly when its tag is the
-// expected one, so no fences or grid barriers are needed).  Per block:
+// tagged 64-bit words (32-bit tag, 32-bit payload; written with agent-scope
+// relaxed atomic stores, read in pairs with 16-byte loads that bypass the
+// non-coherent caches as agent-scope atomic loads do): a word is valid exactly
+// when its tag is the expected one, so no fences or grid barriers are needed.
+// Per block:
 //
 //   N1  row owners (one workgroup per row): x += the down projection's K-split
 //       partials of the previous block; RMSNorm(g_in) -> Q8_0 rows
@@ -25,8 +27,10 @@
 //   D   (32-column tile, eighth of K) units: partial products
 //
 // The rounding steps are those of the launch-based kernels (k_rmsnorm,
-// k_attention_local, k_swiglu_quant); only the fp32 summation order of the
-// matrix products differs (blocks of K per wave, waves added in order).
+// k_attention_local, k_swiglu_quant); the fp32 summation order of the matrix
+// products differs (blocks of K per wave, waves added in order), the attention
+// scores at head dim 128 add eight runs of 16 dims, and P.V sums the keys in
+// order (the oracle's attend_one).
 //
 // Every workgroup knows its weight tiles for all phases in advance, so wave 7
 // streams them into LDS with global_load_lds_dwordx4 one or more phases ahead
