@@ -133,6 +133,9 @@ __device__ __forceinline__ vxm_lblock block_at(const vxm_lparams &p, int l) {
     return vxm_lblock{t->qkv_q, t->o_q, t->gu_q, t->dn_q, t->qkv_d, t->o_d, t->gu_d, t->dn_d, t->g_in, t->g_post};
 }
 
+// The tag of (launch epoch, block, phase).  Consecutive writes of a word always carry
+// different tags; a word left from an older launch (rows past a later launch's M) could
+// only match again after 2^31 / (8 L) launches, 22 million at 12 blocks.
 __device__ __forceinline__ uint32_t make_tag(uint32_t ep, int L, int l, int ph) {
     return ((ep * (uint32_t)(8 * L) + (uint32_t)(8 * l + ph)) << 1) | 1u;   // odd: never a zeroed word
 }
@@ -1148,7 +1151,9 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
     // All 256 workgroups wait on each other's words, so all must be resident: one per CU
     // (the LDS layout takes more than half of a CU's).  Every wait is bounded (kSpin
     // rounds, then the error word), so other work on the device can only turn a launch
-    // into an error, never a hang.  Launches on one stream run one after another.
+    // into an error, never a hang.  Launches on one stream run one after another; two
+    // models evaluating on different streams of one device at once could interleave their
+    // workgroups and end in that error (vxm_locdit_check / vxm_locenc_check report it).
 #ifdef VXM_PERSISTENT_TRACE
     // profiling build: timestamps of every eager launch into
     // $VXM_TRACE_DIR/ltrace_L<blocks>_M<rows>_<n>.bin (launches recorded into a graph run untraced)
