@@ -518,8 +518,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
     // (an issue costs it ~50 ns per 1 KiB instruction when every CU streams at once).
     // With Q = a QKV role, G = a gate/up role:
     //   start:            O(0) and, with Q, QKV(0) (QKV first without G)
-    //   QKV(l) wait (Q):  D(l)
-    //   O(l) wait:        D(l) without Q; gate/up rows 0-31 (l) with G; QKV(l+1) with Q only
+    //   O(l) wait:        D(l); gate/up rows 0-31 (l) with G; QKV(l+1) with Q only
     //   GU(l) wait (G):   gate/up rows 32-63 (l), O(l+1)
     //   D(l) wait:        O(l+1) without G; QKV(l+1) with Q and G
     // The waits before each phase's products count the loads issued after its own.
@@ -602,8 +601,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                 poll_stage<(kMaxM * kXPitch / 2 + kPollThreads - 1) / kPollThreads>(
                     p, chan_rsrc(p.x1, LS::WX * 8), kXPitch, kH / 4, 0, 32, M, tg, lds, LS::ST, LS::ST_SC, bail);
             } else {
-                issue_d(blk);
-                vm_wait<nD>();
+                vm_wait<0>();
             }
             lds_barrier();
             if (*bail) return;
@@ -782,7 +780,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                     p, chan_rsrc(p.att, LS::WA * 8), LS::APitch, LS::QD / 4, LS::BO * os, LS::BO, M, tg, lds, LS::ST,
                     LS::ST_SC, bail);
             } else {
-                if (!is_qkv) issue_d(blk);
+                issue_d(blk);
                 if (is_gu) issue_gu_a(blk);
                 else if (is_qkv && !last) issue_qkv(block_at(p, l + 1));
                 if (is_gu && is_qkv)
