@@ -81,6 +81,8 @@ struct LShape {
     static constexpr int MISC = GN + kH * 4;                  // 8 doubles of reductions, then flags
     static constexpr int BYTES = MISC + 128;
     static_assert(16 * BO * 2 <= 1024, "O scales");
+    static_assert(kMP * 33 * 4 <= MISC - XR, "gate/up outputs in the row-owner area");
+    static_assert(kWaves * 2 * kMT * 64 * 16 <= ST_SC - ST, "gate/up partial sums in the stage");
     static_assert(BYTES <= 160 * 1024, "LDS");
     // attention scratch inside the stage: k (rotated, f16-rounded) [S][HD+4], v [S][HD],
     // q [kRB][HD+4], out [kRB][HD], p [kRB][S+1], row max and 1/sum [kRB] each
@@ -349,6 +351,45 @@ __device__ __forceinline__ void mfma_run(const uint8_t *lds, int wt, int wsc, in
 #pragma unroll
             for (int v = 0; v < 4; v++) acc[t][v] = __builtin_fmaf((float)cc[v], dw[v] * dx[t], acc[t][v]);
         }
+    }
+}
+
+// The same for the two tiles c0, c0 + 1 at once: each block's activation pieces and
+// scales are read once for both (gate/up: 5 instead of 8 LDS operand reads per block
+// pair, the stage being read by every wave).
+template <int MT, int NB, int G>
+__device__ __forceinline__ void mfma_run2(const uint8_t *lds, int wt, int wsc, int nbw, int c0, int st, int st_sc,
+                                          int nbs, int b0, int lane, float (&acc)[2][MT][4]) {
+    static_assert(NB % G == 0, "block groups");
+    const int q = lane >> 4, r = lane & 15, sl = slot_of(q, r);
+#pragma unroll 1
+    for (int i0 = 0; i0 < NB; i0 += G)
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+        const int b = b0 + i0 + i;
+        long a[2], bx[MT];
+        float dx[MT], dw[2][4];
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) {
+            a[cc] = *(const long *)(lds + wt + ((c0 + cc) * (nbw / 2) + (b >> 1)) * 1024 + (b & 1) * 512 + sl);
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                dw[cc][v] = vxm_h2f(*(const uint16_t *)(lds + wsc + ((16 * (c0 + cc) + 4 * q + v) * nbw + b) * 2));
+        }
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            bx[t] = *(const long *)(lds + st + (t * nbs + b) * 512 + sl);
+            dx[t] = *(const float *)(lds + st_sc + (b * kMP + 16 * t + r) * 4);
+        }
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++)
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[cc], bx[t], v4i{}, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    acc[cc][t][v] = __builtin_fmaf((float)ci[v], dw[cc][v] * dx[t], acc[cc][t][v]);
+            }
     }
 }
 
@@ -848,18 +889,54 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             if (*bail) return;
             VXM_LTS(11);
             zero_acc();
-            const int ct = wave & 3, kh = wave >> 2;
-            mfma_run<MT, 16, 8>(lds, LS::RA, LS::RA_SC, 32, ct, LS::ST, LS::ST_SC, 32, 16 * kh, lane, acc);
+            // wave w: tiles 2 (w & 1) and 2 (w & 1) + 1 over the K quarter w >> 1
+            const int ch = wave & 1, kq = wave >> 1;
+            float acc2[2][MT][4];
+#pragma unroll
+            for (int cc = 0; cc < 2; cc++)
+#pragma unroll
+                for (int t = 0; t < MT; t++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) acc2[cc][t][v] = 0.0f;
+            mfma_run2<MT, 8, 4>(lds, LS::RA, LS::RA_SC, 32, 2 * ch, LS::ST, LS::ST_SC, 32, 8 * kq, lane, acc2);
             lds_barrier();
             VXM_LTS(18);
-            red_store<MT>(lds, LS::ST, wave, lane, acc);
+            {
+                float4 *red = (float4 *)(lds + LS::ST);   // [wave][2][MT][64]: 48 KiB at MT = 3
+#pragma unroll
+                for (int cc = 0; cc < 2; cc++)
+#pragma unroll
+                    for (int t = 0; t < MT; t++)
+                        red[((wave * 2 + cc) * MT + t) * 64 + lane] =
+                            make_float4(acc2[cc][t][0], acc2[cc][t][1], acc2[cc][t][2], acc2[cc][t][3]);
+            }
             lds_barrier();
             VXM_LTS(19);
-            float *ps = (float *)(lds + LS::ST + kWaves * kMT * 4 * 64 * 4);   // [kMP][33]
+            // the SwiGLU outputs go to the row-owner area (x and gain), unused here: a gate/up
+            // workgroup (index >= 128) never owns a row (M <= 48)
+            static_assert(kMaxM <= 128, "gate/up workgroups own no row");
+            float *ps = (float *)(lds + LS::XR);   // [kMP][33]
             for (int idx = tid; idx < 4 * MT * 64; idx += kThreads) {
                 const int ct2 = idx / (MT * 64), t = (idx / 64) % MT;
                 float o[4];
-                red_sum<MT>(lds, LS::ST, 4, ct2, t, lane, o);
+                {
+                    // the four K quarters in order
+                    const float4 *red = (const float4 *)(lds + LS::ST);
+                    const int h2 = ct2 >> 1, cc = ct2 & 1;
+                    float4 s = red[(((0 * 2 + h2) * 2 + cc) * MT + t) * 64 + lane];
+#pragma unroll
+                    for (int k = 1; k < 4; k++) {
+                        const float4 u = red[(((2 * k + h2) * 2 + cc) * MT + t) * 64 + lane];
+                        s.x = s.x + u.x;
+                        s.y = s.y + u.y;
+                        s.z = s.z + u.z;
+                        s.w = s.w + u.w;
+                    }
+                    o[0] = s.x;
+                    o[1] = s.y;
+                    o[2] = s.z;
+                    o[3] = s.w;
+                }
                 const int m = 16 * t + r16;
 #pragma unroll
                 for (int e = 0; e < 2; e++) {
