@@ -21,6 +21,37 @@ __device__ __forceinline__ double block_sum_f64(double v, double *sh) {
     return t;
 }
 
+// The same for exact sums (squares of BF16 values: any order gives the same double):
+// each row of 16 lanes on DPP (xor 1, xor 2, half mirror, mirror), the wave's four
+// rows read back as scalars.  Every lane of the block must be active.
+__device__ __forceinline__ double block_sum_exact_f64(double v, double *sh) {
+    auto dpp = [](double x, auto ctrl) {
+        const long long b = __double_as_longlong(x);
+        const int lo = __builtin_amdgcn_update_dpp(0, (int)b, decltype(ctrl)::value, 0xF, 0xF, false);
+        const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), decltype(ctrl)::value, 0xF, 0xF, false);
+        return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+    };
+    v = v + dpp(v, std::integral_constant<int, 0xB1>{});
+    v = v + dpp(v, std::integral_constant<int, 0x4E>{});
+    v = v + dpp(v, std::integral_constant<int, 0x141>{});
+    v = v + dpp(v, std::integral_constant<int, 0x140>{});
+    const long long b = __double_as_longlong(v);
+    double w = 0.0;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)b, 16 * r);
+        const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(b >> 32), 16 * r);
+        w += __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+    }
+    const int wv = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sh[wv] = w;
+    __syncthreads();
+    double t = 0.0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += sh[i];
+    return t;
+}
+
 __device__ __forceinline__ float block_max_f32(float v, float *sh) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
@@ -105,7 +136,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *__restrict__ h, const vx
             for (int i = 0; i < 8; i++) ss += (double)(v[c][i] * v[c][i]);
         }
     }
-    const double tot = block_sum_f64(ss, shd);
+    const double tot = block_sum_exact_f64(ss, shd);
     if (!y && !xq) return;
     const float mean = (float)(tot / (double)n);
     const float sc = __fdiv_rn(1.0f, __fsqrt_rn(mean + eps));

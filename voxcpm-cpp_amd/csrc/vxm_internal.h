@@ -112,6 +112,14 @@ __device__ __forceinline__ float vxm_swiglu(float g, float u) {
     return vxm_bf16(s * vxm_bf16(u));
 }
 
+// Maximum over an aligned quad of lanes through DPP quad permutations (xor 1, then
+// xor 2): every lane of the quad gets it, without an LDS round trip per step.  All four
+// lanes must be active, as for a shuffle.
+__device__ __forceinline__ float vxm_quad_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+}
+
 // Q8_0 of one 32-value block held 8 per lane by four consecutive lanes (lane & 3
 // = part) with the x86 rule (id = 127/amax, round half even) or the _ref rule;
 // the lane with write_d set stores d.  write = false: compute (every lane of the
@@ -121,8 +129,7 @@ __device__ __forceinline__ void quant_block_4lanes(const float v[8], int variant
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = vxm_quad_max(amax);
     const float d = __fdiv_rn(amax, 127.0f);
     float id;
     if (variant == VXM_QUANT_X86) id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
