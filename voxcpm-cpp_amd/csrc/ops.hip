@@ -785,15 +785,44 @@ __global__ __launch_bounds__(256) void k_attention_local(const vxm_parts qkv, in
     {
         const int i = tid >> 6, j = tid & 63;
         if (i < nq) {
+            // the wave reductions on DPP within rows of 16 lanes, the four rows read back
+            // as scalars (no LDS round trip per step)
             const float sj = j < S ? P[i * SP + j] : -INFINITY;
             float m = sj;
+            m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
+            m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
+            m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x141, 0xF, 0xF, false)));
+            m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x140, 0xF, 0xF, false)));
+            {
+                float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
 #pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+                for (int r = 1; r < 4; r++) t = fmaxf(t, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16 * r)));
+                m = t;
+            }
             const float e = j < S ? expf(sj - m) : 0.0f;
             if (j < S) P[i * SP + j] = e;
             double sum = (double)e;
+            auto dpp_d = [](double x, auto ctrl) {
+                const long long b = __double_as_longlong(x);
+                const int lo = __builtin_amdgcn_update_dpp(0, (int)b, decltype(ctrl)::value, 0xF, 0xF, false);
+                const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), decltype(ctrl)::value, 0xF, 0xF, false);
+                return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+            };
+            sum = sum + dpp_d(sum, std::integral_constant<int, 0xB1>{});
+            sum = sum + dpp_d(sum, std::integral_constant<int, 0x4E>{});
+            sum = sum + dpp_d(sum, std::integral_constant<int, 0x141>{});
+            sum = sum + dpp_d(sum, std::integral_constant<int, 0x140>{});
+            {
+                const long long b = __double_as_longlong(sum);
+                double t = 0.0;
 #pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+                for (int r = 0; r < 4; r++) {
+                    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)b, 16 * r);
+                    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(b >> 32), 16 * r);
+                    t += __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+                }
+                sum = t;
+            }
             if (j == 0) {
                 mx[i] = m;
                 inv[i] = (float)(1.0 / sum);
