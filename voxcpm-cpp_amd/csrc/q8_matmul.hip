@@ -47,9 +47,8 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live) v = *(const float4 *)(x + blk * 32 + sub * 4);
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    amax = vxm_quad_max(amax);   // xor 1, xor 2 on DPP; then the other quad of the 8
+    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0x141, 0xF, 0xF, false)));
     if (!live) return;
     const float d = __fdiv_rn(amax, 127.0f);
     float id;
@@ -1342,8 +1341,7 @@ __global__ __launch_bounds__(64 * kSmallRG * KG) void k_gemm_q8_0_small(const in
                 pv[e] = ps[row][8 * part + e];
                 amax = fmaxf(amax, fabsf(pv[e]));
             }
-            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-            amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+            amax = vxm_quad_max(amax);
             const float d = __fdiv_rn(amax, 127.0f);
             float id;
             if (variant == VXM_QUANT_X86) id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
