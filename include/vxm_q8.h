@@ -69,6 +69,21 @@ const char *vxm_last_error(const vxm_ctx *ctx);
 int         vxm_set_quant_variant(vxm_ctx *ctx, int variant);
 int         vxm_set_path(vxm_ctx *ctx, int path);
 
+/* HIP graph capture of the context's stream: no counterpart in the reference
+ * (its host re-issues every graph each step, src/ggml_backend.c:557-599).  For
+ * callers that replay one fixed sequence of vxm_* calls with new contents in
+ * the same device buffers (a decode step, a CFM step).  Between begin and end
+ * the calls on the context are recorded, not run; vxm_graph_launch replays
+ * the recording on the context's stream.  Run the sequence once eagerly
+ * first: a call that would have to grow a scratch buffer (and so allocate and
+ * synchronise) fails under capture with VXM_ERR_INVALID_ARG.  K-split tags
+ * live in device memory, so every replay of a split product is exact. */
+typedef struct vxm_graph vxm_graph;
+int vxm_capture_begin(vxm_ctx *ctx);
+int vxm_capture_end(vxm_ctx *ctx, vxm_graph **out);
+int vxm_graph_launch(vxm_ctx *ctx, const vxm_graph *g);
+int vxm_graph_free(vxm_graph *g);
+
 /* Device memory and host-boundary copies (ggml_backend_tensor_set/get,
  * src/ggml_backend.c:356-380,422-457).  The copies return when complete. */
 int vxm_malloc(vxm_ctx *ctx, size_t bytes, void **out_dev);
@@ -126,9 +141,11 @@ int64_t vxm_stream_read_sink_words(int32_t n, const int64_t *bytes);
  * and the K-split partials live in a fixed device array of
  * vxm_noalloc_scratch_bytes() per device (48 MiB 64 KiB), held until the
  * process ends.  A product whose quantized activation exceeds 32 MiB, or whose
- * K splits exceed their part of the array, is rejected with
- * VXM_ERR_INVALID_ARG.  All calls on one device share the array: calls that
- * overlap on a device (other streams or threads) race. */
+ * K-split plan needs more than the array's 16 MiB of partial words (for
+ * example 2048 x 6144 at M = 520, which vxm_mul_mat_q8_0 splits 3 ways), is
+ * rejected with VXM_ERR_INVALID_ARG, never run on another plan.  All
+ * calls on one device share the array: calls that overlap on a device (other
+ * streams or threads) race. */
 int vxm_mul_mat_q8_0_noalloc(vxm_ctx *ctx, const vxm_weight *w, const float *x_dev, int64_t M,
                              float *y_dev);
 size_t vxm_noalloc_scratch_bytes(void);
@@ -203,8 +220,9 @@ int vxm_minicpm4_forward(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x_dev, int64_
 
 /* Decode (n_tokens == 1) strategy of vxm_minicpm4_forward:
  * VXM_DECODE_AUTO picks the fastest available, VXM_DECODE_KERNELS runs one
- * kernel per op, VXM_DECODE_PERSISTENT runs the whole stack in one
- * cooperative launch.  No reference counterpart (ggml has one graph path). */
+ * kernel per op, VXM_DECODE_PERSISTENT runs the whole stack in one launch
+ * (all 256 workgroups resident).  No reference counterpart (ggml has one
+ * graph path). */
 #define VXM_DECODE_AUTO 0
 #define VXM_DECODE_KERNELS 1
 #define VXM_DECODE_PERSISTENT 2
@@ -213,6 +231,22 @@ int vxm_minicpm4_set_decode_mode(vxm_minicpm4 *m, int mode);
  * persistent decode (a workgroup that timed out waiting for its inputs) as
  * VXM_ERR_BACKEND, then clears it.  Decode calls themselves never block. */
 int vxm_minicpm4_check(vxm_minicpm4 *m);
+/* Debug read-back of every layer, as the reference's GPU path reads back every
+ * graph node (src/ggml_backend.c:422-457) and VCPM_DEBUG_SHAPES dumps named
+ * tensors (src/debug_dump.h:18-43).  With a non-null dump_dev, each later
+ * vxm_minicpm4_forward writes the input of every layer l (after the previous
+ * layer's residual) to dump_dev + l * n_tokens * hidden and the last layer's
+ * output before the final norm to dump_dev + n_layers * n_tokens * hidden:
+ * (n_layers + 1) * n_tokens * hidden floats, on every decode strategy (the
+ * single launch writes them from workgroup 0).  Null turns it off. */
+int vxm_minicpm4_set_layer_dump(vxm_minicpm4 *m, float *dump_dev);
+/* Test hooks of the single-launch decode, no reference counterpart.  Its words
+ * carry a 20-bit launch epoch kept in device memory (advanced by each launch,
+ * so HIP graph replays tag anew); when it wraps, the launch resets every
+ * exchange word.  set: the epoch of the next launch (1 .. 2^20 - 1; needs one
+ * earlier single-launch decode on the model).  Both synchronise. */
+int vxm_minicpm4_set_decode_epoch(vxm_minicpm4 *m, uint32_t epoch);
+int vxm_minicpm4_decode_epoch(vxm_minicpm4 *m, uint32_t *epoch);
 
 /* ---- LocDiT and the CFM solver -------------------------------------------
  * Mirrors vcpm_locdit_config (src/locdit.h:26-34) plus the projection widths. */
@@ -289,8 +323,18 @@ int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev, int32_t P,
 int vxm_locdit_set_block_mode(vxm_locdit *m, int mode);
 /* Synchronises the context's stream and reports a device-side failure of the
  * persistent block kernel (a workgroup that timed out waiting for its inputs)
- * as VXM_ERR_BACKEND, then clears it. */
+ * as VXM_ERR_BACKEND, then clears it.  Forward and solve calls are
+ * asynchronous and cannot report such a failure themselves: call this after
+ * the results of a solve are read.  A failed launch does not affect later
+ * ones. */
 int vxm_locdit_check(vxm_locdit *m);
+/* Debug read-back of every block (as vxm_minicpm4_set_layer_dump): with a
+ * non-null dump_dev each later evaluation writes the rows of both CFG branches
+ * entering every block l to dump_dev + l * rows * hidden (rows = n_seg * (3 +
+ * Pc + P)) and the last block's output, residual added, at l = n_layers: (n_layers
+ * + 1) * rows * hidden floats.  A solve overwrites it at every step (the last
+ * evaluation stays). */
+int vxm_locdit_set_block_dump(vxm_locdit *m, float *dump_dev);
 
 /* ---- LocEnc and the per-token LM update ----------------------------------
  * Mirrors vcpm_locenc_config (src/locenc.h:49-60); max_seq_len and
@@ -337,6 +381,8 @@ int vxm_locenc_forward(vxm_locenc *m, const float *x_dev, int32_t P, float *out_
  * counterpart. */
 int vxm_locenc_set_block_mode(vxm_locenc *m, int mode);
 int vxm_locenc_check(vxm_locenc *m);
+/* As vxm_locdit_set_block_dump for the P + 1 rows of the encoder. */
+int vxm_locenc_set_block_dump(vxm_locenc *m, float *dump_dev);
 
 /* The scalar quantizer core of the FSQ layer, vcpm_fsq_quantize
  * (src/fsq.c:16-29): y = round(tanh(x) * s) * (1/s) elementwise, round half

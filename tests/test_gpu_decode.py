@@ -391,3 +391,119 @@ def test_persistent_decode_two_streams_interleaved(vxm_ctx, orc):
         teardown(ms, kvs)
     finally:
         ctx2.close()
+
+
+def test_persistent_decode_epoch_wrap(vxm_ctx, orc):
+    """The single-launch decode tags its exchanged words with a 20-bit epoch kept in
+    device memory.  Across the wrap (2^20 - 1 -> 1) the launch that wraps resets every
+    exchange word, so a word from before the wrap cannot carry a live tag again.  The
+    hazard is a key-chunk partial: chunk slots 2 and 3 of every head are written only
+    by launches that split the keys 4 ways.  Here the first launch (epoch 1) splits
+    1001 keys 4 ways; the launches just below the wrap split 501 keys 2 ways (slots 2
+    and 3 keep their epoch-1 words); the launch after the wrap runs with epoch 1 again
+    on 1001 keys and a new token.  Every output is held to the oracle."""
+    import vxm
+
+    L, cap = 2, 2048
+    s, rng, c, lws, fn, models, kvs, kcs, vcs = _setup(orc, vxm, vxm_ctx, "tslm", L, cap, 1000, 606)
+    m, kv = models[2], kvs[2]
+    oc = orc_cfg(orc, c)
+    ol = [to_orc(orc, l) for l in lws]
+    base_k = [k.copy() for k in kcs]
+    base_v = [v.copy() for v in vcs]
+    shp = (s["nkv"], cap, s["hd"])
+
+    def decode(pos, what):
+        # the same prior cache every time (rows up to pos from the host)
+        for l in range(L):
+            kv.upload(l, base_k[l].reshape(shp), base_v[l].reshape(shp))
+        x = rng.normal(0, 1, (1, s["H"])).astype(np.float32)
+        xd = _dev(x)
+        print(f"epoch wrap: {what} at pos {pos}", flush=True)
+        m.forward(kv, xd, pos)
+        vxm_ctx.sync()
+        m.check()
+        ref = orc.minicpm4_forward(oc, ol, fn, x, [k.copy() for k in base_k], [v.copy() for v in base_v], cap, pos)
+        assert_stack_close(xd.cpu().numpy(), ref, what=what)
+
+    try:
+        decode(1000, "epoch 1, 4 key chunks")
+        assert m.decode_epoch() == 2
+        m.set_decode_epoch(0xFFFFE)
+        decode(500, "epoch 0xffffe, 2 key chunks")
+        decode(500, "epoch 0xfffff, 2 key chunks (wraps)")
+        assert m.decode_epoch() == 1, "the wrap skips epoch 0"
+        decode(1000, "epoch 1 after the wrap, 4 key chunks")
+        decode(1000, "epoch 2 after the wrap")
+        assert m.decode_epoch() == 3
+        with pytest.raises(vxm.VxmError):
+            m.set_decode_epoch(0)
+        with pytest.raises(vxm.VxmError):
+            m.set_decode_epoch(1 << 20)
+    finally:
+        for mm in models.values():
+            mm.free()
+        for k in kvs.values():
+            k.free()
+
+
+def test_single_launch_kernels_on_two_streams(vxm_ctx, orc):
+    """A single-launch decode and a single-launch LocDiT evaluation issued from two
+    contexts (two streams of one device) with no host synchronisation in between:
+    every eager single-launch kernel is ordered after the device's previous one, so
+    neither interleaves its workgroups with the other, and each result is
+    bit-identical to the same call run alone."""
+    import torch
+    import vxm
+    from locdit_case import make_inputs, make_locdit
+
+    cap = 512
+    s, rng, c, lws, fn, models, kvs, kcs, vcs = _setup(orc, vxm, vxm_ctx, "tslm", 2, cap, 300, 707)
+    dm, dkv = models[2], kvs[2]
+    shp = (s["nkv"], cap, s["hd"])
+    base = [(k.copy(), v.copy()) for k, v in zip(kcs, vcs)]
+    x = rng.normal(0, 1, (1, s["H"])).astype(np.float32)
+    ctx2 = vxm.Context(0)
+    cfg, w, ow, ocfg = make_locdit(orc, 808, 1024, 3, 16, 2, 128, 4096, 64, True)
+    ld = vxm.LocDiT(ctx2, cfg, w)
+    ld.set_block_mode(vxm.DECODE_PERSISTENT)
+    lx, lcond, lmu = make_inputs(809, 4, 4, 64, 1024)
+
+    def run_decode():
+        for l in range(2):
+            dkv.upload(l, base[l][0].reshape(shp), base[l][1].reshape(shp))
+        xd = _dev(x)
+        dm.forward(dkv, xd, 300)
+        return xd
+
+    def run_locdit():
+        return ld.forward(_dev(lx), _dev(lcond), 0.4, 0.0, _dev(lmu))
+
+    try:
+        alone_d = run_decode()
+        vxm_ctx.sync()
+        alone_d = alone_d.cpu().numpy()
+        alone_l = run_locdit()
+        ctx2.sync()
+        alone_l = alone_l.cpu().numpy()
+        torch.cuda.synchronize()
+        for rep in range(3):
+            print(f"two streams, round {rep}", flush=True)
+            yd = run_decode()
+            yl = run_locdit()       # other context, other stream, no sync in between
+            yd2 = run_decode() if rep == 2 else None
+            vxm_ctx.sync()
+            ctx2.sync()
+            dm.check()
+            ld.check()
+            assert np.array_equal(yd.cpu().numpy(), alone_d), f"decode differs in round {rep}"
+            assert np.array_equal(yl.cpu().numpy(), alone_l), f"locdit differs in round {rep}"
+            if yd2 is not None:
+                assert np.array_equal(yd2.cpu().numpy(), alone_d)
+    finally:
+        ld.free()
+        ctx2.close()
+        for mm in models.values():
+            mm.free()
+        for k in kvs.values():
+            k.free()

@@ -344,3 +344,62 @@ def test_prefill_512_equals_two_chunks_of_256(vxm_ctx, orc, stack28):
         m.free()
         kva.free()
         kvb.free()
+
+
+@pytest.mark.parametrize("ctx0", [256, 700])
+def test_decode_every_layer_of_one_28_layer_launch(vxm_ctx, orc, stack28, ctx0):
+    """Depth inside ONE 28-layer single launch (and the per-op path): the library
+    writes every layer's input and the last layer's output (vxm_minicpm4_set_layer_dump,
+    the counterpart of the reference's per-node read-back), and the oracle's block l,
+    fed the launch's own input to layer l and the same prior cache, must give the
+    launch's input to layer l + 1 within the one-layer bar.  Layers 1-27 run on the
+    code that a one-layer model never reaches (the two x buffers by layer parity,
+    layer-table entries past 0, tags with layer bits, the ring across layer
+    boundaries).  At 700 keys every head's keys are split over 3 workgroups, so the
+    chunk merge is pinned at every depth too.  The K / V row each layer appends is
+    compared with the oracle's from the same input."""
+    import torch
+    import vxm
+
+    layers, fn = stack28
+    cap = 1024
+    rng = np.random.default_rng(505 + ctx0)
+    c = cfg_dict(H, L, NH, NKV, HD, F)
+    oc1 = orc_cfg(orc, cfg_dict(H, 1, NH, NKV, HD, F))
+    caches = [_prior_cache(orc, rng, cap, ctx0) for _ in range(L)]
+    x = rng.normal(0, 1, (1, H)).astype(np.float32)
+    worst = 0.0
+    for mode in (2, 1):
+        m = vxm.MiniCPM4(vxm_ctx, c, layers, final_norm=fn)
+        m.set_decode_mode(mode)
+        kv = vxm.KVCache(vxm_ctx, L, NKV, HD, cap)
+        dump = torch.full((L + 1, H), float("nan"), dtype=torch.float32, device="cuda:0")
+        try:
+            for l in range(L):
+                kv.upload(l, *caches[l])
+            m.set_layer_dump(dump)
+            xd = _dev(x)
+            print(f"28-layer decode with layer dump, mode {mode}, ctx {ctx0}", flush=True)
+            m.forward(kv, xd, ctx0)
+            vxm_ctx.sync()
+            m.check()
+            d = dump.cpu().numpy()
+            out = xd.cpu().numpy()
+            kvrows = [kv.download(l) for l in range(L)]
+        finally:
+            m.set_layer_dump(None)
+            m.free()
+            kv.free()
+        assert np.isfinite(d).all(), "a layer's dump was not written"
+        assert np.array_equal(d[0], x[0]), "layer 0's input is the call's x"
+        # the returned row is the final norm of the last layer's output
+        assert np.array_equal(out[0], orc.rms_norm(d[L:L + 1], fn, 1e-6)[0]), "final norm of the dumped output"
+        for l in range(L):
+            kc, vc = caches[l][0].reshape(-1).copy(), caches[l][1].reshape(-1).copy()
+            ref = orc.minicpm4_block(oc1, to_orc(orc, layers[l]), d[l:l + 1], kc, vc, cap, ctx0, 0)
+            worst = max(worst, assert_one_layer(d[l + 1:l + 2], ref, f"mode {mode} layer {l} of one launch"))
+            rows = slice(ctx0, ctx0 + 1)
+            for got, want, nm in ((kvrows[l][0], kc, "K"), (kvrows[l][1], vc, "V")):
+                w3 = want.reshape(NKV, cap, HD)
+                assert _kv_worst(orc, got, w3, rows) <= KV_ULP, (mode, l, nm)
+    print(f"every layer of one launch, ctx {ctx0}: worst rel-L2 {worst:.3g}")

@@ -143,6 +143,41 @@ def test_oracle_block_sensitivity_to_one_ulp(orc):
     assert worst_rel > 1e-3
 
 
+def test_oracle_velocity_sensitivity_to_one_ulp(orc):
+    """The measurement behind the velocity bar of the GPU tests: the velocity of one
+    full-width block (final norm of the x rows, out_proj, BF16), recomputed from the
+    block's input with ONE element moved by one BF16 ulp, moves the oracle's own
+    velocity by a relative L2 above the block bar's 5e-3 for most seeds and, over the
+    eight seeds and six random elements each, by at most 1e-2 relative L2 and 2^-5 of
+    a row's scale."""
+    worst_rel = worst_row = 0.0
+    above = 0
+    for seed in (51, 101, 202, 303, 404, 505, 606, 707):
+        cfg, w, ow, ocfg = make_locdit(orc, seed, 1024, 1, 16, 16, 64, 4096, 64)
+        x, cond, mu = make_inputs(seed + 1, 4, 17, 64, 1024)
+        v, st = orc.locdit_states(ocfg, ow, x, cond, 0.6, 0.0, mu)
+
+        def vel(s0):
+            seq = orc.minicpm4_block(ocfg, ow.layers[0], s0, pos=0, no_causal=1)
+            hn = orc.rms_norm(seq[3 + 17:], ow.norm, 1e-6)
+            return orc.bf16_round(orc.linear(ow.out_proj, hn, ow.feat, 1024, bias=ow.out_bias)).astype(np.float64)
+
+        assert np.array_equal(vel(st[0]), v), "the composition is the oracle's velocity"
+        rng = np.random.default_rng(seed)
+        seed_rel = 0.0
+        for _ in range(6):
+            p = st[0].copy()
+            p.view(np.uint32)[int(rng.integers(0, 24)), int(rng.integers(0, 1024))] += 1 << 16
+            y = vel(p)
+            rel = np.linalg.norm(y - v) / np.linalg.norm(v)
+            row = (np.abs(y - v) / np.abs(v).max(axis=1, keepdims=True)).max()
+            seed_rel, worst_row = max(seed_rel, rel), max(worst_row, row)
+        worst_rel = max(worst_rel, seed_rel)
+        above += seed_rel > 5e-3
+    assert above >= 4 and worst_rel > 8e-3 and worst_row > 2.0 ** -6
+    assert worst_rel <= 1e-2 and worst_row <= 2.0 ** -5
+
+
 def test_oracle_cfm_trajectory_sensitivity(orc):
     """The measurement behind the trajectory bar of the GPU tests: one BF16 ulp on
     one element of x0 moves the oracle's own 3-step CFG trajectory (full width,

@@ -90,6 +90,31 @@ def test_noalloc_repeat_after_allocating_calls(vxm_ctx, orc):
         w.free()
 
 
+def test_noalloc_rejects_split_above_scratch(vxm_ctx, orc):
+    """2048 x 6144 at M = 520: vxm_mul_mat_q8_0 splits K 3 ways, whose partial
+    words (25.6 MB) exceed the array's 16 MiB.  The allocation-free entry rejects
+    the call rather than running another plan (with another summation order)."""
+    import torch
+    import vxm
+
+    N, K, M = 2048, 6144, 520
+    x, wq = _case(orc, N, K, M, 5)
+    w = vxm_ctx.upload_q8_0(wq, N, K)
+    xd = _dev(x)
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda:0")
+    with pytest.raises(vxm.VxmError) as e:
+        vxm_ctx.mul_mat_noalloc(w, xd, y)
+    assert e.value.code == 1 and "split partials" in str(e.value)
+    # the allocating entry runs the split plan; it stays within the matmul bar
+    y_ref = vxm_ctx.mul_mat(w, xd).cpu().numpy()
+    vxm_ctx.sync()
+    xq = orc.quantize_rows(x, orc.QUANT_X86)
+    ref = orc.mul_mat_f64(wq, xq, N, K, M)
+    err = np.abs(y_ref.astype(np.float64) - ref)
+    assert np.all(err <= ATOL + RTOL * np.abs(ref)), f"max err {err.max()}"
+    w.free()
+
+
 def test_noalloc_rejects_oversize(vxm_ctx, orc):
     import torch
     import vxm

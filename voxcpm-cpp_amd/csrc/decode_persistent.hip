@@ -370,11 +370,20 @@ struct vxm_pparams {
     int att_split;     // key chunks per head (1: one workgroup per head)
     const int8_t *dummy_q;     // 2 KiB of zeros: loads of units a wave does not own
     const uint16_t *dummy_d;   // 64 zero scales
+    // [0] live: set by a workgroup that gave up waiting, polled by the others,
+    // cleared at the end of the launch by its last workgroup; [1] sticky: also
+    // set, read and cleared by vxm_minicpm4_check
     int *err;
+    // [0] launch epoch (read by every workgroup at start, advanced by the last
+    // workgroup to finish), [1] workgroups finished in this launch
+    uint32_t *state;
+    uint64_t n_chan;   // words of the channels xb .. attp (contiguous), reset when the epoch wraps
+    // debug: [n_layers + 1][H] -- the input of every layer and the last layer's
+    // output before the final norm (written by workgroup 0), or null
+    float *dump;
     const float2 *rope_cs;   // (cos, sin) table [position][HD/2]
     float eps, res_scale;
     int pos, cap, no_rope;
-    uint32_t epoch;
 #ifdef VXM_PERSISTENT_TRACE
     uint64_t *trace;
     int trace_stride;
@@ -407,6 +416,7 @@ __device__ __forceinline__ bool give_up(const vxm_pparams &p, int &it, int *bail
     // per token)
     if (++it > kSpin || ((it & 31) == 0 && __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
         __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.err + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *bail = 1;
         return true;
     }
@@ -417,7 +427,7 @@ __device__ __forceinline__ bool give_up(const vxm_pparams &p, int &it, int *bail
 // loads of a round in flight) into LDS: PAIRS unpacks two BF16 values per
 // word to dst[2i], dst[2i+1], otherwise one fp32 to dst[i].  Words whose tag
 // is not yet `tag` are read again next round.  Returns this lane's sum of
-// the squares of its values in double (exact for BF16-valued inputs).
+// the squares of its values in double (each square exact for BF16-valued inputs).
 template <int NPL, bool PAIRS, bool RAW = false>
 __device__ double read_words(const vxm_pparams &p, const uint64_t *src, int n, uint32_t tag, float *dst, int *bail) {
     static_assert(NPL <= 64, "words per lane");
@@ -602,7 +612,10 @@ __device__ void quantize_lds_bf16x2(const uint32_t *src, int n, int8_t *xq, floa
 
 // vcpm_rms_norm (src/minicpm4.c:132-152) fused with the Q8_0 of its output:
 // y = BF16(BF16(x * sc) * g), sc = 1 / sqrt(sum(x^2) / n + eps), 4 values per
-// thread, n <= 4 * kThreads.  sumsq is the exact double sum of squares.
+// thread, n <= 4 * kThreads.  sumsq is the double sum of squares, formed in a
+// tree order by the reading waves: equal to ggml's sequential double while the
+// squares span less than about 2^26 (every partial sum exact), else possibly one
+// rounding apart.
 template <int N>
 __device__ __forceinline__ void norm_quant(const float *x, const float *g, double sumsq, float eps, int8_t *xq,
                                            float *xd) {
@@ -904,7 +917,7 @@ __device__ __forceinline__ void attn_load(const uint16_t *base, int jb, int lim,
 // the unsplit attention, unchanged.
 template <class S>
 __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int h, int chunk, float *lds,
-                                                int *bail) {
+                                                int *bail, uint32_t ep) {
     constexpr int QD = S::QD, KVD = S::KVD, HD = S::HD;
     constexpr int SQ = rep_stride(S::NQKV / 2), SAT = rep_stride(QD);
     constexpr int LPK = HD / 8, KPW = 64 / LPK;                  // lanes per key, keys per wave
@@ -912,7 +925,6 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
     constexpr int PERB = kWaves * KPW * KB;                      // keys per batch (320)
     const int tid = tid_now(), wave = tid >> 6, lane = tid & 63;
     const int rp = blockIdx.x % kRep, g = h / S::QPK, pos = p.pos;
-    const uint32_t ep = p.epoch;
     vxm_ptab Ly = layer_at(p, l);
     float *aq = lds + S::L_AQ, *red = lds + S::L_RED, *sc = lds + S::L_BIG;   // scores: BIG is free in phase B
     uint16_t *const kc = Ly->kc, *const vc = Ly->vc;
@@ -1154,7 +1166,7 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
 // waves 1..7 also stream weights and publish the outputs.  All waves walk
 // the same phase schedule and barrier sequence.
 template <class S>
-__device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int *bail) {
+__device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int *bail, uint32_t ep) {
     constexpr int H = S::H, QD = S::QD, KVD = S::KVD, HD = S::HD, F = S::F, NH = S::NH;
     constexpr int SX = rep_stride(H / 2), SQ = rep_stride(S::NQKV / 2), SAT = rep_stride(QD), SP = rep_stride(F / 2);
     const int wg = blockIdx.x;
@@ -1168,7 +1180,6 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
     const int ci = __builtin_amdgcn_readfirstlane(wave - 1);   // compute wave index (uniform)
     const int t = tid_now() - 64;                             // compute thread index
     const int pos = p.pos;
-    const uint32_t ep = p.epoch;
     // the query head this workgroup attends for, or -1
     int head = -1, chunk = 0;
     for (int h = 0; h < NH; h++)
@@ -1221,6 +1232,9 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         lds_barrier();
         if (*bail) return;
         VXM_TS(tid_now() == 0, 0);
+        if (p.dump && wg == 0)
+            for (int i = tid_now() * 4; i < H; i += kThreads * 4)
+                *(float4 *)(p.dump + (size_t)l * H + i) = *(const float4 *)(xs + i);
         {
             double sst = 0.0;
 #pragma unroll
@@ -1261,7 +1275,7 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         if (!reader && head < 0) ring_refill<S, S::OA, S::SA>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         // ---------------- B: attention, one workgroup per query head ----------------
         if (head >= 0) {
-            attention_phase<S>(p, l, head, chunk, lds, bail);
+            attention_phase<S>(p, l, head, chunk, lds, bail, ep);
             if (*bail) return;
             if (!reader) ring_refill<S, S::OA, S::SA>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         }
@@ -1384,8 +1398,6 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         if (!reader) ring_refill<S, S::OE, S::SE>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         cur = nxt;
     }
-    // the refills past the last layer (zero units) land before the workgroup ends
-    ring_wait<0>();
     // ---------------- final norm (workgroup 0) ----------------
     if (wg != 0) return;
     const int Lyr = p.n_layers;
@@ -1399,6 +1411,9 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
 #ifdef VXM_PERSISTENT_TRACE
     if (tid_now() == 0 && p.trace) p.trace[1] = __builtin_amdgcn_s_memrealtime();
 #endif
+    if (p.dump)
+        for (int i = tid_now() * 4; i < H; i += kThreads * 4)
+            *(float4 *)(p.dump + (size_t)Lyr * H + i) = *(const float4 *)(xs + i);
     if (p.final_norm) {
         rmsnorm_lds(xs, gn, H, p.eps, big, red);
         for (int i = tid_now(); i < H; i += kThreads) p.x[i] = big[i];
@@ -1409,22 +1424,59 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
 
 }  // namespace
 
+// The tag epoch of a launch lives in device memory: every workgroup reads it at
+// start, and the last workgroup to finish advances it.  A launch recorded into a
+// HIP graph therefore tags its words anew on every replay.  Tags hold 20 bits
+// of it; when it wraps (every 1,048,575 launches, about 10 minutes of decode at
+// 575 us per token), that last workgroup first resets every channel word to
+// all-ones, so no word written before the wrap (for instance a key-chunk
+// partial of a head split that later launches did not repeat) can carry a live
+// tag again.
+constexpr uint32_t kEpochMask = 0xfffffu;
+
 template <class S>
 __global__ __launch_bounds__(kThreads, 1) void k_decode_persistent(vxm_pparams p) {
     // All of the workgroup's LDS is this one dynamic array, so it starts at
     // address 0 and every 16-byte layout offset is 16-byte aligned.  (A static
     // __shared__ variable beside it would place the dynamic array right after
     // the static bytes, at only 4-byte alignment: every ds_read_b128 of the
-    // ring and the activations would then be split by the LDS.)  The bail
-    // flag lives past the layout, at byte S::BYTES.
+    // ring and the activations would then be split by the LDS.)  The bail and
+    // last-workgroup flags live past the layout, at byte S::BYTES.
     extern __shared__ __attribute__((aligned(16))) float lds[];
     int *bail = (int *)((char *)lds + S::BYTES);
+    int *last = bail + 1;
     if (threadIdx.x == 0) *bail = 0;
 #ifdef VXM_PERSISTENT_TRACE
     if (threadIdx.x == 0 && p.trace) p.trace[(size_t)blockIdx.x * p.trace_stride] = __builtin_amdgcn_s_memrealtime();
 #endif
+    // a scalar load: the previous launch's last workgroup wrote it before that launch ended
+    const uint32_t ep = __builtin_amdgcn_readfirstlane(*(const volatile uint32_t *)p.state);
     // bail is read only after the first barrier of decode_run
-    decode_run<S>(p, lds, bail);
+    decode_run<S>(p, lds, bail, ep);
+    // every ring load of the wave (the refills past the last layer, or those in
+    // flight when a wait gave up) lands before the workgroup ends
+    ring_wait<0>();
+    lds_barrier();
+    if (threadIdx.x == 0) {
+        const uint32_t done = __hip_atomic_fetch_add(p.state + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last = done == kG - 1;
+    }
+    lds_barrier();
+    if (!*last) return;
+    // the last workgroup: every other workgroup has read the epoch and finished
+    // with the channels
+    uint32_t next = (ep + 1u) & kEpochMask;
+    if (next == 0) {
+        next = 1;
+        for (uint64_t i = threadIdx.x; i < p.n_chan; i += kThreads)
+            __hip_atomic_store(p.xb + i, ~0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lds_barrier();
+    }
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(p.state + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.err, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // the live word
+        __hip_atomic_store(p.state, next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1438,8 +1490,9 @@ struct vxm_persistent_state {
     uint64_t *xb = nullptr, *qkvb = nullptr, *attb = nullptr, *h1b = nullptr, *pb = nullptr, *attp = nullptr;
     int8_t *dummy_q = nullptr;
     uint16_t *dummy_d = nullptr;
-    int *err = nullptr;
-    uint32_t epoch = 0;
+    int *err = nullptr;         // [0] live, [1] sticky
+    uint32_t *state = nullptr;  // [0] epoch, [1] arrivals
+    uint64_t n_chan = 0;        // channel words (xb .. attp)
     // the cache whose K/V pointers are in the layer table: its unique id, base
     // and capacity (a freed cache's struct address can come back for a new one)
     uint64_t kv_id = 0;
@@ -1455,38 +1508,26 @@ static constexpr int kMaxLds = 160 * 1024;
 // a device whose other work finishes on its own.  hipLaunchCooperativeKernel
 // guarantees it, but measured 19 us more per token (649 against 630).  Other
 // work on the device can only delay the waits, and every wait is bounded
-// (kSpin rounds, then the error word): an error, never a hang.  Two decodes on
-// different streams of one device could interleave their workgroups and wait
-// on each other until that bound.  So every decode launch on a device is
-// ordered after the previous one there: one event per device, waited on when
-// the stream changes.
-namespace {
-struct LaunchOrder {
-    std::mutex mu;
-    hipEvent_t ev = nullptr;
-    hipStream_t last = nullptr;
-};
-LaunchOrder g_launch_order[64];
-}  // namespace
-
+// (kSpin rounds, then the error word): an error, never a hang.  Eager launches
+// are ordered after the device's previous single-launch kernel
+// (vxm_ordered_launch_begin), so two of them on different streams never
+// interleave their workgroups.
 template <class S>
 static int launch_decode(vxm_ctx *ctx, const vxm_pparams &prm) {
-    const int lds = S::BYTES + 16;   // the layout + the bail flag
+    const int lds = S::BYTES + 16;   // the layout + the bail and last-workgroup flags
     auto kern = k_decode_persistent<S>;
     if (lds > kMaxLds)
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "persistent decode: kv capacity %d needs %d B of LDS", prm.cap, lds);
-    if (ctx->device < 0 || ctx->device >= 64)
-        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "persistent decode: device %d beyond the launch table", ctx->device);
     VXM_HIP(ctx, hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
-    LaunchOrder &o = g_launch_order[ctx->device];
-    std::lock_guard<std::mutex> lock(o.mu);
-    if (!o.ev) VXM_HIP(ctx, hipEventCreateWithFlags(&o.ev, hipEventDisableTiming));
-    if (o.last && o.last != ctx->stream) VXM_HIP(ctx, hipStreamWaitEvent(ctx->stream, o.ev, 0));
+    vxm_launch_slot *slot = nullptr;
+    bool capturing = false;
+    int rc = vxm_ordered_launch_begin(ctx, &slot, &capturing);
+    if (rc) return rc;
     hipLaunchKernelGGL(kern, dim3(kG), dim3(kThreads), (unsigned)lds, ctx->stream, prm);
-    VXM_CHECK_LAUNCH(ctx);
-    VXM_HIP(ctx, hipEventRecord(o.ev, ctx->stream));
-    o.last = ctx->stream;
-    return VXM_OK;
+    const hipError_t le = hipGetLastError();
+    rc = vxm_ordered_launch_end(ctx, slot, capturing);
+    if (le != hipSuccess) return vxm_fail(ctx, VXM_ERR_BACKEND, "persistent decode launch failed: %s", hipGetErrorString(le));
+    return rc;
 }
 
 // Supported shapes: (hidden, heads, kv heads, head dim, ffn).
@@ -1538,7 +1579,7 @@ void vxm_persistent_free(vxm_minicpm4 *m) {
     }
 }
 
-int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t pos) {
+int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t pos, float *dump) {
     vxm_ctx *ctx = m->ctx;
     const vxm_block_dims &d = m->dims;
     if (!persistent_shape(d, ctx->n_cu))
@@ -1551,13 +1592,20 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
     const int64_t qd = (int64_t)d.nh * d.hd, kvd = (int64_t)d.nkv * d.hd;
     if (!m->pstate) m->pstate = new vxm_persistent_state();
     vxm_persistent_state &s = *m->pstate;
+    hipStreamCaptureStatus cap_st = hipStreamCaptureStatusNone;
+    VXM_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cap_st));
+    const bool capturing = cap_st != hipStreamCaptureStatusNone;
+    if (capturing && (!s.base || s.kv_id != kv->id || s.kv_base != kv->base || s.kv_cap != kv->cap))
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG,
+                        "persistent decode: its buffers and layer table are set up by an eager call; run one "
+                        "decode on this model and cache before capturing");
     if (!s.base) {
         const size_t tab = ((size_t)L * sizeof(vxm_player) + 255) & ~(size_t)255;
         const int nx = rep_stride((int)d.H / 2), nq = rep_stride((int)(qd + 2 * kvd) / 2),
                   na = rep_stride((int)qd), np_ = rep_stride((int)d.F / 2);
         const size_t words = (size_t)kRep * (2 * nx + nq + na + nx + np_) + (size_t)d.nh * kAttSplitMax * kAttpWords;
         const size_t dummy = kUnit + 256;
-        const size_t total = tab + words * 8 + dummy + 256;
+        const size_t total = tab + words * 8 + dummy + 256 + 64;
         if (hipMalloc(&s.base, total) != hipSuccess) {
             (void)hipGetLastError();
             return vxm_fail(ctx, VXM_ERR_OOM, "persistent decode buffers failed");
@@ -1574,9 +1622,14 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
         s.dummy_q = (int8_t *)b; b += kUnit;
         s.dummy_d = (uint16_t *)b; b += 256;
         s.err = (int *)b;
-        // tags start as all-ones: never equal to a live (epoch >= 1) tag
+        s.state = (uint32_t *)(b + 64);
+        s.n_chan = words;
+        // tags start as all-ones: never equal to a live (epoch >= 1) tag; the first launch has epoch 1
+        const uint32_t st0[2] = {1u, 0u};
         VXM_HIP(ctx, hipMemsetAsync((char *)s.base + tab, 0xff, words * 8, ctx->stream));
-        VXM_HIP(ctx, hipMemsetAsync(s.dummy_q, 0, dummy + 4, ctx->stream));
+        VXM_HIP(ctx, hipMemsetAsync(s.dummy_q, 0, dummy + 256 + 64, ctx->stream));
+        VXM_HIP(ctx, hipMemcpyAsync(s.state, st0, sizeof st0, hipMemcpyHostToDevice, ctx->stream));
+        VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
         s.kv_id = 0;
     }
     if (s.kv_id != kv->id || s.kv_base != kv->base || s.kv_cap != kv->cap) {
@@ -1593,8 +1646,6 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
         s.kv_base = kv->base;
         s.kv_cap = kv->cap;
     }
-    s.epoch = (s.epoch + 1) & 0xfffffu;
-    if (s.epoch == 0) s.epoch = 1;
     vxm_pparams prm{};
     prm.layers = s.layers;
     prm.n_layers = L;
@@ -1615,13 +1666,15 @@ int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t p
     prm.dummy_q = s.dummy_q;
     prm.dummy_d = s.dummy_d;
     prm.err = s.err;
+    prm.state = s.state;
+    prm.n_chan = s.n_chan;
+    prm.dump = dump;
     prm.rope_cs = d.rope_cs;
     prm.eps = d.eps;
     prm.res_scale = d.res_scale;
     prm.pos = pos;
     prm.cap = kv->cap;
     prm.no_rope = d.no_rope;
-    prm.epoch = s.epoch;
 #ifdef VXM_PERSISTENT_TRACE
     // profiling builds: one trace buffer per process, dumped after every launch
     static uint64_t *tbuf = nullptr;
@@ -1660,10 +1713,29 @@ int vxm_persistent_check(vxm_minicpm4 *m) {
     if (!m->pstate || !m->pstate->err) return VXM_OK;
     int e = 0;
     VXM_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
-    VXM_HIP(m->ctx, hipMemcpy(&e, m->pstate->err, 4, hipMemcpyDeviceToHost));
+    VXM_HIP(m->ctx, hipMemcpy(&e, m->pstate->err + 1, 4, hipMemcpyDeviceToHost));
     if (e) {
-        VXM_HIP(m->ctx, hipMemset(m->pstate->err, 0, 4));
+        VXM_HIP(m->ctx, hipMemset(m->pstate->err + 1, 0, 4));
         return vxm_fail(m->ctx, VXM_ERR_BACKEND, "persistent decode: a workgroup timed out waiting for data");
     }
+    return VXM_OK;
+}
+
+// Test hook: the tag epoch of the next launch (1 .. 2^20 - 1), and the current one.
+int vxm_persistent_set_epoch(vxm_minicpm4 *m, uint32_t epoch) {
+    if (!m->pstate || !m->pstate->state)
+        return vxm_fail(m->ctx, VXM_ERR_INVALID_ARG, "decode epoch: no single-launch decode has run on this model");
+    if (epoch == 0 || epoch > kEpochMask)
+        return vxm_fail(m->ctx, VXM_ERR_INVALID_ARG, "decode epoch %u outside 1 .. %u", epoch, kEpochMask);
+    VXM_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    VXM_HIP(m->ctx, hipMemcpy(m->pstate->state, &epoch, 4, hipMemcpyHostToDevice));
+    return VXM_OK;
+}
+
+int vxm_persistent_get_epoch(vxm_minicpm4 *m, uint32_t *epoch) {
+    *epoch = 0;
+    if (!m->pstate || !m->pstate->state) return VXM_OK;
+    VXM_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    VXM_HIP(m->ctx, hipMemcpy(epoch, m->pstate->state, 4, hipMemcpyDeviceToHost));
     return VXM_OK;
 }

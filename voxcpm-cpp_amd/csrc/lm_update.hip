@@ -32,6 +32,9 @@ struct vxm_locenc {
     int8_t *aq = nullptr;
     uint16_t *ad = nullptr;
     int block_mode = VXM_DECODE_AUTO;   // blocks launch by launch, or all in one persistent launch
+    // debug: each evaluation writes the rows entering every block and the last block's
+    // output (residual added) here, [n_layers + 1][rows][H] (null: off)
+    float *block_dump = nullptr;
     vxm_lpersist *lp = nullptr;
 };
 
@@ -246,12 +249,13 @@ extern "C" int vxm_locenc_forward(vxm_locenc *m, const float *x_dev, int32_t P, 
                        m->in_bias, (int)H);
     VXM_CHECK_LAUNCH(ctx);
     // bidirectional blocks over the S fresh rows, positions 0..S-1, no cache
+    bool residual_added = false;   // the last block's residual already in seq (debug dump)
     const bool persistent = m->cfg.n_layers > 0 && vxm_locdit_persistent_pick(ctx, d, S, (int)S, m->block_mode);
     if (m->block_mode == VXM_DECODE_PERSISTENT && !persistent)
         return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "locenc: no persistent block kernel for this shape / device");
     if (persistent) {
         // all blocks in one launch; seq then holds the last block's output, residual included
-        if ((rc = vxm_locdit_persistent_run(ctx, d, m->blocks, &m->lp, m->seq, S, (int)S))) return rc;
+        if ((rc = vxm_locdit_persistent_run(ctx, d, m->blocks, &m->lp, m->seq, S, (int)S, m->block_dump))) return rc;
     } else {
         const vxm_attn_site site{m->ws.lk, m->ws.lv, (int)S, (int64_t)d.nkv * S * d.hd, (int)S, 0, 0, 0};
         for (int l = 0; l < m->cfg.n_layers; l++) {
@@ -259,14 +263,32 @@ extern "C" int vxm_locenc_forward(vxm_locenc *m, const float *x_dev, int32_t P, 
             if ((rc = vxm_launch_rmsnorm(ctx, m->seq, l ? m->ws.dn_out : vxm_parts{}, 1.0f, b.g_in, S, H, d.eps,
                                          nullptr, m->ws.xq, m->ws.xd, var)))
                 return rc;
+            // the norm added the previous block's residual in place: seq holds block l's input
+            if (m->block_dump)
+                VXM_HIP(ctx, hipMemcpyAsync(m->block_dump + (size_t)l * S * H, m->seq, (size_t)S * H * sizeof(float),
+                                            hipMemcpyDeviceToDevice, ctx->stream));
             if ((rc = vxm_block_run(ctx, d, b, m->ws, m->seq, S, site))) return rc;
+        }
+        if (m->block_dump && m->cfg.n_layers) {
+            // debug: the last residual on its own (the final norm then adds none), and the rows out
+            if ((rc = vxm_launch_residual(ctx, m->seq, m->ws.dn_out, 1.0f, S * H))) return rc;
+            residual_added = true;
+            VXM_HIP(ctx, hipMemcpyAsync(m->block_dump + (size_t)m->cfg.n_layers * S * H, m->seq,
+                                        (size_t)S * H * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
         }
     }
     // last residual + final RMSNorm of the rows that are returned: the
     // special token's row (src/locenc.c:118-128), or every row
     const int64_t rows = off ? 1 : S;
-    return vxm_launch_rmsnorm(ctx, m->seq, m->cfg.n_layers && !persistent ? m->ws.dn_out : vxm_parts{}, 1.0f, m->norm,
+    return vxm_launch_rmsnorm(ctx, m->seq, m->cfg.n_layers && !persistent && !residual_added ? m->ws.dn_out : vxm_parts{},
+                              1.0f, m->norm,
                               rows, H, d.eps, out_dev, nullptr, nullptr, var);
+}
+
+extern "C" int vxm_locenc_set_block_dump(vxm_locenc *m, float *dump_dev) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    m->block_dump = dump_dev;
+    return VXM_OK;
 }
 
 extern "C" int vxm_locenc_set_block_mode(vxm_locenc *m, int mode) {

@@ -53,6 +53,9 @@ struct vxm_locdit {
     hipGraphExec_t cfm_exec = nullptr;
     std::vector<uint64_t> cfm_key, cfm_last_eager;
     int block_mode = VXM_DECODE_AUTO;   // blocks launch by launch, or all in one persistent launch
+    // debug: each evaluation writes the rows entering every block and the last block's
+    // output (residual added) here, [n_layers + 1][rows][H] (null: off)
+    float *block_dump = nullptr;
     vxm_lpersist *lp = nullptr;
 };
 
@@ -286,12 +289,13 @@ static int dit_eval(vxm_locdit *m, const float *x, int P, int Pc, int n_seg, con
                        m->ch, m->cond_bias, m->xh, m->in_bias, (int)S, Pc, (int)H);
     VXM_CHECK_LAUNCH(ctx);
     // non-causal blocks, rope positions from 0 in each segment, fresh K/V per segment
+    bool residual_added = false;   // the last block's residual already in seq (debug dump)
     const bool persistent = m->cfg.n_layers > 0 && vxm_locdit_persistent_pick(ctx, d, M, (int)S, m->block_mode);
     if (m->block_mode == VXM_DECODE_PERSISTENT && !persistent)
         return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "locdit: no persistent block kernel for this shape / device");
     if (persistent) {
         // all blocks in one launch; seq then holds the last block's output, residual included
-        if ((rc = vxm_locdit_persistent_run(ctx, d, m->blocks, &m->lp, m->seq, M, (int)S))) return rc;
+        if ((rc = vxm_locdit_persistent_run(ctx, d, m->blocks, &m->lp, m->seq, M, (int)S, m->block_dump))) return rc;
     } else {
         const vxm_attn_site site{m->ws.lk, m->ws.lv, (int)S, (int64_t)d.nkv * S * d.hd, (int)S, 0, 0, 0};
         for (int l = 0; l < m->cfg.n_layers; l++) {
@@ -299,7 +303,18 @@ static int dit_eval(vxm_locdit *m, const float *x, int P, int Pc, int n_seg, con
             if ((rc = vxm_launch_rmsnorm(ctx, m->seq, l ? m->ws.dn_out : vxm_parts{}, 1.0f, b.g_in, M, H, d.eps,
                                          nullptr, m->ws.xq, m->ws.xd, var)))
                 return rc;
+            // the norm added the previous block's residual in place: seq holds block l's input
+            if (m->block_dump)
+                VXM_HIP(ctx, hipMemcpyAsync(m->block_dump + (size_t)l * M * H, m->seq, (size_t)M * H * sizeof(float),
+                                            hipMemcpyDeviceToDevice, ctx->stream));
             if ((rc = vxm_block_run(ctx, d, b, m->ws, m->seq, M, site))) return rc;
+        }
+        if (m->block_dump && m->cfg.n_layers) {
+            // debug: the last residual on its own (the final norm then adds none), and the rows out
+            if ((rc = vxm_launch_residual(ctx, m->seq, m->ws.dn_out, 1.0f, M * H))) return rc;
+            residual_added = true;
+            VXM_HIP(ctx, hipMemcpyAsync(m->block_dump + (size_t)m->cfg.n_layers * M * H, m->seq,
+                                        (size_t)M * H * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
         }
     }
     // last residual + final RMSNorm of the x rows of each segment (src/locdit.c:373-390)
@@ -308,7 +323,7 @@ static int dit_eval(vxm_locdit *m, const float *x, int P, int Pc, int n_seg, con
         const int64_t r0 = 3 + Pc;
         const vxm_parts &dn = m->ws.dn_out;
         const vxm_parts delta =
-            m->cfg.n_layers && !persistent ? vxm_parts{dn.p + r0 * H, dn.n, dn.stride} : vxm_parts{};
+            m->cfg.n_layers && !persistent && !residual_added ? vxm_parts{dn.p + r0 * H, dn.n, dn.stride} : vxm_parts{};
         if ((rc = vxm_launch_rmsnorm(ctx, m->seq + r0 * H, delta, 1.0f, m->norm, (int64_t)n_seg * P, H, d.eps,
                                      nullptr, m->aq, m->ad, var, P, (int)S)))
             return rc;
@@ -455,6 +470,12 @@ extern "C" int vxm_locdit_create(vxm_ctx *ctx, const vxm_locdit_config *cfg, con
     return VXM_OK;
 }
 
+extern "C" int vxm_locdit_set_block_dump(vxm_locdit *m, float *dump_dev) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    m->block_dump = dump_dev;
+    return VXM_OK;
+}
+
 extern "C" int vxm_locdit_set_block_mode(vxm_locdit *m, int mode) {
     if (!m) return VXM_ERR_INVALID_ARG;
     if (mode < VXM_DECODE_AUTO || mode > VXM_DECODE_PERSISTENT)
@@ -538,16 +559,11 @@ extern "C" int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev,
     }
     if (key != m->cfm_last_eager) {
         m->cfm_last_eager = key;
-        ctx->no_split_tags = true;
-        rc = euler_loop();
-        ctx->no_split_tags = false;
-        return rc;
+        return euler_loop();
     }
     cfm_graph_drop(m);
     VXM_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-    ctx->no_split_tags = true;
     rc = euler_loop();
-    ctx->no_split_tags = false;
     hipGraph_t graph = nullptr;
     const hipError_t ec = hipStreamEndCapture(ctx->stream, &graph);
     if (rc == VXM_OK && ec != hipSuccess)

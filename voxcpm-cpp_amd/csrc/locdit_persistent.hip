@@ -105,8 +105,12 @@ struct vxm_lparams {
     const float2 *cs;        // rope (cos, sin) [position][HD/2]
     float *x;                // [M][1024]: block 0's input in, the last block's output out
     uint64_t *x1, *qkv, *att, *op, *x2, *pp, *dp;   // exchange channels
+    // [0] live: set by a workgroup that gave up waiting, polled by the others, cleared
+    // at the end of the launch by its last workgroup (so one failed launch never makes
+    // later ones give up); [1] sticky: also set, read and cleared by the check calls
     int *err;
     uint32_t *state;         // [0] epoch, [1] workgroups finished in this launch
+    float *dump;             // debug: [L + 1][M][1024] rows entering each block, then the output; or null
     uint64_t *trace;         // profiling build: per workgroup, the start and 16 timestamps per block
 };
 
@@ -166,6 +170,7 @@ __device__ __forceinline__ void lds_barrier() {
 __device__ __forceinline__ bool give_up(const vxm_lparams &p, int &it, int *bail) {
     if (++it > kSpin || ((it & 31) == 0 && __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
         __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.err + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *bail = 1;
         return true;
     }
@@ -624,6 +629,10 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             row_update(lds, LS::ST, LS::XR, LS::GN, LS::MISC, ns, p.eps, p.variant, p.x1 + (size_t)row * kXPitch,
                        make_tag(ep, L, l, PH_X1), true);
             lds_barrier();
+            // debug dump of the row entering block l (waves 0-6: wave 7's vmcnt counts only its DMAs)
+            if (!DMA && p.dump)
+                for (int c = opaque_tid() * 4; c < kH; c += kPollThreads * 4)
+                    *(float4 *)(p.dump + ((size_t)l * M + row) * kH + c) = *(const float4 *)(lds + LS::XR + c * 4);
         }
         VXM_LTS(2);
         // ---- QKV ----
@@ -1030,6 +1039,9 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             const int tid = opaque_tid();
             for (int c = tid * 4; c < kH; c += kThreads * 4)
                 *(float4 *)(p.x + (size_t)row * kH + c) = *(const float4 *)(lds + LS::XR + c * 4);
+            if (!DMA && p.dump)
+                for (int c = tid * 4; c < kH; c += kPollThreads * 4)
+                    *(float4 *)(p.dump + ((size_t)L * M + row) * kH + c) = *(const float4 *)(lds + LS::XR + c * 4);
         }
     }
 }
@@ -1064,8 +1076,10 @@ __global__ __launch_bounds__(kThreads, 1) void k_locdit_persistent(vxm_lparams p
     if (tid == 0) {
         const uint32_t done = __hip_atomic_fetch_add(p.state + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (done == kG - 1) {
-            // the last workgroup: every workgroup has read the epoch; the next launch uses the next one
+            // the last workgroup: every workgroup has read the epoch; the next launch uses the
+            // next one and starts with a clear live error word
             __hip_atomic_store(p.state + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p.err, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(p.state, ep + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
@@ -1117,7 +1131,7 @@ void vxm_locdit_persistent_free(vxm_lpersist *st) {
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::vector<vxm_block> &blocks,
-                              vxm_lpersist **stp, float *x, int64_t M, int S) {
+                              vxm_lpersist **stp, float *x, int64_t M, int S, float *dump) {
     if (!vxm_locdit_persistent_fits(ctx, d, M, S))
         return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "persistent blocks: unsupported shape (M=%lld S=%d)",
                         (long long)M, S);
@@ -1221,14 +1235,15 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
     prm.dp = st->chan[6];
     prm.err = st->err;
     prm.state = st->state;
+    prm.dump = dump;
     if (kNH * prm.nseg * prm.qb > kG)
         return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "persistent blocks: too many attention units");
     // All 256 workgroups wait on each other's words, so all must be resident: one per CU
     // (the LDS layout takes more than half of a CU's).  Every wait is bounded (kSpin
     // rounds, then the error word), so other work on the device can only turn a launch
-    // into an error, never a hang.  Launches on one stream run one after another; two
-    // models evaluating on different streams of one device at once could interleave their
-    // workgroups and end in that error (vxm_locdit_check / vxm_locenc_check report it).
+    // into an error, never a hang (vxm_locdit_check / vxm_locenc_check report it).  Eager
+    // launches are ordered after the device's previous single-launch kernel, whatever its
+    // stream (vxm_ordered_launch_begin), so two never interleave their workgroups.
 #ifdef VXM_PERSISTENT_TRACE
     // profiling build: timestamps of every eager launch into
     // $VXM_TRACE_DIR/ltrace_L<blocks>_M<rows>_<n>.bin (launches recorded into a graph run untraced)
@@ -1253,6 +1268,9 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
 #endif
     // row tiles of 16 as a template argument: the products' loops unroll completely
     const int mt = (int)((M + 15) / 16);
+    vxm_launch_slot *slot = nullptr;
+    bool capturing = false;
+    if (int rc = vxm_ordered_launch_begin(ctx, &slot, &capturing)) return rc;
 #define VXM_LP_LAUNCH(LS, MT)                                                                                \
     hipLaunchKernelGGL((k_locdit_persistent<LS, MT>), dim3(kG), dim3(kThreads), (unsigned)LS::BYTES, ctx->stream, prm)
     if (d.nkv == 16) {
@@ -1265,7 +1283,9 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
         else VXM_LP_LAUNCH(ShapeDitGqa, 3);
     }
 #undef VXM_LP_LAUNCH
-    VXM_CHECK_LAUNCH(ctx);
+    const hipError_t le = hipGetLastError();
+    if (int rc = vxm_ordered_launch_end(ctx, slot, capturing)) return rc;
+    if (le != hipSuccess) return vxm_fail(ctx, VXM_ERR_BACKEND, "persistent blocks launch failed: %s", hipGetErrorString(le));
 #ifdef VXM_PERSISTENT_TRACE
     if (traced) {
         std::vector<uint64_t> th((size_t)kG * tstride);
@@ -1287,9 +1307,9 @@ int vxm_locdit_persistent_check(vxm_ctx *ctx, vxm_lpersist *st) {
     if (!st || !st->err) return VXM_OK;
     int e = 0;
     VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    VXM_HIP(ctx, hipMemcpy(&e, st->err, 4, hipMemcpyDeviceToHost));
+    VXM_HIP(ctx, hipMemcpy(&e, st->err + 1, 4, hipMemcpyDeviceToHost));
     if (e) {
-        VXM_HIP(ctx, hipMemset(st->err, 0, 4));
+        VXM_HIP(ctx, hipMemset(st->err + 1, 0, 4));
         return vxm_fail(ctx, VXM_ERR_BACKEND, "persistent blocks: a workgroup timed out waiting for data");
     }
     return VXM_OK;

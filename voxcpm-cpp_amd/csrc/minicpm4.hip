@@ -387,6 +387,22 @@ extern "C" int vxm_minicpm4_check(vxm_minicpm4 *m) {
     return vxm_persistent_check(m);
 }
 
+extern "C" int vxm_minicpm4_set_layer_dump(vxm_minicpm4 *m, float *dump_dev) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    m->layer_dump = dump_dev;
+    return VXM_OK;
+}
+
+extern "C" int vxm_minicpm4_set_decode_epoch(vxm_minicpm4 *m, uint32_t epoch) {
+    if (!m) return VXM_ERR_INVALID_ARG;
+    return vxm_persistent_set_epoch(m, epoch);
+}
+
+extern "C" int vxm_minicpm4_decode_epoch(vxm_minicpm4 *m, uint32_t *epoch) {
+    if (!m || !epoch) return VXM_ERR_INVALID_ARG;
+    return vxm_persistent_get_epoch(m, epoch);
+}
+
 extern "C" int vxm_minicpm4_set_decode_mode(vxm_minicpm4 *m, int mode) {
     if (!m) return VXM_ERR_INVALID_ARG;
     if (mode < VXM_DECODE_AUTO || mode > VXM_DECODE_PERSISTENT)
@@ -444,7 +460,7 @@ extern "C" int vxm_minicpm4_forward(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x_
     if (n_tokens == 1 && m->decode_mode != VXM_DECODE_KERNELS) {
         const bool ok = vxm_persistent_supported(m, kv) && var == VXM_QUANT_X86;
         if (ok) {
-            if ((rc = vxm_persistent_decode(m, kv, x_dev, pos))) return rc;
+            if ((rc = vxm_persistent_decode(m, kv, x_dev, pos, m->layer_dump))) return rc;
             kv->n_used = pos + 1;
             return VXM_OK;
         }
@@ -459,11 +475,24 @@ extern "C" int vxm_minicpm4_forward(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x_
         if ((rc = vxm_launch_rmsnorm(ctx, x_dev, l ? m->ws.dn_out : vxm_parts{}, d.res_scale, b.g_in, n_tokens, d.H, d.eps,
                                      nullptr, m->ws.xq, m->ws.xd, var)))
             return rc;
+        // the norm added the previous layer's residual in place: x_dev is this layer's input
+        if (m->layer_dump)
+            VXM_HIP(ctx, hipMemcpyAsync(m->layer_dump + (size_t)l * n_tokens * d.H, x_dev,
+                                        (size_t)n_tokens * d.H * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
         vxm_attn_site site{kv->k(l), kv->v(l), kv->cap, 0, (int)n_tokens, pos, pos, 1};
         if ((rc = vxm_block_run(ctx, d, b, m->ws, x_dev, n_tokens, site))) return rc;
     }
     // last residual + final norm (in place), or the residual alone
-    if (m->final_norm) {
+    if (m->layer_dump && m->cfg.n_layers > 0) {
+        // debug: the residual alone first, so the last layer's output can be copied out
+        if ((rc = vxm_launch_residual(ctx, x_dev, m->ws.dn_out, d.res_scale, n_tokens * d.H))) return rc;
+        VXM_HIP(ctx, hipMemcpyAsync(m->layer_dump + (size_t)m->cfg.n_layers * n_tokens * d.H, x_dev,
+                                    (size_t)n_tokens * d.H * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
+        if (m->final_norm &&
+            (rc = vxm_launch_rmsnorm(ctx, x_dev, vxm_parts{}, 1.0f, m->final_norm, n_tokens, d.H, d.eps, x_dev, nullptr,
+                                     nullptr, var)))
+            return rc;
+    } else if (m->final_norm) {
         if ((rc = vxm_launch_rmsnorm(ctx, x_dev, m->ws.dn_out, d.res_scale, m->final_norm, n_tokens, d.H, d.eps, x_dev,
                                      nullptr, nullptr, var)))
             return rc;

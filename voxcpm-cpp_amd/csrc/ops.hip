@@ -21,9 +21,14 @@ __device__ __forceinline__ double block_sum_f64(double v, double *sh) {
     return t;
 }
 
-// The same for exact sums (squares of BF16 values: any order gives the same double):
-// each row of 16 lanes on DPP (xor 1, xor 2, half mirror, mirror), the wave's four
-// rows read back as scalars.  Every lane of the block must be active.
+// The same for sums of squares in a tree order (each row of 16 lanes on DPP: xor 1,
+// xor 2, half mirror, mirror; the wave's four rows read back as scalars).  Every lane
+// of the block must be active.  The squares of BF16 values have 16 significant
+// bits (of fp32 values, 24), so while a row's squares span less than about 2^26
+// (values within 2^13; fp32 values within 2^9) every partial sum of up to 2^11 of
+// them is exact in double and any order gives ggml's sequential double.  Beyond
+// that the tree and the sequential order can round the double differently, and
+// (float)(sum / n) can then differ by one ulp.
 __device__ __forceinline__ double block_sum_exact_f64(double v, double *sh) {
     auto dpp = [](double x, auto ctrl) {
         const long long b = __double_as_longlong(x);

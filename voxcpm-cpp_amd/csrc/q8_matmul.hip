@@ -371,10 +371,13 @@ struct GemmLds {
 __device__ __forceinline__ void gemm_finish(float (&acc)[2][16], float *red, int *last_sh, float *__restrict__ y,
                                             uint64_t *__restrict__ part, int *__restrict__ cnt, int M, int N,
                                             int m0, int n0, int tm, int tn, int tiles_n, int z, int splits,
-                                            uint32_t epoch, int *__restrict__ err) {
+                                            const uint32_t *__restrict__ epoch_p, int *__restrict__ err) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, kq = wave >> 1;
+    // the launch's split tag: a device word advanced before every split launch
+    // (a scalar load; a graph replay reads the value its own prepare step wrote)
+    const uint32_t epoch = splits > 1 ? *epoch_p : 0u;
     const int lr = lane & 31, lh = lane >> 5;
     // add the K quarters in order (quarter 0 + 1 + 2 + 3): every quarter hands its strips to
     // LDS, then quarter group kq finalizes result registers v = 4 kq .. 4 kq + 3 of both
@@ -484,7 +487,7 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
     const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd, const int8_t *__restrict__ wq,
     const uint16_t *__restrict__ wd, float *__restrict__ y, uint64_t *__restrict__ part, int *__restrict__ cnt,
     int32_t *__restrict__ dots, int M, int N, int K, int tiles_m, int tiles_n, int bps, int splits,
-    uint32_t epoch, int *__restrict__ err) {
+    const uint32_t *__restrict__ epoch_p, int *__restrict__ err) {
     static_assert(KS % 8 == 0, "a stage is a multiple of 8 blocks (64 KS scales per side = whole 512-thread rounds)");
     constexpr int ROW = GemmLds<KS>::ROW;
     constexpr int CH = KS / 4;                 // 16-byte chunks per thread per side and stage
@@ -624,7 +627,7 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
         __syncthreads();
     }
     if (DOTS) return;
-    gemm_finish(acc, (float *)&L, &last_sh, y, part, cnt, M, N, m0, n0, tm, tn, tiles_n, z, splits, epoch, err);
+    gemm_finish(acc, (float *)&L, &last_sh, y, part, cnt, M, N, m0, n0, tm, tn, tiles_n, z, splits, epoch_p, err);
 }
 
 // ---------------------------------------------------------------------------
@@ -773,7 +776,8 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd, const int8_t *__restrict__ wq,
     const uint16_t *__restrict__ wt, float *__restrict__ y, uint64_t *__restrict__ part, int *__restrict__ cnt,
     int32_t *__restrict__ dots, int M, int N, int K, int tiles_m, int tiles_n, int bps, int splits,
-    uint32_t epoch, int *__restrict__ err, int8_t *__restrict__ sq, uint16_t *__restrict__ sd, int variant,
+    const uint32_t *__restrict__ epoch_p, int *__restrict__ err, int8_t *__restrict__ sq, uint16_t *__restrict__ sd,
+    int variant,
     const vxm_qkv_epi qe) {
     using C = TileCfg<TN>;
     extern __shared__ __attribute__((aligned(16))) int8_t ring[];
@@ -996,6 +1000,8 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     // four neighbouring lanes = four neighbouring columns of one row: 16-byte LDS
     // reads and (N % 4 == 0, the usual case) 16-byte stores
     const int64_t MN = (int64_t)M * N;
+    // the launch's split tag (device word, advanced before every split launch)
+    const uint32_t epoch = splits > 1 ? *epoch_p : 0u;
     const bool vec = (N & 3) == 0 && splits == 1 && ((uintptr_t)y & 15) == 0;
 #pragma unroll 2
     for (int f = 4 * tid; f < PER; f += 4 * kTileThreads) {
@@ -1404,8 +1410,7 @@ static GemmPlan gemm_plan(vxm_ctx *ctx, int64_t M, int N, int nb) {
     p.tile_n = 0;
     p.ks = p.tiles_m == 1 ? 16 : 8;
     int s = 1;
-    // no split under graph capture: the split tags are per launch
-    while (!ctx->no_split_tags && s < kGemmMaxSplits && (int64_t)p.tiles_m * p.tiles_n * s < ctx->n_cu &&
+    while (s < kGemmMaxSplits && (int64_t)p.tiles_m * p.tiles_n * s < ctx->n_cu &&
            nb / (s * 2) >= 2 * p.ks)
         s *= 2;
     p.bps = (nb + s - 1) / s;
@@ -1435,7 +1440,7 @@ static bool tile_plan(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const
             const int bps = ((nb + s - 1) / s + 7) / 8 * 8;
             const int splits = (nb + bps - 1) / bps;
             if (bps > kTileMaxBps || splits != s) continue;
-            if (splits > 1 && (ctx->no_split_tags || (size_t)splits * M * N * sizeof(uint64_t) > max_split_bytes))
+            if (splits > 1 && (size_t)splits * M * N * sizeof(uint64_t) > max_split_bytes)
                 continue;
             const int tiles_m = (int)((M + GM - 1) / GM), tiles_n = (N + tn - 1) / tn;
             const int64_t wgs = (int64_t)tiles_m * tiles_n * splits, rounds = (wgs + ctx->n_cu - 1) / ctx->n_cu;
@@ -1458,7 +1463,7 @@ static bool tile_plan(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const
 // above the default limit: raise it once per device for each instantiation.
 template <int TN, bool DOTS>
 static int launch_gemm_tile_t(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
-                              float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, uint32_t epoch,
+                              float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, const uint32_t *epoch,
                               int8_t *sq, uint16_t *sd, int variant, const vxm_qkv_epi &qe) {
     static std::atomic<uint64_t> attr_done{0};
     const uint64_t bit = 1ull << (ctx->device & 63);
@@ -1481,7 +1486,7 @@ static int launch_gemm_tile_t(vxm_ctx *ctx, const vxm_weight *w, const int8_t *x
 // qe.q_out != nullptr: the QKV epilogue (k_rope_kv's work, one split) instead of y
 template <bool DOTS>
 static int launch_gemm_tile(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
-                            float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, uint32_t epoch,
+                            float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, const uint32_t *epoch,
                             int8_t *sq = nullptr, uint16_t *sd = nullptr, int variant = 0,
                             const vxm_qkv_epi &qe = vxm_qkv_epi{}) {
     return p.tile_n == 128
@@ -1491,7 +1496,7 @@ static int launch_gemm_tile(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq,
 
 template <int KS>
 static void launch_gemm_ks(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
-                           float *y, const GemmPlan &p, uint64_t *part, int *cnt, uint32_t epoch) {
+                           float *y, const GemmPlan &p, uint64_t *part, int *cnt, const uint32_t *epoch) {
     const int grid_x = 8 * p.tiles_m * ((p.tiles_n + 7) / 8);
     hipLaunchKernelGGL((k_gemm_q8_0_mfma<KS, false>), dim3(grid_x, p.splits), dim3(kGemmThreads), 0, ctx->stream,
                        xq, xd, w->qs, w->d, y, part, cnt, nullptr, (int)M, (int)w->n, (int)w->k, p.tiles_m,
@@ -1504,7 +1509,7 @@ static void launch_gemm_dots_ks(vxm_ctx *ctx, const vxm_weight *w, const int8_t 
     const int grid_x = 8 * p.tiles_m * ((p.tiles_n + 7) / 8);
     hipLaunchKernelGGL((k_gemm_q8_0_mfma<KS, true>), dim3(grid_x, p.splits), dim3(kGemmThreads), 0, ctx->stream,
                        xq, xd, w->qs, w->d, nullptr, nullptr, nullptr, dots, (int)M, (int)w->n, (int)w->k,
-                       p.tiles_m, p.tiles_n, p.bps, p.splits, 0u, ctx->dev_err);
+                       p.tiles_m, p.tiles_n, p.bps, p.splits, nullptr, ctx->dev_err);
 }
 
 // Buffer-load offsets are 32-bit: every row tile of A and W must lie below 2 GiB.
@@ -1522,12 +1527,26 @@ struct MmWork {
     size_t ncnt;
     float *parts;        // the small-M GEMM's K-split slices
     size_t parts_bytes;
-    std::atomic<uint32_t> *epoch;   // source of tags no earlier launch on these words used
+    uint32_t *epoch;     // device word: the tag of the last split launch on these words
 };
 
 __global__ void k_fill_zero(uint4 *__restrict__ p, int64_t n16) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
         p[i] = make_uint4(0, 0, 0, 0);
+}
+
+// Before every split launch: the next split tag into the device word *ep (0 is
+// skipped: the partial words start zeroed), and n16 16-byte words of arrival
+// counters cleared.  The tag lives in device memory, so a launch recorded into
+// a HIP graph reads a new tag on every replay: a replay can never take a word
+// that an earlier replay left for its own tag.
+__global__ void k_split_prepare(uint32_t *__restrict__ ep, uint4 *__restrict__ cnt, int64_t n16) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        const uint32_t e = *ep + 1u;
+        *ep = e ? e : 1u;
+    }
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
+        cnt[i] = make_uint4(0, 0, 0, 0);
 }
 
 static int launch_gemm(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
@@ -1536,13 +1555,16 @@ static int launch_gemm(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, cons
     if (!gemm_fits(M, N, K))
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "mul_mat: %lld x %d x %d exceeds the GEMM's 2 GiB operand range",
                         (long long)M, N, K);
+    // the same plan with or without a caller's workspace: a workspace too small
+    // for it is an error, never a silently different (unsplit) summation order
     GemmPlan p;
-    if (!tile_plan(ctx, w, xq, xd, M, wk ? wk->words_bytes : SIZE_MAX, p)) p = gemm_plan(ctx, M, N, nb);
+    if (!tile_plan(ctx, w, xq, xd, M, SIZE_MAX, p)) p = gemm_plan(ctx, M, N, nb);
     uint64_t *part = nullptr;
     int *cnt = nullptr;
-    uint32_t epoch = 0;
+    uint32_t *epoch = nullptr;
     if (p.splits > 1) {
         const size_t wbytes = (size_t)p.splits * M * N * sizeof(uint64_t), ncnt = (size_t)p.tiles_m * p.tiles_n;
+        int64_t n16 = 0;
         if (wk) {
             if (wbytes > wk->words_bytes || ncnt > wk->ncnt)
                 return vxm_fail(ctx, VXM_ERR_INVALID_ARG,
@@ -1551,21 +1573,18 @@ static int launch_gemm(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, cons
                                 (long long)M, N, K, wbytes, ncnt, wk->words_bytes, wk->ncnt);
             part = wk->words;
             cnt = wk->cnt;
-            do epoch = ++*wk->epoch;
-            while (epoch == 0);   // the words start zeroed: tag 0 is never live
+            epoch = wk->epoch;
             // the counters start this launch at zero whatever an earlier call left
-            const int64_t n16 = (int64_t)((ncnt * sizeof(int) + 15) / 16);
-            hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, ctx->stream,
-                               (uint4 *)cnt, n16);
+            n16 = (int64_t)((ncnt * sizeof(int) + 15) / 16);
         } else {
             int rc = vxm_ensure_split(ctx, wbytes, ncnt);
             if (rc) return rc;
             part = (uint64_t *)ctx->split_buf;
-            cnt = ctx->split_cnt;
-            // tag of this launch's partial words; the buffer starts zeroed, so 0 is never used
-            if (++ctx->split_epoch == 0) ctx->split_epoch = 1;
-            epoch = ctx->split_epoch;
+            cnt = ctx->split_cnt;   // zero between launches: the last workgroup of a tile resets its counter
+            epoch = ctx->split_epoch_dev;
         }
+        hipLaunchKernelGGL(k_split_prepare, dim3((unsigned)(n16 > 0 ? (n16 + 255) / 256 : 1)), dim3(256), 0,
+                           ctx->stream, epoch, (uint4 *)cnt, n16);
         ctx->split_launched = true;
     }
     if (p.tile_n) {
@@ -1707,7 +1726,7 @@ bool vxm_launch_gate_up_swiglu(vxm_ctx *ctx, const vxm_weight *w, const int8_t *
     } else {
         GemmPlan p;
         if (!tile_plan(ctx, w, xq, xd, M, 0, p) || p.splits != 1) return false;
-        if ((*rc = launch_gemm_tile<false>(ctx, w, xq, xd, M, nullptr, nullptr, p, nullptr, nullptr, 0u, sq, sd,
+        if ((*rc = launch_gemm_tile<false>(ctx, w, xq, xd, M, nullptr, nullptr, p, nullptr, nullptr, nullptr, sq, sd,
                                            variant)))
             return true;
     }
@@ -1736,7 +1755,7 @@ bool vxm_launch_qkv_rope(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, co
                        (long long)(qe.pos0 + std::min<int64_t>(M, qe.S)));
         return true;
     }
-    if ((*rc = launch_gemm_tile<false>(ctx, w, xq, xd, M, nullptr, nullptr, p, nullptr, nullptr, 0u, nullptr, nullptr,
+    if ((*rc = launch_gemm_tile<false>(ctx, w, xq, xd, M, nullptr, nullptr, p, nullptr, nullptr, nullptr, nullptr, nullptr,
                                        0, qe)))
         return true;
     if (hipGetLastError() != hipSuccess) *rc = vxm_fail(ctx, VXM_ERR_BACKEND, "QKV + rope launch failed");
@@ -1819,7 +1838,7 @@ static int launch_block_dots(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq
             GemmPlan p;
             if (!tile_plan(ctx, w, xq, xd, M, SIZE_MAX, p)) p = gemm_plan(ctx, M, N, K / 32);
             if (p.tile_n) {
-                int rc = launch_gemm_tile<true>(ctx, w, xq, xd, M, nullptr, out, p, nullptr, nullptr, 0u);
+                int rc = launch_gemm_tile<true>(ctx, w, xq, xd, M, nullptr, out, p, nullptr, nullptr, nullptr);
                 if (rc) return rc;
             } else if (p.ks == 16) {
                 launch_gemm_dots_ks<16>(ctx, w, xq, xd, M, out, p);
@@ -1892,8 +1911,10 @@ extern "C" int vxm_block_dots_q8_0(vxm_ctx *ctx, const vxm_weight *w, const int8
 // vxm_mul_mat_q8_0_noalloc runs the kernels of vxm_mul_mat_q8_0, with the same
 // plans, but takes every buffer beyond x and y from `scratch`, a file-scope
 // device array that the code object carries: no call allocates.  Layout:
-//   [0, kScrCnt)                 per-tile arrival counters of the tiled GEMM's
+//   [0, kScrCnt - 256)           per-tile arrival counters of the tiled GEMM's
 //                                K splits (zeroed by each call that splits)
+//   [kScrCnt - 256, kScrCnt)     the split tag word (advanced on the device
+//                                before each split launch)
 //   [kScrCnt, +kScrWords)        its tagged partial words, and nothing else, so
 //                                no leftover of another use can carry a live tag
 //   [kScrCnt + kScrWords, end)   the quantized activation, then the small-M
@@ -1906,11 +1927,10 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 // The device address of `scratch` on each device (the host-side name is a
 // stand-in, never a device address), set once per device with that device
-// current, and each device's tag source for the split words.
+// current.
 constexpr int kScrMaxDev = 64;
 static std::mutex g_scr_mu;
 static unsigned char *g_scr_ptr[kScrMaxDev];
-static std::atomic<uint32_t> g_scr_epoch[kScrMaxDev];
 
 int vxm_scratch_setup(vxm_ctx *ctx) {
     ctx->scratch = nullptr;
@@ -1959,8 +1979,9 @@ extern "C" int vxm_mul_mat_q8_0_noalloc(vxm_ctx *ctx, const vxm_weight *w, const
     unsigned char *gen = base + kScrCnt + kScrWords;
     int8_t *xq = (int8_t *)gen;
     uint16_t *xd = (uint16_t *)(gen + qbytes);
-    const MmWork wk{(uint64_t *)(base + kScrCnt), kScrWords, (int *)base, kScrCnt / sizeof(int),
-                    (float *)(gen + abytes), kScrGeneral - abytes, &g_scr_epoch[ctx->device]};
+    // the last 256 bytes of the counter region hold the split tag word
+    const MmWork wk{(uint64_t *)(base + kScrCnt), kScrWords, (int *)base, (kScrCnt - 256) / sizeof(int),
+                    (float *)(gen + abytes), kScrGeneral - abytes, (uint32_t *)(base + kScrCnt - 256)};
     rc = vxm_launch_quantize(ctx, x_dev, M, K, ctx->quant_variant, xq, xd);
     if (rc) return rc;
     return launch_mul_mat(ctx, w, xq, xd, M, y_dev, &wk);

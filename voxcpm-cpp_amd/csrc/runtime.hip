@@ -3,7 +3,9 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include "vxm_internal.h"
+#include <mutex>
+
+#include "vxm_model.h"
 
 int vxm_fail(vxm_ctx *ctx, int code, const char *fmt, ...) {
     char buf[512];
@@ -62,6 +64,7 @@ extern "C" int vxm_open(int device, vxm_ctx **out) {
         g_open_err = "device error word allocation failed";
         return VXM_ERR_BACKEND;
     }
+    ctx->split_epoch_dev = (uint32_t *)((char *)ctx->dev_err + 64);   // zero: no split launched yet
     vxm_scratch_setup(ctx);   // a failure is reported by the allocation-free entry only
     *out = ctx;
     return VXM_OK;
@@ -120,6 +123,123 @@ extern "C" int vxm_set_path(vxm_ctx *ctx, int path) {
     return VXM_OK;
 }
 
+static bool capturing(vxm_ctx *ctx) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return st != hipStreamCaptureStatusNone;
+}
+
+// A scratch buffer that must grow cannot be replaced under graph capture (the
+// free and the allocation would synchronise the stream being recorded).
+#define VXM_NO_GROWTH_UNDER_CAPTURE(ctx, what, bytes)                                                    \
+    do {                                                                                                 \
+        if (capturing(ctx))                                                                              \
+            return vxm_fail((ctx), VXM_ERR_INVALID_ARG,                                                  \
+                            "%s of %zu bytes would have to grow under graph capture: run the sequence " \
+                            "once before capturing it",                                                  \
+                            (what), (size_t)(bytes));                                                    \
+    } while (0)
+
+// ---- one launch order per device for the single-launch kernels --------------
+
+struct vxm_launch_slot {
+    std::mutex mu;
+    hipEvent_t ev = nullptr;
+    hipStream_t last = nullptr;
+};
+static vxm_launch_slot g_launch_slots[64];
+
+// Holds the device's slot from begin to end (the launch goes in between).
+int vxm_ordered_launch_begin(vxm_ctx *ctx, vxm_launch_slot **slot, bool *cap) {
+    *slot = nullptr;
+    *cap = false;
+    if (ctx->device < 0 || ctx->device >= 64)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "single-launch kernel: device %d beyond the launch table",
+                        ctx->device);
+    *cap = capturing(ctx);
+    vxm_launch_slot &o = g_launch_slots[ctx->device];
+    o.mu.lock();
+    *slot = &o;
+    if (*cap) return VXM_OK;
+    hipError_t e = hipSuccess;
+    if (!o.ev) e = hipEventCreateWithFlags(&o.ev, hipEventDisableTiming);
+    if (e == hipSuccess && o.last && o.last != ctx->stream) e = hipStreamWaitEvent(ctx->stream, o.ev, 0);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        o.mu.unlock();
+        *slot = nullptr;
+        return vxm_fail(ctx, VXM_ERR_BACKEND, "single-launch kernel: launch ordering failed: %s", hipGetErrorString(e));
+    }
+    return VXM_OK;
+}
+
+int vxm_ordered_launch_end(vxm_ctx *ctx, vxm_launch_slot *slot, bool cap) {
+    if (!slot) return VXM_OK;
+    int rc = VXM_OK;
+    if (!cap) {
+        const hipError_t e = hipEventRecord(slot->ev, ctx->stream);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            rc = vxm_fail(ctx, VXM_ERR_BACKEND, "single-launch kernel: ordering event failed: %s", hipGetErrorString(e));
+        } else {
+            slot->last = ctx->stream;
+        }
+    }
+    slot->mu.unlock();
+    return rc;
+}
+
+// ---- graph capture of the context's stream ---------------------------------
+struct vxm_graph {
+    hipGraphExec_t exec = nullptr;
+    int device = 0;
+};
+
+extern "C" int vxm_capture_begin(vxm_ctx *ctx) {
+    if (!ctx) return VXM_ERR_INVALID_ARG;
+    if (capturing(ctx)) return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "capture_begin: the stream is already capturing");
+    VXM_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    return VXM_OK;
+}
+
+extern "C" int vxm_capture_end(vxm_ctx *ctx, vxm_graph **out) {
+    if (!ctx || !out) return VXM_ERR_INVALID_ARG;
+    *out = nullptr;
+    hipGraph_t graph = nullptr;
+    VXM_HIP(ctx, hipStreamEndCapture(ctx->stream, &graph));
+    if (!graph) return vxm_fail(ctx, VXM_ERR_BACKEND, "capture_end: the capture recorded no graph");
+    vxm_graph *g = new vxm_graph();
+    g->device = ctx->device;
+    const hipError_t e = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        delete g;
+        return vxm_fail(ctx, VXM_ERR_BACKEND, "capture_end: graph instantiation failed: %s", hipGetErrorString(e));
+    }
+    *out = g;
+    return VXM_OK;
+}
+
+extern "C" int vxm_graph_launch(vxm_ctx *ctx, const vxm_graph *g) {
+    if (!ctx || !g || !g->exec) return VXM_ERR_INVALID_ARG;
+    if (g->device != ctx->device)
+        return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "graph_launch: graph of device %d on a context of device %d",
+                        g->device, ctx->device);
+    VXM_HIP(ctx, hipGraphLaunch(g->exec, ctx->stream));
+    return VXM_OK;
+}
+
+extern "C" int vxm_graph_free(vxm_graph *g) {
+    if (!g) return VXM_OK;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    delete g;
+    return VXM_OK;
+}
+
 extern "C" int vxm_malloc(vxm_ctx *ctx, size_t bytes, void **out_dev) {
     if (!ctx || !out_dev) return VXM_ERR_INVALID_ARG;
     *out_dev = nullptr;
@@ -153,6 +273,7 @@ extern "C" int vxm_memcpy_d2h(vxm_ctx *ctx, void *dst_host, const void *src_dev,
 
 int vxm_ensure_act(vxm_ctx *ctx, size_t bytes) {
     if (ctx->act_bytes >= bytes) return VXM_OK;
+    VXM_NO_GROWTH_UNDER_CAPTURE(ctx, "activation scratch", bytes);
     VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     if (ctx->act_buf) VXM_HIP(ctx, hipFree(ctx->act_buf));
     ctx->act_buf = nullptr;
@@ -168,6 +289,7 @@ int vxm_ensure_act(vxm_ctx *ctx, size_t bytes) {
 
 int vxm_ensure_parts(vxm_ctx *ctx, size_t bytes) {
     if (ctx->parts_bytes >= bytes) return VXM_OK;
+    VXM_NO_GROWTH_UNDER_CAPTURE(ctx, "GEMM slice scratch", bytes);
     VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     if (ctx->parts_buf) VXM_HIP(ctx, hipFree(ctx->parts_buf));
     ctx->parts_buf = nullptr;
@@ -181,6 +303,8 @@ int vxm_ensure_parts(vxm_ctx *ctx, size_t bytes) {
 }
 
 int vxm_ensure_split(vxm_ctx *ctx, size_t bytes, size_t n_counters) {
+    if (ctx->split_bytes < bytes || ctx->split_ncnt < n_counters)
+        VXM_NO_GROWTH_UNDER_CAPTURE(ctx, "GEMM split scratch", bytes);
     if (ctx->split_bytes < bytes) {
         VXM_HIP(ctx, hipStreamSynchronize(ctx->stream));
         if (ctx->split_buf) VXM_HIP(ctx, hipFree(ctx->split_buf));

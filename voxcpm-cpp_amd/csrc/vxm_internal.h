@@ -28,7 +28,9 @@ struct vxm_ctx {
     size_t split_bytes = 0;
     int *split_cnt = nullptr;
     size_t split_ncnt = 0;
-    uint32_t split_epoch = 0;   // tag of the last split launch's partial words
+    // device word (in the error buffer) holding the tag of the last split
+    // launch's partial words, advanced on the device before each split launch
+    uint32_t *split_epoch_dev = nullptr;
     // device error word: set by a split fix-up whose partial words never
     // arrived (its output is NaN); vxm_sync reports and clears it
     int *dev_err = nullptr;
@@ -36,11 +38,6 @@ struct vxm_ctx {
     // K-split slices of the small-M GEMM behind the public matmul entries
     void *parts_buf = nullptr;
     size_t parts_bytes = 0;
-    // set around the CFM Euler loop, eager or captured into a HIP graph: the
-    // tiled GEMM takes no K split there, because its split tags are per launch
-    // (a graph would replay stale tags) and an eager run must add in the same
-    // order as the replays
-    bool no_split_tags = false;
     // this device's copy of the allocation-free matmul's scratch array (its
     // device address), or null with the reason in scratch_err
     unsigned char *scratch = nullptr;

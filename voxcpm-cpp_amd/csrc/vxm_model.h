@@ -73,13 +73,18 @@ struct vxm_minicpm4 {
     vxm_workspace ws;
     int decode_mode = VXM_DECODE_AUTO;
     vxm_persistent_state *pstate = nullptr;
+    // debug: every forward writes the input of each layer and the last layer's
+    // output before the final norm here, [n_layers + 1][n_tokens][H] (null: off)
+    float *layer_dump = nullptr;
 };
 
 // persistent single-launch decode (decode_persistent.hip)
 bool vxm_persistent_supported(const vxm_minicpm4 *m, const vxm_kv_cache *kv);
 int vxm_persistent_max_cap(const vxm_block_dims &d);
-int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t pos);
+int vxm_persistent_decode(vxm_minicpm4 *m, vxm_kv_cache *kv, float *x, int32_t pos, float *dump);
 int vxm_persistent_check(vxm_minicpm4 *m);
+int vxm_persistent_set_epoch(vxm_minicpm4 *m, uint32_t epoch);
+int vxm_persistent_get_epoch(vxm_minicpm4 *m, uint32_t *epoch);
 void vxm_persistent_free(vxm_minicpm4 *m);
 
 int vxm_ws_ensure(vxm_ctx *ctx, vxm_workspace &ws, int64_t M, int64_t H, int64_t qd, int64_t kvd, int64_t F,
@@ -101,7 +106,19 @@ struct vxm_lpersist;
 bool vxm_locdit_persistent_fits(vxm_ctx *ctx, const vxm_block_dims &d, int64_t M, int S);
 // the block strategy (VXM_DECODE_*) resolved for one evaluation: true = the single launch
 bool vxm_locdit_persistent_pick(vxm_ctx *ctx, const vxm_block_dims &d, int64_t M, int S, int mode);
+// dump (debug, or null): [L + 1][M][H], the rows entering every block and the last block's output
 int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::vector<vxm_block> &blocks,
-                              vxm_lpersist **st, float *x, int64_t M, int S);
+                              vxm_lpersist **st, float *x, int64_t M, int S, float *dump);
 int vxm_locdit_persistent_check(vxm_ctx *ctx, vxm_lpersist *st);
 void vxm_locdit_persistent_free(vxm_lpersist *st);
+
+// Every single-launch kernel (the decode, the LocDiT / LocEnc blocks) needs all
+// 256 workgroups resident at once.  Two such launches on different streams of
+// one device could interleave their workgroups and wait on each other until the
+// bounded waits give up, so each eager launch is ordered after the previous one
+// on its device (one event per device, waited on when the stream changes).
+// Launches recorded into a HIP graph are not ordered this way: replays must not
+// overlap another stream's single-launch work on the device.
+struct vxm_launch_slot;
+int vxm_ordered_launch_begin(vxm_ctx *ctx, vxm_launch_slot **slot, bool *capturing);
+int vxm_ordered_launch_end(vxm_ctx *ctx, vxm_launch_slot *slot, bool capturing);

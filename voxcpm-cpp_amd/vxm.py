@@ -64,6 +64,10 @@ _SIGS = {
     "vxm_last_error": (C.c_char_p, [_P]),
     "vxm_set_quant_variant": (_I, [_P, _I]),
     "vxm_set_path": (_I, [_P, _I]),
+    "vxm_capture_begin": (_I, [_P]),
+    "vxm_capture_end": (_I, [_P, C.POINTER(_P)]),
+    "vxm_graph_launch": (_I, [_P, _P]),
+    "vxm_graph_free": (_I, [_P]),
     "vxm_malloc": (_I, [_P, C.c_size_t, C.POINTER(_P)]),
     "vxm_free": (_I, [_P, _P]),
     "vxm_memcpy_h2d": (_I, [_P, _P, _P, C.c_size_t]),
@@ -95,6 +99,11 @@ _SIGS = {
     "vxm_minicpm4_forward": (_I, [_P, _P, _P, _I64, C.c_int32]),
     "vxm_minicpm4_set_decode_mode": (_I, [_P, _I]),
     "vxm_minicpm4_check": (_I, [_P]),
+    "vxm_minicpm4_set_layer_dump": (_I, [_P, _P]),
+    "vxm_minicpm4_set_decode_epoch": (_I, [_P, C.c_uint32]),
+    "vxm_minicpm4_decode_epoch": (_I, [_P, C.POINTER(C.c_uint32)]),
+    "vxm_locdit_set_block_dump": (_I, [_P, _P]),
+    "vxm_locenc_set_block_dump": (_I, [_P, _P]),
     "vxm_host_quantize_q8_0": (_I, [_P, _I64, _I64, _P]),
     "vxm_host_randn": (_I, [_U64, _U64, _I64, _F, _F, _P]),
     "vxm_locdit_create": (_I, [_P, _P, _P, C.POINTER(_P)]),
@@ -170,6 +179,21 @@ def _ptr(t):
     return C.c_void_p(int(t))
 
 
+class Graph:
+    """A recorded sequence of calls on a context (vxm_capture_end)."""
+
+    def __init__(self, ctx, h):
+        self.ctx, self.h = ctx, h
+
+    def launch(self):
+        self.ctx.check(lib().vxm_graph_launch(self.ctx.h, self.h))
+
+    def free(self):
+        if self.h:
+            lib().vxm_graph_free(self.h)
+            self.h = None
+
+
 class Context:
     """One device + one stream (vxm_open); closes on ``close()``."""
 
@@ -215,6 +239,16 @@ class Context:
 
     def set_quant_variant(self, v):
         self.check(lib().vxm_set_quant_variant(self.h, v))
+
+    # ---- HIP graph capture of the context's stream ----
+    def capture_begin(self):
+        self.check(lib().vxm_capture_begin(self.h))
+
+    def capture_end(self):
+        """End the capture; returns a Graph that replays the recorded calls."""
+        h = C.c_void_p()
+        self.check(lib().vxm_capture_end(self.h, C.byref(h)))
+        return Graph(self, h)
 
     def set_path(self, p):
         self.check(lib().vxm_set_path(self.h, p))
@@ -451,6 +485,20 @@ class MiniCPM4:
         """Sync and raise if a persistent decode launch failed on the device."""
         self.ctx.check(lib().vxm_minicpm4_check(self.h))
 
+    def set_layer_dump(self, dump):
+        """Debug: every forward writes each layer's input and the last layer's output
+        (before the final norm) to dump, fp32 [n_layers + 1][n_tokens][hidden]; None: off."""
+        self.ctx.check(lib().vxm_minicpm4_set_layer_dump(self.h, _ptr(dump)))
+
+    def set_decode_epoch(self, epoch):
+        """Test hook: the tag epoch of the next single-launch decode (1 .. 2^20 - 1)."""
+        self.ctx.check(lib().vxm_minicpm4_set_decode_epoch(self.h, epoch))
+
+    def decode_epoch(self):
+        e = C.c_uint32()
+        self.ctx.check(lib().vxm_minicpm4_decode_epoch(self.h, C.byref(e)))
+        return e.value
+
     def forward(self, kv, x, pos):
         self.ctx.check(lib().vxm_minicpm4_forward(self.h, kv.h, _ptr(x), x.shape[0], pos))
         return x
@@ -550,6 +598,11 @@ class LocDiT:
     def check(self):
         """Synchronise; raise if a persistent block launch timed out on the device."""
         self.ctx.check(lib().vxm_locdit_check(self.h))
+
+    def set_block_dump(self, dump):
+        """Debug: each evaluation writes the rows entering every block and the last block's
+        output to dump, fp32 [n_layers + 1][rows][hidden]; None: off."""
+        self.ctx.check(lib().vxm_locdit_set_block_dump(self.h, _ptr(dump)))
 
     def free(self):
         if self.h:
@@ -714,6 +767,10 @@ class LocEnc:
     def check(self):
         """Synchronise; raise if a persistent block launch timed out on the device."""
         self.ctx.check(lib().vxm_locenc_check(self.h))
+
+    def set_block_dump(self, dump):
+        """Debug: as LocDiT.set_block_dump for the P + 1 encoder rows."""
+        self.ctx.check(lib().vxm_locenc_set_block_dump(self.h, _ptr(dump)))
 
     def free(self):
         if self.h:
