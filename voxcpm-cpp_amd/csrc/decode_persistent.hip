@@ -105,11 +105,20 @@ constexpr int kWaves = 8;              // waves per workgroup: 1 reader + 7 comp
 constexpr int kXReaders = VXM_X_READERS, kAttReaders = VXM_ATT_READERS, kPReaders = VXM_P_READERS;
 constexpr int kH1Readers = VXM_H1_READERS;
 
-constexpr int kCW = kWaves - 1;
+// Waves 0 .. kNR-1 issue no weight loads (their exchange reads never wait behind
+// a refill); the others stream weights through the ring and compute.
+#ifndef VXM_NREADERS
+#define VXM_NREADERS 1
+#endif
+constexpr int kNR = VXM_NREADERS;
+constexpr int kCW = kWaves - kNR;
 constexpr int kThreads = kWaves * 64;
 constexpr int kG = 256;                // workgroups: one per CU
 constexpr int kSpin = 1 << 17;         // poll rounds before giving up
-constexpr int kLook = 7;               // 2 KiB weight units in the LDS ring per compute wave
+#ifndef VXM_LOOK
+#define VXM_LOOK 7
+#endif
+constexpr int kLook = VXM_LOOK;        // 2 KiB weight units in the LDS ring per compute wave
 constexpr int kUnit = 2048;            // quant bytes per unit (64 blocks)
 constexpr int kSlot = kUnit + 128;     // LDS bytes per ring slot: quants, then 64 fp16 scales
 // Every channel is written as kRep replicas; workgroup b reads replica
@@ -423,41 +432,57 @@ __device__ __forceinline__ bool give_up(const vxm_pparams &p, int &it, int *bail
     return false;
 }
 
-// Wave 0: read the n tagged words src[0..n) (lane l owns words l + 64k, all
-// loads of a round in flight) into LDS: PAIRS unpacks two BF16 values per
-// word to dst[2i], dst[2i+1], otherwise one fp32 to dst[i].  Words whose tag
-// is not yet `tag` are read again next round.  Returns this lane's sum of
-// the squares of its values in double (each square exact for BF16-valued inputs).
-template <int NPL, bool PAIRS, bool RAW = false>
-__device__ double read_words(const vxm_pparams &p, const uint64_t *src, int n, uint32_t tag, float *dst, int *bail) {
-    static_assert(NPL <= 64, "words per lane");
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// A channel replica as a buffer resource; 16-byte loads through it carry the sc1
+// bit (aux 16), so, like agent-scope atomic loads, they bypass the non-coherent
+// caches.  Each 8-byte half of a load is one word written by one 64-bit atomic
+// store, so each half is whole; the two halves are checked separately.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t chan_rsrc(const uint64_t *base, int words) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, words * 8, 0x00020000);
+}
+__device__ __forceinline__ v4u load_pair(__amdgpu_buffer_rsrc_t rs, int pair) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rs, pair * 16, 0, 16);
+}
+
+// One reading wave: the np word pairs src[2i], src[2i + 1] (i < np; lane l owns
+// pairs l + 64k, all loads of a round in flight, 16 bytes each) into LDS:
+// PAIRS unpacks the four BF16 values of a pair to dst[4i .. 4i + 3], RAW stores
+// the two BF16 pairs as they are, otherwise two fp32 to dst[2i], dst[2i + 1].
+// Pairs not yet carrying `tag` in both words are read again next round.
+// Returns this lane's sum of the squares of its values in double (each square
+// exact for BF16-valued inputs).
+template <int NPP, bool PAIRS, bool RAW = false>
+__device__ double read_words(const vxm_pparams &p, const uint64_t *src, int np, uint32_t tag, float *dst, int *bail) {
+    static_assert(NPP <= 32, "pairs per lane");
     const int lane = tid_now() & 63;
-    uint64_t pending = 0;
+    const __amdgpu_buffer_rsrc_t rs = chan_rsrc(src, 2 * np);
+    uint32_t pending = 0;
 #pragma unroll
-    for (int k = 0; k < NPL; k++)
-        if (lane + 64 * k < n) pending |= 1ull << k;
+    for (int k = 0; k < NPP; k++)
+        if (lane + 64 * k < np) pending |= 1u << k;
     double ss = 0.0;
     int it = 0;
     while (true) {
-        uint64_t w[NPL];
+        v4u w[NPP];
 #pragma unroll
-        for (int k = 0; k < NPL; k++)
-            if (pending & (1ull << k)) w[k] = get_word(src + lane + 64 * k);
+        for (int k = 0; k < NPP; k++)
+            if (pending & (1u << k)) w[k] = load_pair(rs, lane + 64 * k);
 #pragma unroll
-        for (int k = 0; k < NPL; k++) {
-            if ((pending & (1ull << k)) && (uint32_t)(w[k] >> 32) == tag) {
-                const uint32_t v = (uint32_t)w[k];
+        for (int k = 0; k < NPP; k++) {
+            if ((pending & (1u << k)) && w[k].y == tag && w[k].w == tag) {
                 const int i = lane + 64 * k;
                 if (RAW) {
-                    ((uint32_t *)dst)[i] = v;   // the BF16 pair as is
+                    *(uint2 *)(dst + 2 * i) = make_uint2(w[k].x, w[k].z);   // the BF16 pairs as they are
                 } else if (PAIRS) {
-                    const float a = __uint_as_float(v << 16), b = __uint_as_float(v & 0xffff0000u);
-                    *(float2 *)(dst + 2 * i) = make_float2(a, b);
-                    ss += (double)(a * a) + (double)(b * b);
+                    const float a0 = __uint_as_float(w[k].x << 16), b0 = __uint_as_float(w[k].x & 0xffff0000u);
+                    const float a1 = __uint_as_float(w[k].z << 16), b1 = __uint_as_float(w[k].z & 0xffff0000u);
+                    *(float4 *)(dst + 4 * i) = make_float4(a0, b0, a1, b1);
+                    ss += ((double)(a0 * a0) + (double)(b0 * b0)) + ((double)(a1 * a1) + (double)(b1 * b1));
                 } else {
-                    dst[i] = __uint_as_float(v);
+                    *(float2 *)(dst + 2 * i) = make_float2(__uint_as_float(w[k].x), __uint_as_float(w[k].z));
                 }
-                pending &= ~(1ull << k);
+                pending &= ~(1u << k);
             }
         }
         if (__all(pending == 0)) break;
@@ -467,32 +492,32 @@ __device__ double read_words(const vxm_pparams &p, const uint64_t *src, int n, u
     return ss;
 }
 
-// Words [i0, i0 + n) of a Q8_0 channel: words below nq hold four quants each
-// (stored to xq as they are), the words from nq on one block scale each (to
-// xd[i - nq]).  Polls until every word carries tag.
-template <int NPL>
-__device__ void read_q8_words(const vxm_pparams &p, const uint64_t *src, int i0, int n, int nq, uint32_t tag,
+// Word pairs [p0, p0 + np) of a Q8_0 channel (16-byte loads): words below nq
+// (even) hold four quants each (stored to xq as they are), the words from nq on
+// one block scale each (to xd[i - nq]).  Polls until every word carries tag.
+template <int NPP>
+__device__ void read_q8_words(const vxm_pparams &p, const uint64_t *src, int p0, int np, int nq, uint32_t tag,
                               int8_t *xq, float *xd, int *bail) {
-    static_assert(NPL <= 64, "words per lane");
+    static_assert(NPP <= 32, "pairs per lane");
     const int lane = tid_now() & 63;
-    uint64_t pending = 0;
+    const __amdgpu_buffer_rsrc_t rs = chan_rsrc(src, 2 * (p0 + np));
+    uint32_t pending = 0;
 #pragma unroll
-    for (int k = 0; k < NPL; k++)
-        if (lane + 64 * k < n) pending |= 1ull << k;
+    for (int k = 0; k < NPP; k++)
+        if (lane + 64 * k < np) pending |= 1u << k;
     int it = 0;
     while (true) {
-        uint64_t w[NPL];
+        v4u w[NPP];
 #pragma unroll
-        for (int k = 0; k < NPL; k++)
-            if (pending & (1ull << k)) w[k] = get_word(src + i0 + lane + 64 * k);
+        for (int k = 0; k < NPP; k++)
+            if (pending & (1u << k)) w[k] = load_pair(rs, p0 + lane + 64 * k);
 #pragma unroll
-        for (int k = 0; k < NPL; k++) {
-            if ((pending & (1ull << k)) && (uint32_t)(w[k] >> 32) == tag) {
-                const uint32_t v = (uint32_t)w[k];
-                const int i = i0 + lane + 64 * k;
-                if (i < nq) ((uint32_t *)xq)[i] = v;
-                else xd[i - nq] = __uint_as_float(v);
-                pending &= ~(1ull << k);
+        for (int k = 0; k < NPP; k++) {
+            if ((pending & (1u << k)) && w[k].y == tag && w[k].w == tag) {
+                const int i = 2 * (p0 + lane + 64 * k);
+                if (i < nq) *(uint2 *)(xq + 4 * i) = make_uint2(w[k].x, w[k].z);
+                else *(float2 *)(xd + i - nq) = make_float2(__uint_as_float(w[k].x), __uint_as_float(w[k].z));
+                pending &= ~(1u << k);
             }
         }
         if (__all(pending == 0)) break;
@@ -882,14 +907,24 @@ __device__ __forceinline__ void ring_refill(const vxm_pparams &p, const UnitBase
     }
 }
 
-// Attention of query head h for layer l (vcpm_attention's gqa_group_attn,
-// src/minicpm4.c:232-248): wave 0 reads q_h, k_g, v_g; all waves then read
-// the f16 cache rows [0, pos) of group g, use the fresh k, v for row pos,
-// and publish the 128 fp32 outputs.  The group's first head appends k, v.
-// K or V rows of one attention batch: lane (kin, sub) of wave w loads dims
-// sub*8..+8 of key jb + (k * kWaves + w) * KPW + kin for k < KB; keys at or
-// past lim (the current token, which comes from LDS, or the chunk's end)
-// load nothing.
+// Rows of one attention batch into registers.  K: lane (kin, sub) of wave w
+// loads dims sub*16 .. +16 (two 16-byte loads) of key jb + (k * kWaves + w) * 8
+// + kin, k < KBK: eight lanes per key, so a score is 8 v_dot2 and three DPP
+// steps.  V: dims sub*8 .. +8 (one load) of key jb + (k * kWaves + w) * 4 + kin,
+// k < KB, sixteen lanes per key.  Keys at or past lim (the current token, which
+// comes from LDS, or the chunk's end) load nothing.
+template <int KBK, int HD>
+__device__ __forceinline__ void attn_load_k(const uint16_t *base, int jb, int lim, uint4 (&r)[KBK][2]) {
+    static_assert(HD == 128, "eight lanes of 16 dims per key");
+    const int tid = tid_now(), wave = tid >> 6, lane = tid & 63, sub = lane & 7, kin = lane >> 3;
+#pragma unroll
+    for (int k = 0; k < KBK; k++) {
+        const int j = jb + (k * kWaves + wave) * 8 + kin;
+        const uint4 *src = (const uint4 *)(base + (int64_t)j * HD + sub * 16);
+        r[k][0] = j < lim ? src[0] : make_uint4(0, 0, 0, 0);
+        r[k][1] = j < lim ? src[1] : make_uint4(0, 0, 0, 0);
+    }
+}
 template <int KB, int HD>
 __device__ __forceinline__ void attn_load(const uint16_t *base, int jb, int lim, uint4 (&r)[KB]) {
     constexpr int LPK = HD / 8, KPW = 64 / LPK;
@@ -901,12 +936,38 @@ __device__ __forceinline__ void attn_load(const uint16_t *base, int jb, int lim,
     }
 }
 
+// the sum over each aligned group of 8 lanes, the same bits in all 8 (each step
+// adds the same two values in either order)
+__device__ __forceinline__ float sum8_all(float v) {
+    v = v + dpp_f<kDppXor1>(v);
+    v = v + dpp_f<kDppXor2>(v);
+    return v + dpp_f<kDppMirror8>(v);
+}
+
+// q . k for eight lanes of 16 dims: v_dot2_f32_f16 on f16 pairs (the BF16-valued q
+// and the f16 cache are exact in f16, the products exact in f32; only the
+// summation order differs from a sequential fp32 dot product)
+__device__ __forceinline__ float score8(const half2_t (&q2)[8], const uint4 (&kr)[2]) {
+    const uint32_t w[8] = {kr[0].x, kr[0].y, kr[0].z, kr[0].w, kr[1].x, kr[1].y, kr[1].z, kr[1].w};
+    float pt = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) pt = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w[i]), q2[i], pt, false);
+    return sum8_all(pt);
+}
+
 // Attention of query head h for layer l (vcpm_attention's gqa_group_attn,
 // src/minicpm4.c:232-248).  The cached K and V rows [0, pos) do not depend
 // on this layer's projections, so every wave issues its loads of the first
 // batch (up to 320 keys) before wave 0 reads q_h, k_g, v_g: the cache fetch
 // overlaps the QKV exchange.  The current token's k, v come from LDS; the
 // group's first head appends them to the cache.  Output: 128 fp32.
+//
+// Softmax in three barriers: the scores (scaled) go to LDS with each wave's
+// max, the exponentials replace them with each wave's double sum, and P.V
+// multiplies each exponential by (float)(1 / sum) as it reads it -- the
+// normalised p of the reference, formed where it is used.  The current key (row
+// pos) is the last key of its lanes in both loops, so its score and its P.V
+// term are added after the loops, from LDS, in the same order.
 //
 // With p.att_split = S > 1 (long contexts) this workgroup takes chunk c of
 // the keys, [c CH, (c + 1) CH) with CH = ceil((pos + 1) / S): a softmax
@@ -920,21 +981,25 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
                                                 int *bail, uint32_t ep) {
     constexpr int QD = S::QD, KVD = S::KVD, HD = S::HD;
     constexpr int SQ = rep_stride(S::NQKV / 2), SAT = rep_stride(QD);
-    constexpr int LPK = HD / 8, KPW = 64 / LPK;                  // lanes per key, keys per wave
-    constexpr int KB = 10;                                       // keys per lane per batch
+    constexpr int LPK = HD / 8, KPW = 64 / LPK;                  // V: lanes per key, keys per wave
+    constexpr int KB = 10;                                       // V: keys per lane per batch
     constexpr int PERB = kWaves * KPW * KB;                      // keys per batch (320)
+    constexpr int KBK = 5;                                       // K: keys per lane per batch
+    static_assert(kWaves * 8 * KBK == PERB, "K and V batches cover the same keys");
     const int tid = tid_now(), wave = tid >> 6, lane = tid & 63;
     const int rp = blockIdx.x % kRep, g = h / S::QPK, pos = p.pos;
     vxm_ptab Ly = layer_at(p, l);
     float *aq = lds + S::L_AQ, *red = lds + S::L_RED, *sc = lds + S::L_BIG;   // scores: BIG is free in phase B
+    float *wmax = lds + S::L_PART;                      // unit partials are free in phase B
+    double *wsum = (double *)(lds + S::L_PART + 8);
     uint16_t *const kc = Ly->kc, *const vc = Ly->vc;
     const uint16_t *kb = kc + (int64_t)g * p.cap * HD;
     const uint16_t *vb = vc + (int64_t)g * p.cap * HD;
     const int kv_len = pos + 1, nsplit = p.att_split;
     const int chl = (kv_len + nsplit - 1) / nsplit;
     const int j0 = chunk * chl, j1 = min(kv_len, j0 + chl), lim = min(j1, pos);
-    uint4 kr[KB], vr[KB];
-    attn_load<KB, HD>(kb, j0, lim, kr);
+    uint4 kr[KBK][2], vr[KB];
+    attn_load_k<KBK, HD>(kb, j0, lim, kr);
     attn_load<KB, HD>(vb, j0, lim, vr);
     if (wave == 0) {
         // q_h and k_g (pair-interleaved: word w = dims w, w + HD/2) and v_g
@@ -984,72 +1049,88 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
         }
     }
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
-    const int sub = lane % LPK, kin = lane / LPK;
-    // q_h as f16 pairs: q is BF16-valued (8 mantissa bits), so f16 holds it
-    // exactly at the magnitudes of a projection; the f16 x f16 products of
-    // v_dot2_f32_f16 are exact in f32 and only the summation order differs
-    // from a sequential fp32 dot product
-    half2_t q2[4];
+    const bool has_pos = pos >= j0 && pos < j1;   // the last chunk holds the current key
+    // ---- scores: lane (kin8, sub8) holds q dims sub8*16 .. +16 as f16 pairs ----
+    const int sub8 = lane & 7, kin8 = lane >> 3;
+    half2_t q2[8];
 #pragma unroll
-    for (int i = 0; i < 4; i++) q2[i] = half2_t{(_Float16)qh[sub * 8 + 2 * i], (_Float16)qh[sub * 8 + 2 * i + 1]};
-    // scores: batch jb covers keys jb + (k * kWaves + wave) * KPW + kin
+    for (int i = 0; i < 8; i++) q2[i] = half2_t{(_Float16)qh[sub8 * 16 + 2 * i], (_Float16)qh[sub8 * 16 + 2 * i + 1]};
     float mx = -INFINITY;
     for (int jb = j0; jb < j1; jb += PERB) {
-        if (jb > j0) attn_load<KB, HD>(kb, jb, lim, kr);
+        if (jb > j0) attn_load_k<KBK, HD>(kb, jb, lim, kr);
 #pragma unroll
-        for (int k = 0; k < KB; k++) {
-            const int j = jb + (k * kWaves + wave) * KPW + kin;
-            uint32_t wv[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
-            if (j == pos) {
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    wv[i] = (uint32_t)vxm_f2h(kcur[sub * 8 + 2 * i]) | ((uint32_t)vxm_f2h(kcur[sub * 8 + 2 * i + 1]) << 16);
-            }
-            float pt = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; i++) pt = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, wv[i]), q2[i], pt, false);
-            pt = row16_sum_15(pt);
-            if (j < j1 && sub == LPK - 1) {
-                const float s2 = pt * scale;
-                sc[j - j0] = s2;
+        for (int k = 0; k < KBK; k++) {
+            const int j = jb + (k * kWaves + wave) * 8 + kin8;
+            const float s2 = score8(q2, kr[k]) * scale;
+            if (j < lim) {
+                if (sub8 == 0) sc[j - j0] = s2;
                 mx = fmaxf(mx, s2);
             }
         }
     }
+    if (has_pos) {
+        // the current key from LDS, on the lanes whose key it is (the last key of those lanes)
+        const int d = pos - j0, rel = d % PERB, wp = (rel / 8) % kWaves, kp = rel % 8;
+        if (wave == wp && kin8 == kp) {
+            uint4 kq[2];
+            uint32_t *kw = (uint32_t *)kq;
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                kw[i] = (uint32_t)vxm_f2h(kcur[sub8 * 16 + 2 * i]) | ((uint32_t)vxm_f2h(kcur[sub8 * 16 + 2 * i + 1]) << 16);
+            const float s2 = score8(q2, kq) * scale;
+            if (sub8 == 0) sc[d] = s2;
+            mx = fmaxf(mx, s2);
+        }
+    }
     VXM_TS(tid_now() == 0, 2);
-    mx = wg_max_f(mx, red);
+    mx = wave_max_63(mx);
+    if (lane == 63) wmax[wave] = mx;
+    lds_barrier();   // scores and wave maxima in LDS
+    mx = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; w++) mx = fmaxf(mx, wmax[w]);
     double sum = 0.0;
     for (int j = tid; j < j1 - j0; j += kThreads) {
         const float e = expf(sc[j] - mx);
         sc[j] = e;
         sum += (double)e;
     }
-    sum = wg_sum_d(sum, red);
+    sum = wave_sum_63_d(sum);
+    if (lane == 63) wsum[wave] = sum;
+    lds_barrier();   // exponentials and wave sums in LDS
+    sum = 0.0;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) sum += wsum[w];
     const float inv = (float)(1.0 / sum);
-    for (int j = tid; j < j1 - j0; j += kThreads) sc[j] = sc[j] * inv;
-    lds_barrier();
     VXM_TS(tid_now() == 0, 11);
-    // out[d] = sum_j p_j v_j[d]: lane (kin, sub) accumulates dims sub*8..+8 over its keys
+    // out[d] = sum_j p_j v_j[d], p_j = e_j * inv: lane (kin, sub) accumulates dims sub*8..+8 over its keys
+    const int sub = lane % LPK, kin = lane / LPK;
     float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int jb = j0; jb < j1; jb += PERB) {
         if (jb > j0) attn_load<KB, HD>(vb, jb, lim, vr);
 #pragma unroll
         for (int k = 0; k < KB; k++) {
             const int j = jb + (k * kWaves + wave) * KPW + kin;
-            if (j >= j1) continue;
-            const float pj = sc[j - j0];
-            uint32_t wv[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
-            if (j == pos) {
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    wv[i] = (uint32_t)vxm_f2h(vcur[sub * 8 + 2 * i]) | ((uint32_t)vxm_f2h(vcur[sub * 8 + 2 * i + 1]) << 16);
-            }
+            if (j >= lim) continue;
+            const float pj = sc[j - j0] * inv;
             // one mixed-precision fma per value: the f16 operand is widened exactly
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const half2_t v2 = __builtin_bit_cast(half2_t, wv[i]);
+                const uint32_t wv = i == 0 ? vr[k].x : i == 1 ? vr[k].y : i == 2 ? vr[k].z : vr[k].w;
+                const half2_t v2 = __builtin_bit_cast(half2_t, wv);
                 o[2 * i] = __builtin_fmaf(pj, (float)v2.x, o[2 * i]);
                 o[2 * i + 1] = __builtin_fmaf(pj, (float)v2.y, o[2 * i + 1]);
+            }
+        }
+    }
+    if (has_pos) {
+        const int d = pos - j0, rel = d % PERB, wp = (rel / KPW) % kWaves, kp = rel % KPW;
+        if (wave == wp && kin == kp) {
+            const float pj = sc[d] * inv;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float vf = (float)__builtin_bit_cast(_Float16, vxm_f2h(vcur[sub * 8 + i]));
+                o[i] = __builtin_fmaf(pj, vf, o[i]);
             }
         }
     }
@@ -1062,21 +1143,49 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
         const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(o[i]), __float_as_uint(o[i]), false, false);
         o[i] = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
     }
-    lds_barrier();   // red is reused below
     if (kin == 0) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) red[wave * HD + sub * 8 + i] = o[i];
+        *(float4 *)(red + wave * HD + sub * 8) = make_float4(o[0], o[1], o[2], o[3]);
+        *(float4 *)(red + wave * HD + sub * 8 + 4) = make_float4(o[4], o[5], o[6], o[7]);
     }
-    lds_barrier();
+    lds_barrier();   // the wave partials in LDS
     const uint32_t tg = make_tag(ep, l, PH_ATT);
-    static_assert(kThreads % HD == 0 && (kRep % (kThreads / HD) == 0 || kRep < kThreads / HD),
-                  "attention output replicas");
-    // thread t owns dim t % HD; the wave partials are summed once, in a fixed order
+    static_assert(HD % 32 == 0 && HD / 4 <= 64, "one wave quantizes a head");
+    if (nsplit == 1) {
+        // wave 0: lane i < HD / 4 adds the wave partials of dims 4i .. 4i + 3 in wave
+        // order, quantizes them (Q8_0, the O projection's input rule) and publishes:
+        // word h HD/4 + i holds the quants of dims 4i .. 4i + 3 of head h, word
+        // NH HD/4 + h HD/32 + b the scale of its block b -- a quarter of the words
+        // of fp32 outputs, so each of the 256 readers of phase C loads a quarter
+        // of the bytes
+        if (wave == 0) {
+            const int i = lane % (HD / 4);   // lanes past HD / 4 repeat the first ones
+            float4 a = *(const float4 *)(red + 4 * i);
+#pragma unroll
+            for (int w = 1; w < kWaves; w++) {
+                const float4 b = *(const float4 *)(red + w * HD + 4 * i);
+                a.x = a.x + b.x; a.y = a.y + b.y; a.z = a.z + b.z; a.w = a.w + b.w;
+            }
+            const float q4[4] = {a.x, a.y, a.z, a.w};
+            uint32_t w;
+            float dsc;
+            quant4_reg(q4, w, dsc);
+            if (lane < HD / 4) {
+#pragma unroll
+                for (int r = 0; r < kRep; r++) {
+                    put_word(p.attb + r * SAT + h * (HD / 4) + i, w, tg);
+                    if ((i & 7) == 0) put_word(p.attb + r * SAT + S::NH * (HD / 4) + h * (HD / 32) + i / 8, __float_as_uint(dsc), tg);
+                }
+            }
+        }
+        VXM_TS(tid_now() == 0, 4);
+        return;
+    }
+    // key chunks: thread t owns dim t % HD; the wave partials are summed once, in a fixed order
     const int d = tid % HD;
     float v = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWaves; w++) v += red[w * HD + d];
-    if (nsplit > 1) {
+    {
         constexpr int CW = HD + 2;   // o[HD], m, l of one chunk in LDS
         const uint32_t tp = make_tag(ep, l, PH_ATTP);
         uint64_t *mine = p.attp + ((int64_t)h * kAttSplitMax + chunk) * kAttpWords;
@@ -1133,18 +1242,12 @@ __device__ __forceinline__ void attention_phase(const vxm_pparams &p, int l, int
         // the next phase's input lands in the same LDS
         lds_barrier();
     }
-    // Q8_0 of the head's HD outputs, the quantization the O projection applies to
-    // its input (quant4 over aligned 32-value blocks, which never cross a head):
-    // word h HD/4 + i holds the quants of dims 4i .. 4i + 3 of head h, word
-    // NH HD/4 + h HD/32 + b the scale of its block b.  A quarter of the words of
-    // fp32 outputs, so each of the 256 readers of phase C loads a quarter of the
-    // bytes.  aq's q, k, v are dead here (their last reads precede the barriers
-    // above).
-    static_assert(HD % 32 == 0 && HD / 4 <= 64, "one wave quantizes a head");
+    // Q8_0 of the merged head output (quant4 over aligned 32-value blocks) and the
+    // publication, as in the unsplit case; aq's q, k, v are dead here
     if (tid < HD) aq[tid] = v;
     lds_barrier();
     if (wave == 0) {
-        const int i = lane % (HD / 4);   // lanes past HD / 4 repeat the first ones
+        const int i = lane % (HD / 4);
         const float4 a = *(const float4 *)(aq + 4 * i);
         const float q4[4] = {a.x, a.y, a.z, a.w};
         uint32_t w;
@@ -1176,9 +1279,9 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
     double *ssq = (double *)red;   // sum of squares from the reading wave
     int8_t *xq = (int8_t *)lds + S::XQ_OFF;
     const int wave = tid_now() >> 6, lane = tid_now() & 63;
-    const bool reader = wave == 0;
-    const int ci = __builtin_amdgcn_readfirstlane(wave - 1);   // compute wave index (uniform)
-    const int t = tid_now() - 64;                             // compute thread index
+    const bool reader = wave < kNR;
+    const int ci = __builtin_amdgcn_readfirstlane(wave - kNR);   // compute wave index (uniform)
+    const int t = tid_now() - 64 * kNR;                         // compute thread index
     const int pos = p.pos;
     // the query head this workgroup attends for, or -1
     int head = -1, chunk = 0;
@@ -1208,14 +1311,14 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         vxm_ptab Ly = layer_at(p, l);
         const UnitBases nxt = unit_bases(p, l + 1);
         // ---------------- A: norm + QKV + rope ----------------
-        static_assert((H / 2) % (64 * kXReaders) == 0 && H / 2 / kXReaders <= 64 * 64, "x readers");
-        if (reader) stage_f32(Ly->g_in, H, gn);
+        static_assert((H / 2) % (128 * kXReaders) == 0 && H / 2 / kXReaders <= 64 * 64, "x readers");
+        if (wave == 0) stage_f32(Ly->g_in, H, gn);
         if (wave < kXReaders) {
             // waves 0 .. kXReaders-1 each read a share of x (and its sum of squares)
             constexpr int XW = H / 2 / kXReaders;   // words per reading wave
             double ss = 0.0;
             if (l == 0) {
-                if (reader) {
+                if (wave == 0) {
                     for (int i = lane * 4; i < H; i += 256) {
                         const float4 v = *(const float4 *)(p.x + i);
                         *(float4 *)(xs + i) = v;
@@ -1223,8 +1326,8 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
                     }
                 }
             } else {
-                ss = read_words<XW / 64, true>(p, p.xb + ((l & 1) * kRep + rp) * SX + wave * XW, XW,
-                                               make_tag(ep, l, PH_X), xs + 2 * wave * XW, bail);
+                ss = read_words<cdiv(XW / 2, 64), true>(p, p.xb + ((l & 1) * kRep + rp) * SX + wave * XW, XW / 2,
+                                                        make_tag(ep, l, PH_X), xs + 2 * wave * XW, bail);
             }
             ss = wave_sum_63_d(ss);
             if (lane == 63) ssq[wave] = ss;
@@ -1286,11 +1389,11 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
             // flight together
             const uint64_t *src = p.attb + rp * SAT;
             const uint32_t tag = make_tag(ep, l, PH_ATT);
-            constexpr int NQW = NH * (HD / 4), NW = NQW + NH * (HD / 32), AW = cdiv(NW, kAttReaders);
-            static_assert(AW <= 64 * 64, "attention channel shares");
+            constexpr int NQW = NH * (HD / 4), NW = NQW + NH * (HD / 32), AP = cdiv(NW / 2, kAttReaders);
+            static_assert(NW % 2 == 0 && NQW % 2 == 0 && AP <= 64 * 32, "attention channel shares");
             wait_sentinels(p, src, NH, HD / 4, tag, bail);
-            const int i0 = wave * AW;
-            if (!*bail) read_q8_words<cdiv(AW, 64)>(p, src, i0, min(AW, NW - i0), NQW, tag, xq, xd, bail);
+            const int p0 = wave * AP;
+            if (!*bail) read_q8_words<cdiv(AP, 64)>(p, src, p0, min(AP, NW / 2 - p0), NQW, tag, xq, xd, bail);
         }
         lds_barrier();
         if (*bail) return;
@@ -1315,12 +1418,12 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         }
         if (!reader) ring_refill<S, S::OC, S::SC>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         // ---------------- D: post norm + gate/up + SwiGLU ----------------
-        if (reader) stage_f32(Ly->g_post, H, gn);
+        if (wave == 0) stage_f32(Ly->g_post, H, gn);
         if (wave < kH1Readers) {
             constexpr int HW = H / 2 / kH1Readers;   // words per reading wave
-            static_assert(HW % 64 == 0 && HW / 64 <= 64, "h1 readers");
-            double ss = read_words<HW / 64, true>(p, p.h1b + rp * SX + wave * HW, HW, make_tag(ep, l, PH_H1),
-                                                  h1s + 2 * wave * HW, bail);
+            static_assert(HW % 128 == 0 && HW / 128 <= 32, "h1 readers");
+            double ss = read_words<HW / 128, true>(p, p.h1b + rp * SX + wave * HW, HW / 2, make_tag(ep, l, PH_H1),
+                                                   h1s + 2 * wave * HW, bail);
             ss = wave_sum_63_d(ss);
             if (lane == 63) ssq[wave] = ss;
         }
@@ -1364,9 +1467,9 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         if (wave < kPReaders) {
             // waves 0 .. kPReaders-1 each read a share of p
             constexpr int QW = F / 2 / kPReaders;
-            static_assert(QW % 64 == 0 && QW / 64 <= 64, "p channel shares");
+            static_assert(QW % 128 == 0 && QW / 128 <= 32, "p channel shares");
             const uint32_t tag = make_tag(ep, l, PH_P);
-            read_words<QW / 64, true, true>(p, p.pb + rp * SP + wave * QW, QW, tag, big + wave * QW, bail);
+            read_words<QW / 128, true, true>(p, p.pb + rp * SP + wave * QW, QW / 2, tag, big + wave * QW, bail);
         }
         lds_barrier();
         if (*bail) return;
@@ -1401,9 +1504,9 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
     // ---------------- final norm (workgroup 0) ----------------
     if (wg != 0) return;
     const int Lyr = p.n_layers;
-    if (reader) {
+    if (wave == 0) {
         if (p.final_norm) stage_f32(p.final_norm, H, gn);
-        read_words<cdiv(H / 2, 64), true>(p, p.xb + ((Lyr & 1) * kRep + rp) * SX, H / 2, make_tag(ep, Lyr, PH_X), xs,
+        read_words<cdiv(H / 4, 64), true>(p, p.xb + ((Lyr & 1) * kRep + rp) * SX, H / 4, make_tag(ep, Lyr, PH_X), xs,
                                           bail);
     }
     lds_barrier();
