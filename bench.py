@@ -577,6 +577,8 @@ def main():
     ap.add_argument("--prefill-only", action="store_true",
                     help="time only the prefill legs (MFMA GEMMs and the 512-token 28-layer prefill)")
     ap.add_argument("--prefill-tokens", type=int, default=512)
+    ap.add_argument("--prefill-long-tokens", type=int, default=2048,
+                    help="tokens of the long-prompt prefill leg (0: skip it)")
     ap.add_argument("--cfm-only", action="store_true", help="time only the CFM solve leg")
     ap.add_argument("--blocks", default="auto", choices=list(BLOCK_MODES),
                     help="LocDiT block strategy of the CFM legs (auto: the library's pick per shape)")
@@ -655,6 +657,16 @@ def main():
                "attention_GFLOP": round(a_flops / 1e9, 2), "finite": fin, "gemm": gemms}
         log(f"prefill {M} tokens x {L} layers: {us_pre:.1f} us ({M / (us_pre * 1e-6):.0f} tok/s), "
             f"GEMM work {g_ops / (us_pre * 1e-6) / 1e12:.1f} TOP/s over the step, finite={fin}")
+        if args.prefill_long_tokens > 0:
+            # a long prompt: spans past one 512-key score tile take the three-pass MFMA attention
+            ML = args.prefill_long_tokens
+            us_l, fin_l = bench_prefill(ctx, torch, vxm, pl, L, ML, 2)
+            g_l, a_l = prefill_ops(ML)
+            pre["long_prompt"] = {"tokens": ML, "layers": L, "us": round(us_l, 1),
+                                  "tokens_per_s": round(ML / (us_l * 1e-6), 1),
+                                  "gemm_TOPs": round(g_l / (us_l * 1e-6) / 1e12, 1),
+                                  "attention_GFLOP": round(a_l / 1e9, 2), "finite": fin_l}
+            log(f"prefill {ML} tokens x {L} layers: {us_l:.1f} us ({ML / (us_l * 1e-6):.0f} tok/s), finite={fin_l}")
         del pl
         if args.prefill_only:
             print(json.dumps({"prefill": pre}))

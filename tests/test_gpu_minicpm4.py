@@ -376,3 +376,57 @@ def test_block_noncausal_tiled_attention(vxm_ctx, orc):
     ref = orc.minicpm4_block(orc_cfg(orc, c), to_orc(orc, lw), x, None, None, 0, 0, 1)
     assert_prefill_close(xd.cpu().numpy(), ref, what="block non-causal tiled")
     model.free()
+
+
+# Spans above 512 keys take the three-pass MFMA attention (chunks of 512 keys).
+@pytest.mark.parametrize("M,pos,hd,full", [(1024, 0, 128, False), (512, 3584, 128, False), (96, 1000, 64, False),
+                                           (600, 0, 64, False), (1024, 0, 128, True), (512, 3584, 128, True)])
+def test_block_prefill_long_span_attention(vxm_ctx, orc, M, pos, hd, full):
+    """Prefill blocks whose key span exceeds one 512-key score tile: 1024 tokens from
+    position 0, 512 tokens after 3584 cached rows (4096 keys), a short tile after 1000
+    rows and a ragged 600-token span.  At the small width of the other prefill block
+    tests (hidden 256) the block bar of many-token blocks; at the TSLM's full width
+    (hidden 2048, 16 heads of 128) the one-layer bar of the full-size tests (one BF16
+    flip moves a full-width block by a relative L2 of 4e-3, test_gpu_fullsize.py).
+    The K / V rows the block appends are compared as well."""
+    import vxm
+
+    rng = np.random.default_rng(900 + M + pos + hd + full)
+    if full:
+        H, nh, nkv, F = 2048, 16, 2, 6144
+    else:
+        H, nh, nkv, F = 256, 512 // hd, 2, 512
+    lw = rand_layer(orc, rng, H, nh, nkv, hd, F)
+    c = cfg_dict(H, 1, nh, nkv, hd, F)
+    cap = pos + M + 64
+    prior_k = orc.fp32_to_fp16_bits(orc.bf16_round(rng.normal(0, 1, (nkv, cap, hd)).astype(np.float32)))
+    prior_v = orc.fp32_to_fp16_bits(orc.bf16_round(rng.normal(0, 1, (nkv, cap, hd)).astype(np.float32)))
+    prior_k[:, pos:] = 0
+    prior_v[:, pos:] = 0
+    x = rng.normal(0, 1, (M, H)).astype(np.float32)
+    model = vxm.MiniCPM4(vxm_ctx, c, [lw])
+    kv = vxm.KVCache(vxm_ctx, 1, nkv, hd, cap)
+    try:
+        kv.upload(0, prior_k, prior_v)
+        xd = _dev(x)
+        what = f"long-span prefill M={M} pos={pos} hd={hd} full={full}"
+        print(what, flush=True)
+        model.block(kv, 0, xd, pos)
+        vxm_ctx.sync()
+        kc = prior_k.reshape(-1).copy()
+        vc = prior_v.reshape(-1).copy()
+        ref = orc.minicpm4_block(orc_cfg(orc, c), to_orc(orc, lw), x, kc, vc, cap, pos, 0)
+        if full:
+            from test_gpu_fullsize import assert_one_layer
+
+            assert_one_layer(xd.cpu().numpy(), ref, what)
+        else:
+            assert_prefill_close(xd.cpu().numpy(), ref, what=what)
+        gk, gv = kv.download(0)
+        rows = slice(pos, pos + M)
+        want_k = kc.reshape(nkv, cap, hd)[:, rows]
+        want_v = vc.reshape(nkv, cap, hd)[:, rows]
+        assert (gk[:, rows] == want_k).mean() >= 0.99 and (gv[:, rows] == want_v).mean() >= 0.99
+    finally:
+        kv.free()
+        model.free()

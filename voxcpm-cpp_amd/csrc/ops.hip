@@ -351,7 +351,7 @@ __global__ __launch_bounds__(256) void k_attention(const float *__restrict__ q, 
 //           halves (two products, ~22 bits of p), V through the wave's own LDS
 //           buffer, transposed as key-pair words; the four key quarters are
 //           added in order at the end.
-// The score buffer holds AKV keys: longer spans take k_attention.
+// The score buffer holds AKV keys: longer spans take k_attention_mfma_long.
 // ---------------------------------------------------------------------------
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -608,6 +608,237 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma(const float *__restrict_
     VXM_ATTN_TS(4);
 }
 
+// Spans above AKV keys: the same tiles, lane layouts and rounding steps in three
+// passes over chunks of AKV keys, the scores recomputed in each pass (from K rows
+// that the L2 mostly holds by then): 1. each query row's max over all its keys,
+// 2. its double sum of exp(s - max), 3. per chunk, p = e * (float)(1 / sum) into
+// LDS and the P V products, accumulated over the chunks in each wave's registers.
+// Every p has the value the one-pass kernel gives for the same score; only the
+// order of the double sum and of the fp32 P V sums (chunk by chunk) differ.
+template <int HD>
+__global__ __launch_bounds__(ATH) void k_attention_mfma_long(const float *__restrict__ q,
+                                                             const uint16_t *__restrict__ kc,
+                                                             const uint16_t *__restrict__ vc, float *__restrict__ out,
+                                                             int M, int nh, int nkv, int cap, int kv_base, int causal,
+                                                             int8_t *__restrict__ xq, uint16_t *__restrict__ xd,
+                                                             int variant) {
+    constexpr int NW = ATH / 64;       // waves
+    constexpr int SP = AKV + 4;        // fp32 P row pitch
+    constexpr int KSTEPS = HD / 16;    // MFMA steps over the head dimension
+    constexpr int HDH = HD / 2;        // dims of one output half
+    constexpr int DT = HDH / 32;       // 32-dim output tiles per wave
+    constexpr int VP = 32 + 8;         // f16 pitch of a wave's transposed V block
+    constexpr int VITEMS = 16 * (HDH / 8) / 64;
+    constexpr int CB = AKV / 32;       // key blocks per chunk
+    constexpr int SB = CB / NW;        // most score blocks of one wave per chunk
+    constexpr int VB = CB / 4;         // most P V blocks of one key quarter per chunk
+    __shared__ __align__(16) float Sc[AQ * SP];
+    __shared__ __align__(16) _Float16 Vt[NW][HDH * VP];
+    __shared__ float smax[AQ][NW];
+    __shared__ double ssum[AQ][NW];
+    constexpr int QP = HD + 8;
+    __shared__ __align__(16) _Float16 Qh[AQ * QP];
+    static_assert(NW == 8 && VITEMS >= 1 && 4 * AQ * HD <= AQ * SP, "8 waves; the key-quarter sums reuse P's buffer");
+    const int h = blockIdx.x, t0 = blockIdx.y * AQ, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kvh = h / (nh / nkv);
+    const uint16_t *kb = kc + (int64_t)kvh * cap * HD;
+    const uint16_t *vb = vc + (int64_t)kvh * cap * HD;
+    const int nq = min(AQ, M - t0);
+    const int kv_end = causal ? kv_base + t0 + nq : M;
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
+    const int lr = lane & 31, lh = lane >> 5;
+    const int nblk = (kv_end + 31) / 32, nch = (nblk + CB - 1) / CB;
+    const int kq = wave & 3, dh = wave >> 2;
+    constexpr int QL = AQ * HD / 4 / ATH;
+#pragma unroll
+    for (int u = 0; u < QL; u++) {
+        const int i = (u * ATH + tid) * 4, r = i / HD, d = i % HD;
+        const float4 qf = *(const float4 *)(q + (int64_t)(t0 + min(r, nq - 1)) * nh * HD + h * HD + d);
+        const bool qlive = r < nq;
+        _Float16 *dst = Qh + r * QP + d;
+        dst[0] = (_Float16)(qlive ? qf.x : 0.0f);
+        dst[1] = (_Float16)(qlive ? qf.y : 0.0f);
+        dst[2] = (_Float16)(qlive ? qf.z : 0.0f);
+        dst[3] = (_Float16)(qlive ? qf.w : 0.0f);
+    }
+    __syncthreads();
+    v8h qa[KSTEPS];
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; kk++) qa[kk] = *(const v8h *)(Qh + lr * QP + 16 * kk + 8 * lh);
+    const int kvl = lr < nq ? (causal ? kv_base + t0 + lr + 1 : M) : 0;
+    // the scores (S^T = K Q^T, scaled) of this wave's blocks of chunk c: block cb0 + i,
+    // i < ncb; value v of lane (lr, lh) is query t0 + lr, key 32 b + 8 (v / 4) + 4 lh + v % 4
+    auto scores = [&](int c, v16f (&sc)[SB], int &cb0, int &ncb) {
+        const int nbc = min(CB, nblk - c * CB);
+        cb0 = c * CB + nbc * wave / NW;
+        ncb = c * CB + nbc * (wave + 1) / NW - cb0;
+        uint4 kr[SB][KSTEPS];
+#pragma unroll
+        for (int i = 0; i < SB; i++) {
+            const int key = min(32 * (cb0 + i) + lr, kv_end - 1);   // unconditional: clamped rows
+#pragma unroll
+            for (int kk = 0; kk < KSTEPS; kk++) kr[i][kk] = *(const uint4 *)(kb + (int64_t)key * HD + 16 * kk + 8 * lh);
+        }
+#pragma unroll
+        for (int i = 0; i < SB; i++) {
+            v16f acc = v16f{};
+#pragma unroll
+            for (int kk = 0; kk < KSTEPS; kk++) {
+                v8h av;
+                __builtin_memcpy(&av, &kr[i][kk], 16);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qa[kk], acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int v = 0; v < 16; v++) sc[i][v] = acc[v] * scale;
+        }
+    };
+    auto live = [&](int i, int ncb, int b, int v) { return i < ncb && 32 * b + 8 * (v >> 2) + 4 * lh + (v & 3) < kvl; };
+    v16f sc[SB];
+    int cb0, ncb;
+    // pass 1: each query row's max over its keys (the lane's, its partner's, the waves')
+    float m = -INFINITY;
+    for (int c = 0; c < nch; c++) {
+        scores(c, sc, cb0, ncb);
+#pragma unroll
+        for (int i = 0; i < SB; i++)
+#pragma unroll
+            for (int v = 0; v < 16; v++)
+                if (live(i, ncb, cb0 + i, v)) m = fmaxf(m, sc[i][v]);
+    }
+    m = fmaxf(m, __shfl_xor(m, 32));
+    if (lh == 0) smax[lr][wave] = m;
+    __syncthreads();
+    m = smax[lr][0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) m = fmaxf(m, smax[lr][w]);
+    // pass 2: the double sum of e = exp(s - max)
+    double sum = 0.0;
+    for (int c = 0; c < nch; c++) {
+        scores(c, sc, cb0, ncb);
+#pragma unroll
+        for (int i = 0; i < SB; i++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) sum += (double)(live(i, ncb, cb0 + i, v) ? expf(sc[i][v] - m) : 0.0f);
+    }
+    sum += __shfl_xor(sum, 32);
+    if (lh == 0) ssum[lr][wave] = sum;
+    __syncthreads();
+    sum = ssum[lr][0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) sum += ssum[lr][w];
+    const float inv = kvl > 0 ? (float)(1.0 / sum) : 0.0f;
+    // pass 3: per chunk, P rows into LDS, then partial O = P V of key quarter kq of the
+    // chunk's blocks for dims [64 dh, 64 dh + 64), accumulated over the chunks
+    v16f o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) o[dt] = v16f{};
+    _Float16 *vt = Vt[wave];
+    const uint16_t *vbh = vb + HDH * dh;
+    for (int c = 0; c < nch; c++) {
+        const int nbc = min(CB, nblk - c * CB), cbase = c * CB;
+        const int bq0 = cbase + nbc * kq / 4, nbq = cbase + nbc * (kq + 1) / 4 - bq0;
+        // the V rows of the wave's P V blocks, in flight during the scores
+        uint4 vr[VB][VITEMS][2];
+#pragma unroll
+        for (int i = 0; i < VB; i++)
+#pragma unroll
+            for (int u = 0; u < VITEMS; u++) {
+                const int item = u * 64 + lane, r = 32 * (bq0 + i) + 2 * (item % 16), d = 8 * (item / 16);
+#pragma unroll
+                for (int e = 0; e < 2; e++)
+                    vr[i][u][e] = *(const uint4 *)(vbh + (int64_t)min(r + e, kv_end - 1) * HD + d);
+            }
+        scores(c, sc, cb0, ncb);
+#pragma unroll
+        for (int i = 0; i < SB; i++) {
+            if (i >= ncb) break;
+            float pv[16];
+#pragma unroll
+            for (int v = 0; v < 16; v++) pv[v] = live(i, ncb, cb0 + i, v) ? expf(sc[i][v] - m) * inv : 0.0f;
+#pragma unroll
+            for (int r4 = 0; r4 < 4; r4++)
+                *(float4 *)(Sc + lr * SP + 32 * (cb0 + i - cbase) + 8 * r4 + 4 * lh) =
+                    make_float4(pv[4 * r4], pv[4 * r4 + 1], pv[4 * r4 + 2], pv[4 * r4 + 3]);
+        }
+        __syncthreads();   // every wave's P rows of the chunk in LDS
+#pragma unroll
+        for (int i = 0; i < VB; i++) {
+            if (i >= nbq) break;
+            const int b = bq0 + i;
+#pragma unroll
+            for (int u = 0; u < VITEMS; u++) {
+                const int item = u * 64 + lane, r = 2 * (item % 16), d = 8 * (item / 16);
+                const uint32_t a[4] = {vr[i][u][0].x, vr[i][u][0].y, vr[i][u][0].z, vr[i][u][0].w};
+                const uint32_t bb[4] = {vr[i][u][1].x, vr[i][u][1].y, vr[i][u][1].z, vr[i][u][1].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    *(uint32_t *)(vt + (d + 2 * e) * VP + r) = (a[e] & 0xffffu) | (bb[e] << 16);
+                    *(uint32_t *)(vt + (d + 2 * e + 1) * VP + r) = (a[e] >> 16) | (bb[e] & 0xffff0000u);
+                }
+            }
+#pragma unroll
+            for (int ks = 0; ks < 32; ks += 16) {
+                const float *pr = Sc + lr * SP + 32 * (b - cbase) + ks + 8 * lh;
+                const float4 p0 = *(const float4 *)pr, p1 = *(const float4 *)(pr + 4);
+                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                v8h ahi, alo;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const _Float16 hi = (_Float16)pv[e];
+                    ahi[e] = hi;
+                    alo[e] = (_Float16)(pv[e] - (float)hi);
+                }
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) {
+                    const v8h bv = *(const v8h *)(vt + (32 * dt + lr) * VP + ks + 8 * lh);
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, bv, o[dt], 0, 0, 0);
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, bv, o[dt], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();   // the chunk's P rows are read before the next chunk's overwrite them
+    }
+    // the key quarters in order through LDS (P's buffer is free)
+    float *red = Sc;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+            red[(kq * AQ + 8 * (v >> 2) + 4 * lh + (v & 3)) * HD + HDH * dh + 32 * dt + lr] = o[dt][v];
+    __syncthreads();
+    if (xq) {
+        for (int i = 8 * tid; i < AQ * HD; i += 8 * ATH) {
+            const int qi = i / HD, d = i % HD;
+            float v[8];
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                float4 s = *(const float4 *)(red + i + 4 * hf);
+#pragma unroll
+                for (int w = 1; w < 4; w++) {
+                    const float4 t = *(const float4 *)(red + w * AQ * HD + i + 4 * hf);
+                    s.x = s.x + t.x; s.y = s.y + t.y; s.z = s.z + t.z; s.w = s.w + t.w;
+                }
+                v[4 * hf] = s.x; v[4 * hf + 1] = s.y; v[4 * hf + 2] = s.z; v[4 * hf + 3] = s.w;
+            }
+            const int64_t o2 = (int64_t)(t0 + min(qi, nq - 1)) * nh * HD + h * HD + d;
+            quant_block_4lanes(v, variant, xq + o2, xd + o2 / 32, (tid & 3) == 0, qi < nq);
+        }
+    } else {
+        for (int i = 4 * tid; i < AQ * HD; i += 4 * ATH) {
+            const int qi = i / HD, d = i % HD;
+            if (qi >= nq) continue;
+            float4 s = *(const float4 *)(red + i);
+#pragma unroll
+            for (int w = 1; w < 4; w++) {
+                const float4 t = *(const float4 *)(red + w * AQ * HD + i);
+                s.x = s.x + t.x; s.y = s.y + t.y; s.z = s.z + t.z; s.w = s.w + t.w;
+            }
+            *(float4 *)(out + (int64_t)(t0 + qi) * nh * HD + h * HD + d) = s;
+        }
+    }
+}
+
 int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
                          int64_t M, int nh, int nkv, int hd, int cap, int64_t seg_stride, int S, int kv_base,
                          int causal, int8_t *xq, uint16_t *xd, int variant) {
@@ -616,14 +847,22 @@ int vxm_launch_attention(vxm_ctx *ctx, const float *q, const uint16_t *kc, const
         return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "attention: head_dim %d / heads %d,%d unsupported", hd, nh, nkv);
     // many queries of a single segment whose key span fits the score buffer: the MFMA kernel
     const int64_t span = causal ? kv_base + M : M;
-    if (S == M && M >= AQ && span <= AKV && span <= cap && (hd == 128 || hd == 64)) {
+    if (S == M && M >= AQ && span <= cap && (hd == 128 || hd == 64)) {
         const dim3 grid(nh, (unsigned)((M + AQ - 1) / AQ));
-        if (hd == 128)
-            hipLaunchKernelGGL(k_attention_mfma<128>, grid, dim3(ATH), 0, ctx->stream, q, kc, vc, out, (int)M, nh,
-                               nkv, cap, kv_base, causal, xq, xd, variant);
-        else
-            hipLaunchKernelGGL(k_attention_mfma<64>, grid, dim3(ATH), 0, ctx->stream, q, kc, vc, out, (int)M, nh,
-                               nkv, cap, kv_base, causal, xq, xd, variant);
+        if (span <= AKV) {
+            if (hd == 128)
+                hipLaunchKernelGGL(k_attention_mfma<128>, grid, dim3(ATH), 0, ctx->stream, q, kc, vc, out, (int)M, nh,
+                                   nkv, cap, kv_base, causal, xq, xd, variant);
+            else
+                hipLaunchKernelGGL(k_attention_mfma<64>, grid, dim3(ATH), 0, ctx->stream, q, kc, vc, out, (int)M, nh,
+                                   nkv, cap, kv_base, causal, xq, xd, variant);
+        } else if (hd == 128) {
+            hipLaunchKernelGGL(k_attention_mfma_long<128>, grid, dim3(ATH), 0, ctx->stream, q, kc, vc, out, (int)M,
+                               nh, nkv, cap, kv_base, causal, xq, xd, variant);
+        } else {
+            hipLaunchKernelGGL(k_attention_mfma_long<64>, grid, dim3(ATH), 0, ctx->stream, q, kc, vc, out, (int)M,
+                               nh, nkv, cap, kv_base, causal, xq, xd, variant);
+        }
         VXM_CHECK_LAUNCH(ctx);
         return VXM_OK;
     }
