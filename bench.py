@@ -208,8 +208,11 @@ def bench_read_floor(ctx, torch, vxm, nbytes, copies, reps, per_launch):
     return us
 
 
-def bench_decode(ctx, torch, vxm, layers, n_layers, copies, ctx0, steps, warmup, mode):
-    """Decode `steps` tokens from context ctx0, rotating over `copies` weight copies."""
+def bench_decode(ctx, torch, vxm, layers, n_layers, copies, ctx0, steps, warmup, mode, synced=False):
+    """Decode `steps` tokens from context ctx0, rotating over `copies` weight copies.  synced: after
+    every token the hidden state is copied to the host (vxm_memcpy_d2h, which waits for it), the one
+    read-back per step that the reference's synchronous graph call implies."""
+    import numpy as np
     cfg = dict(hidden_size=H, n_layers=n_layers, n_heads=NH, n_kv_heads=NKV, head_dim=HD, intermediate_size=F,
                rms_norm_eps=1e-6, rope_theta=10000)
     fn = vxm.host_randn(11, H, 1.0, 0.02)
@@ -225,10 +228,14 @@ def bench_decode(ctx, torch, vxm, layers, n_layers, copies, ctx0, steps, warmup,
         models[i % copies].forward(kv, x, ctx0 + i)
     ctx.sync()
     kv.set_used(ctx0)
+    host = np.empty(H if n_layers else 1, np.float32)
+    L_ = vxm.lib()
     t = Timer(torch, ctx)
     t.start()
     for i in range(steps):
         models[i % copies].forward(kv, x, ctx0 + i)
+        if synced:
+            ctx.check(L_.vxm_memcpy_d2h(ctx.h, host.ctypes.data_as(vxm.C.c_void_p), vxm._ptr(x), host.nbytes))
     ms = t.stop_ms()
     for m in models:
         m.check()
@@ -750,6 +757,8 @@ def main():
     gbs = sb / (us_step * 1e-6) / 1e9
     log(f"28-layer decode step: {us_step:.1f} us/token, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM), "
         f"finite={finite}")
+    us_sync, _ = bench_decode(ctx, torch, vxm, layers, L, args.copies, 256, args.steps, args.warmup, mode, synced=True)
+    log(f"28-layer decode step with one host read-back per token: {us_sync:.1f} us/token")
     lmu = None
     if not args.decode_only:
         us_u, fin_u, prm = bench_lm_update(ctx, torch, vxm, layers, 256, args.steps, args.warmup,
@@ -817,6 +826,10 @@ def main():
                    "decode_mode": args.mode, "context_start": 256, "context_end": 256 + args.steps},
         "us_per_step": round(us_step, 2),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "decode_synced": {"us_per_step": round(us_sync, 2),
+                          "note": "the same tokens with the 8 KB hidden state copied to the host after each one "
+                                  "(vxm_memcpy_d2h, which waits for it), the read-back per step of the reference's "
+                                  "synchronous vcpm_backend_compute_graph"},
         "step_bytes": int(sb),
         "gemv": res,
         "layer_decode_ctx512_us": round(us1, 3) if us1 is not None else None,
