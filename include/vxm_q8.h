@@ -72,12 +72,16 @@ int         vxm_set_path(vxm_ctx *ctx, int path);
 /* HIP graph capture of the context's stream: no counterpart in the reference
  * (its host re-issues every graph each step, src/ggml_backend.c:557-599).  For
  * callers that replay one fixed sequence of vxm_* calls with new contents in
- * the same device buffers (a decode step, a CFM step).  Between begin and end
- * the calls on the context are recorded, not run; vxm_graph_launch replays
- * the recording on the context's stream.  Run the sequence once eagerly
- * first: a call that would have to grow a scratch buffer (and so allocate and
- * synchronise) fails under capture with VXM_ERR_INVALID_ARG.  K-split tags
- * live in device memory, so every replay of a split product is exact. */
+ * the same device buffers (matmuls, norms, an encoder pass).  Between begin
+ * and end the calls on the context are recorded, not run; vxm_graph_launch
+ * replays the recording on the context's stream.  Host scalars (a decode
+ * position, a time step) are recorded with the values they had.  Run the
+ * sequence once eagerly first: a call that would have to grow a scratch
+ * buffer or set up a single-launch kernel's buffers (and so allocate and
+ * synchronise) fails under capture with VXM_ERR_INVALID_ARG.
+ * vxm_locdit_forward stages host-computed time embeddings and cannot be
+ * captured; vxm_cfm_solve records and replays its own Euler loop.  Every tag
+ * a kernel compares lives in device memory, so every replay is exact. */
 typedef struct vxm_graph vxm_graph;
 int vxm_capture_begin(vxm_ctx *ctx);
 int vxm_capture_end(vxm_ctx *ctx, vxm_graph **out);

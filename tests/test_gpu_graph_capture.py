@@ -116,3 +116,63 @@ def test_capture_refuses_scratch_growth(vxm_ctx, orc):
         ctx.sync()
         g.free()
         w.free()
+
+
+def test_capture_refuses_first_single_launch_blocks(orc):
+    """The single-launch LocEnc blocks set up their exchange buffers and block table
+    on their first eager evaluation; captured before that, the call fails with a
+    clear error (nothing is allocated into the recording), and after one eager
+    evaluation the same call captures and replays bit-identically, tagging anew
+    on every replay."""
+    import torch
+    import vxm
+    from test_lm_update_host import make_locenc
+
+    def dev(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+    with vxm.Context(0) as ctx:
+        cfg, w, _, _ = make_locenc(orc, 813, H=1024, L=2, nh=16, nkv=2, hd=128, F=4096, special=True)
+        enc = vxm.LocEnc(ctx, cfg, w)
+        x = dev(np.random.default_rng(814).normal(0, 1, (4, 64)).astype(np.float32))
+        out = torch.full((1024,), float("nan"), dtype=torch.float32, device="cuda:0")
+        try:
+            # one evaluation launch by launch: the context's scratch and the encoder's own
+            # buffers exist, the single launch's buffers do not yet
+            enc.set_block_mode(vxm.DECODE_KERNELS)
+            enc.forward(x, out)
+            ctx.sync()
+            enc.set_block_mode(vxm.DECODE_PERSISTENT)
+            ctx.capture_begin()
+            err = None
+            try:
+                enc.forward(x, out)
+            except vxm.VxmError as e:
+                err = e
+            finally:
+                try:
+                    ctx.capture_end().free()
+                except vxm.VxmError:
+                    pass
+            assert err is not None and err.code == 1 and "persistent blocks" in str(err) and "eager" in str(err), err
+            ref = enc.forward(x).cpu().numpy()   # eager: sets up the single launch's buffers
+            enc.check()
+            ctx.capture_begin()
+            try:
+                enc.forward(x, out)
+            finally:
+                g = ctx.capture_end()
+            try:
+                for _ in range(3):
+                    out.fill_(float("nan"))
+                    torch.cuda.synchronize()
+                    g.launch()
+                    ctx.sync()
+                    assert np.array_equal(out.cpu().numpy(), ref)
+                    enc.check()
+                    # eager launches between replays advance the same device epoch
+                    assert np.array_equal(enc.forward(x).cpu().numpy(), ref)
+            finally:
+                g.free()
+        finally:
+            enc.free()

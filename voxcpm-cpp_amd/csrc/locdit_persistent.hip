@@ -1151,6 +1151,14 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
     }
     vxm_lpersist *st = *stp;
     if (!st || st->L != L || st->key != key) {
+        // the exchange buffers and block table are made (hipMalloc, synchronous copies) by an eager
+        // call; under graph capture that would record nothing and fail
+        hipStreamCaptureStatus cap_st = hipStreamCaptureStatusNone;
+        VXM_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cap_st));
+        if (cap_st != hipStreamCaptureStatusNone)
+            return vxm_fail(ctx, VXM_ERR_INVALID_ARG,
+                            "persistent blocks: their buffers and block table are set up by an eager call; run "
+                            "one evaluation with these weights before capturing");
         vxm_locdit_persistent_free(st);
         *stp = nullptr;
         st = new vxm_lpersist();
