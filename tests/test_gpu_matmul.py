@@ -127,8 +127,8 @@ def test_decode_gemv_full_size_seed0(vxm_ctx, orc, N, K):
 # (path, N, K, M): the kernel vxm_mul_mat_q8_0_q8_0 runs for each is the one whose
 # int32 block sums vxm_block_dots_q8_0 returns -- chunked GEMV <C, R> (M < 8, K a
 # multiple of 1024 in {1, 2, 4, 6} KiB), generic GEMV, small-M MFMA (one or two wave
-# groups, K splits), the DMA-fed tile GEMM (64 x 64 or 64 x 128 tiles, K % 256 == 0,
-# K splits), the register-staged tiled GEMM (16- or 8-block stages, K splits)
+# groups, K splits), the DMA-fed tile GEMM (64 x 64, 64 x 128 or 128 x 128 tiles,
+# K % 256 == 0, K splits), the register-staged tiled GEMM (16- or 8-block stages, K splits)
 _PRODUCTION_DOTS = [
     (0, 6144, 2048, 1),     # decode gate/up GEMV <2, 2>
     (0, 2048, 6144, 1),     # decode down GEMV <6, 1>
@@ -142,6 +142,7 @@ _PRODUCTION_DOTS = [
     (2, 1024, 4096, 5),     # small-M at 5 rows (the block pipeline's choice)
     (0, 2048, 2048, 512),   # prefill O: tile GEMM, 64 x 64 tiles
     (0, 2560, 1024, 512),   # tile GEMM, 64 x 128 tiles (the prefill QKV choice)
+    (0, 8192, 256, 512),    # tile GEMM, 128 x 128 tiles (one full round of 256; long-prompt gate/up, O)
     (0, 256, 8192, 128),    # tile GEMM, four K splits (more blocks than one activation scale panel holds)
     (0, 1001, 512, 100),    # tile GEMM, ragged M and N (N % 4 != 0: no 16-byte stores)
     (3, 2048, 2048, 33),    # tiled, 16-block stages, K split

@@ -631,17 +631,20 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
 }
 
 // ---------------------------------------------------------------------------
-// Tiled Q8_0 x Q8_0 GEMM for prefill-sized M (> 64): one 64 x TN output tile
-// per workgroup (TN = 64 or 128, 512 threads), every operand byte brought
-// into LDS by direct HBM -> LDS loads (global_load_lds_dwordx4: lane l of an
-// instruction writes 16 bytes at M0 + 16 l) into a ring of kTileSlots stages,
-// three of them in flight while one is multiplied.
+// Tiled Q8_0 x Q8_0 GEMM for prefill-sized M (> 64): one TM x TN output tile
+// per workgroup (64 x 64, 64 x 128 or 128 x 128; 512 threads), every operand
+// byte brought into LDS by direct HBM -> LDS loads (global_load_lds_dwordx4:
+// lane l of an instruction writes 16 bytes at M0 + 16 l) into a ring of
+// kTileSlots stages, three of them in flight while one is multiplied.
 //
-// Waves: wave w owns the 32-row strip sm = w & 1 and the 64-column half
-// h = (w >> 1) & (H - 1) of the tile (H = TN / 64) for K part kp (KP = 4 / H
-// parts): the two blocks 2 kp, 2 kp + 1 of every SB-block stage (SB = 8 / H,
-// so a stage holds RB = 32 SB bytes of each operand row).  The K parts are
-// added in order through LDS at the end.
+// Waves: wave w owns the 32-row strip sm = w % WM (WM = TM / 32) and the
+// 64-column half h = (w / WM) % H of the tile (H = TN / 64) for K part
+// kp = w / (WM H) (KP = 8 / (WM H) parts): PAIRS block pairs from block
+// 2 PAIRS kp of every SB-block stage (SB = 8 / H for 64-row tiles, 4 for
+// 128 x 128, whose waves take both pairs of a stage: twice the blocks between
+// barriers, and half the operand bytes per output of 64 x 128).  A stage holds
+// RB = 32 SB bytes of each operand row.  The K parts are added in order
+// through LDS at the end.
 //
 // Per block a wave issues two v_mfma_i32_32x32x32_i8 (its 32 x 64 integer
 // block sums) and one two-block f32 outer product (the 2 x 32 x 32 scale
@@ -672,7 +675,6 @@ __global__ __launch_bounds__(kGemmThreads, VXM_GEMM_WAVES_PER_SIMD) void k_gemm_
 // block sums to dots[(m*N + n)*nb + b] instead (no scaling, no split fix-up).
 // ---------------------------------------------------------------------------
 constexpr int kTileSlots = 4;
-constexpr int kTileMaxBps = 192;      // K blocks per split (activation scale panel <= 25 KiB)
 constexpr int kTileThreads = 512;
 
 #ifdef VXM_TILE_TRACE
@@ -691,11 +693,13 @@ __device__ uint64_t vxm_tile_trace[256 * 8 * 64 * 4];
     } while (0)
 #endif
 
-template <int TN>
+template <int TM, int TN>
 struct TileCfg {
+    static constexpr int WM = TM / 32;                 // 32-row strips
     static constexpr int H = TN / 64;                  // 64-column halves
-    static constexpr int KP = 4 / H;                   // K parts
-    static constexpr int SB = 8 / H;                   // blocks per stage
+    static constexpr int KP = 8 / (WM * H);            // K parts
+    static constexpr int SB = TM == 64 ? 8 / H : 4;    // blocks per stage
+    static constexpr int PAIRS = SB / (2 * KP);        // block pairs of a wave per stage
     static constexpr int RB = SB * 32;                 // operand row bytes per stage
     static constexpr int R16 = RB / 16;                // 16-byte pieces per row
     // LDS position of piece p of row r: p ^ swz(r).  An operand read of 16 bytes per
@@ -704,18 +708,23 @@ struct TileCfg {
     // the odd rows of any 16 must each take 8 distinct pieces, and any 8 consecutive
     // rows too (the same reads served 8 lanes per 128 bytes)
     static __device__ __forceinline__ int swz(int r) { return R16 == 8 ? (r & 7) ^ ((r >> 3) & 1) : r & 15; }
-    static constexpr int ABytes = GM * RB, BBytes = TN * RB;
+    static constexpr int ABytes = TM * RB, BBytes = TN * RB;
     static constexpr int Slot = ABytes + BBytes + 1024;   // + TN x SB weight scales
     static constexpr int LoadsAB = (ABytes + BBytes) / 1024 / 8;   // operand loads per wave and stage
-    static constexpr int Red = KP * 2 * H * 32 * 64;   // floats of the K-part reduction
+    static constexpr int Red = KP * WM * H * 32 * 64;  // floats of the K-part reduction
+    static constexpr int MaxBps = TM == 64 ? 192 : 96;  // K blocks per split (activation scale panel)
+    static_assert((TM == 64 || TM == 128) && (TN == 64 || TN == 128) && WM * H * KP == 8, "eight waves");
+    static_assert(PAIRS >= 1 && SB == 2 * KP * PAIRS, "every wave takes whole block pairs of a stage");
     static_assert((ABytes + BBytes) % 8192 == 0, "operand loads must split evenly over the waves");
     static_assert(Red * 4 <= kTileSlots * Slot, "the reduction reuses the ring");
 };
 
-static size_t tile_lds_bytes(int tn, int bps) {
-    const int slot = tn == 128 ? TileCfg<128>::Slot : TileCfg<64>::Slot;
-    return (size_t)kTileSlots * slot + 1024 * (size_t)(bps / 8 + 1);
+static size_t tile_lds_bytes(int tm, int tn, int bps) {
+    const int slot = tm == 128 ? TileCfg<128, 128>::Slot : tn == 128 ? TileCfg<64, 128>::Slot : TileCfg<64, 64>::Slot;
+    return (size_t)kTileSlots * slot + 1024 * (size_t)(tm / 64) * (size_t)(bps / 8 + 1);
 }
+
+static int tile_max_bps(int tm) { return tm == 128 ? TileCfg<128, 128>::MaxBps : TileCfg<64, 64>::MaxBps; }
 
 // 16 bytes per lane from src into LDS at lds_base + 16 lane.
 __device__ __forceinline__ void lds_dma16(uint32_t lds_base, const void *src) {
@@ -771,7 +780,7 @@ __device__ __forceinline__ void ring_barrier() {   // orders LDS only: loads in 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int TN, bool DOTS>
+template <int TM, int TN, bool DOTS>
 __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd, const int8_t *__restrict__ wq,
     const uint16_t *__restrict__ wt, float *__restrict__ y, uint64_t *__restrict__ part, int *__restrict__ cnt,
@@ -779,13 +788,13 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     const uint32_t *__restrict__ epoch_p, int *__restrict__ err, int8_t *__restrict__ sq, uint16_t *__restrict__ sd,
     int variant,
     const vxm_qkv_epi qe) {
-    using C = TileCfg<TN>;
+    using C = TileCfg<TM, TN>;
     extern __shared__ __attribute__((aligned(16))) int8_t ring[];
     __shared__ int last_sh;
     const int id = blockIdx.x, xcd = id % 8, k8 = id / 8;
     const int tn = (k8 / tiles_m) * 8 + xcd, tm = k8 % tiles_m;
     if (tn >= tiles_n) return;
-    const int m0 = tm * GM, n0 = tn * TN;
+    const int m0 = tm * TM, n0 = tn * TN;
     const int nb = K / 32, nb4 = nb / 4;
     const int z = blockIdx.y;
     const int b0 = z * bps, b1 = min(nb, b0 + bps);
@@ -794,16 +803,16 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     const int pitch = 16 * (P + 1);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int sm = wave & 1, h = (wave >> 1) & (C::H - 1), kp = wave >> (C::H == 2 ? 2 : 1);
+    const int sm = wave % C::WM, h = (wave / C::WM) % C::H, kp = wave / (C::WM * C::H);
     const int lr = lane & 31, lh = lane >> 5;
-    const int j0 = 2 * kp;   // this wave's first block of a stage
+    const int j0 = 2 * C::PAIRS * kp;   // this wave's first block of a stage
     const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
     const int8_t *panel = ring + kTileSlots * C::Slot;
     VXM_TILE_TS(62, 0);
 
     // activation scale panel: piece f = 64 i + lane of instruction i is row f / (P + 1),
     // piece f % (P + 1) (the last piece of a row is padding and loads a valid dummy)
-    for (int i = wave; i <= P; i += 8) {
+    for (int i = wave; i < (TM / 64) * (P + 1); i += 8) {
         const int f = 64 * i + lane, row = f / (P + 1), pc = f % (P + 1);
         const int r = min(m0 + row, M - 1), q = pc < P ? pc : 0;
         lds_dma16(ring_lds + kTileSlots * C::Slot + 1024 * i, xd + (int64_t)r * nb + b0 + 8 * q);
@@ -816,10 +825,10 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
         const int kb0 = b0 + C::SB * st;
         if (i < C::LoadsAB) {
             const int q = wave * C::LoadsAB + i;
-            const int rr = q * (64 / C::R16) + lane / C::R16;   // row of A (< 64) then B
+            const int rr = q * (64 / C::R16) + lane / C::R16;   // row of A (< TM) then B
             const int pg = (lane % C::R16) ^ C::swz(rr);
-            const int8_t *src = rr < GM ? xq + (int64_t)min(m0 + rr, M - 1) * K
-                                        : wq + (int64_t)min(n0 + rr - GM, N - 1) * K;
+            const int8_t *src = rr < TM ? xq + (int64_t)min(m0 + rr, M - 1) * K
+                                        : wq + (int64_t)min(n0 + rr - TM, N - 1) * K;
             lds_dma16(base + q * 1024, src + kb0 * 32 + pg * 16);
         } else {
             // 16-byte piece p = 8 wave + lane of the stage's 1 KiB: 64-row group
@@ -841,8 +850,11 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     // LDS offsets of this lane's operand rows and scales
     const int ar = 32 * sm + lr, br0 = 64 * h + lr, br1 = br0 + 32, sr = 64 * h + 32 * lh + lr;
     const int a_off = ar * C::RB, b0_off = C::ABytes + br0 * C::RB, b1_off = C::ABytes + br1 * C::RB;
+    // (pair pr of the stage: blocks j0 + 2 pr, j0 + 2 pr + 1, 4 bytes further in the TN = 128 layout,
+    // the only one with more than one pair)
     const int s_off = C::ABytes + C::BBytes +
                       (C::H == 2 ? (sr >> 6) * 512 + (sr & 63) * 8 + j0 * 2 : (j0 >> 2) * 512 + sr * 8 + (j0 & 3) * 2);
+    static_assert(C::PAIRS == 1 || C::H == 2, "pairs past the first sit in the 4-block rows of the TN = 128 scales");
     const int8_t *pa_row = panel + ar * pitch;
 
     // operands of block j of a stage: this lane's 16 bytes of its A row and of its two B rows
@@ -880,66 +892,77 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     vm_wait_stages<L>(min(2, ns - 1));
     ring_barrier();   // the panel and stage 0 are in LDS
 
-    // Block pipeline: X = this stage's first block, Y = its second.  Each MFMA is
-    // followed by a third of the conversion of the other block -- Y of the stage
-    // before while X's MFMAs run, X while Y's run -- so the matrix core works
-    // under the VALU and no conversion waits for a product (scheduling fences
-    // keep that order).  Y starts as zeros, whose conversion adds nothing.  The
-    // loads of stage st + 3 go out first, into the slot that stage st - 1 freed
-    // at the last barrier.
+    // Block pipeline: X = the first block of a pair, Y = its second (a wave takes
+    // PAIRS pairs of every stage).  Each MFMA is followed by a third of the
+    // conversion of the other block -- Y of the pair before while X's MFMAs run, X
+    // while Y's run -- so the matrix core works under the VALU and no conversion
+    // waits for a product (scheduling fences keep that order).  The blocks are
+    // converted in K order.  Y starts as zeros, whose conversion adds nothing.
+    // The loads of stage st + 3 go out first, into the slot that stage st - 1
+    // freed at the last barrier.
     v16i xc0, xc1, yc0 = {}, yc1 = {};
     v32f xs, ys = {};
 #define VXM_FENCE __builtin_amdgcn_sched_barrier(0)
     for (int st = 0; st < ns; st++) {
         VXM_TILE_TS(st, 0);
         const int8_t *sb = ring + (st % kTileSlots) * C::Slot;
-        const uint32_t pa = *(const uint32_t *)(pa_row + 2 * (C::SB * st + j0));
-        const uint32_t pw = *(const uint32_t *)(sb + s_off);
-        const int kb = b0 + C::SB * st + j0;
+        uint32_t pa[C::PAIRS], pw[C::PAIRS];
+#pragma unroll
+        for (int pr = 0; pr < C::PAIRS; pr++) {
+            pa[pr] = *(const uint32_t *)(pa_row + 2 * (C::SB * st + j0 + 2 * pr));
+            pw[pr] = *(const uint32_t *)(sb + s_off + 4 * pr);
+        }
         const bool more = st + kTileSlots - 1 < ns;
         if (more) issue(st + kTileSlots - 1);
-        v4i xa, xw0, xw1, ya, yw0, yw1;
-        operands(sb, j0, xa, xw0, xw1);
-        operands(sb, j0 + 1, ya, yw0, yw1);
-        if (DOTS) {
-            xc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, xw0, v16i{}, 0, 0, 0);
-            xc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, xw1, v16i{}, 0, 0, 0);
-            yc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ya, yw0, v16i{}, 0, 0, 0);
-            yc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ya, yw1, v16i{}, 0, 0, 0);
-            dots_out(xc0, xc1, kb);
-            dots_out(yc0, yc1, kb + 1);
-        } else {
-            const float dax = vxm_h2f((uint16_t)pa), dwx = vxm_h2f((uint16_t)pw);
-            const float day = vxm_h2f((uint16_t)(pa >> 16)), dwy = vxm_h2f((uint16_t)(pw >> 16));
-            VXM_FENCE;
-            xs = __builtin_amdgcn_mfma_f32_32x32x1f32(dax, dwx, v32f{}, 0, 0, 0);
-            VXM_FENCE;
-            epi_part(yc0, yc1, ys, 0, 6);
-            VXM_FENCE;
-            xc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, xw0, v16i{}, 0, 0, 0);
-            VXM_FENCE;
-            epi_part(yc0, yc1, ys, 6, 11);
-            VXM_FENCE;
-            xc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, xw1, v16i{}, 0, 0, 0);
-            VXM_FENCE;
-            epi_part(yc0, yc1, ys, 11, 16);
-            VXM_FENCE;
-            ys = __builtin_amdgcn_mfma_f32_32x32x1f32(day, dwy, v32f{}, 0, 0, 0);
-            VXM_FENCE;
-            epi_part(xc0, xc1, xs, 0, 6);
-            VXM_FENCE;
-            yc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ya, yw0, v16i{}, 0, 0, 0);
-            VXM_FENCE;
-            epi_part(xc0, xc1, xs, 6, 11);
-            VXM_FENCE;
-            yc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ya, yw1, v16i{}, 0, 0, 0);
-            VXM_FENCE;
-            epi_part(xc0, xc1, xs, 11, 16);
-            VXM_FENCE;
-            // the sums are needed here, not after the stage wait: keep the conversions
-            // in this block (otherwise they sink past the barrier, behind the MFMAs)
+        v4i xa[C::PAIRS], xw0[C::PAIRS], xw1[C::PAIRS], ya[C::PAIRS], yw0[C::PAIRS], yw1[C::PAIRS];
 #pragma unroll
-            for (int v = 0; v < 16; v++) asm volatile("" ::"v"(acc[0][v]), "v"(acc[1][v]));
+        for (int pr = 0; pr < C::PAIRS; pr++) {
+            operands(sb, j0 + 2 * pr, xa[pr], xw0[pr], xw1[pr]);
+            operands(sb, j0 + 2 * pr + 1, ya[pr], yw0[pr], yw1[pr]);
+        }
+#pragma unroll
+        for (int pr = 0; pr < C::PAIRS; pr++) {
+            if (DOTS) {
+                const int kb = b0 + C::SB * st + j0 + 2 * pr;
+                xc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[pr], xw0[pr], v16i{}, 0, 0, 0);
+                xc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[pr], xw1[pr], v16i{}, 0, 0, 0);
+                yc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ya[pr], yw0[pr], v16i{}, 0, 0, 0);
+                yc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ya[pr], yw1[pr], v16i{}, 0, 0, 0);
+                dots_out(xc0, xc1, kb);
+                dots_out(yc0, yc1, kb + 1);
+            } else {
+                const float dax = vxm_h2f((uint16_t)pa[pr]), dwx = vxm_h2f((uint16_t)pw[pr]);
+                const float day = vxm_h2f((uint16_t)(pa[pr] >> 16)), dwy = vxm_h2f((uint16_t)(pw[pr] >> 16));
+                VXM_FENCE;
+                xs = __builtin_amdgcn_mfma_f32_32x32x1f32(dax, dwx, v32f{}, 0, 0, 0);
+                VXM_FENCE;
+                epi_part(yc0, yc1, ys, 0, 6);
+                VXM_FENCE;
+                xc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[pr], xw0[pr], v16i{}, 0, 0, 0);
+                VXM_FENCE;
+                epi_part(yc0, yc1, ys, 6, 11);
+                VXM_FENCE;
+                xc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[pr], xw1[pr], v16i{}, 0, 0, 0);
+                VXM_FENCE;
+                epi_part(yc0, yc1, ys, 11, 16);
+                VXM_FENCE;
+                ys = __builtin_amdgcn_mfma_f32_32x32x1f32(day, dwy, v32f{}, 0, 0, 0);
+                VXM_FENCE;
+                epi_part(xc0, xc1, xs, 0, 6);
+                VXM_FENCE;
+                yc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ya[pr], yw0[pr], v16i{}, 0, 0, 0);
+                VXM_FENCE;
+                epi_part(xc0, xc1, xs, 6, 11);
+                VXM_FENCE;
+                yc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ya[pr], yw1[pr], v16i{}, 0, 0, 0);
+                VXM_FENCE;
+                epi_part(xc0, xc1, xs, 11, 16);
+                VXM_FENCE;
+                // the sums are needed here, not after the stage wait: keep the conversions
+                // in this block (otherwise they sink past the barrier, behind the MFMAs)
+#pragma unroll
+                for (int v = 0; v < 16; v++) asm volatile("" ::"v"(acc[0][v]), "v"(acc[1][v]));
+            }
         }
         VXM_TILE_TS(st, 1);
         if (st + 1 < ns) {
@@ -958,24 +981,27 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     // K parts in order through LDS: red[kp][wave of the part][32 values][64 lanes]
     __syncthreads();   // every wave is done with the ring
     float *red = (float *)ring;
-    const int wi = wave & (2 * C::H - 1);
+    constexpr int WP = C::WM * C::H;           // waves of one K part
+    const int wi = wave % WP;                  // = sm + WM h
 #pragma unroll
     for (int v = 0; v < 16; v++) {
-        red[((kp * 2 * C::H + wi) * 32 + v) * 64 + lane] = acc[0][v];
-        red[((kp * 2 * C::H + wi) * 32 + 16 + v) * 64 + lane] = acc[1][v];
+        red[((kp * WP + wi) * 32 + v) * 64 + lane] = acc[0][v];
+        red[((kp * WP + wi) * 32 + 16 + v) * 64 + lane] = acc[1][v];
     }
     __syncthreads();
-    constexpr int PER = 2 * C::H * 32 * 64;   // floats of one K part
+    constexpr int PER = WP * 32 * 64;          // floats of one K part
     if (sq) {
         // gate/up with SwiGLU and Q8_0 (one split): columns 2n and 2n + 1 are gate n and
         // up n, so the 64 columns of a row in one wave half are one 32-value block of
         // p = vxm_swiglu(gate, up).  Four threads per (row, half): 16 columns each
         const int F = N / 2;
-        if (tid < 4 * GM * C::H) {
-            const int bi = tid >> 2, part = tid & 3, mi = bi % GM, g = bi / GM;
+        // whole waves take the same iterations (4 TM H is a multiple of 64), so the four
+        // lanes of a block always run together
+        for (int tq = tid; tq < 4 * TM * C::H; tq += kTileThreads) {
+            const int bi = tq >> 2, part = tq & 3, mi = bi % TM, g = bi / TM;
             const int r32 = mi & 31;
             const int v = 16 * (part >> 1) + 4 * (r32 >> 3) + (r32 & 3);
-            const int f = (((mi >> 5) + 2 * g) * 32 + v) * 64 + 32 * ((r32 >> 2) & 1) + 16 * (part & 1);
+            const int f = (((mi >> 5) + C::WM * g) * 32 + v) * 64 + 32 * ((r32 >> 2) & 1) + 16 * (part & 1);
             float gu[16];
 #pragma unroll
             for (int c4 = 0; c4 < 4; c4++) {
@@ -991,9 +1017,11 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
 #pragma unroll
             for (int e = 0; e < 8; e++) pv[e] = vxm_swiglu(gu[2 * e], gu[2 * e + 1]);
             const int m = m0 + mi;
-            const int64_t o = (int64_t)min(m, M - 1) * F + (n0 + 64 * g) / 2 + 8 * part;
-            // rows past M quantize too (the amax exchange needs all four lanes) but store nothing
-            quant_block_4lanes(pv, variant, sq + o, sd + o / 32, part == 0, m < M);
+            const bool live = m < M && n0 + 64 * g < N;   // N % 64 == 0: a half is in or out
+            const int64_t o = live ? (int64_t)m * F + (n0 + 64 * g) / 2 + 8 * part : 0;
+            // rows past M and a half past N quantize too (the amax exchange needs all four
+            // lanes) but store nothing
+            quant_block_4lanes(pv, variant, sq + o, sd + o / 32, part == 0, live);
         }
         return;
     }
@@ -1013,8 +1041,8 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
         }
         const int fw = f >> 11, v = (f >> 6) & 31, fl = f & 63;
         const int vv = v & 15;
-        const int m = m0 + 32 * (fw & 1) + 8 * (vv >> 2) + 4 * (fl >> 5) + (vv & 3);
-        const int n = n0 + 64 * (fw >> 1) + 32 * (v >> 4) + (fl & 31);
+        const int m = m0 + 32 * (fw % C::WM) + 8 * (vv >> 2) + 4 * (fl >> 5) + (vv & 3);
+        const int n = n0 + 64 * (fw / C::WM) + 32 * (v >> 4) + (fl & 31);
         if (m >= M) continue;
         if (qe.q_out) {
             // k_rope_kv on columns n .. n + 3 of token m (one split, N % 4 == 0): two
@@ -1084,33 +1112,47 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     }
     __syncthreads();
     if (!last_sh) return;
+    // thread t adds elements t + 512 j, EPR at a time: every word of a round (EPR x splits)
+    // is requested before any tag is checked, so a round costs one memory round trip
+    constexpr int EPT = TM * TN / kTileThreads, EPR = 8;
+    static_assert(EPT % EPR == 0, "whole rounds");
     bool stale = false;
-    for (int e = tid; e < GM * TN; e += kTileThreads) {
-        const int m = m0 + e / TN, n = n0 + e % TN;
-        if (m >= M || n >= N) continue;
-        const int64_t i = (int64_t)m * N + n;
-        uint64_t w[kGemmMaxSplits];
+    for (int j0 = 0; j0 < EPT; j0 += EPR) {
+        uint64_t w[EPR][kGemmMaxSplits];
 #pragma unroll
-        for (int zz = 0; zz < kGemmMaxSplits; zz++)
-            w[zz] = zz < splits ? __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                : ((uint64_t)epoch << 32);
-        float s = 0.0f;
-        bool st_e = false;
+        for (int j = 0; j < EPR; j++) {
+            const int e = tid + kTileThreads * (j0 + j), m = m0 + e / TN, n = n0 + e % TN;
+            const bool live = m < M && n < N;
+            const int64_t i = live ? (int64_t)m * N + n : 0;
 #pragma unroll
-        for (int zz = 0; zz < kGemmMaxSplits; zz++) {
-            if (zz >= splits) break;
-            uint64_t v = w[zz];
-            for (int spin = 0; (uint32_t)(v >> 32) != epoch && spin < kGemmSpin; spin++) {
-                __builtin_amdgcn_s_sleep(1);
-                v = __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            st_e |= (uint32_t)(v >> 32) != epoch;
-            const float p = __uint_as_float((uint32_t)v);
-            s = zz ? s + p : p;
+            for (int zz = 0; zz < kGemmMaxSplits; zz++)
+                w[j][zz] = (live && zz < splits)
+                               ? __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                               : ((uint64_t)epoch << 32);
         }
-        // a partial that never arrived: a visible NaN and the context's error word
-        y[i] = st_e ? __builtin_nanf("") : s;
-        stale |= st_e;
+#pragma unroll
+        for (int j = 0; j < EPR; j++) {
+            const int e = tid + kTileThreads * (j0 + j), m = m0 + e / TN, n = n0 + e % TN;
+            if (m >= M || n >= N) continue;
+            const int64_t i = (int64_t)m * N + n;
+            float s = 0.0f;
+            bool st_e = false;
+#pragma unroll
+            for (int zz = 0; zz < kGemmMaxSplits; zz++) {
+                if (zz >= splits) break;
+                uint64_t v = w[j][zz];
+                for (int spin = 0; (uint32_t)(v >> 32) != epoch && spin < kGemmSpin; spin++) {
+                    __builtin_amdgcn_s_sleep(1);
+                    v = __hip_atomic_load(part + zz * MN + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                st_e |= (uint32_t)(v >> 32) != epoch;
+                const float p = __uint_as_float((uint32_t)v);
+                s = zz ? s + p : p;
+            }
+            // a partial that never arrived: a visible NaN and the context's error word
+            y[i] = st_e ? __builtin_nanf("") : s;
+            stale |= st_e;
+        }
     }
     if (stale) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1400,14 +1442,14 @@ __global__ void k_sum_parts(const float *__restrict__ p, int n, int64_t stride, 
 // CU.  tile_n > 0: k_gemm_q8_0_tile with 64 x tile_n tiles instead.
 struct GemmPlan {
     int tiles_m, tiles_n, splits, bps, ks;
-    int tile_n;
+    int tile_n, tile_m;
 };
 
 static GemmPlan gemm_plan(vxm_ctx *ctx, int64_t M, int N, int nb) {
     GemmPlan p;
     p.tiles_m = (int)((M + GM - 1) / GM);
     p.tiles_n = (N + GN - 1) / GN;
-    p.tile_n = 0;
+    p.tile_n = p.tile_m = 0;
     p.ks = p.tiles_m == 1 ? 16 : 8;
     int s = 1;
     while (s < kGemmMaxSplits && (int64_t)p.tiles_m * p.tiles_n * s < ctx->n_cu &&
@@ -1422,29 +1464,49 @@ static GemmPlan gemm_plan(vxm_ctx *ctx, int64_t M, int N, int nb) {
 #define VXM_GEMM_TILE 1
 #endif
 
-// k_gemm_q8_0_tile plan: the tile width (64 or 128 columns) and K split with the
-// fewest block steps on the busiest CU, one workgroup per CU: rounds of the grid
-// x blocks per split x tile width (a 64 x 128 step costs twice a 64 x 64 one:
-// the per-block conversion work is per output), plus a fix-up charge per round
-// when the K is split.  Ties go to the wider tile (fewer operand bytes per
-// output).  Splits keep whole 8-block steps and at most kTileMaxBps blocks (the
-// activation scale panel); their partial words must fit max_split_bytes.
-// Returns false when the shape is not the tile kernel's (K % 256, alignment).
+// Relative cost of a 128 x 128 block step per output against a 64-row tile's:
+// twice the blocks per wave between barriers and half the operand bytes per
+// output.  Percent (measured: a 128 x 128 tile of 64 blocks takes 1.57x the time
+// of a 64 x 128 one).
+#ifndef VXM_TILE128_COST
+#define VXM_TILE128_COST 79
+#endif
+// Charge of a K split, in block steps per round (the tagged partial words and
+// the last workgroup's fix-up).
+#ifndef VXM_TILE_SPLIT_CHARGE
+#define VXM_TILE_SPLIT_CHARGE 24
+#endif
+
+// k_gemm_q8_0_tile plan: the tile (64 x 64, 64 x 128 or 128 x 128) and K split
+// with the fewest block steps on the busiest CU, one workgroup per CU: rounds of
+// the grid x blocks per split x tile outputs (the per-block conversion work is
+// per output; a 128 x 128 step is charged VXM_TILE128_COST percent of four
+// 64 x 64 steps), plus a fix-up charge per round when the K is split.  Ties go
+// to the larger tile (fewer operand bytes per output).  Splits keep whole
+// 8-block steps and at most the tile's MaxBps blocks (the activation scale
+// panel); their partial words must fit max_split_bytes.  Returns false when the
+// shape is not the tile kernel's (K % 256, alignment).
 static bool tile_plan(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                       size_t max_split_bytes, GemmPlan &best) {
     const int N = (int)w->n, nb = (int)(w->k / 32);
     if (!VXM_GEMM_TILE || !w->dt || nb % 8 != 0 || ((uintptr_t)xq & 15) || ((uintptr_t)xd & 15)) return false;
     int64_t best_cost = -1;
-    for (int tn : {128, 64}) {
+    const int shapes[3][2] = {{128, 128}, {64, 128}, {64, 64}};
+    for (const auto &sh : shapes) {
+        const int tm = sh[0], tn = sh[1];
         for (int s = 1; s <= kGemmMaxSplits; s++) {
             const int bps = ((nb + s - 1) / s + 7) / 8 * 8;
             const int splits = (nb + bps - 1) / bps;
-            if (bps > kTileMaxBps || splits != s) continue;
+            if (bps > tile_max_bps(tm) || splits != s) continue;
+            // 128 x 128 tiles unsplit only: their 16K tagged partial words per split cost
+            // ~50 us per launch in the measured split plans
+            if (tm == 128 && splits > 1) continue;
             if (splits > 1 && (size_t)splits * M * N * sizeof(uint64_t) > max_split_bytes)
                 continue;
-            const int tiles_m = (int)((M + GM - 1) / GM), tiles_n = (N + tn - 1) / tn;
+            const int tiles_m = (int)((M + tm - 1) / tm), tiles_n = (N + tn - 1) / tn;
             const int64_t wgs = (int64_t)tiles_m * tiles_n * splits, rounds = (wgs + ctx->n_cu - 1) / ctx->n_cu;
-            const int64_t cost = rounds * (bps + (splits > 1 ? 24 : 0)) * tn;
+            int64_t cost = rounds * (bps + (splits > 1 ? VXM_TILE_SPLIT_CHARGE : 0)) * tn * (tm / 64) * 100;
+            if (tm == 128) cost = cost * VXM_TILE128_COST / 100;
             if (best_cost < 0 || cost < best_cost) {
                 best_cost = cost;
                 best.tiles_m = tiles_m;
@@ -1453,6 +1515,7 @@ static bool tile_plan(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const
                 best.bps = bps;
                 best.ks = 0;
                 best.tile_n = tn;
+                best.tile_m = tm;
             }
         }
     }
@@ -1461,21 +1524,21 @@ static bool tile_plan(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const
 
 // The tile kernel's dynamic LDS (4 stages + the scale panel, up to 157 KiB) is
 // above the default limit: raise it once per device for each instantiation.
-template <int TN, bool DOTS>
+template <int TM, int TN, bool DOTS>
 static int launch_gemm_tile_t(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
                               float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, const uint32_t *epoch,
                               int8_t *sq, uint16_t *sd, int variant, const vxm_qkv_epi &qe) {
     static std::atomic<uint64_t> attr_done{0};
     const uint64_t bit = 1ull << (ctx->device & 63);
     if (!(attr_done.load() & bit)) {
-        VXM_HIP(ctx, hipFuncSetAttribute((const void *)k_gemm_q8_0_tile<TN, DOTS>,
+        VXM_HIP(ctx, hipFuncSetAttribute((const void *)k_gemm_q8_0_tile<TM, TN, DOTS>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         (int)tile_lds_bytes(TN, kTileMaxBps)));
+                                         (int)tile_lds_bytes(TM, TN, tile_max_bps(TM))));
         attr_done.fetch_or(bit);
     }
     const int grid_x = 8 * p.tiles_m * ((p.tiles_n + 7) / 8);
-    hipLaunchKernelGGL((k_gemm_q8_0_tile<TN, DOTS>), dim3(grid_x, p.splits), dim3(kTileThreads),
-                       (unsigned)tile_lds_bytes(TN, p.bps), ctx->stream, xq, xd, w->qs, w->dt, y, part, cnt, dots,
+    hipLaunchKernelGGL((k_gemm_q8_0_tile<TM, TN, DOTS>), dim3(grid_x, p.splits), dim3(kTileThreads),
+                       (unsigned)tile_lds_bytes(TM, TN, p.bps), ctx->stream, xq, xd, w->qs, w->dt, y, part, cnt, dots,
                        (int)M, (int)w->n, (int)w->k, p.tiles_m, p.tiles_n, p.bps, p.splits, epoch, ctx->dev_err,
                        sq, sd, variant, qe);
     return VXM_OK;
@@ -1489,9 +1552,11 @@ static int launch_gemm_tile(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq,
                             float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, const uint32_t *epoch,
                             int8_t *sq = nullptr, uint16_t *sd = nullptr, int variant = 0,
                             const vxm_qkv_epi &qe = vxm_qkv_epi{}) {
+    if (p.tile_m == 128)
+        return launch_gemm_tile_t<128, 128, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant, qe);
     return p.tile_n == 128
-               ? launch_gemm_tile_t<128, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant, qe)
-               : launch_gemm_tile_t<64, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant, qe);
+               ? launch_gemm_tile_t<64, 128, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant, qe)
+               : launch_gemm_tile_t<64, 64, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant, qe);
 }
 
 template <int KS>
@@ -1515,7 +1580,7 @@ static void launch_gemm_dots_ks(vxm_ctx *ctx, const vxm_weight *w, const int8_t 
 // Buffer-load offsets are 32-bit: every row tile of A and W must lie below 2 GiB.
 static bool gemm_fits(int64_t M, int64_t N, int64_t K) {
     const int64_t lim = (int64_t)1 << 31;
-    return (M + GM) * K < lim && (N + GN) * K < lim;
+    return (M + 128) * K < lim && (N + 128) * K < lim;
 }
 
 // Buffers of the public matmul entries' K splits when the caller brings them
