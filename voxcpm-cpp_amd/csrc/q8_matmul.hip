@@ -760,6 +760,19 @@ __device__ __forceinline__ void lds_dma16_8(uint32_t lds_base, const void *src) 
         : "memory", "scc");
 }
 
+// Two tagged 64-bit words in one 16-byte store that bypasses the non-coherent
+// caches (sc1): each 8-byte half is written as an agent-scope relaxed atomic
+// store of that word would be (the same instruction's 8-byte form), so a
+// reader checking each word's tag sees the old or the new word.  p is 16-byte
+// aligned.  A store of more than 8 bytes reads its data registers after
+// issue, and the compiler's hazard checks do not see into the asm: the s_nop
+// keeps the next instructions from overwriting them first.
+__device__ __forceinline__ void store_words2_sc1(uint64_t *p, uint64_t a, uint64_t b) {
+    typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
+    const v4u_t v = {(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
+    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p), "v"(v) : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void vm_wait() {
     static_assert(N >= 0 && N <= 63, "vmcnt range");
@@ -1086,6 +1099,14 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
         const int64_t idx = (int64_t)m * N + n;
         if (vec && n + 3 < N) {
             *(float4 *)(y + idx) = s;
+            continue;
+        }
+        if (splits > 1 && (N & 3) == 0 && n + 3 < N) {
+            // four partial words as two 16-byte stores (idx and z M N are even: aligned)
+            const uint64_t tag = (uint64_t)epoch << 32;
+            uint64_t *dst = part + (int64_t)z * MN + idx;
+            store_words2_sc1(dst, tag | __float_as_uint(s.x), tag | __float_as_uint(s.y));
+            store_words2_sc1(dst + 2, tag | __float_as_uint(s.z), tag | __float_as_uint(s.w));
             continue;
         }
         const float sv[4] = {s.x, s.y, s.z, s.w};
@@ -1471,6 +1492,9 @@ static GemmPlan gemm_plan(vxm_ctx *ctx, int64_t M, int N, int nb) {
 #ifndef VXM_TILE128_COST
 #define VXM_TILE128_COST 79
 #endif
+#ifndef VXM_TILE128_SPLITS
+#define VXM_TILE128_SPLITS 0
+#endif
 // Charge of a K split, in block steps per round (the tagged partial words and
 // the last workgroup's fix-up).
 #ifndef VXM_TILE_SPLIT_CHARGE
@@ -1498,9 +1522,9 @@ static bool tile_plan(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const
             const int bps = ((nb + s - 1) / s + 7) / 8 * 8;
             const int splits = (nb + bps - 1) / bps;
             if (bps > tile_max_bps(tm) || splits != s) continue;
-            // 128 x 128 tiles unsplit only: their 16K tagged partial words per split cost
-            // ~50 us per launch in the measured split plans
-            if (tm == 128 && splits > 1) continue;
+            // 128 x 128 tiles unsplit only: split, they measured far slower than the 64-row
+            // plans (O 2048 x 2048 at M = 512, 4 splits: 42 against 12.7 us)
+            if (tm == 128 && splits > 1 && !VXM_TILE128_SPLITS) continue;
             if (splits > 1 && (size_t)splits * M * N * sizeof(uint64_t) > max_split_bytes)
                 continue;
             const int tiles_m = (int)((M + tm - 1) / tm), tiles_n = (N + tn - 1) / tn;
