@@ -608,13 +608,14 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma(const float *__restrict_
     VXM_ATTN_TS(4);
 }
 
-// Spans above AKV keys: the same tiles, lane layouts and rounding steps in three
-// passes over chunks of AKV keys, the scores recomputed in each pass (from K rows
-// that the L2 mostly holds by then): 1. each query row's max over all its keys,
-// 2. its double sum of exp(s - max), 3. per chunk, p = e * (float)(1 / sum) into
-// LDS and the P V products, accumulated over the chunks in each wave's registers.
-// Every p has the value the one-pass kernel gives for the same score; only the
-// order of the double sum and of the fp32 P V sums (chunk by chunk) differ.
+// Spans above AKV keys: the same tiles, lane layouts and score arithmetic in one
+// pass over chunks of AKV keys with a running row max (every K and V row read
+// once, every score formed once).  Per chunk: the chunk's row max m_c over all 8
+// waves, m = max(m, m_c), the rescale a = exp(m_old - m) of the row's running
+// P V sums and double exp sum, e = exp(s - m) into LDS and the P V products.  At
+// the end the output is divided by the sum: o = (sum e v) * (float)(1 / sum e).
+// Against the one-pass kernel only the rounding differs (each chunk's rescale,
+// e instead of e / sum entering P V, and the summation orders).
 template <int HD>
 __global__ __launch_bounds__(ATH) void k_attention_mfma_long(const float *__restrict__ q,
                                                              const uint16_t *__restrict__ kc,
@@ -636,6 +637,7 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma_long(const float *__rest
     __shared__ __align__(16) _Float16 Vt[NW][HDH * VP];
     __shared__ float smax[AQ][NW];
     __shared__ double ssum[AQ][NW];
+    __shared__ float salpha[AQ], sinv[AQ];
     constexpr int QP = HD + 8;
     __shared__ __align__(16) _Float16 Qh[AQ * QP];
     static_assert(NW == 8 && VITEMS >= 1 && 4 * AQ * HD <= AQ * SP, "8 waves; the key-quarter sums reuse P's buffer");
@@ -696,40 +698,8 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma_long(const float *__rest
     auto live = [&](int i, int ncb, int b, int v) { return i < ncb && 32 * b + 8 * (v >> 2) + 4 * lh + (v & 3) < kvl; };
     v16f sc[SB];
     int cb0, ncb;
-    // pass 1: each query row's max over its keys (the lane's, its partner's, the waves')
-    float m = -INFINITY;
-    for (int c = 0; c < nch; c++) {
-        scores(c, sc, cb0, ncb);
-#pragma unroll
-        for (int i = 0; i < SB; i++)
-#pragma unroll
-            for (int v = 0; v < 16; v++)
-                if (live(i, ncb, cb0 + i, v)) m = fmaxf(m, sc[i][v]);
-    }
-    m = fmaxf(m, __shfl_xor(m, 32));
-    if (lh == 0) smax[lr][wave] = m;
-    __syncthreads();
-    m = smax[lr][0];
-#pragma unroll
-    for (int w = 1; w < NW; w++) m = fmaxf(m, smax[lr][w]);
-    // pass 2: the double sum of e = exp(s - max)
-    double sum = 0.0;
-    for (int c = 0; c < nch; c++) {
-        scores(c, sc, cb0, ncb);
-#pragma unroll
-        for (int i = 0; i < SB; i++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) sum += (double)(live(i, ncb, cb0 + i, v) ? expf(sc[i][v] - m) : 0.0f);
-    }
-    sum += __shfl_xor(sum, 32);
-    if (lh == 0) ssum[lr][wave] = sum;
-    __syncthreads();
-    sum = ssum[lr][0];
-#pragma unroll
-    for (int w = 1; w < NW; w++) sum += ssum[lr][w];
-    const float inv = kvl > 0 ? (float)(1.0 / sum) : 0.0f;
-    // pass 3: per chunk, P rows into LDS, then partial O = P V of key quarter kq of the
-    // chunk's blocks for dims [64 dh, 64 dh + 64), accumulated over the chunks
+    float mrow = -INFINITY;   // running max of row lr (the same in every lane and wave)
+    double lsum = 0.0;        // this lane's running double sum of e over its keys
     v16f o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) o[dt] = v16f{};
@@ -750,18 +720,49 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma_long(const float *__rest
                     vr[i][u][e] = *(const uint4 *)(vbh + (int64_t)min(r + e, kv_end - 1) * HD + d);
             }
         scores(c, sc, cb0, ncb);
+        // the chunk's row max (the lane's, its partner's, the waves')
+        float mc = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < SB; i++)
+#pragma unroll
+            for (int v = 0; v < 16; v++)
+                if (live(i, ncb, cb0 + i, v)) mc = fmaxf(mc, sc[i][v]);
+        mc = fmaxf(mc, __shfl_xor(mc, 32));
+        if (lh == 0) smax[lr][wave] = mc;
+        __syncthreads();   // every wave's chunk max
+        float mn = mrow;
+#pragma unroll
+        for (int w = 0; w < NW; w++) mn = fmaxf(mn, smax[lr][w]);
+        // rescale of the row's sums so far (0 for the first live chunk, 1 while m holds;
+        // a row with no live key yet keeps -inf and scale 1 over its zero sums)
+        const float alpha = mn == -INFINITY ? 1.0f : expf(mrow - mn);
+        mrow = mn;
+        if (wave == 0 && lh == 0) salpha[lr] = alpha;
+        lsum *= (double)alpha;
 #pragma unroll
         for (int i = 0; i < SB; i++) {
             if (i >= ncb) break;
             float pv[16];
 #pragma unroll
-            for (int v = 0; v < 16; v++) pv[v] = live(i, ncb, cb0 + i, v) ? expf(sc[i][v] - m) * inv : 0.0f;
+            for (int v = 0; v < 16; v++) {
+                pv[v] = live(i, ncb, cb0 + i, v) ? expf(sc[i][v] - mn) : 0.0f;
+                lsum += (double)pv[v];
+            }
 #pragma unroll
             for (int r4 = 0; r4 < 4; r4++)
                 *(float4 *)(Sc + lr * SP + 32 * (cb0 + i - cbase) + 8 * r4 + 4 * lh) =
                     make_float4(pv[4 * r4], pv[4 * r4 + 1], pv[4 * r4 + 2], pv[4 * r4 + 3]);
         }
-        __syncthreads();   // every wave's P rows of the chunk in LDS
+        __syncthreads();   // every wave's e rows of the chunk and the rows' rescales in LDS
+        // the partial P V of earlier chunks, rescaled to the new max (row of value v of
+        // the accumulators: 8 (v / 4) + 4 lh + v % 4)
+        float al[16];
+#pragma unroll
+        for (int v = 0; v < 16; v++) al[v] = salpha[8 * (v >> 2) + 4 * lh + (v & 3)];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) o[dt][v] = o[dt][v] * al[v];
 #pragma unroll
         for (int i = 0; i < VB; i++) {
             if (i >= nbq) break;
@@ -797,7 +798,17 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma_long(const float *__rest
                 }
             }
         }
-        __syncthreads();   // the chunk's P rows are read before the next chunk's overwrite them
+        __syncthreads();   // the chunk's e rows, maxima and rescales are read before the next chunk's
+    }
+    // the row's double sum (lanes, partner, waves) and its inverse for the output rows
+    lsum += __shfl_xor(lsum, 32);
+    if (lh == 0) ssum[lr][wave] = lsum;
+    __syncthreads();
+    if (wave == 0 && lh == 0) {
+        double sum = ssum[lr][0];
+#pragma unroll
+        for (int w = 1; w < NW; w++) sum += ssum[lr][w];
+        sinv[lr] = kvl > 0 ? (float)(1.0 / sum) : 0.0f;
     }
     // the key quarters in order through LDS (P's buffer is free)
     float *red = Sc;
@@ -811,6 +822,7 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma_long(const float *__rest
         for (int i = 8 * tid; i < AQ * HD; i += 8 * ATH) {
             const int qi = i / HD, d = i % HD;
             float v[8];
+            const float inv = sinv[qi];
 #pragma unroll
             for (int hf = 0; hf < 2; hf++) {
                 float4 s = *(const float4 *)(red + i + 4 * hf);
@@ -819,7 +831,7 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma_long(const float *__rest
                     const float4 t = *(const float4 *)(red + w * AQ * HD + i + 4 * hf);
                     s.x = s.x + t.x; s.y = s.y + t.y; s.z = s.z + t.z; s.w = s.w + t.w;
                 }
-                v[4 * hf] = s.x; v[4 * hf + 1] = s.y; v[4 * hf + 2] = s.z; v[4 * hf + 3] = s.w;
+                v[4 * hf] = s.x * inv; v[4 * hf + 1] = s.y * inv; v[4 * hf + 2] = s.z * inv; v[4 * hf + 3] = s.w * inv;
             }
             const int64_t o2 = (int64_t)(t0 + min(qi, nq - 1)) * nh * HD + h * HD + d;
             quant_block_4lanes(v, variant, xq + o2, xd + o2 / 32, (tid & 3) == 0, qi < nq);
@@ -834,6 +846,8 @@ __global__ __launch_bounds__(ATH) void k_attention_mfma_long(const float *__rest
                 const float4 t = *(const float4 *)(red + w * AQ * HD + i);
                 s.x = s.x + t.x; s.y = s.y + t.y; s.z = s.z + t.z; s.w = s.w + t.w;
             }
+            const float inv = sinv[qi];
+            s.x = s.x * inv; s.y = s.y * inv; s.z = s.z * inv; s.w = s.w * inv;
             *(float4 *)(out + (int64_t)(t0 + qi) * nh * HD + h * HD + d) = s;
         }
     }
