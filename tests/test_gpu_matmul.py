@@ -394,3 +394,22 @@ def test_stream_read_checksum(vxm_ctx):
     for h in hs:
         ref ^= np.bitwise_xor.reduce(h)
     assert int(np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))) == int(ref)
+
+
+@pytest.mark.parametrize("nbytes,offset", [(8192, 0), (16, 0), (65536, 0), (65552, 0), (8192, 4), (100, 0), (96, 16)])
+def test_memcpy_d2h_sizes(vxm_ctx, nbytes, offset):
+    """vxm_memcpy_d2h returns exactly the device bytes: small 16-byte-aligned copies
+    through the pinned staging buffer (the per-token hidden state), larger, unaligned
+    or ragged ones through the DMA copy; twice in a row with new contents."""
+    import ctypes
+    import torch
+    import vxm
+
+    for rep in range(2):
+        src = torch.randint(0, 256, (nbytes + offset,), dtype=torch.uint8, device="cuda:0")
+        want = src.cpu().numpy()[offset:]
+        got = np.full(nbytes, 0xA5, dtype=np.uint8)
+        vxm_ctx.check(
+            vxm.lib().vxm_memcpy_d2h(vxm_ctx.h, got.ctypes.data_as(ctypes.c_void_p),
+                                         ctypes.c_void_p(src.data_ptr() + offset), nbytes))
+        assert np.array_equal(got, want), (nbytes, offset, rep)

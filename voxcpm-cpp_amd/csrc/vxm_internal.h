@@ -42,6 +42,11 @@ struct vxm_ctx {
     // device address), or null with the reason in scratch_err
     unsigned char *scratch = nullptr;
     std::string scratch_err;
+    // pinned, device-mapped host staging of small device-to-host copies (the
+    // per-token hidden state): host and device addresses
+    void *pin_out = nullptr;
+    void *pin_out_dev = nullptr;
+    unsigned pin_seq = 0;   // sequence number the copy kernel writes after the data
 };
 
 // Device layout of a Q8_0 matrix (n_rows x k).  The GGUF row of k/32 34-byte
