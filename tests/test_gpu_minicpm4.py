@@ -293,11 +293,13 @@ def test_block_prefill_tiled_attention(vxm_ctx, orc, M, pos, hd):
     model.free()
 
 
-@pytest.mark.parametrize("M,F", [(100, 512), (512, 768)])
+@pytest.mark.parametrize("M,F", [(100, 512), (512, 768), (512, 6176)])
 def test_block_prefill_fused_swiglu_bit_identical(vxm_ctx, orc, M, F):
     """Above 64 rows the gate/up GEMM applies SwiGLU and quantizes the down projection's
     input in its own epilogue; PATH_MFMA_TILED runs the same GEMM followed by
-    k_swiglu_quant.  The block outputs and the appended KV rows are identical bit for bit."""
+    k_swiglu_quant.  The block outputs and the appended KV rows are identical bit for bit.
+    F = 6176: 2F % 128 == 64, so the last 128 x 128 tile's second 64-column half lies
+    past N and its epilogue must store nothing."""
     import vxm
 
     rng = np.random.default_rng(41 + M)
