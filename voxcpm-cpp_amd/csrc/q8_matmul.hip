@@ -797,7 +797,7 @@ template <int TM, int TN, bool DOTS>
 __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd, const int8_t *__restrict__ wq,
     const uint16_t *__restrict__ wt, float *__restrict__ y, uint64_t *__restrict__ part, int *__restrict__ cnt,
-    int32_t *__restrict__ dots, int M, int N, int K, int tiles_m, int tiles_n, int bps, int splits,
+    int32_t *__restrict__ dots, int M, int N, int K, int tiles_m, int tiles_n, int bps, int splits, int n_base,
     const uint32_t *__restrict__ epoch_p, int *__restrict__ err, int8_t *__restrict__ sq, uint16_t *__restrict__ sd,
     int variant,
     const vxm_qkv_epi qe) {
@@ -807,7 +807,7 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
     const int id = blockIdx.x, xcd = id % 8, k8 = id / 8;
     const int tn = (k8 / tiles_m) * 8 + xcd, tm = k8 % tiles_m;
     if (tn >= tiles_n) return;
-    const int m0 = tm * TM, n0 = tn * TN;
+    const int m0 = tm * TM, n0 = n_base + tn * TN;   // n_base: this launch's first column (a multiple of 128)
     const int nb = K / 32, nb4 = nb / 4;
     const int z = blockIdx.y;
     const int b0 = z * bps, b1 = min(nb, b0 + bps);
@@ -846,7 +846,7 @@ __global__ __launch_bounds__(kTileThreads, 1) void k_gemm_q8_0_tile(
         } else {
             // 16-byte piece p = 8 wave + lane of the stage's 1 KiB: 64-row group
             // p >> 5 (TN = 128) or 4-block step p >> 5 (TN = 64), rows 2 (p & 31) ..
-            const int p = 8 * wave + (lane & 7), g = C::H == 2 ? 2 * tn + (p >> 5) : tn,
+            const int p = 8 * wave + (lane & 7), g = n0 / 64 + (C::H == 2 ? p >> 5 : 0),
                       c = C::H == 2 ? 0 : p >> 5;
             lds_dma16_8(base + C::ABytes + C::BBytes + 128 * wave,
                         wt + ((int64_t)g * nb4 + kb0 / 4 + c) * 256 + (p & 31) * 8);
@@ -1464,6 +1464,9 @@ __global__ void k_sum_parts(const float *__restrict__ p, int n, int64_t stride, 
 struct GemmPlan {
     int tiles_m, tiles_n, splits, bps, ks;
     int tile_n, tile_m;
+    // two-part tile plans (unsplit): columns [0, n_split) on tile_m x tile_n tiles,
+    // [n_split, N) on a second launch of tile_m1 x tile_n1 tiles; n_split = 0: one part
+    int n_split, tile_m1, tile_n1, tiles_m1, tiles_n1;
 };
 
 static GemmPlan gemm_plan(vxm_ctx *ctx, int64_t M, int N, int nb) {
@@ -1471,6 +1474,7 @@ static GemmPlan gemm_plan(vxm_ctx *ctx, int64_t M, int N, int nb) {
     p.tiles_m = (int)((M + GM - 1) / GM);
     p.tiles_n = (N + GN - 1) / GN;
     p.tile_n = p.tile_m = 0;
+    p.n_split = 0;
     p.ks = p.tiles_m == 1 ? 16 : 8;
     int s = 1;
     while (s < kGemmMaxSplits && (int64_t)p.tiles_m * p.tiles_n * s < ctx->n_cu &&
@@ -1494,6 +1498,11 @@ static GemmPlan gemm_plan(vxm_ctx *ctx, int64_t M, int N, int nb) {
 #endif
 #ifndef VXM_TILE128_SPLITS
 #define VXM_TILE128_SPLITS 0
+#endif
+// Charge of a second launch in a two-part plan, in 64 x 128 block steps (the
+// gap between two dependent launches, ~1.5 us).
+#ifndef VXM_TILE_PART_CHARGE
+#define VXM_TILE_PART_CHARGE 5
 #endif
 // Charge of a K split, in block steps per round (the tagged partial words and
 // the last workgroup's fix-up).
@@ -1540,6 +1549,38 @@ static bool tile_plan(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const
                 best.ks = 0;
                 best.tile_n = tn;
                 best.tile_m = tm;
+                best.n_split = 0;
+            }
+        }
+    }
+    // two launches: whole rounds of 128 x 128 tiles over the first columns, the rest
+    // on 64-row tiles (a grid of 128 x 128 tiles that would leave its last round
+    // part-empty, e.g. 384 tiles for 512 x 12288)
+    const int tm128 = (int)((M + 127) / 128);
+    if (nb <= tile_max_bps(128) && tm128 <= ctx->n_cu && ctx->n_cu % tm128 == 0) {
+        const int cols = ctx->n_cu / tm128 * 128;   // columns of one full round
+        for (int r = 1; (int64_t)r * cols < N; r++) {
+            const int na = r * cols, rest = N - na;
+            for (int tn : {128, 64}) {
+                const int64_t tiles_b = (int64_t)((M + 63) / 64) * ((rest + tn - 1) / tn),
+                              rounds_b = (tiles_b + ctx->n_cu - 1) / ctx->n_cu;
+                const int64_t cost = (int64_t)r * nb * 256 * VXM_TILE128_COST + rounds_b * nb * tn * 100 +
+                                     (int64_t)VXM_TILE_PART_CHARGE * 128 * 100;
+                if (cost < best_cost) {
+                    best_cost = cost;
+                    best.tiles_m = tm128;
+                    best.tiles_n = na / 128;
+                    best.splits = 1;
+                    best.bps = ((nb + 7) / 8) * 8;
+                    best.ks = 0;
+                    best.tile_n = 128;
+                    best.tile_m = 128;
+                    best.n_split = na;
+                    best.tile_m1 = 64;
+                    best.tile_n1 = tn;
+                    best.tiles_m1 = (int)((M + 63) / 64);
+                    best.tiles_n1 = (rest + tn - 1) / tn;
+                }
             }
         }
     }
@@ -1550,7 +1591,8 @@ static bool tile_plan(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const
 // above the default limit: raise it once per device for each instantiation.
 template <int TM, int TN, bool DOTS>
 static int launch_gemm_tile_t(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
-                              float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, const uint32_t *epoch,
+                              float *y, int32_t *dots, const GemmPlan &p, int tiles_m, int tiles_n, int n_base,
+                              uint64_t *part, int *cnt, const uint32_t *epoch,
                               int8_t *sq, uint16_t *sd, int variant, const vxm_qkv_epi &qe) {
     static std::atomic<uint64_t> attr_done{0};
     const uint64_t bit = 1ull << (ctx->device & 63);
@@ -1560,12 +1602,26 @@ static int launch_gemm_tile_t(vxm_ctx *ctx, const vxm_weight *w, const int8_t *x
                                          (int)tile_lds_bytes(TM, TN, tile_max_bps(TM))));
         attr_done.fetch_or(bit);
     }
-    const int grid_x = 8 * p.tiles_m * ((p.tiles_n + 7) / 8);
+    const int grid_x = 8 * tiles_m * ((tiles_n + 7) / 8);
     hipLaunchKernelGGL((k_gemm_q8_0_tile<TM, TN, DOTS>), dim3(grid_x, p.splits), dim3(kTileThreads),
                        (unsigned)tile_lds_bytes(TM, TN, p.bps), ctx->stream, xq, xd, w->qs, w->dt, y, part, cnt, dots,
-                       (int)M, (int)w->n, (int)w->k, p.tiles_m, p.tiles_n, p.bps, p.splits, epoch, ctx->dev_err,
+                       (int)M, (int)w->n, (int)w->k, tiles_m, tiles_n, p.bps, p.splits, n_base, epoch, ctx->dev_err,
                        sq, sd, variant, qe);
     return VXM_OK;
+}
+
+template <bool DOTS>
+static int launch_gemm_tile_part(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq, const uint16_t *xd, int64_t M,
+                                 float *y, int32_t *dots, const GemmPlan &p, int tm, int tn, int tiles_m, int tiles_n,
+                                 int n_base, uint64_t *part, int *cnt, const uint32_t *epoch, int8_t *sq,
+                                 uint16_t *sd, int variant, const vxm_qkv_epi &qe) {
+    if (tm == 128)
+        return launch_gemm_tile_t<128, 128, DOTS>(ctx, w, xq, xd, M, y, dots, p, tiles_m, tiles_n, n_base, part, cnt,
+                                                  epoch, sq, sd, variant, qe);
+    return tn == 128 ? launch_gemm_tile_t<64, 128, DOTS>(ctx, w, xq, xd, M, y, dots, p, tiles_m, tiles_n, n_base, part,
+                                                         cnt, epoch, sq, sd, variant, qe)
+                     : launch_gemm_tile_t<64, 64, DOTS>(ctx, w, xq, xd, M, y, dots, p, tiles_m, tiles_n, n_base, part,
+                                                        cnt, epoch, sq, sd, variant, qe);
 }
 
 // sq != nullptr: SwiGLU + Q8_0 epilogue (gate/up weight with interleaved rows, one
@@ -1576,11 +1632,11 @@ static int launch_gemm_tile(vxm_ctx *ctx, const vxm_weight *w, const int8_t *xq,
                             float *y, int32_t *dots, const GemmPlan &p, uint64_t *part, int *cnt, const uint32_t *epoch,
                             int8_t *sq = nullptr, uint16_t *sd = nullptr, int variant = 0,
                             const vxm_qkv_epi &qe = vxm_qkv_epi{}) {
-    if (p.tile_m == 128)
-        return launch_gemm_tile_t<128, 128, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant, qe);
-    return p.tile_n == 128
-               ? launch_gemm_tile_t<64, 128, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant, qe)
-               : launch_gemm_tile_t<64, 64, DOTS>(ctx, w, xq, xd, M, y, dots, p, part, cnt, epoch, sq, sd, variant, qe);
+    int rc = launch_gemm_tile_part<DOTS>(ctx, w, xq, xd, M, y, dots, p, p.tile_m, p.tile_n, p.tiles_m, p.tiles_n, 0,
+                                         part, cnt, epoch, sq, sd, variant, qe);
+    if (rc || !p.n_split) return rc;
+    return launch_gemm_tile_part<DOTS>(ctx, w, xq, xd, M, y, dots, p, p.tile_m1, p.tile_n1, p.tiles_m1, p.tiles_n1,
+                                       p.n_split, part, cnt, epoch, sq, sd, variant, qe);
 }
 
 template <int KS>
