@@ -20,6 +20,9 @@
  *    contiguous floats, row m at x + m*K.  Outputs are [N, M]: y[m*N + n].
  *  - A quantized activation is two device arrays: xq int8 [M][K] and xd fp16
  *    bits [M][K/32] (the scale of block b of row m at xd[m*(K/32) + b]).
+ *  - A context and the objects made on it are used by one host thread at a
+ *    time (as a reference generation state is); separate contexts may be used
+ *    from separate threads.
  */
 #ifndef VXM_Q8_H
 #define VXM_Q8_H
@@ -89,7 +92,11 @@ int vxm_graph_launch(vxm_ctx *ctx, const vxm_graph *g);
 int vxm_graph_free(vxm_graph *g);
 
 /* Device memory and host-boundary copies (ggml_backend_tensor_set/get,
- * src/ggml_backend.c:356-380,422-457).  The copies return when complete. */
+ * src/ggml_backend.c:356-380,422-457).  The copies return when complete.  A
+ * device-to-host copy of at most 64 KiB from a 16-byte aligned source (a
+ * decode step's hidden state) is written by a copy kernel on the context's
+ * stream into pinned host staging, which the call polls briefly before it
+ * falls back to synchronising the stream. */
 int vxm_malloc(vxm_ctx *ctx, size_t bytes, void **out_dev);
 int vxm_free(vxm_ctx *ctx, void *dev);
 int vxm_memcpy_h2d(vxm_ctx *ctx, void *dst_dev, const void *src_host, size_t bytes);
