@@ -36,14 +36,16 @@ struct vxm_locdit {
     void *buf = nullptr;
     size_t buf_bytes = 0;
     float *seq = nullptr;      // [2S][H] residual stream of both segments
-    float *xh = nullptr;       // [P][H] raw in_proj(x)
     float *ch = nullptr;       // [Pc][H] raw cond_proj(cond)
     float *emb = nullptr;      // [R][H] sinusoid rows: steps' t, then dt
     float *th = nullptr;       // [R][H] time MLP hidden / output
     float *tc = nullptr;       // [R][H] bf16(t_feat + dt_feat) per step
-    float *vo = nullptr;       // [2P][feat] raw out_proj
+    float *vo = nullptr;       // raw out_proj [n_seg P][feat] as K-split slices
+    int vo_parts = 1;          //   (slice z at vo + z n_seg P feat)
     int8_t *aq = nullptr;      // Q8_0 scratch of the small projections
     uint16_t *ad = nullptr;
+    int8_t *xq8 = nullptr;     // Q8_0 of x [P][feat]: in_proj's input, written by the
+    uint16_t *xd8 = nullptr;   //   Euler update for the next evaluation
     // pinned staging of the host-computed embeddings, reused once its copy is done
     float *pin = nullptr;
     size_t pin_floats = 0;
@@ -91,25 +93,53 @@ __global__ void k_time_combine(const float *__restrict__ tt, const float *__rest
 // Both segments' sequences [mu(2), t(1), cond(Pc), x(P)] (src/locdit.c:296-317):
 // segment g < n_mu takes mu, the others zero rows; cond and x rows are the
 // raw projections plus bias, BF16 (src/locdit.c:232-252).  One workgroup per row.
+// The rows of one evaluation's sequence (src/locdit.c:216-300): per segment
+// mu (2 rows, or zeros), the time row, bf16(cond_proj + bias) of the cond
+// rows, bf16(in_proj(x) + bias) of the x rows.  The x rows' in_proj is formed
+// here from the Q8_0 of x (xq8 / xd8, K = feat) and the Q8_0 weight (wq / wd,
+// rows of feat): per output the exact int32 block sums, each times
+// d_w * d_x, added in block order -- the GEMV's terms (its lane tree adds
+// the terms of K = 64, two blocks, in the same single addition).
 __global__ void k_locdit_assemble(float *__restrict__ seq, const float *__restrict__ mu, int n_mu,
                                   const float *__restrict__ tc, const float *__restrict__ ch,
-                                  const float *__restrict__ cb, const float *__restrict__ xh,
-                                  const float *__restrict__ xb, int S, int Pc, int H) {
+                                  const float *__restrict__ cb, const int8_t *__restrict__ xq8,
+                                  const uint16_t *__restrict__ xd8, const int8_t *__restrict__ wq,
+                                  const uint16_t *__restrict__ wd, const float *__restrict__ xb, int S, int Pc, int H,
+                                  int feat) {
     const int row = blockIdx.x, g = row / S, r = row % S;
     float *dst = seq + (int64_t)row * H;
+    if (r >= 3 + Pc) {
+        const int xi = r - 3 - Pc, nb = feat / 32;
+        const int8_t *xr = xq8 + (int64_t)xi * feat;
+        const uint16_t *xs = xd8 + (int64_t)xi * nb;
+        for (int i = threadIdx.x; i < H; i += blockDim.x) {
+            const int8_t *wr = wq + (int64_t)i * feat;
+            float acc = 0.0f;
+            for (int b = 0; b < nb; b++) {
+                int si = 0;
+#pragma unroll
+                for (int k = 0; k < 32; k += 16) {
+                    const int4 wv = *(const int4 *)(wr + 32 * b + k), xv = *(const int4 *)(xr + 32 * b + k);
+                    si = vxm_dot16(wv, xv, si);
+                }
+                const float t = (float)si * (vxm_h2f(wd[(int64_t)i * nb + b]) * vxm_h2f(xs[b]));
+                acc = b ? acc + t : t;
+            }
+            float v = acc;
+            if (xb) v = v + xb[i];
+            dst[i] = vxm_bf16(v);
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < H; i += blockDim.x) {
         float v;
         if (r < 2) {
             v = (g < n_mu && mu) ? mu[r * H + i] : 0.0f;
         } else if (r == 2) {
             v = tc[i];
-        } else if (r < 3 + Pc) {
+        } else {
             v = ch[(int64_t)(r - 3) * H + i];
             if (cb) v = v + cb[i];
-            v = vxm_bf16(v);
-        } else {
-            v = xh[(int64_t)(r - 3 - Pc) * H + i];
-            if (xb) v = v + xb[i];
             v = vxm_bf16(v);
         }
         dst[i] = v;
@@ -121,16 +151,27 @@ __global__ void k_locdit_assemble(float *__restrict__ seq, const float *__restri
 // st = bf16(bf16(sum bf16(p q)) / bf16(sum bf16(q q) + 1e-8)), sums in double
 // in element order, v = bf16(ns + bf16(cfg * bf16(p - ns))), ns = bf16(q st));
 // x = bf16(x + bf16(dt * v)) (src/gen_step.c:624-627).  One workgroup;
-// dynamic LDS holds the 2n products (n <= kCfmMaxN).
+// dynamic LDS holds the 2n products (n <= kCfmMaxN).  vo is out_proj's K-split
+// slices, added in slice order as they are read (the fix-up launch's sums).
+// With xq8 the updated x also goes out as Q8_0 (the next evaluation's in_proj
+// input; the activation rule of `variant`, 32 lanes per block).
 constexpr int kCfmMaxN = 2048;   // 2 x 2048 doubles = 32 KiB of LDS
-__global__ __launch_bounds__(256) void k_cfm_update(const float *__restrict__ vo, const float *__restrict__ ob,
+__device__ __forceinline__ float parts_at(const vxm_parts &v, int64_t j) {
+    float s = v.p[j];
+    for (int z = 1; z < v.n; z++) s = s + v.p[z * v.stride + j];
+    return s;
+}
+
+__global__ __launch_bounds__(256) void k_cfm_update(const vxm_parts vo, const float *__restrict__ ob,
                                                     int feat, int n, int use_cfg, float cfg_value, float dt,
-                                                    float *__restrict__ x, float *__restrict__ v_out) {
+                                                    float *__restrict__ x, float *__restrict__ v_out,
+                                                    int8_t *__restrict__ xq8, uint16_t *__restrict__ xd8,
+                                                    int variant) {
     extern __shared__ double prod[];   // [2][n]
     __shared__ float st_sh;
     if (use_cfg) {
         for (int j = threadIdx.x; j < n; j += blockDim.x) {
-            float p = vo[j], q = vo[n + j];
+            float p = parts_at(vo, j), q = parts_at(vo, n + j);
             if (ob) { p = p + ob[j % feat]; q = q + ob[j % feat]; }
             p = vxm_bf16(p);
             q = vxm_bf16(q);
@@ -152,13 +193,14 @@ __global__ __launch_bounds__(256) void k_cfm_update(const float *__restrict__ vo
     }
     const float st = use_cfg ? st_sh : 0.0f;
     const float cfg_b = vxm_bf16(cfg_value);
+    // n % 32 == 0: the 32 lanes of a half wave hold one whole block of x
     for (int j = threadIdx.x; j < n; j += blockDim.x) {
-        float p = vo[j];
+        float p = parts_at(vo, j);
         if (ob) p = p + ob[j % feat];
         p = vxm_bf16(p);
         float v = p;
         if (use_cfg) {
-            float q = vo[n + j];
+            float q = parts_at(vo, n + j);
             if (ob) q = q + ob[j % feat];
             q = vxm_bf16(q);
             const float ns = vxm_bf16(q * st);
@@ -167,7 +209,26 @@ __global__ __launch_bounds__(256) void k_cfm_update(const float *__restrict__ vo
             v = vxm_bf16(ns + gg);
         }
         if (v_out) v_out[j] = v;
-        if (x) x[j] = vxm_bf16(x[j] + vxm_bf16(dt * v));
+        if (x) {
+            const float xn = vxm_bf16(x[j] + vxm_bf16(dt * v));
+            x[j] = xn;
+            if (xq8) {
+                // quantize_row_q8_0 of the block (k_quantize_q8_0's rule): d = amax / 127 as
+                // fp16, q = round(x * id)
+                float amax = fabsf(xn);
+#pragma unroll
+                for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+                const float d = __fdiv_rn(amax, 127.0f);
+                float id;
+                if (variant == VXM_QUANT_X86) id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+                else id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+                float q;
+                if (variant == VXM_QUANT_X86) q = fminf(fmaxf(rintf(xn * id), -128.0f), 127.0f);
+                else q = roundf(xn * id);
+                xq8[j] = (int8_t)(int)q;
+                if ((j & 31) == 0) xd8[j / 32] = vxm_f2h(d);
+            }
+        }
     }
 }
 
@@ -192,11 +253,13 @@ static int ensure_bufs(vxm_locdit *m, int64_t S, int64_t P, int64_t Pc, int64_t 
     const int64_t arows = std::max<int64_t>(std::max<int64_t>(P, Pc), std::max<int64_t>(R, 2 * P));
     struct Part { size_t bytes; void **dst; };
     std::vector<Part> parts = {
-        {(size_t)(2 * S * H * 4), (void **)&m->seq},  {(size_t)(P * H * 4), (void **)&m->xh},
+        {(size_t)(2 * S * H * 4), (void **)&m->seq},
         {(size_t)(std::max<int64_t>(Pc, 1) * H * 4), (void **)&m->ch},
         {(size_t)(R * H * 4), (void **)&m->emb},      {(size_t)(R * H * 4), (void **)&m->th},
-        {(size_t)(R * H * 4), (void **)&m->tc},       {(size_t)(2 * P * feat * 4), (void **)&m->vo},
+        {(size_t)(R * H * 4), (void **)&m->tc},
+        {(size_t)(VXM_MAX_PARTS * 2 * P * feat * 4), (void **)&m->vo},
         {(size_t)(arows * kq), (void **)&m->aq},      {(size_t)(arows * (kq / 32) * 2), (void **)&m->ad},
+        {(size_t)(P * feat), (void **)&m->xq8},       {(size_t)(P * (feat / 32) * 2), (void **)&m->xd8},
     };
     size_t total = 0;
     for (auto &p : parts) total += (p.bytes + 255) & ~(size_t)255;
@@ -274,19 +337,21 @@ static int time_features(vxm_locdit *m, const float *t_host, int rows, float dt)
 }
 
 // One batched LocDiT evaluation of n_seg segments (segment 0 takes mu when
-// n_mu = 1) for the time row tc_row; x [P][feat] on the device, ch already
-// holds the raw cond projection.  Leaves vo = raw out_proj [n_seg * P][feat].
-static int dit_eval(vxm_locdit *m, const float *x, int P, int Pc, int n_seg, const float *mu, int n_mu,
-                    const float *tc_row) {
+// n_mu = 1) for the time row tc_row; x [P][feat] on the device (its Q8_0
+// already in xq8 / xd8 when x_quantized: the Euler update wrote it), ch already
+// holds the raw cond projection.  Leaves vo = raw out_proj [n_seg * P][feat]
+// as K-split slices (vo_parts).
+static int dit_eval(vxm_locdit *m, const float *x, bool x_quantized, int P, int Pc, int n_seg, const float *mu,
+                    int n_mu, const float *tc_row) {
     vxm_ctx *ctx = m->ctx;
     const vxm_block_dims &d = m->dims;
     const int64_t H = d.H, feat = m->cfg.feat_dim, S = 3 + Pc + P, M = n_seg * S;
     const int var = ctx->quant_variant;
     int rc;
-    if ((rc = vxm_launch_quantize(ctx, x, P, feat, var, m->aq, m->ad))) return rc;
-    if ((rc = vxm_launch_mul_mat(ctx, m->in_proj, m->aq, m->ad, P, m->xh))) return rc;
+    if (!x_quantized && (rc = vxm_launch_quantize(ctx, x, P, feat, var, m->xq8, m->xd8))) return rc;
     hipLaunchKernelGGL(k_locdit_assemble, dim3((unsigned)M), dim3(256), 0, ctx->stream, m->seq, mu, n_mu, tc_row,
-                       m->ch, m->cond_bias, m->xh, m->in_bias, (int)S, Pc, (int)H);
+                       m->ch, m->cond_bias, m->xq8, m->xd8, m->in_proj->qs, m->in_proj->d, m->in_bias, (int)S, Pc,
+                       (int)H, (int)feat);
     VXM_CHECK_LAUNCH(ctx);
     // non-causal blocks, rope positions from 0 in each segment, fresh K/V per segment
     bool residual_added = false;   // the last block's residual already in seq (debug dump)
@@ -328,7 +393,9 @@ static int dit_eval(vxm_locdit *m, const float *x, int P, int Pc, int n_seg, con
                                      nullptr, m->aq, m->ad, var, P, (int)S)))
             return rc;
     }
-    return vxm_launch_mul_mat(ctx, m->out_proj, m->aq, m->ad, (int64_t)n_seg * P, m->vo);
+    // the K-split slices stay separate: the Euler update adds them as it reads them
+    return vxm_launch_mul_mat_parts(ctx, m->out_proj, m->aq, m->ad, (int64_t)n_seg * P, m->vo, VXM_MAX_PARTS,
+                                    &m->vo_parts);
 }
 
 static int check_dims(vxm_locdit *m, const float *x, const float *cond, int32_t P, int32_t Pc) {
@@ -379,12 +446,16 @@ static void cfm_graph_drop(vxm_locdit *m) {
     m->cfm_key.clear();
 }
 
-static int cfm_update(vxm_locdit *m, int P, int use_cfg, float cfg_value, float dt, float *x, float *v_out) {
+// x_q8: the updated x also goes out as Q8_0 (xq8 / xd8) for the next evaluation
+static int cfm_update(vxm_locdit *m, int P, int n_seg, int use_cfg, float cfg_value, float dt, float *x,
+                      float *v_out, bool x_q8) {
     vxm_ctx *ctx = m->ctx;
     const int feat = m->cfg.feat_dim, n = P * feat;
     const size_t lds = use_cfg ? (size_t)2 * n * sizeof(double) : 0;
-    hipLaunchKernelGGL(k_cfm_update, dim3(1), dim3(256), lds, ctx->stream, m->vo, m->out_bias, feat, n, use_cfg,
-                       cfg_value, dt, x, v_out);
+    const vxm_parts vo{m->vo, m->vo_parts, (int64_t)n_seg * n};
+    hipLaunchKernelGGL(k_cfm_update, dim3(1), dim3(256), lds, ctx->stream, vo, m->out_bias, feat, n, use_cfg,
+                       cfg_value, dt, x, v_out, x_q8 ? m->xq8 : nullptr, x_q8 ? m->xd8 : nullptr,
+                       ctx->quant_variant);
     VXM_CHECK_LAUNCH(ctx);
     return VXM_OK;
 }
@@ -503,9 +574,9 @@ extern "C" int vxm_locdit_forward(vxm_locdit *m, const float *x_dev, const float
     if (!out_dev) return vxm_fail(m->ctx, VXM_ERR_INVALID_ARG, "locdit: out is NULL");
     if ((rc = prepare(m, cond_dev, P, Pc, 1, 1))) return rc;
     if ((rc = time_features(m, &t, 1, dt))) return rc;
-    if ((rc = dit_eval(m, x_dev, P, Pc, 1, mu_dev, mu_dev ? 1 : 0, m->tc))) return rc;
+    if ((rc = dit_eval(m, x_dev, false, P, Pc, 1, mu_dev, mu_dev ? 1 : 0, m->tc))) return rc;
     // velocity = bf16(out_proj + bias), no CFG and no Euler step
-    return cfm_update(m, P, 0, 1.0f, 0.0f, nullptr, out_dev);
+    return cfm_update(m, P, 1, 0, 1.0f, 0.0f, nullptr, out_dev, false);
 }
 
 extern "C" int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev, int32_t P, int32_t Pc,
@@ -540,8 +611,9 @@ extern "C" int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev,
     const int64_t H = m->dims.H;
     auto euler_loop = [&]() -> int {
         for (int k = 0; k < live; k++) {
-            int r = dit_eval(m, x_dev, P, Pc, n_seg, mu_dev, 1, m->tc + (int64_t)k * H);
-            if (r == VXM_OK) r = cfm_update(m, P, use_cfg, cfg_value, dts[k], x_dev, nullptr);
+            // from the second step on, x's Q8_0 comes from the previous step's update
+            int r = dit_eval(m, x_dev, k > 0, P, Pc, n_seg, mu_dev, 1, m->tc + (int64_t)k * H);
+            if (r == VXM_OK) r = cfm_update(m, P, n_seg, use_cfg, cfg_value, dts[k], x_dev, nullptr, k + 1 < live);
             if (r) return r;
         }
         return VXM_OK;
