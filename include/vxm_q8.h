@@ -327,8 +327,9 @@ int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev, int32_t P,
  * values).  The persistent kernel runs every block of an evaluation in one
  * launch; it supports hidden 1024, FFN 4096, 16 query heads of (16 kv x 64)
  * or (2 kv x 128), at most 48 rows in segments of at most 32, on 256 CUs.
- * AUTO takes it for the 2 kv x 128 layout, where it measured faster, and
- * launches block by block otherwise; KERNELS always launches block by block;
+ * AUTO takes it wherever it applies (it measured faster than block-by-block
+ * launches at both layouts) and launches block by block otherwise; KERNELS
+ * always launches block by block;
  * PERSISTENT fails with VXM_ERR_NOT_IMPLEMENTED where the kernel does not
  * apply.  No reference counterpart (ggml evaluates one graph per call). */
 int vxm_locdit_set_block_mode(vxm_locdit *m, int mode);
@@ -387,7 +388,7 @@ int vxm_locenc_free(vxm_locenc *m);
  * [P][hidden]. */
 int vxm_locenc_forward(vxm_locenc *m, const float *x_dev, int32_t P, float *out_dev);
 /* Block strategy of vxm_locenc_forward, as vxm_locdit_set_block_mode (the
- * same persistent kernel; AUTO takes it for the 16 q / 2 kv x 128 layout), and
+ * same persistent kernel; AUTO takes it wherever it applies), and
  * the report of its device-side failures, as vxm_locdit_check.  No reference
  * counterpart. */
 int vxm_locenc_set_block_mode(vxm_locenc *m, int mode);

@@ -51,6 +51,7 @@ constexpr int kWaves = 8, kThreads = kWaves * 64, kG = 256;
 constexpr int kPollThreads = 7 * 64;   // waves 0-6 read exchanged words; wave 7 streams weights
 constexpr int kSpin = 1 << 17;         // poll rounds before giving up
 constexpr int kMaxM = 48, kMT = 3, kMP = 48, kMaxS = 32, kRB = 8;
+constexpr int kMaxQT = 3;   // QKV column tiles per workgroup
 constexpr int kH = 1024, kF = 4096, kNH = 16;
 constexpr int kXPitch = kH / 4 + kH / 32;   // words per row of a norm output (quants, then scales)
 constexpr int kPPitch = kF / 4 + kF / 32;   // words per row of the SwiGLU output
@@ -81,6 +82,8 @@ struct LShape {
     static constexpr int MISC = GN + kH * 4;                  // 8 doubles of reductions, then flags
     static constexpr int BYTES = MISC + 128;
     static_assert(16 * BO * 2 <= 1024, "O scales");
+    static_assert(UQ <= kMaxQT * (kG / kMT) && kMaxQT * 16 * kH <= RA_SC - RA && kMaxQT * 1024 <= RO - RA_SC,
+                  "QKV tiles of a workgroup");
     static_assert(kMP * 33 * 4 <= MISC - XR, "gate/up outputs in the row-owner area");
     static_assert(kWaves * 2 * kMT * 64 * 16 <= ST_SC - ST, "gate/up partial sums in the stage");
     static_assert(BYTES <= 160 * 1024, "LDS");
@@ -236,20 +239,20 @@ __device__ __forceinline__ void poll(const vxm_lparams &p, __amdgpu_buffer_rsrc_
 
 __device__ __forceinline__ int slot_of(int q, int r) { return 16 * (16 * (q >> 1) + r) + 8 * (q & 1); }
 
-// Rows [0, M) x blocks [kb0, kb0 + nb) of a Q8_0 channel (row pitch `pitch` words:
+// Rows [r0, r0 + M) x blocks [kb0, kb0 + nb) of a Q8_0 channel (row pitch `pitch` words:
 // qwords quant words, then one scale word per block; pitch, qwords, kb0 and nb even)
-// into the stage: quants in the block-slot layout [row tile][block][512], scales f32
-// [block][kMP].  A pair of quant words is one 8-byte piece of a block.
+// into the stage as rows 0 .. M - 1: quants in the block-slot layout [row tile][block][512],
+// scales f32 [block][kMP].  A pair of quant words is one 8-byte piece of a block.
 template <int NPT>
 __device__ __forceinline__ void poll_stage(const vxm_lparams &p, __amdgpu_buffer_rsrc_t rs, int pitch, int qwords,
-                                           int kb0, int nb, int M, uint32_t tag, uint8_t *lds, int st, int st_sc,
-                                           int *bail) {
+                                           int kb0, int nb, int r0, int M, uint32_t tag, uint8_t *lds, int st,
+                                           int st_sc, int *bail) {
     const int per = 4 * nb + nb / 2;   // pairs per row
     poll<NPT>(
         p, rs, M * per, tag,
         [&](int i) {
             const int m = i / per, j = i - m * per;
-            return (m * pitch + (j < 4 * nb ? 8 * kb0 + 2 * j : qwords + kb0 + 2 * (j - 4 * nb))) * 8;
+            return ((r0 + m) * pitch + (j < 4 * nb ? 8 * kb0 + 2 * j : qwords + kb0 + 2 * (j - 4 * nb))) * 8;
         },
         [&](int i, uint32_t a, uint32_t b) {
             const int m = i / per, j = i - m * per;
@@ -326,35 +329,54 @@ __device__ __forceinline__ void dma_scales(int wsc, const uint16_t *wd, int nbk,
     }
 }
 
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// The scale products d_w * d_x of a 16 x 16 int32 block product go to the matrix core
+// as well: v_mfma_f32_16x16x1_4b_f32 forms four 16 x 16 outer products at once (lane
+// 16 k + i supplies element i of block k's two vectors; block k's result sits in
+// registers 4 k .. 4 k + 3 in the layout of the int8 product's result).  Each product
+// has K = 1 and a zero accumulator, so it is the single fp32 rounding of d_w * d_x
+// that a VALU multiply gives, and the VALU is left with the convert and the fma per
+// value and block (3 -> 2 instructions).  Measured per LocDiT evaluation: 540 -> 535.5
+// us at 2 x 24 rows, 441 -> 439 at 2 x 11.  The gate/up products (mfma_run2) keep
+// their VALU scale products: with the same change there, 2 x 24 rows took 551 us.
+
 // acc[t][v] += products of tile rows 16 c + 4 q + v with stage rows 16 t + r (t < MT)
 // over the NB blocks from b0: weight tile (nbw blocks per row) at wt / wsc, stage
 // (nbs blocks) at st / st_sc.  MT and NB are compile-time: groups of up to 4 blocks
-// unroll, so each group's LDS reads are issued ahead of the products that need them.
+// unroll, so each group's LDS reads are issued ahead of the products that need them;
+// one scale product per row tile covers the group (blocks past NB get zero scales).
 template <int MT, int NB, int G = (NB < 4 ? NB : 4)>
 __device__ __forceinline__ void mfma_run(const uint8_t *lds, int wt, int wsc, int nbw, int c, int st, int st_sc,
                                          int nbs, int b0, int lane, float (&acc)[MT][4]) {
-    static_assert(NB % G == 0, "block groups");
+    static_assert(NB % G == 0 && G <= 4, "block groups");
     const int q = lane >> 4, r = lane & 15, sl = slot_of(q, r);
 #pragma unroll 1
-    for (int i0 = 0; i0 < NB; i0 += G)
-#pragma unroll
-    for (int i = 0; i < G; i++) {
-        const int b = b0 + i0 + i;
-        const long a = *(const long *)(lds + wt + (c * (nbw / 2) + (b >> 1)) * 1024 + (b & 1) * 512 + sl);
-        long bx[MT];
-        float dx[MT], dw[4];
+    for (int i0 = 0; i0 < NB; i0 += G) {
+        // scale products of blocks b0 + i0 + k, k < 4: lane (k = q, i = r) supplies weight
+        // row 16 c + r and stage row 16 t + r of block b0 + i0 + q
+        const bool sv = q < G;
+        const int bs = b0 + i0 + (sv ? q : 0);
+        const float aw = sv ? vxm_h2f(*(const uint16_t *)(lds + wsc + ((16 * c + r) * nbw + bs) * 2)) : 0.0f;
+        v16f sc[MT];
 #pragma unroll
         for (int t = 0; t < MT; t++) {
-            bx[t] = *(const long *)(lds + st + (t * nbs + b) * 512 + sl);
-            dx[t] = *(const float *)(lds + st_sc + (b * kMP + 16 * t + r) * 4);
+            const float bxs = sv ? *(const float *)(lds + st_sc + (bs * kMP + 16 * t + r) * 4) : 0.0f;
+            sc[t] = __builtin_amdgcn_mfma_f32_16x16x1f32(aw, bxs, v16f{}, 0, 0, 0);
         }
 #pragma unroll
-        for (int v = 0; v < 4; v++) dw[v] = vxm_h2f(*(const uint16_t *)(lds + wsc + ((16 * c + 4 * q + v) * nbw + b) * 2));
+        for (int i = 0; i < G; i++) {
+            const int b = b0 + i0 + i;
+            const long a = *(const long *)(lds + wt + (c * (nbw / 2) + (b >> 1)) * 1024 + (b & 1) * 512 + sl);
+            long bx[MT];
 #pragma unroll
-        for (int t = 0; t < MT; t++) {
-            const v4i cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bx[t], v4i{}, 0, 0, 0);
+            for (int t = 0; t < MT; t++) bx[t] = *(const long *)(lds + st + (t * nbs + b) * 512 + sl);
 #pragma unroll
-            for (int v = 0; v < 4; v++) acc[t][v] = __builtin_fmaf((float)cc[v], dw[v] * dx[t], acc[t][v]);
+            for (int t = 0; t < MT; t++) {
+                const v4i cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bx[t], v4i{}, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[t][v] = __builtin_fmaf((float)cc[v], sc[t][4 * i + v], acc[t][v]);
+            }
         }
     }
 }
@@ -552,9 +574,21 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
     const int wg = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int M = p.M, S = p.S, L = p.L;
     const int row = wg < M ? wg : -1;
-    const int uq = wg - 64, n_att = kNH * p.nseg * p.qb;
-    const bool is_qkv = uq >= 0 && uq < LS::UQ, is_att = wg < n_att, is_gu = wg >= 128;
-    const int ugu = wg - 128;
+    const int n_att = kNH * p.nseg * p.qb;
+    const bool is_att = wg < n_att;
+    // QKV units: (16-column tile, row group).  The rows are cut into ngq groups of at most
+    // 16 (one MFMA row tile), each read by wpq workgroups; workgroup jq of group gq takes
+    // the tiles jq, jq + wpq, ... (at most kMaxQT), so a workgroup reads only its group's
+    // activations from the exchange.
+    const int ngq = (M + 15) / 16, wpq = kG / ngq, gq = wg / wpq, jq = wg % wpq;
+    const int qrows = (M + ngq - 1) / ngq, qr0 = gq * qrows, nrq = min(qrows, M - qr0);
+    const int nct = gq < ngq && jq < LS::UQ ? (LS::UQ - 1 - jq) / wpq + 1 : 0;
+    const bool is_qkv = nct > 0;
+    // gate/up units: (64-row tile, row group): above 16 rows two groups on all 256
+    // workgroups, else one group on workgroups 128-255
+    const int ngg = M > 16 ? 2 : 1, gu = ngg == 2 ? wg : wg - 128;
+    const bool is_gu = gu >= 0;
+    const int ugu = gu & 127, grows = (M + ngg - 1) / ngg, gr0 = (gu >> 7) * grows, nrg = min(grows, M - gr0);
     const int oc = wg & 63, os = wg >> 6;   // O unit: 16-column tile, K quarter
     const int dc = wg & 31, ds = wg >> 5;   // down unit: 32-column tile, K eighth
     // loads per prefetch (16 rows x 2 blocks, or 64 f16 scale rows of 8 blocks, per instruction)
@@ -567,14 +601,22 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
     //   O(l) wait:        D(l); gate/up rows 0-31 (l) with G; QKV(l+1) with Q only
     //   GU(l) wait (G):   gate/up rows 32-63 (l), O(l+1)
     //   D(l) wait:        O(l+1) without G; QKV(l+1) with Q and G
-    // The waits before each phase's products count the loads issued after its own.
+    // The waits before each phase's products count the loads issued after its own.  A
+    // workgroup with Q and no G has one QKV tile (one row group: M <= 16), so nQKV loads;
+    // with Q and G every wait covers the QKV loads whatever their number (at most
+    // nO + kMaxQT nQKV = 60 loads are in flight, below vmcnt's 63).
+    static_assert(nO + kMaxQT * nQKV <= 63 && nD + nGA + nO <= 63, "loads in flight");
     auto issue_o = [&](const vxm_lblock &b) {
         dma_tile(LS::RO, 0, b.o_q, LS::QD, 16 * oc, LS::BO * os, LS::BO, dlane);
         dma_scales(LS::RO_SC, b.o_d, LS::QD / 32, 16 * oc, 16, LS::BO * os, LS::BO, dlane);
     };
     auto issue_qkv = [&](const vxm_lblock &b) {
-        dma_tile(LS::RA, 0, b.qkv_q, kH, 16 * uq, 0, 32, dlane);
-        dma_scales(LS::RA_SC, b.qkv_d, kH / 32, 16 * uq, 16, 0, 32, dlane);
+        for (int k = 0; k < kMaxQT; k++) {
+            if (k >= nct) break;
+            const int n0 = 16 * (jq + k * wpq);
+            dma_tile(LS::RA, k, b.qkv_q, kH, n0, 0, 32, dlane);
+            dma_scales(LS::RA_SC + 1024 * k, b.qkv_d, kH / 32, n0, 16, 0, 32, dlane);
+        }
     };
     auto issue_d = [&](const vxm_lblock &b) {
         for (int c = 0; c < 2; c++) dma_tile(LS::RD, c, b.dn_q, kF, 32 * dc + 16 * c, 16 * ds, 16, dlane);
@@ -638,38 +680,47 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
         // ---- QKV ----
         if (is_qkv) {
             const int tid = opaque_tid(), lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
-            // the rope (cos, sin) of this thread's two output pairs, fetched before the wait
-            // (row 16 t + r16 at position row % S; pairs i, i + 1 of the head)
-            const int n0 = 16 * uq + 4 * q4, ip = (n0 % LS::HD) / 2, mrow = min(16 * (tid >> 6) + r16, M - 1);
+            // the rope (cos, sin) of this thread's two output pairs, fetched before the wait:
+            // wave k < nct holds tile k, lane (q4, r16) row qr0 + r16 at position row % S,
+            // pairs i, i + 1 of the head
+            const int qk = min(tid >> 6, kMaxQT - 1);
+            const int n0 = 16 * (jq + qk * wpq) + 4 * q4, ip = (n0 % LS::HD) / 2, mrow = qr0 + min(r16, nrq - 1);
             float2 rc0 = make_float2(1.0f, 0.0f), rc1 = rc0;
-            if (!DMA && tid < MT * 64 && n0 < LS::QD + LS::KVD) {
+            if (!DMA && tid < nct * 64 && n0 < LS::QD + LS::KVD) {
                 rc0 = p.cs[(size_t)(mrow % S) * LS::HALF + ip];
                 rc1 = p.cs[(size_t)(mrow % S) * LS::HALF + ip + 1];
             }
             if (!DMA) {
                 const uint32_t tg = make_tag(ep, L, l, PH_X1);
-                poll_stage<(kMaxM * kXPitch / 2 + kPollThreads - 1) / kPollThreads>(
-                    p, chan_rsrc(p.x1, LS::WX * 8), kXPitch, kH / 4, 0, 32, M, tg, lds, LS::ST, LS::ST_SC, bail);
+                poll_stage<(16 * kXPitch / 2 + kPollThreads - 1) / kPollThreads>(
+                    p, chan_rsrc(p.x1, LS::WX * 8), kXPitch, kH / 4, 0, 32, qr0, nrq, tg, lds, LS::ST, LS::ST_SC, bail);
             } else {
                 vm_wait<0>();
             }
             lds_barrier();
             if (*bail) return;
             VXM_LTS(3);
-            zero_acc();
-            mfma_run<MT, 4>(lds, LS::RA, LS::RA_SC, 32, 0, LS::ST, LS::ST_SC, 32, 4 * wave, lane, acc);
+            float qacc[kMaxQT][1][4];
+#pragma unroll
+            for (int k = 0; k < kMaxQT; k++) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) qacc[k][0][v] = 0.0f;
+                if (k < nct) mfma_run<1, 4>(lds, LS::RA, LS::RA_SC, 32, k, LS::ST, LS::ST_SC, 32, 4 * wave, lane, qacc[k]);
+            }
             lds_barrier();
             VXM_LTS(16);
-            red_store<MT>(lds, LS::ST, wave, lane, acc);
+#pragma unroll
+            for (int k = 0; k < kMaxQT; k++)
+                if (k < nct) red_store<1>(lds, LS::ST + 8192 * k, wave, lane, qacc[k]);
             lds_barrier();
             VXM_LTS(17);
-            if (!DMA && tid < MT * 64) {
+            if (!DMA && tid < nct * 64) {
                 const uint32_t tg = make_tag(ep, L, l, PH_QKV);
-                const int t = tid >> 6, m = 16 * t + r16;
+                const int m = qr0 + r16;
                 float o[4];
-                red_sum<MT>(lds, LS::ST, 1, 0, t, lane, o);
-                if (m < M) {
-                    const int n = 16 * uq + 4 * q4;   // columns n .. n + 3: two pairs
+                red_sum<1>(lds, LS::ST + 8192 * qk, 1, 0, 0, lane, o);
+                if (r16 < nrq) {
+                    const int n = n0;   // columns n .. n + 3: two pairs
                     uint64_t *dst = p.qkv + (size_t)m * (LS::NQKV / 2) + n / 2;
 #pragma unroll
                     for (int e = 0; e < 2; e++) {
@@ -827,7 +878,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             if (!DMA) {
                 const uint32_t tg = make_tag(ep, L, l, PH_ATT);
                 poll_stage<(kMaxM * 9 * LS::BO / 2 + kPollThreads - 1) / kPollThreads>(
-                    p, chan_rsrc(p.att, LS::WA * 8), LS::APitch, LS::QD / 4, LS::BO * os, LS::BO, M, tg, lds, LS::ST,
+                    p, chan_rsrc(p.att, LS::WA * 8), LS::APitch, LS::QD / 4, LS::BO * os, LS::BO, 0, M, tg, lds, LS::ST,
                     LS::ST_SC, bail);
             } else {
                 issue_d(blk);
@@ -878,13 +929,15 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             lds_barrier();
         }
         VXM_LTS(10);
-        // ---- gate/up: 64 interleaved rows -> 32 SwiGLU outputs -> one Q8_0 block per row ----
+        // ---- gate/up: 64 interleaved rows -> 32 SwiGLU outputs -> one Q8_0 block per row,
+        // for the rows gr0 .. gr0 + nrg - 1 of this unit's group ----
         if (is_gu) {
+            constexpr int MTG = MT == 3 ? 2 : 1;   // row tiles of a group: at most 24 rows
             const int tid = opaque_tid(), lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
             if (!DMA) {
                 const uint32_t tg = make_tag(ep, L, l, PH_X2);
-                poll_stage<(kMaxM * kXPitch / 2 + kPollThreads - 1) / kPollThreads>(
-                    p, chan_rsrc(p.x2, LS::WX * 8), kXPitch, kH / 4, 0, 32, M, tg, lds, LS::ST, LS::ST_SC, bail);
+                poll_stage<(16 * MTG * kXPitch / 2 + kPollThreads - 1) / kPollThreads>(
+                    p, chan_rsrc(p.x2, LS::WX * 8), kXPitch, kH / 4, 0, 32, gr0, nrg, tg, lds, LS::ST, LS::ST_SC, bail);
             } else {
                 issue_gu_b(blk);
                 if (last) {
@@ -897,45 +950,43 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             lds_barrier();
             if (*bail) return;
             VXM_LTS(11);
-            zero_acc();
             // wave w: tiles 2 (w & 1) and 2 (w & 1) + 1 over the K quarter w >> 1
             const int ch = wave & 1, kq = wave >> 1;
-            float acc2[2][MT][4];
+            float acc2[2][MTG][4];
 #pragma unroll
             for (int cc = 0; cc < 2; cc++)
 #pragma unroll
-                for (int t = 0; t < MT; t++)
+                for (int t = 0; t < MTG; t++)
 #pragma unroll
                     for (int v = 0; v < 4; v++) acc2[cc][t][v] = 0.0f;
-            mfma_run2<MT, 8, 4>(lds, LS::RA, LS::RA_SC, 32, 2 * ch, LS::ST, LS::ST_SC, 32, 8 * kq, lane, acc2);
+            mfma_run2<MTG, 8, 4>(lds, LS::RA, LS::RA_SC, 32, 2 * ch, LS::ST, LS::ST_SC, 32, 8 * kq, lane, acc2);
             lds_barrier();
             VXM_LTS(18);
             {
-                float4 *red = (float4 *)(lds + LS::ST);   // [wave][2][MT][64]: 48 KiB at MT = 3
+                float4 *red = (float4 *)(lds + LS::ST);   // [wave][2][MTG][64]: 32 KiB at MTG = 2
 #pragma unroll
                 for (int cc = 0; cc < 2; cc++)
 #pragma unroll
-                    for (int t = 0; t < MT; t++)
-                        red[((wave * 2 + cc) * MT + t) * 64 + lane] =
+                    for (int t = 0; t < MTG; t++)
+                        red[((wave * 2 + cc) * MTG + t) * 64 + lane] =
                             make_float4(acc2[cc][t][0], acc2[cc][t][1], acc2[cc][t][2], acc2[cc][t][3]);
             }
             lds_barrier();
             VXM_LTS(19);
-            // the SwiGLU outputs go to the row-owner area (x and gain), unused here: a gate/up
-            // workgroup (index >= 128) never owns a row (M <= 48)
-            static_assert(kMaxM <= 128, "gate/up workgroups own no row");
-            float *ps = (float *)(lds + LS::XR);   // [kMP][33]
-            for (int idx = tid; idx < 4 * MT * 64; idx += kThreads) {
-                const int ct2 = idx / (MT * 64), t = (idx / 64) % MT;
+            // the SwiGLU outputs after the partial sums in the stage area ([group row][33])
+            static_assert(32 * 1024 + (kMaxM / 2) * 33 * 4 <= LS::ST_SC - LS::ST, "gate/up outputs in the stage");
+            float *ps = (float *)(lds + LS::ST + 32 * 1024);
+            for (int idx = tid; idx < 4 * MTG * 64; idx += kThreads) {
+                const int ct2 = idx / (MTG * 64), t = (idx / 64) % MTG;
                 float o[4];
                 {
                     // the four K quarters in order
                     const float4 *red = (const float4 *)(lds + LS::ST);
                     const int h2 = ct2 >> 1, cc = ct2 & 1;
-                    float4 s = red[(((0 * 2 + h2) * 2 + cc) * MT + t) * 64 + lane];
+                    float4 s = red[(((0 * 2 + h2) * 2 + cc) * MTG + t) * 64 + lane];
 #pragma unroll
                     for (int k = 1; k < 4; k++) {
-                        const float4 u = red[(((2 * k + h2) * 2 + cc) * MT + t) * 64 + lane];
+                        const float4 u = red[(((2 * k + h2) * 2 + cc) * MTG + t) * 64 + lane];
                         s.x = s.x + u.x;
                         s.y = s.y + u.y;
                         s.z = s.z + u.z;
@@ -957,13 +1008,13 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             }
             lds_barrier();
             VXM_LTS(20);
-            if (!DMA && tid < 4 * M) {
+            if (!DMA && tid < 4 * nrg) {
                 const uint32_t tg = make_tag(ep, L, l, PH_P);
-                const int m = tid >> 2, part = tid & 3;
+                const int mi = tid >> 2, part = tid & 3;
                 float o[8], amax = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
-                    o[e] = ps[m * 33 + 8 * part + e];
+                    o[e] = ps[mi * 33 + 8 * part + e];
                     amax = fmaxf(amax, fabsf(o[e]));
                 }
                 amax = max4(amax);
@@ -975,7 +1026,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                     lo |= q8_byte(o[e], id, p.variant) << (8 * e);
                     hi |= q8_byte(o[4 + e], id, p.variant) << (8 * e);
                 }
-                uint64_t *dst = p.pp + (size_t)m * kPPitch;
+                uint64_t *dst = p.pp + (size_t)(gr0 + mi) * kPPitch;
                 const int col = 32 * ugu + 8 * part;
                 put_word(dst + col / 4, lo, tg);
                 put_word(dst + col / 4 + 1, hi, tg);
@@ -990,7 +1041,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             if (!DMA) {
                 const uint32_t tg = make_tag(ep, L, l, PH_P);
                 poll_stage<(kMaxM * 9 * 16 / 2 + kPollThreads - 1) / kPollThreads>(
-                    p, chan_rsrc(p.pp, LS::WP * 8), kPPitch, kF / 4, 16 * ds, 16, M, tg, lds, LS::ST, LS::ST_SC, bail);
+                    p, chan_rsrc(p.pp, LS::WP * 8), kPPitch, kF / 4, 16 * ds, 16, 0, M, tg, lds, LS::ST, LS::ST_SC, bail);
             } else {
                 if (!last && !is_gu) issue_o(block_at(p, l + 1));
                 if (!last && is_gu && is_qkv) issue_qkv(block_at(p, l + 1));
@@ -1113,13 +1164,13 @@ bool vxm_locdit_persistent_fits(vxm_ctx *ctx, const vxm_block_dims &d, int64_t M
     return true;
 }
 
-// AUTO takes the single launch where it measured faster than launch by launch: the
-// 16 q / 2 kv x 128 layout (the reference's LocDiT at 2 x 11 rows and the LocEnc), not
-// the 16 x 64 MHA layout at 2 x 24 rows, whose larger exchanges (every row's
-// activations to every tile of QKV and gate/up) cost more than the launches they save.
+// AUTO takes the single launch wherever it fits: with QKV and gate/up split by row
+// groups it measured faster than launch by launch at both layouts (per LocDiT
+// evaluation: 486.6 against 518.6 us at 16 x 64 heads and 2 x 24 rows, 410 against 474
+// at 16 / 2 x 128 and 2 x 11).
 bool vxm_locdit_persistent_pick(vxm_ctx *ctx, const vxm_block_dims &d, int64_t M, int S, int mode) {
     if (mode == VXM_DECODE_KERNELS || !vxm_locdit_persistent_fits(ctx, d, M, S)) return false;
-    return mode == VXM_DECODE_PERSISTENT || d.hd == 128;
+    return true;
 }
 
 void vxm_locdit_persistent_free(vxm_lpersist *st) {
