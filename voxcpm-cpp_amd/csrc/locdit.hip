@@ -358,9 +358,19 @@ static int dit_eval(vxm_locdit *m, const float *x, bool x_quantized, int P, int 
     const bool persistent = m->cfg.n_layers > 0 && vxm_locdit_persistent_pick(ctx, d, M, (int)S, m->block_mode);
     if (m->block_mode == VXM_DECODE_PERSISTENT && !persistent)
         return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "locdit: no persistent block kernel for this shape / device");
+    // the final RMSNorm of the x rows fused into the single launch (needs the gain)
+    const bool fin_fused = persistent && m->norm;
     if (persistent) {
         // all blocks in one launch; seq then holds the last block's output, residual included
-        if ((rc = vxm_locdit_persistent_run(ctx, d, m->blocks, &m->lp, m->seq, M, (int)S, m->block_dump))) return rc;
+        vxm_lfinal fin;
+        if (fin_fused) {
+            fin.g = m->norm;
+            fin.r0 = 3 + Pc;
+            fin.q = m->aq;
+            fin.d = m->ad;
+        }
+        if ((rc = vxm_locdit_persistent_run(ctx, d, m->blocks, &m->lp, m->seq, M, (int)S, m->block_dump, fin)))
+            return rc;
     } else {
         const vxm_attn_site site{m->ws.lk, m->ws.lv, (int)S, (int64_t)d.nkv * S * d.hd, (int)S, 0, 0, 0};
         for (int l = 0; l < m->cfg.n_layers; l++) {
@@ -383,8 +393,9 @@ static int dit_eval(vxm_locdit *m, const float *x, bool x_quantized, int P, int 
         }
     }
     // last residual + final RMSNorm of the x rows of each segment (src/locdit.c:373-390)
-    // one launch over the P x rows of every segment (rows 3 + Pc .. S - 1 of each)
-    {
+    // one launch over the P x rows of every segment (rows 3 + Pc .. S - 1 of each), unless
+    // the single launch did it
+    if (!fin_fused) {
         const int64_t r0 = 3 + Pc;
         const vxm_parts &dn = m->ws.dn_out;
         const vxm_parts delta =

@@ -114,6 +114,12 @@ struct vxm_lparams {
     int *err;
     uint32_t *state;         // [0] epoch, [1] workgroups finished in this launch
     float *dump;             // debug: [L + 1][M][1024] rows entering each block, then the output; or null
+    // the final RMSNorm of rows fin_r0 .. S - 1 of each segment (gain fin_g, or none: null)
+    // as Q8_0 rows fin_q / fin_d, segment-major
+    const float *fin_g;
+    int fin_r0;
+    int8_t *fin_q;
+    uint16_t *fin_d;
     uint64_t *trace;         // profiling build: per workgroup, the start and 16 timestamps per block
 };
 
@@ -563,6 +569,27 @@ __device__ __forceinline__ void row_update(uint8_t *lds, int st, int xr, int gn,
     const uint32_t ho = dpp_u<kDppX1>(h);
     if ((t & 1) == 0) put_word(chan_row + t / 2, h | (ho << 16), tag);
     if ((t & 15) == 0) put_word(chan_row + kH / 4 + t / 16, __float_as_uint(vxm_h2f(vxm_f2h(d))), tag);
+}
+
+// Row owner, after the last block: the final RMSNorm of its row x (LDS, with the gain
+// staged at gn) as plain Q8_0 (k_rmsnorm's steps and Q8_0 rule: what the launch after
+// the blocks would compute), q [1024] and d [32] of the output row.
+__device__ __forceinline__ void row_final_norm(uint8_t *lds, int xr, int gn, int misc, float eps, int variant,
+                                               int8_t *q, uint16_t *dsc) {
+    const int t = threadIdx.x, c = 2 * t;
+    const float *x = (const float *)(lds + xr);
+    const float2 g = *(const float2 *)(lds + gn + 4 * c);
+    const float x0 = x[c], x1 = x[c + 1];
+    const double tot = wg_sum_d((double)(x0 * x0) + (double)(x1 * x1), lds, misc);
+    const float mean = (float)(tot / (double)kH);
+    const float sc = __fdiv_rn(1.0f, __fsqrt_rn(mean + eps));
+    const float y0 = bf16r(bf16r(x0 * sc) * g.x), y1 = bf16r(bf16r(x1 * sc) * g.y);
+    float amax = fmaxf(fabsf(y0), fabsf(y1));
+    amax = max16(amax);
+    float d, id;
+    q8_scale(amax, variant, d, id);
+    *(uint16_t *)(q + c) = (uint16_t)(q8_byte(y0, id, variant) | (q8_byte(y1, id, variant) << 8));
+    if ((t & 15) == 0) dsc[t / 16] = vxm_f2h(d);
 }
 
 // One wave's program for all blocks.  DMA = wave 7: it streams the weight tiles and
@@ -1077,11 +1104,15 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             lds_barrier();
         }
         VXM_LTS(14);
-        // the last block: row owners add its down projection and write x out
+        // the last block: row owners add its down projection and write x out (and with
+        // fin_g, the x rows their final norm)
         if (last && row >= 0) {
-            if (!DMA)
+            const bool fin = p.fin_g && row % S >= p.fin_r0;
+            if (!DMA) {
+                if (fin) stage_gain(p.fin_g);
                 poll_partials<(kDSplits * kH / 2 + kPollThreads - 1) / kPollThreads>(
                     p, chan_rsrc(p.dp, LS::WDP * 8), kDSplits, M, row, make_tag(ep, L, l, PH_D), lds, LS::ST, bail);
+            }
             lds_barrier();
             if (*bail) return;
             VXM_LTS(15);
@@ -1093,6 +1124,11 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             if (!DMA && p.dump)
                 for (int c = tid * 4; c < kH; c += kPollThreads * 4)
                     *(float4 *)(p.dump + ((size_t)L * M + row) * kH + c) = *(const float4 *)(lds + LS::XR + c * 4);
+            if (fin) {
+                const int orow = (row / S) * (S - p.fin_r0) + row % S - p.fin_r0;
+                row_final_norm(lds, LS::XR, LS::GN, LS::MISC, p.eps, p.variant, p.fin_q + (size_t)orow * kH,
+                               p.fin_d + (size_t)orow * (kH / 32));
+            }
         }
     }
 }
@@ -1182,7 +1218,7 @@ void vxm_locdit_persistent_free(vxm_lpersist *st) {
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::vector<vxm_block> &blocks,
-                              vxm_lpersist **stp, float *x, int64_t M, int S, float *dump) {
+                              vxm_lpersist **stp, float *x, int64_t M, int S, float *dump, const vxm_lfinal &fin) {
     if (!vxm_locdit_persistent_fits(ctx, d, M, S))
         return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "persistent blocks: unsupported shape (M=%lld S=%d)",
                         (long long)M, S);
@@ -1295,6 +1331,14 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
     prm.err = st->err;
     prm.state = st->state;
     prm.dump = dump;
+    if (fin.g) {
+        if (fin.r0 < 0 || fin.r0 >= S || !fin.q || !fin.d)
+            return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "persistent blocks: final norm rows %d of %d", fin.r0, S);
+        prm.fin_g = fin.g;
+        prm.fin_r0 = fin.r0;
+        prm.fin_q = fin.q;
+        prm.fin_d = fin.d;
+    }
     if (kNH * prm.nseg * prm.qb > kG)
         return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "persistent blocks: too many attention units");
     // All 256 workgroups wait on each other's words, so all must be resident: one per CU

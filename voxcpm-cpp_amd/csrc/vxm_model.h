@@ -106,9 +106,19 @@ struct vxm_lpersist;
 bool vxm_locdit_persistent_fits(vxm_ctx *ctx, const vxm_block_dims &d, int64_t M, int S);
 // the block strategy (VXM_DECODE_*) resolved for one evaluation: true = the single launch
 bool vxm_locdit_persistent_pick(vxm_ctx *ctx, const vxm_block_dims &d, int64_t M, int S, int mode);
+// The final RMSNorm of the x rows fused into the launch (or none: g null): rows r0 .. S - 1 of
+// every segment, normalised with gain g, as Q8_0 rows q [n_seg * (S - r0)][H] / d [..][H / 32]
+// (segment-major), the steps of vxm_launch_rmsnorm with its Q8_0 output.
+struct vxm_lfinal {
+    const float *g = nullptr;
+    int r0 = 0;
+    int8_t *q = nullptr;
+    uint16_t *d = nullptr;
+};
 // dump (debug, or null): [L + 1][M][H], the rows entering every block and the last block's output
 int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::vector<vxm_block> &blocks,
-                              vxm_lpersist **st, float *x, int64_t M, int S, float *dump);
+                              vxm_lpersist **st, float *x, int64_t M, int S, float *dump,
+                              const vxm_lfinal &fin = vxm_lfinal{});
 int vxm_locdit_persistent_check(vxm_ctx *ctx, vxm_lpersist *st);
 void vxm_locdit_persistent_free(vxm_lpersist *st);
 
