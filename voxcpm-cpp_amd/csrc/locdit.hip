@@ -154,11 +154,20 @@ __global__ void k_locdit_assemble(float *__restrict__ seq, const float *__restri
 // dynamic LDS holds the 2n products (n <= kCfmMaxN).  vo is out_proj's K-split
 // slices, added in slice order as they are read (the fix-up launch's sums).
 // With xq8 the updated x also goes out as Q8_0 (the next evaluation's in_proj
-// input; the activation rule of `variant`, 32 lanes per block).
+// input; the activation rule of `variant`, 32 lanes per block).  Thread t holds
+// elements t + 256 k in registers from its first loads (every slice, the bias
+// and x requested at once) to its stores, so the serial sums are the only wait
+// between them.
 constexpr int kCfmMaxN = 2048;   // 2 x 2048 doubles = 32 KiB of LDS
+constexpr int kCfmNPT = kCfmMaxN / 256;
 __device__ __forceinline__ float parts_at(const vxm_parts &v, int64_t j) {
-    float s = v.p[j];
-    for (int z = 1; z < v.n; z++) s = s + v.p[z * v.stride + j];
+    float t[VXM_MAX_PARTS];
+#pragma unroll
+    for (int z = 0; z < VXM_MAX_PARTS; z++) t[z] = z < v.n ? v.p[z * v.stride + j] : 0.0f;
+    float s = t[0];
+#pragma unroll
+    for (int z = 1; z < VXM_MAX_PARTS; z++)
+        if (z < v.n) s = s + t[z];
     return s;
 }
 
@@ -169,17 +178,32 @@ __global__ __launch_bounds__(256) void k_cfm_update(const vxm_parts vo, const fl
                                                     int variant) {
     extern __shared__ double prod[];   // [2][n]
     __shared__ float st_sh;
+    const int t = threadIdx.x;
+    float pv[kCfmNPT], qv[kCfmNPT], xv[kCfmNPT];
+#pragma unroll
+    for (int k = 0; k < kCfmNPT; k++) {
+        const int j = t + 256 * k;
+        if (j >= n) break;
+        float p = parts_at(vo, j);
+        if (ob) p = p + ob[j % feat];
+        pv[k] = vxm_bf16(p);
+        if (use_cfg) {
+            float q = parts_at(vo, n + j);
+            if (ob) q = q + ob[j % feat];
+            qv[k] = vxm_bf16(q);
+        }
+        if (x) xv[k] = x[j];
+    }
     if (use_cfg) {
-        for (int j = threadIdx.x; j < n; j += blockDim.x) {
-            float p = parts_at(vo, j), q = parts_at(vo, n + j);
-            if (ob) { p = p + ob[j % feat]; q = q + ob[j % feat]; }
-            p = vxm_bf16(p);
-            q = vxm_bf16(q);
-            prod[j] = (double)vxm_bf16(p * q);
-            prod[n + j] = (double)vxm_bf16(q * q);
+#pragma unroll
+        for (int k = 0; k < kCfmNPT; k++) {
+            const int j = t + 256 * k;
+            if (j >= n) break;
+            prod[j] = (double)vxm_bf16(pv[k] * qv[k]);
+            prod[n + j] = (double)vxm_bf16(qv[k] * qv[k]);
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
+        if (t == 0) {
             double dot = 0.0, sq = 0.0;
             for (int j = 0; j < n; j++) {
                 dot += prod[j];
@@ -194,15 +218,14 @@ __global__ __launch_bounds__(256) void k_cfm_update(const vxm_parts vo, const fl
     const float st = use_cfg ? st_sh : 0.0f;
     const float cfg_b = vxm_bf16(cfg_value);
     // n % 32 == 0: the 32 lanes of a half wave hold one whole block of x
-    for (int j = threadIdx.x; j < n; j += blockDim.x) {
-        float p = parts_at(vo, j);
-        if (ob) p = p + ob[j % feat];
-        p = vxm_bf16(p);
+#pragma unroll
+    for (int k = 0; k < kCfmNPT; k++) {
+        const int j = t + 256 * k;
+        if (j >= n) break;
+        const float p = pv[k];
         float v = p;
         if (use_cfg) {
-            float q = parts_at(vo, n + j);
-            if (ob) q = q + ob[j % feat];
-            q = vxm_bf16(q);
+            const float q = qv[k];
             const float ns = vxm_bf16(q * st);
             const float gd = vxm_bf16(p - ns);
             const float gg = vxm_bf16(cfg_b * gd);
@@ -210,7 +233,7 @@ __global__ __launch_bounds__(256) void k_cfm_update(const vxm_parts vo, const fl
         }
         if (v_out) v_out[j] = v;
         if (x) {
-            const float xn = vxm_bf16(x[j] + vxm_bf16(dt * v));
+            const float xn = vxm_bf16(xv[k] + vxm_bf16(dt * v));
             x[j] = xn;
             if (xq8) {
                 // quantize_row_q8_0 of the block (k_quantize_q8_0's rule): d = amax / 127 as
