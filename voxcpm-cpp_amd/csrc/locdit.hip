@@ -643,7 +643,43 @@ extern "C" int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev,
     if ((rc = prepare(m, cond_dev, P, Pc, live, n_seg))) return rc;
     if ((rc = time_features(m, ts.data(), live, 0.0f))) return rc;   // dt input is 0 (src/gen_step.c:601)
     const int64_t H = m->dims.H;
+    // the whole loop in one launch of the single-launch blocks where it applies: the row
+    // owners assemble each step's rows, one workgroup forms out_proj, CFG-Zero* and the
+    // Euler step (the steps of k_locdit_assemble, k_rmsnorm and k_cfm_update)
+    const int64_t S = 3 + (int64_t)Pc + P, M = n_seg * S;
+    vxm_lsolve sv;
+    sv.n_eval = live;
+    sv.dts = dts.data();
+    sv.tc = m->tc;
+    sv.mu = mu_dev;
+    sv.n_mu = 1;
+    sv.ch = Pc ? m->ch : nullptr;
+    sv.cb = m->cond_bias;
+    sv.in_proj = m->in_proj;
+    sv.in_b = m->in_bias;
+    sv.out_proj = m->out_proj;
+    sv.out_b = m->out_bias;
+    sv.P = P;
+    sv.Pc = Pc;
+    sv.feat = m->cfg.feat_dim;
+    sv.n_seg = n_seg;
+    sv.use_cfg = use_cfg;
+    sv.cfg = cfg_value;
+    sv.x = x_dev;
+    sv.xq0 = m->xq8;
+    sv.xd0 = m->xd8;
+    const bool fused = m->cfg.n_layers > 0 && m->norm && !m->block_dump &&
+                       vxm_locdit_persistent_pick(m->ctx, m->dims, M, (int)S, m->block_mode) &&
+                       vxm_locdit_persistent_solve_fits(m->ctx, m->dims, M, (int)S, sv);
     auto euler_loop = [&]() -> int {
+        if (fused) {
+            int r = vxm_launch_quantize(m->ctx, x_dev, P, m->cfg.feat_dim, m->ctx->quant_variant, m->xq8, m->xd8);
+            if (r) return r;
+            vxm_lfinal fin;
+            fin.g = m->norm;
+            fin.r0 = 3 + Pc;
+            return vxm_locdit_persistent_run(m->ctx, m->dims, m->blocks, &m->lp, m->seq, M, (int)S, nullptr, fin, &sv);
+        }
         for (int k = 0; k < live; k++) {
             // from the second step on, x's Q8_0 comes from the previous step's update
             int r = dit_eval(m, x_dev, k > 0, P, Pc, n_seg, mu_dev, 1, m->tc + (int64_t)k * H);

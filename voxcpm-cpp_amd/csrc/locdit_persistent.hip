@@ -52,6 +52,9 @@ constexpr int kPollThreads = 7 * 64;   // waves 0-6 read exchanged words; wave 7
 constexpr int kSpin = 1 << 17;         // poll rounds before giving up
 constexpr int kMaxM = 48, kMT = 3, kMP = 48, kMaxS = 32, kRB = 8;
 constexpr int kMaxQT = 3;   // QKV column tiles per workgroup
+// A CFM solve in one launch: at most kMaxEval Euler steps of x [P][kFeat], P * kFeat <= kSolveMaxN
+constexpr int kMaxEval = 64, kFeat = 64, kSolveMaxN = 2048;
+constexpr int kXqWords = kFeat / 4 + kFeat / 32;   // words per row of the Q8_0 x channel
 constexpr int kH = 1024, kF = 4096, kNH = 16;
 constexpr int kXPitch = kH / 4 + kH / 32;   // words per row of a norm output (quants, then scales)
 constexpr int kPPitch = kF / 4 + kF / 32;   // words per row of the SwiGLU output
@@ -120,6 +123,28 @@ struct vxm_lparams {
     int fin_r0;
     int8_t *fin_q;
     uint16_t *fin_d;
+    // solve mode (n_eval > 0): n_eval Euler steps of vxm_cfm_solve in this launch.  Each
+    // evaluation starts with the row owners assembling their rows (mu, the step's time
+    // row tc, the cond rows ch + cb, the x rows' in_proj), runs the L blocks, and ends
+    // with the x rows' final norm (fin_g) going to workgroup kG - 1, which forms
+    // out_proj, the CFG-Zero* blend and the Euler step of xs, and hands the Q8_0 of the
+    // new x to the next evaluation's row owners.
+    int n_eval, P, Pc, n_seg, n_mu, use_cfg;
+    float cfg;
+    const float *tc;                 // [n_eval][1024] time rows
+    const float *mu;                 // [2][1024] mu rows of segment 0, or null
+    const float *ch, *cb;            // [Pc][1024] raw cond projection, its bias (or null)
+    const int8_t *in_q;              // in_proj [1024][kFeat], scales [1024][2], bias (or null)
+    const uint16_t *in_d;
+    const float *in_b;
+    const int8_t *out_q;             // out_proj [kFeat][1024], scales [kFeat][32], bias (or null)
+    const uint16_t *out_d;
+    const float *out_b;
+    float *xs;                       // [P][kFeat] x, updated in place by every step
+    const int8_t *xq0;               // its Q8_0 at the start [P][kFeat], scales [P][2]
+    const uint16_t *xd0;
+    uint64_t *fq, *xqc;              // channels: the final norm's Q8_0 rows, the new x's Q8_0
+    float dts[kMaxEval];             // the steps' sizes
     uint64_t *trace;         // profiling build: per workgroup, the start and 16 timestamps per block
 };
 
@@ -679,9 +704,101 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             for (int v = 0; v < 4; v++) acc[t][v] = 0.0f;
     };
 
-    for (int l = 0; l < L; l++) {
+    // solve mode: the evaluations' tags are those of n_eval (L + 1) blocks, block l of
+    // evaluation k being k (L + 1) + l and k (L + 1) + L its final exchanges
+    const bool solve = p.n_eval > 0;
+    const int nev = solve ? p.n_eval : 1, LT = solve ? nev * (L + 1) : L;
+    const bool upd = solve && wg == kG - 1;   // the workgroup of out_proj and the Euler step
+    // out_proj's weights into the region of the QKV / gate-up tiles: tiles 0-1 and the scales
+    // at the last down wait of an evaluation, tiles 2-3 at the update's wait
+    // (the lane through an opaque move: out_proj's addresses do not change from one
+    // evaluation to the next, and hoisted they would hold 72 VGPRs across every phase)
+    auto issue_out_a = [&]() {
+        const int ol = opaque_tid() & 63;
+        for (int c = 0; c < 2; c++) dma_tile(LS::RA, c, p.out_q, kH, 16 * c, 0, 32, ol);
+        dma_scales(LS::RA_SC, p.out_d, kH / 32, 0, kFeat, 0, 32, ol);
+    };
+    auto issue_out_b = [&]() {
+        const int ol = opaque_tid() & 63;
+        for (int c = 2; c < 4; c++) dma_tile(LS::RA, c, p.out_q, kH, 16 * c, 0, 32, ol);
+    };
+    static_assert(kFeat == 64 && 4 * 16 * 32 * 2 <= LS::RO - LS::RA_SC, "out_proj tile");
+    // one flat loop over (evaluation k, block l): a nested evaluation loop made the compiler
+    // hold more values across it (220 against 160 VGPRs)
+    for (int it = 0; it < nev * L; it++) {
+    const int k = it / L, l = it - k * L;
+    auto tagb = [&](int lb, int ph) { return make_tag(ep, LT, solve ? k * (L + 1) + lb : lb, ph); };
+    // ---- solve mode: the row owners assemble evaluation k's rows (k_locdit_assemble) ----
+    if (solve && l == 0 && row >= 0) {
+        const int r = row % S, g = row / S, xi = r - 3 - p.Pc;
+        int8_t *aq = (int8_t *)(lds + LS::ST);               // the x row's Q8_0: 64 quants,
+        uint16_t *ad = (uint16_t *)(lds + LS::ST + kFeat);   // 2 scales
+        if (!DMA) {
+            const int t = opaque_tid();
+            if (xi >= 0 && k == 0) {
+                if (t < kFeat / 4) *(uint32_t *)(aq + 4 * t) = *(const uint32_t *)(p.xq0 + (size_t)xi * kFeat + 4 * t);
+                if (t < kFeat / 32) ad[t] = p.xd0[(size_t)xi * (kFeat / 32) + t];
+            } else if (xi >= 0) {
+                // the previous step's Q8_0 of x (its tail exchange: block index -1 of this
+                // evaluation): kXqWords words (quants, then fp16 scales) as pairs
+                poll<1>(
+                    p, chan_rsrc(p.xqc, kMaxS * kXqWords * 8), kXqWords / 2, tagb(-1, PH_X2),
+                    [&](int i) { return (xi * kXqWords + 2 * i) * 8; },
+                    [&](int i, uint32_t a, uint32_t b) {
+                        if (i < kFeat / 8) {
+                            *(uint32_t *)(aq + 8 * i) = a;
+                            *(uint32_t *)(aq + 8 * i + 4) = b;
+                        } else {
+                            ad[0] = (uint16_t)a;
+                            ad[1] = (uint16_t)b;
+                        }
+                    },
+                    bail);
+            } else {
+                for (int c = t * 4; c < kH; c += kPollThreads * 4) {
+                    float4 v;
+                    if (r < 2) {
+                        v = g < p.n_mu && p.mu ? *(const float4 *)(p.mu + (size_t)r * kH + c) : make_float4(0, 0, 0, 0);
+                    } else if (r == 2) {
+                        v = *(const float4 *)(p.tc + (size_t)k * kH + c);
+                    } else {
+                        v = *(const float4 *)(p.ch + (size_t)(r - 3) * kH + c);
+                        if (p.cb) {
+                            const float4 b = *(const float4 *)(p.cb + c);
+                            v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
+                        }
+                        v = make_float4(bf16r(v.x), bf16r(v.y), bf16r(v.z), bf16r(v.w));
+                    }
+                    *(float4 *)(lds + LS::XR + 4 * c) = v;
+                }
+            }
+        }
+        lds_barrier();
+        if (*bail) return;
+        if (xi >= 0 && !DMA) {
+            // in_proj: per output the exact int32 block sums times d_w * d_x, added in block
+            // order, + bias, BF16 (the arithmetic of k_locdit_assemble)
+            for (int i = opaque_tid(); i < kH; i += kPollThreads) {
+                const int8_t *wr = p.in_q + (size_t)i * kFeat;
+                float acc = 0.0f;
+#pragma unroll
+                for (int b = 0; b < kFeat / 32; b++) {
+                    int si = 0;
+#pragma unroll
+                    for (int h = 0; h < 32; h += 16)
+                        si = vxm_dot16(*(const int4 *)(wr + 32 * b + h), *(const int4 *)(aq + 32 * b + h), si);
+                    const float t = (float)si * (vxm_h2f(p.in_d[(size_t)i * (kFeat / 32) + b]) * vxm_h2f(ad[b]));
+                    acc = b ? acc + t : t;
+                }
+                if (p.in_b) acc = acc + p.in_b[i];
+                *(float *)(lds + LS::XR + 4 * i) = bf16r(acc);
+            }
+        }
+        lds_barrier();
+    }
+    {
         const vxm_lblock blk = block_at(p, l);
-        const bool last = l == L - 1;
+        const bool last = l == L - 1 && k == nev - 1, end = l == L - 1;
         VXM_LTS(0);
         // ---- N1: x += down partials of block l - 1; RMSNorm(g_in) -> Q8_0 ----
         if (row >= 0) {
@@ -690,13 +807,13 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                 stage_gain(blk.g_in);
                 if (ns)
                     poll_partials<(kDSplits * kH / 2 + kPollThreads - 1) / kPollThreads>(
-                        p, chan_rsrc(p.dp, LS::WDP * 8), ns, M, row, make_tag(ep, L, l - 1, PH_D), lds, LS::ST, bail);
+                        p, chan_rsrc(p.dp, LS::WDP * 8), ns, M, row, tagb(l - 1, PH_D), lds, LS::ST, bail);
             }
             lds_barrier();
             if (*bail) return;
             VXM_LTS(1);
             row_update(lds, LS::ST, LS::XR, LS::GN, LS::MISC, ns, p.eps, p.variant, p.x1 + (size_t)row * kXPitch,
-                       make_tag(ep, L, l, PH_X1), true);
+                       tagb(l, PH_X1), true);
             lds_barrier();
             // debug dump of the row entering block l (waves 0-6: wave 7's vmcnt counts only its DMAs)
             if (!DMA && p.dump)
@@ -718,7 +835,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                 rc1 = p.cs[(size_t)(mrow % S) * LS::HALF + ip + 1];
             }
             if (!DMA) {
-                const uint32_t tg = make_tag(ep, L, l, PH_X1);
+                const uint32_t tg = tagb(l, PH_X1);
                 poll_stage<(16 * kXPitch / 2 + kPollThreads - 1) / kPollThreads>(
                     p, chan_rsrc(p.x1, LS::WX * 8), kXPitch, kH / 4, 0, 32, qr0, nrq, tg, lds, LS::ST, LS::ST_SC, bail);
             } else {
@@ -742,7 +859,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             lds_barrier();
             VXM_LTS(17);
             if (!DMA && tid < nct * 64) {
-                const uint32_t tg = make_tag(ep, L, l, PH_QKV);
+                const uint32_t tg = tagb(l, PH_QKV);
                 const int m = qr0 + r16;
                 float o[4];
                 red_sum<1>(lds, LS::ST + 8192 * qk, 1, 0, 0, lane, o);
@@ -786,7 +903,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                 constexpr int W = LS::NQKV / 2, HP2 = HALF / 2;
                 const int nqp = nq * HP2, n = nqp + 2 * S * HP2;
                 poll<((kRB + 2 * kMaxS) * HP2 + kPollThreads - 1) / kPollThreads>(
-                    p, chan_rsrc(p.qkv, LS::WQKV * 8), n, make_tag(ep, L, l, PH_QKV),
+                    p, chan_rsrc(p.qkv, LS::WQKV * 8), n, tagb(l, PH_QKV),
                     [&](int i) {
                         if (i < nqp) return ((m0 + q0 + i / HP2) * W + h * HALF + 2 * (i % HP2)) * 8;
                         const int e = i - nqp, part = e / (S * HP2), j = (e / HP2) % S, wi = 2 * (e % HP2);
@@ -873,7 +990,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             // Q8_0 of the output rows: thread (i, c) holds dims 8c .. 8c+7, four threads a block
             constexpr int CPR = HD / 8;
             if (!DMA && tid < nq * CPR) {
-                const uint32_t tg = make_tag(ep, L, l, PH_ATT);
+                const uint32_t tg = tagb(l, PH_ATT);
                 const int i = tid / CPR, c = tid % CPR;
                 float o[8], amax = 0.0f;
 #pragma unroll
@@ -903,14 +1020,14 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
         {
             const int tid = opaque_tid(), lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
             if (!DMA) {
-                const uint32_t tg = make_tag(ep, L, l, PH_ATT);
+                const uint32_t tg = tagb(l, PH_ATT);
                 poll_stage<(kMaxM * 9 * LS::BO / 2 + kPollThreads - 1) / kPollThreads>(
                     p, chan_rsrc(p.att, LS::WA * 8), LS::APitch, LS::QD / 4, LS::BO * os, LS::BO, 0, M, tg, lds, LS::ST,
                     LS::ST_SC, bail);
             } else {
                 issue_d(blk);
                 if (is_gu) issue_gu_a(blk);
-                else if (is_qkv && !last) issue_qkv(block_at(p, l + 1));
+                else if (is_qkv && !last) issue_qkv(block_at(p, (l + 1) % L));
                 if (is_gu && is_qkv)
                     vm_wait<63>();
                 else if (is_gu)
@@ -928,7 +1045,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             red_store<MT>(lds, LS::ST, wave, lane, acc);
             lds_barrier();
             if (!DMA && tid < MT * 64) {
-                const uint32_t tg = make_tag(ep, L, l, PH_O);
+                const uint32_t tg = tagb(l, PH_O);
                 const int t = tid >> 6, m = 16 * t + r16;
                 float o[4];
                 red_sum<MT>(lds, LS::ST, 1, 0, t, lane, o);
@@ -946,13 +1063,13 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             if (!DMA) {
                 stage_gain(blk.g_post);
                 poll_partials<(kOSplits * kH / 2 + kPollThreads - 1) / kPollThreads>(
-                    p, chan_rsrc(p.op, LS::WOP * 8), kOSplits, M, row, make_tag(ep, L, l, PH_O), lds, LS::ST, bail);
+                    p, chan_rsrc(p.op, LS::WOP * 8), kOSplits, M, row, tagb(l, PH_O), lds, LS::ST, bail);
             }
             lds_barrier();
             if (*bail) return;
             VXM_LTS(9);
             row_update(lds, LS::ST, LS::XR, LS::GN, LS::MISC, kOSplits, p.eps, p.variant,
-                       p.x2 + (size_t)row * kXPitch, make_tag(ep, L, l, PH_X2), true);
+                       p.x2 + (size_t)row * kXPitch, tagb(l, PH_X2), true);
             lds_barrier();
         }
         VXM_LTS(10);
@@ -962,7 +1079,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             constexpr int MTG = MT == 3 ? 2 : 1;   // row tiles of a group: at most 24 rows
             const int tid = opaque_tid(), lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
             if (!DMA) {
-                const uint32_t tg = make_tag(ep, L, l, PH_X2);
+                const uint32_t tg = tagb(l, PH_X2);
                 poll_stage<(16 * MTG * kXPitch / 2 + kPollThreads - 1) / kPollThreads>(
                     p, chan_rsrc(p.x2, LS::WX * 8), kXPitch, kH / 4, 0, 32, gr0, nrg, tg, lds, LS::ST, LS::ST_SC, bail);
             } else {
@@ -970,7 +1087,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                 if (last) {
                     vm_wait<0>();
                 } else {
-                    issue_o(block_at(p, l + 1));
+                    issue_o(block_at(p, (l + 1) % L));
                     vm_wait<nO>();
                 }
             }
@@ -1036,7 +1153,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             lds_barrier();
             VXM_LTS(20);
             if (!DMA && tid < 4 * nrg) {
-                const uint32_t tg = make_tag(ep, L, l, PH_P);
+                const uint32_t tg = tagb(l, PH_P);
                 const int mi = tid >> 2, part = tid & 3;
                 float o[8], amax = 0.0f;
 #pragma unroll
@@ -1066,12 +1183,15 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
         {
             const int tid = opaque_tid(), lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
             if (!DMA) {
-                const uint32_t tg = make_tag(ep, L, l, PH_P);
+                const uint32_t tg = tagb(l, PH_P);
                 poll_stage<(kMaxM * 9 * 16 / 2 + kPollThreads - 1) / kPollThreads>(
                     p, chan_rsrc(p.pp, LS::WP * 8), kPPitch, kF / 4, 16 * ds, 16, 0, M, tg, lds, LS::ST, LS::ST_SC, bail);
             } else {
-                if (!last && !is_gu) issue_o(block_at(p, l + 1));
-                if (!last && is_gu && is_qkv) issue_qkv(block_at(p, l + 1));
+                if (!last && !is_gu) issue_o(block_at(p, (l + 1) % L));
+                // the update workgroup takes out_proj into the QKV region here and the next
+                // evaluation's QKV tiles after its products
+                if (!last && is_gu && is_qkv && !(upd && end)) issue_qkv(block_at(p, (l + 1) % L));
+                if (upd && end) issue_out_a();
                 if (is_gu)
                     vm_wait<63>();
                 else if (last)
@@ -1091,7 +1211,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             red_store<MT>(lds, LS::ST, wave, lane, acc);
             lds_barrier();
             if (!DMA && tid < 2 * MT * 64) {
-                const uint32_t tg = make_tag(ep, L, l, PH_D);
+                const uint32_t tg = tagb(l, PH_D);
                 const int ct2 = tid / (MT * 64), t = (tid / 64) % MT, m = 16 * t + r16;
                 float o[4];
                 red_sum<MT>(lds, LS::ST, 2, ct2, t, lane, o);
@@ -1104,14 +1224,29 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             lds_barrier();
         }
         VXM_LTS(14);
+        // solve mode, an evaluation's last block: the x rows' owners add its down projection
+        // and publish their final norm's Q8_0 (segment-major rows) for the update workgroup
+        if (solve && end && row >= 0 && row % S >= p.fin_r0) {
+            if (!DMA) {
+                stage_gain(p.fin_g);
+                poll_partials<(kDSplits * kH / 2 + kPollThreads - 1) / kPollThreads>(
+                    p, chan_rsrc(p.dp, LS::WDP * 8), kDSplits, M, row, tagb(l, PH_D), lds, LS::ST, bail);
+            }
+            lds_barrier();
+            if (*bail) return;
+            const int orow = (row / S) * (S - p.fin_r0) + row % S - p.fin_r0;
+            row_update(lds, LS::ST, LS::XR, LS::GN, LS::MISC, kDSplits, p.eps, p.variant,
+                       p.fq + (size_t)orow * kXPitch, tagb(L, PH_X1), true);
+            lds_barrier();
+        }
         // the last block: row owners add its down projection and write x out (and with
         // fin_g, the x rows their final norm)
-        if (last && row >= 0) {
+        if (!solve && last && row >= 0) {
             const bool fin = p.fin_g && row % S >= p.fin_r0;
             if (!DMA) {
                 if (fin) stage_gain(p.fin_g);
                 poll_partials<(kDSplits * kH / 2 + kPollThreads - 1) / kPollThreads>(
-                    p, chan_rsrc(p.dp, LS::WDP * 8), kDSplits, M, row, make_tag(ep, L, l, PH_D), lds, LS::ST, bail);
+                    p, chan_rsrc(p.dp, LS::WDP * 8), kDSplits, M, row, tagb(l, PH_D), lds, LS::ST, bail);
             }
             lds_barrier();
             if (*bail) return;
@@ -1131,6 +1266,123 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             }
         }
     }
+    // ---- solve mode: out_proj, CFG-Zero* and the Euler step (k_cfm_update's steps) ----
+    if (upd && l == L - 1) {
+        const int NR = p.n_seg * p.P, n = p.P * kFeat, tid = opaque_tid(), lane = tid & 63;
+        if (!DMA) {
+            poll_stage<(kMaxM * kXPitch / 2 + kPollThreads - 1) / kPollThreads>(
+                p, chan_rsrc(p.fq, LS::WX * 8), kXPitch, kH / 4, 0, 32, 0, NR, tagb(L, PH_X1), lds, LS::ST,
+                LS::ST_SC, bail);
+        } else {
+            vm_wait<31>();
+            issue_out_b();
+            vm_wait<0>();
+        }
+        lds_barrier();
+        if (*bail) return;
+        // wave w: out_proj column tile w & 3 over the K half w >> 2
+        zero_acc();
+        mfma_run<MT, 16>(lds, LS::RA, LS::RA_SC, 32, wave & 3, LS::ST, LS::ST_SC, 32, 16 * (wave >> 2), lane, acc);
+        lds_barrier();
+        red_store<MT>(lds, LS::ST, wave, lane, acc);
+        lds_barrier();
+        // vo [NR][64] fp32 after the partials: the two K halves in order
+        float *vo = (float *)(lds + LS::ST + kWaves * MT * 1024);
+        static_assert(kWaves * kMT * 1024 + kMaxM * kFeat * 4 <= LS::ST_SC - LS::ST, "out_proj rows in the stage");
+        for (int idx = tid; idx < 4 * MT * 64; idx += kThreads) {
+            const int ct = idx / (MT * 64), t = (idx / 64) % MT, ln = idx & 63, m = 16 * t + (ln & 15);
+            float o[4];
+            red_sum<MT>(lds, LS::ST, 4, ct, t, ln, o);
+            if (m < NR)
+#pragma unroll
+                for (int v = 0; v < 4; v++) vo[m * kFeat + 16 * ct + 4 * (ln >> 4) + v] = o[v];
+        }
+        lds_barrier();
+        // element j of the conditional rows [0, n) and the unconditional [n, 2n): waves 0-6,
+        // elements tid + 448 e held in registers; the products for the sums in double go to
+        // the weight region (out_proj is read)
+        constexpr int UPT = (kSolveMaxN + kPollThreads - 1) / kPollThreads;
+        double *prod = (double *)(lds + LS::RA);
+        static_assert(2 * kSolveMaxN * 8 <= LS::RA_SC - LS::RA, "CFG products");
+        float pv[UPT], qv[UPT], xv[UPT];
+        if (!DMA) {
+#pragma unroll
+            for (int e = 0; e < UPT; e++) {
+                const int j = tid + kPollThreads * e;
+                if (j >= n) break;
+                const int c = j % kFeat;
+                float pp = vo[j];
+                if (p.out_b) pp = pp + p.out_b[c];
+                pv[e] = bf16r(pp);
+                if (p.use_cfg) {
+                    float qq = vo[n + j];
+                    if (p.out_b) qq = qq + p.out_b[c];
+                    qv[e] = bf16r(qq);
+                    prod[j] = (double)bf16r(pv[e] * qv[e]);
+                    prod[n + j] = (double)bf16r(qv[e] * qv[e]);
+                }
+                xv[e] = p.xs[j];
+            }
+        }
+        lds_barrier();
+        float *st_sh = (float *)(lds + LS::MISC + 72);
+        if (p.use_cfg && tid == 0) {
+            double dot = 0.0, sq = 0.0;
+            for (int j = 0; j < n; j++) {
+                dot += prod[j];
+                sq += prod[n + j];
+            }
+            const float dot_b = bf16r((float)dot);
+            const float norm_b = bf16r((float)sq + 1.0e-8f);
+            *st_sh = bf16r(__fdiv_rn(dot_b, norm_b));
+        }
+        lds_barrier();
+        const bool more = k + 1 < nev;
+        int8_t *nq = (int8_t *)(lds + LS::ST);                        // the new x's Q8_0
+        uint16_t *nd = (uint16_t *)(lds + LS::ST + kSolveMaxN);
+        if (!DMA) {
+            const float st = p.use_cfg ? *st_sh : 0.0f, cfg_b = bf16r(p.cfg), dt = p.dts[k];
+            // n % 32 == 0 and 448 % 32 == 0: the 32 lanes of a half wave hold one block of x
+#pragma unroll
+            for (int e = 0; e < UPT; e++) {
+                const int j = tid + kPollThreads * e;
+                if (j >= n) break;
+                float v = pv[e];
+                if (p.use_cfg) {
+                    const float ns = bf16r(qv[e] * st);
+                    const float gd = bf16r(pv[e] - ns);
+                    const float gg = bf16r(cfg_b * gd);
+                    v = bf16r(ns + gg);
+                }
+                const float xn = bf16r(xv[e] + bf16r(dt * v));
+                p.xs[j] = xn;
+                if (more) {
+                    float amax = fabsf(xn);
+#pragma unroll
+                    for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+                    float d, id;
+                    q8_scale(amax, p.variant, d, id);
+                    nq[j] = (int8_t)q8_byte(xn, id, p.variant);
+                    if ((j & 31) == 0) nd[j / 32] = vxm_f2h(d);
+                }
+            }
+        }
+        lds_barrier();
+        if (more) {
+            // the new x's Q8_0 to the next evaluation's row owners, then its QKV tiles (the
+            // weight region is free again)
+            if (!DMA)
+                for (int w = tid; w < p.P * kXqWords; w += kPollThreads) {
+                    const int xi = w / kXqWords, e = w % kXqWords;
+                    const uint32_t pay = e < kFeat / 4 ? *(const uint32_t *)(nq + xi * kFeat + 4 * e)
+                                                       : (uint32_t)nd[xi * (kFeat / 32) + e - kFeat / 4];
+                    put_word(p.xqc + w, pay, tagb(L, PH_X2));
+                }
+            if (DMA && is_qkv) issue_qkv(block_at(p, 0));
+            lds_barrier();
+        }
+    }
+    }
 }
 
 template <class LS, int MT>
@@ -1148,8 +1400,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_locdit_persistent(vxm_lparams p
         if (p.trace) p.trace[(size_t)wg * (1 + kTraceSlots * p.L)] = __builtin_amdgcn_s_memrealtime();
 #endif
     }
-    // block 0's input rows
-    if (wg < p.M)
+    // block 0's input rows (in solve mode the row owners assemble them)
+    if (wg < p.M && p.n_eval == 0)
         for (int c = tid * 4; c < kH; c += kThreads * 4)
             *(float4 *)(lds + LS::XR + c * 4) = *(const float4 *)(p.x + (size_t)wg * kH + c);
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
@@ -1185,7 +1437,7 @@ struct vxm_lpersist {
     vxm_lblock *blocks = nullptr;
     int L = 0;
     std::vector<const void *> key;   // the weight pointers the table holds
-    uint64_t *chan[7] = {};
+    uint64_t *chan[9] = {};
     int *err = nullptr;
     uint32_t *state = nullptr;
 };
@@ -1217,10 +1469,30 @@ void vxm_locdit_persistent_free(vxm_lpersist *st) {
 
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
+bool vxm_locdit_persistent_solve_fits(vxm_ctx *ctx, const vxm_block_dims &d, int64_t M, int S,
+                                      const vxm_lsolve &sv) {
+    if (!vxm_locdit_persistent_fits(ctx, d, M, S)) return false;
+    if (sv.n_eval <= 0 || sv.n_eval > kMaxEval || sv.feat != kFeat || sv.P <= 0 || sv.Pc < 0 ||
+        sv.P * kFeat > kSolveMaxN || 3 + sv.Pc + sv.P != S || sv.n_seg * S != M || sv.n_seg < 1 || sv.n_seg > 2)
+        return false;
+    if (sv.use_cfg && sv.n_seg != 2) return false;
+    if (!sv.in_proj || !sv.out_proj || sv.in_proj->n != kH || sv.in_proj->k != kFeat || sv.out_proj->n != kFeat ||
+        sv.out_proj->k != kH || !aligned16(sv.in_proj->qs) || !aligned16(sv.out_proj->qs) ||
+        !aligned16(sv.out_proj->d))
+        return false;
+    // float4 reads of the assembled rows
+    if (!aligned16(sv.tc) || !aligned16(sv.mu) || !aligned16(sv.ch) || !aligned16(sv.cb)) return false;
+    return sv.dts && sv.tc && sv.x && sv.xq0 && sv.xd0 && (sv.Pc == 0 || sv.ch);
+}
+
 int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::vector<vxm_block> &blocks,
-                              vxm_lpersist **stp, float *x, int64_t M, int S, float *dump, const vxm_lfinal &fin) {
+                              vxm_lpersist **stp, float *x, int64_t M, int S, float *dump, const vxm_lfinal &fin,
+                              const vxm_lsolve *sv) {
     if (!vxm_locdit_persistent_fits(ctx, d, M, S))
         return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "persistent blocks: unsupported shape (M=%lld S=%d)",
+                        (long long)M, S);
+    if (sv && (!vxm_locdit_persistent_solve_fits(ctx, d, M, S, *sv) || !fin.g || fin.r0 != 3 + sv->Pc || dump))
+        return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "persistent blocks: unsupported solve (M=%lld S=%d)",
                         (long long)M, S);
     const int L = (int)blocks.size();
     if (L <= 0) return VXM_OK;
@@ -1252,13 +1524,15 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
         st->L = L;
         st->key = key;
         const int qd = kNH * d.hd, nqkv = qd + 2 * d.nkv * d.hd;
-        const size_t words[7] = {(size_t)kMaxM * kXPitch,
+        const size_t words[9] = {(size_t)kMaxM * kXPitch,
                                  (size_t)kMaxM * nqkv / 2,
                                  (size_t)kMaxM * (qd / 4 + qd / 32),
                                  (size_t)kOSplits * kMaxM * kH,
                                  (size_t)kMaxM * kXPitch,
                                  (size_t)kMaxM * kPPitch,
-                                 (size_t)kDSplits * kMaxM * kH};
+                                 (size_t)kDSplits * kMaxM * kH,
+                                 (size_t)kMaxM * kXPitch,
+                                 (size_t)kMaxS * kXqWords};
         size_t total = 0;
         for (size_t w : words) total += (w * 8 + 255) & ~(size_t)255;
         const size_t tab = ((size_t)L * sizeof(vxm_lblock) + 255) & ~(size_t)255;
@@ -1269,7 +1543,7 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
             return vxm_fail(ctx, VXM_ERR_OOM, "persistent blocks: %zu bytes of exchange buffers", bytes);
         }
         char *b = (char *)st->base;
-        for (int c = 0; c < 7; c++) {
+        for (int c = 0; c < 9; c++) {
             st->chan[c] = (uint64_t *)b;
             b += (words[c] * 8 + 255) & ~(size_t)255;
         }
@@ -1332,12 +1606,37 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
     prm.state = st->state;
     prm.dump = dump;
     if (fin.g) {
-        if (fin.r0 < 0 || fin.r0 >= S || !fin.q || !fin.d)
+        if (fin.r0 < 0 || fin.r0 >= S || (!sv && (!fin.q || !fin.d)))
             return vxm_fail(ctx, VXM_ERR_INVALID_ARG, "persistent blocks: final norm rows %d of %d", fin.r0, S);
         prm.fin_g = fin.g;
         prm.fin_r0 = fin.r0;
         prm.fin_q = fin.q;
         prm.fin_d = fin.d;
+    }
+    if (sv) {
+        prm.n_eval = sv->n_eval;
+        prm.P = sv->P;
+        prm.Pc = sv->Pc;
+        prm.n_seg = sv->n_seg;
+        prm.n_mu = sv->n_mu;
+        prm.use_cfg = sv->use_cfg;
+        prm.cfg = sv->cfg;
+        prm.tc = sv->tc;
+        prm.mu = sv->mu;
+        prm.ch = sv->ch;
+        prm.cb = sv->cb;
+        prm.in_q = sv->in_proj->qs;
+        prm.in_d = sv->in_proj->d;
+        prm.in_b = sv->in_b;
+        prm.out_q = sv->out_proj->qs;
+        prm.out_d = sv->out_proj->d;
+        prm.out_b = sv->out_b;
+        prm.xs = sv->x;
+        prm.xq0 = sv->xq0;
+        prm.xd0 = sv->xd0;
+        prm.fq = st->chan[7];
+        prm.xqc = st->chan[8];
+        for (int k = 0; k < sv->n_eval; k++) prm.dts[k] = sv->dts[k];
     }
     if (kNH * prm.nseg * prm.qb > kG)
         return vxm_fail(ctx, VXM_ERR_NOT_IMPLEMENTED, "persistent blocks: too many attention units");
@@ -1364,7 +1663,7 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
         VXM_HIP(ctx, hipMalloc(&tbuf, tbytes));
         tcap = tbytes;
     }
-    if (traced) {
+    if (traced && !sv) {   // a solve's evaluations are not traced
         VXM_HIP(ctx, hipMemset(tbuf, 0, tbytes));
         prm.trace = tbuf;
     }

@@ -115,10 +115,32 @@ struct vxm_lfinal {
     int8_t *q = nullptr;
     uint16_t *d = nullptr;
 };
+// A whole CFM solve in the launch (vxm_cfm_solve's Euler loop): n_eval steps of sizes dts
+// (host), time rows tc [n_eval][H], segment 0 with mu (n_mu = 1) or none, cond rows
+// ch [Pc][H] + cb, x [P][feat] updated in place from its Q8_0 xq0 / xd0; the final norm
+// (fin.g, r0 = 3 + Pc) and out_proj / in_proj run inside the launch.
+struct vxm_lsolve {
+    int n_eval = 0;
+    const float *dts = nullptr;
+    const float *tc = nullptr, *mu = nullptr, *ch = nullptr, *cb = nullptr;
+    int n_mu = 0;
+    const vxm_weight *in_proj = nullptr, *out_proj = nullptr;
+    const float *in_b = nullptr, *out_b = nullptr;
+    int P = 0, Pc = 0, feat = 0, n_seg = 1, use_cfg = 0;
+    float cfg = 1.0f;
+    float *x = nullptr;
+    const int8_t *xq0 = nullptr;
+    const uint16_t *xd0 = nullptr;
+};
+// whether vxm_locdit_persistent_run can take the solve (steps, feat, P, weight layout)
+bool vxm_locdit_persistent_solve_fits(vxm_ctx *ctx, const vxm_block_dims &d, int64_t M, int S,
+                                      const vxm_lsolve &sv);
 // dump (debug, or null): [L + 1][M][H], the rows entering every block and the last block's output
+// (not with a solve); with sv, the launch runs the solve (fin gives the final norm's gain and rows,
+// its q / d are unused) and x is not read or written
 int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::vector<vxm_block> &blocks,
                               vxm_lpersist **st, float *x, int64_t M, int S, float *dump,
-                              const vxm_lfinal &fin = vxm_lfinal{});
+                              const vxm_lfinal &fin = vxm_lfinal{}, const vxm_lsolve *sv = nullptr);
 int vxm_locdit_persistent_check(vxm_ctx *ctx, vxm_lpersist *st);
 void vxm_locdit_persistent_free(vxm_lpersist *st);
 
