@@ -204,10 +204,20 @@ __global__ __launch_bounds__(256) void k_cfm_update(const vxm_parts vo, const fl
         }
         __syncthreads();
         if (t == 0) {
+            // in element order; 16 elements' products read ahead of their additions (n % 32 == 0)
             double dot = 0.0, sq = 0.0;
-            for (int j = 0; j < n; j++) {
-                dot += prod[j];
-                sq += prod[n + j];
+            for (int j0 = 0; j0 < n; j0 += 16) {
+                double a[16], b[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    a[i] = prod[j0 + i];
+                    b[i] = prod[n + j0 + i];
+                }
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    dot += a[i];
+                    sq += b[i];
+                }
             }
             const float dot_b = vxm_bf16((float)dot);
             const float norm_b = vxm_bf16((float)sq + 1.0e-8f);

@@ -148,12 +148,15 @@ struct vxm_lparams {
     uint64_t *trace;         // profiling build: per workgroup, the start and 16 timestamps per block
 };
 
-constexpr int kTraceSlots = 24;
+// slots per block; a solve's blocks are numbered over its evaluations (it = k L + l), and the
+// solve's own phases take slots 24-31 (assemble inputs / done, update inputs / done, then inside
+// the update: products, out_proj rows, the CFG sums, the Euler step and Q8_0)
+constexpr int kTraceSlots = 32;
 #ifdef VXM_PERSISTENT_TRACE
 #define VXM_LTS(k)                                                                                                 \
     do {                                                                                                           \
         if (threadIdx.x == 0 && p.trace)                                                                           \
-            p.trace[(size_t)blockIdx.x * (1 + kTraceSlots * p.L) + 1 + kTraceSlots * l + (k)] =                   \
+            p.trace[(size_t)blockIdx.x * (1 + kTraceSlots * p.L * max(p.n_eval, 1)) + 1 + kTraceSlots * it + (k)] = \
                 __builtin_amdgcn_s_memrealtime();                                                                  \
     } while (0)
 #else
@@ -775,6 +778,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
         }
         lds_barrier();
         if (*bail) return;
+        VXM_LTS(24);
         if (xi >= 0 && !DMA) {
             // in_proj: per output the exact int32 block sums times d_w * d_x, added in block
             // order, + bias, BF16 (the arithmetic of k_locdit_assemble)
@@ -795,6 +799,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             }
         }
         lds_barrier();
+        VXM_LTS(25);
     }
     {
         const vxm_lblock blk = block_at(p, l);
@@ -1234,6 +1239,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             }
             lds_barrier();
             if (*bail) return;
+            VXM_LTS(15);
             const int orow = (row / S) * (S - p.fin_r0) + row % S - p.fin_r0;
             row_update(lds, LS::ST, LS::XR, LS::GN, LS::MISC, kDSplits, p.eps, p.variant,
                        p.fq + (size_t)orow * kXPitch, tagb(L, PH_X1), true);
@@ -1280,10 +1286,12 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
         }
         lds_barrier();
         if (*bail) return;
+        VXM_LTS(26);
         // wave w: out_proj column tile w & 3 over the K half w >> 2
         zero_acc();
         mfma_run<MT, 16>(lds, LS::RA, LS::RA_SC, 32, wave & 3, LS::ST, LS::ST_SC, 32, 16 * (wave >> 2), lane, acc);
         lds_barrier();
+        VXM_LTS(28);
         red_store<MT>(lds, LS::ST, wave, lane, acc);
         lds_barrier();
         // vo [NR][64] fp32 after the partials: the two K halves in order
@@ -1298,6 +1306,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                 for (int v = 0; v < 4; v++) vo[m * kFeat + 16 * ct + 4 * (ln >> 4) + v] = o[v];
         }
         lds_barrier();
+        VXM_LTS(29);
         // element j of the conditional rows [0, n) and the unconditional [n, 2n): waves 0-6,
         // elements tid + 448 e held in registers; the products for the sums in double go to
         // the weight region (out_proj is read)
@@ -1327,16 +1336,27 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
         lds_barrier();
         float *st_sh = (float *)(lds + LS::MISC + 72);
         if (p.use_cfg && tid == 0) {
+            // in element order; 16 elements' products read ahead of their additions (n % 32 == 0)
             double dot = 0.0, sq = 0.0;
-            for (int j = 0; j < n; j++) {
-                dot += prod[j];
-                sq += prod[n + j];
+            for (int j0 = 0; j0 < n; j0 += 16) {
+                double a[16], b[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    a[i] = prod[j0 + i];
+                    b[i] = prod[n + j0 + i];
+                }
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    dot += a[i];
+                    sq += b[i];
+                }
             }
             const float dot_b = bf16r((float)dot);
             const float norm_b = bf16r((float)sq + 1.0e-8f);
             *st_sh = bf16r(__fdiv_rn(dot_b, norm_b));
         }
         lds_barrier();
+        VXM_LTS(30);
         const bool more = k + 1 < nev;
         int8_t *nq = (int8_t *)(lds + LS::ST);                        // the new x's Q8_0
         uint16_t *nd = (uint16_t *)(lds + LS::ST + kSolveMaxN);
@@ -1368,6 +1388,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             }
         }
         lds_barrier();
+        VXM_LTS(31);
         if (more) {
             // the new x's Q8_0 to the next evaluation's row owners, then its QKV tiles (the
             // weight region is free again)
@@ -1381,6 +1402,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             if (DMA && is_qkv) issue_qkv(block_at(p, 0));
             lds_barrier();
         }
+        VXM_LTS(27);
     }
     }
 }
@@ -1397,7 +1419,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_locdit_persistent(vxm_lparams p
         *bail = 0;
         *ep_sh = __hip_atomic_load(p.state, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef VXM_PERSISTENT_TRACE
-        if (p.trace) p.trace[(size_t)wg * (1 + kTraceSlots * p.L)] = __builtin_amdgcn_s_memrealtime();
+        if (p.trace) p.trace[(size_t)wg * (1 + kTraceSlots * p.L * max(p.n_eval, 1))] = __builtin_amdgcn_s_memrealtime();
 #endif
     }
     // block 0's input rows (in solve mode the row owners assemble them)
@@ -1649,7 +1671,8 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
 #ifdef VXM_PERSISTENT_TRACE
     // profiling build: timestamps of every eager launch into
     // $VXM_TRACE_DIR/ltrace_L<blocks>_M<rows>_<n>.bin (launches recorded into a graph run untraced)
-    const size_t tstride = 1 + (size_t)kTraceSlots * L, tbytes = (size_t)kG * tstride * 8;
+    const int tblocks = L * (sv ? sv->n_eval : 1);
+    const size_t tstride = 1 + (size_t)kTraceSlots * tblocks, tbytes = (size_t)kG * tstride * 8;
     static uint64_t *tbuf = nullptr;
     static size_t tcap = 0;
     static int ncall = 0;
@@ -1663,7 +1686,7 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
         VXM_HIP(ctx, hipMalloc(&tbuf, tbytes));
         tcap = tbytes;
     }
-    if (traced && !sv) {   // a solve's evaluations are not traced
+    if (traced) {
         VXM_HIP(ctx, hipMemset(tbuf, 0, tbytes));
         prm.trace = tbuf;
     }
@@ -1695,7 +1718,7 @@ int vxm_locdit_persistent_run(vxm_ctx *ctx, const vxm_block_dims &d, const std::
         VXM_HIP(ctx, hipMemcpy(th.data(), tbuf, tbytes, hipMemcpyDeviceToHost));
         const char *dir = getenv("VXM_TRACE_DIR");
         char fn[512];
-        snprintf(fn, sizeof fn, "%s/ltrace_L%d_M%d_%04d.bin", dir ? dir : ".", L, (int)M, ncall++);
+        snprintf(fn, sizeof fn, "%s/ltrace_L%d_M%d_%04d.bin", dir ? dir : ".", tblocks, (int)M, ncall++);
         if (FILE *f = fopen(fn, "wb")) {
             fwrite(th.data(), 8, th.size(), f);
             fclose(f);
