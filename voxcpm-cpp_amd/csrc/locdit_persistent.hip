@@ -645,7 +645,14 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
     const bool is_gu = gu >= 0;
     const int ugu = gu & 127, grows = (M + ngg - 1) / ngg, gr0 = (gu >> 7) * grows, nrg = min(grows, M - gr0);
     const int oc = wg & 63, os = wg >> 6;   // O unit: 16-column tile, K quarter
-    const int dc = wg & 31, ds = wg >> 5;   // down unit: 32-column tile, K eighth
+    // down unit: 32-column tile dc over K eighth ds (all rows); above 16 rows (drow) a
+    // 64-column tile dc2 over K eighth ds2 for the gate/up row groups, its weights in the
+    // QKV / gate-up region once the gate/up products are done (the rows of each consumer
+    // halved: 55 -> 28 KB of exchanged words at 48 rows)
+    const int dc = wg & 31, ds = wg >> 5;
+    const bool drow = M > 16;
+    const int dc2 = wg & 15, ds2 = (wg >> 4) & 7;
+    const int dgrp = wg >> 7, dr0 = dgrp * grows, nrd = min(grows, M - dr0);
     // loads per prefetch (16 rows x 2 blocks, or 64 f16 scale rows of 8 blocks, per instruction)
     constexpr int nO = LS::BO / 2 + 1, nD = 17, nQKV = 17, nGA = 36;
     const int dlane = threadIdx.x & 63;
@@ -676,6 +683,10 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
     auto issue_d = [&](const vxm_lblock &b) {
         for (int c = 0; c < 2; c++) dma_tile(LS::RD, c, b.dn_q, kF, 32 * dc + 16 * c, 16 * ds, 16, dlane);
         dma_scales(LS::RD_SC, b.dn_d, kF / 32, 32 * dc, 32, 16 * ds, 16, dlane);
+    };
+    auto issue_d2 = [&](const vxm_lblock &b) {   // 34 loads
+        for (int c = 0; c < 4; c++) dma_tile(LS::RA, c, b.dn_q, kF, 64 * dc2 + 16 * c, 16 * ds2, 16, dlane);
+        dma_scales(LS::RA_SC, b.dn_d, kF / 32, 64 * dc2, 64, 16 * ds2, 16, dlane);
     };
     auto issue_gu_a = [&](const vxm_lblock &b) {
         for (int c = 0; c < 2; c++) dma_tile(LS::RA, c, b.gu_q, kH, 64 * ugu + 16 * c, 0, 32, dlane);
@@ -731,6 +742,10 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
     for (int it = 0; it < nev * L; it++) {
     const int k = it / L, l = it - k * L;
     auto tagb = [&](int lb, int ph) { return make_tag(ep, LT, solve ? k * (L + 1) + lb : lb, ph); };
+    // above 16 rows the QKV tiles of block l share the region with the previous block's down
+    // tile, so they go out here (the first block's at the start, the update workgroup's after
+    // its out_proj products)
+    if (DMA && drow && is_qkv && it > 0 && !(upd && l == 0)) issue_qkv(block_at(p, l));
     // ---- solve mode: the row owners assemble evaluation k's rows (k_locdit_assemble) ----
     if (solve && l == 0 && row >= 0) {
         const int r = row % S, g = row / S, xi = r - 3 - p.Pc;
@@ -1030,11 +1045,13 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                     p, chan_rsrc(p.att, LS::WA * 8), LS::APitch, LS::QD / 4, LS::BO * os, LS::BO, 0, M, tg, lds, LS::ST,
                     LS::ST_SC, bail);
             } else {
-                issue_d(blk);
+                if (!drow) issue_d(blk);
                 if (is_gu) issue_gu_a(blk);
                 else if (is_qkv && !last) issue_qkv(block_at(p, (l + 1) % L));
                 if (is_gu && is_qkv)
                     vm_wait<63>();
+                else if (is_gu && drow)
+                    vm_wait<nGA>();
                 else if (is_gu)
                     vm_wait<nD + nGA>();
                 else
@@ -1184,8 +1201,57 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             lds_barrier();
         }
         VXM_LTS(12);
+        // ---- down, above 16 rows: 64-column tile dc2 over K eighth ds2 for one row group ----
+        if (drow) {
+            constexpr int MTD = MT == 3 ? 2 : 1;   // row tiles of a group: at most 24 rows
+            const int tid = opaque_tid(), lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
+            if (!DMA) {
+                const uint32_t tg = tagb(l, PH_P);
+                poll_stage<(16 * MTD * 9 * 16 / 2 + kPollThreads - 1) / kPollThreads>(
+                    p, chan_rsrc(p.pp, LS::WP * 8), kPPitch, kF / 4, 16 * ds2, 16, dr0, nrd, tg, lds, LS::ST,
+                    LS::ST_SC, bail);
+            } else {
+                // the gate/up products are done: the region takes this block's down tile now
+                issue_d2(blk);
+                vm_wait<0>();
+            }
+            lds_barrier();
+            if (*bail) return;
+            VXM_LTS(13);
+            // wave w: column tile w & 3 over the K half w >> 2 of the eighth
+            float ad[MTD][4];
+#pragma unroll
+            for (int t = 0; t < MTD; t++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) ad[t][v] = 0.0f;
+            mfma_run<MTD, 8>(lds, LS::RA, LS::RA_SC, 16, wave & 3, LS::ST, LS::ST_SC, 16, 8 * (wave >> 2), lane, ad);
+            lds_barrier();
+            // the region is free again: at an evaluation's end the update workgroup takes
+            // out_proj's first half (the next block's QKV tiles go out at its top, where the
+            // wave is not in a workgroup barrier's way: issued here, they held up the reduction
+            // by ~2 us)
+            if (DMA && upd && end) issue_out_a();
+            red_store<MTD>(lds, LS::ST, wave, lane, ad);
+            lds_barrier();
+            // 4 MTD (column tile, row tile) pairs of 64 lanes over waves 0-6 (up to 512 threads)
+            if (!DMA) {
+                const uint32_t tg = tagb(l, PH_D);
+                for (int idx = tid; idx < 4 * MTD * 64; idx += kPollThreads) {
+                    const int ct2 = idx / (MTD * 64), t = (idx / 64) % MTD, ln = idx & 63;
+                    const int m = 16 * t + (ln & 15);
+                    float o[4];
+                    red_sum<MTD>(lds, LS::ST, 4, ct2, t, ln, o);
+                    if (m < nrd) {
+                        uint64_t *dst = p.dp + ((size_t)ds2 * M + dr0 + m) * kH + 64 * dc2 + 16 * ct2 + 4 * (ln >> 4);
+#pragma unroll
+                        for (int v = 0; v < 4; v++) put_word(dst + v, __float_as_uint(o[v]), tg);
+                    }
+                }
+            }
+            lds_barrier();
+        }
         // ---- down: 32-column tile dc over K eighth ds ----
-        {
+        else {
             const int tid = opaque_tid(), lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
             if (!DMA) {
                 const uint32_t tg = tagb(l, PH_P);
