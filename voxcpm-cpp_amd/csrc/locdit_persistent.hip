@@ -85,7 +85,7 @@ struct LShape {
     static constexpr int MISC = GN + kH * 4;                  // 8 doubles of reductions, then flags
     static constexpr int BYTES = MISC + 128;
     static_assert(16 * BO * 2 <= 1024, "O scales");
-    static_assert(UQ <= kMaxQT * (kG / kMT) && kMaxQT * 16 * kH <= RA_SC - RA && kMaxQT * 1024 <= RO - RA_SC,
+    static_assert(UQ <= kMaxQT * ((kG - kMaxM) / kMT) && kMaxQT * 16 * kH <= RA_SC - RA && kMaxQT * 1024 <= RO - RA_SC,
                   "QKV tiles of a workgroup");
     static_assert(kMP * 33 * 4 <= MISC - XR, "gate/up outputs in the row-owner area");
     static_assert(kWaves * 2 * kMT * 64 * 16 <= ST_SC - ST, "gate/up partial sums in the stage");
@@ -634,8 +634,12 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
     // QKV units: (16-column tile, row group).  The rows are cut into ngq groups of at most
     // 16 (one MFMA row tile), each read by wpq workgroups; workgroup jq of group gq takes
     // the tiles jq, jq + wpq, ... (at most kMaxQT), so a workgroup reads only its group's
-    // activations from the exchange.
-    const int ngq = (M + 15) / 16, wpq = kG / ngq, gq = wg / wpq, jq = wg % wpq;
+    // activations from the exchange.  Up to 32 rows the row owners (workgroups below M) take
+    // none: their norms and the weight loads of QKV units hold each other up (380.5 against
+    // 382.7 us per evaluation at 2 x 11 rows; at 2 x 24, 472 against 465 with them excluded).
+    const int q0 = M <= 32 ? M : 0;
+    const int ngq = (M + 15) / 16, wpq = (kG - q0) / ngq, wq = wg - q0;
+    const int gq = wq >= 0 ? wq / wpq : ngq, jq = wq >= 0 ? wq % wpq : 0;
     const int qrows = (M + ngq - 1) / ngq, qr0 = gq * qrows, nrq = min(qrows, M - qr0);
     const int nct = gq < ngq && jq < LS::UQ ? (LS::UQ - 1 - jq) / wpq + 1 : 0;
     const bool is_qkv = nct > 0;
