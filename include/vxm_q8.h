@@ -311,7 +311,10 @@ int vxm_locdit_forward(vxm_locdit *m, const float *x_dev, const float *cond_dev,
  * CFG-Zero* (vcpm_cfm_cfg_zero_star, src/cfm_solver.c:65-93) and
  * x = bf16(x + bf16(dt * v)).  Without CFG (cfg_value == 1 or mu == NULL,
  * src/gen_step.c:475) only the conditional branch runs.  x [P][feat_dim] is
- * updated in place.
+ * updated in place.  Where the single-launch blocks apply (see
+ * vxm_locdit_set_block_mode) and feat_dim is 64 with at most 64 live steps,
+ * every step -- its rows' assembly, the blocks, the final norm, out_proj,
+ * CFG-Zero* and the Euler step -- runs inside one launch.
  * The first call with a given set of arguments (x, cond and mu pointers, P, Pc,
  * n_steps, cfg_value, schedule, use_zero_star) runs the loop eagerly; the
  * second records it as a HIP graph and every later call with the same
