@@ -176,6 +176,41 @@ def test_block_dots_of_the_kernel_that_runs(vxm_ctx, orc, path, N, K, M):
     w.free()
 
 
+@pytest.mark.parametrize("N,K,M", [(2048, 2048, 512), (2560, 1024, 512), (8192, 256, 512), (256, 8192, 128),
+                                   (1001, 512, 100), (8192, 1024, 48)])
+def test_gemm_subnormal_scales(vxm_ctx, orc, N, K, M):
+    """Every third weight row and every other activation row are scaled so far down that
+    each of their Q8_0 scales is an fp16 subnormal (block maxima near 3e-5, d near 2e-7).
+    The scale products d_x * d_w must still be the exact fp32 products: each output is
+    the fp64 combine of the kernel's own int32 block sums to within fp32 summation error
+    (a subnormal scale flushed to zero would zero whole rows)."""
+    rng = np.random.default_rng(3 * N + K + M)
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    w[::3] *= 5e-4
+    x[::2] *= 1e-5
+    wq = orc.quantize_rows(w, orc.QUANT_REF)
+    _, dw = orc.split_q8(wq, N, K)
+    dwf = dw.view(np.float16).astype(np.float32)
+    assert (np.abs(dwf[::3]) < 2.0 ** -14).all() and (dwf[::3] != 0).any()
+    w_dev = vxm_ctx.upload_q8_0(wq, N, K)
+    xq, xd = vxm_ctx.quantize_q8_0(_dev(x), 1)
+    sums = _np(vxm_ctx.block_dots(w_dev, xq, xd))
+    y = _np(vxm_ctx.mul_mat_q8(w_dev, xq, xd))
+    vxm_ctx.sync()
+    xq_ref = orc.quantize_rows(x, 1)
+    assert np.array_equal(sums, orc.block_dots(wq, xq_ref, N, K, M))
+    _, dx = orc.split_q8(xq_ref, M, K)
+    dxf = dx.view(np.float16).astype(np.float32)
+    assert (np.abs(dxf[::2]) < 2.0 ** -14).all()
+    terms = (sums.astype(np.float32) * (dxf[:, None, :] * dwf[None, :, :])).astype(np.float64)
+    ref, mag = terms.sum(axis=2), np.abs(terms).sum(axis=2)
+    err = np.abs(y.astype(np.float64) - ref)
+    assert (err <= 1e-5 * mag + 1e-30).all(), f"max err / magnitude {(err / np.maximum(mag, 1e-300)).max()}"
+    assert (y[::2][:, ::3] != 0).mean() > 0.9   # the subnormal x subnormal products are not flushed
+    w_dev.free()
+
+
 def test_tile_gemm_unaligned_output(vxm_ctx, orc):
     """An output pointer that is 4- but not 16-byte aligned takes the tile GEMM's
     scalar stores: the same bits as into an aligned buffer."""
