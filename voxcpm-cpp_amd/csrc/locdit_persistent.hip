@@ -364,16 +364,25 @@ __device__ __forceinline__ void dma_scales(int wsc, const uint16_t *wd, int nbk,
 }
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
 // The scale products d_w * d_x of a 16 x 16 int32 block product go to the matrix core
-// as well: v_mfma_f32_16x16x1_4b_f32 forms four 16 x 16 outer products at once (lane
-// 16 k + i supplies element i of block k's two vectors; block k's result sits in
-// registers 4 k .. 4 k + 3 in the layout of the int8 product's result).  Each product
-// has K = 1 and a zero accumulator, so it is the single fp32 rounding of d_w * d_x
-// that a VALU multiply gives, and the VALU is left with the convert and the fma per
-// value and block (3 -> 2 instructions).  Measured per LocDiT evaluation: 540 -> 535.5
-// us at 2 x 24 rows, 441 -> 439 at 2 x 11.  The gate/up products (mfma_run2) keep
-// their VALU scale products: with the same change there, 2 x 24 rows took 551 us.
+// as well: v_mfma_f32_16x16x4_4b_f16 forms four 16 x 16 outer products at once (lane
+// 16 k + i supplies element i of block k's two vectors, as fp16 bits in k-slot 0 with
+// the other slots zero; block k's result sits in registers 4 k .. 4 k + 3 in the layout
+// of the int8 product's result).  A product of two fp16 values has at most 22
+// significant bits, so each is the exact fp32 value d_w * d_x that a VALU multiply of
+// the converted scales gives (subnormal scales included), and the VALU is left with the
+// convert and the fma per value and block (3 -> 2 instructions).  The stage's scales are
+// kept as fp32 copies of fp16 values, so converting them back is exact.  The fp16 form
+// takes a quarter of the matrix-core cycles of v_mfma_f32_16x16x1_4b_f32 on the
+// converted scales, which made the gate/up products (mfma_run2) slower when they used it.
+__device__ __forceinline__ v16f scale_outer16_f16(uint32_t a, uint32_t b) {
+    const v2u av = {a, 0u}, bv = {b, 0u};
+    return __builtin_amdgcn_mfma_f32_16x16x4f16(__builtin_bit_cast(v4h, av), __builtin_bit_cast(v4h, bv), v16f{}, 0,
+                                                0, 0);
+}
 
 // acc[t][v] += products of tile rows 16 c + 4 q + v with stage rows 16 t + r (t < MT)
 // over the NB blocks from b0: weight tile (nbw blocks per row) at wt / wsc, stage
@@ -391,12 +400,12 @@ __device__ __forceinline__ void mfma_run(const uint8_t *lds, int wt, int wsc, in
         // row 16 c + r and stage row 16 t + r of block b0 + i0 + q
         const bool sv = q < G;
         const int bs = b0 + i0 + (sv ? q : 0);
-        const float aw = sv ? vxm_h2f(*(const uint16_t *)(lds + wsc + ((16 * c + r) * nbw + bs) * 2)) : 0.0f;
+        const uint32_t aw = sv ? *(const uint16_t *)(lds + wsc + ((16 * c + r) * nbw + bs) * 2) : 0u;
         v16f sc[MT];
 #pragma unroll
         for (int t = 0; t < MT; t++) {
-            const float bxs = sv ? *(const float *)(lds + st_sc + (bs * kMP + 16 * t + r) * 4) : 0.0f;
-            sc[t] = __builtin_amdgcn_mfma_f32_16x16x1f32(aw, bxs, v16f{}, 0, 0, 0);
+            const uint32_t bxs = sv ? vxm_f2h(*(const float *)(lds + st_sc + (bs * kMP + 16 * t + r) * 4)) : 0u;
+            sc[t] = scale_outer16_f16(aw, bxs);
         }
 #pragma unroll
         for (int i = 0; i < G; i++) {
@@ -421,36 +430,48 @@ __device__ __forceinline__ void mfma_run(const uint8_t *lds, int wt, int wsc, in
 template <int MT, int NB, int G>
 __device__ __forceinline__ void mfma_run2(const uint8_t *lds, int wt, int wsc, int nbw, int c0, int st, int st_sc,
                                           int nbs, int b0, int lane, float (&acc)[2][MT][4]) {
-    static_assert(NB % G == 0, "block groups");
+    static_assert(NB % G == 0 && G <= 4, "block groups");
     const int q = lane >> 4, r = lane & 15, sl = slot_of(q, r);
 #pragma unroll 1
-    for (int i0 = 0; i0 < NB; i0 += G)
-#pragma unroll
-    for (int i = 0; i < G; i++) {
-        const int b = b0 + i0 + i;
-        long a[2], bx[MT];
-        float dx[MT], dw[2][4];
+    for (int i0 = 0; i0 < NB; i0 += G) {
+        // every operand of the group first: each block's activation pieces are read once
+        // for both tiles; then per tile its scale products (one per row tile, covering the
+        // group: lane (k = q, i = r) supplies weight row 16 (c0 + cc) + r and stage row
+        // 16 t + r of block b0 + i0 + q) and its products, blocks in order
+        const bool sv = q < G;
+        const int bs = b0 + i0 + (sv ? q : 0);
+        long a[2][G], bx[G][MT];
+        uint32_t aw[2], bxs[MT];
 #pragma unroll
         for (int cc = 0; cc < 2; cc++) {
-            a[cc] = *(const long *)(lds + wt + ((c0 + cc) * (nbw / 2) + (b >> 1)) * 1024 + (b & 1) * 512 + sl);
+            aw[cc] = sv ? *(const uint16_t *)(lds + wsc + ((16 * (c0 + cc) + r) * nbw + bs) * 2) : 0u;
 #pragma unroll
-            for (int v = 0; v < 4; v++)
-                dw[cc][v] = vxm_h2f(*(const uint16_t *)(lds + wsc + ((16 * (c0 + cc) + 4 * q + v) * nbw + b) * 2));
+            for (int i = 0; i < G; i++) {
+                const int b = b0 + i0 + i;
+                a[cc][i] = *(const long *)(lds + wt + ((c0 + cc) * (nbw / 2) + (b >> 1)) * 1024 + (b & 1) * 512 + sl);
+            }
         }
 #pragma unroll
         for (int t = 0; t < MT; t++) {
-            bx[t] = *(const long *)(lds + st + (t * nbs + b) * 512 + sl);
-            dx[t] = *(const float *)(lds + st_sc + (b * kMP + 16 * t + r) * 4);
+            bxs[t] = sv ? vxm_f2h(*(const float *)(lds + st_sc + (bs * kMP + 16 * t + r) * 4)) : 0u;
+#pragma unroll
+            for (int i = 0; i < G; i++) bx[i][t] = *(const long *)(lds + st + (t * nbs + b0 + i0 + i) * 512 + sl);
         }
 #pragma unroll
-        for (int cc = 0; cc < 2; cc++)
+        for (int cc = 0; cc < 2; cc++) {
+            v16f sc[MT];
 #pragma unroll
-            for (int t = 0; t < MT; t++) {
-                const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[cc], bx[t], v4i{}, 0, 0, 0);
+            for (int t = 0; t < MT; t++) sc[t] = scale_outer16_f16(aw[cc], bxs[t]);
 #pragma unroll
-                for (int v = 0; v < 4; v++)
-                    acc[cc][t][v] = __builtin_fmaf((float)ci[v], dw[cc][v] * dx[t], acc[cc][t][v]);
-            }
+            for (int i = 0; i < G; i++)
+#pragma unroll
+                for (int t = 0; t < MT; t++) {
+                    const v4i ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[cc][i], bx[i][t], v4i{}, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        acc[cc][t][v] = __builtin_fmaf((float)ci[v], sc[t][4 * i + v], acc[cc][t][v]);
+                }
+        }
     }
 }
 
