@@ -111,6 +111,12 @@ constexpr int kH1Readers = VXM_H1_READERS;
 #define VXM_NREADERS 1
 #endif
 constexpr int kNR = VXM_NREADERS;
+// 1: the second part of phase D's ring refills is issued by the reader wave during
+// phase E (ring_refill_readers); 0: by each compute wave before E's Q8_0 of p
+#ifndef VXM_D2_READER
+#define VXM_D2_READER 1
+#endif
+constexpr bool kD2Reader = VXM_D2_READER && VXM_NREADERS == 1;
 constexpr int kCW = kWaves - kNR;
 constexpr int kThreads = kWaves * 64;
 constexpr int kG = 256;                // workgroups: one per CU
@@ -864,13 +870,17 @@ __device__ __forceinline__ float wave_sum4_rows(const float (&v)[4]) {
 // once saturate the CU's address unit, and a wave's load issue blocks until
 // it is accepted, so refills issued between units stalled the compute by
 // about as long as the compute itself.
-template <class S, int OFF, int K, int G = 0>
+// X: of the P - K stream positions after the phase's slots that are in flight at its
+// start, the last X were issued by the reader wave (ring_refill_readers), not by this
+// wave, and do not count in its vmcnt.
+template <class S, int OFF, int K, int G = 0, int X = 0>
 __device__ __forceinline__ void ring_phase(const int8_t *ring, int l, int ci, int lane, const int8_t *xq,
                                            const float *xd, float *part) {
     static_assert(K <= S::P, "a phase's slots are all in the ring at its start");
+    static_assert(X <= S::P - K, "positions after the phase");
     if constexpr (G < K) {
         constexpr int n = K - G < 4 ? K - G : 4;
-        ring_wait<3 * (S::P - G - n)>();
+        ring_wait<3 * (S::P - G - n - X)>();
         UnitOps o[4];
         o[0] = unit_load<S, OFF + G>(ring, l, ci, lane, xq, xd);
         if constexpr (n > 1) o[1] = unit_load<S, OFF + G + 1>(ring, l, ci, lane, xq, xd);
@@ -890,7 +900,7 @@ __device__ __forceinline__ void ring_phase(const int8_t *ring, int l, int ci, in
             // units past the phase's (or a wave's dummy units) are not stored
             if (u >= 0 && u < Slot<S, OFF + G>::U) part[u] = tot;
         }
-        ring_phase<S, OFF, K, G + 4>(ring, l, ci, lane, xq, xd, part);
+        ring_phase<S, OFF, K, G + 4, X>(ring, l, ci, lane, xq, xd, part);
     }
 }
 
@@ -905,6 +915,33 @@ __device__ __forceinline__ void ring_refill(const vxm_pparams &p, const UnitBase
         ring_issue<S, sn>(p, wrap ? nxt : cur, ring_lds, l + (wrap ? 1 : 0), wg, ci, lane);
         ring_refill<S, OFF, K, k + 1>(p, cur, nxt, ring_lds, l, wg, ci, lane);
     }
+}
+
+// The same refills, slots OFF + K0 .. OFF + K - 1, for every compute wave's ring,
+// issued by a reader wave (ring0 = the LDS address of compute wave 0's ring).  Units
+// a wave does not own are skipped: no compute wave counts these loads.  The reader
+// wave's later loads (its share of the next exchange reads) retire after them, so by
+// the time it passes the barrier that follows its next exchange read they are in LDS.
+template <class S, int OFF, int K0, int K, int k = K0>
+__device__ __forceinline__ void ring_refill_slots(const vxm_pparams &p, const UnitBases &cur, const UnitBases &nxt,
+                                                  uint32_t ring_ci, int l, int wg, int ci, int lane) {
+    if constexpr (k < K) {
+        constexpr int s = OFF + k, sn = (s + S::P) % S::NS;
+        constexpr bool wrap = s + S::P >= S::NS;
+        const int8_t *q;
+        const uint16_t *d;
+        bool live;
+        unit_addr<S, sn>(p, wrap ? nxt : cur, wg, ci, q, d, live);
+        if (live) dma_unit(ring_ci + ring_slot<S, sn>(l + (wrap ? 1 : 0)) * kSlot, q, d, lane, true);
+        ring_refill_slots<S, OFF, K0, K, k + 1>(p, cur, nxt, ring_ci, l, wg, ci, lane);
+    }
+}
+
+template <class S, int OFF, int K0, int K>
+__device__ __forceinline__ void ring_refill_readers(const vxm_pparams &p, const UnitBases &cur, const UnitBases &nxt,
+                                                    uint32_t ring0, int l, int wg, int lane) {
+    for (int ci = 0; ci < kCW; ci++)
+        ring_refill_slots<S, OFF, K0, K>(p, cur, nxt, ring0 + ci * (S::RING * kSlot), l, wg, ci, lane);
 }
 
 // Rows of one attention batch into registers.  K: lane (kin, sub) of wave w
@@ -1474,12 +1511,17 @@ __device__ __forceinline__ void decode_run(const vxm_pparams &p, float *lds, int
         lds_barrier();
         if (*bail) return;
         VXM_TS(tid_now() == 0, 9);
-        if (!reader) ring_refill<S, S::OD, S::SD, kDE>(p, cur, nxt, ring_lds, l, wg, ci, lane);
+        if (!kD2Reader && !reader) ring_refill<S, S::OD, S::SD, kDE>(p, cur, nxt, ring_lds, l, wg, ci, lane);
         VXM_TS(tid_now() == 0, 15);
         quantize_lds_bf16x2((const uint32_t *)big, F, xq, xd);
         lds_barrier();
         VXM_TS(tid_now() == 0, 14);
-        if (!reader) ring_phase<S, S::OE, S::SE>(ring, l, ci, lane, xq, xd, part);
+        // The rest of D's refills (the next layer's first A / C units) go out from the
+        // reader wave while the compute waves form E's units: issued by the compute
+        // waves before the Q8_0 of p, they held it (and the units) back by about as long
+        // as the address unit took to accept them.
+        if (!reader) ring_phase<S, S::OE, S::SE, 0, kD2Reader ? S::SD - kDE : 0>(ring, l, ci, lane, xq, xd, part);
+        else if (kD2Reader) ring_refill_readers<S, S::OD, kDE, S::SD>(p, cur, nxt, ring_lds, l, wg, lane);
         lds_barrier();
         VXM_TS(tid_now() == 0, 10);
         if (!reader && t < S::RE / 2 * kRep) {

@@ -365,6 +365,9 @@ __device__ uint64_t vxm_attn_trace[4096 * 8];
         if (tid == 0 && blockIdx.x * gridDim.y + blockIdx.y < 4096)                                           \
             vxm_attn_trace[(blockIdx.x * gridDim.y + blockIdx.y) * 8 + (k)] = __builtin_amdgcn_s_memtime(); \
     } while (0)
+extern "C" int vxm_attn_trace_read(void *host, size_t bytes) {   // profiling builds only
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(vxm_attn_trace), bytes, 0, hipMemcpyDeviceToHost);
+}
 #else
 #define VXM_ATTN_TS(k) \
     do {               \
