@@ -940,6 +940,11 @@ __device__ __forceinline__ void ring_refill_slots(const vxm_pparams &p, const Un
 template <class S, int OFF, int K0, int K>
 __device__ __forceinline__ void ring_refill_readers(const vxm_pparams &p, const UnitBases &cur, const UnitBases &nxt,
                                                     uint32_t ring0, int l, int wg, int lane) {
+    // (the profiling build keeps this loop rolled: unrolled, its timestamps' registers
+    // made it spill here, and each spill reload waited for the DMAs before it)
+#ifdef VXM_PERSISTENT_TRACE
+#pragma unroll 1
+#endif
     for (int ci = 0; ci < kCW; ci++)
         ring_refill_slots<S, OFF, K0, K>(p, cur, nxt, ring0 + ci * (S::RING * kSlot), l, wg, ci, lane);
 }
