@@ -319,7 +319,10 @@ int vxm_locdit_forward(vxm_locdit *m, const float *x_dev, const float *cond_dev,
  * n_steps, cfg_value, schedule, use_zero_star) runs the loop eagerly; the
  * second records it as a HIP graph and every later call with the same
  * arguments (and the same internal buffers) replays that graph, reading the
- * current contents of x, cond and mu.  Results are identical either way. */
+ * current contents of x, cond and mu.  The steps' time rows (time_mlp and
+ * delta_time_mlp, src/locdit.c:140-159) depend only on the steps' t: a solve
+ * whose t are those of the model's previous time rows (every patch of an
+ * utterance) reuses them.  Results are identical either way. */
 #define VXM_CFM_SWAY 0      /* vcpm_cfm_sway_t_bf16 (src/cfm_solver.c:27-37) */
 #define VXM_CFM_UNIFORM 1   /* t = bf16(1 - step / n_steps) */
 int vxm_cfm_solve(vxm_locdit *m, float *x_dev, const float *cond_dev, int32_t P, int32_t Pc,

@@ -309,6 +309,18 @@ def test_cfm_graph_replays_match_eager(vxm_ctx, orc, cfg):
     assert not np.array_equal(five, eager)
     for rep in range(3):                 # back to the first key: eager, recorded, replayed
         assert np.array_equal(solve(), eager), f"return run {rep}"
+    # the time rows are kept between solves of one schedule; the sway schedule has as many
+    # steps (the same buffers) with other t, so its rows replace them, and back again
+    x.copy_(x0d)
+    m.cfm_solve(x, cd, md, 10, 2.0, 0, True)
+    torch.cuda.synchronize()
+    sway = x.cpu().numpy()
+    assert not np.array_equal(sway, eager)
+    assert np.array_equal(solve(), eager), "uniform after sway"
+    x.copy_(x0d)
+    m.cfm_solve(x, cd, md, 10, 2.0, 0, True)
+    torch.cuda.synchronize()
+    assert np.array_equal(x.cpu().numpy(), sway), "sway after uniform"
     m.free()
 
 

@@ -46,6 +46,11 @@ struct vxm_locdit {
     uint16_t *ad = nullptr;
     int8_t *xq8 = nullptr;     // Q8_0 of x [P][feat]: in_proj's input, written by the
     uint16_t *xd8 = nullptr;   //   Euler update for the next evaluation
+    // tc holds the time rows of the last time_features call as long as the buffers
+    // keep their carving: tf_key = (rows, the bits of dt and of every step's t) of
+    // that call (empty: nothing valid), carve = the carving's (S, P, Pc, R, base)
+    std::vector<uint32_t> tf_key;
+    std::vector<int64_t> carve;
     // pinned staging of the host-computed embeddings, reused once its copy is done
     float *pin = nullptr;
     size_t pin_floats = 0;
@@ -309,6 +314,12 @@ static int ensure_bufs(vxm_locdit *m, int64_t S, int64_t P, int64_t Pc, int64_t 
     }
     char *b = (char *)m->buf;
     for (auto &p : parts) { *p.dst = b; b += (p.bytes + 255) & ~(size_t)255; }
+    // a new carving moves tc (and lays other buffers over its old rows)
+    const std::vector<int64_t> cv = {S, P, Pc, R, (int64_t)(uintptr_t)m->buf};
+    if (cv != m->carve) {
+        m->tf_key.clear();
+        m->carve = cv;
+    }
     // staging for R embedding rows
     const size_t need = (size_t)(R * H);
     if (need > m->pin_floats) {
@@ -335,6 +346,18 @@ static int time_features(vxm_locdit *m, const float *t_host, int rows, float dt)
     vxm_ctx *ctx = m->ctx;
     const int64_t H = m->dims.H;
     const int var = ctx->quant_variant;
+    // The time rows are a function of the steps' t and dt alone (the weights are the
+    // model's): a solve with the same schedule as the last one (every patch of an
+    // utterance) finds them in tc already.  Under a caller's capture nothing runs now,
+    // so nothing is reused and nothing is remembered.
+    std::vector<uint32_t> key((size_t)rows + 2);
+    key[0] = (uint32_t)rows;
+    memcpy(&key[1], &dt, 4);
+    if (rows > 0) memcpy(&key[2], t_host, (size_t)rows * 4);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    VXM_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cap));
+    if (cap == hipStreamCaptureStatusNone && !m->tf_key.empty() && key == m->tf_key) return VXM_OK;
+    m->tf_key.clear();
     // the pinned buffer may still feed the previous call's copy
     VXM_HIP(ctx, hipEventSynchronize(m->pin_done));
     for (int r = 0; r < rows; r++) {
@@ -366,6 +389,7 @@ static int time_features(vxm_locdit *m, const float *t_host, int rows, float dt)
     hipLaunchKernelGGL(k_time_combine, dim3(elementwise_grid(rows * H)), dim3(256), 0, ctx->stream, m->emb,
                        m->t_b2, m->emb + (int64_t)rows * H, m->dt_b2, m->tc, (int64_t)rows, H);
     VXM_CHECK_LAUNCH(ctx);
+    if (cap == hipStreamCaptureStatusNone) m->tf_key = std::move(key);
     return VXM_OK;
 }
 
