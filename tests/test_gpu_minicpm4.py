@@ -363,6 +363,43 @@ def test_block_prefill_fused_rope_and_attention_quant_bit_identical(vxm_ctx, orc
     assert all(np.isfinite(a).all() for a in y0)
 
 
+@pytest.mark.parametrize("M,L", [(512, 3), (333, 2), (2048, 2)])
+def test_forward_prefill_fused_epilogues_bit_identical(vxm_ctx, orc, M, L):
+    """The whole L-layer prefill with every fused epilogue the tile GEMM takes (RoPE and
+    the f16 K/V append in the QKV GEMM, SwiGLU and the Q8_0 in gate/up) against
+    PATH_MFMA_TILED, which runs the same GEMMs and the separate kernels: an odd M (a
+    ragged row tile) and M = 2048 (128 x 128 tiles, the long-span attention) included,
+    the hidden state after the final norm and every cache row are identical bit for bit."""
+    import vxm
+
+    rng = np.random.default_rng(91 + M + L)
+    H, nh, nkv, hd, F = 2048, 16, 2, 128, 6144
+    lws = [rand_layer(orc, rng, H, nh, nkv, hd, F) for _ in range(L)]
+    c = cfg_dict(H, L, nh, nkv, hd, F)
+    x = rng.normal(0, 1, (M, H)).astype(np.float32)
+    fn = (1.0 + 0.02 * rng.normal(0, 1, H)).astype(np.float32)
+    outs = []
+    for path in (vxm.PATH_AUTO, vxm.PATH_MFMA_TILED):
+        vxm_ctx.set_path(path)
+        try:
+            model = vxm.MiniCPM4(vxm_ctx, c, lws, final_norm=fn)
+            kv = vxm.KVCache(vxm_ctx, L, nkv, hd, M)
+            xd = _dev(x)
+            print(f"fused epilogues M={M} L={L} path={path}", flush=True)
+            model.forward(kv, xd, 0)
+            vxm_ctx.sync()
+            outs.append((xd.cpu().numpy(), [kv.download(l) for l in range(L)]))
+            kv.free()
+            model.free()
+        finally:
+            vxm_ctx.set_path(vxm.PATH_AUTO)
+    (y0, kv0), (y1, kv1) = outs
+    assert np.isfinite(y0).all()
+    assert np.array_equal(y0, y1)
+    for a, b in zip(kv0, kv1):
+        assert all(np.array_equal(p, q) for p, q in zip(a, b))
+
+
 def test_block_noncausal_tiled_attention(vxm_ctx, orc):
     import vxm
 
