@@ -47,8 +47,9 @@ struct vxm_locdit {
     int8_t *xq8 = nullptr;     // Q8_0 of x [P][feat]: in_proj's input, written by the
     uint16_t *xd8 = nullptr;   //   Euler update for the next evaluation
     // tc holds the time rows of the last time_features call as long as the buffers
-    // keep their carving: tf_key = (rows, the bits of dt and of every step's t) of
-    // that call (empty: nothing valid), carve = the carving's (S, P, Pc, R, base)
+    // keep their carving: tf_key = (rows, quantizer, path, the bits of dt and of every
+    // step's t) of that call (empty: nothing valid), carve = the carving's (S, P, Pc, R,
+    // base)
     std::vector<uint32_t> tf_key;
     std::vector<int64_t> carve;
     // pinned staging of the host-computed embeddings, reused once its copy is done
@@ -346,14 +347,17 @@ static int time_features(vxm_locdit *m, const float *t_host, int rows, float dt)
     vxm_ctx *ctx = m->ctx;
     const int64_t H = m->dims.H;
     const int var = ctx->quant_variant;
-    // The time rows are a function of the steps' t and dt alone (the weights are the
-    // model's): a solve with the same schedule as the last one (every patch of an
-    // utterance) finds them in tc already.  Under a caller's capture nothing runs now,
-    // so nothing is reused and nothing is remembered.
-    std::vector<uint32_t> key((size_t)rows + 2);
+    // The time rows are a function of the steps' t and dt (the weights are the model's)
+    // and of the context settings that pick the quantizer and the kernels: a solve with
+    // the same schedule as the last one (every patch of an utterance) finds them in tc
+    // already.  Under a caller's capture nothing runs now, so nothing is reused and
+    // nothing is remembered.
+    std::vector<uint32_t> key((size_t)rows + 4);
     key[0] = (uint32_t)rows;
-    memcpy(&key[1], &dt, 4);
-    if (rows > 0) memcpy(&key[2], t_host, (size_t)rows * 4);
+    key[1] = (uint32_t)var;
+    key[2] = (uint32_t)ctx->path;
+    memcpy(&key[3], &dt, 4);
+    if (rows > 0) memcpy(&key[4], t_host, (size_t)rows * 4);
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     VXM_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cap));
     if (cap == hipStreamCaptureStatusNone && !m->tf_key.empty() && key == m->tf_key) return VXM_OK;
