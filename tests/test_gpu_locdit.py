@@ -321,6 +321,19 @@ def test_cfm_graph_replays_match_eager(vxm_ctx, orc, cfg):
     m.cfm_solve(x, cd, md, 10, 2.0, 0, True)
     torch.cuda.synchronize()
     assert np.array_equal(x.cpu().numpy(), sway), "sway after uniform"
+    # the quantizer is part of what the time rows depend on: after a switch they are formed
+    # anew, as a model that only ever ran with the other quantizer forms them
+    vxm_ctx.set_quant_variant(0)
+    try:
+        ref_q = solve()
+        fresh, _, _ = _model(vxm_ctx, orc, 81, **dims)
+        x.copy_(x0d)
+        fresh.cfm_solve(x, cd, md, 10, 2.0, 1, True)
+        torch.cuda.synchronize()
+        assert np.array_equal(x.cpu().numpy(), ref_q), "time rows after a quantizer switch"
+        fresh.free()
+    finally:
+        vxm_ctx.set_quant_variant(1)
     m.free()
 
 
