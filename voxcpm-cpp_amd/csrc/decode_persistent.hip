@@ -78,7 +78,10 @@ constexpr int kTraceSlots = 16;
 
 namespace {
 
-constexpr int kWaves = 8;              // waves per workgroup: 1 reader + 7 compute
+#ifndef VXM_WAVES
+#define VXM_WAVES 8
+#endif
+constexpr int kWaves = VXM_WAVES;      // waves per workgroup: kNR readers + the compute waves
 // Waves that read each exchanged input: x (phase A), the attention output
 // (phase C), h1 (phase D) and p (phase E).  An exchange read is a round of
 // agent-scope loads whose cost is their issue and their trip to the memory
