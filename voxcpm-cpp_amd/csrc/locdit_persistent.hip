@@ -1378,20 +1378,21 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
         lds_barrier();
         if (*bail) return;
         VXM_LTS(26);
-        // wave w: out_proj column tile w & 3 over the K half w >> 2
-        zero_acc();
-        mfma_run<MT, 16>(lds, LS::RA, LS::RA_SC, 32, wave & 3, LS::ST, LS::ST_SC, 32, 16 * (wave >> 2), lane, acc);
+        // wave w: out_proj column tile w & 3 over the K half w >> 2, on the x rows' one
+        // row tile (NR <= 16: the solve's fit)
+        float acco[1][4] = {};
+        mfma_run<1, 16>(lds, LS::RA, LS::RA_SC, 32, wave & 3, LS::ST, LS::ST_SC, 32, 16 * (wave >> 2), lane, acco);
         lds_barrier();
         VXM_LTS(28);
-        red_store<MT>(lds, LS::ST, wave, lane, acc);
+        red_store<1>(lds, LS::ST, wave, lane, acco);
         lds_barrier();
         // vo [NR][64] fp32 after the partials: the two K halves in order
-        float *vo = (float *)(lds + LS::ST + kWaves * MT * 1024);
-        static_assert(kWaves * kMT * 1024 + kMaxM * kFeat * 4 <= LS::ST_SC - LS::ST, "out_proj rows in the stage");
-        for (int idx = tid; idx < 4 * MT * 64; idx += kThreads) {
-            const int ct = idx / (MT * 64), t = (idx / 64) % MT, ln = idx & 63, m = 16 * t + (ln & 15);
+        float *vo = (float *)(lds + LS::ST + kWaves * 1024);
+        static_assert(kWaves * 1024 + kMaxM * kFeat * 4 <= LS::ST_SC - LS::ST, "out_proj rows in the stage");
+        for (int idx = tid; idx < 4 * 64; idx += kThreads) {
+            const int ct = idx / 64, t = 0, ln = idx & 63, m = ln & 15;
             float o[4];
-            red_sum<MT>(lds, LS::ST, 4, ct, t, ln, o);
+            red_sum<1>(lds, LS::ST, 4, ct, t, ln, o);
             if (m < NR)
 #pragma unroll
                 for (int v = 0; v < 4; v++) vo[m * kFeat + 16 * ct + 4 * (ln >> 4) + v] = o[v];
@@ -1589,6 +1590,7 @@ bool vxm_locdit_persistent_solve_fits(vxm_ctx *ctx, const vxm_block_dims &d, int
         sv.P * kFeat > kSolveMaxN || 3 + sv.Pc + sv.P != S || sv.n_seg * S != M || sv.n_seg < 1 || sv.n_seg > 2)
         return false;
     if (sv.use_cfg && sv.n_seg != 2) return false;
+    if (sv.n_seg * sv.P > 16) return false;   // out_proj takes the x rows as one row tile
     if (!sv.in_proj || !sv.out_proj || sv.in_proj->n != kH || sv.in_proj->k != kFeat || sv.out_proj->n != kFeat ||
         sv.out_proj->k != kH || !aligned16(sv.in_proj->qs) || !aligned16(sv.out_proj->qs) ||
         !aligned16(sv.out_proj->d))
