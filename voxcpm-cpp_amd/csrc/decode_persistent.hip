@@ -133,9 +133,10 @@ constexpr int kSlot = kUnit + 128;     // LDS bytes per ring slot: quants, then 
 // Every channel is written as kRep replicas; workgroup b reads replica
 // b % kRep, so the coherent loads of 256 workgroups spread over more lines.
 // Each replica costs its producer one more agent-scope store per word:
-// measured (us per token) 32 replicas 741, 16 693, 8 677, 4 667, 2 666, 1 672.
+// measured (us per token) 32 replicas 741, 16 693, 8 677, 4 667, 2 666, 1 672;
+// with today's phases 8 replicas 568, 4 555.6, 2 550.6, 1 551.5.
 #ifndef VXM_REPLICAS
-#define VXM_REPLICAS 4
+#define VXM_REPLICAS 2
 #endif
 constexpr int kRep = VXM_REPLICAS;
 constexpr int kPad = 64;               // words between replicas
