@@ -353,3 +353,35 @@ def test_persistent_prefixes_track_the_launch_based_path(vxm_ctx, orc, shape):
         rp, rk, rpk = _rel(vp, ref), _rel(vk, ref), _rel(vp, vk)
         print(f"{shape} L={Lp}: persistent-oracle {rp:.3e}  kernels-oracle {rk:.3e}  persistent-kernels {rpk:.3e}")
         assert np.isfinite(vp).all() and rpk <= 2 * rk + 1e-3, (Lp, rp, rk, rpk)
+
+
+@pytest.mark.parametrize("P", [8, 12])
+def test_persistent_solve_x_row_limit(vxm_ctx, orc, P):
+    """A CFG solve whose two branches hold 16 x rows (P = 8: the whole solve in one
+    launch, out_proj on its one 16-row tile of x rows) and 24 (P = 12: beyond that
+    tile, so one single launch per evaluation): on two full-width blocks the
+    trajectory bar against the oracle on both block modes, and the single launches no
+    farther from the launch-based path than twice that path's distance from the
+    oracle plus 1e-3."""
+    import vxm
+    from test_gpu_locdit import assert_trajectory_close
+
+    m, ow, ocfg = _model(vxm_ctx, orc, 211, dict(GQA, L=2))
+    x0, cond, mu = make_inputs(212, P, PC["gqa"], 64, 1024)
+    ref = orc.cfm_solve(ocfg, ow, x0, cond, mu, 3, 2.0, 1, 1)
+    outs = {}
+    try:
+        for mode in (vxm.DECODE_PERSISTENT, vxm.DECODE_KERNELS):
+            m.set_block_mode(mode)
+            print(f"P={P} solve, mode {mode}", flush=True)
+            x = _dev(x0)
+            m.cfm_solve(x, _dev(cond), _dev(mu), 3, 2.0, vxm.CFM_UNIFORM, True)
+            m.check()
+            outs[mode] = x.cpu().numpy()
+            assert_trajectory_close(outs[mode], ref, f"P={P} mode {mode}")
+    finally:
+        m.free()
+    vp, vk = outs[vxm.DECODE_PERSISTENT], outs[vxm.DECODE_KERNELS]
+    rk, rpk = _rel(vk, ref), _rel(vp, vk)
+    print(f"P={P}: kernels-oracle {rk:.3e}  persistent-kernels {rpk:.3e}")
+    assert rpk <= 2 * rk + 1e-3, (rk, rpk)
