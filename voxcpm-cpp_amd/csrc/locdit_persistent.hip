@@ -978,7 +978,6 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
             }
             lds_barrier();
             if (*bail) return;
-            VXM_LTS(21);
             VXM_LTS(5);
             // scores s_ij = (k_j . q_i) * scale: LPS lanes per score (8 at HD = 128, where the
             // serial 128-term sum was the longer wait; 1 at HD = 64), each a run of HD / LPS dims
@@ -1032,6 +1031,7 @@ __device__ __forceinline__ void run_blocks(const vxm_lparams &p, uint8_t *lds, i
                 O[i * HD + d] = o;
             }
             lds_barrier();
+            VXM_LTS(21);
             // Q8_0 of the output rows: thread (i, c) holds dims 8c .. 8c+7, four threads a block
             constexpr int CPR = HD / 8;
             if (!DMA && tid < nq * CPR) {

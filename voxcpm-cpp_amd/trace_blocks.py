@@ -81,7 +81,8 @@ def main():
     print(f"| per block | {th:.2f} | {tw:.2f} |")
     # steps inside phases: median over the workgroups that run them of (slot b - slot a)
     steps = [("QKV: products", 3, 16), ("QKV: partial sums to LDS", 16, 17), ("QKV: epilogue + publish", 17, 4),
-             ("attention: scores", 21, 22), ("attention: softmax", 22, 23), ("attention: P.V + Q8_0 + publish", 23, 6),
+             ("attention: scores", 5, 22), ("attention: softmax", 22, 23), ("attention: P.V", 23, 21),
+             ("attention: Q8_0 + publish", 21, 6),
              ("gate/up: products", 11, 18), ("gate/up: partial sums to LDS", 18, 19), ("gate/up: SwiGLU", 19, 20),
              ("gate/up: Q8_0 + publish", 20, 12)]
     sub = {n: [] for n, _, _ in steps}
