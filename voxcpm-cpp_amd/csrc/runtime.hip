@@ -73,10 +73,13 @@ extern "C" int vxm_open(int device, vxm_ctx **out) {
     return VXM_OK;
 }
 
+static void forget_stream(vxm_ctx *ctx);
+
 extern "C" int vxm_close(vxm_ctx *ctx) {
     if (!ctx) return VXM_ERR_INVALID_ARG;
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
+    forget_stream(ctx);
     if (ctx->act_buf) hipFree(ctx->act_buf);
     if (ctx->split_buf) hipFree(ctx->split_buf);
     if (ctx->split_cnt) hipFree(ctx->split_cnt);
@@ -156,7 +159,14 @@ struct vxm_launch_slot {
 };
 static vxm_launch_slot g_launch_slots[64];
 
-// Holds the device's slot from begin to end (the launch goes in between).
+// Holds the device's slot from begin to end (the launch goes in between).  The
+// ordering event is recorded lazily: a launch from another stream records it on the
+// stream of the device's last single launch (so it covers that launch and whatever
+// that stream queued after it) and waits for it, while launches from one stream,
+// ordered by the stream itself, record nothing (a marker after every launch cost
+// 2.2 us per decode token: 550.5 against 548.3 us).  A wait binds to the event as
+// recorded when the wait is queued, so no cycle of waits can form.  The slot names
+// only streams of open contexts: vxm_close clears it.
 int vxm_ordered_launch_begin(vxm_ctx *ctx, vxm_launch_slot **slot, bool *cap) {
     *slot = nullptr;
     *cap = false;
@@ -169,8 +179,11 @@ int vxm_ordered_launch_begin(vxm_ctx *ctx, vxm_launch_slot **slot, bool *cap) {
     *slot = &o;
     if (*cap) return VXM_OK;
     hipError_t e = hipSuccess;
-    if (!o.ev) e = hipEventCreateWithFlags(&o.ev, hipEventDisableTiming);
-    if (e == hipSuccess && o.last && o.last != ctx->stream) e = hipStreamWaitEvent(ctx->stream, o.ev, 0);
+    if (o.last && o.last != ctx->stream) {
+        if (!o.ev) e = hipEventCreateWithFlags(&o.ev, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventRecord(o.ev, o.last);
+        if (e == hipSuccess) e = hipStreamWaitEvent(ctx->stream, o.ev, 0);
+    }
     if (e != hipSuccess) {
         (void)hipGetLastError();
         o.mu.unlock();
@@ -182,18 +195,17 @@ int vxm_ordered_launch_begin(vxm_ctx *ctx, vxm_launch_slot **slot, bool *cap) {
 
 int vxm_ordered_launch_end(vxm_ctx *ctx, vxm_launch_slot *slot, bool cap) {
     if (!slot) return VXM_OK;
-    int rc = VXM_OK;
-    if (!cap) {
-        const hipError_t e = hipEventRecord(slot->ev, ctx->stream);
-        if (e != hipSuccess) {
-            (void)hipGetLastError();
-            rc = vxm_fail(ctx, VXM_ERR_BACKEND, "single-launch kernel: ordering event failed: %s", hipGetErrorString(e));
-        } else {
-            slot->last = ctx->stream;
-        }
-    }
+    if (!cap) slot->last = ctx->stream;
     slot->mu.unlock();
-    return rc;
+    return VXM_OK;
+}
+
+// A closing context's stream leaves the launch table (its work has completed).
+static void forget_stream(vxm_ctx *ctx) {
+    if (ctx->device < 0 || ctx->device >= 64) return;
+    vxm_launch_slot &o = g_launch_slots[ctx->device];
+    std::lock_guard<std::mutex> g(o.mu);
+    if (o.last == ctx->stream) o.last = nullptr;
 }
 
 // ---- graph capture of the context's stream ---------------------------------
