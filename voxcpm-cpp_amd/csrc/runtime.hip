@@ -164,7 +164,7 @@ static vxm_launch_slot g_launch_slots[64];
 // stream of the device's last single launch (so it covers that launch and whatever
 // that stream queued after it) and waits for it, while launches from one stream,
 // ordered by the stream itself, record nothing (a marker after every launch cost
-// 2.2 us per decode token: 550.5 against 548.3 us).  A wait binds to the event as
+// 3.3 us per decode token: 551.6 against 548.3 us).  A wait binds to the event as
 // recorded when the wait is queued, so no cycle of waits can form.  The slot names
 // only streams of open contexts: vxm_close clears it.
 int vxm_ordered_launch_begin(vxm_ctx *ctx, vxm_launch_slot **slot, bool *cap) {
